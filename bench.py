@@ -1,0 +1,237 @@
+#!/usr/bin/env python3
+"""Benchmark of the Q8_0 bs=1 decode hot path on one MI355X.
+
+Workload ("C2"): greedy decode of a random-init
+Qwen2.5-0.5B-architecture Q8_0 model (24 layers, hidden 896, FFN 4864, 14 Q / 2 KV heads,
+head_dim 64, vocab 151936, tied lm_head), fp16 KV cache with max context 1024, a 32-token
+uniform-random prompt, 128 decoded tokens at batch 1.  A step is one decode token: one
+replay of the captured HIP graph (embedding gather -> 24 layers -> logits -> argmax), with
+every weight and the KV cache resident in HBM before the timed region starts.
+
+Printed (one JSON line on stdout): decode tok/s, the roofline of the dominant kernel (the
+Q8_0 GEMV of the vocab projection, 151936 x 896, timed with HIP events on the library's
+stream over rotated weight copies so the 256 MB Infinity Cache cannot serve it), and the
+CPU baseline: the oracle (C restatement of the reference arithmetic, OpenMP over GEMV rows)
+decoding a bounded sample of the same workload on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "bs=1 decode tok/s (Q8_0 0.5B/8B-arch) + Q8_0 GEMV HBM GB/s % of peak"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Events:
+    def __init__(self, dev):
+        from llamatov_amd import _lib
+        self._lib = _lib
+        self.dev = dev
+        self.a, self.b = ctypes.c_void_p(), ctypes.c_void_p()
+        _lib.call("lt_event_create", dev.handle, ctypes.byref(self.a))
+        _lib.call("lt_event_create", dev.handle, ctypes.byref(self.b))
+
+    def start(self):
+        self._lib.call("lt_event_record", self.dev.handle, self.a)
+
+    def stop_ms(self) -> float:
+        self._lib.call("lt_event_record", self.dev.handle, self.b)
+        ms = ctypes.c_float()
+        self._lib.call("lt_event_elapsed_ms", self.a, self.b, ctypes.byref(ms))
+        return float(ms.value)
+
+    def free(self):
+        self._lib.call("lt_event_destroy", self.a)
+        self._lib.call("lt_event_destroy", self.b)
+
+
+def gemv_roofline(dev, w_embd: np.ndarray, N: int, K: int, launches: int = 60) -> dict:
+    """Time the logits GEMV kernel on rotated copies of the vocab matrix (>= 512 MB)."""
+    from llamatov_amd import dev_residency as dr
+    from llamatov_amd._lib import call
+    blk_bytes = w_embd.nbytes
+    copies = max(2, int(np.ceil(600e6 / blk_bytes)))
+    ws = [dr.DevTensor.from_host(w_embd, dev) for _ in range(copies)]
+    rng = np.random.default_rng(3)
+    xq = dr.DevTensor.from_host(rng.integers(-127, 128, K, dtype=np.int64).astype(np.int8), dev)
+    xd = dr.DevTensor.from_host((rng.standard_normal(K // 32) * 0.05).astype(np.float16).view(np.uint16), dev)
+    y = dr.DevTensor.empty((N,), np.float32, dev)
+    for i in range(copies):  # warm the code path
+        call("lt_q8_gemv_logits", dev.handle, ws[i].vp, xq.vp, xd.vp, y.vp, N, K)
+    dev.sync()
+    ev = Events(dev)
+    ev.start()
+    for i in range(launches):
+        call("lt_q8_gemv_logits", dev.handle, ws[i % copies].vp, xq.vp, xd.vp, y.vp, N, K)
+    ms = ev.stop_ms()
+    ev.free()
+    for t in ws + [xq, xd, y]:
+        t.free()
+    avg_s = ms / 1e3 / launches
+    alg_bytes = N * (K // 32) * 34 + K + (K // 32) * 2 + 4 * N
+    achieved = alg_bytes / avg_s / 1e9
+    return {"kernel": "k_q8_gemv<false,1> (lt_q8_gemv_logits)", "shape": [N, K],
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "bytes_per_launch": alg_bytes, "avg_launch_us": round(avg_s * 1e6, 3),
+            "weight_copies": copies}
+
+
+def cpu_baseline(cfg, weights, prompt, n_decode: int, kv_f16: bool) -> tuple[dict, list[int]]:
+    from oracle import oracle as orc
+    m = orc.OracleModel(cfg, weights, kv_f16=kv_f16)
+    logits = None
+    for t in prompt:
+        logits = m.step(t)
+    toks = []
+    t0 = time.perf_counter()
+    for _ in range(n_decode):
+        tok = orc.argmax(logits)
+        toks.append(tok)
+        logits = m.step(tok)
+    dt = time.perf_counter() - t0
+    cores = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
+    return ({"value": round(n_decode / dt, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+             "sample": f"C2 model, {len(prompt)}-token prompt prefilled untimed, then {n_decode} greedy "
+                       f"decode steps timed (oracle/lt_oracle.c, OpenMP over GEMV rows)"}, toks)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128, help="timed decode tokens")
+    ap.add_argument("--warmup", type=int, default=16, help="untimed decode tokens before timing")
+    ap.add_argument("--kv", choices=["f16", "f32"], default="f16")
+    ap.add_argument("--prompt", type=int, default=32)
+    ap.add_argument("--cpu-tokens", type=int, default=128, help="decode tokens in the CPU baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-roofline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on exactly one GPU; --gpus {args.gpus} is not supported "
+              "(the hot path is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+        return 2
+
+    from llamatov_amd import dev_residency as dr
+    from llamatov_amd import model as M
+    from llamatov_amd._lib import LT_KV_F16, LT_KV_F32
+
+    cfg = M.QWEN25_05B
+    if args.prompt + args.steps > cfg.max_ctx or args.prompt + args.warmup > cfg.max_ctx:
+        print("bench.py: prompt + steps exceeds the 1024-position KV cache", file=sys.stderr)
+        return 2
+    kv_dtype = LT_KV_F16 if args.kv == "f16" else LT_KV_F32
+    log("generating synthetic weights")
+    t0 = time.perf_counter()
+    w = M.synth_weights(cfg, seed=1234)
+    log(f"weights ready in {time.perf_counter() - t0:.1f}s; uploading")
+    dev = dr.get_device()
+    model = dr.ResidentModel(cfg, w, dev)
+    plan = dr.DecodePlan(model, dr.Profile(kv_dtype=kv_dtype), hist_cap=4096)
+    runner = dr.GraphRunner(plan)
+    prompt = M.random_prompt(cfg, args.prompt, seed=7)
+
+    log("prefill (eager) + capture")
+    runner.seed(prompt)
+    first = plan.read_token()
+    runner.capture()
+
+    def rewind():
+        dev.h2d(plan.lens.ptr, np.full(cfg.n_layers, len(prompt), np.int32))
+        for c in plan.caches:
+            c.length = len(prompt)
+        plan.set_token(first)
+        dev.sync()
+
+    # warmup: untimed replays from the post-prompt state
+    log(f"warmup {args.warmup}")
+    runner.replay_tokens(args.warmup)
+    dev.sync()
+
+    # timed: K back-to-back replays from the post-prompt state (the C2 decode)
+    rewind()
+    hist0 = plan.history_count()
+    ev = Events(dev)
+    t0 = time.perf_counter()
+    ev.start()
+    for _ in range(args.steps):
+        runner._launch()
+    gpu_ms = ev.stop_ms()
+    dev.sync()
+    wall = time.perf_counter() - t0
+    tokens = [first] + plan.history()[hist0:hist0 + args.steps]
+    log(f"timed {args.steps} steps: wall {wall * 1e3:.2f} ms, events {gpu_ms:.2f} ms")
+
+    # the same decode with a host round trip per token (reference replay_token protocol)
+    rewind()
+    t1 = time.perf_counter()
+    sync_tokens = [first]
+    for _ in range(args.steps):
+        sync_tokens.append(runner.replay_token())
+    wall_sync = time.perf_counter() - t1
+    ev.free()
+
+    tok_s = args.steps / wall
+    step_bytes = cfg.weight_bytes() + sum(
+        cfg.n_layers * 2 * (len(prompt) + i + 1) * cfg.kv_dim * (2 if kv_dtype == LT_KV_F16 else 4)
+        for i in range(args.steps)) / args.steps
+    result = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": f"C2: {cfg.name} Q8_0 greedy decode, prompt {len(prompt)}, {args.steps} tokens, "
+                        f"bs=1, {args.kv} KV cache max ctx {cfg.max_ctx}, one HIP-graph replay per token",
+            "model": cfg.name, "global_batch": 1, "seq_len": len(prompt) + args.steps,
+            "parallelism": "none (1 GPU)",
+        },
+        "host_sync_tok_s": round(args.steps / wall_sync, 2),
+        "gpu_event_ms_per_step": round(gpu_ms / args.steps, 4),
+        "decode_step_bytes": int(step_bytes),
+        "decode_roofline_frac": round(step_bytes * tok_s / (HBM_PEAK_GBS * 1e9), 4),
+        "tokens_consistent": tokens == sync_tokens,
+    }
+
+    if not args.no_roofline:
+        log("GEMV roofline leg")
+        result["roofline"] = gemv_roofline(dev, w["token_embd.weight"], cfg.vocab, cfg.n_embd)
+
+    if not args.no_cpu_baseline:
+        n_cpu = min(args.cpu_tokens, args.steps)
+        log(f"CPU baseline: oracle over {n_cpu} decode tokens")
+        cb, cpu_tokens = cpu_baseline(cfg, w, prompt, n_cpu, kv_dtype == LT_KV_F16)
+        result["cpu_baseline"] = cb
+        result["tokens_match_cpu"] = cpu_tokens == tokens[:n_cpu]
+
+    runner.free()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

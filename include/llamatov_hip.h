@@ -1,0 +1,175 @@
+/* llamatov_hip.h -- C ABI of libllamatov_hip.so, the gfx950 (MI355X) implementation of
+ * LlamaTov's Q8_0 bs=1 decode hot path.
+ *
+ * The reference boundary is Python ctypes -> CUDA driver API -> extern "C" kernels
+ * (bpd/lib/fact_dispatch.py:36-72; launch pattern bpd/lib/dev_residency.py:558-566).
+ * Each entry point below replaces one reference kernel launch (or driver call) and
+ * keeps its argument meaning; the reference launcher each one replaces is cited.
+ *
+ * Conventions
+ *  - Every function returns int: 0 = success, otherwise an LT_E* code (negative) or a
+ *    positive hipError_t.  lt_last_error() returns the message of the last failure on
+ *    the calling thread.
+ *  - All tensor pointers are raw device pointers (from lt_malloc or any HIP allocation)
+ *    unless the name says host.  Sizes are element counts.
+ *  - Q8_0 weights are GGUF Q8_0 blocks, row-major [N][K/32], 34 bytes each
+ *    (fp16 scale little-endian, then 32 int8), starting at a 4-byte aligned address.
+ *  - Activation quant: int8 xq[K] plus fp16 scales xd[K/32] (uint16 bit patterns).
+ *  - Work is enqueued on the context's stream, asynchronously; lt_sync() waits.
+ *    Between lt_graph_begin and lt_graph_end the launches are recorded into a HIP
+ *    graph instead of executed.
+ *  - Not re-entrant per context: one host thread drives one lt_ctx.
+ */
+#ifndef LLAMATOV_HIP_H
+#define LLAMATOV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define LT_API __attribute__((visibility("default")))
+#else
+#define LT_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LT_OK 0
+#define LT_EINVAL (-1)     /* bad argument: null pointer, bad size, misalignment */
+#define LT_ESTATE (-2)     /* call not valid in the current state (e.g. nested capture) */
+#define LT_ENOMEM (-3)     /* workspace too small */
+
+#define LT_KV_F32 0        /* KV cache element type: fp32 (reference DeviceKVCache, elem_bytes=4) */
+#define LT_KV_F16 1        /* fp16, round-to-nearest-even on store, exact widen on load */
+
+typedef struct lt_ctx lt_ctx;
+typedef struct lt_graph lt_graph;
+
+/* ---- runtime (replaces fact_dispatch._ctx/_libcuda and the cuMem* calls,
+ *      bpd/lib/fact_dispatch.py:46-72; DevTensor bpd/lib/dev_residency.py:387-415) ---- */
+LT_API int lt_version(void);
+LT_API int lt_last_error(char* buf, size_t n);
+LT_API int lt_device_count(int* n);
+LT_API int lt_init(int device, lt_ctx** out);
+LT_API int lt_free_ctx(lt_ctx* ctx);
+LT_API int lt_malloc(lt_ctx* ctx, void** ptr, size_t nbytes);
+LT_API int lt_free(lt_ctx* ctx, void* ptr);
+LT_API int lt_memcpy_h2d(lt_ctx* ctx, void* dst, const void* host_src, size_t nbytes);
+LT_API int lt_memcpy_d2h(lt_ctx* ctx, void* host_dst, const void* src, size_t nbytes);
+LT_API int lt_memcpy_d2d(lt_ctx* ctx, void* dst, const void* src, size_t nbytes);
+/* Stream-ordered byte fill by a kernel (capturable, unlike a memset node). */
+LT_API int lt_fill_u8(lt_ctx* ctx, void* dst, uint8_t value, size_t nbytes);
+LT_API int lt_sync(lt_ctx* ctx);
+
+/* ---- op launchers -------------------------------------------------------------------- */
+
+/* Activation quant, k_quant_q8 (bpd/lib/dev_residency.py:867-886, launcher _launch_quant
+ * :891-904): per 32-block d16 = fp16(amax/127) (1.0 if amax == 0),
+ * q = clamp(rint(x/float(d16)), +-127).  K % 32 == 0. */
+LT_API int lt_quant_q8(lt_ctx* ctx, const float* x, int8_t* xq, uint16_t* xd, int K);
+
+/* k_silu_mul_quant (bpd/lib/dev_residency.py:573-604, _launch_silu_quant :606-613):
+ * v = (g/(1+exp(-g)))*u then lt_quant_q8's quantizer.  K % 32 == 0. */
+LT_API int lt_silu_mul_quant(lt_ctx* ctx, const float* g, const float* u, int8_t* xq, uint16_t* xd, int K);
+
+/* k_rmsnorm block_row over M rows of N (norm_softmax_from_facts.pl:83-108, launcher
+ * rms_norm_dev bpd/lib/dev_residency.py:746-781): 256-lane strided fma sum of squares,
+ * pairwise tree, inv = rsqrt(ss/N + eps), y = (x*inv)*w.  eps is an argument here
+ * (the reference bakes it into the cubin). */
+LT_API int lt_rmsnorm(lt_ctx* ctx, const float* x, const float* w, float* y, int M, int N, float eps);
+
+/* k_rms_quant (bpd/kernelgen/emitters/fused_rms_quant.pl:31-78, _launch_rms_quant
+ * bpd/lib/dev_residency.py:624-629): lt_rmsnorm of one row followed by lt_quant_q8,
+ * without writing the normalized row. */
+LT_API int lt_rmsnorm_quant(lt_ctx* ctx, const float* x, const float* w, int8_t* xq, uint16_t* xd,
+                     int N, float eps);
+
+/* Q8_0 GEMV, k_q8_0_gemv tiled_v4 / k_q8_0_gemv_addres tiled_v4_addres
+ * (q8_0_from_facts.pl:212-253, 374-416; launchers q8_linear_dev, q8_linear_add_residual_dev,
+ * q8_linear_dev_bias bpd/lib/dev_residency.py:905-1045, 1177-1193):
+ *   y[n] = canonical-order sum over blocks of fma(wd*xd, isum, .)  (+ resid[n] if non-null).
+ * resid doubles as the bias vector (the reference's bias fold).  K % 32 == 0. */
+LT_API int lt_q8_gemv(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd,
+               const float* resid, float* y, int N, int K);
+
+/* The vocab projection of the folded logits, q8_linear_dev_into on the lm_head
+ * (_compute_folded_logits, bpd/lib/dev_residency.py:1596-1623): the same arithmetic as
+ * lt_q8_gemv without a residual, compiled as its own kernel symbol so profiles separate
+ * the step's largest launch from the per-layer projections. */
+LT_API int lt_q8_gemv_logits(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd,
+                             float* y, int N, int K);
+
+/* Debug hook: per-(row, block) int32 dots isum[N][K/32] of the same kernel arithmetic. */
+LT_API int lt_q8_gemv_isums(lt_ctx* ctx, const void* W, const int8_t* xq, int32_t* isum, int N, int K);
+
+/* RoPE over nheads contiguous heads in place (k_rope, rope_from_facts.pl:40-69; fused q|k
+ * launcher rope_dev_qk_fused bpd/lib/dev_residency.py:722-741).  The position is read on
+ * the device from *pos (the cache length before the append, so the launch is capturable).
+ * freqs[hd/2] is the device inverse-frequency table from lt_rope_freqs (the reference
+ * evaluates powf(theta, -2j/hd) per thread; the table is that value rounded once). */
+LT_API int lt_rope_qk(lt_ctx* ctx, float* qk, const int* pos, int nheads, int hd, const float* freqs);
+
+/* Host helper, no GPU work: freqs[j] = theta^(-(2j)/hd), exponent formed in binary32. */
+LT_API int lt_rope_freqs(int hd, float theta, float* host_freqs);
+
+/* k_append_kv_incr (bpd/lib/dev_residency.py:303-315, DeviceKVCache.append_at_len_incr
+ * :508-521): kc[*len][:] = k, vc[*len][:] = v (width = nkv*hd elements), then *len += 1.
+ * kv_dtype LT_KV_F32 or LT_KV_F16 (fp16 RNE store).  maxt is the cache capacity in
+ * positions; a full cache (*len >= maxt) is left unchanged (the reference does not check). */
+LT_API int lt_kv_append_incr(lt_ctx* ctx, void* kc, const float* k, void* vc, const float* v,
+                      int* len, int width, int maxt, int kv_dtype);
+
+/* Decode attention over a position-major cache [t][nkv][hd] per sequence
+ * (k_attn_decode_masked bpd/lib/dev_residency.py:1955-2031; split-K design
+ * bpd/kernelgen/experimental/attn_decode_split.cu:14-91 with the declared order
+ * bpd/lib/ir_param_axes.pl:303-341).
+ *   q   [batch][nh*hd] fp32,  out [batch][nh*hd] fp32,
+ *   kc, vc  [batch][maxt][nkv*hd] (kv_dtype), len[batch] device ints (valid positions).
+ * nsplit == 1: the single-pass order of k_attn_decode_masked.  nsplit > 1: split-K with
+ * contiguous ceil(L/nsplit) ranges and an ascending-split combine.  The result does not
+ * depend on maxt.  ws must hold lt_attn_workspace_size(...) bytes (0 for nsplit == 1). */
+LT_API int lt_attn_decode(lt_ctx* ctx, const float* q, const void* kc, const void* vc, const int* len,
+                   float* out, int batch, int nh, int nkv, int hd, float scale, int maxt,
+                   int nsplit, int kv_dtype, void* ws, size_t ws_bytes);
+LT_API size_t lt_attn_workspace_size(int batch, int nh, int hd, int nsplit);
+
+/* Greedy argmax over n logits, ties to the lowest index (k_argmax_s1/_s2,
+ * bpd/lib/dev_residency.py:225-273, argmax_dev :1074-1110).  ws must hold
+ * lt_argmax_workspace_size() bytes.  out is a device int. */
+LT_API int lt_argmax(lt_ctx* ctx, const float* x, int n, int* out, void* ws, size_t ws_bytes);
+LT_API size_t lt_argmax_workspace_size(void);
+
+/* lt_argmax that also appends the winner to a device token history: hist[*count] = id,
+ * *count += 1 while *count < cap.  Lets a captured decode step be replayed back to back
+ * (greedy decoding needs no host round trip per token; the reference reads each id back,
+ * GraphRunner.replay_token bpd/lib/dev_residency.py:1795-1818). */
+LT_API int lt_argmax_record(lt_ctx* ctx, const float* x, int n, int* out, int* hist, int* count, int cap,
+                     void* ws, size_t ws_bytes);
+
+/* Embedding row of the device token id *tok from Q8_0 token_embd [vocab][E/32]:
+ * x = q*d (replaces the host gather emb.T[tok] + cuMemcpyHtoD into _RESID_IN,
+ * bpd/lib/dev_residency.py:1357-1358, 1806-1809).  Rejects *tok outside [0, vocab)
+ * by writing zeros and setting *err (device int, may be null) to 1. */
+LT_API int lt_embed_q8(lt_ctx* ctx, const void* emb, const int* tok, float* x, int E, int vocab, int* err);
+
+/* ---- graphs (replaces cuStreamBeginCapture/EndCapture/GraphInstantiate/GraphLaunch,
+ *      GraphRunner.capture / replay, bpd/lib/dev_residency.py:1732-1818) ---- */
+LT_API int lt_graph_begin(lt_ctx* ctx);
+LT_API int lt_graph_end(lt_ctx* ctx, lt_graph** out);
+LT_API int lt_graph_launch(lt_ctx* ctx, lt_graph* g);
+LT_API int lt_graph_free(lt_graph* g);
+
+/* ---- measurement: HIP events on the context's stream (replaces the reference's
+ *      time.time() around cuLaunchKernel loops, bpd/kernelgen/referee/gemv_sweep.py:69-85) ---- */
+LT_API int lt_event_create(lt_ctx* ctx, void** ev);
+LT_API int lt_event_record(lt_ctx* ctx, void* ev);
+LT_API int lt_event_elapsed_ms(void* start, void* stop, float* ms);
+LT_API int lt_event_destroy(void* ev);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LLAMATOV_HIP_H */

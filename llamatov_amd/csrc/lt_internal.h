@@ -1,0 +1,38 @@
+// lt_internal.h -- shared declarations of the libllamatov_hip.so translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/llamatov_hip.h"
+#include "lt_numerics.h"
+
+struct lt_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  bool capturing = false;
+  int num_cus = 0;
+};
+
+int lt_fail(int code, const char* fmt, ...);
+int lt_fail_hip(hipError_t e, const char* what, const char* file, int line);
+int lt_check_launch(const char* kernel);
+
+#define LT_CHECK(call)                                              \
+  do {                                                              \
+    hipError_t e_ = (call);                                         \
+    if (e_ != hipSuccess) return lt_fail_hip(e_, #call, __FILE__, __LINE__); \
+  } while (0)
+
+#define LT_REQUIRE(cond, ...)                                       \
+  do {                                                              \
+    if (!(cond)) return lt_fail(LT_EINVAL, __VA_ARGS__);            \
+  } while (0)
+
+static inline bool lt_aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Device helpers shared by the kernel translation units.
+__device__ __forceinline__ float lt_h2f(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}

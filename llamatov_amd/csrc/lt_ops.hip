@@ -1,0 +1,536 @@
+// lt_ops.hip -- gfx950 kernels and C-ABI launchers for the per-op Q8_0 decode path:
+// activation quant, SiLU*mul+quant, RMSNorm (+quant), Q8_0 GEMV (+residual/bias),
+// RoPE, KV append, embedding gather, argmax.
+//
+// Wave64 mapping of the reference's wave-32 orders: every order the reference defines
+// over 32 lanes (the GEMV's lanes(32) strided fold + shfl_down tree, the quant's
+// per-block amax) runs on one 32-lane half of a 64-lane wavefront, so two reference
+// warps share one CDNA wave and the per-lane arithmetic and the tree pairing are the
+// reference's.  Compile with -ffp-contract=off: every fma in this file is explicit.
+#include "lt_internal.h"
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// 16-byte vector with 4-byte alignment: global_load_dwordx4 needs only dword alignment.
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+constexpr int kBlockBytes = 34;
+
+// ---------------------------------------------------------------------------------
+// Byte fill (capturable replacement of a memset node).
+// ---------------------------------------------------------------------------------
+__global__ void k_fill_u8(uint8_t* dst, uint8_t v, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) dst[i] = v;
+}
+
+// ---------------------------------------------------------------------------------
+// Activation quant: one 32-lane half-wave per 32-element block, lane = element
+// (the warp-per-block k_quant_q8 of bpd/lib/dev_residency.py:867-886).  amax is a max
+// and hence order-free; d16 and q use the shared lt_numerics.h quantizer.
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ void quant_block_halfwave(float v, int lane, int8_t* xq_blk,
+                                                     uint16_t* xd_slot) {
+  float a = fabsf(v);
+#pragma unroll
+  for (int m = 16; m > 0; m >>= 1) a = fmaxf(a, __shfl_xor(a, m, 32));
+  uint16_t d16 = lt_q8_scale_bits(a);
+  if (lane == 0) *xd_slot = d16;
+  float dq = lt_h2f(d16);
+  xq_blk[lane] = (int8_t)lt_q8_quant1(v, dq);
+}
+
+__global__ __launch_bounds__(256) void k_quant_q8(const float* __restrict__ x,
+                                                  int8_t* __restrict__ xq,
+                                                  uint16_t* __restrict__ xd, int nb) {
+  int b = blockIdx.x * 8 + (threadIdx.x >> 5);
+  int lane = threadIdx.x & 31;
+  if (b >= nb) return;  // uniform per half-wave
+  float v = x[b * 32 + lane];
+  quant_block_halfwave(v, lane, xq + b * 32, xd + b);
+}
+
+__global__ __launch_bounds__(256) void k_silu_mul_quant(const float* __restrict__ g,
+                                                        const float* __restrict__ u,
+                                                        int8_t* __restrict__ xq,
+                                                        uint16_t* __restrict__ xd, int nb) {
+  int b = blockIdx.x * 8 + (threadIdx.x >> 5);
+  int lane = threadIdx.x & 31;
+  if (b >= nb) return;
+  int i = b * 32 + lane;
+  float v = lt_silu_mul(g[i], u[i]);
+  quant_block_halfwave(v, lane, xq + b * 32, xd + b);
+}
+
+// ---------------------------------------------------------------------------------
+// RMSNorm, order rms_ss lanes(256) strided + pairwise tree (norm_softmax_from_facts.pl:
+// 49, 83-108).  Thread t of the 256-thread block is reference lane t.  The tree's first
+// two levels (s = 128, 64) are formed explicitly from LDS by wave 0, the last six
+// (s = 32..1) by shuffle-down inside that wave; the pairing is the reference's.
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ float rms_inv_block256(const float* __restrict__ xr, int N, float eps,
+                                                  float* red /* LDS [256] */, float* sinv) {
+  const int t = threadIdx.x;
+  float p = 0.0f;
+  for (int j = t; j < N; j += 256) p = fmaf(xr[j], xr[j], p);
+  red[t] = p;
+  __syncthreads();
+  if (t < 64) {
+    float a = red[t] + red[t + 128];
+    float b = red[t + 64] + red[t + 192];
+    float c = a + b;
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) c = c + __shfl_down(c, s, 64);
+    if (t == 0) *sinv = lt_rsqrtf(c / (float)N + eps);
+  }
+  __syncthreads();
+  return *sinv;
+}
+
+__global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
+                                                 const float* __restrict__ w,
+                                                 float* __restrict__ y, int N, float eps) {
+  __shared__ float red[256];
+  __shared__ float sinv;
+  const float* xr = x + (size_t)blockIdx.x * N;
+  float* yr = y + (size_t)blockIdx.x * N;
+  float inv = rms_inv_block256(xr, N, eps, red, &sinv);
+  for (int j = threadIdx.x; j < N; j += 256) yr[j] = (xr[j] * inv) * w[j];
+}
+
+// k_rms_quant: normalize into LDS, then quantize each 32-block on a half-wave.
+__global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__ x,
+                                                       const float* __restrict__ w,
+                                                       int8_t* __restrict__ xq,
+                                                       uint16_t* __restrict__ xd, int N,
+                                                       float eps) {
+  extern __shared__ float ybuf[];  // [N]
+  __shared__ float red[256];
+  __shared__ float sinv;
+  float inv = rms_inv_block256(x, N, eps, red, &sinv);
+  for (int j = threadIdx.x; j < N; j += 256) ybuf[j] = (x[j] * inv) * w[j];
+  __syncthreads();
+  int lane = threadIdx.x & 31;
+  for (int b = threadIdx.x >> 5; b < N / 32; b += 8)
+    quant_block_halfwave(ybuf[b * 32 + lane], lane, xq + b * 32, xd + b);
+}
+
+// ---------------------------------------------------------------------------------
+// Q8_0 GEMV over native 34-byte GGUF blocks.
+//
+// One 32-lane half-wave per output row (reference warp = row, q8_0_from_facts.pl:
+// 212-253); lane L folds blocks b = L, L+32, ... in ascending order with
+// acc = fma(wd*xd, (float)isum, acc); the half-wave then merges with shuffle-down
+// s = 16, 8, 4, 2, 1.  Adjacent lanes read adjacent blocks, so a half-wave streams a
+// contiguous 1088-byte span of the row per step.
+//
+// A block starts at an even address.  Each lane loads the 9 aligned dwords that
+// cover its 34 bytes (dwordx4, dwordx4, dword) and re-aligns the 32 quant bytes with
+// v_perm_b32: byte offset 2 within the first dword for 4-aligned blocks, 4 for
+// 2-mod-4 blocks.  isum = 8 x v_dot4_i32_i8 (exact integer; order-free).
+// The activation (int8[K] + fp16[K/32]) is staged once per workgroup in LDS.
+// ---------------------------------------------------------------------------------
+struct BlockRegs {
+  uint32_t q[8];
+  uint16_t d;
+};
+
+// Block gi (global index row*nb + b) starts at byte 34*gi of the 4-aligned matrix, so
+// it is 4-aligned for even gi and 2 mod 4 for odd gi.  An even block's 9th dword ends 2
+// bytes past the block; for the matrix's final block (gi == last) those 2 bytes lie
+// outside the allocation, so that one block reads its last 2 bytes as a ushort.
+__device__ __forceinline__ void load_q8_block(const uint8_t* __restrict__ W, size_t gi, size_t last,
+                                              BlockRegs& r) {
+  const size_t off = gi * kBlockBytes;
+  const uint32_t* p = (const uint32_t*)(W + (off & ~(size_t)3));
+  const u32x4_a4 v0 = *(const u32x4_a4*)p;
+  const u32x4_a4 v1 = *(const u32x4_a4*)(p + 4);
+  const uint32_t w8 = (gi == last && !(gi & 1u)) ? (uint32_t)*(const uint16_t*)(W + off + 32) : p[8];
+  const uint32_t w[9] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, w8};
+  const bool odd = (gi & 1u) != 0;
+  const uint32_t sel = odd ? 0x07060504u : 0x05040302u;
+  r.d = odd ? (uint16_t)(w[0] >> 16) : (uint16_t)(w[0] & 0xFFFFu);
+#pragma unroll
+  for (int i = 0; i < 8; i++) r.q[i] = __builtin_amdgcn_perm(w[i + 1], w[i], sel);
+}
+
+__device__ __forceinline__ int dot_q8_block(const BlockRegs& r, const int8_t* sx /* LDS, 16B aligned */) {
+  u32x4 x0, x1;
+  __builtin_memcpy(&x0, sx, 16);
+  __builtin_memcpy(&x1, sx + 16, 16);
+  int s = 0;
+  s = __builtin_amdgcn_sdot4((int)r.q[0], (int)x0.x, s, false);
+  s = __builtin_amdgcn_sdot4((int)r.q[1], (int)x0.y, s, false);
+  s = __builtin_amdgcn_sdot4((int)r.q[2], (int)x0.z, s, false);
+  s = __builtin_amdgcn_sdot4((int)r.q[3], (int)x0.w, s, false);
+  s = __builtin_amdgcn_sdot4((int)r.q[4], (int)x1.x, s, false);
+  s = __builtin_amdgcn_sdot4((int)r.q[5], (int)x1.y, s, false);
+  s = __builtin_amdgcn_sdot4((int)r.q[6], (int)x1.z, s, false);
+  s = __builtin_amdgcn_sdot4((int)r.q[7], (int)x1.w, s, false);
+  return s;
+}
+
+__device__ __forceinline__ void stage_activation(const int8_t* __restrict__ xq,
+                                                 const uint16_t* __restrict__ xd, int K,
+                                                 uint8_t* smem) {
+  const u32x4* src = (const u32x4*)xq;
+  u32x4* dst = (u32x4*)smem;
+  for (int i = threadIdx.x; i < K / 16; i += blockDim.x) dst[i] = src[i];
+  uint16_t* sxd = (uint16_t*)(smem + K);
+  for (int i = threadIdx.x; i < K / 32; i += blockDim.x) sxd[i] = xd[i];
+  __syncthreads();
+}
+
+// The half-wave's row dot in the canonical order.  Returns the merged value on lane 0.
+__device__ __forceinline__ float q8_row_canonical(const uint8_t* __restrict__ W, int row, int nb,
+                                                  size_t last, const uint8_t* smem, int K, int lane) {
+  const size_t g0 = (size_t)row * nb;
+  const int8_t* sxq = (const int8_t*)smem;
+  const uint16_t* sxd = (const uint16_t*)(smem + K);
+  float acc = 0.0f;
+  int b = lane;
+  for (; b + 96 < nb; b += 128) {
+    BlockRegs r[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) load_q8_block(W, g0 + b + 32 * u, last, r[u]);
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      int bb = b + 32 * u;
+      int isum = dot_q8_block(r[u], sxq + bb * 32);
+      float wd = lt_h2f(r[u].d);
+      float xdv = lt_h2f(sxd[bb]);
+      acc = fmaf(wd * xdv, (float)isum, acc);
+    }
+  }
+  for (; b < nb; b += 32) {
+    BlockRegs r;
+    load_q8_block(W, g0 + b, last, r);
+    int isum = dot_q8_block(r, sxq + b * 32);
+    float wd = lt_h2f(r.d);
+    float xdv = lt_h2f(sxd[b]);
+    acc = fmaf(wd * xdv, (float)isum, acc);
+  }
+#pragma unroll
+  for (int s = 16; s > 0; s >>= 1) acc = acc + __shfl_down(acc, s, 32);
+  return acc;
+}
+
+// kRole only separates kernel symbols in profiles (0: per-layer projections, 1: logits).
+template <bool kResid, int kRole = 0>
+__global__ __launch_bounds__(256) void k_q8_gemv(const uint8_t* __restrict__ W,
+                                                 const int8_t* __restrict__ xq,
+                                                 const uint16_t* __restrict__ xd,
+                                                 const float* __restrict__ resid,
+                                                 float* __restrict__ y, int N, int K) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  stage_activation(xq, xd, K, smem);
+  const int lane = threadIdx.x & 31;
+  const int row = blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (row >= N) return;  // uniform per half-wave; no barrier follows
+  const int nb = K >> 5;
+  float acc = q8_row_canonical(W, row, nb, (size_t)N * nb - 1, smem, K, lane);
+  if (lane == 0) y[row] = kResid ? acc + resid[row] : acc;
+}
+
+__global__ __launch_bounds__(256) void k_q8_gemv_isums(const uint8_t* __restrict__ W,
+                                                       const int8_t* __restrict__ xq,
+                                                       int32_t* __restrict__ isum, int N, int K) {
+  const int nb = K >> 5;
+  const int lane = threadIdx.x & 31;
+  const int row = blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (row >= N) return;
+  for (int b = lane; b < nb; b += 32) {
+    BlockRegs r;
+    load_q8_block(W, (size_t)row * nb + b, (size_t)N * nb - 1, r);
+    u32x4 x0, x1;
+    __builtin_memcpy(&x0, xq + b * 32, 16);
+    __builtin_memcpy(&x1, xq + b * 32 + 16, 16);
+    int8_t tmp[32];
+    __builtin_memcpy(tmp, &x0, 16);
+    __builtin_memcpy(tmp + 16, &x1, 16);
+    isum[(size_t)row * nb + b] = dot_q8_block(r, tmp);
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// RoPE, NeoX half split (rope_from_facts.pl:40-69).  Thread per (head, j).
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_rope(float* __restrict__ x, const int* __restrict__ pos,
+                                              int nheads, int hd, const float* __restrict__ freqs) {
+  const int half = hd >> 1;
+  const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= nheads * half) return;
+  const int j = gid % half;
+  const int h = gid / half;
+  const float ang = (float)(*pos) * freqs[j];
+  float s, c;
+  lt_sincosf(ang, &s, &c);
+  float* base = x + (size_t)h * hd;
+  const float x1 = base[j], x2 = base[j + half];
+  base[j] = fmaf(x1, c, -(x2 * s));
+  base[j + half] = fmaf(x1, s, x2 * c);
+}
+
+// ---------------------------------------------------------------------------------
+// KV append at the device length then length += 1 (k_append_kv_incr,
+// bpd/lib/dev_residency.py:303-315).  One workgroup; the barrier orders every row write
+// before the increment.  A full cache (len >= maxt) is left untouched.
+// ---------------------------------------------------------------------------------
+template <bool kF16>
+__global__ __launch_bounds__(256) void k_kv_append_incr(void* __restrict__ kc,
+                                                        const float* __restrict__ k,
+                                                        void* __restrict__ vc,
+                                                        const float* __restrict__ v,
+                                                        int* __restrict__ len, int width, int maxt) {
+  const int L = *len;
+  if (L < 0 || L >= maxt) return;  // uniform: every thread reads the same L
+  for (int i = threadIdx.x; i < width; i += blockDim.x) {
+    size_t off = (size_t)L * width + i;
+    if (kF16) {
+      ((uint16_t*)kc)[off] = lt_float_to_half_bits(k[i]);
+      ((uint16_t*)vc)[off] = lt_float_to_half_bits(v[i]);
+    } else {
+      ((float*)kc)[off] = k[i];
+      ((float*)vc)[off] = v[i];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) *len = L + 1;
+}
+
+// ---------------------------------------------------------------------------------
+// Embedding gather from Q8_0 token_embd: x = q * d (exact in fp32).
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_embed_q8(const uint8_t* __restrict__ emb,
+                                                  const int* __restrict__ tok,
+                                                  float* __restrict__ x, int E, int vocab,
+                                                  int* __restrict__ err) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= E) return;
+  const int t = *tok;
+  if (t < 0 || t >= vocab) {
+    x[i] = 0.0f;
+    if (err && i == 0) *err = 1;
+    return;
+  }
+  const uint8_t* blk = emb + ((size_t)t * (E / 32) + (i >> 5)) * kBlockBytes;
+  const uint16_t d = (uint16_t)(blk[0] | (blk[1] << 8));
+  x[i] = (float)(int8_t)blk[2 + (i & 31)] * lt_h2f(d);
+}
+
+// ---------------------------------------------------------------------------------
+// Argmax, ties to the lowest index (k_argmax_s1/_s2, bpd/lib/dev_residency.py:225-273).
+// Stage 1: 256 workgroups over contiguous chunks; stage 2: one workgroup.
+// ---------------------------------------------------------------------------------
+constexpr int kArgmaxBlocks = 256;
+
+__device__ __forceinline__ bool am_better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+__device__ __forceinline__ void am_block_reduce(float& bv, int& bi, float* sv, int* si) {
+  // wave-level then LDS across the 4 waves
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) {
+    float ov = __shfl_xor(bv, m, 64);
+    int oi = __shfl_xor(bi, m, 64);
+    if (am_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { sv[w] = bv; si[w] = bi; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < 4; k++)
+      if (am_better(sv[k], si[k], bv, bi)) { bv = sv[k]; bi = si[k]; }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_argmax_s1(const float* __restrict__ x, int n,
+                                                   float* __restrict__ pval,
+                                                   int* __restrict__ pidx) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const long chunk = ((long)n + kArgmaxBlocks - 1) / kArgmaxBlocks;
+  const long lo = (long)blockIdx.x * chunk;
+  long hi = lo + chunk;
+  if (hi > n) hi = n;
+  float bv = -__builtin_inff();
+  int bi = 0x7FFFFFFF;
+  for (long i = lo + threadIdx.x; i < hi; i += 256) {
+    float v = x[i];
+    if (am_better(v, (int)i, bv, bi)) { bv = v; bi = (int)i; }
+  }
+  am_block_reduce(bv, bi, sv, si);
+  if (threadIdx.x == 0) { pval[blockIdx.x] = bv; pidx[blockIdx.x] = bi; }
+}
+
+// Stage 2 optionally appends the winner to a device token history (hist[*count] = id,
+// *count += 1, while *count < cap) so back-to-back graph replays keep every token.
+__global__ __launch_bounds__(256) void k_argmax_s2(const float* __restrict__ pval,
+                                                   const int* __restrict__ pidx,
+                                                   int* __restrict__ out, int* __restrict__ hist,
+                                                   int* __restrict__ count, int cap) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  float bv = pval[threadIdx.x];
+  int bi = pidx[threadIdx.x];
+  am_block_reduce(bv, bi, sv, si);
+  if (threadIdx.x == 0) {
+    *out = bi;
+    if (hist) {
+      const int c = *count;
+      if (c >= 0 && c < cap) {
+        hist[c] = bi;
+        *count = c + 1;
+      }
+    }
+  }
+}
+
+inline int grid_for(long n, int per) { return (int)((n + per - 1) / per); }
+
+}  // namespace
+
+extern "C" {
+
+int lt_fill_u8(lt_ctx* ctx, void* dst, uint8_t value, size_t nbytes) {
+  LT_REQUIRE(ctx && (dst || !nbytes), "lt_fill_u8: null argument");
+  if (!nbytes) return LT_OK;
+  int grid = (int)((nbytes + 255) / 256);
+  if (grid > 4096) grid = 4096;
+  k_fill_u8<<<grid, 256, 0, ctx->stream>>>((uint8_t*)dst, value, nbytes);
+  return lt_check_launch("k_fill_u8");
+}
+
+int lt_quant_q8(lt_ctx* ctx, const float* x, int8_t* xq, uint16_t* xd, int K) {
+  LT_REQUIRE(ctx && x && xq && xd, "lt_quant_q8: null argument");
+  LT_REQUIRE(K > 0 && K % 32 == 0, "lt_quant_q8: K=%d must be a positive multiple of 32", K);
+  int nb = K / 32;
+  k_quant_q8<<<grid_for(nb, 8), 256, 0, ctx->stream>>>(x, xq, xd, nb);
+  return lt_check_launch("k_quant_q8");
+}
+
+int lt_silu_mul_quant(lt_ctx* ctx, const float* g, const float* u, int8_t* xq, uint16_t* xd, int K) {
+  LT_REQUIRE(ctx && g && u && xq && xd, "lt_silu_mul_quant: null argument");
+  LT_REQUIRE(K > 0 && K % 32 == 0, "lt_silu_mul_quant: K=%d must be a positive multiple of 32", K);
+  int nb = K / 32;
+  k_silu_mul_quant<<<grid_for(nb, 8), 256, 0, ctx->stream>>>(g, u, xq, xd, nb);
+  return lt_check_launch("k_silu_mul_quant");
+}
+
+int lt_rmsnorm(lt_ctx* ctx, const float* x, const float* w, float* y, int M, int N, float eps) {
+  LT_REQUIRE(ctx && x && w && y, "lt_rmsnorm: null argument");
+  LT_REQUIRE(M > 0 && N > 0, "lt_rmsnorm: M=%d N=%d", M, N);
+  k_rmsnorm<<<M, 256, 0, ctx->stream>>>(x, w, y, N, eps);
+  return lt_check_launch("k_rmsnorm");
+}
+
+int lt_rmsnorm_quant(lt_ctx* ctx, const float* x, const float* w, int8_t* xq, uint16_t* xd, int N,
+                     float eps) {
+  LT_REQUIRE(ctx && x && w && xq && xd, "lt_rmsnorm_quant: null argument");
+  LT_REQUIRE(N > 0 && N % 32 == 0 && N <= 16384, "lt_rmsnorm_quant: N=%d (multiple of 32, <= 16384)", N);
+  k_rmsnorm_quant<<<1, 256, (size_t)N * sizeof(float), ctx->stream>>>(x, w, xq, xd, N, eps);
+  return lt_check_launch("k_rmsnorm_quant");
+}
+
+int lt_q8_gemv(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd, const float* resid,
+               float* y, int N, int K) {
+  LT_REQUIRE(ctx && W && xq && xd && y, "lt_q8_gemv: null argument");
+  LT_REQUIRE(N > 0 && K > 0 && K % 32 == 0 && K <= 32768, "lt_q8_gemv: N=%d K=%d (K multiple of 32, <= 32768)", N, K);
+  LT_REQUIRE(lt_aligned(W, 4), "lt_q8_gemv: W must be 4-byte aligned");
+  LT_REQUIRE(lt_aligned(xq, 16), "lt_q8_gemv: xq must be 16-byte aligned");
+  LT_REQUIRE(lt_aligned(xd, 2), "lt_q8_gemv: xd must be 2-byte aligned");
+  size_t shm = (size_t)K + (size_t)(K / 32) * 2;
+  int grid = grid_for(N, 8);
+  if (resid)
+    k_q8_gemv<true><<<grid, 256, shm, ctx->stream>>>((const uint8_t*)W, xq, xd, resid, y, N, K);
+  else
+    k_q8_gemv<false><<<grid, 256, shm, ctx->stream>>>((const uint8_t*)W, xq, xd, nullptr, y, N, K);
+  return lt_check_launch("k_q8_gemv");
+}
+
+int lt_q8_gemv_logits(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd, float* y,
+                      int N, int K) {
+  LT_REQUIRE(ctx && W && xq && xd && y, "lt_q8_gemv_logits: null argument");
+  LT_REQUIRE(N > 0 && K > 0 && K % 32 == 0 && K <= 32768, "lt_q8_gemv_logits: N=%d K=%d", N, K);
+  LT_REQUIRE(lt_aligned(W, 4) && lt_aligned(xq, 16) && lt_aligned(xd, 2), "lt_q8_gemv_logits: misaligned argument");
+  size_t shm = (size_t)K + (size_t)(K / 32) * 2;
+  k_q8_gemv<false, 1><<<grid_for(N, 8), 256, shm, ctx->stream>>>((const uint8_t*)W, xq, xd, nullptr, y, N, K);
+  return lt_check_launch("k_q8_gemv_logits");
+}
+
+int lt_q8_gemv_isums(lt_ctx* ctx, const void* W, const int8_t* xq, int32_t* isum, int N, int K) {
+  LT_REQUIRE(ctx && W && xq && isum, "lt_q8_gemv_isums: null argument");
+  LT_REQUIRE(N > 0 && K > 0 && K % 32 == 0, "lt_q8_gemv_isums: N=%d K=%d", N, K);
+  LT_REQUIRE(lt_aligned(W, 4) && lt_aligned(xq, 16), "lt_q8_gemv_isums: misaligned W or xq");
+  k_q8_gemv_isums<<<grid_for(N, 8), 256, 0, ctx->stream>>>((const uint8_t*)W, xq, isum, N, K);
+  return lt_check_launch("k_q8_gemv_isums");
+}
+
+int lt_rope_freqs(int hd, float theta, float* host_freqs) {
+  LT_REQUIRE(host_freqs && hd > 0 && hd % 2 == 0, "lt_rope_freqs: hd=%d", hd);
+  for (int j = 0; j < hd / 2; j++) {
+    float e = -(2.0f * (float)j) / (float)hd;
+    host_freqs[j] = (float)pow((double)theta, (double)e);
+  }
+  return LT_OK;
+}
+
+int lt_rope_qk(lt_ctx* ctx, float* qk, const int* pos, int nheads, int hd, const float* freqs) {
+  LT_REQUIRE(ctx && qk && pos && freqs, "lt_rope_qk: null argument");
+  LT_REQUIRE(nheads > 0 && hd > 0 && hd % 2 == 0, "lt_rope_qk: nheads=%d hd=%d", nheads, hd);
+  int total = nheads * (hd / 2);
+  k_rope<<<grid_for(total, 256), 256, 0, ctx->stream>>>(qk, pos, nheads, hd, freqs);
+  return lt_check_launch("k_rope");
+}
+
+int lt_kv_append_incr(lt_ctx* ctx, void* kc, const float* k, void* vc, const float* v, int* len,
+                      int width, int maxt, int kv_dtype) {
+  LT_REQUIRE(ctx && kc && k && vc && v && len, "lt_kv_append_incr: null argument");
+  LT_REQUIRE(width > 0 && maxt > 0, "lt_kv_append_incr: width=%d maxt=%d", width, maxt);
+  LT_REQUIRE(kv_dtype == LT_KV_F32 || kv_dtype == LT_KV_F16, "lt_kv_append_incr: kv_dtype=%d", kv_dtype);
+  if (kv_dtype == LT_KV_F16)
+    k_kv_append_incr<true><<<1, 256, 0, ctx->stream>>>(kc, k, vc, v, len, width, maxt);
+  else
+    k_kv_append_incr<false><<<1, 256, 0, ctx->stream>>>(kc, k, vc, v, len, width, maxt);
+  return lt_check_launch("k_kv_append_incr");
+}
+
+int lt_embed_q8(lt_ctx* ctx, const void* emb, const int* tok, float* x, int E, int vocab, int* err) {
+  LT_REQUIRE(ctx && emb && tok && x, "lt_embed_q8: null argument");
+  LT_REQUIRE(E > 0 && E % 32 == 0 && vocab > 0, "lt_embed_q8: E=%d vocab=%d", E, vocab);
+  k_embed_q8<<<grid_for(E, 256), 256, 0, ctx->stream>>>((const uint8_t*)emb, tok, x, E, vocab, err);
+  return lt_check_launch("k_embed_q8");
+}
+
+size_t lt_argmax_workspace_size(void) { return (size_t)kArgmaxBlocks * 8; }
+
+static int argmax_impl(lt_ctx* ctx, const float* x, int n, int* out, int* hist, int* count, int cap,
+                       void* ws, size_t ws_bytes) {
+  LT_REQUIRE(ctx && x && out && ws, "lt_argmax: null argument");
+  LT_REQUIRE(n > 0, "lt_argmax: n=%d must be > 0", n);
+  if (ws_bytes < lt_argmax_workspace_size())
+    return lt_fail(LT_ENOMEM, "lt_argmax: workspace %zu < %zu bytes", ws_bytes, lt_argmax_workspace_size());
+  LT_REQUIRE(lt_aligned(ws, 4), "lt_argmax: workspace must be 4-byte aligned");
+  float* pval = (float*)ws;
+  int* pidx = (int*)((char*)ws + kArgmaxBlocks * 4);
+  k_argmax_s1<<<kArgmaxBlocks, 256, 0, ctx->stream>>>(x, n, pval, pidx);
+  int rc = lt_check_launch("k_argmax_s1");
+  if (rc) return rc;
+  k_argmax_s2<<<1, 256, 0, ctx->stream>>>(pval, pidx, out, hist, count, cap);
+  return lt_check_launch("k_argmax_s2");
+}
+
+int lt_argmax(lt_ctx* ctx, const float* x, int n, int* out, void* ws, size_t ws_bytes) {
+  return argmax_impl(ctx, x, n, out, nullptr, nullptr, 0, ws, ws_bytes);
+}
+
+int lt_argmax_record(lt_ctx* ctx, const float* x, int n, int* out, int* hist, int* count, int cap,
+                     void* ws, size_t ws_bytes) {
+  LT_REQUIRE(hist && count && cap > 0, "lt_argmax_record: null history or cap=%d", cap);
+  return argmax_impl(ctx, x, n, out, hist, count, cap, ws, ws_bytes);
+}
+
+}  // extern "C"

@@ -1,0 +1,571 @@
+"""Device-resident Q8_0 decode on MI355X: the host surface of the reference's
+bpd/lib/dev_residency.py, driving libllamatov_hip.so through ctypes.
+
+Names mirror the reference so callers read the same:
+  DevTensor (dev_residency.py:387-415), DeviceKVCache (:418-541), rms_norm_dev (:746-781),
+  q8_linear_dev (:905-985), q8_linear_add_residual_dev (:988-1045), q8_linear_dev_bias
+  (:1177-1193), rope_dev_qk_fused (:722-741), attn_decode_from_cache_masked (:2016-2031),
+  argmax_dev (:1074-1110), forward_pass_resident (:1328-1593), GraphRunner (:1626-1818),
+  PRODUCTION_PROFILE / attest_profile / assert_certified_composition (:1209-1281).
+
+Design differences (MI355X-first; results are the same bits):
+  * Q8_0 weights are the GGUF 34-byte blocks, uploaded once at load (ResidentModel); the
+    reference dequantizes to fp32 on the host and re-quantizes at first use.
+  * Every buffer a decode step touches is allocated up front in a DecodePlan, so the
+    step is capturable without a slab arena and graph pointers never move.
+  * The token id lives on the device: the step gathers its embedding from the Q8_0
+    token_embd and the argmax writes the next id back into the same buffer, so greedy
+    decoding can replay the graph back to back with no host round trip per token.
+"""
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from ._lib import LT_KV_F16, LT_KV_F32, call
+from .model import ModelConfig, fused_layer_tensors
+
+
+# ----------------------------------------------------------------------------------
+# Device context and tensors
+# ----------------------------------------------------------------------------------
+class Device:
+    """One lt_ctx (one HIP device + one stream).  The reference's fact_dispatch._ctx()."""
+
+    def __init__(self, index: int = 0):
+        _lib.load()
+        h = ctypes.c_void_p()
+        call("lt_init", index, ctypes.byref(h))
+        self.handle = h
+        self.index = index
+        self.capturing = False
+
+    def malloc(self, nbytes: int) -> int:
+        p = ctypes.c_void_p()
+        call("lt_malloc", self.handle, ctypes.byref(p), max(int(nbytes), 1))
+        return int(p.value)
+
+    def free(self, ptr: int) -> None:
+        if ptr:
+            call("lt_free", self.handle, ctypes.c_void_p(ptr))
+
+    def h2d(self, ptr: int, arr: np.ndarray) -> None:
+        a = np.ascontiguousarray(arr)
+        call("lt_memcpy_h2d", self.handle, ctypes.c_void_p(ptr), a.ctypes.data_as(ctypes.c_void_p), a.nbytes)
+
+    def d2h(self, arr: np.ndarray, ptr: int) -> np.ndarray:
+        assert arr.flags.c_contiguous
+        call("lt_memcpy_d2h", self.handle, arr.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(ptr), arr.nbytes)
+        return arr
+
+    def d2d(self, dst: int, src: int, nbytes: int) -> None:
+        call("lt_memcpy_d2d", self.handle, ctypes.c_void_p(dst), ctypes.c_void_p(src), int(nbytes))
+
+    def fill(self, ptr: int, value: int, nbytes: int) -> None:
+        call("lt_fill_u8", self.handle, ctypes.c_void_p(ptr), value, int(nbytes))
+
+    def sync(self) -> None:
+        call("lt_sync", self.handle)
+
+
+_DEVICE: Device | None = None
+
+
+def get_device() -> Device:
+    global _DEVICE
+    if _DEVICE is None:
+        _DEVICE = Device(0)
+    return _DEVICE
+
+
+class DevTensor:
+    """A device buffer: raw pointer + shape + numpy dtype (reference DevTensor is fp32-only)."""
+    __slots__ = ("ptr", "shape", "dtype", "n", "nbytes", "_owns", "dev")
+
+    def __init__(self, ptr: int, shape, dtype=np.float32, owns: bool = True, dev: Device | None = None):
+        self.ptr = int(ptr)
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        self.n = int(np.prod(self.shape)) if self.shape else 1
+        self.nbytes = self.n * self.dtype.itemsize
+        self._owns = owns
+        self.dev = dev or get_device()
+
+    @staticmethod
+    def empty(shape, dtype=np.float32, dev: Device | None = None) -> "DevTensor":
+        dev = dev or get_device()
+        n = int(np.prod(shape)) if shape else 1
+        return DevTensor(dev.malloc(n * np.dtype(dtype).itemsize), shape, dtype, True, dev)
+
+    @staticmethod
+    def from_host(arr: np.ndarray, dev: Device | None = None) -> "DevTensor":
+        a = np.ascontiguousarray(arr)
+        t = DevTensor.empty(a.shape, a.dtype, dev)
+        t.dev.h2d(t.ptr, a)
+        return t
+
+    def view(self, offset_elems: int, shape, dtype=None) -> "DevTensor":
+        dt = np.dtype(dtype) if dtype is not None else self.dtype
+        return DevTensor(self.ptr + offset_elems * self.dtype.itemsize, shape, dt, False, self.dev)
+
+    def to_host(self) -> np.ndarray:
+        self.dev.sync()
+        out = np.empty(self.shape, self.dtype)
+        return self.dev.d2h(out, self.ptr)
+
+    def upload(self, arr: np.ndarray) -> None:
+        a = np.ascontiguousarray(arr, dtype=self.dtype)
+        if a.nbytes != self.nbytes:
+            raise ValueError(f"upload of {a.nbytes} bytes into a {self.nbytes}-byte tensor")
+        self.dev.h2d(self.ptr, a)
+
+    def free(self) -> None:
+        if self._owns and self.ptr:
+            self.dev.free(self.ptr)
+            self.ptr = 0
+
+    @property
+    def vp(self) -> ctypes.c_void_p:
+        return ctypes.c_void_p(self.ptr)
+
+
+def _vp(x) -> ctypes.c_void_p:
+    if x is None:
+        return ctypes.c_void_p(0)
+    if isinstance(x, DevTensor):
+        return x.vp
+    return ctypes.c_void_p(int(x))
+
+
+# ----------------------------------------------------------------------------------
+# Op launchers (thin mirrors of the reference op functions)
+# ----------------------------------------------------------------------------------
+class Q8Weight:
+    """A Q8_0 weight resident on the device as GGUF blocks [N][K/32]."""
+    __slots__ = ("t", "N", "K")
+
+    def __init__(self, blocks: np.ndarray, K: int, dev: Device | None = None):
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        N = blocks.shape[0]
+        if blocks.shape[1] != K // 32 * 34:
+            raise ValueError(f"Q8Weight: {blocks.shape} is not [N, {K // 32 * 34}]")
+        self.t = DevTensor.from_host(blocks, dev)
+        self.N, self.K = N, K
+
+
+def quant_q8_dev(x: DevTensor, xq: DevTensor, xd: DevTensor, K: int | None = None) -> None:
+    K = K or x.n
+    call("lt_quant_q8", x.dev.handle, x.vp, xq.vp, xd.vp, K)
+
+
+def rms_norm_dev(x: DevTensor, w: DevTensor, eps: float, out: DevTensor) -> DevTensor:
+    """k_rmsnorm block_row into `out` (reference rms_norm_dev / rms_norm_dev_into)."""
+    N = x.shape[-1]
+    M = x.n // N
+    call("lt_rmsnorm", x.dev.handle, x.vp, w.vp, out.vp, M, N, ctypes.c_float(eps))
+    return out
+
+
+def q8_gemv_dev(W: Q8Weight, xq: DevTensor, xd: DevTensor, out: DevTensor,
+                resid: DevTensor | None = None) -> DevTensor:
+    call("lt_q8_gemv", out.dev.handle, W.t.vp, xq.vp, xd.vp, _vp(resid), out.vp, W.N, W.K)
+    return out
+
+
+def q8_linear_dev(x: DevTensor, W: Q8Weight, out: DevTensor, xq: DevTensor, xd: DevTensor) -> DevTensor:
+    """quant + GEMV (reference q8_linear_dev / q8_linear_dev_into)."""
+    quant_q8_dev(x, xq, xd, W.K)
+    return q8_gemv_dev(W, xq, xd, out)
+
+
+def q8_linear_add_residual_dev(x: DevTensor, W: Q8Weight, resid: DevTensor, out: DevTensor,
+                               xq: DevTensor, xd: DevTensor, silu_src=None) -> DevTensor:
+    """quant (or SiLU*mul+quant when silu_src=(g, u)) + GEMV with the residual added at the
+    store (reference q8_linear_add_residual_dev, :988-1045)."""
+    if silu_src is not None:
+        g, u = silu_src
+        call("lt_silu_mul_quant", out.dev.handle, g.vp, u.vp, xq.vp, xd.vp, W.K)
+    else:
+        quant_q8_dev(x, xq, xd, W.K)
+    return q8_gemv_dev(W, xq, xd, out, resid)
+
+
+def q8_linear_dev_bias(x: DevTensor, W: Q8Weight, bias: DevTensor | None, out: DevTensor,
+                       xq: DevTensor, xd: DevTensor) -> DevTensor:
+    """Bias folded into the GEMV store (reference q8_linear_dev_bias, :1177-1193)."""
+    if bias is None:
+        return q8_linear_dev(x, W, out, xq, xd)
+    return q8_linear_add_residual_dev(x, W, bias, out, xq, xd)
+
+
+def rope_dev_qk_fused(qk: DevTensor, pos_ptr: int, nh: int, nkv: int, hd: int, freqs: DevTensor) -> None:
+    call("lt_rope_qk", qk.dev.handle, qk.vp, _vp(pos_ptr), nh + nkv, hd, freqs.vp)
+
+
+def attn_decode_from_cache_masked(q: DevTensor, cache: "DeviceKVCache", nh: int, scale: float,
+                                  len_ptr: int, out: DevTensor, nsplit: int = 1,
+                                  ws: DevTensor | None = None) -> DevTensor:
+    call("lt_attn_decode", q.dev.handle, q.vp, cache.k.vp, cache.v.vp, _vp(len_ptr), out.vp, 1, nh,
+         cache.nkv, cache.hd, ctypes.c_float(scale), cache.max_seq, nsplit, cache.kv_dtype,
+         _vp(ws), ws.nbytes if ws is not None else 0)
+    return out
+
+
+def argmax_dev(logits: DevTensor, n: int, out_ptr: int, ws: DevTensor) -> int:
+    if n <= 0:
+        raise ValueError(f"argmax_dev: n={n} (must be > 0)")
+    call("lt_argmax", logits.dev.handle, logits.vp, n, _vp(out_ptr), ws.vp, ws.nbytes)
+    return out_ptr
+
+
+def rope_freqs(hd: int, theta: float) -> np.ndarray:
+    f = np.empty(hd // 2, dtype=np.float32)
+    call("lt_rope_freqs", hd, ctypes.c_float(theta), f.ctypes.data_as(ctypes.c_void_p))
+    return f
+
+
+# ----------------------------------------------------------------------------------
+# KV cache
+# ----------------------------------------------------------------------------------
+class DeviceKVCache:
+    """Device KV cache for one layer: position-major [max_seq][nkv*hd] K and V and a device
+    int length (reference DeviceKVCache, bpd/lib/dev_residency.py:418-541).  kv_dtype
+    LT_KV_F32 (the reference's elem_bytes=4) or LT_KV_F16."""
+
+    def __init__(self, max_seq: int, nkv: int, hd: int, kv_dtype: int = LT_KV_F32,
+                 len_ptr: int | None = None, dev: Device | None = None):
+        self.dev = dev or get_device()
+        self.max_seq, self.nkv, self.hd = int(max_seq), int(nkv), int(hd)
+        self.width = self.nkv * self.hd
+        self.kv_dtype = kv_dtype
+        self.elem_bytes = 2 if kv_dtype == LT_KV_F16 else 4
+        dt = np.uint16 if kv_dtype == LT_KV_F16 else np.float32
+        self.k = DevTensor.empty((self.max_seq, self.width), dt, self.dev)
+        self.v = DevTensor.empty((self.max_seq, self.width), dt, self.dev)
+        self._len_owned = len_ptr is None
+        self.len_ptr = self.dev.malloc(4) if len_ptr is None else int(len_ptr)
+        self.length = 0
+        self.set_length(0)
+
+    def set_length(self, n: int) -> None:
+        self.length = int(n)
+        self.dev.h2d(self.len_ptr, np.array([n], dtype=np.int32))
+
+    def device_length(self) -> int:
+        out = np.zeros(1, np.int32)
+        self.dev.sync()
+        self.dev.d2h(out, self.len_ptr)
+        return int(out[0])
+
+    def append_at_len_incr(self, k: DevTensor, v: DevTensor) -> None:
+        call("lt_kv_append_incr", self.dev.handle, self.k.vp, k.vp, self.v.vp, v.vp,
+             _vp(self.len_ptr), self.width, self.max_seq, self.kv_dtype)
+
+    def rows_host(self, which: str, n: int | None = None) -> np.ndarray:
+        n = self.length if n is None else n
+        t = self.k if which == "k" else self.v
+        out = np.empty((self.max_seq, self.width), t.dtype)
+        self.dev.sync()
+        self.dev.d2h(out, t.ptr)
+        return out[:n]
+
+    def free(self) -> None:
+        self.k.free()
+        self.v.free()
+        if self._len_owned:
+            self.dev.free(self.len_ptr)
+
+
+# ----------------------------------------------------------------------------------
+# Production profile (a frozen config object instead of the reference's env flags)
+# ----------------------------------------------------------------------------------
+@dataclass(frozen=True)
+class Profile:
+    """The certified ensemble.  Every variant below is bit-identical to the reference's
+    per-op chain; the fields select kernels, not numerics, except attn_nsplit (> 1 selects
+    the split-K declared order) and kv_dtype."""
+    kv_dtype: int = LT_KV_F32
+    attn_nsplit: int = 1
+    fused_rms_quant: bool = False   # k_rms_quant instead of k_rmsnorm + k_quant_q8
+    graph: bool = True
+
+
+PRODUCTION_PROFILE = Profile()
+_CERTIFIED_NSPLIT = {1, 2, 4, 8, 16, 32, 64, 128}
+
+
+def attest_profile(p: Profile) -> dict:
+    return dataclasses.asdict(p)
+
+
+def assert_certified_composition(p: Profile) -> None:
+    """Refuse uncertified ensembles (reference dev_residency.py:1268-1281)."""
+    if p.kv_dtype not in (LT_KV_F32, LT_KV_F16):
+        raise RuntimeError(f"uncertified kv_dtype {p.kv_dtype}")
+    if p.attn_nsplit not in _CERTIFIED_NSPLIT:
+        raise RuntimeError(f"uncertified attn_nsplit {p.attn_nsplit}")
+
+
+# ----------------------------------------------------------------------------------
+# Resident model and the fixed-buffer decode plan
+# ----------------------------------------------------------------------------------
+class ResidentModel:
+    """All weights on the device, uploaded once: Q8_0 blocks verbatim, q|k|v and gate|up
+    concatenated at load (the reference concatenates at first use, dev_residency.py:1283-1326),
+    tied lm_head sharing token_embd's blocks."""
+
+    def __init__(self, cfg: ModelConfig, weights: dict, dev: Device | None = None):
+        self.cfg = cfg
+        self.dev = dev or get_device()
+        E, F = cfg.n_embd, cfg.n_ff
+        self.tok_embd = Q8Weight(weights["token_embd.weight"], E, self.dev)
+        self.output = self.tok_embd if cfg.tied else Q8Weight(weights["output.weight"], E, self.dev)
+        self.output_norm = DevTensor.from_host(weights["output_norm.weight"].astype(np.float32), self.dev)
+        self.layers = []
+        for il in range(cfg.n_layers):
+            t = fused_layer_tensors(cfg, weights, il)
+            self.layers.append({
+                "attn_norm": DevTensor.from_host(t["attn_norm"].astype(np.float32), self.dev),
+                "wqkv": Q8Weight(t["wqkv"], E, self.dev),
+                "bqkv": DevTensor.from_host(t["bqkv"], self.dev) if t["bqkv"] is not None else None,
+                "wo": Q8Weight(t["wo"], cfg.q_dim, self.dev),
+                "ffn_norm": DevTensor.from_host(t["ffn_norm"].astype(np.float32), self.dev),
+                "wgu": Q8Weight(t["wgu"], E, self.dev),
+                "wdown": Q8Weight(t["wdown"], F, self.dev),
+            })
+        self.freqs = DevTensor.from_host(rope_freqs(cfg.head_dim, cfg.rope_theta), self.dev)
+
+    def free(self) -> None:
+        self.tok_embd.t.free()
+        if self.output is not self.tok_embd:
+            self.output.t.free()
+        self.output_norm.free()
+        self.freqs.free()
+        for L in self.layers:
+            for v in L.values():
+                if isinstance(v, Q8Weight):
+                    v.t.free()
+                elif isinstance(v, DevTensor):
+                    v.free()
+
+
+class DecodePlan:
+    """Fixed device buffers and the launch sequence of one decode token."""
+
+    def __init__(self, model: ResidentModel, profile: Profile = PRODUCTION_PROFILE,
+                 max_ctx: int | None = None, hist_cap: int = 4096):
+        assert_certified_composition(profile)
+        self.model, self.cfg, self.profile = model, model.cfg, profile
+        self.dev = model.dev
+        cfg = self.cfg
+        E, F, hd = cfg.n_embd, cfg.n_ff, cfg.head_dim
+        self.max_ctx = int(max_ctx or cfg.max_ctx)
+        kmax = max(E, F, cfg.q_dim)
+        D = self.dev
+        self.tok = DevTensor.empty((1,), np.int32, D)
+        self.err = DevTensor.empty((1,), np.int32, D)
+        self.hist = DevTensor.empty((hist_cap,), np.int32, D)
+        self.hist_count = DevTensor.empty((1,), np.int32, D)
+        self.hist_cap = hist_cap
+        self.lens = DevTensor.empty((cfg.n_layers,), np.int32, D)
+        self.resid_in = DevTensor.empty((E,), np.float32, D)
+        self.carry = DevTensor.empty((E,), np.float32, D)
+        self.xres = DevTensor.empty((E,), np.float32, D)
+        self.h = DevTensor.empty((E,), np.float32, D)
+        self.qkv = DevTensor.empty((cfg.n_qkv,), np.float32, D)
+        self.att = DevTensor.empty((cfg.q_dim,), np.float32, D)
+        self.gu = DevTensor.empty((2 * F,), np.float32, D)
+        self.logits = DevTensor.empty((cfg.vocab,), np.float32, D)
+        self.xq = DevTensor.empty((kmax,), np.int8, D)
+        self.xd = DevTensor.empty((kmax // 32,), np.uint16, D)
+        ws_n = _lib.raw("lt_argmax_workspace_size")()
+        self.am_ws = DevTensor.empty((ws_n,), np.uint8, D)
+        aw = _lib.raw("lt_attn_workspace_size")(1, cfg.n_head, hd, profile.attn_nsplit)
+        self.attn_ws = DevTensor.empty((aw,), np.uint8, D) if aw else None
+        self.caches = [DeviceKVCache(self.max_ctx, cfg.n_head_kv, hd, profile.kv_dtype,
+                                     len_ptr=self.lens.ptr + 4 * il, dev=D)
+                       for il in range(cfg.n_layers)]
+        self.scale = float(hd ** -0.5)
+        self.reset()
+
+    # -- state --------------------------------------------------------------------
+    def reset(self) -> None:
+        """Empty caches (length 0), zero token history."""
+        self.dev.h2d(self.lens.ptr, np.zeros(self.cfg.n_layers, np.int32))
+        for c in self.caches:
+            c.length = 0
+        self.dev.h2d(self.hist_count.ptr, np.zeros(1, np.int32))
+        self.dev.h2d(self.err.ptr, np.zeros(1, np.int32))
+
+    def set_token(self, tok: int) -> None:
+        self.dev.h2d(self.tok.ptr, np.array([tok], np.int32))
+
+    def read_token(self) -> int:
+        out = np.zeros(1, np.int32)
+        self.dev.d2h(out, self.tok.ptr)
+        return int(out[0])
+
+    def read_logits(self) -> np.ndarray:
+        return self.logits.to_host()
+
+    def history_count(self) -> int:
+        out = np.zeros(1, np.int32)
+        self.dev.d2h(out, self.hist_count.ptr)
+        return int(out[0])
+
+    def history(self) -> list[int]:
+        n = self.history_count()
+        out = np.zeros(self.hist_cap, np.int32)
+        self.dev.d2h(out, self.hist.ptr)
+        return [int(t) for t in out[:n]]
+
+    def lengths(self) -> np.ndarray:
+        out = np.zeros(self.cfg.n_layers, np.int32)
+        self.dev.sync()
+        return self.dev.d2h(out, self.lens.ptr)
+
+    # -- the step ----------------------------------------------------------------
+    def enqueue_step(self) -> None:
+        """Launch one token: embed(tok) -> layers -> logits -> argmax -> tok.
+        The launch order is forward_pass_resident's fully-device branch
+        (bpd/lib/dev_residency.py:1365-1477) followed by _compute_folded_logits (:1596-1623)
+        and the device argmax of replay_token (:1795-1818)."""
+        cfg, m, p = self.cfg, self.model, self.profile
+        h = self.dev.handle
+        E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
+        eps = ctypes.c_float(cfg.norm_eps)
+        call("lt_embed_q8", h, m.tok_embd.t.vp, self.tok.vp, self.resid_in.vp, E, cfg.vocab, self.err.vp)
+        x = self.resid_in
+        for il, L in enumerate(m.layers):
+            cache = self.caches[il]
+            self._rms_quant(x, L["attn_norm"], E, eps)
+            q8_gemv_dev(L["wqkv"], self.xq, self.xd, self.qkv, L["bqkv"])
+            call("lt_rope_qk", h, self.qkv.vp, _vp(cache.len_ptr), nh + nkv, hd, m.freqs.vp)
+            k = self.qkv.view(cfg.q_dim, (cfg.kv_dim,))
+            v = self.qkv.view(cfg.q_dim + cfg.kv_dim, (cfg.kv_dim,))
+            cache.append_at_len_incr(k, v)
+            call("lt_attn_decode", h, self.qkv.vp, cache.k.vp, cache.v.vp, _vp(cache.len_ptr),
+                 self.att.vp, 1, nh, nkv, hd, ctypes.c_float(self.scale), cache.max_seq,
+                 p.attn_nsplit, p.kv_dtype, _vp(self.attn_ws),
+                 self.attn_ws.nbytes if self.attn_ws is not None else 0)
+            quant_q8_dev(self.att, self.xq, self.xd, cfg.q_dim)
+            q8_gemv_dev(L["wo"], self.xq, self.xd, self.xres, x)
+            self._rms_quant(self.xres, L["ffn_norm"], E, eps)
+            q8_gemv_dev(L["wgu"], self.xq, self.xd, self.gu)
+            g = self.gu.view(0, (F,))
+            u = self.gu.view(F, (F,))
+            call("lt_silu_mul_quant", h, g.vp, u.vp, self.xq.vp, self.xd.vp, F)
+            q8_gemv_dev(L["wdown"], self.xq, self.xd, self.carry, self.xres)
+            x = self.carry
+        self._rms_quant(x, m.output_norm, E, eps)
+        call("lt_q8_gemv_logits", h, m.output.t.vp, self.xq.vp, self.xd.vp, self.logits.vp,
+             m.output.N, m.output.K)
+        call("lt_argmax_record", h, self.logits.vp, cfg.vocab, self.tok.vp, self.hist.vp,
+             self.hist_count.vp, self.hist_cap, self.am_ws.vp, self.am_ws.nbytes)
+
+    def _rms_quant(self, x: DevTensor, w: DevTensor, E: int, eps) -> None:
+        h = self.dev.handle
+        if self.profile.fused_rms_quant:
+            call("lt_rmsnorm_quant", h, x.vp, w.vp, self.xq.vp, self.xd.vp, E, eps)
+        else:
+            call("lt_rmsnorm", h, x.vp, w.vp, self.h.vp, 1, E, eps)
+            call("lt_quant_q8", h, self.h.vp, self.xq.vp, self.xd.vp, E)
+
+    def step(self, tok: int | None = None) -> None:
+        """Eager step (tok=None: use the device token left by the previous argmax)."""
+        if tok is not None:
+            self.set_token(tok)
+        self.enqueue_step()
+        for c in self.caches:
+            c.length += 1
+
+    def free(self) -> None:
+        for c in self.caches:
+            c.free()
+        for t in (self.tok, self.err, self.hist, self.hist_count, self.lens, self.resid_in, self.carry,
+                  self.xres, self.h, self.qkv, self.att, self.gu, self.logits, self.xq, self.xd,
+                  self.am_ws, self.attn_ws):
+            if t is not None:
+                t.free()
+
+
+def forward_pass_resident(plan: DecodePlan, tokens) -> np.ndarray:
+    """Feed tokens one at a time through the single-token device path (the reference's
+    device-uniform prefill, dev_residency.py:1338-1356); return the last token's logits."""
+    toks = [int(t) for t in np.asarray(tokens).reshape(-1)]
+    for t in toks:
+        plan.step(t)
+    return plan.read_logits()
+
+
+class GraphRunner:
+    """Capture one decode step into a HIP graph and replay it per token
+    (reference GraphRunner, bpd/lib/dev_residency.py:1626-1818)."""
+
+    def __init__(self, plan: DecodePlan):
+        self.plan = plan
+        self.dev = plan.dev
+        self.graph = ctypes.c_void_p()
+        self.captured = False
+
+    def seed(self, prompt) -> np.ndarray:
+        """Eager prefill over the prompt (fixed buffers, all kernels loaded); returns the
+        last prompt token's logits.  The device token then holds the first greedy token."""
+        logits = forward_pass_resident(self.plan, prompt)
+        self.dev.sync()
+        return logits
+
+    def capture(self) -> None:
+        if self.captured:
+            raise RuntimeError("GraphRunner.capture: already captured")
+        call("lt_graph_begin", self.dev.handle)
+        try:
+            self.plan.enqueue_step()
+        except Exception:
+            g = ctypes.c_void_p()
+            _lib.raw("lt_graph_end")(self.dev.handle, ctypes.byref(g))
+            if g.value:
+                _lib.raw("lt_graph_free")(g)
+            raise
+        call("lt_graph_end", self.dev.handle, ctypes.byref(self.graph))
+        self.captured = True
+
+    def _launch(self) -> None:
+        if not self.captured:
+            raise RuntimeError("call capture() before replay")
+        call("lt_graph_launch", self.dev.handle, self.graph)
+        for c in self.plan.caches:
+            c.length += 1
+
+    def replay_logits(self, tok: int) -> np.ndarray:
+        self.plan.set_token(tok)
+        self._launch()
+        return self.plan.read_logits()
+
+    def replay_token(self, tok: int | None = None) -> int:
+        """One graph replay; returns the greedy next token (4 bytes cross to the host)."""
+        if tok is not None:
+            self.plan.set_token(tok)
+        self._launch()
+        return self.plan.read_token()
+
+    def replay_tokens(self, n: int) -> list[int]:
+        """n back-to-back replays continuing from the device token; the host reads the n
+        generated ids once at the end from the device history.  Same tokens as n calls of
+        replay_token()."""
+        start = self.plan.history_count()
+        if start + n > self.plan.hist_cap:
+            raise ValueError(f"token history capacity {self.plan.hist_cap} exceeded")
+        for _ in range(n):
+            self._launch()
+        return self.plan.history()[start:start + n]
+
+    def free(self) -> None:
+        if self.captured:
+            call("lt_graph_free", self.graph)
+            self.captured = False

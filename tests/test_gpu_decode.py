@@ -1,0 +1,146 @@
+"""Decode-level parity: the device decode step against the oracle's step, graph replay
+against eager (the reference's GR gate, gr_referee.py), prefill KV against incremental KV
+(A1, decode_referee.py), and greedy token identity (long_run_referee.py) at the
+BASELINE configuration 2 geometry."""
+import numpy as np
+import pytest
+
+from llamatov_amd import dev_residency as dr
+from llamatov_amd import model as M
+from llamatov_amd._lib import LT_KV_F16, LT_KV_F32
+
+pytestmark = pytest.mark.gpu
+
+
+def case(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+_WEIGHTS = {}
+
+
+def weights(cfg, seed=1234):
+    key = (cfg.name, seed)
+    if key not in _WEIGHTS:
+        _WEIGHTS[key] = M.synth_weights(cfg, seed)
+    return _WEIGHTS[key]
+
+
+_RESIDENT = {}
+
+
+def resident(cfg, gpu):
+    if cfg.name not in _RESIDENT:
+        _RESIDENT[cfg.name] = dr.ResidentModel(cfg, weights(cfg), gpu)
+    return _RESIDENT[cfg.name]
+
+
+def bitexact(a, b):
+    return np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
+
+
+@pytest.mark.parametrize("kv_dtype,nsplit,fused", [(LT_KV_F32, 1, False), (LT_KV_F16, 1, True),
+                                                   (LT_KV_F32, 4, True)])
+def test_tiny_stepwise_logits_bitexact(gpu, oracle, kv_dtype, nsplit, fused):
+    cfg = M.TINY
+    case(f"tiny stepwise kv={kv_dtype} nsplit={nsplit} fused={fused}")
+    prof = dr.Profile(kv_dtype=kv_dtype, attn_nsplit=nsplit, fused_rms_quant=fused)
+    plan = dr.DecodePlan(resident(cfg, gpu), prof)
+    orc = oracle.OracleModel(cfg, weights(cfg), kv_f16=kv_dtype == LT_KV_F16, attn_nsplit=nsplit)
+    toks = M.random_prompt(cfg, 6, seed=3)
+    for i in range(30):
+        t = toks[i] if i < len(toks) else int(np.argmax(exp))
+        plan.step(t)
+        got = plan.read_logits()
+        exp = orc.step(t)
+        assert bitexact(got, exp), f"step {i}: max |d| = {np.abs(got - exp).max()}"
+        assert plan.read_token() == oracle.argmax(exp)
+    assert list(plan.lengths()) == [30] * cfg.n_layers
+    for il in range(cfg.n_layers):
+        for which in "kv":
+            assert np.array_equal(plan.caches[il].rows_host(which, 30), orc.kv_rows(il, which, 30))
+    plan.free()
+
+
+def test_graph_replay_equals_eager(gpu):
+    """GR gate: graph replay is bit-identical to the eager step, device length advances,
+    and the token chain from replay_tokens equals replay_token one by one."""
+    cfg = M.TINY
+    case("tiny graph vs eager")
+    m = resident(cfg, gpu)
+    prompt = M.random_prompt(cfg, 5, seed=8)
+    eager = dr.DecodePlan(m)
+    graph = dr.DecodePlan(m)
+    dr.forward_pass_resident(eager, prompt)
+    gr = dr.GraphRunner(graph)
+    gr.seed(prompt)
+    gr.capture()
+    for i in range(12):
+        t = eager.read_token()
+        eager.step(t)
+        lg = gr.replay_logits(t)
+        assert bitexact(lg, eager.read_logits()), f"replay {i}"
+        assert list(graph.lengths()) == list(eager.lengths())
+    for il in range(cfg.n_layers):
+        n = int(eager.lengths()[il])
+        assert np.array_equal(graph.caches[il].rows_host("k", n), eager.caches[il].rows_host("k", n))
+    # back-to-back replays with the device-side token chain
+    seq1 = [gr.replay_token() for _ in range(8)]
+    ref = [eager.read_token()]
+    for _ in range(8):
+        eager.step(ref[-1])
+        ref.append(eager.read_token())
+    assert seq1 == ref[1:]
+    seq2 = gr.replay_tokens(8)
+    for t in seq2:
+        eager.step(eager.read_token())
+    assert seq2[-1] == eager.read_token()
+    gr.free()
+    eager.free()
+    graph.free()
+
+
+def test_prefill_kv_equals_incremental(gpu):
+    """A1: a fresh prefill over gen[:t] reproduces the incremental KV cache bit for bit."""
+    cfg = M.TINY
+    case("tiny A1")
+    m = resident(cfg, gpu)
+    prompt = M.random_prompt(cfg, 4, seed=9)
+    inc = dr.DecodePlan(m)
+    dr.forward_pass_resident(inc, prompt)
+    seq = list(prompt)
+    for _ in range(10):
+        seq.append(inc.read_token())
+        inc.step(seq[-1])
+    fresh = dr.DecodePlan(m)
+    lg = dr.forward_pass_resident(fresh, seq)
+    assert bitexact(lg, inc.read_logits())
+    for il in range(cfg.n_layers):
+        assert np.array_equal(fresh.caches[il].rows_host("k", len(seq)), inc.caches[il].rows_host("k", len(seq)))
+        assert np.array_equal(fresh.caches[il].rows_host("v", len(seq)), inc.caches[il].rows_host("v", len(seq)))
+    inc.free()
+    fresh.free()
+
+
+@pytest.mark.parametrize("cfg_name,n_prompt,n_gen,kv_dtype", [
+    ("small-qwen-arch", 32, 32, LT_KV_F32),
+    ("qwen2.5-0.5b-arch", 32, 128, LT_KV_F32),
+    ("qwen2.5-0.5b-arch", 32, 128, LT_KV_F16),
+])
+def test_greedy_tokens_identical(gpu, oracle, cfg_name, n_prompt, n_gen, kv_dtype):
+    """Greedy token identity with the oracle, through the captured graph."""
+    cfg = M.CONFIGS[cfg_name]
+    case(f"greedy {cfg_name} {n_prompt}+{n_gen} kv={kv_dtype}")
+    prompt = M.random_prompt(cfg, n_prompt, seed=7)
+    orc = oracle.OracleModel(cfg, weights(cfg), kv_f16=kv_dtype == LT_KV_F16)
+    exp, margins = orc.generate(prompt, n_gen)
+    plan = dr.DecodePlan(resident(cfg, gpu), dr.Profile(kv_dtype=kv_dtype))
+    gr = dr.GraphRunner(plan)
+    gr.seed(prompt)
+    first = plan.read_token()
+    gr.capture()
+    got = [first] + gr.replay_tokens(n_gen - 1)
+    print(f"[margins] min top1-top2 margin {float(margins.min()):.3e}", flush=True)
+    assert got == exp
+    gr.free()
+    plan.free()
