@@ -121,6 +121,9 @@ def main() -> int:
     ap.add_argument("--cpu-tokens", type=int, default=128, help="decode tokens in the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch the step's kernels directly instead of replaying the captured graph "
+                         "(same kernels; for profilers that cannot trace graph launches)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -150,7 +153,14 @@ def main() -> int:
     log("prefill (eager) + capture")
     runner.seed(prompt)
     first = plan.read_token()
-    runner.capture()
+    if not args.eager:
+        runner.capture()
+
+    def one_step():
+        if args.eager:
+            plan.step()
+        else:
+            runner._launch()
 
     def rewind():
         dev.h2d(plan.lens.ptr, np.full(cfg.n_layers, len(prompt), np.int32))
@@ -161,7 +171,8 @@ def main() -> int:
 
     # warmup: untimed replays from the post-prompt state
     log(f"warmup {args.warmup}")
-    runner.replay_tokens(args.warmup)
+    for _ in range(args.warmup):
+        one_step()
     dev.sync()
 
     # timed: K back-to-back replays from the post-prompt state (the C2 decode)
@@ -171,7 +182,7 @@ def main() -> int:
     t0 = time.perf_counter()
     ev.start()
     for _ in range(args.steps):
-        runner._launch()
+        one_step()
     gpu_ms = ev.stop_ms()
     dev.sync()
     wall = time.perf_counter() - t0
@@ -183,7 +194,8 @@ def main() -> int:
     t1 = time.perf_counter()
     sync_tokens = [first]
     for _ in range(args.steps):
-        sync_tokens.append(runner.replay_token())
+        one_step()
+        sync_tokens.append(plan.read_token())
     wall_sync = time.perf_counter() - t1
     ev.free()
 
@@ -215,6 +227,7 @@ def main() -> int:
         "decode_step_bytes": int(step_bytes),
         "decode_roofline_frac": round(step_bytes * tok_s / (HBM_PEAK_GBS * 1e9), 4),
         "tokens_consistent": tokens == sync_tokens,
+        "launch_mode": "eager" if args.eager else "graph",
     }
 
     if not args.no_roofline:
