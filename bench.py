@@ -60,36 +60,83 @@ class Events:
         self._lib.call("lt_event_destroy", self.b)
 
 
-def gemv_roofline(dev, w_embd: np.ndarray, N: int, K: int, launches: int = 60) -> dict:
-    """Time the logits GEMV kernel on rotated copies of the vocab matrix (>= 512 MB)."""
+def gemv_roofline(dev, w_embd: np.ndarray, N: int, K: int, eps: float, launches: int = 60) -> dict:
+    """The decode step's dominant kernel, the vocab projection (final RMSNorm -> quant ->
+    151936 x 896 Q8_0 GEMV; lt_q8_gemv_rms, the step's launch without its argmax epilogue),
+    timed with HIP events on the library's stream over rotated weight copies (>= 512 MB, so
+    the 256 MB Infinity Cache cannot serve it)."""
     from llamatov_amd import dev_residency as dr
     from llamatov_amd._lib import call
     blk_bytes = w_embd.nbytes
     copies = max(2, int(np.ceil(600e6 / blk_bytes)))
     ws = [dr.DevTensor.from_host(w_embd, dev) for _ in range(copies)]
     rng = np.random.default_rng(3)
-    xq = dr.DevTensor.from_host(rng.integers(-127, 128, K, dtype=np.int64).astype(np.int8), dev)
-    xd = dr.DevTensor.from_host((rng.standard_normal(K // 32) * 0.05).astype(np.float16).view(np.uint16), dev)
+    x = dr.DevTensor.from_host(rng.standard_normal(K).astype(np.float32), dev)
+    nw = dr.DevTensor.from_host(np.ones(K, np.float32), dev)
     y = dr.DevTensor.empty((N,), np.float32, dev)
+    e = ctypes.c_float(eps)
     for i in range(copies):  # warm the code path
-        call("lt_q8_gemv_logits", dev.handle, ws[i].vp, xq.vp, xd.vp, y.vp, N, K)
+        call("lt_q8_gemv_rms", dev.handle, x.vp, nw.vp, e, ws[i].vp, None, y.vp, N, K)
     dev.sync()
     ev = Events(dev)
     ev.start()
     for i in range(launches):
-        call("lt_q8_gemv_logits", dev.handle, ws[i % copies].vp, xq.vp, xd.vp, y.vp, N, K)
+        call("lt_q8_gemv_rms", dev.handle, x.vp, nw.vp, e, ws[i % copies].vp, None, y.vp, N, K)
     ms = ev.stop_ms()
     ev.free()
-    for t in ws + [xq, xd, y]:
+    for t in ws + [x, nw, y]:
         t.free()
     avg_s = ms / 1e3 / launches
-    alg_bytes = N * (K // 32) * 34 + K + (K // 32) * 2 + 4 * N
+    alg_bytes = N * (K // 32) * 34 + 8 * K + 4 * N
     achieved = alg_bytes / avg_s / 1e9
-    return {"kernel": "k_q8_gemv<false,1> (lt_q8_gemv_logits)", "shape": [N, K],
-            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+    return {"kernel": "k_gemv_fused<4, PRO_RMS, EPI_STORE, 4> (lt_q8_gemv_rms, vocab projection)",
+            "shape": [N, K], "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
             "bytes_per_launch": alg_bytes, "avg_launch_us": round(avg_s * 1e6, 3),
             "weight_copies": copies}
+
+
+GEMV_SWEEP = [("C1 ffn_up 0.5B", 4864, 896), ("C3 q/o 8B", 4096, 4096), ("C3 gate/up 8B", 14336, 4096),
+              ("C3 down 8B", 4096, 14336), ("C3 lm_head 8B", 128256, 4096), ("C2 lm_head 0.5B", 151936, 896)]
+
+
+def gemv_sweep(dev, launches: int = 40) -> list[dict]:
+    """Q8_0 GEMV bandwidth (BASELINE configs 1 and 3, plus the 0.5B vocab projection):
+    lt_q8_gemv on random blocks, rotating >= 600 MB of weight copies so the MALL cannot
+    serve them, timed with HIP events on the library's stream."""
+    from llamatov_amd import dev_residency as dr
+    from llamatov_amd._lib import call
+    out = []
+    rng = np.random.default_rng(5)
+    for name, N, K in GEMV_SWEEP:
+        nb = K // 32
+        blk = np.empty((N, nb, 34), np.uint8)
+        blk[..., 2:] = rng.integers(-127, 128, size=(N, nb, 32), dtype=np.int8).view(np.uint8)
+        blk[..., :2] = (rng.standard_normal((N, nb)) * 0.01).astype(np.float16).view(np.uint8).reshape(N, nb, 2)
+        wbytes = blk.nbytes
+        copies = max(2, int(np.ceil(600e6 / wbytes)))
+        ws = [dr.DevTensor.from_host(blk.reshape(N, nb * 34), dev) for _ in range(copies)]
+        del blk
+        xq = dr.DevTensor.from_host(rng.integers(-127, 128, K, dtype=np.int64).astype(np.int8), dev)
+        xd = dr.DevTensor.from_host((rng.standard_normal(nb) * 0.05).astype(np.float16).view(np.uint16), dev)
+        y = dr.DevTensor.empty((N,), np.float32, dev)
+        for i in range(copies):
+            call("lt_q8_gemv", dev.handle, ws[i].vp, xq.vp, xd.vp, None, y.vp, N, K)
+        dev.sync()
+        ev = Events(dev)
+        ev.start()
+        for i in range(launches):
+            call("lt_q8_gemv", dev.handle, ws[i % copies].vp, xq.vp, xd.vp, None, y.vp, N, K)
+        ms = ev.stop_ms()
+        ev.free()
+        for t in ws + [xq, xd, y]:
+            t.free()
+        avg = ms / 1e3 / launches
+        alg = N * nb * 34 + K + 2 * nb + 4 * N
+        out.append({"shape": f"{name} {N}x{K}", "us": round(avg * 1e6, 2), "GB/s": round(alg / avg / 1e9, 1),
+                    "frac": round(alg / avg / 1e9 / HBM_PEAK_GBS, 4)})
+        log(f"gemv {name} {N}x{K}: {avg * 1e6:.2f} us, {alg / avg / 1e9:.0f} GB/s")
+    return out
 
 
 def cpu_baseline(cfg, weights, prompt, n_decode: int, kv_f16: bool) -> tuple[dict, list[int]]:
@@ -121,6 +168,11 @@ def main() -> int:
     ap.add_argument("--cpu-tokens", type=int, default=128, help="decode tokens in the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--gemv-sweep", action="store_true",
+                    help="also time the Q8_0 GEMV on the BASELINE config 1/3 shapes (adds gemv_sweep)")
+    ap.add_argument("--per-op", action="store_true",
+                    help="thirteen per-op launches per layer (the reference's kernel-per-op chain) "
+                         "instead of the five fused launches")
     ap.add_argument("--eager", action="store_true",
                     help="launch the step's kernels directly instead of replaying the captured graph "
                          "(same kernels; for profilers that cannot trace graph launches)")
@@ -145,8 +197,8 @@ def main() -> int:
     w = M.synth_weights(cfg, seed=1234)
     log(f"weights ready in {time.perf_counter() - t0:.1f}s; uploading")
     dev = dr.get_device()
-    model = dr.ResidentModel(cfg, w, dev)
-    plan = dr.DecodePlan(model, dr.Profile(kv_dtype=kv_dtype), hist_cap=4096)
+    model = dr.ResidentModel(cfg, w, dev, layouts="per_op" if args.per_op else "fused")
+    plan = dr.DecodePlan(model, dr.Profile(kv_dtype=kv_dtype, fused_step=not args.per_op), hist_cap=4096)
     runner = dr.GraphRunner(plan)
     prompt = M.random_prompt(cfg, args.prompt, seed=7)
 
@@ -228,11 +280,16 @@ def main() -> int:
         "decode_roofline_frac": round(step_bytes * tok_s / (HBM_PEAK_GBS * 1e9), 4),
         "tokens_consistent": tokens == sync_tokens,
         "launch_mode": "eager" if args.eager else "graph",
+        "step_kernels": "per_op" if args.per_op else "fused",
     }
 
     if not args.no_roofline:
         log("GEMV roofline leg")
-        result["roofline"] = gemv_roofline(dev, w["token_embd.weight"], cfg.vocab, cfg.n_embd)
+        result["roofline"] = gemv_roofline(dev, w["token_embd.weight"], cfg.vocab, cfg.n_embd, cfg.norm_eps)
+
+    if args.gemv_sweep:
+        log("GEMV sweep")
+        result["gemv_sweep"] = gemv_sweep(dev)
 
     if not args.no_cpu_baseline:
         n_cpu = min(args.cpu_tokens, args.steps)

@@ -94,13 +94,6 @@ LT_API int lt_rmsnorm_quant(lt_ctx* ctx, const float* x, const float* w, int8_t*
 LT_API int lt_q8_gemv(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd,
                const float* resid, float* y, int N, int K);
 
-/* The vocab projection of the folded logits, q8_linear_dev_into on the lm_head
- * (_compute_folded_logits, bpd/lib/dev_residency.py:1596-1623): the same arithmetic as
- * lt_q8_gemv without a residual, compiled as its own kernel symbol so profiles separate
- * the step's largest launch from the per-layer projections. */
-LT_API int lt_q8_gemv_logits(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd,
-                             float* y, int N, int K);
-
 /* Debug hook: per-(row, block) int32 dots isum[N][K/32] of the same kernel arithmetic. */
 LT_API int lt_q8_gemv_isums(lt_ctx* ctx, const void* W, const int8_t* xq, int32_t* isum, int N, int K);
 
@@ -153,6 +146,76 @@ LT_API int lt_argmax_record(lt_ctx* ctx, const float* x, int n, int* out, int* h
  * bpd/lib/dev_residency.py:1357-1358, 1806-1809).  Rejects *tok outside [0, vocab)
  * by writing zeros and setting *err (device int, may be null) to 1. */
 LT_API int lt_embed_q8(lt_ctx* ctx, const void* emb, const int* tok, float* x, int E, int vocab, int* err);
+
+/* ---- fused decode-step launchers --------------------------------------------------------
+ * Each one is a chain of the reference's per-op launches fused into one kernel with the
+ * arithmetic of each op unchanged (every output bit equals the per-op chain's).  A replayed
+ * graph node costs ~1.5 us on MI355X, so the step uses five launches per layer instead of
+ * thirteen.  Every workgroup quantizes the activation into its own LDS (the prologue). */
+
+/* rms_norm_dev -> quant -> k_q8_0_gemv_addres: q8_linear_dev with rms_src
+ * (bpd/lib/dev_residency.py:905-985 with _launch_rms_quant :624-629, the QKV launch of
+ * forward_pass_resident :1380-1395 with the bias fold of q8_linear_dev_bias :1177-1193).
+ * y = Q8GEMV(W, quant(rmsnorm(x)*nw)) (+ resid[n] if non-null).  K % 32 == 0, K <= 16384. */
+LT_API int lt_q8_gemv_rms(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* W,
+                          const float* resid, float* y, int N, int K);
+
+/* lt_q8_gemv_rms on the embedding row of the device token *tok (Q8_0 token_embd
+ * [vocab][K/32]; replaces the host gather + cuMemcpyHtoD into _RESID_IN,
+ * bpd/lib/dev_residency.py:1357-1358, 1806-1809).  Workgroup 0 also stores the row into
+ * x_out (the layer's residual).  A token outside [0, vocab) gives a zero row and sets
+ * *err = 1 (err may be null).  K <= 8192. */
+LT_API int lt_q8_gemv_embed_rms(lt_ctx* ctx, const void* emb, const int* tok, int vocab, float* x_out,
+                                int* err, const float* nw, float eps, const void* W, const float* resid,
+                                float* y, int N, int K);
+
+/* quant -> GEMV (+resid): the reference's k_q8_0_gemv_qfused / tiled_v4_qfused
+ * (q8_0_from_facts.pl:316-365, dev_residency.py:914-930).  Used for the down projection
+ * on the SiLU*up vector written by lt_q8_gemv_rms_silu. */
+LT_API int lt_q8_gemv_quant(lt_ctx* ctx, const float* x, const void* W, const float* resid, float* y,
+                            int N, int K);
+
+/* O projection after lt_attn_step (q8_linear_add_residual_dev on the attention output,
+ * bpd/lib/dev_residency.py:1426-1440): GEMV (+resid) of the attention output, K = nh*hd.
+ * nsplit == 1: the input is the quantized attention output (xq, xd) lt_attn_step wrote.
+ * nsplit > 1: the split partials in ws are first merged in ascending split order
+ * (bpd/kernelgen/experimental/attn_decode_split.cu:37-91) and quantized.  If len is
+ * non-null, workgroup 0 then does *len += 1 (while *len < maxt): the length bump of
+ * k_append_kv_incr (:303-315), deferred to this launch because lt_attn_step's workgroups
+ * all read *len. */
+LT_API int lt_q8_gemv_attn_out(lt_ctx* ctx, const int8_t* xq, const uint16_t* xd, const void* ws, size_t ws_bytes,
+                               int nsplit, int nh, int hd, const void* W, const float* resid, float* y, int N,
+                               int K, int* len, int maxt);
+
+/* rms_norm_dev -> quant -> gate|up GEMV -> SiLU(g)*u -> quant (gateup_fused_dev +
+ * k_silu_mul_quant, bpd/lib/dev_residency.py:1321-1326, 573-604; tiled_v4_silu
+ * q8_0_from_facts.pl:423-464).  Wgu holds 2F rows INTERLEAVED: row 2j = gate row j,
+ * row 2j+1 = up row j.  v_j = (g_j / (1 + exp(-g_j))) * u_j is quantized like
+ * lt_quant_q8 into vq[F] / vd[F/32], the input of the down projection.  F % 32 == 0. */
+LT_API int lt_q8_gemv_rms_silu(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* Wgu,
+                               int8_t* vq, uint16_t* vd, int F, int K);
+
+/* Final norm -> quant -> vocab GEMV -> greedy argmax (_compute_folded_logits
+ * bpd/lib/dev_residency.py:1596-1623 + argmax_dev :1074-1110): writes logits[N], then the
+ * index of the maximum (ties to the lowest index) to *out, appending it to hist like
+ * lt_argmax_record when hist is non-null.  ws holds lt_q8_gemv_argmax_workspace_size(N). */
+LT_API int lt_q8_gemv_rms_argmax(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* W,
+                                 float* logits, int N, int K, int* out, int* hist, int* count, int cap,
+                                 void* ws, size_t ws_bytes);
+LT_API size_t lt_q8_gemv_argmax_workspace_size(int N);
+
+/* RoPE(q, k) -> KV append -> decode attention for one token of one sequence
+ * (rope_dev_qk_fused + DeviceKVCache.append_at_len_incr + attn_decode_from_cache_masked,
+ * bpd/lib/dev_residency.py:1396-1425).  qkv = [q (nh*hd) | k (nkv*hd) | v (nkv*hd)] before
+ * RoPE (bias included); the new token is position L = *len; K/V row L is written to the
+ * cache and attention runs over L+1 positions.  *len is not changed here (see
+ * lt_q8_gemv_attn_out).  nsplit == 1 writes the output fp32 into out[nh*hd] (if non-null)
+ * and quantized into xq[nh*hd] / xd[nh*hd/32] (if non-null; hd % 32 == 0); nsplit > 1
+ * writes split partials into ws (lt_attn_workspace_size(1, nh, hd, nsplit) bytes) for
+ * lt_q8_gemv_attn_out. */
+LT_API int lt_attn_step(lt_ctx* ctx, const float* qkv, const float* freqs, void* kc, void* vc, const int* len,
+                        float* out, int8_t* xq, uint16_t* xd, int nh, int nkv, int hd, float scale, int maxt,
+                        int nsplit, int kv_dtype, void* ws, size_t ws_bytes);
 
 /* ---- graphs (replaces cuStreamBeginCapture/EndCapture/GraphInstantiate/GraphLaunch,
  *      GraphRunner.capture / replay, bpd/lib/dev_residency.py:1732-1818) ---- */

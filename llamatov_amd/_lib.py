@@ -37,7 +37,6 @@ _SIGS = {
     "lt_rmsnorm": (c_int, [_P, _P, _P, _P, c_int, c_int, c_float]),
     "lt_rmsnorm_quant": (c_int, [_P, _P, _P, _P, _P, c_int, c_float]),
     "lt_q8_gemv": (c_int, [_P, _P, _P, _P, _P, _P, c_int, c_int]),
-    "lt_q8_gemv_logits": (c_int, [_P, _P, _P, _P, _P, c_int, c_int]),
     "lt_q8_gemv_isums": (c_int, [_P, _P, _P, _P, c_int, c_int]),
     "lt_rope_qk": (c_int, [_P, _P, _P, c_int, c_int, _P]),
     "lt_rope_freqs": (c_int, [c_int, c_float, _P]),
@@ -49,6 +48,17 @@ _SIGS = {
     "lt_argmax_workspace_size": (c_size_t, []),
     "lt_argmax_record": (c_int, [_P, _P, c_int, _P, _P, _P, c_int, _P, c_size_t]),
     "lt_embed_q8": (c_int, [_P, _P, _P, _P, c_int, c_int, _P]),
+    "lt_q8_gemv_rms": (c_int, [_P, _P, _P, c_float, _P, _P, _P, c_int, c_int]),
+    "lt_q8_gemv_embed_rms": (c_int, [_P, _P, _P, c_int, _P, _P, _P, c_float, _P, _P, _P, c_int, c_int]),
+    "lt_q8_gemv_quant": (c_int, [_P, _P, _P, _P, _P, c_int, c_int]),
+    "lt_q8_gemv_attn_out": (c_int, [_P, _P, _P, _P, c_size_t, c_int, c_int, c_int, _P, _P, _P, c_int, c_int,
+                                    _P, c_int]),
+    "lt_q8_gemv_rms_silu": (c_int, [_P, _P, _P, c_float, _P, _P, _P, c_int, c_int]),
+    "lt_q8_gemv_rms_argmax": (c_int, [_P, _P, _P, c_float, _P, _P, c_int, c_int, _P, _P, _P, c_int,
+                                      _P, c_size_t]),
+    "lt_q8_gemv_argmax_workspace_size": (c_size_t, [c_int]),
+    "lt_attn_step": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_float, c_int, c_int,
+                             c_int, _P, c_size_t]),
     "lt_graph_begin": (c_int, [_P]),
     "lt_graph_end": (c_int, [_P, POINTER(c_void_p)]),
     "lt_graph_launch": (c_int, [_P, _P]),

@@ -1,0 +1,1054 @@
+// lt_fused.hip -- the fused decode-step kernels of libllamatov_hip.so.
+//
+// A decode token on MI355X is bound by the fixed cost of each launch (a replayed graph
+// node costs ~1.5 us even when empty), so the step is cut to five launches per layer
+// instead of thirteen, each one a reference op chain fused without changing a bit:
+//
+//   lt_q8_gemv_rms / _embed_rms   rmsnorm -> quant -> QKV GEMV (+bias)
+//   lt_attn_step                  RoPE(q,k) -> KV append -> masked attention
+//   lt_q8_gemv_attn_out           split-K merge -> quant -> O GEMV (+x), length bump
+//   lt_q8_gemv_rms_silu           rmsnorm -> quant -> gate|up GEMV -> SiLU(g)*u
+//   lt_q8_gemv_quant              quant -> down GEMV (+xres)
+// and per token lt_q8_gemv_rms_argmax (final norm -> quant -> vocab GEMV -> argmax).
+//
+// Every workgroup of a fused GEMV builds the quantized activation itself, in LDS (the
+// prologue), before it streams its rows of the weight matrix; the prologue's inputs are
+// a few KB and stay in L2, so the redundancy costs far less than a launch.  The
+// weight loads of a workgroup's first rows are issued before the prologue, so the
+// prologue runs under their HBM latency.  The arithmetic of each stage is the per-op
+// kernel's (lt_ops.hip, lt_attn.hip) operation for operation.
+#include "lt_q8_device.h"
+
+#include <cstdlib>
+
+namespace {
+
+using namespace lt;
+
+enum Pro { PRO_STAGE = 0, PRO_QUANT = 1, PRO_RMS = 2, PRO_EMBED_RMS = 3, PRO_MERGE = 4 };
+enum Epi { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_ARGMAX = 3 };
+
+struct GemvParams {
+  const uint8_t* W;
+  int N, K;
+  // row mapping: half-wave hw of workgroup w takes rows w*row0 + hw + step*i, i < max_rows
+  int row0, step, max_rows;
+  // prologue sources
+  const float* x;          // PRO_QUANT / PRO_RMS input, PRO_MERGE single-split input
+  const float* nw;         // norm weight
+  float eps;
+  const int8_t* xq;        // PRO_STAGE
+  const uint16_t* xd;
+  const uint8_t* emb;      // PRO_EMBED_RMS: Q8_0 token_embd [vocab][K/32]
+  const int* tok;
+  int vocab;
+  float* x_out;            // PRO_EMBED_RMS: block 0 stores the embedding row here
+  int* err;
+  const float* wsm;        // PRO_MERGE split partials
+  const float* wsz;
+  const float* wso;
+  int nh, hd, nsplit;
+  int* len;                // PRO_MERGE: block 0 bumps *len (when < maxt)
+  int maxt;
+  // epilogue
+  const float* resid;      // EPI_RESID
+  float* y;
+  int8_t* yq;              // EPI_SILU: the quantized SiLU(g)*u vector
+  uint16_t* yd;
+  float* pval;             // EPI_ARGMAX per-workgroup partials
+  int* pidx;
+};
+
+constexpr int kThreads = 256;
+constexpr int kHalfWaves = kThreads / 32;
+constexpr int kResidPre = 4;   // residuals prefetched per half-wave
+constexpr int kSiluRows = 64;  // gate|up rows per workgroup: one 32-element quant block
+
+__device__ __forceinline__ bool am_better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+// ---- prologues: the quantized activation, written as per-block records in LDS ---------
+//
+// Each prologue leaves, for every 32-element block b, the activation record rec[b] that
+// fold_raw reads (both byte phases and the fp32 scale).  Its global inputs are loaded
+// before the weight loads are issued (loads complete in issue order, so the prologue never
+// waits behind the weights), and its arithmetic runs while the weights are in flight.
+
+// Quantize one 32-element block held one element per lane of a half-wave (k_quant_q8's
+// quantizer: d16 = fp16(amax/127), 1 if amax == 0; q = clamp(rint(v / float(d16)), +-127))
+// and write it into the block's record: byte l+2 of phase E and byte 44+l of phase O hold
+// q of element l; the other bytes of the two phases are zero; dwords 9 and 19 hold the
+// scale as fp32.
+__device__ __forceinline__ void quant_to_rec(float v, int lane, uint32_t* recw) {
+  const float a = halfwave_max(fabsf(v));
+  const uint16_t d16 = lt_q8_scale_bits(a);
+  const float dq = lt_h2f(d16);
+  const int8_t q = (int8_t)lt_q8_quant1(v, dq);
+  uint8_t* rb = (uint8_t*)recw;
+  rb[2 + lane] = (uint8_t)q;
+  rb[44 + lane] = (uint8_t)q;
+  if (lane == 0) {
+    ((uint16_t*)rb)[0] = 0;          // E bytes 0, 1
+    recw[kRecPhase] = 0u;            // O dword 0
+    recw[9] = __builtin_bit_cast(uint32_t, dq);
+    recw[kRecPhase + 9] = __builtin_bit_cast(uint32_t, dq);
+  }
+  if (lane == 31) ((uint16_t*)rb)[17] = 0;   // E bytes 34, 35
+}
+
+// Register slots: slot s of thread t holds element s*256 + t, so a slot's 32-element
+// block lives on one half-wave.
+template <int KS>
+struct Slots {
+  float x[KS];
+  float w[KS];
+};
+
+template <int KS>
+__device__ __forceinline__ void load_slots(const float* __restrict__ x, const float* __restrict__ w, int K,
+                                           Slots<KS>& S) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int s = 0; s < KS; s++) {
+    const int j = s * kThreads + t;
+    S.x[s] = j < K ? x[j] : 0.0f;
+    if (w) S.w[s] = j < K ? w[j] : 0.0f;
+  }
+}
+
+// Quantize the slots into records (optionally normalized: y = (x*inv)*w).
+template <int KS, bool kNorm>
+__device__ __forceinline__ void slots_to_rec(const Slots<KS>& S, float inv, int K, uint32_t* rec) {
+  const int t = threadIdx.x;
+  const int lane = t & 31;
+#pragma unroll
+  for (int s = 0; s < KS; s++) {
+    const int j0 = s * kThreads + (t & ~31);   // first element of this half-wave's block
+    if (j0 < K) {                              // uniform per half-wave (K % 32 == 0)
+      const float v = kNorm ? (S.x[s] * inv) * S.w[s] : S.x[s];
+      quant_to_rec(v, lane, rec + (j0 >> 5) * kRecDwords);
+    }
+  }
+}
+
+// rms_ss order (norm_softmax_from_facts.pl:49, 83-108): thread t folds x[t], x[t+256], ...
+// by fma, then the pairwise tree 128..1; inv = rsqrt(ss/N + eps).
+template <int KS>
+__device__ __forceinline__ float rms_inv(const Slots<KS>& S, int K, float eps, float* red, float* sinv) {
+  const int t = threadIdx.x;
+  float p = 0.0f;
+#pragma unroll
+  for (int s = 0; s < KS; s++)
+    if (s * kThreads + t < K) p = fmaf(S.x[s], S.x[s], p);
+  red[t] = p;
+  __syncthreads();
+  if (t < 64) {
+    float a = red[t] + red[t + 128];
+    float b = red[t + 64] + red[t + 192];
+    float c = a + b;
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) c = c + __shfl_down(c, s, 64);
+    if (t == 0) *sinv = lt_rsqrtf(c / (float)K + eps);
+  }
+  __syncthreads();
+  return *sinv;
+}
+
+// Split-K merge of the attention partials (the declared combine, ascending split order,
+// bpd/kernelgen/experimental/attn_decode_split.cu:37-91: M = max m_s, w_s = exp(m_s - M),
+// Z = sum fma(w_s, Z_s), O = sum fma(w_s, O_s), out = O/Z), then the quant.
+__device__ __forceinline__ void pro_merge_quant(const GemvParams& P, uint32_t* rec) {
+  const int lane = threadIdx.x & 31;
+  const int S = P.nsplit;
+  for (int b = threadIdx.x >> 5; b < P.K / 32; b += kHalfWaves) {
+    const int j = b * 32 + lane;
+    const int h = j / P.hd;
+    const int d = j - h * P.hd;
+    const float* m = P.wsm + (size_t)h * S;
+    const float* z = P.wsz + (size_t)h * S;
+    float M = -1e30f;
+    for (int s = 0; s < S; s++) M = fmaxf(M, m[s]);
+    float Z = 0.0f, acc = 0.0f;
+    for (int s = 0; s < S; s++) {
+      const float w = lt_expf(m[s] - M);
+      Z = fmaf(w, z[s], Z);
+      acc = fmaf(w, P.wso[((size_t)h * S + s) * P.hd + d], acc);
+    }
+    quant_to_rec(acc / Z, lane, rec + b * kRecDwords);
+  }
+}
+
+// Staged int8 quants + fp16 scales: copied through LDS, then laid out as records.
+constexpr int kStageChunks = 4;   // 16-byte chunks of xq per thread (K <= 16384)
+
+struct StageRegs {
+  u32x4 c[kStageChunks];
+  uint16_t d[2];
+};
+
+__device__ __forceinline__ void load_stage(const int8_t* __restrict__ xq, const uint16_t* __restrict__ xd,
+                                           int K, StageRegs& R) {
+  const u32x4* src = (const u32x4*)xq;
+#pragma unroll
+  for (int k = 0; k < kStageChunks; k++) {
+    const int i = threadIdx.x + kThreads * k;
+    if (i < K / 16) R.c[k] = src[i];
+  }
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int i = threadIdx.x + kThreads * k;
+    R.d[k] = i < K / 32 ? xd[i] : (uint16_t)0;
+  }
+}
+
+__device__ __forceinline__ void stage_to_rec(const StageRegs& R, int K, uint8_t* sxq, uint32_t* rec) {
+  u32x4* dst = (u32x4*)sxq;
+#pragma unroll
+  for (int k = 0; k < kStageChunks; k++) {
+    const int i = threadIdx.x + kThreads * k;
+    if (i < K / 16) dst[i] = R.c[k];
+  }
+  __syncthreads();
+  const uint32_t* X = (const uint32_t*)sxq;   // 8 dwords per block
+  const int nb = K >> 5;
+  for (int i = threadIdx.x; i < nb * 9; i += kThreads) {
+    const int b = i / 9;
+    const int j = i - b * 9;
+    uint32_t* r = rec + b * kRecDwords;
+    const uint32_t lo = j > 0 ? X[b * 8 + j - 1] : 0u;
+    const uint32_t hi = j < 8 ? X[b * 8 + j] : 0u;
+    r[j] = __builtin_amdgcn_perm(hi, lo, 0x05040302u);
+    r[kRecPhase + j] = lo;
+  }
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int b = threadIdx.x + kThreads * k;
+    if (b < nb) {
+      const uint32_t xdf = __builtin_bit_cast(uint32_t, lt_h2f(R.d[k]));
+      rec[b * kRecDwords + 9] = xdf;
+      rec[b * kRecDwords + kRecPhase + 9] = xdf;
+    }
+  }
+}
+
+// ---- the fused GEMV ----------------------------------------------------------------
+//
+// Half-wave hw (0..7) of workgroup w takes rows w*row0 + hw + step*i (i < max_rows): 8
+// contiguous rows per workgroup pass, or workgroups striding over groups of 8 rows.  Each
+// row is the canonical Q8_0 dot: lane L folds blocks L, L+32, ... by fma, then the 5-level
+// shfl_down tree (q8_0_from_facts.pl:466-516).
+//
+// A half-wave walks the flattened sequence of items (row i, block slot k), k < nk =
+// ceil(nb/32), lane L's block of item (i, k) being L + 32k.  It keeps D items in flight: a
+// ring of D block registers, each refilled with item m + D right after item m is folded,
+// so every lane streams D blocks ahead across row boundaries.  The weights are read with
+// buffer loads: items past the half-wave's last one get an out-of-range offset and read
+// zeros without touching memory, so the loop issues every load unconditionally (the
+// compiler's load counters stay exact and the loads pipeline).
+constexpr uint32_t kNoBlock = 0x80000000u;
+
+template <int KS, Pro PRO, Epi EPI, int D>
+__global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int K = P.K;
+  const int nb = K >> 5;
+  float* red = (float*)smem;                                  // [256] + sinv + pad
+  float* sinv = red + kThreads;
+  uint32_t* rec = (uint32_t*)(red + kThreads + 4);            // [nb][kRecDwords]
+  uint8_t* sxq = (uint8_t*)(rec + nb * kRecDwords);           // [K]: PRO_STAGE staging
+  float* xrow = (float*)(sxq + ((K + 15) & ~15));             // [K]: PRO_EMBED_RMS row
+  __shared__ float s_rows[kSiluRows];
+
+  const int hw = threadIdx.x >> 5;
+  const int lane = threadIdx.x & 31;
+
+  // (1) the prologue's global inputs
+  Slots<KS> S;
+  StageRegs SR;
+  int tok = 0;
+  if constexpr (PRO == PRO_RMS) load_slots<KS>(P.x, P.nw, K, S);
+  else if constexpr (PRO == PRO_QUANT) load_slots<KS>(P.x, nullptr, K, S);
+  else if constexpr (PRO == PRO_STAGE) load_stage(P.xq, P.xd, K, SR);
+  else if constexpr (PRO == PRO_MERGE) { if (P.nsplit == 1) load_stage(P.xq, P.xd, K, SR); }
+  else if constexpr (PRO == PRO_EMBED_RMS) tok = *P.tok;
+
+  // (2) the weights
+  const int rbase = blockIdx.x * P.row0 + hw;
+  const int step = P.step;
+  const int nk = (nb + 31) >> 5;
+  auto rows_from = [&](int r0) {
+    int n = P.N > r0 ? (P.N - r0 + step - 1) / step : 0;
+    return n < P.max_rows ? n : P.max_rows;
+  };
+  const int nrows = rows_from(rbase);
+  const int total = nrows * nk;
+  // the even half-wave of a wave has the most rows: its count makes the loop wave-uniform
+  const int trips = (rows_from(blockIdx.x * P.row0 + (hw & ~1)) * nk + D - 1) / D;
+  const uint32_t row_step_bytes = (uint32_t)step * (uint32_t)nb * (uint32_t)kBlockBytes;
+  constexpr uint32_t kSlotBytes = 32u * kBlockBytes;
+  const uint32_t lane_bytes = (uint32_t)lane * (uint32_t)kBlockBytes;
+  const uint32_t mat_bytes = (uint32_t)P.N * (uint32_t)nb * (uint32_t)kBlockBytes;
+  // the final even block's 9th dword reaches 2 bytes past the matrix: that dword starts
+  // inside it, so it lies in the same mapped page; its 2 extra bytes meet zero activations
+  const __amdgpu_buffer_rsrc_t wrsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)P.W, 0, (int)((mat_bytes + 3u) & ~3u), 0x00020000);
+
+  RawBlock ring[D];
+  int is = 0, ik = 0;                                                   // next item to issue
+  uint32_t issue_row = (uint32_t)rbase * (uint32_t)nb * (uint32_t)kBlockBytes;
+  auto issue = [&](RawBlock& r) {
+    const bool real = is < total && lane + 32 * ik < nb;
+    const uint32_t off = real ? issue_row + lane_bytes + (uint32_t)ik * kSlotBytes : kNoBlock;
+    const uint32_t o4 = off & ~3u;
+    const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)o4, 0, 0);
+    const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)(o4 + 16u), 0, 0);
+    r.w[0] = v0.x; r.w[1] = v0.y; r.w[2] = v0.z; r.w[3] = v0.w;
+    r.w[4] = v1.x; r.w[5] = v1.y; r.w[6] = v1.z; r.w[7] = v1.w;
+    r.w[8] = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)(o4 + 32u), 0, 0);
+    is++;
+    if (++ik == nk) { ik = 0; issue_row += row_step_bytes; }
+  };
+#pragma unroll
+  for (int d = 0; d < D; d++) issue(ring[d]);
+  // the epilogue's residuals, fetched with the weights
+  float rpre[kResidPre];
+  if constexpr (EPI == EPI_RESID) {
+#pragma unroll
+    for (int i = 0; i < kResidPre; i++) rpre[i] = (lane == 0 && i < nrows) ? P.resid[rbase + step * i] : 0.0f;
+  }
+
+  // (3) the prologue's arithmetic, under the weight loads
+  if constexpr (PRO == PRO_RMS) {
+    const float inv = rms_inv<KS>(S, K, P.eps, red, sinv);
+    slots_to_rec<KS, true>(S, inv, K, rec);
+  } else if constexpr (PRO == PRO_QUANT) {
+    slots_to_rec<KS, false>(S, 0.0f, K, rec);
+  } else if constexpr (PRO == PRO_STAGE) {
+    stage_to_rec(SR, K, sxq, rec);
+  } else if constexpr (PRO == PRO_MERGE) {
+    if (P.nsplit > 1) pro_merge_quant(P, rec);
+    else stage_to_rec(SR, K, sxq, rec);
+    if (P.len && blockIdx.x == 0 && threadIdx.x == 0) {
+      const int L = *P.len;
+      if (L >= 0 && L < P.maxt) *P.len = L + 1;
+    }
+  } else if constexpr (PRO == PRO_EMBED_RMS) {
+    // embedding row of the device token (x = q*d, exact); workgroup 0 keeps it as the
+    // layer's residual
+    const bool bad = tok < 0 || tok >= P.vocab;
+    for (int j = threadIdx.x; j < K; j += kThreads) {
+      float v = 0.0f;
+      if (!bad) {
+        const uint8_t* blk = P.emb + ((size_t)tok * (K / 32) + (j >> 5)) * kBlockBytes;
+        const uint16_t dd = (uint16_t)(blk[0] | (blk[1] << 8));
+        v = (float)(int8_t)blk[2 + (j & 31)] * lt_h2f(dd);
+      }
+      xrow[j] = v;
+      if (blockIdx.x == 0) P.x_out[j] = v;
+    }
+    if (bad && blockIdx.x == 0 && threadIdx.x == 0 && P.err) *P.err = 1;
+    __syncthreads();
+    load_slots<KS>(xrow, P.nw, K, S);
+    const float inv = rms_inv<KS>(S, K, P.eps, red, sinv);
+    slots_to_rec<KS, true>(S, inv, K, rec);
+  }
+  __syncthreads();
+
+  // (4) stream the rows
+  float bv = -__builtin_inff();
+  int bi = 0x7FFFFFFF;
+  float acc = 0.0f;
+  int fm = 0, fi = 0, fk = 0;         // item being folded: index, row, slot
+  uint32_t fold_row = (uint32_t)rbase * (uint32_t)nb * (uint32_t)kBlockBytes;
+  for (int t = 0; t < trips; t++) {
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+      const int b = lane + 32 * fk;
+      const bool odd = ((fold_row + lane_bytes + (uint32_t)fk * kSlotBytes) & 2u) != 0;
+      const float folded = fold_raw(ring[d], odd, rec + (b < nb ? b : 0) * kRecDwords, acc);
+      acc = (fm < total && b < nb) ? folded : acc;
+      issue(ring[d]);
+      fm++;
+      if (++fk == nk) {                 // row end: the same item for both half-waves
+        const float v = halfwave_tree_dpp(acc);   // the row value, on lane 0 of the half-wave
+        const int row = rbase + step * fi;
+        if (lane == 0 && fi < nrows) {
+          if constexpr (EPI == EPI_SILU) {
+            s_rows[row - blockIdx.x * kSiluRows] = v;
+          } else {
+            float o = v;
+            if constexpr (EPI == EPI_RESID) {
+              float rv = 0.0f;
+              if (fi < kResidPre) {
+#pragma unroll
+                for (int i = 0; i < kResidPre; i++)   // static indices keep rpre in registers
+                  if (fi == i) rv = rpre[i];
+              } else {
+                rv = P.resid[row];
+              }
+              o = v + rv;
+            }
+            P.y[row] = o;
+            if (EPI == EPI_ARGMAX && am_better(o, row, bv, bi)) { bv = o; bi = row; }
+          }
+        }
+        acc = 0.0f;
+        fk = 0;
+        fi++;
+        fold_row += row_step_bytes;
+      }
+    }
+  }
+
+  if constexpr (EPI == EPI_SILU) {
+    // the workgroup's 64 rows are the gate/up pairs of one 32-element block: SiLU(g)*u
+    // one pair per lane of half-wave 0, then k_silu_mul_quant's quantizer
+    __syncthreads();
+    if (hw == 0) {
+      const float v = lt_silu_mul(s_rows[2 * lane], s_rows[2 * lane + 1]);
+      quant_block_hw(v, lane, P.yq + blockIdx.x * 32, P.yd + blockIdx.x);
+    }
+  }
+  if constexpr (EPI == EPI_ARGMAX) {
+    __shared__ float sv[kHalfWaves];
+    __shared__ int si[kHalfWaves];
+    if (lane == 0) { sv[hw] = bv; si[hw] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float v = sv[0];
+      int ix = si[0];
+      for (int k = 1; k < kHalfWaves; k++)
+        if (am_better(sv[k], si[k], v, ix)) { v = sv[k]; ix = si[k]; }
+      P.pval[blockIdx.x] = v;
+      P.pidx[blockIdx.x] = ix;
+    }
+  }
+}
+
+// Reduce G argmax partials (ties to the lowest index) and publish the token; optionally
+// append it to the device history (hist[*count] = id, *count += 1 while < cap).  1024
+// threads; each issues all of its partial loads before comparing.
+constexpr int kFinThreads = 1024;
+constexpr int kFinPer = 8;   // partials per thread per round
+
+__global__ __launch_bounds__(kFinThreads) void k_argmax_finalize(const float* __restrict__ pval,
+                                                                 const int* __restrict__ pidx, int G,
+                                                                 int* __restrict__ out, int* __restrict__ hist,
+                                                                 int* __restrict__ count, int cap) {
+  __shared__ float sv[kFinThreads / 64];
+  __shared__ int si[kFinThreads / 64];
+  float bv = -__builtin_inff();
+  int bi = 0x7FFFFFFF;
+  for (int base = 0; base < G; base += kFinThreads * kFinPer) {
+    float v[kFinPer];
+    int ix[kFinPer];
+#pragma unroll
+    for (int k = 0; k < kFinPer; k++) {
+      const int i = base + k * kFinThreads + threadIdx.x;
+      v[k] = i < G ? pval[i] : -__builtin_inff();
+      ix[k] = i < G ? pidx[i] : 0x7FFFFFFF;
+    }
+#pragma unroll
+    for (int k = 0; k < kFinPer; k++)
+      if (am_better(v[k], ix[k], bv, bi)) { bv = v[k]; bi = ix[k]; }
+  }
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) {
+    const float ov = __shfl_xor(bv, m, 64);
+    const int oi = __shfl_xor(bi, m, 64);
+    if (am_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { sv[w] = bv; si[w] = bi; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < kFinThreads / 64; k++)
+      if (am_better(sv[k], si[k], bv, bi)) { bv = sv[k]; bi = si[k]; }
+    *out = bi;
+    if (hist) {
+      const int c = *count;
+      if (c >= 0 && c < cap) {
+        hist[c] = bi;
+        *count = c + 1;
+      }
+    }
+  }
+}
+
+// ---- fused RoPE + KV append + attention --------------------------------------------
+//
+// One workgroup per (split, group of HPW query heads sharing a KV head).  The new token
+// sits at position L = *len.  Every workgroup ropes its own q heads and the group's new
+// k row (rope_from_facts.pl:40-69, the arithmetic of k_rope), rounds k and v through
+// fp16 when the cache is fp16, and uses those values for position L directly; the one
+// workgroup with split 0 and the group's first head stores the row into the cache
+// (k_append_kv_incr, dev_residency.py:303-315).  Positions < L are read from the cache.
+// The attention arithmetic is lt_attn.hip's (the reference's masked single pass, or the
+// declared split-K partials when nsplit > 1).  V is staged through LDS in chunks so the
+// sequential per-dimension fma chains read LDS, not HBM.
+constexpr int kVChunkFloats = 8192;   // 32 KB of staged V per chunk
+
+template <bool kF16>
+__device__ __forceinline__ float kv_at(const void* base, size_t idx) {
+  return kF16 ? lt_h2f(((const uint16_t*)base)[idx]) : ((const float*)base)[idx];
+}
+
+template <bool kF16>
+__device__ __forceinline__ float kv_round(float v) {
+  return kF16 ? lt_half_to_float_bits(lt_float_to_half_bits(v)) : v;
+}
+
+template <bool kF16, int HPW>
+__global__ __launch_bounds__(256) void k_attn_step(
+    const float* __restrict__ qkv, const float* __restrict__ freqs, void* __restrict__ kc,
+    void* __restrict__ vc, const int* __restrict__ len, float* __restrict__ out,
+    int8_t* __restrict__ oq, uint16_t* __restrict__ od, float* __restrict__ wsm,
+    float* __restrict__ wsz, float* __restrict__ wso, int nh, int nkv, int hd, float scale, int maxt,
+    int nsplit, int per_max) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  float* sq = lds;                      // [HPW][hd] roped q
+  float* sk = sq + HPW * hd;            // [hd] new k (roped, cache-rounded)
+  float* sv = sk + hd;                  // [hd] new v (cache-rounded)
+  float* se = sv + hd;                  // [HPW][per_max] scores, then exps
+  float* svt = se + HPW * per_max;      // [kVChunkFloats] staged V (then the output)
+  __shared__ float s_mx[HPW];
+  __shared__ float s_z[HPW];
+
+  const int tid = threadIdx.x;
+  const int sp = blockIdx.x;
+  const int h0 = blockIdx.y * HPW;
+  const int rep = nh / nkv;
+  const int g = h0 / rep;
+  const int half = hd >> 1;
+  const int qd = nh * hd;
+  const int kvd = nkv * hd;
+  const size_t kvrow = (size_t)kvd;
+  constexpr int kEpu = kF16 ? 8 : 4;               // elements per 16-byte unit
+  constexpr int kUpt = kVChunkFloats / kEpu / 256;  // V units per thread per chunk
+  constexpr int kKU = HPW <= 2 ? 16 : 1;            // K units prefetched per thread (fp16, hd <= 128)
+  const int upr = hd / kEpu;                        // units per position row
+  const int cpos = kVChunkFloats / hd;              // positions per V chunk
+
+  // RoPE inputs do not depend on the length: load them first
+  const int nrope = (HPW + 1) * half;
+  float x1 = 0.0f, x2 = 0.0f, vnew = 0.0f, fr = 0.0f;
+  if (tid < nrope) {
+    const int r = tid / half;
+    const int j = tid - r * half;
+    const float* src = r < HPW ? qkv + (size_t)(h0 + r) * hd : qkv + qd + (size_t)g * hd;
+    x1 = src[j];
+    x2 = src[j + half];
+    fr = freqs[j];
+  }
+  if (tid < hd) vnew = qkv[qd + kvd + (size_t)g * hd + tid];
+
+  const int L = *len;
+  const bool valid = L >= 0 && L < maxt;
+  const int nctx = valid ? L + 1 : 0;
+  const int per = (nctx + nsplit - 1) / nsplit;
+  const int p0 = sp * per;
+  int p1 = p0 + per;
+  if (p1 > nctx) p1 = nctx;
+  const int n = p1 > p0 ? p1 - p0 : 0;
+  const size_t head_base = (size_t)p0 * kvrow + (size_t)g * hd;
+
+  // issue this thread's first K row and the first V chunk now, under the RoPE work
+  const bool kpre = kF16 && upr <= kKU && tid < n && p0 + tid != L;
+  u32x4 kraw[kKU];
+  if (kpre) {
+#pragma unroll
+    for (int u = 0; u < kKU; u++)
+      if (u < upr) __builtin_memcpy(&kraw[u], (const uint16_t*)kc + head_base + (size_t)tid * kvrow + u * kEpu, 16);
+  }
+  const int cn0 = n < cpos ? n : cpos;
+  u32x4 vraw[kUpt];
+#pragma unroll
+  for (int k = 0; k < kUpt; k++) {
+    const int u = tid + 256 * k;
+    const int t = u / upr;
+    if (t < cn0 && p0 + t != L) {
+      const size_t e = head_base + (size_t)t * kvrow + (size_t)(u - t * upr) * kEpu;
+      if (kF16) __builtin_memcpy(&vraw[k], (const uint16_t*)vc + e, 16);
+      else __builtin_memcpy(&vraw[k], (const float*)vc + e, 16);
+    }
+  }
+
+  // RoPE (the arithmetic of k_rope) of the q heads and of the group's k; v rounded
+  const float pos = (float)(valid ? L : 0);
+  for (int i = tid; i < nrope; i += 256) {
+    const int r = i / half;
+    const int j = i - r * half;
+    if (i != tid) {
+      const float* src = r < HPW ? qkv + (size_t)(h0 + r) * hd : qkv + qd + (size_t)g * hd;
+      x1 = src[j];
+      x2 = src[j + half];
+      fr = freqs[j];
+    }
+    float s, c;
+    lt_sincosf(pos * fr, &s, &c);
+    const float o1 = fmaf(x1, c, -(x2 * s));
+    const float o2 = fmaf(x1, s, x2 * c);
+    if (r < HPW) {
+      sq[r * hd + j] = o1;
+      sq[r * hd + j + half] = o2;
+    } else {
+      sk[j] = kv_round<kF16>(o1);
+      sk[j + half] = kv_round<kF16>(o2);
+    }
+  }
+  if (tid < hd) sv[tid] = kv_round<kF16>(vnew);
+  __syncthreads();
+
+  if (valid && sp == 0 && (h0 % rep) == 0 && tid < hd) {
+    const size_t off = (size_t)L * kvrow + (size_t)g * hd + tid;
+    if (kF16) {
+      ((uint16_t*)kc)[off] = lt_float_to_half_bits(sk[tid]);
+      ((uint16_t*)vc)[off] = lt_float_to_half_bits(sv[tid]);
+    } else {
+      ((float*)kc)[off] = sk[tid];
+      ((float*)vc)[off] = sv[tid];
+    }
+  }
+
+  // scores: thread per position, HPW sequential fma chains over i
+  for (int t = tid; t < n; t += 256) {
+    float acc[HPW];
+#pragma unroll
+    for (int r = 0; r < HPW; r++) acc[r] = 0.0f;
+    if (p0 + t == L) {
+      for (int i = 0; i < hd; i++) {
+        const float kv = sk[i];
+#pragma unroll
+        for (int r = 0; r < HPW; r++) acc[r] = fmaf(sq[r * hd + i], kv, acc[r]);
+      }
+    } else if (kpre && t == tid) {
+#pragma unroll
+      for (int u = 0; u < kKU; u++) {
+        if (u < upr) {
+          const uint32_t a[4] = {kraw[u].x, kraw[u].y, kraw[u].z, kraw[u].w};
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const float k0 = lt_h2f((uint16_t)(a[q] & 0xFFFFu));
+            const float k1 = lt_h2f((uint16_t)(a[q] >> 16));
+            const int i = u * 8 + 2 * q;
+#pragma unroll
+            for (int r = 0; r < HPW; r++) {
+              acc[r] = fmaf(sq[r * hd + i], k0, acc[r]);
+              acc[r] = fmaf(sq[r * hd + i + 1], k1, acc[r]);
+            }
+          }
+        }
+      }
+    } else {
+      const size_t rowi = head_base + (size_t)t * kvrow;
+      for (int i0 = 0; i0 < hd; i0 += 8) {
+        float kv[8];
+        if (kF16) {
+          u32x4 w;
+          __builtin_memcpy(&w, (const uint16_t*)kc + rowi + i0, 16);
+          const uint32_t a[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            kv[2 * q] = lt_h2f((uint16_t)(a[q] & 0xFFFFu));
+            kv[2 * q + 1] = lt_h2f((uint16_t)(a[q] >> 16));
+          }
+        } else {
+          u32x4 w0, w1;
+          __builtin_memcpy(&w0, (const float*)kc + rowi + i0, 16);
+          __builtin_memcpy(&w1, (const float*)kc + rowi + i0 + 4, 16);
+          const uint32_t a[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+          for (int q = 0; q < 8; q++) kv[q] = __builtin_bit_cast(float, a[q]);
+        }
+#pragma unroll
+        for (int ii = 0; ii < 8; ii++)
+#pragma unroll
+          for (int r = 0; r < HPW; r++) acc[r] = fmaf(sq[r * hd + i0 + ii], kv[ii], acc[r]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < HPW; r++) se[r * per_max + t] = acc[r] * scale;
+  }
+  __syncthreads();
+
+  const int wave = tid >> 6, wl = tid & 63;
+  for (int r = wave; r < HPW; r += 4) {
+    float m = -1e30f;
+    for (int t = wl; t < n; t += 64) m = fmaxf(m, se[r * per_max + t]);
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
+    if (wl == 0) s_mx[r] = m;
+  }
+  __syncthreads();
+  for (int r = 0; r < HPW; r++) {
+    const float m = s_mx[r];
+    for (int t = tid; t < n; t += 256) se[r * per_max + t] = lt_expf(se[r * per_max + t] - m);
+  }
+  __syncthreads();
+  for (int r = wave; r < HPW; r += 4) {
+    float ls = 0.0f;
+    for (int t = wl; t < n; t += 64) ls = ls + se[r * per_max + t];
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) ls = ls + __shfl_down(ls, s, 64);
+    if (wl == 0) s_z[r] = ls;
+  }
+
+  // O: thread per (head, dim); each a sequential fma chain over t, V staged in LDS in
+  // chunks of cpos positions (16-byte loads, all issued before the stores; chunk 0 was
+  // issued at the top)
+  const int nout = HPW * hd;
+  float acc0 = 0.0f, acc1 = 0.0f;   // thread handles outputs tid and tid + 256
+  for (int c0 = 0; c0 < n; c0 += cpos) {
+    const int cn = n - c0 < cpos ? n - c0 : cpos;
+    if (c0 > 0) {
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < kUpt; k++) {
+        const int u = tid + 256 * k;
+        const int t = u / upr;
+        if (t < cn && p0 + c0 + t != L) {
+          const size_t e = head_base + (size_t)(c0 + t) * kvrow + (size_t)(u - t * upr) * kEpu;
+          if (kF16) __builtin_memcpy(&vraw[k], (const uint16_t*)vc + e, 16);
+          else __builtin_memcpy(&vraw[k], (const float*)vc + e, 16);
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kUpt; k++) {
+      const int u = tid + 256 * k;
+      const int t = u / upr;
+      if (t < cn) {
+        const int c = u - t * upr;
+        float* dst = svt + t * hd + c * kEpu;
+        if (p0 + c0 + t == L) {
+#pragma unroll
+          for (int q = 0; q < kEpu; q++) dst[q] = sv[c * kEpu + q];
+        } else {
+          const uint32_t a[4] = {vraw[k].x, vraw[k].y, vraw[k].z, vraw[k].w};
+          if (kF16) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              dst[2 * q] = lt_h2f((uint16_t)(a[q] & 0xFFFFu));
+              dst[2 * q + 1] = lt_h2f((uint16_t)(a[q] >> 16));
+            }
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; q++) dst[q] = __builtin_bit_cast(float, a[q]);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    if (tid < nout) {
+      const int r = tid / hd, d = tid - r * hd;
+      const float* e = se + r * per_max + c0;
+      for (int t = 0; t < cn; t++) acc0 = fmaf(e[t], svt[t * hd + d], acc0);
+    }
+    if (tid + 256 < nout) {
+      const int o = tid + 256;
+      const int r = o / hd, d = o - r * hd;
+      const float* e = se + r * per_max + c0;
+      for (int t = 0; t < cn; t++) acc1 = fmaf(e[t], svt[t * hd + d], acc1);
+    }
+  }
+  __syncthreads();
+  for (int k = 0; k < 2; k++) {
+    const int o = tid + 256 * k;
+    if (o >= nout) break;
+    const int r = o / hd, d = o - r * hd;
+    const float a = k ? acc1 : acc0;
+    const int h = h0 + r;
+    if (nsplit == 1) {
+      const float v = valid ? a / s_z[r] : 0.0f;
+      if (out) out[(size_t)h * hd + d] = v;
+      svt[o] = v;
+    } else {
+      wso[((size_t)h * nsplit + sp) * hd + d] = a;
+    }
+  }
+  if (nsplit > 1 && tid < HPW) {
+    const int h = h0 + tid;
+    wsm[(size_t)h * nsplit + sp] = s_mx[tid];
+    wsz[(size_t)h * nsplit + sp] = s_z[tid];
+  }
+  if (nsplit == 1 && oq) {
+    // the workgroup's heads are whole 32-element blocks of the attention vector: quantize
+    // them for the O projection (k_quant_q8's quantizer)
+    __syncthreads();
+    const int lane = tid & 31;
+    const size_t o0 = (size_t)h0 * hd;
+    for (int b = tid >> 5; b < nout / 32; b += 8)
+      quant_block_hw(svt[b * 32 + lane], lane, oq + o0 + b * 32, od + (o0 >> 5) + b);
+  }
+}
+
+inline int grid_for(long n, int per) { return (int)((n + per - 1) / per); }
+
+// Row mapping.  The gate|up GEMV takes 64 contiguous rows per workgroup (one quant block
+// of its SiLU output).  Otherwise each workgroup takes one group of 8 rows when the groups
+// fit in one wave of resident workgroups; larger matrices get exactly one resident wave of
+// workgroups striding over the groups, so no tail wave is left (LT_GEMV_ROWS=R forces R
+// contiguous rows per workgroup, for tuning sweeps).
+int env_rows() {
+  static int env = -1;
+  if (env < 0) {
+    const char* s = getenv("LT_GEMV_ROWS");
+    env = s ? atoi(s) : 0;
+    if (env < 0 || env % 8) env = 0;
+  }
+  return env;
+}
+
+template <typename Kern>
+int resident_wgs(Kern kern, size_t shm, int num_cus) {
+  static size_t cached_shm[8];
+  static int cached_n[8];
+  static int used = 0;
+  for (int i = 0; i < used; i++)
+    if (cached_shm[i] == shm) return cached_n[i];
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, shm) != hipSuccess || per_cu < 1)
+    per_cu = 1;
+  const int n = per_cu * (num_cus > 0 ? num_cus : 1);
+  if (used < 8) { cached_shm[used] = shm; cached_n[used] = n; used++; }
+  return n;
+}
+
+template <int KS, Pro PRO, Epi EPI, int D>
+hipError_t launch_gemv_k(GemvParams P, size_t shm, hipStream_t st, int num_cus, int* grid_out) {
+  auto kern = k_gemv_fused<KS, PRO, EPI, D>;
+  const int groups = (P.N + 7) / 8;
+  int grid;
+  if (EPI == EPI_SILU) {
+    P.row0 = kSiluRows; P.step = 8; P.max_rows = kSiluRows / 8;
+    grid = P.N / kSiluRows;
+  } else if (env_rows() > 0) {
+    const int R = env_rows();
+    P.row0 = R; P.step = 8; P.max_rows = R / 8;
+    grid = (P.N + R - 1) / R;
+  } else {
+    const int cap = resident_wgs(kern, shm, num_cus);
+    if (groups <= cap) {
+      P.row0 = 8; P.step = 8; P.max_rows = 1;
+      grid = groups;
+    } else {
+      grid = cap;
+      P.row0 = 8; P.step = 8 * cap; P.max_rows = 0x7FFFFFFF;
+    }
+  }
+  if (grid_out) *grid_out = grid;
+  kern<<<grid, kThreads, shm, st>>>(P);
+  return hipGetLastError();
+}
+
+template <Pro PRO, Epi EPI>
+hipError_t launch_gemv(const GemvParams& P, lt_ctx* ctx, int* grid_out) {
+  const int nb = P.K / 32;
+  size_t shm = (kThreads + 4) * sizeof(float) + (size_t)nb * kRecDwords * 4;
+  if (PRO == PRO_STAGE || PRO == PRO_MERGE) shm += (size_t)((P.K + 15) & ~15);
+  if (PRO == PRO_EMBED_RMS) shm += (size_t)((P.K + 15) & ~15) + (size_t)P.K * sizeof(float);
+  hipStream_t st = ctx->stream;
+  const int ncu = ctx->num_cus;
+  if constexpr (PRO == PRO_STAGE) {
+    return launch_gemv_k<1, PRO, EPI, 8>(P, shm, st, ncu, grid_out);
+  } else {
+    if (P.K <= 1024) return launch_gemv_k<4, PRO, EPI, 8>(P, shm, st, ncu, grid_out);
+    if (P.K <= 4096) return launch_gemv_k<16, PRO, EPI, 8>(P, shm, st, ncu, grid_out);
+    return launch_gemv_k<64, PRO, EPI, 4>(P, shm, st, ncu, grid_out);
+  }
+}
+
+int check_gemv(const char* fn, const void* W, int N, int K) {
+  LT_REQUIRE(W, "%s: null weight", fn);
+  LT_REQUIRE(N > 0 && K > 0 && K % 32 == 0 && K <= 16384, "%s: N=%d K=%d (K multiple of 32, <= 16384)", fn, N, K);
+  LT_REQUIRE((uint64_t)N * (uint64_t)(K / 32) * 34u < ((uint64_t)1 << 32),
+             "%s: a %d x %d Q8_0 matrix must be below 4 GiB (split it by rows)", fn, N, K);
+  LT_REQUIRE(lt_aligned(W, 4), "%s: W must be 4-byte aligned", fn);
+  return LT_OK;
+}
+
+int finish(hipError_t e, const char* kernel) {
+  if (e != hipSuccess) return lt_fail_hip(e, kernel, __FILE__, __LINE__);
+  return LT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lt_q8_gemv(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd, const float* resid,
+               float* y, int N, int K) {
+  LT_REQUIRE(ctx && xq && xd && y, "lt_q8_gemv: null argument");
+  if (int rc = check_gemv("lt_q8_gemv", W, N, K)) return rc;
+  LT_REQUIRE(lt_aligned(xq, 16), "lt_q8_gemv: xq must be 16-byte aligned");
+  LT_REQUIRE(lt_aligned(xd, 2), "lt_q8_gemv: xd must be 2-byte aligned");
+  GemvParams P{};
+  P.W = (const uint8_t*)W; P.N = N; P.K = K; P.xq = xq; P.xd = xd; P.resid = resid; P.y = y;
+  hipError_t e = resid ? launch_gemv<PRO_STAGE, EPI_RESID>(P, ctx, nullptr)
+                       : launch_gemv<PRO_STAGE, EPI_STORE>(P, ctx, nullptr);
+  return finish(e, "k_gemv_fused<stage>");
+}
+
+int lt_q8_gemv_rms(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* W,
+                   const float* resid, float* y, int N, int K) {
+  LT_REQUIRE(ctx && x && nw && y, "lt_q8_gemv_rms: null argument");
+  if (int rc = check_gemv("lt_q8_gemv_rms", W, N, K)) return rc;
+  GemvParams P{};
+  P.W = (const uint8_t*)W; P.N = N; P.K = K; P.x = x; P.nw = nw; P.eps = eps; P.resid = resid; P.y = y;
+  hipError_t e = resid ? launch_gemv<PRO_RMS, EPI_RESID>(P, ctx, nullptr)
+                       : launch_gemv<PRO_RMS, EPI_STORE>(P, ctx, nullptr);
+  return finish(e, "k_gemv_fused<rms>");
+}
+
+int lt_q8_gemv_embed_rms(lt_ctx* ctx, const void* emb, const int* tok, int vocab, float* x_out, int* err,
+                         const float* nw, float eps, const void* W, const float* resid, float* y, int N, int K) {
+  LT_REQUIRE(ctx && emb && tok && x_out && nw && y, "lt_q8_gemv_embed_rms: null argument");
+  LT_REQUIRE(vocab > 0, "lt_q8_gemv_embed_rms: vocab=%d", vocab);
+  LT_REQUIRE(K <= 4096, "lt_q8_gemv_embed_rms: K=%d (<= 4096)", K);
+  if (int rc = check_gemv("lt_q8_gemv_embed_rms", W, N, K)) return rc;
+  GemvParams P{};
+  P.W = (const uint8_t*)W; P.N = N; P.K = K; P.emb = (const uint8_t*)emb; P.tok = tok; P.vocab = vocab;
+  P.x_out = x_out; P.err = err; P.nw = nw; P.eps = eps; P.resid = resid; P.y = y;
+  hipError_t e = resid ? launch_gemv<PRO_EMBED_RMS, EPI_RESID>(P, ctx, nullptr)
+                       : launch_gemv<PRO_EMBED_RMS, EPI_STORE>(P, ctx, nullptr);
+  return finish(e, "k_gemv_fused<embed_rms>");
+}
+
+int lt_q8_gemv_quant(lt_ctx* ctx, const float* x, const void* W, const float* resid, float* y, int N, int K) {
+  LT_REQUIRE(ctx && x && y, "lt_q8_gemv_quant: null argument");
+  if (int rc = check_gemv("lt_q8_gemv_quant", W, N, K)) return rc;
+  GemvParams P{};
+  P.W = (const uint8_t*)W; P.N = N; P.K = K; P.x = x; P.resid = resid; P.y = y;
+  hipError_t e = resid ? launch_gemv<PRO_QUANT, EPI_RESID>(P, ctx, nullptr)
+                       : launch_gemv<PRO_QUANT, EPI_STORE>(P, ctx, nullptr);
+  return finish(e, "k_gemv_fused<quant>");
+}
+
+int lt_q8_gemv_attn_out(lt_ctx* ctx, const int8_t* xq, const uint16_t* xd, const void* ws, size_t ws_bytes,
+                        int nsplit, int nh, int hd, const void* W, const float* resid, float* y, int N, int K,
+                        int* len, int maxt) {
+  LT_REQUIRE(ctx && y, "lt_q8_gemv_attn_out: null argument");
+  if (int rc = check_gemv("lt_q8_gemv_attn_out", W, N, K)) return rc;
+  LT_REQUIRE(nh > 0 && hd > 0 && nh * hd == K, "lt_q8_gemv_attn_out: nh*hd=%d*%d must equal K=%d", nh, hd, K);
+  LT_REQUIRE(nsplit >= 1, "lt_q8_gemv_attn_out: nsplit=%d", nsplit);
+  LT_REQUIRE(!len || maxt > 0, "lt_q8_gemv_attn_out: maxt=%d", maxt);
+  GemvParams P{};
+  P.W = (const uint8_t*)W; P.N = N; P.K = K; P.nsplit = nsplit; P.nh = nh; P.hd = hd;
+  P.resid = resid; P.y = y; P.len = len; P.maxt = maxt;
+  if (nsplit == 1) {
+    LT_REQUIRE(xq && xd && lt_aligned(xq, 16), "lt_q8_gemv_attn_out: nsplit=1 needs the quantized attention (xq 16-byte aligned)");
+    P.xq = xq;
+    P.xd = xd;
+  } else {
+    const size_t need = lt_attn_workspace_size(1, nh, hd, nsplit);
+    LT_REQUIRE(ws && lt_aligned(ws, 16), "lt_q8_gemv_attn_out: nsplit=%d needs a 16-byte aligned workspace", nsplit);
+    if (ws_bytes < need) return lt_fail(LT_ENOMEM, "lt_q8_gemv_attn_out: workspace %zu < %zu bytes", ws_bytes, need);
+    const size_t nrow = (size_t)nh * nsplit;
+    P.wsm = (const float*)ws;
+    P.wsz = P.wsm + nrow;
+    P.wso = (const float*)(((uintptr_t)(P.wsz + nrow) + 15) & ~(uintptr_t)15);
+  }
+  hipError_t e = resid ? launch_gemv<PRO_MERGE, EPI_RESID>(P, ctx, nullptr)
+                       : launch_gemv<PRO_MERGE, EPI_STORE>(P, ctx, nullptr);
+  return finish(e, "k_gemv_fused<merge>");
+}
+
+int lt_q8_gemv_rms_silu(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* Wgu, int8_t* vq,
+                        uint16_t* vd, int F, int K) {
+  LT_REQUIRE(ctx && x && nw && vq && vd, "lt_q8_gemv_rms_silu: null argument");
+  LT_REQUIRE(F > 0 && F % 32 == 0, "lt_q8_gemv_rms_silu: F=%d (multiple of 32)", F);
+  if (int rc = check_gemv("lt_q8_gemv_rms_silu", Wgu, 2 * F, K)) return rc;
+  GemvParams P{};
+  P.W = (const uint8_t*)Wgu; P.N = 2 * F; P.K = K; P.x = x; P.nw = nw; P.eps = eps; P.yq = vq; P.yd = vd;
+  return finish(launch_gemv<PRO_RMS, EPI_SILU>(P, ctx, nullptr), "k_gemv_fused<rms,silu>");
+}
+
+size_t lt_q8_gemv_argmax_workspace_size(int N) {
+  if (N <= 0) return 0;
+  const int env = env_rows();
+  const int G = grid_for(N, env > 0 ? env : 8);   // the most workgroups a launch can use
+  return (size_t)G * 8 + 64;
+}
+
+int lt_q8_gemv_rms_argmax(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* W,
+                          float* logits, int N, int K, int* out, int* hist, int* count, int cap,
+                          void* ws, size_t ws_bytes) {
+  LT_REQUIRE(ctx && x && nw && logits && out && ws, "lt_q8_gemv_rms_argmax: null argument");
+  LT_REQUIRE(!hist || (count && cap > 0), "lt_q8_gemv_rms_argmax: history needs count and cap > 0");
+  if (int rc = check_gemv("lt_q8_gemv_rms_argmax", W, N, K)) return rc;
+  const size_t need = lt_q8_gemv_argmax_workspace_size(N);
+  if (ws_bytes < need) return lt_fail(LT_ENOMEM, "lt_q8_gemv_rms_argmax: workspace %zu < %zu bytes", ws_bytes, need);
+  LT_REQUIRE(lt_aligned(ws, 4), "lt_q8_gemv_rms_argmax: workspace must be 4-byte aligned");
+  GemvParams P{};
+  P.W = (const uint8_t*)W; P.N = N; P.K = K; P.x = x; P.nw = nw; P.eps = eps; P.y = logits;
+  const int env = env_rows();
+  const int G = grid_for(N, env > 0 ? env : 8);
+  P.pval = (float*)ws;
+  P.pidx = (int*)((char*)ws + (size_t)G * 4);
+  int grid = 0;
+  if (int rc = finish(launch_gemv<PRO_RMS, EPI_ARGMAX>(P, ctx, &grid), "k_gemv_fused<rms,argmax>")) return rc;
+  k_argmax_finalize<<<1, kFinThreads, 0, ctx->stream>>>(P.pval, P.pidx, grid, out, hist, count, cap);
+  return lt_check_launch("k_argmax_finalize");
+}
+
+int lt_attn_step(lt_ctx* ctx, const float* qkv, const float* freqs, void* kc, void* vc, const int* len,
+                 float* out, int8_t* xq, uint16_t* xd, int nh, int nkv, int hd, float scale, int maxt, int nsplit,
+                 int kv_dtype, void* ws, size_t ws_bytes) {
+  LT_REQUIRE(ctx && qkv && freqs && kc && vc && len, "lt_attn_step: null argument");
+  LT_REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0, "lt_attn_step: nh=%d nkv=%d", nh, nkv);
+  LT_REQUIRE(hd > 0 && hd % 8 == 0 && hd <= 256, "lt_attn_step: hd=%d (multiple of 8, <= 256)", hd);
+  LT_REQUIRE(maxt > 0 && nsplit >= 1 && nsplit <= maxt, "lt_attn_step: maxt=%d nsplit=%d", maxt, nsplit);
+  LT_REQUIRE(kv_dtype == LT_KV_F32 || kv_dtype == LT_KV_F16, "lt_attn_step: kv_dtype=%d", kv_dtype);
+  LT_REQUIRE(lt_aligned(kc, 16) && lt_aligned(vc, 16), "lt_attn_step: K/V caches must be 16-byte aligned");
+  // Short caches are latency-bound: one head per workgroup keeps each thread's sequential
+  // chains short.  Large caches are bandwidth-bound: the heads of a KV group share one
+  // workgroup so every K/V row is read once.
+  const int rep = nh / nkv;
+  const size_t cache_bytes = (size_t)maxt * nkv * hd * (kv_dtype == LT_KV_F16 ? 2 : 4);
+  int hpw = 1;
+  if (cache_bytes > ((size_t)4 << 20))
+    for (int c : {8, 7, 4, 2})
+      if (rep % c == 0 && c * hd <= 512) { hpw = c; break; }
+  const int per_max = (maxt + nsplit - 1) / nsplit;
+  const size_t shm = ((size_t)hpw * hd + 2 * hd + (size_t)hpw * per_max + kVChunkFloats) * sizeof(float);
+  if (shm > 64 * 1024)
+    return lt_fail(LT_EINVAL, "lt_attn_step: %zu bytes of LDS for maxt=%d nsplit=%d; raise nsplit", shm, maxt, nsplit);
+  float *wsm = nullptr, *wsz = nullptr, *wso = nullptr;
+  if (nsplit == 1) {
+    LT_REQUIRE(out || xq, "lt_attn_step: nsplit=1 needs out or xq/xd");
+    LT_REQUIRE(!xq || (xd && hd % 32 == 0), "lt_attn_step: quantized output needs xd and hd %% 32 == 0");
+  } else {
+    const size_t need = lt_attn_workspace_size(1, nh, hd, nsplit);
+    LT_REQUIRE(ws && lt_aligned(ws, 16), "lt_attn_step: nsplit=%d needs a 16-byte aligned workspace", nsplit);
+    if (ws_bytes < need) return lt_fail(LT_ENOMEM, "lt_attn_step: workspace %zu < %zu bytes", ws_bytes, need);
+    const size_t nrow = (size_t)nh * nsplit;
+    wsm = (float*)ws;
+    wsz = wsm + nrow;
+    wso = (float*)(((uintptr_t)(wsz + nrow) + 15) & ~(uintptr_t)15);
+  }
+  dim3 grid(nsplit, nh / hpw);
+  const bool f16 = kv_dtype == LT_KV_F16;
+#define LT_STEP_CASE(H)                                                                                   \
+  case H:                                                                                                 \
+    if (f16) k_attn_step<true, H><<<grid, 256, shm, ctx->stream>>>(qkv, freqs, kc, vc, len, out, xq, xd,   \
+                                                                  wsm, wsz, wso, nh, nkv, hd, scale, maxt, \
+                                                                  nsplit, per_max);                        \
+    else k_attn_step<false, H><<<grid, 256, shm, ctx->stream>>>(qkv, freqs, kc, vc, len, out, xq, xd,     \
+                                                               wsm, wsz, wso, nh, nkv, hd, scale, maxt,    \
+                                                               nsplit, per_max);                           \
+    break;
+  switch (hpw) {
+    LT_STEP_CASE(1)
+    LT_STEP_CASE(2)
+    LT_STEP_CASE(4)
+    LT_STEP_CASE(7)
+    LT_STEP_CASE(8)
+    default:
+      return lt_fail(LT_EINVAL, "lt_attn_step: unsupported heads per workgroup %d", hpw);
+  }
+#undef LT_STEP_CASE
+  return lt_check_launch("k_attn_step");
+}
+
+}  // extern "C"

@@ -7,15 +7,11 @@
 // per-block amax) runs on one 32-lane half of a 64-lane wavefront, so two reference
 // warps share one CDNA wave and the per-lane arithmetic and the tree pairing are the
 // reference's.  Compile with -ffp-contract=off: every fma in this file is explicit.
-#include "lt_internal.h"
+#include "lt_q8_device.h"
 
 namespace {
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-// 16-byte vector with 4-byte alignment: global_load_dwordx4 needs only dword alignment.
-typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
-
-constexpr int kBlockBytes = 34;
+using namespace lt;
 
 // ---------------------------------------------------------------------------------
 // Byte fill (capturable replacement of a memset node).
@@ -31,17 +27,6 @@ __global__ void k_fill_u8(uint8_t* dst, uint8_t v, size_t n) {
 // (the warp-per-block k_quant_q8 of bpd/lib/dev_residency.py:867-886).  amax is a max
 // and hence order-free; d16 and q use the shared lt_numerics.h quantizer.
 // ---------------------------------------------------------------------------------
-__device__ __forceinline__ void quant_block_halfwave(float v, int lane, int8_t* xq_blk,
-                                                     uint16_t* xd_slot) {
-  float a = fabsf(v);
-#pragma unroll
-  for (int m = 16; m > 0; m >>= 1) a = fmaxf(a, __shfl_xor(a, m, 32));
-  uint16_t d16 = lt_q8_scale_bits(a);
-  if (lane == 0) *xd_slot = d16;
-  float dq = lt_h2f(d16);
-  xq_blk[lane] = (int8_t)lt_q8_quant1(v, dq);
-}
-
 __global__ __launch_bounds__(256) void k_quant_q8(const float* __restrict__ x,
                                                   int8_t* __restrict__ xq,
                                                   uint16_t* __restrict__ xd, int nb) {
@@ -49,7 +34,7 @@ __global__ __launch_bounds__(256) void k_quant_q8(const float* __restrict__ x,
   int lane = threadIdx.x & 31;
   if (b >= nb) return;  // uniform per half-wave
   float v = x[b * 32 + lane];
-  quant_block_halfwave(v, lane, xq + b * 32, xd + b);
+  quant_block_hw(v, lane, xq + b * 32, xd + b);
 }
 
 __global__ __launch_bounds__(256) void k_silu_mul_quant(const float* __restrict__ g,
@@ -61,7 +46,7 @@ __global__ __launch_bounds__(256) void k_silu_mul_quant(const float* __restrict_
   if (b >= nb) return;
   int i = b * 32 + lane;
   float v = lt_silu_mul(g[i], u[i]);
-  quant_block_halfwave(v, lane, xq + b * 32, xd + b);
+  quant_block_hw(v, lane, xq + b * 32, xd + b);
 }
 
 // ---------------------------------------------------------------------------------
@@ -114,126 +99,13 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__
   __syncthreads();
   int lane = threadIdx.x & 31;
   for (int b = threadIdx.x >> 5; b < N / 32; b += 8)
-    quant_block_halfwave(ybuf[b * 32 + lane], lane, xq + b * 32, xd + b);
+    quant_block_hw(ybuf[b * 32 + lane], lane, xq + b * 32, xd + b);
 }
 
 // ---------------------------------------------------------------------------------
-// Q8_0 GEMV over native 34-byte GGUF blocks.
-//
-// One 32-lane half-wave per output row (reference warp = row, q8_0_from_facts.pl:
-// 212-253); lane L folds blocks b = L, L+32, ... in ascending order with
-// acc = fma(wd*xd, (float)isum, acc); the half-wave then merges with shuffle-down
-// s = 16, 8, 4, 2, 1.  Adjacent lanes read adjacent blocks, so a half-wave streams a
-// contiguous 1088-byte span of the row per step.
-//
-// A block starts at an even address.  Each lane loads the 9 aligned dwords that
-// cover its 34 bytes (dwordx4, dwordx4, dword) and re-aligns the 32 quant bytes with
-// v_perm_b32: byte offset 2 within the first dword for 4-aligned blocks, 4 for
-// 2-mod-4 blocks.  isum = 8 x v_dot4_i32_i8 (exact integer; order-free).
-// The activation (int8[K] + fp16[K/32]) is staged once per workgroup in LDS.
+// Per-(row, block) int32 dots of the GEMV arithmetic (a debug hook; the GEMV itself is
+// k_gemv_fused in lt_fused.hip).
 // ---------------------------------------------------------------------------------
-struct BlockRegs {
-  uint32_t q[8];
-  uint16_t d;
-};
-
-// Block gi (global index row*nb + b) starts at byte 34*gi of the 4-aligned matrix, so
-// it is 4-aligned for even gi and 2 mod 4 for odd gi.  An even block's 9th dword ends 2
-// bytes past the block; for the matrix's final block (gi == last) those 2 bytes lie
-// outside the allocation, so that one block reads its last 2 bytes as a ushort.
-__device__ __forceinline__ void load_q8_block(const uint8_t* __restrict__ W, size_t gi, size_t last,
-                                              BlockRegs& r) {
-  const size_t off = gi * kBlockBytes;
-  const uint32_t* p = (const uint32_t*)(W + (off & ~(size_t)3));
-  const u32x4_a4 v0 = *(const u32x4_a4*)p;
-  const u32x4_a4 v1 = *(const u32x4_a4*)(p + 4);
-  const uint32_t w8 = (gi == last && !(gi & 1u)) ? (uint32_t)*(const uint16_t*)(W + off + 32) : p[8];
-  const uint32_t w[9] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, w8};
-  const bool odd = (gi & 1u) != 0;
-  const uint32_t sel = odd ? 0x07060504u : 0x05040302u;
-  r.d = odd ? (uint16_t)(w[0] >> 16) : (uint16_t)(w[0] & 0xFFFFu);
-#pragma unroll
-  for (int i = 0; i < 8; i++) r.q[i] = __builtin_amdgcn_perm(w[i + 1], w[i], sel);
-}
-
-__device__ __forceinline__ int dot_q8_block(const BlockRegs& r, const int8_t* sx /* LDS, 16B aligned */) {
-  u32x4 x0, x1;
-  __builtin_memcpy(&x0, sx, 16);
-  __builtin_memcpy(&x1, sx + 16, 16);
-  int s = 0;
-  s = __builtin_amdgcn_sdot4((int)r.q[0], (int)x0.x, s, false);
-  s = __builtin_amdgcn_sdot4((int)r.q[1], (int)x0.y, s, false);
-  s = __builtin_amdgcn_sdot4((int)r.q[2], (int)x0.z, s, false);
-  s = __builtin_amdgcn_sdot4((int)r.q[3], (int)x0.w, s, false);
-  s = __builtin_amdgcn_sdot4((int)r.q[4], (int)x1.x, s, false);
-  s = __builtin_amdgcn_sdot4((int)r.q[5], (int)x1.y, s, false);
-  s = __builtin_amdgcn_sdot4((int)r.q[6], (int)x1.z, s, false);
-  s = __builtin_amdgcn_sdot4((int)r.q[7], (int)x1.w, s, false);
-  return s;
-}
-
-__device__ __forceinline__ void stage_activation(const int8_t* __restrict__ xq,
-                                                 const uint16_t* __restrict__ xd, int K,
-                                                 uint8_t* smem) {
-  const u32x4* src = (const u32x4*)xq;
-  u32x4* dst = (u32x4*)smem;
-  for (int i = threadIdx.x; i < K / 16; i += blockDim.x) dst[i] = src[i];
-  uint16_t* sxd = (uint16_t*)(smem + K);
-  for (int i = threadIdx.x; i < K / 32; i += blockDim.x) sxd[i] = xd[i];
-  __syncthreads();
-}
-
-// The half-wave's row dot in the canonical order.  Returns the merged value on lane 0.
-__device__ __forceinline__ float q8_row_canonical(const uint8_t* __restrict__ W, int row, int nb,
-                                                  size_t last, const uint8_t* smem, int K, int lane) {
-  const size_t g0 = (size_t)row * nb;
-  const int8_t* sxq = (const int8_t*)smem;
-  const uint16_t* sxd = (const uint16_t*)(smem + K);
-  float acc = 0.0f;
-  int b = lane;
-  for (; b + 96 < nb; b += 128) {
-    BlockRegs r[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) load_q8_block(W, g0 + b + 32 * u, last, r[u]);
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      int bb = b + 32 * u;
-      int isum = dot_q8_block(r[u], sxq + bb * 32);
-      float wd = lt_h2f(r[u].d);
-      float xdv = lt_h2f(sxd[bb]);
-      acc = fmaf(wd * xdv, (float)isum, acc);
-    }
-  }
-  for (; b < nb; b += 32) {
-    BlockRegs r;
-    load_q8_block(W, g0 + b, last, r);
-    int isum = dot_q8_block(r, sxq + b * 32);
-    float wd = lt_h2f(r.d);
-    float xdv = lt_h2f(sxd[b]);
-    acc = fmaf(wd * xdv, (float)isum, acc);
-  }
-#pragma unroll
-  for (int s = 16; s > 0; s >>= 1) acc = acc + __shfl_down(acc, s, 32);
-  return acc;
-}
-
-// kRole only separates kernel symbols in profiles (0: per-layer projections, 1: logits).
-template <bool kResid, int kRole = 0>
-__global__ __launch_bounds__(256) void k_q8_gemv(const uint8_t* __restrict__ W,
-                                                 const int8_t* __restrict__ xq,
-                                                 const uint16_t* __restrict__ xd,
-                                                 const float* __restrict__ resid,
-                                                 float* __restrict__ y, int N, int K) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  stage_activation(xq, xd, K, smem);
-  const int lane = threadIdx.x & 31;
-  const int row = blockIdx.x * 8 + (threadIdx.x >> 5);
-  if (row >= N) return;  // uniform per half-wave; no barrier follows
-  const int nb = K >> 5;
-  float acc = q8_row_canonical(W, row, nb, (size_t)N * nb - 1, smem, K, lane);
-  if (lane == 0) y[row] = kResid ? acc + resid[row] : acc;
-}
-
 __global__ __launch_bounds__(256) void k_q8_gemv_isums(const uint8_t* __restrict__ W,
                                                        const int8_t* __restrict__ xq,
                                                        int32_t* __restrict__ isum, int N, int K) {
@@ -433,32 +305,6 @@ int lt_rmsnorm_quant(lt_ctx* ctx, const float* x, const float* w, int8_t* xq, ui
   LT_REQUIRE(N > 0 && N % 32 == 0 && N <= 16384, "lt_rmsnorm_quant: N=%d (multiple of 32, <= 16384)", N);
   k_rmsnorm_quant<<<1, 256, (size_t)N * sizeof(float), ctx->stream>>>(x, w, xq, xd, N, eps);
   return lt_check_launch("k_rmsnorm_quant");
-}
-
-int lt_q8_gemv(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd, const float* resid,
-               float* y, int N, int K) {
-  LT_REQUIRE(ctx && W && xq && xd && y, "lt_q8_gemv: null argument");
-  LT_REQUIRE(N > 0 && K > 0 && K % 32 == 0 && K <= 32768, "lt_q8_gemv: N=%d K=%d (K multiple of 32, <= 32768)", N, K);
-  LT_REQUIRE(lt_aligned(W, 4), "lt_q8_gemv: W must be 4-byte aligned");
-  LT_REQUIRE(lt_aligned(xq, 16), "lt_q8_gemv: xq must be 16-byte aligned");
-  LT_REQUIRE(lt_aligned(xd, 2), "lt_q8_gemv: xd must be 2-byte aligned");
-  size_t shm = (size_t)K + (size_t)(K / 32) * 2;
-  int grid = grid_for(N, 8);
-  if (resid)
-    k_q8_gemv<true><<<grid, 256, shm, ctx->stream>>>((const uint8_t*)W, xq, xd, resid, y, N, K);
-  else
-    k_q8_gemv<false><<<grid, 256, shm, ctx->stream>>>((const uint8_t*)W, xq, xd, nullptr, y, N, K);
-  return lt_check_launch("k_q8_gemv");
-}
-
-int lt_q8_gemv_logits(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd, float* y,
-                      int N, int K) {
-  LT_REQUIRE(ctx && W && xq && xd && y, "lt_q8_gemv_logits: null argument");
-  LT_REQUIRE(N > 0 && K > 0 && K % 32 == 0 && K <= 32768, "lt_q8_gemv_logits: N=%d K=%d", N, K);
-  LT_REQUIRE(lt_aligned(W, 4) && lt_aligned(xq, 16) && lt_aligned(xd, 2), "lt_q8_gemv_logits: misaligned argument");
-  size_t shm = (size_t)K + (size_t)(K / 32) * 2;
-  k_q8_gemv<false, 1><<<grid_for(N, 8), 256, shm, ctx->stream>>>((const uint8_t*)W, xq, xd, nullptr, y, N, K);
-  return lt_check_launch("k_q8_gemv_logits");
 }
 
 int lt_q8_gemv_isums(lt_ctx* ctx, const void* W, const int8_t* xq, int32_t* isum, int N, int K) {

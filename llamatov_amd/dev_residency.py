@@ -28,7 +28,7 @@ import numpy as np
 
 from . import _lib
 from ._lib import LT_KV_F16, LT_KV_F32, call
-from .model import ModelConfig, fused_layer_tensors
+from .model import ModelConfig, fused_layer_tensors, interleave_gateup
 
 
 # ----------------------------------------------------------------------------------
@@ -291,7 +291,8 @@ class Profile:
     the split-K declared order) and kv_dtype."""
     kv_dtype: int = LT_KV_F32
     attn_nsplit: int = 1
-    fused_rms_quant: bool = False   # k_rms_quant instead of k_rmsnorm + k_quant_q8
+    fused_step: bool = True         # five fused launches per layer (lt_fused.hip)
+    fused_rms_quant: bool = False   # per-op path only: k_rms_quant instead of k_rmsnorm + k_quant_q8
     graph: bool = True
 
 
@@ -317,11 +318,18 @@ def assert_certified_composition(p: Profile) -> None:
 class ResidentModel:
     """All weights on the device, uploaded once: Q8_0 blocks verbatim, q|k|v and gate|up
     concatenated at load (the reference concatenates at first use, dev_residency.py:1283-1326),
-    tied lm_head sharing token_embd's blocks."""
+    tied lm_head sharing token_embd's blocks.
 
-    def __init__(self, cfg: ModelConfig, weights: dict, dev: Device | None = None):
+    layouts selects the gate|up layouts uploaded: "fused" (rows interleaved gate j, up j, for
+    lt_q8_gemv_rms_silu), "per_op" (gate rows then up rows, the reference's concatenation,
+    for lt_q8_gemv + lt_silu_mul_quant) or "both"."""
+
+    def __init__(self, cfg: ModelConfig, weights: dict, dev: Device | None = None, layouts: str = "both"):
+        if layouts not in ("fused", "per_op", "both"):
+            raise ValueError(f"layouts={layouts!r}")
         self.cfg = cfg
         self.dev = dev or get_device()
+        self.layouts = layouts
         E, F = cfg.n_embd, cfg.n_ff
         self.tok_embd = Q8Weight(weights["token_embd.weight"], E, self.dev)
         self.output = self.tok_embd if cfg.tied else Q8Weight(weights["output.weight"], E, self.dev)
@@ -329,15 +337,21 @@ class ResidentModel:
         self.layers = []
         for il in range(cfg.n_layers):
             t = fused_layer_tensors(cfg, weights, il)
-            self.layers.append({
+            L = {
                 "attn_norm": DevTensor.from_host(t["attn_norm"].astype(np.float32), self.dev),
                 "wqkv": Q8Weight(t["wqkv"], E, self.dev),
                 "bqkv": DevTensor.from_host(t["bqkv"], self.dev) if t["bqkv"] is not None else None,
                 "wo": Q8Weight(t["wo"], cfg.q_dim, self.dev),
                 "ffn_norm": DevTensor.from_host(t["ffn_norm"].astype(np.float32), self.dev),
-                "wgu": Q8Weight(t["wgu"], E, self.dev),
                 "wdown": Q8Weight(t["wdown"], F, self.dev),
-            })
+            }
+            if layouts in ("per_op", "both"):
+                L["wgu"] = Q8Weight(t["wgu"], E, self.dev)
+            if layouts in ("fused", "both"):
+                p = f"blk.{il}"
+                L["wgu_il"] = Q8Weight(interleave_gateup(weights[f"{p}.ffn_gate.weight"],
+                                                         weights[f"{p}.ffn_up.weight"]), E, self.dev)
+            self.layers.append(L)
         self.freqs = DevTensor.from_host(rope_freqs(cfg.head_dim, cfg.rope_theta), self.dev)
 
     def free(self) -> None:
@@ -360,6 +374,9 @@ class DecodePlan:
     def __init__(self, model: ResidentModel, profile: Profile = PRODUCTION_PROFILE,
                  max_ctx: int | None = None, hist_cap: int = 4096):
         assert_certified_composition(profile)
+        need = "fused" if profile.fused_step else "per_op"
+        if model.layouts not in (need, "both"):
+            raise ValueError(f"DecodePlan: profile needs the {need!r} gate|up layout, model has {model.layouts!r}")
         self.model, self.cfg, self.profile = model, model.cfg, profile
         self.dev = model.dev
         cfg = self.cfg
@@ -380,10 +397,11 @@ class DecodePlan:
         self.qkv = DevTensor.empty((cfg.n_qkv,), np.float32, D)
         self.att = DevTensor.empty((cfg.q_dim,), np.float32, D)
         self.gu = DevTensor.empty((2 * F,), np.float32, D)
+        self.v = DevTensor.empty((F,), np.float32, D)
         self.logits = DevTensor.empty((cfg.vocab,), np.float32, D)
         self.xq = DevTensor.empty((kmax,), np.int8, D)
         self.xd = DevTensor.empty((kmax // 32,), np.uint16, D)
-        ws_n = _lib.raw("lt_argmax_workspace_size")()
+        ws_n = max(_lib.raw("lt_argmax_workspace_size")(), _lib.raw("lt_q8_gemv_argmax_workspace_size")(cfg.vocab))
         self.am_ws = DevTensor.empty((ws_n,), np.uint8, D)
         aw = _lib.raw("lt_attn_workspace_size")(1, cfg.n_head, hd, profile.attn_nsplit)
         self.attn_ws = DevTensor.empty((aw,), np.uint8, D) if aw else None
@@ -431,6 +449,48 @@ class DecodePlan:
 
     # -- the step ----------------------------------------------------------------
     def enqueue_step(self) -> None:
+        """Launch one decode token (fused or per-op, as the profile says)."""
+        if self.profile.fused_step:
+            self._enqueue_fused()
+        else:
+            self._enqueue_per_op()
+
+    def _enqueue_fused(self) -> None:
+        """Five launches per layer (lt_fused.hip), then the vocab GEMV with its argmax:
+        the same arithmetic as _enqueue_per_op, bit for bit.
+          QKV   rmsnorm -> quant -> GEMV + bias        (layer 0: from the embedding of tok)
+          attn  RoPE -> KV append -> attention -> quant
+          O     [split merge -> quant] -> GEMV + x, length += 1
+          FFN1  rmsnorm -> quant -> gate|up GEMV -> SiLU(g)*u -> quant
+          FFN2  down GEMV + xres"""
+        cfg, m, p = self.cfg, self.model, self.profile
+        h = self.dev.handle
+        E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
+        eps = ctypes.c_float(cfg.norm_eps)
+        ws, ws_n = _vp(self.attn_ws), (self.attn_ws.nbytes if self.attn_ws is not None else 0)
+        for il, L in enumerate(m.layers):
+            cache = self.caches[il]
+            x = self.resid_in if il == 0 else self.carry
+            if il == 0:
+                call("lt_q8_gemv_embed_rms", h, m.tok_embd.t.vp, self.tok.vp, cfg.vocab, self.resid_in.vp,
+                     self.err.vp, L["attn_norm"].vp, eps, L["wqkv"].t.vp, _vp(L["bqkv"]), self.qkv.vp,
+                     cfg.n_qkv, E)
+            else:
+                call("lt_q8_gemv_rms", h, x.vp, L["attn_norm"].vp, eps, L["wqkv"].t.vp, _vp(L["bqkv"]),
+                     self.qkv.vp, cfg.n_qkv, E)
+            call("lt_attn_step", h, self.qkv.vp, m.freqs.vp, cache.k.vp, cache.v.vp, _vp(cache.len_ptr),
+                 None, self.xq.vp, self.xd.vp, nh, nkv, hd, ctypes.c_float(self.scale), cache.max_seq,
+                 p.attn_nsplit, p.kv_dtype, ws, ws_n)
+            call("lt_q8_gemv_attn_out", h, self.xq.vp, self.xd.vp, ws, ws_n, p.attn_nsplit, nh, hd, L["wo"].t.vp,
+                 x.vp, self.xres.vp, E, cfg.q_dim, _vp(cache.len_ptr), cache.max_seq)
+            call("lt_q8_gemv_rms_silu", h, self.xres.vp, L["ffn_norm"].vp, eps, L["wgu_il"].t.vp, self.xq.vp,
+                 self.xd.vp, F, E)
+            call("lt_q8_gemv", h, L["wdown"].t.vp, self.xq.vp, self.xd.vp, self.xres.vp, self.carry.vp, E, F)
+        call("lt_q8_gemv_rms_argmax", h, self.carry.vp, m.output_norm.vp, eps, m.output.t.vp, self.logits.vp,
+             cfg.vocab, E, self.tok.vp, self.hist.vp, self.hist_count.vp, self.hist_cap,
+             self.am_ws.vp, self.am_ws.nbytes)
+
+    def _enqueue_per_op(self) -> None:
         """Launch one token: embed(tok) -> layers -> logits -> argmax -> tok.
         The launch order is forward_pass_resident's fully-device branch
         (bpd/lib/dev_residency.py:1365-1477) followed by _compute_folded_logits (:1596-1623)
@@ -463,7 +523,7 @@ class DecodePlan:
             q8_gemv_dev(L["wdown"], self.xq, self.xd, self.carry, self.xres)
             x = self.carry
         self._rms_quant(x, m.output_norm, E, eps)
-        call("lt_q8_gemv_logits", h, m.output.t.vp, self.xq.vp, self.xd.vp, self.logits.vp,
+        call("lt_q8_gemv", h, m.output.t.vp, self.xq.vp, self.xd.vp, None, self.logits.vp,
              m.output.N, m.output.K)
         call("lt_argmax_record", h, self.logits.vp, cfg.vocab, self.tok.vp, self.hist.vp,
              self.hist_count.vp, self.hist_cap, self.am_ws.vp, self.am_ws.nbytes)
@@ -488,7 +548,7 @@ class DecodePlan:
         for c in self.caches:
             c.free()
         for t in (self.tok, self.err, self.hist, self.hist_count, self.lens, self.resid_in, self.carry,
-                  self.xres, self.h, self.qkv, self.att, self.gu, self.logits, self.xq, self.xd,
+                  self.xres, self.h, self.qkv, self.att, self.gu, self.v, self.logits, self.xq, self.xd,
                   self.am_ws, self.attn_ws):
             if t is not None:
                 t.free()

@@ -185,6 +185,17 @@ def fused_layer_tensors(cfg: ModelConfig, w: dict, il: int) -> dict[str, np.ndar
     return out
 
 
+def interleave_gateup(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """gate [F, rb] and up [F, rb] Q8_0 block rows -> [2F, rb] with row 2j = gate j and
+    row 2j+1 = up j: the layout of the fused gate|up GEMV, whose workgroups hold a gate row
+    and its up row on the two halves of one wave.  Each row's dot product is unchanged."""
+    F = gate.shape[0]
+    out = np.empty((2 * F, gate.shape[1]), dtype=gate.dtype)
+    out[0::2] = gate
+    out[1::2] = up
+    return out
+
+
 def random_prompt(cfg: ModelConfig, n: int, seed: int = 7) -> list[int]:
     rng = np.random.default_rng(seed)
     return [int(t) for t in rng.integers(0, cfg.vocab, size=n)]

@@ -75,6 +75,11 @@ OR_API void or_quant_q8(const float* x, int K, int8_t* xq, uint16_t* xd) {
   }
 }
 
+/* SiLU(g)*u elementwise, v = (g/(1+exp(-g)))*u (bpd/lib/dev_residency.py:583). */
+OR_API void or_silu_mul(const float* g, const float* u, int K, float* v) {
+  for (int i = 0; i < K; i++) v[i] = lt_silu_mul(g[i], u[i]);
+}
+
 /* k_silu_mul_quant (bpd/lib/dev_residency.py:573-604): v = (g/(1+exp(-g)))*u, then quant. */
 OR_API void or_silu_mul_quant(const float* g, const float* u, int K, int8_t* xq, uint16_t* xd) {
   float* v = (float*)malloc(sizeof(float) * (size_t)K);

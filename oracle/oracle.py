@@ -39,6 +39,7 @@ def lib() -> ctypes.CDLL:
             "or_quantize_rows": (None, [P, c_int, c_int, P]),
             "or_quant_q8": (None, [P, c_int, P, P]),
             "or_silu_mul_quant": (None, [P, P, c_int, P, P]),
+            "or_silu_mul": (None, [P, P, c_int, P]),
             "or_q8_block_dots": (None, [P, P, c_int, c_int, P]),
             "or_q8_gemv": (None, [P, P, P, P, P, c_int, c_int]),
             "or_rmsnorm": (None, [P, P, P, c_int, c_float]),
@@ -125,6 +126,14 @@ def silu_mul_quant(g: np.ndarray, u: np.ndarray) -> tuple[np.ndarray, np.ndarray
     xd = np.empty(K // 32, np.uint16)
     lib().or_silu_mul_quant(_p(g), _p(u), K, _p(xq), _p(xd))
     return xq, xd
+
+
+def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    g = np.ascontiguousarray(g, np.float32).reshape(-1)
+    u = np.ascontiguousarray(u, np.float32).reshape(-1)
+    v = np.empty_like(g)
+    lib().or_silu_mul(_p(g), _p(u), g.size, _p(v))
+    return v
 
 
 def block_dots(W: np.ndarray, xq: np.ndarray, K: int) -> np.ndarray:

@@ -39,12 +39,14 @@ def bitexact(a, b):
     return np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
 
 
+@pytest.mark.parametrize("step", ["fused", "per_op"])
 @pytest.mark.parametrize("kv_dtype,nsplit,fused", [(LT_KV_F32, 1, False), (LT_KV_F16, 1, True),
-                                                   (LT_KV_F32, 4, True)])
-def test_tiny_stepwise_logits_bitexact(gpu, oracle, kv_dtype, nsplit, fused):
+                                                   (LT_KV_F32, 4, True), (LT_KV_F16, 2, False)])
+def test_tiny_stepwise_logits_bitexact(gpu, oracle, step, kv_dtype, nsplit, fused):
     cfg = M.TINY
-    case(f"tiny stepwise kv={kv_dtype} nsplit={nsplit} fused={fused}")
-    prof = dr.Profile(kv_dtype=kv_dtype, attn_nsplit=nsplit, fused_rms_quant=fused)
+    case(f"tiny stepwise {step} kv={kv_dtype} nsplit={nsplit} fused_rms={fused}")
+    prof = dr.Profile(kv_dtype=kv_dtype, attn_nsplit=nsplit, fused_rms_quant=fused,
+                      fused_step=step == "fused")
     plan = dr.DecodePlan(resident(cfg, gpu), prof)
     orc = oracle.OracleModel(cfg, weights(cfg), kv_f16=kv_dtype == LT_KV_F16, attn_nsplit=nsplit)
     toks = M.random_prompt(cfg, 6, seed=3)
@@ -122,19 +124,21 @@ def test_prefill_kv_equals_incremental(gpu):
     fresh.free()
 
 
-@pytest.mark.parametrize("cfg_name,n_prompt,n_gen,kv_dtype", [
-    ("small-qwen-arch", 32, 32, LT_KV_F32),
-    ("qwen2.5-0.5b-arch", 32, 128, LT_KV_F32),
-    ("qwen2.5-0.5b-arch", 32, 128, LT_KV_F16),
+@pytest.mark.parametrize("cfg_name,n_prompt,n_gen,kv_dtype,step", [
+    ("small-qwen-arch", 32, 32, LT_KV_F32, "fused"),
+    ("small-qwen-arch", 32, 32, LT_KV_F32, "per_op"),
+    ("qwen2.5-0.5b-arch", 32, 128, LT_KV_F32, "fused"),
+    ("qwen2.5-0.5b-arch", 32, 128, LT_KV_F16, "fused"),
+    ("qwen2.5-0.5b-arch", 32, 128, LT_KV_F16, "per_op"),
 ])
-def test_greedy_tokens_identical(gpu, oracle, cfg_name, n_prompt, n_gen, kv_dtype):
+def test_greedy_tokens_identical(gpu, oracle, cfg_name, n_prompt, n_gen, kv_dtype, step):
     """Greedy token identity with the oracle, through the captured graph."""
     cfg = M.CONFIGS[cfg_name]
-    case(f"greedy {cfg_name} {n_prompt}+{n_gen} kv={kv_dtype}")
+    case(f"greedy {cfg_name} {n_prompt}+{n_gen} kv={kv_dtype} {step}")
     prompt = M.random_prompt(cfg, n_prompt, seed=7)
     orc = oracle.OracleModel(cfg, weights(cfg), kv_f16=kv_dtype == LT_KV_F16)
     exp, margins = orc.generate(prompt, n_gen)
-    plan = dr.DecodePlan(resident(cfg, gpu), dr.Profile(kv_dtype=kv_dtype))
+    plan = dr.DecodePlan(resident(cfg, gpu), dr.Profile(kv_dtype=kv_dtype, fused_step=step == "fused"))
     gr = dr.GraphRunner(plan)
     gr.seed(prompt)
     first = plan.read_token()
