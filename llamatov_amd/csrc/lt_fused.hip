@@ -146,9 +146,7 @@ __device__ __forceinline__ float rms_inv(const Slots<KS>& S, int K, float eps, f
   if (t < 64) {
     float a = red[t] + red[t + 128];
     float b = red[t + 64] + red[t + 192];
-    float c = a + b;
-#pragma unroll
-    for (int s = 32; s > 0; s >>= 1) c = c + __shfl_down(c, s, 64);
+    const float c = wave_tree_dpp(a + b);
     if (t == 0) *sinv = lt_rsqrtf(c / (float)K + eps);
   }
   __syncthreads();
@@ -262,6 +260,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
 
   const int hw = threadIdx.x >> 5;
   const int lane = threadIdx.x & 31;
+  // @phase gemv 0
 
   // (1) the prologue's global inputs
   Slots<KS> S;
@@ -317,6 +316,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
 #pragma unroll
     for (int i = 0; i < kResidPre; i++) rpre[i] = (lane == 0 && i < nrows) ? P.resid[rbase + step * i] : 0.0f;
   }
+  // @phase gemv 1
 
   // (3) the prologue's arithmetic, under the weight loads
   if constexpr (PRO == PRO_RMS) {
@@ -354,6 +354,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
     slots_to_rec<KS, true>(S, inv, K, rec);
   }
   __syncthreads();
+  // @phase gemv 2
 
   // (4) stream the rows
   float bv = -__builtin_inff();
@@ -361,46 +362,53 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
   float acc = 0.0f;
   int fm = 0, fi = 0, fk = 0;         // item being folded: index, row, slot
   uint32_t fold_row = (uint32_t)rbase * (uint32_t)nb * (uint32_t)kBlockBytes;
-  for (int t = 0; t < trips; t++) {
+  // all trips but the last refill the ring; the last one only drains it
+  auto fold_item = [&](RawBlock& r, bool refill) {
+    const int b = lane + 32 * fk;
+    const bool odd = ((fold_row + lane_bytes + (uint32_t)fk * kSlotBytes) & 2u) != 0;
+    const float folded = fold_raw(r, odd, rec + (b < nb ? b : 0) * kRecDwords, acc);
+    acc = (fm < total && b < nb) ? folded : acc;
+    if (refill) issue(r);
+    fm++;
+    if (++fk == nk) {                   // row end: the same item for both half-waves
+      const float v = halfwave_tree_dpp(acc);   // the row value, on lane 0 of the half-wave
+      const int row = rbase + step * fi;
+      if (lane == 0 && fi < nrows) {
+        if constexpr (EPI == EPI_SILU) {
+          s_rows[row - blockIdx.x * kSiluRows] = v;
+        } else {
+          float o = v;
+          if constexpr (EPI == EPI_RESID) {
+            float rv = 0.0f;
+            if (fi < kResidPre) {
 #pragma unroll
-    for (int d = 0; d < D; d++) {
-      const int b = lane + 32 * fk;
-      const bool odd = ((fold_row + lane_bytes + (uint32_t)fk * kSlotBytes) & 2u) != 0;
-      const float folded = fold_raw(ring[d], odd, rec + (b < nb ? b : 0) * kRecDwords, acc);
-      acc = (fm < total && b < nb) ? folded : acc;
-      issue(ring[d]);
-      fm++;
-      if (++fk == nk) {                 // row end: the same item for both half-waves
-        const float v = halfwave_tree_dpp(acc);   // the row value, on lane 0 of the half-wave
-        const int row = rbase + step * fi;
-        if (lane == 0 && fi < nrows) {
-          if constexpr (EPI == EPI_SILU) {
-            s_rows[row - blockIdx.x * kSiluRows] = v;
-          } else {
-            float o = v;
-            if constexpr (EPI == EPI_RESID) {
-              float rv = 0.0f;
-              if (fi < kResidPre) {
-#pragma unroll
-                for (int i = 0; i < kResidPre; i++)   // static indices keep rpre in registers
-                  if (fi == i) rv = rpre[i];
-              } else {
-                rv = P.resid[row];
-              }
-              o = v + rv;
+              for (int i = 0; i < kResidPre; i++)   // static indices keep rpre in registers
+                if (fi == i) rv = rpre[i];
+            } else {
+              rv = P.resid[row];
             }
-            P.y[row] = o;
-            if (EPI == EPI_ARGMAX && am_better(o, row, bv, bi)) { bv = o; bi = row; }
+            o = v + rv;
           }
+          P.y[row] = o;
+          if (EPI == EPI_ARGMAX && am_better(o, row, bv, bi)) { bv = o; bi = row; }
         }
-        acc = 0.0f;
-        fk = 0;
-        fi++;
-        fold_row += row_step_bytes;
       }
+      acc = 0.0f;
+      fk = 0;
+      fi++;
+      fold_row += row_step_bytes;
     }
+  };
+  for (int t = 0; t + 1 < trips; t++) {
+#pragma unroll
+    for (int d = 0; d < D; d++) fold_item(ring[d], true);
+  }
+  if (trips > 0) {
+#pragma unroll
+    for (int d = 0; d < D; d++) fold_item(ring[d], false);
   }
 
+  // @phase gemv 3
   if constexpr (EPI == EPI_SILU) {
     // the workgroup's 64 rows are the gate/up pairs of one 32-element block: SiLU(g)*u
     // one pair per lane of half-wave 0, then k_silu_mul_quant's quantizer
@@ -424,6 +432,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
       P.pidx[blockIdx.x] = ix;
     }
   }
+  // @phase gemv 4
 }
 
 // Reduce G argmax partials (ties to the lowest index) and publish the token; optionally
@@ -530,6 +539,7 @@ __global__ __launch_bounds__(256) void k_attn_step(
   const int upr = hd / kEpu;                        // units per position row
   const int cpos = kVChunkFloats / hd;              // positions per V chunk
 
+  // @phase attn 0
   // RoPE inputs do not depend on the length: load them first
   const int nrope = (HPW + 1) * half;
   float x1 = 0.0f, x2 = 0.0f, vnew = 0.0f, fr = 0.0f;
@@ -553,6 +563,7 @@ __global__ __launch_bounds__(256) void k_attn_step(
   const int n = p1 > p0 ? p1 - p0 : 0;
   const size_t head_base = (size_t)p0 * kvrow + (size_t)g * hd;
 
+  // @phase attn 1
   // issue this thread's first K row and the first V chunk now, under the RoPE work
   const bool kpre = kF16 && upr <= kKU && tid < n && p0 + tid != L;
   u32x4 kraw[kKU];
@@ -599,6 +610,7 @@ __global__ __launch_bounds__(256) void k_attn_step(
   }
   if (tid < hd) sv[tid] = kv_round<kF16>(vnew);
   __syncthreads();
+  // @phase attn 2
 
   if (valid && sp == 0 && (h0 % rep) == 0 && tid < hd) {
     const size_t off = (size_t)L * kvrow + (size_t)g * hd + tid;
@@ -672,12 +684,12 @@ __global__ __launch_bounds__(256) void k_attn_step(
   }
   __syncthreads();
 
+  // @phase attn 3
   const int wave = tid >> 6, wl = tid & 63;
   for (int r = wave; r < HPW; r += 4) {
     float m = -1e30f;
     for (int t = wl; t < n; t += 64) m = fmaxf(m, se[r * per_max + t]);
-#pragma unroll
-    for (int s = 32; s > 0; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
+    m = wave_max(m);
     if (wl == 0) s_mx[r] = m;
   }
   __syncthreads();
@@ -689,11 +701,11 @@ __global__ __launch_bounds__(256) void k_attn_step(
   for (int r = wave; r < HPW; r += 4) {
     float ls = 0.0f;
     for (int t = wl; t < n; t += 64) ls = ls + se[r * per_max + t];
-#pragma unroll
-    for (int s = 32; s > 0; s >>= 1) ls = ls + __shfl_down(ls, s, 64);
+    ls = wave_tree_dpp(ls);   // the frozen 64-lane tree, s = 32 .. 1
     if (wl == 0) s_z[r] = ls;
   }
 
+  // @phase attn 4
   // O: thread per (head, dim); each a sequential fma chain over t, V staged in LDS in
   // chunks of cpos positions (16-byte loads, all issued before the stores; chunk 0 was
   // issued at the top)
@@ -772,6 +784,7 @@ __global__ __launch_bounds__(256) void k_attn_step(
     wsm[(size_t)h * nsplit + sp] = s_mx[tid];
     wsz[(size_t)h * nsplit + sp] = s_z[tid];
   }
+  // @phase attn 5
   if (nsplit == 1 && oq) {
     // the workgroup's heads are whole 32-element blocks of the attention vector: quantize
     // them for the O projection (k_quant_q8's quantizer)
@@ -781,6 +794,7 @@ __global__ __launch_bounds__(256) void k_attn_step(
     for (int b = tid >> 5; b < nout / 32; b += 8)
       quant_block_hw(svt[b * 32 + lane], lane, oq + o0 + b * 32, od + (o0 >> 5) + b);
   }
+  // @phase attn 6
 }
 
 inline int grid_for(long n, int per) { return (int)((n + per - 1) / per); }
@@ -850,10 +864,17 @@ hipError_t launch_gemv(const GemvParams& P, lt_ctx* ctx, int* grid_out) {
   if (PRO == PRO_EMBED_RMS) shm += (size_t)((P.K + 15) & ~15) + (size_t)P.K * sizeof(float);
   hipStream_t st = ctx->stream;
   const int ncu = ctx->num_cus;
+  // ring depth: 2 when a half-wave has at most 2 blocks to stream, else 8 (4 for the
+  // register-heavy K > 4096 prologues)
+  const int nk = (P.K / 32 + 31) / 32;
+  const bool shallow = EPI != EPI_SILU && env_rows() == 0 && (P.N + 7) / 8 <= 1024 && nk <= 2;
   if constexpr (PRO == PRO_STAGE) {
-    return launch_gemv_k<1, PRO, EPI, 8>(P, shm, st, ncu, grid_out);
+    return shallow ? launch_gemv_k<1, PRO, EPI, 2>(P, shm, st, ncu, grid_out)
+                   : launch_gemv_k<1, PRO, EPI, 8>(P, shm, st, ncu, grid_out);
   } else {
-    if (P.K <= 1024) return launch_gemv_k<4, PRO, EPI, 8>(P, shm, st, ncu, grid_out);
+    if (P.K <= 1024)
+      return shallow ? launch_gemv_k<4, PRO, EPI, 2>(P, shm, st, ncu, grid_out)
+                     : launch_gemv_k<4, PRO, EPI, 8>(P, shm, st, ncu, grid_out);
     if (P.K <= 4096) return launch_gemv_k<16, PRO, EPI, 8>(P, shm, st, ncu, grid_out);
     return launch_gemv_k<64, PRO, EPI, 4>(P, shm, st, ncu, grid_out);
   }

@@ -133,6 +133,18 @@ __device__ __forceinline__ float halfwave_tree_dpp(float acc) {
   return acc;
 }
 
+// The 64-lane versions (order: s = 32 first, then the half-wave tree): lane t < 32 reads
+// lane t + 32 through ds_bpermute, the rest by swizzle/DPP.  Sum: lane 0 ends with the
+// total of the reference's 6-level shfl_down tree; max: every lane ends with the maximum.
+__device__ __forceinline__ float wave_tree_dpp(float acc) {
+  acc = acc + __shfl_down(acc, 32, 64);
+  return halfwave_tree_dpp(acc);
+}
+__device__ __forceinline__ float wave_max(float a) {
+  a = fmaxf(a, __shfl_xor(a, 32, 64));
+  return halfwave_max(a);
+}
+
 // quant_block_halfwave with the DPP max.
 __device__ __forceinline__ void quant_block_hw(float v, int lane, int8_t* xq_blk, uint16_t* xd_slot) {
   const float a = halfwave_max(fabsf(v));

@@ -146,16 +146,60 @@ def _vp(x) -> ctypes.c_void_p:
 # Op launchers (thin mirrors of the reference op functions)
 # ----------------------------------------------------------------------------------
 class Q8Weight:
-    """A Q8_0 weight resident on the device as GGUF blocks [N][K/32]."""
+    """A Q8_0 weight resident on the device as GGUF blocks [N][K/32]: uploads its own copy,
+    or wraps a slice of a DeviceArena (t=...)."""
     __slots__ = ("t", "N", "K")
 
-    def __init__(self, blocks: np.ndarray, K: int, dev: Device | None = None):
+    def __init__(self, blocks: np.ndarray | None, K: int, dev: Device | None = None,
+                 t: "DevTensor | None" = None, N: int | None = None):
+        if t is not None:
+            self.t, self.N, self.K = t, int(N), K
+            return
         blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
         N = blocks.shape[0]
         if blocks.shape[1] != K // 32 * 34:
             raise ValueError(f"Q8Weight: {blocks.shape} is not [N, {K // 32 * 34}]")
         self.t = DevTensor.from_host(blocks, dev)
         self.N, self.K = N, K
+
+
+class DeviceArena:
+    """One device allocation holding a model's tensors back to back (256-byte aligned
+    slices, 2 MiB-aligned base): a single mapping with large pages, so streaming the
+    weights of a decode step never walks more page tables than it has to.  The slices
+    are non-owning DevTensor views; free() releases the whole arena."""
+    ALIGN = 256
+    BASE_ALIGN = 2 << 20
+
+    def __init__(self, dev: Device | None = None):
+        self.dev = dev or get_device()
+        self.items: list[tuple[np.ndarray, list]] = []
+        self.ptr = 0
+
+    def add(self, arr: np.ndarray) -> list:
+        """Stage an array; the returned one-element list receives its DevTensor at commit()."""
+        slot: list = []
+        self.items.append((np.ascontiguousarray(arr), slot))
+        return slot
+
+    def commit(self) -> None:
+        offs, total = [], 0
+        for a, _ in self.items:
+            offs.append(total)
+            total += (a.nbytes + self.ALIGN - 1) // self.ALIGN * self.ALIGN
+        self.ptr = self.dev.malloc(total + self.BASE_ALIGN)
+        base = (self.ptr + self.BASE_ALIGN - 1) // self.BASE_ALIGN * self.BASE_ALIGN
+        for (a, slot), off in zip(self.items, offs):
+            t = DevTensor(base + off, a.shape, a.dtype, owns=False, dev=self.dev)
+            self.dev.h2d(t.ptr, a)
+            slot.append(t)
+        self.nbytes = total
+        self.items = []
+
+    def free(self) -> None:
+        if self.ptr:
+            self.dev.free(self.ptr)
+            self.ptr = 0
 
 
 def quant_q8_dev(x: DevTensor, xq: DevTensor, xd: DevTensor, K: int | None = None) -> None:
@@ -331,41 +375,52 @@ class ResidentModel:
         self.dev = dev or get_device()
         self.layouts = layouts
         E, F = cfg.n_embd, cfg.n_ff
-        self.tok_embd = Q8Weight(weights["token_embd.weight"], E, self.dev)
-        self.output = self.tok_embd if cfg.tied else Q8Weight(weights["output.weight"], E, self.dev)
-        self.output_norm = DevTensor.from_host(weights["output_norm.weight"].astype(np.float32), self.dev)
+        arena = DeviceArena(self.dev)
+        staged = []   # (kind, owner dict, key, slot, N, K)
+
+        def q8(owner, key, blocks, K):
+            staged.append(("q8", owner, key, arena.add(blocks), blocks.shape[0], K))
+
+        def vec(owner, key, arr):
+            if arr is None:
+                owner[key] = None
+                return
+            staged.append(("vec", owner, key, arena.add(np.asarray(arr, np.float32)), 0, 0))
+
+        top: dict = {}
+        q8(top, "tok_embd", weights["token_embd.weight"], E)
+        if not cfg.tied:
+            q8(top, "output", weights["output.weight"], E)
+        vec(top, "output_norm", weights["output_norm.weight"])
+        vec(top, "freqs", rope_freqs(cfg.head_dim, cfg.rope_theta))
         self.layers = []
         for il in range(cfg.n_layers):
             t = fused_layer_tensors(cfg, weights, il)
-            L = {
-                "attn_norm": DevTensor.from_host(t["attn_norm"].astype(np.float32), self.dev),
-                "wqkv": Q8Weight(t["wqkv"], E, self.dev),
-                "bqkv": DevTensor.from_host(t["bqkv"], self.dev) if t["bqkv"] is not None else None,
-                "wo": Q8Weight(t["wo"], cfg.q_dim, self.dev),
-                "ffn_norm": DevTensor.from_host(t["ffn_norm"].astype(np.float32), self.dev),
-                "wdown": Q8Weight(t["wdown"], F, self.dev),
-            }
+            L: dict = {}
+            vec(L, "attn_norm", t["attn_norm"])
+            q8(L, "wqkv", t["wqkv"], E)
+            vec(L, "bqkv", t["bqkv"])
+            q8(L, "wo", t["wo"], cfg.q_dim)
+            vec(L, "ffn_norm", t["ffn_norm"])
+            q8(L, "wdown", t["wdown"], F)
             if layouts in ("per_op", "both"):
-                L["wgu"] = Q8Weight(t["wgu"], E, self.dev)
+                q8(L, "wgu", t["wgu"], E)
             if layouts in ("fused", "both"):
                 p = f"blk.{il}"
-                L["wgu_il"] = Q8Weight(interleave_gateup(weights[f"{p}.ffn_gate.weight"],
-                                                         weights[f"{p}.ffn_up.weight"]), E, self.dev)
+                q8(L, "wgu_il", interleave_gateup(weights[f"{p}.ffn_gate.weight"],
+                                                  weights[f"{p}.ffn_up.weight"]), E)
             self.layers.append(L)
-        self.freqs = DevTensor.from_host(rope_freqs(cfg.head_dim, cfg.rope_theta), self.dev)
+        arena.commit()
+        for kind, owner, key, slot, N, K in staged:
+            owner[key] = Q8Weight(None, K, t=slot[0], N=N) if kind == "q8" else slot[0]
+        self.arena = arena
+        self.tok_embd = top["tok_embd"]
+        self.output = top.get("output", self.tok_embd)
+        self.output_norm = top["output_norm"]
+        self.freqs = top["freqs"]
 
     def free(self) -> None:
-        self.tok_embd.t.free()
-        if self.output is not self.tok_embd:
-            self.output.t.free()
-        self.output_norm.free()
-        self.freqs.free()
-        for L in self.layers:
-            for v in L.values():
-                if isinstance(v, Q8Weight):
-                    v.t.free()
-                elif isinstance(v, DevTensor):
-                    v.free()
+        self.arena.free()
 
 
 class DecodePlan:
