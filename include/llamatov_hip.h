@@ -217,6 +217,50 @@ LT_API int lt_attn_step(lt_ctx* ctx, const float* qkv, const float* freqs, void*
                         float* out, int8_t* xq, uint16_t* xd, int nh, int nkv, int hd, float scale, int maxt,
                         int nsplit, int kv_dtype, void* ws, size_t ws_bytes);
 
+/* ---- batched prefill -----------------------------------------------------------------
+ * The reference prefills token by token through the decode GEMV and requires a batched
+ * prefill to be device-uniform: bit-identical per element to the single-token path
+ * (bpd/lib/dev_residency.py:1338-1356).  These launchers meet that: the prefill KV cache
+ * and logits equal the token-by-token ones bit for bit. */
+
+/* Tiled int8-MFMA Q8_0 GEMM (no reference counterpart): Y[t][n] for T tokens, each element
+ * bit-identical to lt_q8_gemv on token t (exact MFMA block dots, then the GEMV's canonical
+ * fp32 fold and tree).  Xq [T][K] int8, Xd [T][K/32] fp16 bits (lt_quant_q8 over T*K
+ * elements), Y [T][N]; bias [N] broadcast over tokens, or resid [T][N] (at most one).
+ * K % 32 == 0; the matrix must be below 2 GiB. */
+LT_API int lt_q8_gemm(lt_ctx* ctx, const void* W, const int8_t* Xq, const uint16_t* Xd, const float* bias,
+                      const float* resid, float* Y, int T, int N, int K);
+
+/* lt_q8_gemm on an interleaved gate|up matrix (2F rows, row 2j = gate j, row 2j+1 = up j)
+ * followed by V[t][j] = SiLU(g)*u ((g / (1 + exp(-g))) * u), V [T][F]. */
+LT_API int lt_q8_gemm_silu(lt_ctx* ctx, const void* Wgu, const int8_t* Xq, const uint16_t* Xd, float* V, int T,
+                           int F, int K);
+
+/* RoPE (lt_rope_qk's arithmetic) of T rows of q|k, row t at position *pos0 + t; rows are
+ * row_stride floats apart and hold nheads contiguous heads of hd. */
+LT_API int lt_rope_batch(lt_ctx* ctx, float* qk, int T, int row_stride, const int* pos0, int nheads, int hd,
+                         const float* freqs);
+
+/* KV rows of T tokens into the cache at *len .. *len + T - 1 (k = src[t*src_stride + k_off ..],
+ * v = src[t*src_stride + v_off ..], width elements each; fp32 or fp16 RNE).  *len is not
+ * changed (lt_len_add bumps it after the attention that reads it). */
+LT_API int lt_kv_append_batch(lt_ctx* ctx, void* kc, void* vc, const float* src, int src_stride, int k_off,
+                              int v_off, int T, const int* len, int width, int maxt, int kv_dtype);
+
+/* *len += T, capped at maxt. */
+LT_API int lt_len_add(lt_ctx* ctx, int* len, int T, int maxt);
+
+/* Causal attention of T query tokens of one sequence over its cache (k_attn_decode_masked's
+ * order per query): query t (q + t*q_stride) attends *len0 + t + 1 positions; out [T][nh*hd].
+ * nsplit and ws as lt_attn_decode with batch = T. */
+LT_API int lt_attn_prefill(lt_ctx* ctx, const float* q, int q_stride, const void* kc, const void* vc,
+                           const int* len0, float* out, int T, int nh, int nkv, int hd, float scale, int maxt,
+                           int nsplit, int kv_dtype, void* ws, size_t ws_bytes);
+
+/* Embedding rows of T device token ids (lt_embed_q8 per token), x [T][E]. */
+LT_API int lt_embed_q8_batch(lt_ctx* ctx, const void* emb, const int* toks, float* x, int T, int E, int vocab,
+                             int* err);
+
 /* ---- graphs (replaces cuStreamBeginCapture/EndCapture/GraphInstantiate/GraphLaunch,
  *      GraphRunner.capture / replay, bpd/lib/dev_residency.py:1732-1818) ---- */
 LT_API int lt_graph_begin(lt_ctx* ctx);

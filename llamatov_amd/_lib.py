@@ -59,6 +59,14 @@ _SIGS = {
     "lt_q8_gemv_argmax_workspace_size": (c_size_t, [c_int]),
     "lt_attn_step": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_float, c_int, c_int,
                              c_int, _P, c_size_t]),
+    "lt_q8_gemm": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int]),
+    "lt_q8_gemm_silu": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int]),
+    "lt_rope_batch": (c_int, [_P, _P, c_int, c_int, _P, c_int, c_int, _P]),
+    "lt_kv_append_batch": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, _P, c_int, c_int, c_int]),
+    "lt_len_add": (c_int, [_P, _P, c_int, c_int]),
+    "lt_attn_prefill": (c_int, [_P, _P, c_int, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float, c_int,
+                                c_int, c_int, _P, c_size_t]),
+    "lt_embed_q8_batch": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _P]),
     "lt_graph_begin": (c_int, [_P]),
     "lt_graph_end": (c_int, [_P, POINTER(c_void_p)]),
     "lt_graph_launch": (c_int, [_P, _P]),

@@ -58,12 +58,14 @@ __device__ __forceinline__ void load2(const void* base, size_t idx, float& a, fl
   }
 }
 
+// prefill != 0: the batch is T query tokens of one sequence sharing one cache, query b
+// attending *len + b + 1 positions (causal); q rows are q_stride floats apart.
 template <bool kF16, bool kSplit, int HPW>
 __global__ __launch_bounds__(256) void k_attn_decode(
     const float* __restrict__ q, const void* __restrict__ kc, const void* __restrict__ vc,
     const int* __restrict__ len, float* __restrict__ out, float* __restrict__ wsm,
     float* __restrict__ wsz, float* __restrict__ wso, int nh, int nkv, int hd, float scale,
-    int maxt, int nsplit, int per_max) {
+    int maxt, int nsplit, int per_max, int q_stride, int prefill) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   float* sq = lds;             // [HPW][hd]
   float* se = lds + HPW * hd;  // [HPW][per_max]
@@ -77,7 +79,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(
   const int rep = nh / nkv;
   const int g = h0 / rep;
 
-  int L = len[b];
+  int L = prefill ? len[0] + b + 1 : len[b];
   L = L < 0 ? 0 : (L > maxt ? maxt : L);
   const int per = (L + nsplit - 1) / nsplit;
   const int p0 = sp * per;
@@ -86,10 +88,10 @@ __global__ __launch_bounds__(256) void k_attn_decode(
   const int n = p1 > p0 ? p1 - p0 : 0;
 
   const size_t kvrow = (size_t)nkv * hd;
-  const size_t seq_base = (size_t)b * (size_t)maxt * kvrow;
+  const size_t seq_base = prefill ? 0 : (size_t)b * (size_t)maxt * kvrow;
   const size_t head_base = seq_base + (size_t)p0 * kvrow + (size_t)g * hd;
 
-  for (int i = tid; i < HPW * hd; i += 256) sq[i] = q[((size_t)b * nh + h0) * hd + i];
+  for (int i = tid; i < HPW * hd; i += 256) sq[i] = q[(size_t)b * q_stride + (size_t)h0 * hd + i];
   __syncthreads();
 
   // scores: thread per position, HPW sequential-fma chains over i
@@ -201,12 +203,13 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
 template <bool kF16, bool kSplit>
 hipError_t launch_attn(int hpw, dim3 grid, size_t shm, hipStream_t st, const float* q, const void* kc,
                        const void* vc, const int* len, float* out, float* wsm, float* wsz, float* wso,
-                       int nh, int nkv, int hd, float scale, int maxt, int nsplit, int per_max) {
+                       int nh, int nkv, int hd, float scale, int maxt, int nsplit, int per_max,
+                       int q_stride, int prefill) {
 #define LT_ATTN_CASE(H)                                                                      \
   case H:                                                                                    \
     k_attn_decode<kF16, kSplit, H><<<grid, 256, shm, st>>>(q, kc, vc, len, out, wsm, wsz, wso, \
                                                            nh, nkv, hd, scale, maxt, nsplit,  \
-                                                           per_max);                          \
+                                                           per_max, q_stride, prefill);       \
     break;
   switch (hpw) {
     LT_ATTN_CASE(1)
@@ -229,10 +232,11 @@ size_t lt_attn_workspace_size(int batch, int nh, int hd, int nsplit) {
   return (size_t)batch * nh * nsplit * (size_t)(2 + hd) * sizeof(float) + 256;
 }
 
-int lt_attn_decode(lt_ctx* ctx, const float* q, const void* kc, const void* vc, const int* len,
-                   float* out, int batch, int nh, int nkv, int hd, float scale, int maxt, int nsplit,
-                   int kv_dtype, void* ws, size_t ws_bytes) {
+static int attn_impl(lt_ctx* ctx, const float* q, const void* kc, const void* vc, const int* len,
+                     float* out, int batch, int nh, int nkv, int hd, float scale, int maxt, int nsplit,
+                     int kv_dtype, void* ws, size_t ws_bytes, int q_stride, int prefill) {
   LT_REQUIRE(ctx && q && kc && vc && len && out, "lt_attn_decode: null argument");
+  LT_REQUIRE(q_stride >= nh * hd, "lt_attn: q_stride=%d < nh*hd", q_stride);
   LT_REQUIRE(batch > 0 && nh > 0 && nkv > 0 && nh % nkv == 0, "lt_attn_decode: batch=%d nh=%d nkv=%d", batch, nh, nkv);
   LT_REQUIRE(hd > 0 && hd % 8 == 0 && hd <= 512, "lt_attn_decode: hd=%d (multiple of 8, <= 512)", hd);
   LT_REQUIRE(maxt > 0 && nsplit >= 1 && nsplit <= maxt, "lt_attn_decode: maxt=%d nsplit=%d", maxt, nsplit);
@@ -264,17 +268,31 @@ int lt_attn_decode(lt_ctx* ctx, const float* q, const void* kc, const void* vc, 
   hipError_t e;
   const bool f16 = kv_dtype == LT_KV_F16;
   if (nsplit == 1)
-    e = f16 ? launch_attn<true, false>(hpw, grid, shm, ctx->stream, q, kc, vc, len, out, wsm, wsz, wso, nh, nkv, hd, scale, maxt, nsplit, per_max)
-            : launch_attn<false, false>(hpw, grid, shm, ctx->stream, q, kc, vc, len, out, wsm, wsz, wso, nh, nkv, hd, scale, maxt, nsplit, per_max);
+    e = f16 ? launch_attn<true, false>(hpw, grid, shm, ctx->stream, q, kc, vc, len, out, wsm, wsz, wso, nh, nkv, hd, scale, maxt, nsplit, per_max, q_stride, prefill)
+            : launch_attn<false, false>(hpw, grid, shm, ctx->stream, q, kc, vc, len, out, wsm, wsz, wso, nh, nkv, hd, scale, maxt, nsplit, per_max, q_stride, prefill);
   else
-    e = f16 ? launch_attn<true, true>(hpw, grid, shm, ctx->stream, q, kc, vc, len, out, wsm, wsz, wso, nh, nkv, hd, scale, maxt, nsplit, per_max)
-            : launch_attn<false, true>(hpw, grid, shm, ctx->stream, q, kc, vc, len, out, wsm, wsz, wso, nh, nkv, hd, scale, maxt, nsplit, per_max);
+    e = f16 ? launch_attn<true, true>(hpw, grid, shm, ctx->stream, q, kc, vc, len, out, wsm, wsz, wso, nh, nkv, hd, scale, maxt, nsplit, per_max, q_stride, prefill)
+            : launch_attn<false, true>(hpw, grid, shm, ctx->stream, q, kc, vc, len, out, wsm, wsz, wso, nh, nkv, hd, scale, maxt, nsplit, per_max, q_stride, prefill);
   if (e != hipSuccess) return lt_fail_hip(e, "k_attn_decode launch", __FILE__, __LINE__);
   if (nsplit > 1) {
     k_attn_combine<<<dim3(nh, batch), hd < 256 ? hd : 256, 0, ctx->stream>>>(wsm, wsz, wso, out, nh, hd, nsplit);
     return lt_check_launch("k_attn_combine");
   }
   return LT_OK;
+}
+
+int lt_attn_decode(lt_ctx* ctx, const float* q, const void* kc, const void* vc, const int* len,
+                   float* out, int batch, int nh, int nkv, int hd, float scale, int maxt, int nsplit,
+                   int kv_dtype, void* ws, size_t ws_bytes) {
+  return attn_impl(ctx, q, kc, vc, len, out, batch, nh, nkv, hd, scale, maxt, nsplit, kv_dtype, ws, ws_bytes,
+                   nh * hd, 0);
+}
+
+int lt_attn_prefill(lt_ctx* ctx, const float* q, int q_stride, const void* kc, const void* vc, const int* len0,
+                    float* out, int T, int nh, int nkv, int hd, float scale, int maxt, int nsplit, int kv_dtype,
+                    void* ws, size_t ws_bytes) {
+  return attn_impl(ctx, q, kc, vc, len0, out, T, nh, nkv, hd, scale, maxt, nsplit, kv_dtype, ws, ws_bytes,
+                   q_stride, 1);
 }
 
 }  // extern "C"

@@ -1,0 +1,312 @@
+// lt_prefill.hip -- the batched (prefill) path: a tiled int8-MFMA Q8_0 GEMM and the
+// batched RoPE / KV append that go with it.
+//
+// The reference prefills one token at a time through the decode GEMV and requires any
+// batched prefill to stay "device-uniform": every element bit-identical to the
+// single-token path (bpd/lib/dev_residency.py:1338-1356).  The GEMM here meets that
+// exactly.  For a 32-row x 32-token tile, one v_mfma_i32_32x32x32_i8 per Q8_0 block gives
+// the exact int32 block dots isum[n][t]; the fp32 arithmetic then replays the GEMV's
+// canonical order (q8_0_from_facts.pl:466-516) per element:
+//   leaf L (0..31) = fma-fold over blocks L, L+32, ... of wd*xd*isum (one rounding each),
+//   result = the 5-level pairwise tree over the 32 leaves.
+// The leaves are visited in bit-reversed order, which is the post-order of that tree, so a
+// stack of 5 partial sums per element replays the pairing with every addition in place.
+#include "lt_q8_device.h"
+
+namespace {
+
+using namespace lt;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int kGemmWaves = 4;                  // waves per workgroup: 4 x 32 tokens share 32 rows
+constexpr int kGemmTokens = 32 * kGemmWaves;   // tokens per workgroup
+
+enum GemmEpi { GE_STORE = 0, GE_BIAS = 1, GE_RESID = 2, GE_SILU = 3 };
+
+struct GemmParams {
+  const uint8_t* W;      // Q8_0 blocks [N][K/32]
+  const int8_t* Xq;      // [T][K]
+  const uint16_t* Xd;    // [T][K/32] fp16 bits
+  const float* bias;     // [N] (GE_BIAS)
+  const float* resid;    // [T][N] (GE_RESID)
+  float* Y;              // [T][N], or [T][N/2] for GE_SILU
+  int T, N, K;
+  int nrt, ntt;          // row tiles (32 rows), token tiles (kGemmTokens)
+};
+
+// C layout of v_mfma_i32_32x32x32_i8: register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4,
+// column l%32.  A lane l supplies row l%32, B lane l column l%32, each the 16 bytes
+// 16*(l/32) .. +16 of the block (the same half of k for A and B).
+__device__ __forceinline__ int c_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+template <GemmEpi EPI>
+__global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
+  __shared__ __attribute__((aligned(16))) float s_wd[kGemmWaves][32];
+  const int wave = threadIdx.x >> 6;
+  const int l = threadIdx.x & 63;
+  const int h = l >> 5;
+  const int c = l & 31;
+
+  // XCD-aware tile order: workgroups are dispatched round robin over the 8 XCDs, so the
+  // token tiles of one row tile get ids 8 apart and share an XCD (and its L2).
+  const int g = blockIdx.x;
+  const int rt = (g / (8 * P.ntt)) * 8 + (g & 7);
+  const int tt = (g >> 3) % P.ntt;
+  if (rt >= P.nrt) return;   // uniform per workgroup
+  const int n0 = rt * 32;
+  const int t0 = tt * kGemmTokens + wave * 32;
+  const int nb = P.K >> 5;
+
+  // A lane: weight row n0 + c (clamped; results of clamped rows are discarded)
+  const int arow = n0 + c < P.N ? n0 + c : P.N - 1;
+  const uint32_t row_off = (uint32_t)arow * (uint32_t)nb * (uint32_t)kBlockBytes;
+  const uint32_t mat_bytes = (uint32_t)P.N * (uint32_t)nb * (uint32_t)kBlockBytes;
+  // the 16 quant bytes of a block half begin 2 bytes into the block; the 5th dword can lie
+  // past the matrix: buffer loads bound it (out-of-range dwords read as zero)
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)P.W, 0, (int)((mat_bytes + 3u) & ~3u), 0x00020000);
+  // B lane: token t0 + c (clamped)
+  const int btok = t0 + c < P.T ? t0 + c : P.T - 1;
+  const int8_t* xrow = P.Xq + (size_t)btok * P.K + 16 * h;
+  const uint16_t* xdrow = P.Xd + (size_t)btok * nb;
+
+  auto block = [&](int b, float (&p)[16]) {
+    const uint32_t off = row_off + (uint32_t)b * (uint32_t)kBlockBytes;
+    const uint32_t start = off + 2u + 16u * (uint32_t)h;
+    const uint32_t base = start & ~3u;
+    const uint32_t sh = start & 3u;   // 0 or 2
+    const v4i w03 = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)base, 0, 0));
+    const uint32_t w4 = __builtin_amdgcn_raw_buffer_load_b32(wr, (int)(base + 16u), 0, 0);
+    v4i a;
+    a.x = (int)__builtin_amdgcn_alignbyte((uint32_t)w03.y, (uint32_t)w03.x, sh);
+    a.y = (int)__builtin_amdgcn_alignbyte((uint32_t)w03.z, (uint32_t)w03.y, sh);
+    a.z = (int)__builtin_amdgcn_alignbyte((uint32_t)w03.w, (uint32_t)w03.z, sh);
+    a.w = (int)__builtin_amdgcn_alignbyte(w4, (uint32_t)w03.w, sh);
+    v4i bq;
+    __builtin_memcpy(&bq, xrow + 32 * b, 16);
+    const float xd = lt_h2f(xdrow[b]);
+    // this wave's 32 row scales of block b, one per A lane, fanned out through LDS
+    if (h == 0) s_wd[wave][c] = lt_h2f(*(const uint16_t*)(P.W + off));
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float wd[16];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      float4 v4;
+      __builtin_memcpy(&v4, &s_wd[wave][8 * q + 4 * h], 16);
+      wd[4 * q + 0] = v4.x; wd[4 * q + 1] = v4.y; wd[4 * q + 2] = v4.z; wd[4 * q + 3] = v4.w;
+    }
+    const v16i z = {};
+    const v16i isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, z, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 16; r++) p[r] = fmaf(wd[r] * xd, (float)isum[r], p[r]);
+    // the scales are read before the next block's writes (LDS keeps a wave's order)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  float st[5][16];   // pending partial sums of the tree, one per level
+  float v[16];
+  for (int i = 0; i < 32; i++) {
+    const int L = (int)(__builtin_bitreverse32((uint32_t)i) >> 27);
+#pragma unroll
+    for (int r = 0; r < 16; r++) v[r] = 0.0f;
+    for (int b = L; b < nb; b += 32) block(b, v);
+    // combine: leaf i closes every level whose bit is set in i (i is uniform, and the
+    // register indices are static, so the stack stays in registers)
+    bool carry = true;
+#pragma unroll
+    for (int lvl = 0; lvl < 5; lvl++) {
+      if (carry) {
+        if ((i >> lvl) & 1) {
+#pragma unroll
+          for (int r = 0; r < 16; r++) v[r] = st[lvl][r] + v[r];
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; r++) st[lvl][r] = v[r];
+          carry = false;
+        }
+      }
+    }
+  }
+  // after leaf 31 every level has closed: v holds the row values
+  const float* res = v;
+
+  const int t = t0 + c;
+  if (t >= P.T) return;
+  if constexpr (EPI == GE_SILU) {
+    // rows 2j (gate) and 2j+1 (up) are registers r, r+1 of the same lane
+    const int F = P.N >> 1;
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) {
+      const int n = n0 + c_row(r, h);
+      if (n < P.N) P.Y[(size_t)t * F + (n >> 1)] = lt_silu_mul(res[r], res[r + 1]);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int n = n0 + c_row(r, h);
+      if (n < P.N) {
+        float o = res[r];
+        if constexpr (EPI == GE_BIAS) o = o + P.bias[n];
+        if constexpr (EPI == GE_RESID) o = o + P.resid[(size_t)t * P.N + n];
+        P.Y[(size_t)t * P.N + n] = o;
+      }
+    }
+  }
+}
+
+// RoPE of T rows of q|k at positions *pos0 + t (k_rope's arithmetic per token).
+__global__ __launch_bounds__(256) void k_rope_batch(float* __restrict__ x, int T, int row_stride,
+                                                    const int* __restrict__ pos0, int nheads, int hd,
+                                                    const float* __restrict__ freqs) {
+  const int half = hd >> 1;
+  const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long per_tok = (long)nheads * half;
+  if (gid >= per_tok * T) return;
+  const int t = (int)(gid / per_tok);
+  const int rem = (int)(gid - (long)t * per_tok);
+  const int hh = rem / half;
+  const int j = rem - hh * half;
+  const float ang = (float)(*pos0 + t) * freqs[j];
+  float s, cc;
+  lt_sincosf(ang, &s, &cc);
+  float* base = x + (size_t)t * row_stride + (size_t)hh * hd;
+  const float x1 = base[j], x2 = base[j + half];
+  base[j] = fmaf(x1, cc, -(x2 * s));
+  base[j + half] = fmaf(x1, s, x2 * cc);
+}
+
+// KV append of T rows (k_append_kv_incr per token): rows *len .. *len+T-1 (those below
+// maxt).  The length is bumped by k_len_add, after the attention that reads it.
+template <bool kF16>
+__global__ __launch_bounds__(256) void k_kv_append_batch(void* __restrict__ kc, void* __restrict__ vc,
+                                                         const float* __restrict__ src, int src_stride,
+                                                         int k_off, int v_off, int T,
+                                                         const int* __restrict__ len, int width, int maxt) {
+  const int t = blockIdx.x;
+  const int L = *len + t;
+  if (L < 0 || L >= maxt) return;  // uniform per workgroup
+  const float* row = src + (size_t)t * src_stride;
+  for (int i = threadIdx.x; i < width; i += blockDim.x) {
+    const size_t off = (size_t)L * width + i;
+    if (kF16) {
+      ((uint16_t*)kc)[off] = lt_float_to_half_bits(row[k_off + i]);
+      ((uint16_t*)vc)[off] = lt_float_to_half_bits(row[v_off + i]);
+    } else {
+      ((float*)kc)[off] = row[k_off + i];
+      ((float*)vc)[off] = row[v_off + i];
+    }
+  }
+}
+
+// Embedding rows of T device token ids from Q8_0 token_embd (x = q*d, exact); a token
+// outside [0, vocab) gives a zero row and sets *err.
+__global__ __launch_bounds__(256) void k_embed_batch(const uint8_t* __restrict__ emb, const int* __restrict__ toks,
+                                                     float* __restrict__ x, int E, int vocab, int* __restrict__ err) {
+  const int t = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= E) return;
+  const int tk = toks[t];
+  float v = 0.0f;
+  if (tk < 0 || tk >= vocab) {
+    if (err && i == 0) *err = 1;
+  } else {
+    const uint8_t* blk = emb + ((size_t)tk * (E / 32) + (i >> 5)) * kBlockBytes;
+    const uint16_t d = (uint16_t)(blk[0] | (blk[1] << 8));
+    v = (float)(int8_t)blk[2 + (i & 31)] * lt_h2f(d);
+  }
+  x[(size_t)t * E + i] = v;
+}
+
+__global__ void k_len_add(int* __restrict__ len, int T, int maxt) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    const int L = *len + T;
+    *len = L < maxt ? L : maxt;
+  }
+}
+
+int check_gemm(const char* fn, const void* W, const int8_t* Xq, const uint16_t* Xd, const float* Y, int T, int N,
+               int K) {
+  LT_REQUIRE(W && Xq && Xd && Y, "%s: null argument", fn);
+  LT_REQUIRE(T > 0 && N > 0 && K > 0 && K % 32 == 0, "%s: T=%d N=%d K=%d (K multiple of 32)", fn, T, N, K);
+  LT_REQUIRE((uint64_t)N * (uint64_t)(K / 32) * 34u < ((uint64_t)1 << 31),
+             "%s: a %d x %d Q8_0 matrix must be below 2 GiB (split it by rows)", fn, N, K);
+  LT_REQUIRE(lt_aligned(W, 4) && lt_aligned(Xq, 16) && lt_aligned(Xd, 2), "%s: misaligned argument", fn);
+  return LT_OK;
+}
+
+template <GemmEpi EPI>
+int launch_gemm(lt_ctx* ctx, GemmParams P) {
+  P.nrt = (P.N + 31) / 32;
+  P.ntt = (P.T + kGemmTokens - 1) / kGemmTokens;
+  const long grid = (long)((P.nrt + 7) / 8) * 8 * P.ntt;
+  k_q8_gemm<EPI><<<(unsigned)grid, 256, 0, ctx->stream>>>(P);
+  return lt_check_launch("k_q8_gemm");
+}
+
+}  // namespace
+
+extern "C" {
+
+int lt_q8_gemm(lt_ctx* ctx, const void* W, const int8_t* Xq, const uint16_t* Xd, const float* bias,
+               const float* resid, float* Y, int T, int N, int K) {
+  LT_REQUIRE(ctx, "lt_q8_gemm: null ctx");
+  if (int rc = check_gemm("lt_q8_gemm", W, Xq, Xd, Y, T, N, K)) return rc;
+  LT_REQUIRE(!(bias && resid), "lt_q8_gemm: give bias or resid, not both");
+  GemmParams P{};
+  P.W = (const uint8_t*)W; P.Xq = Xq; P.Xd = Xd; P.bias = bias; P.resid = resid; P.Y = Y;
+  P.T = T; P.N = N; P.K = K;
+  if (bias) return launch_gemm<GE_BIAS>(ctx, P);
+  if (resid) return launch_gemm<GE_RESID>(ctx, P);
+  return launch_gemm<GE_STORE>(ctx, P);
+}
+
+int lt_q8_gemm_silu(lt_ctx* ctx, const void* Wgu, const int8_t* Xq, const uint16_t* Xd, float* V, int T, int F,
+                    int K) {
+  LT_REQUIRE(ctx && F > 0, "lt_q8_gemm_silu: null ctx or F=%d", F);
+  if (int rc = check_gemm("lt_q8_gemm_silu", Wgu, Xq, Xd, V, T, 2 * F, K)) return rc;
+  GemmParams P{};
+  P.W = (const uint8_t*)Wgu; P.Xq = Xq; P.Xd = Xd; P.Y = V;
+  P.T = T; P.N = 2 * F; P.K = K;
+  return launch_gemm<GE_SILU>(ctx, P);
+}
+
+int lt_rope_batch(lt_ctx* ctx, float* qk, int T, int row_stride, const int* pos0, int nheads, int hd,
+                  const float* freqs) {
+  LT_REQUIRE(ctx && qk && pos0 && freqs, "lt_rope_batch: null argument");
+  LT_REQUIRE(T > 0 && nheads > 0 && hd > 0 && hd % 2 == 0 && row_stride >= nheads * hd,
+             "lt_rope_batch: T=%d nheads=%d hd=%d row_stride=%d", T, nheads, hd, row_stride);
+  const long total = (long)T * nheads * (hd / 2);
+  k_rope_batch<<<(unsigned)((total + 255) / 256), 256, 0, ctx->stream>>>(qk, T, row_stride, pos0, nheads, hd, freqs);
+  return lt_check_launch("k_rope_batch");
+}
+
+int lt_kv_append_batch(lt_ctx* ctx, void* kc, void* vc, const float* src, int src_stride, int k_off, int v_off,
+                       int T, const int* len, int width, int maxt, int kv_dtype) {
+  LT_REQUIRE(ctx && kc && vc && src && len, "lt_kv_append_batch: null argument");
+  LT_REQUIRE(T > 0 && width > 0 && maxt > 0, "lt_kv_append_batch: T=%d width=%d maxt=%d", T, width, maxt);
+  LT_REQUIRE(kv_dtype == LT_KV_F32 || kv_dtype == LT_KV_F16, "lt_kv_append_batch: kv_dtype=%d", kv_dtype);
+  if (kv_dtype == LT_KV_F16)
+    k_kv_append_batch<true><<<T, 256, 0, ctx->stream>>>(kc, vc, src, src_stride, k_off, v_off, T, len, width, maxt);
+  else
+    k_kv_append_batch<false><<<T, 256, 0, ctx->stream>>>(kc, vc, src, src_stride, k_off, v_off, T, len, width, maxt);
+  return lt_check_launch("k_kv_append_batch");
+}
+
+int lt_embed_q8_batch(lt_ctx* ctx, const void* emb, const int* toks, float* x, int T, int E, int vocab, int* err) {
+  LT_REQUIRE(ctx && emb && toks && x, "lt_embed_q8_batch: null argument");
+  LT_REQUIRE(T > 0 && E > 0 && E % 32 == 0 && vocab > 0, "lt_embed_q8_batch: T=%d E=%d vocab=%d", T, E, vocab);
+  k_embed_batch<<<dim3((E + 255) / 256, T), 256, 0, ctx->stream>>>((const uint8_t*)emb, toks, x, E, vocab, err);
+  return lt_check_launch("k_embed_batch");
+}
+
+int lt_len_add(lt_ctx* ctx, int* len, int T, int maxt) {
+  LT_REQUIRE(ctx && len && T >= 0 && maxt > 0, "lt_len_add: bad argument");
+  k_len_add<<<1, 64, 0, ctx->stream>>>(len, T, maxt);
+  return lt_check_launch("k_len_add");
+}
+
+}  // extern "C"

@@ -464,7 +464,16 @@ class DecodePlan:
                                      len_ptr=self.lens.ptr + 4 * il, dev=D)
                        for il in range(cfg.n_layers)]
         self.scale = float(hd ** -0.5)
+        self._prefill: PrefillBuffers | None = None
         self.reset()
+
+    def prefill_buffers(self, T: int) -> "PrefillBuffers":
+        if self._prefill is None or self._prefill.T < T:
+            if self._prefill is not None:
+                self.dev.sync()
+                self._prefill.free()
+            self._prefill = PrefillBuffers(self, max(T, 32))
+        return self._prefill
 
     # -- state --------------------------------------------------------------------
     def reset(self) -> None:
@@ -600,6 +609,8 @@ class DecodePlan:
             c.length += 1
 
     def free(self) -> None:
+        if self._prefill is not None:
+            self._prefill.free()
         for c in self.caches:
             c.free()
         for t in (self.tok, self.err, self.hist, self.hist_count, self.lens, self.resid_in, self.carry,
@@ -607,6 +618,81 @@ class DecodePlan:
                   self.am_ws, self.attn_ws):
             if t is not None:
                 t.free()
+
+
+class PrefillBuffers:
+    """Device buffers of a batched prefill of up to T tokens."""
+
+    def __init__(self, plan: "DecodePlan", T: int):
+        cfg, D = plan.cfg, plan.dev
+        E, F = cfg.n_embd, cfg.n_ff
+        kmax = max(E, F, cfg.q_dim)
+        self.T = T
+        self.toks = DevTensor.empty((T,), np.int32, D)
+        self.x = DevTensor.empty((T, E), np.float32, D)
+        self.h = DevTensor.empty((T, E), np.float32, D)
+        self.xres = DevTensor.empty((T, E), np.float32, D)
+        self.qkv = DevTensor.empty((T, cfg.n_qkv), np.float32, D)
+        self.att = DevTensor.empty((T, cfg.q_dim), np.float32, D)
+        self.v = DevTensor.empty((T, F), np.float32, D)
+        self.xq = DevTensor.empty((T * kmax,), np.int8, D)
+        self.xd = DevTensor.empty((T * kmax // 32,), np.uint16, D)
+        aw = _lib.raw("lt_attn_workspace_size")(T, cfg.n_head, cfg.head_dim, plan.profile.attn_nsplit)
+        self.ws = DevTensor.empty((aw,), np.uint8, D) if aw else None
+
+    def free(self) -> None:
+        for t in (self.toks, self.x, self.h, self.xres, self.qkv, self.att, self.v, self.xq, self.xd, self.ws):
+            if t is not None:
+                t.free()
+
+
+def forward_prefill(plan: DecodePlan, tokens) -> None:
+    """Batched prefill of a prompt: every linear layer runs once over all T tokens through
+    the tiled int8-MFMA Q8_0 GEMM (lt_q8_gemm), with batched RMSNorm/quant/RoPE/KV append and
+    causal attention.  It is device-uniform with the single-token path the reference uses
+    (bpd/lib/dev_residency.py:1338-1356): the KV cache, the last token's logits and the
+    greedy token it leaves on the device are bit-identical to forward_pass_resident's."""
+    toks = np.asarray([int(t) for t in np.asarray(tokens).reshape(-1)], np.int32)
+    T = int(toks.size)
+    if T == 0:
+        return
+    cfg, m, p, D = plan.cfg, plan.model, plan.profile, plan.dev
+    if plan.caches[0].length + T > plan.max_ctx:
+        raise ValueError(f"prefill of {T} tokens overflows the {plan.max_ctx}-position KV cache")
+    if "wgu_il" not in m.layers[0]:
+        raise ValueError("forward_prefill needs the fused gate|up layout (ResidentModel layouts 'fused' or 'both')")
+    B = plan.prefill_buffers(T)
+    h = D.handle
+    E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
+    QD, KD, NQ = cfg.q_dim, cfg.kv_dim, cfg.n_qkv
+    eps = ctypes.c_float(cfg.norm_eps)
+    D.h2d(B.toks.ptr, toks)
+    call("lt_embed_q8_batch", h, m.tok_embd.t.vp, B.toks.vp, B.x.vp, T, E, cfg.vocab, plan.err.vp)
+    ws, ws_n = _vp(B.ws), (B.ws.nbytes if B.ws is not None else 0)
+    for il, L in enumerate(m.layers):
+        cache = plan.caches[il]
+        lp = _vp(cache.len_ptr)
+        call("lt_rmsnorm", h, B.x.vp, L["attn_norm"].vp, B.h.vp, T, E, eps)
+        call("lt_quant_q8", h, B.h.vp, B.xq.vp, B.xd.vp, T * E)
+        call("lt_q8_gemm", h, L["wqkv"].t.vp, B.xq.vp, B.xd.vp, _vp(L["bqkv"]), None, B.qkv.vp, T, NQ, E)
+        call("lt_rope_batch", h, B.qkv.vp, T, NQ, lp, nh + nkv, hd, m.freqs.vp)
+        call("lt_kv_append_batch", h, cache.k.vp, cache.v.vp, B.qkv.vp, NQ, QD, QD + KD, T, lp, KD,
+             cache.max_seq, p.kv_dtype)
+        call("lt_attn_prefill", h, B.qkv.vp, NQ, cache.k.vp, cache.v.vp, lp, B.att.vp, T, nh, nkv, hd,
+             ctypes.c_float(plan.scale), cache.max_seq, p.attn_nsplit, p.kv_dtype, ws, ws_n)
+        call("lt_len_add", h, lp, T, cache.max_seq)
+        call("lt_quant_q8", h, B.att.vp, B.xq.vp, B.xd.vp, T * QD)
+        call("lt_q8_gemm", h, L["wo"].t.vp, B.xq.vp, B.xd.vp, None, B.x.vp, B.xres.vp, T, E, QD)
+        call("lt_rmsnorm", h, B.xres.vp, L["ffn_norm"].vp, B.h.vp, T, E, eps)
+        call("lt_quant_q8", h, B.h.vp, B.xq.vp, B.xd.vp, T * E)
+        call("lt_q8_gemm_silu", h, L["wgu_il"].t.vp, B.xq.vp, B.xd.vp, B.v.vp, T, F, E)
+        call("lt_quant_q8", h, B.v.vp, B.xq.vp, B.xd.vp, T * F)
+        call("lt_q8_gemm", h, L["wdown"].t.vp, B.xq.vp, B.xd.vp, None, B.xres.vp, B.x.vp, T, E, F)
+        cache.length += T
+    # the last token's logits and greedy token, as the decode step computes them
+    D.d2d(plan.carry.ptr, B.x.ptr + (T - 1) * E * 4, E * 4)
+    call("lt_q8_gemv_rms_argmax", h, plan.carry.vp, m.output_norm.vp, eps, m.output.t.vp, plan.logits.vp,
+         cfg.vocab, E, plan.tok.vp, None, None, 0, plan.am_ws.vp, plan.am_ws.nbytes)
 
 
 def forward_pass_resident(plan: DecodePlan, tokens) -> np.ndarray:
@@ -628,10 +714,15 @@ class GraphRunner:
         self.graph = ctypes.c_void_p()
         self.captured = False
 
-    def seed(self, prompt) -> np.ndarray:
+    def seed(self, prompt, batched: bool = False) -> np.ndarray:
         """Eager prefill over the prompt (fixed buffers, all kernels loaded); returns the
-        last prompt token's logits.  The device token then holds the first greedy token."""
-        logits = forward_pass_resident(self.plan, prompt)
+        last prompt token's logits.  The device token then holds the first greedy token.
+        batched=True runs forward_prefill (the int8-MFMA GEMM path; bit-identical)."""
+        if batched:
+            forward_prefill(self.plan, prompt)
+            logits = self.plan.read_logits()
+        else:
+            logits = forward_pass_resident(self.plan, prompt)
         self.dev.sync()
         return logits
 
