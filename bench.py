@@ -139,6 +139,105 @@ def gemv_sweep(dev, launches: int = 40) -> list[dict]:
     return out
 
 
+INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, TOP/s (2 ops per MAC)
+
+
+def attention_sweep(dev, reps: int = 20) -> list[dict]:
+    """GQA decode attention, 32 Q / 8 KV heads, head_dim 128, fp16 KV
+    N(0,1), one query token per sequence, L in {4k, 16k, 32k}, batch 1 and 8 (split-K over
+    context with the ascending-split merge).  Algorithmic bytes: the K and V rows read plus
+    q and out."""
+    from llamatov_amd import dev_residency as dr
+    from llamatov_amd._lib import LT_KV_F16, call, raw
+    out = []
+    nh, nkv, hd = 32, 8, 128
+    rng = np.random.default_rng(9)
+    for L in (4096, 16384, 32768):
+        for B in (1, 8):
+            kv = (rng.standard_normal((B * L * nkv * hd,), dtype=np.float32)).astype(np.float16).view(np.uint16)
+            kc = dr.DevTensor.from_host(kv, dev)
+            vc = dr.DevTensor.from_host(kv[::-1].copy(), dev)
+            del kv
+            q = dr.DevTensor.from_host(rng.standard_normal(B * nh * hd).astype(np.float32), dev)
+            lens = dr.DevTensor.from_host(np.full(B, L, np.int32), dev)
+            o = dr.DevTensor.empty((B * nh * hd,), np.float32, dev)
+            nsplit = max(1, min(256, (L + 255) // 256 if B == 1 else (L + 1023) // 1024))
+            wsn = raw("lt_attn_workspace_size")(B, nh, hd, nsplit)
+            ws = dr.DevTensor.empty((max(wsn, 16),), np.uint8, dev)
+            args = (dev.handle, q.vp, kc.vp, vc.vp, lens.vp, o.vp, B, nh, nkv, hd, ctypes.c_float(hd ** -0.5), L,
+                    nsplit, LT_KV_F16, ws.vp, ws.nbytes)
+            call("lt_attn_decode", *args)
+            dev.sync()
+            ev = Events(dev)
+            ev.start()
+            for _ in range(reps):
+                call("lt_attn_decode", *args)
+            ms = ev.stop_ms() / reps
+            ev.free()
+            alg = B * 2 * L * nkv * hd * 2 + 2 * B * nh * hd * 4
+            out.append({"L": L, "batch": B, "nsplit": nsplit, "us": round(ms * 1e3, 2),
+                        "GB/s": round(alg / (ms * 1e-3) / 1e9, 1), "frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+            log(f"attention L={L} B={B} nsplit={nsplit}: {ms * 1e3:.1f} us, {alg / (ms * 1e-3) / 1e9:.0f} GB/s")
+            for t in (kc, vc, q, lens, o, ws):
+                t.free()
+    return out
+
+
+def c5_leg(dev, n_prefill: int = 512, n_decode: int = 256, eager: bool = False) -> dict:
+    """random-init Llama-3-8B-architecture Q8_0 model (N(0,0.02) weights
+    quantized with the engine quantizer), a 512-token prefill of random ids through the
+    tiled int8-MFMA GEMM, then 256 greedy decode tokens (graph replay) with an fp16 KV cache."""
+    from llamatov_amd import dev_residency as dr
+    from llamatov_amd import model as M
+    from llamatov_amd._lib import LT_KV_F16
+    cfg = M.LLAMA3_8B
+    t0 = time.perf_counter()
+    w = M.synth_weights(cfg, seed=4321)
+    log(f"C5 weights generated in {time.perf_counter() - t0:.1f}s")
+    model = dr.ResidentModel(cfg, w, dev, layouts="fused")
+    del w
+    plan = dr.DecodePlan(model, dr.Profile(kv_dtype=LT_KV_F16), max_ctx=n_prefill + n_decode + 8, hist_cap=4096)
+    prompt = M.random_prompt(cfg, n_prefill, seed=17)
+    # warm the prefill kernels on a short prompt, then rewind
+    dr.forward_prefill(plan, prompt[:8])
+    plan.prefill_buffers(n_prefill)      # activation buffers are set-up, not prefill work
+    dev.sync()
+    plan.reset()
+    ev = Events(dev)
+    ev.start()
+    dr.forward_prefill(plan, prompt)
+    pre_ms = ev.stop_ms()
+    macs = n_prefill * cfg.n_layers * (cfg.n_qkv * cfg.n_embd + cfg.n_embd * cfg.q_dim + 2 * cfg.n_ff * cfg.n_embd
+                                      + cfg.n_embd * cfg.n_ff)
+    runner = dr.GraphRunner(plan)
+    one = plan.step if eager else runner._launch
+    if not eager:
+        runner.capture()
+    for _ in range(4):   # warm replay (these tokens are part of the decode)
+        one()
+    dev.sync()
+    ev.start()
+    for _ in range(n_decode - 4):
+        one()
+    dec_ms = ev.stop_ms()
+    tok_s = (n_decode - 4) / (dec_ms / 1e3)
+    kv_bytes = sum(cfg.n_layers * 2 * (n_prefill + i + 1) * cfg.kv_dim * 2 for i in range(n_decode)) / n_decode
+    step_bytes = cfg.weight_bytes() + kv_bytes
+    res = {"model": cfg.name, "prefill_tokens": n_prefill, "prefill_ms": round(pre_ms, 3),
+           "prefill_tok_s": round(n_prefill / (pre_ms / 1e3), 1),
+           "prefill_mfma_util": round(2 * macs / (pre_ms / 1e3) / (INT8_PEAK_TOPS * 1e12), 4),
+           "prefill_gemm_macs": int(macs), "decode_tokens": n_decode, "decode_tok_s": round(tok_s, 2),
+           "decode_ms_per_token": round(dec_ms / (n_decode - 4), 4), "decode_step_bytes": int(step_bytes),
+           "decode_roofline_frac": round(step_bytes * tok_s / (HBM_PEAK_GBS * 1e9), 4)}
+    log(f"C5: prefill {pre_ms:.1f} ms ({res['prefill_mfma_util'] * 100:.1f}% of int8 MFMA peak), "
+        f"decode {tok_s:.1f} tok/s")
+    ev.free()
+    runner.free()
+    plan.free()
+    model.free()
+    return res
+
+
 def cpu_baseline(cfg, weights, prompt, n_decode: int, kv_f16: bool) -> tuple[dict, list[int]]:
     from oracle import oracle as orc
     m = orc.OracleModel(cfg, weights, kv_f16=kv_f16)
@@ -168,6 +267,9 @@ def main() -> int:
     ap.add_argument("--cpu-tokens", type=int, default=128, help="decode tokens in the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--c4", action="store_true", help="also time BASELINE config 4 attention (adds c4_attention)")
+    ap.add_argument("--c5", action="store_true",
+                    help="also run BASELINE config 5 (Llama-3-8B arch: 512-token MFMA prefill + 256 decode; adds c5)")
     ap.add_argument("--gemv-sweep", action="store_true",
                     help="also time the Q8_0 GEMV on the BASELINE config 1/3 shapes (adds gemv_sweep)")
     ap.add_argument("--per-op", action="store_true",
@@ -290,6 +392,9 @@ def main() -> int:
     if args.gemv_sweep:
         log("GEMV sweep")
         result["gemv_sweep"] = gemv_sweep(dev)
+    if args.c4:
+        log("C4 attention sweep")
+        result["c4_attention"] = attention_sweep(dev)
 
     if not args.no_cpu_baseline:
         n_cpu = min(args.cpu_tokens, args.steps)
@@ -299,6 +404,11 @@ def main() -> int:
         result["tokens_match_cpu"] = cpu_tokens == tokens[:n_cpu]
 
     runner.free()
+    if args.c5:
+        plan.free()
+        model.free()
+        log("C5 leg")
+        result["c5"] = c5_leg(dev, eager=args.eager)
     print(json.dumps(result), flush=True)
     return 0
 

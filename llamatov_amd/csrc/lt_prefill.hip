@@ -22,6 +22,7 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kGemmWaves = 4;                  // waves per workgroup: 4 x 32 tokens share 32 rows
 constexpr int kGemmTokens = 32 * kGemmWaves;   // tokens per workgroup
+constexpr int kDepth = 4;                      // blocks in flight per wave
 
 enum GemmEpi { GE_STORE = 0, GE_BIAS = 1, GE_RESID = 2, GE_SILU = 3 };
 
@@ -71,23 +72,33 @@ __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
   const int8_t* xrow = P.Xq + (size_t)btok * P.K + 16 * h;
   const uint16_t* xdrow = P.Xd + (size_t)btok * nb;
 
-  auto block = [&](int b, float (&p)[16]) {
+  // Operands of one block, prefetched: the A lane's 16 quant bytes (realigned), its row's
+  // scale, and the B lane's 16 quant bytes and scale.
+  struct Ops {
+    v4i a, bq;
+    float wd, xd;
+  };
+  auto load_ops = [&](int b, Ops& o) {
     const uint32_t off = row_off + (uint32_t)b * (uint32_t)kBlockBytes;
     const uint32_t start = off + 2u + 16u * (uint32_t)h;
     const uint32_t base = start & ~3u;
     const uint32_t sh = start & 3u;   // 0 or 2
     const v4i w03 = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)base, 0, 0));
     const uint32_t w4 = __builtin_amdgcn_raw_buffer_load_b32(wr, (int)(base + 16u), 0, 0);
-    v4i a;
-    a.x = (int)__builtin_amdgcn_alignbyte((uint32_t)w03.y, (uint32_t)w03.x, sh);
-    a.y = (int)__builtin_amdgcn_alignbyte((uint32_t)w03.z, (uint32_t)w03.y, sh);
-    a.z = (int)__builtin_amdgcn_alignbyte((uint32_t)w03.w, (uint32_t)w03.z, sh);
-    a.w = (int)__builtin_amdgcn_alignbyte(w4, (uint32_t)w03.w, sh);
-    v4i bq;
-    __builtin_memcpy(&bq, xrow + 32 * b, 16);
-    const float xd = lt_h2f(xdrow[b]);
-    // this wave's 32 row scales of block b, one per A lane, fanned out through LDS
-    if (h == 0) s_wd[wave][c] = lt_h2f(*(const uint16_t*)(P.W + off));
+    o.a.x = (int)__builtin_amdgcn_alignbyte((uint32_t)w03.y, (uint32_t)w03.x, sh);
+    o.a.y = (int)__builtin_amdgcn_alignbyte((uint32_t)w03.z, (uint32_t)w03.y, sh);
+    o.a.z = (int)__builtin_amdgcn_alignbyte((uint32_t)w03.w, (uint32_t)w03.z, sh);
+    o.a.w = (int)__builtin_amdgcn_alignbyte(w4, (uint32_t)w03.w, sh);
+    __builtin_memcpy(&o.bq, xrow + 32 * b, 16);
+    o.xd = lt_h2f(xdrow[b]);
+    o.wd = lt_h2f(*(const uint16_t*)(P.W + off));
+  };
+  // fold one block into the leaf's 16 running sums: exact MFMA dots, then
+  // v = fma(wd*xd, isum, v) per element (the row scales reach the C rows through LDS)
+  auto fold_ops = [&](const Ops& o, float (&v)[16]) {
+    const v16i z = {};
+    const v16i isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, o.bq, z, 0, 0, 0);
+    if (h == 0) s_wd[wave][c] = o.wd;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -98,41 +109,87 @@ __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
       __builtin_memcpy(&v4, &s_wd[wave][8 * q + 4 * h], 16);
       wd[4 * q + 0] = v4.x; wd[4 * q + 1] = v4.y; wd[4 * q + 2] = v4.z; wd[4 * q + 3] = v4.w;
     }
-    const v16i z = {};
-    const v16i isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, z, 0, 0, 0);
-#pragma unroll
-    for (int r = 0; r < 16; r++) p[r] = fmaf(wd[r] * xd, (float)isum[r], p[r]);
     // the scales are read before the next block's writes (LDS keeps a wave's order)
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int r = 0; r < 16; r++) v[r] = fmaf(wd[r] * o.xd, (float)isum[r], v[r]);
   };
 
-  float st[5][16];   // pending partial sums of the tree, one per level
-  float v[16];
-  for (int i = 0; i < 32; i++) {
-    const int L = (int)(__builtin_bitreverse32((uint32_t)i) >> 27);
+  // The blocks in post-order: leaf i (0..31) is lane L = bitrev5(i) and holds blocks
+  // L, L+32, ... < nb (leaves with L >= nb hold none).  A producer cursor walks that
+  // sequence kDepth blocks ahead of the consumer, refilling a ring of prefetched operands.
+  auto leaf_lane = [](int i) { return (int)(__builtin_bitreverse32((uint32_t)i) >> 27); };
+  int pi = 0, pb = 0;   // producer: leaf, next block (pb = -1: done)
+  auto produce = [&](Ops& o) {
+    if (pb >= 0) {
+      load_ops(pb, o);
+      pb += 32;
+      while (pb >= nb) {           // next non-empty leaf
+        if (++pi == 32) { pb = -1; break; }
+        pb = leaf_lane(pi);
+      }
+    }
+  };
+  Ops ring[kDepth];
 #pragma unroll
-    for (int r = 0; r < 16; r++) v[r] = 0.0f;
-    for (int b = L; b < nb; b += 32) block(b, v);
-    // combine: leaf i closes every level whose bit is set in i (i is uniform, and the
-    // register indices are static, so the stack stays in registers)
+  for (int d = 0; d < kDepth; d++) produce(ring[d]);
+
+  float st[5][16];   // pending partial sums of the tree, one per level
+  float v[16], res[16];
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    v[r] = 0.0f;
+    res[r] = 0.0f;
+  }
+#pragma unroll
+  for (int l2 = 0; l2 < 5; l2++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) st[l2][r] = 0.0f;
+  // combine leaf i into the stack: it closes every level whose bit is set in i (i is
+  // uniform and the register indices are static, so the stack stays in registers)
+  auto close_leaf = [&](int i) {
+    // branch-free selects on static levels: leaf i adds into levels 0.. while their bit
+    // is set and parks its sum at the first clear one
     bool carry = true;
 #pragma unroll
     for (int lvl = 0; lvl < 5; lvl++) {
-      if (carry) {
-        if ((i >> lvl) & 1) {
+      const bool bit = ((i >> lvl) & 1) != 0;
+      const bool comb = carry && bit;
+      const bool park = carry && !bit;
 #pragma unroll
-          for (int r = 0; r < 16; r++) v[r] = st[lvl][r] + v[r];
-        } else {
+      for (int r = 0; r < 16; r++) {
+        const float sum = st[lvl][r] + v[r];
+        st[lvl][r] = park ? v[r] : st[lvl][r];
+        v[r] = comb ? sum : v[r];
+      }
+      carry = comb;
+    }
+    const bool last = i == 31;     // the last leaf closes every level: v is the row value
 #pragma unroll
-          for (int r = 0; r < 16; r++) st[lvl][r] = v[r];
-          carry = false;
+    for (int r = 0; r < 16; r++) res[r] = last ? v[r] : res[r];
+  };
+  int ci = 0, cb = 0;   // consumer: leaf, block
+  for (int s0 = 0; s0 < nb; s0 += kDepth) {
+#pragma unroll
+    for (int d = 0; d < kDepth; d++) {
+      if (s0 + d < nb) {
+        fold_ops(ring[d], v);
+        produce(ring[d]);
+        cb += 32;
+        if (cb >= nb) {            // leaf ci is complete; close it and any empty leaves after it
+          close_leaf(ci);
+          while (++ci < 32 && (cb = leaf_lane(ci)) >= nb) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) v[r] = 0.0f;
+            close_leaf(ci);
+          }
+#pragma unroll
+          for (int r = 0; r < 16; r++) v[r] = 0.0f;
         }
       }
     }
   }
-  // after leaf 31 every level has closed: v holds the row values
-  const float* res = v;
 
   const int t = t0 + c;
   if (t >= P.T) return;
