@@ -261,6 +261,16 @@ LT_API int lt_attn_prefill(lt_ctx* ctx, const float* q, int q_stride, const void
 LT_API int lt_embed_q8_batch(lt_ctx* ctx, const void* emb, const int* toks, float* x, int T, int E, int vocab,
                              int* err);
 
+/* ---- numerics self-check (no reference counterpart: a diagnostic of this build) ----
+ * Runs on the device and writes 4 counters to host memory: out[0] = non-NaN binary32
+ * patterns whose hardware fp16 conversion (the quantizer's scale) differs from
+ * round-to-nearest-even with gradual underflow (all 2^32 - 2^24 + 2 of them are tried),
+ * out[1] = quantizer quotients x / dq formed without division that differ in any bit from
+ * the device's IEEE division (normal quotients), out[2] = those that quantize differently,
+ * out[3] = quotient cases tried (every positive finite fp16 dq, x at and around every
+ * (k + 1/2) * dq for |k| <= 140).  Synchronous; 0 or an error code. */
+LT_API int lt_selftest_numerics(lt_ctx* ctx, unsigned long long* out);
+
 /* ---- graphs (replaces cuStreamBeginCapture/EndCapture/GraphInstantiate/GraphLaunch,
  *      GraphRunner.capture / replay, bpd/lib/dev_residency.py:1732-1818) ---- */
 LT_API int lt_graph_begin(lt_ctx* ctx);

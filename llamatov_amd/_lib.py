@@ -67,6 +67,7 @@ _SIGS = {
     "lt_attn_prefill": (c_int, [_P, _P, c_int, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float, c_int,
                                 c_int, c_int, _P, c_size_t]),
     "lt_embed_q8_batch": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _P]),
+    "lt_selftest_numerics": (c_int, [_P, _P]),
     "lt_graph_begin": (c_int, [_P]),
     "lt_graph_end": (c_int, [_P, POINTER(c_void_p)]),
     "lt_graph_launch": (c_int, [_P, _P]),

@@ -76,71 +76,136 @@ __device__ __forceinline__ bool am_better(float v, int i, float bv, int bi) {
 // waits behind the weights), and its arithmetic runs while the weights are in flight.
 
 // Quantize one 32-element block held one element per lane of a half-wave (k_quant_q8's
-// quantizer: d16 = fp16(amax/127), 1 if amax == 0; q = clamp(rint(v / float(d16)), +-127))
-// and write it into the block's record: byte l+2 of phase E and byte 44+l of phase O hold
-// q of element l; the other bytes of the two phases are zero; dwords 9 and 19 hold the
-// scale as fp32.
+// quantizer) and write it into the block's record: byte l+2 of phase E and byte 44+l of
+// phase O hold q of element l; the other bytes of the two phases are zero; dwords 9 and 19
+// hold the scale as fp32.
 __device__ __forceinline__ void quant_to_rec(float v, int lane, uint32_t* recw) {
-  const float a = halfwave_max(fabsf(v));
-  const uint16_t d16 = lt_q8_scale_bits(a);
-  const float dq = lt_h2f(d16);
-  const int8_t q = (int8_t)lt_q8_quant1(v, dq);
+  const QScale sc = q8_scale(halfwave_max(fabsf(v)));
+  const int8_t q = (int8_t)q8_quant(v, sc);
   uint8_t* rb = (uint8_t*)recw;
   rb[2 + lane] = (uint8_t)q;
   rb[44 + lane] = (uint8_t)q;
   if (lane == 0) {
     ((uint16_t*)rb)[0] = 0;          // E bytes 0, 1
     recw[kRecPhase] = 0u;            // O dword 0
-    recw[9] = __builtin_bit_cast(uint32_t, dq);
-    recw[kRecPhase + 9] = __builtin_bit_cast(uint32_t, dq);
+    recw[9] = __builtin_bit_cast(uint32_t, sc.dq);
+    recw[kRecPhase + 9] = __builtin_bit_cast(uint32_t, sc.dq);
   }
   if (lane == 31) ((uint16_t*)rb)[17] = 0;   // E bytes 34, 35
 }
 
-// Register slots: slot s of thread t holds element s*256 + t, so a slot's 32-element
-// block lives on one half-wave.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// A buffer resource over n floats: loads past the end return zeros without touching
+// memory, so the prologue loads are unconditional (no branches, exact load counters).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t f32_rsrc(const float* p, int n) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, 0, n * 4, 0x00020000);
+}
+
+// Two register layouts of the prologue's fp32 input:
+//  - strided: slot s of thread t holds element s*256 + t (the rms_ss order's lanes);
+//  - vector:  group v of thread t holds elements 4t + 1024v .. +3, so a 32-element block
+//    lives on 8 consecutive lanes (quant4 / q4_to_rec).
+// KS = ceil(K/256) strided slots; KV vector groups are held at once (all of them for
+// K <= 4096, else the groups are processed KV at a time).
 template <int KS>
 struct Slots {
-  float x[KS];
-  float w[KS];
+  static constexpr int KV = KS >= 16 ? 4 : 1;
+  static constexpr int NV = KS >= 16 ? KS / 4 : 1;   // vector groups in all
+  float s[KS];       // strided x (sum of squares only)
+  f32x4 x[KV];       // vector x
+  f32x4 w[KV];       // vector norm weight
 };
 
 template <int KS>
-__device__ __forceinline__ void load_slots(const float* __restrict__ x, const float* __restrict__ w, int K,
-                                           Slots<KS>& S) {
+__device__ __forceinline__ void load_vgroups(const float* __restrict__ x, const float* __restrict__ w, int K,
+                                             int v0, Slots<KS>& S) {
+  const __amdgpu_buffer_rsrc_t rx = f32_rsrc(x, K);
   const int t = threadIdx.x;
 #pragma unroll
-  for (int s = 0; s < KS; s++) {
-    const int j = s * kThreads + t;
-    S.x[s] = j < K ? x[j] : 0.0f;
-    if (w) S.w[s] = j < K ? w[j] : 0.0f;
+  for (int v = 0; v < Slots<KS>::KV; v++)
+    S.x[v] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (t + kThreads * (v0 + v)) * 16, 0, 0));
+  if (w) {
+    const __amdgpu_buffer_rsrc_t rw = f32_rsrc(w, K);
+#pragma unroll
+    for (int v = 0; v < Slots<KS>::KV; v++)
+      S.w[v] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (t + kThreads * (v0 + v)) * 16, 0, 0));
   }
 }
 
-// Quantize the slots into records (optionally normalized: y = (x*inv)*w).
-template <int KS, bool kNorm>
-__device__ __forceinline__ void slots_to_rec(const Slots<KS>& S, float inv, int K, uint32_t* rec) {
-  const int t = threadIdx.x;
-  const int lane = t & 31;
+// kStrided: also load the strided copy of x for the sum of squares.
+template <int KS, bool kStrided>
+__device__ __forceinline__ void load_slots(const float* __restrict__ x, const float* __restrict__ w, int K,
+                                           Slots<KS>& S) {
+  if (kStrided) {
+    const __amdgpu_buffer_rsrc_t rx = f32_rsrc(x, K);
 #pragma unroll
-  for (int s = 0; s < KS; s++) {
-    const int j0 = s * kThreads + (t & ~31);   // first element of this half-wave's block
-    if (j0 < K) {                              // uniform per half-wave (K % 32 == 0)
-      const float v = kNorm ? (S.x[s] * inv) * S.w[s] : S.x[s];
-      quant_to_rec(v, lane, rec + (j0 >> 5) * kRecDwords);
+    for (int s = 0; s < KS; s++)
+      S.s[s] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, (s * kThreads + (int)threadIdx.x) * 4, 0, 0));
+  }
+  load_vgroups<KS>(x, w, K, 0, S);
+}
+
+// Quantize the vector groups into records (optionally normalized: y = (x*inv)*w).  The
+// groups past the first KV are loaded here (K > 4096).
+template <int KS, bool kNorm>
+__device__ __forceinline__ void slots_to_rec(Slots<KS>& S, const float* __restrict__ x, const float* __restrict__ w,
+                                             float inv, int K, uint32_t* rec) {
+  const int t = threadIdx.x;
+  const int j = t & 7;
+  const int nb = K >> 5;
+  constexpr int KV = Slots<KS>::KV;
+#pragma unroll
+  for (int v0 = 0; v0 < Slots<KS>::NV; v0 += KV) {
+    if (v0 > 0) load_vgroups<KS>(x, kNorm ? w : nullptr, K, v0, S);
+    uint32_t p[KV];
+    QScale sc[KV];
+#pragma unroll
+    for (int v = 0; v < KV; v++) {
+      f32x4 y = S.x[v];
+      if (kNorm) {
+        y.x = (y.x * inv) * S.w[v].x;
+        y.y = (y.y * inv) * S.w[v].y;
+        y.z = (y.z * inv) * S.w[v].z;
+        y.w = (y.w * inv) * S.w[v].w;
+      }
+      p[v] = quant4(y.x, y.y, y.z, y.w, sc[v]);
+    }
+#pragma unroll
+    for (int v = 0; v < KV; v++) {
+      const int b = (t >> 3) + 32 * (v0 + v);
+      q4_to_rec(p[v], sc[v].dq, j, b < nb, rec + b * kRecDwords);
     }
   }
 }
 
+// The slots of an fp32 row already in LDS (the embedding prologue), norm weight from
+// global memory.
+template <int KS>
+__device__ __forceinline__ void lds_slots(const float* xrow, const float* __restrict__ w, int K, Slots<KS>& S) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int s = 0; s < KS; s++) S.s[s] = s * kThreads + t < K ? xrow[s * kThreads + t] : 0.0f;
+#pragma unroll
+  for (int v = 0; v < Slots<KS>::KV; v++) {
+    const int e = 4 * (t + kThreads * v);
+    S.x[v] = e < K ? *(const f32x4*)(xrow + e) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  const __amdgpu_buffer_rsrc_t rw = f32_rsrc(w, K);
+#pragma unroll
+  for (int v = 0; v < Slots<KS>::KV; v++)
+    S.w[v] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (t + kThreads * v) * 16, 0, 0));
+}
+
 // rms_ss order (norm_softmax_from_facts.pl:49, 83-108): thread t folds x[t], x[t+256], ...
-// by fma, then the pairwise tree 128..1; inv = rsqrt(ss/N + eps).
+// by fma, then the pairwise tree 128..1; inv = rsqrt(ss/N + eps).  Slots past K hold
+// zeros, which leave the fold unchanged (p + 0*0 == p for p >= 0).
 template <int KS>
 __device__ __forceinline__ float rms_inv(const Slots<KS>& S, int K, float eps, float* red, float* sinv) {
   const int t = threadIdx.x;
   float p = 0.0f;
 #pragma unroll
-  for (int s = 0; s < KS; s++)
-    if (s * kThreads + t < K) p = fmaf(S.x[s], S.x[s], p);
+  for (int s = 0; s < KS; s++) p = fmaf(S.s[s], S.s[s], p);
   red[t] = p;
   __syncthreads();
   if (t < 64) {
@@ -187,17 +252,15 @@ struct StageRegs {
 
 __device__ __forceinline__ void load_stage(const int8_t* __restrict__ xq, const uint16_t* __restrict__ xd,
                                            int K, StageRegs& R) {
-  const u32x4* src = (const u32x4*)xq;
+  // buffer loads: chunks past K and scales past K/32 read zeros, with no branches
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)xq, 0, K, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc((void*)xd, 0, (K / 32) * 2, 0x00020000);
 #pragma unroll
-  for (int k = 0; k < kStageChunks; k++) {
-    const int i = threadIdx.x + kThreads * k;
-    if (i < K / 16) R.c[k] = src[i];
-  }
+  for (int k = 0; k < kStageChunks; k++)
+    R.c[k] = __builtin_amdgcn_raw_buffer_load_b128(rq, (threadIdx.x + kThreads * k) * 16, 0, 0);
 #pragma unroll
-  for (int k = 0; k < 2; k++) {
-    const int i = threadIdx.x + kThreads * k;
-    R.d[k] = i < K / 32 ? xd[i] : (uint16_t)0;
-  }
+  for (int k = 0; k < 2; k++)
+    R.d[k] = __builtin_amdgcn_raw_buffer_load_b16(rd, (threadIdx.x + kThreads * k) * 2, 0, 0);
 }
 
 __device__ __forceinline__ void stage_to_rec(const StageRegs& R, int K, uint8_t* sxq, uint32_t* rec) {
@@ -254,7 +317,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
   float* red = (float*)smem;                                  // [256] + sinv + pad
   float* sinv = red + kThreads;
   uint32_t* rec = (uint32_t*)(red + kThreads + 4);            // [nb][kRecDwords]
-  uint8_t* sxq = (uint8_t*)(rec + nb * kRecDwords);           // [K]: PRO_STAGE staging
+  uint8_t* sxq = (uint8_t*)(rec + ((nb * kRecDwords + 3) & ~3));   // [K]: PRO_STAGE staging (16-aligned)
   float* xrow = (float*)(sxq + ((K + 15) & ~15));             // [K]: PRO_EMBED_RMS row
   __shared__ float s_rows[kSiluRows];
 
@@ -266,8 +329,8 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
   Slots<KS> S;
   StageRegs SR;
   int tok = 0;
-  if constexpr (PRO == PRO_RMS) load_slots<KS>(P.x, P.nw, K, S);
-  else if constexpr (PRO == PRO_QUANT) load_slots<KS>(P.x, nullptr, K, S);
+  if constexpr (PRO == PRO_RMS) load_slots<KS, true>(P.x, P.nw, K, S);
+  else if constexpr (PRO == PRO_QUANT) load_slots<KS, false>(P.x, nullptr, K, S);
   else if constexpr (PRO == PRO_STAGE) load_stage(P.xq, P.xd, K, SR);
   else if constexpr (PRO == PRO_MERGE) { if (P.nsplit == 1) load_stage(P.xq, P.xd, K, SR); }
   else if constexpr (PRO == PRO_EMBED_RMS) tok = *P.tok;
@@ -313,17 +376,22 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
   // the epilogue's residuals, fetched with the weights
   float rpre[kResidPre];
   if constexpr (EPI == EPI_RESID) {
+    const __amdgpu_buffer_rsrc_t rres = f32_rsrc(P.resid, P.N);
 #pragma unroll
-    for (int i = 0; i < kResidPre; i++) rpre[i] = (lane == 0 && i < nrows) ? P.resid[rbase + step * i] : 0.0f;
+    for (int i = 0; i < kResidPre; i++) {   // buffer loads: no branches, exact load counters
+      const int off = (lane == 0 && i < nrows) ? (rbase + step * i) * 4 : (int)kNoBlock;
+      rpre[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rres, off, 0, 0));
+    }
   }
   // @phase gemv 1
 
   // (3) the prologue's arithmetic, under the weight loads
   if constexpr (PRO == PRO_RMS) {
     const float inv = rms_inv<KS>(S, K, P.eps, red, sinv);
-    slots_to_rec<KS, true>(S, inv, K, rec);
+    // @phase gemv 5
+    slots_to_rec<KS, true>(S, P.x, P.nw, inv, K, rec);
   } else if constexpr (PRO == PRO_QUANT) {
-    slots_to_rec<KS, false>(S, 0.0f, K, rec);
+    slots_to_rec<KS, false>(S, P.x, nullptr, 0.0f, K, rec);
   } else if constexpr (PRO == PRO_STAGE) {
     stage_to_rec(SR, K, sxq, rec);
   } else if constexpr (PRO == PRO_MERGE) {
@@ -349,9 +417,10 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
     }
     if (bad && blockIdx.x == 0 && threadIdx.x == 0 && P.err) *P.err = 1;
     __syncthreads();
-    load_slots<KS>(xrow, P.nw, K, S);
+    static_assert(KS <= 16, "the embedding prologue holds every vector group (K <= 4096)");
+    lds_slots<KS>(xrow, P.nw, K, S);
     const float inv = rms_inv<KS>(S, K, P.eps, red, sinv);
-    slots_to_rec<KS, true>(S, inv, K, rec);
+    slots_to_rec<KS, true>(S, nullptr, P.nw, inv, K, rec);
   }
   __syncthreads();
   // @phase gemv 2
@@ -859,7 +928,7 @@ hipError_t launch_gemv_k(GemvParams P, size_t shm, hipStream_t st, int num_cus, 
 template <Pro PRO, Epi EPI>
 hipError_t launch_gemv(const GemvParams& P, lt_ctx* ctx, int* grid_out) {
   const int nb = P.K / 32;
-  size_t shm = (kThreads + 4) * sizeof(float) + (size_t)nb * kRecDwords * 4;
+  size_t shm = (kThreads + 4) * sizeof(float) + (size_t)((nb * kRecDwords + 3) & ~3) * 4;
   if (PRO == PRO_STAGE || PRO == PRO_MERGE) shm += (size_t)((P.K + 15) & ~15);
   if (PRO == PRO_EMBED_RMS) shm += (size_t)((P.K + 15) & ~15) + (size_t)P.K * sizeof(float);
   hipStream_t st = ctx->stream;
@@ -876,7 +945,8 @@ hipError_t launch_gemv(const GemvParams& P, lt_ctx* ctx, int* grid_out) {
       return shallow ? launch_gemv_k<4, PRO, EPI, 2>(P, shm, st, ncu, grid_out)
                      : launch_gemv_k<4, PRO, EPI, 8>(P, shm, st, ncu, grid_out);
     if (P.K <= 4096) return launch_gemv_k<16, PRO, EPI, 8>(P, shm, st, ncu, grid_out);
-    return launch_gemv_k<64, PRO, EPI, 4>(P, shm, st, ncu, grid_out);
+    if constexpr (PRO == PRO_EMBED_RMS) return hipErrorInvalidValue;   // K <= 4096 (entry check)
+    else return launch_gemv_k<64, PRO, EPI, 4>(P, shm, st, ncu, grid_out);
   }
 }
 

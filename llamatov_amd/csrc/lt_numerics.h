@@ -210,9 +210,29 @@ LT_HD float lt_rintf(float x) {
 #endif
 }
 
-LT_HD int lt_q8_quant1(float x, float dq) {
-  int q = (int)lt_rintf(x / dq);
-  return q < -127 ? -127 : (q > 127 ? 127 : q);
+/* clamp(rint(v), -127, 127) with the saturating float->int conversion of the GPUs the
+ * quantizer runs on: +-inf and out-of-range values saturate, NaN converts to 0. */
+LT_HD int lt_q8_round_clamp(float v) {
+  float t = lt_rintf(v);
+  t = (t == t) ? t : 0.0f;
+  return (int)fminf(fmaxf(t, -127.0f), 127.0f);
+}
+
+LT_HD int lt_q8_quant1(float x, float dq) { return lt_q8_round_clamp(x / dq); }
+
+/* x / dq without a division per element, for r = RN(1/dq) (one IEEE division per block).
+ * q = RN(x*r) is within 2 ulp of x/dq; each step q' = RN(q + RN(x - q*dq) * r) uses the
+ * residual x - q*dq, which fma computes exactly when q is within 2 ulp.  Markstein (1990,
+ * "Computation of elementary functions on the IBM RISC System/6000 processor"): when r is
+ * the correctly rounded reciprocal and q is faithful, one step yields the correctly rounded
+ * quotient; the first step makes q faithful, the second rounds it correctly.  For finite
+ * nonzero dq and finite x this equals x / dq bit for bit whenever |x / dq| is a normal
+ * number (below that, both round to an integer 0 in the quantizer); dq = inf gives NaN
+ * here and +-0 in IEEE division, both of which the quantizer maps to 0. */
+LT_HD float lt_q8_quotient(float x, float dq, float r) {
+  float q = x * r;
+  q = fmaf(fmaf(-q, dq, x), r, q);
+  return fmaf(fmaf(-q, dq, x), r, q);
 }
 
 /* SiLU(g) * u exactly as the reference writes it: (g / (1 + exp(-g))) * u.

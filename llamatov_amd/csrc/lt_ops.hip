@@ -263,6 +263,49 @@ __global__ __launch_bounds__(256) void k_argmax_s2(const float* __restrict__ pva
 
 inline int grid_for(long n, int per) { return (int)((n + per - 1) / per); }
 
+// ---- numerics self-check (lt_selftest_numerics) ---------------------------------------
+// Every non-NaN binary32 pattern: the hardware conversion lt_f2h against the portable
+// round-to-nearest-even lt_float_to_half_bits.
+__global__ __launch_bounds__(256) void k_check_f2h(unsigned long long* bad) {
+  unsigned long long n = 0;
+  const uint32_t stride = gridDim.x * 256u;
+  for (uint64_t u = (uint64_t)blockIdx.x * 256u + threadIdx.x; u < (1ull << 32); u += stride) {
+    const float f = __builtin_bit_cast(float, (uint32_t)u);
+    if (f == f && lt_f2h(f) != lt_float_to_half_bits(f)) n++;
+  }
+  if (n) atomicAdd(bad, n);
+}
+
+// Workgroup h (1 .. 0x7BFF): dq = fp16 h; x at and around every (k + 1/2) * dq and at
+// k * dq for |k| <= 140; lt_q8_quotient against IEEE division.
+__global__ __launch_bounds__(256) void k_check_quotient(unsigned long long* out) {
+  const uint32_t h = blockIdx.x + 1u;
+  const float dq = lt_h2f((uint16_t)h);
+  const float r = 1.0f / dq;
+  unsigned long long bits = 0, qbad = 0, cases = 0;
+  for (int c = threadIdx.x; c < 281 * 8; c += 256) {
+    const int k = c / 8 - 140, d = c % 8;
+    float x;
+    if (d == 7) {
+      x = (float)k * dq;
+    } else {
+      const float base = ((float)k + 0.5f) * dq;
+      x = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, base) + (uint32_t)(d - 3));
+    }
+    if (!(fabsf(x) <= 3.402823466e38f)) continue;
+    cases++;
+    const float want = x / dq;
+    const float got = lt_q8_quotient(x, dq, r);
+    if (fabsf(want) >= 1.17549435e-38f && fabsf(want) <= 3.402823466e38f &&
+        __builtin_bit_cast(uint32_t, want) != __builtin_bit_cast(uint32_t, got))
+      bits++;
+    if (lt_q8_round_clamp(want) != lt_q8_round_clamp(got)) qbad++;
+  }
+  if (bits) atomicAdd(&out[0], bits);
+  if (qbad) atomicAdd(&out[1], qbad);
+  atomicAdd(&out[2], cases);
+}
+
 }  // namespace
 
 extern "C" {
@@ -377,6 +420,26 @@ int lt_argmax_record(lt_ctx* ctx, const float* x, int n, int* out, int* hist, in
                      void* ws, size_t ws_bytes) {
   LT_REQUIRE(hist && count && cap > 0, "lt_argmax_record: null history or cap=%d", cap);
   return argmax_impl(ctx, x, n, out, hist, count, cap, ws, ws_bytes);
+}
+
+int lt_selftest_numerics(lt_ctx* ctx, unsigned long long* out) {
+  LT_REQUIRE(ctx && out, "lt_selftest_numerics: null argument");
+  unsigned long long* d = nullptr;
+  LT_CHECK(hipMalloc(&d, 4 * sizeof(unsigned long long)));
+  hipError_t e = hipMemsetAsync(d, 0, 4 * sizeof(unsigned long long), ctx->stream);
+  if (e == hipSuccess) {
+    k_check_f2h<<<4096, 256, 0, ctx->stream>>>(d);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) {
+    k_check_quotient<<<0x7BFF, 256, 0, ctx->stream>>>(d + 1);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpyAsync(out, d, 4 * sizeof(unsigned long long), hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  hipFree(d);
+  if (e != hipSuccess) return lt_fail_hip(e, "lt_selftest_numerics", __FILE__, __LINE__);
+  return LT_OK;
 }
 
 }  // extern "C"

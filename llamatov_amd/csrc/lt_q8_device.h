@@ -18,20 +18,6 @@ typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 constexpr int kBlockBytes = 34;
 
-// Quantize one 32-element block held one element per lane of a 32-lane half-wave:
-// amax by xor-shuffle (a max, hence order-free), d16 = fp16(amax/127) (1 if amax == 0),
-// q = clamp(rint(v / float(d16)), +-127); lane 0 stores the scale.
-__device__ __forceinline__ void quant_block_halfwave(float v, int lane, int8_t* xq_blk,
-                                                     uint16_t* xd_slot) {
-  float a = fabsf(v);
-#pragma unroll
-  for (int m = 16; m > 0; m >>= 1) a = fmaxf(a, __shfl_xor(a, m, 32));
-  uint16_t d16 = lt_q8_scale_bits(a);
-  if (lane == 0) *xd_slot = d16;
-  float dq = lt_h2f(d16);
-  xq_blk[lane] = (int8_t)lt_q8_quant1(v, dq);
-}
-
 // One Q8_0 block in registers: the 32 quants re-aligned to dwords, and the fp16 scale.
 struct BlockRegs {
   uint32_t q[8];
@@ -145,12 +131,68 @@ __device__ __forceinline__ float wave_max(float a) {
   return halfwave_max(a);
 }
 
-// quant_block_halfwave with the DPP max.
+// ---- the engine quantizer without per-element division -----------------------------
+// d16 = fp16(amax/127) (1 if not amax > 0) by the hardware conversion v_cvt_f16_f32
+// (round to nearest even, gradual underflow, overflow to inf: the bits of
+// lt_float_to_half_bits for every non-NaN input; amax/127 is never NaN), and
+// q = clamp(rint(x / dq), +-127) with x / dq formed as lt_q8_quotient from one reciprocal
+// per block.  The one case the quotient does not cover, dq = 0 (every |x| of the block
+// below 127 * 2^-25), is x / 0 = +-inf or NaN: +-127 or 0.  Bit-identical to
+// lt_q8_scale_bits + lt_q8_quant1.
+__device__ __forceinline__ uint16_t lt_f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+struct QScale {
+  uint16_t h;   // fp16 scale bits
+  float dq;     // the scale as fp32
+  float r;      // RN(1 / dq)
+};
+
+__device__ __forceinline__ QScale q8_scale(float amax) {
+  QScale s;
+  s.h = lt_f2h(amax > 0.0f ? amax / 127.0f : 1.0f);
+  s.dq = lt_h2f(s.h);
+  s.r = 1.0f / s.dq;
+  return s;
+}
+
+__device__ __forceinline__ int q8_quant_zero_scale(float x) { return x > 0.0f ? 127 : (x < 0.0f ? -127 : 0); }
+
+__device__ __forceinline__ int q8_quant(float x, const QScale& s) {
+  int q = lt_q8_round_clamp(lt_q8_quotient(x, s.dq, s.r));
+  if (__builtin_expect(s.h == 0, 0)) q = q8_quant_zero_scale(x);
+  return q;
+}
+
+// quant_block_halfwave with the DPP max and the division-free quantizer.
 __device__ __forceinline__ void quant_block_hw(float v, int lane, int8_t* xq_blk, uint16_t* xd_slot) {
-  const float a = halfwave_max(fabsf(v));
-  const uint16_t d16 = lt_q8_scale_bits(a);
-  if (lane == 0) *xd_slot = d16;
-  xq_blk[lane] = (int8_t)lt_q8_quant1(v, lt_h2f(d16));
+  const QScale s = q8_scale(halfwave_max(fabsf(v)));
+  if (lane == 0) *xd_slot = s.h;
+  xq_blk[lane] = (int8_t)q8_quant(v, s);
+}
+
+// Maximum over the 8 lanes 8g .. 8g+7 (half of a DPP row): order-free.
+__device__ __forceinline__ float group8_max(float a) {
+  a = fmaxf(a, dpp_f<0xB1>(a));   // lane ^ 1
+  a = fmaxf(a, dpp_f<0x4E>(a));   // lane ^ 2
+  a = fmaxf(a, dpp_f<0x141>(a));  // mirror within 8: the two quads combine
+  return a;
+}
+
+// One 32-element block held 4 consecutive elements per lane on 8 consecutive lanes (lane
+// j = lane & 7 holds elements 4j .. 4j+3): returns the block's scale and this lane's four
+// quants packed little-endian (element 4j+i in byte i).
+__device__ __forceinline__ uint32_t quant4(float x0, float x1, float x2, float x3, QScale& s) {
+  const float a = fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3)));
+  s = q8_scale(group8_max(a));
+  auto pack = [](int q0, int q1, int q2, int q3) {
+    return ((uint32_t)q0 & 0xFFu) | (((uint32_t)q1 & 0xFFu) << 8) | (((uint32_t)q2 & 0xFFu) << 16) |
+           ((uint32_t)q3 << 24);
+  };
+  uint32_t p = pack(lt_q8_round_clamp(lt_q8_quotient(x0, s.dq, s.r)), lt_q8_round_clamp(lt_q8_quotient(x1, s.dq, s.r)),
+                    lt_q8_round_clamp(lt_q8_quotient(x2, s.dq, s.r)), lt_q8_round_clamp(lt_q8_quotient(x3, s.dq, s.r)));
+  if (__builtin_expect(s.h == 0, 0))   // the whole block is below 127 * 2^-25: x / 0
+    p = pack(q8_quant_zero_scale(x0), q8_quant_zero_scale(x1), q8_quant_zero_scale(x2), q8_quant_zero_scale(x3));
+  return p;
 }
 
 // ---- raw 34-byte block loads dotted against a phase-matched activation ---------------
@@ -202,6 +244,28 @@ __device__ __forceinline__ float fold_raw(const RawBlock& r, bool odd, const uin
 
 // Build the activation records of nb blocks from the staged quants sxq[32*nb] (int8) and
 // scales sxd[nb] (fp16 bits); called by every thread of the workgroup.
+// Write a block quantized by quant4 into its record: lane j of the block's 8-lane group
+// holds quants 4j .. 4j+3 in p.  Phase O (dwords kRecPhase+1 ..) takes p as it is; phase E
+// is shifted by 2 bytes, so its dword j joins the previous lane's upper two quants (DPP
+// row_shr:1) with this lane's lower two; its dword 0 starts with two zero bytes and dword 8
+// holds the last two quants.  Every lane executes the DPP; `write` selects the lanes whose
+// block exists.
+__device__ __forceinline__ void q4_to_rec(uint32_t p, float dq, int j, bool write, uint32_t* rec) {
+  const uint32_t prev = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)p, 0x111, 0xF, 0xF, true);
+  const uint32_t e = j == 0 ? (p << 16) : __builtin_amdgcn_alignbyte(p, prev, 2);
+  if (write) {
+    rec[j] = e;
+    rec[kRecPhase + 1 + j] = p;
+    if (j == 7) rec[8] = p >> 16;
+    if (j == 0) {
+      const uint32_t d = __builtin_bit_cast(uint32_t, dq);
+      rec[9] = d;
+      rec[kRecPhase] = 0u;
+      rec[kRecPhase + 9] = d;
+    }
+  }
+}
+
 __device__ __forceinline__ void build_act_records(const int8_t* sxq, const uint16_t* sxd, int nb,
                                                   uint32_t* rec, int tid, int nthreads) {
   const uint32_t* X = (const uint32_t*)sxq;   // 8 dwords per block
