@@ -140,6 +140,7 @@ def gemv_sweep(dev, launches: int = 40) -> list[dict]:
 
 
 INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, TOP/s (2 ops per MAC)
+C5_ATTN_NSPLIT = 16       # C5 decode attention: ceil(776/16) = 49 positions per split
 
 
 def attention_sweep(dev, reps: int = 20) -> list[dict]:
@@ -196,7 +197,9 @@ def c5_leg(dev, n_prefill: int = 512, n_decode: int = 256, eager: bool = False) 
     log(f"C5 weights generated in {time.perf_counter() - t0:.1f}s")
     model = dr.ResidentModel(cfg, w, dev, layouts="fused")
     del w
-    plan = dr.DecodePlan(model, dr.Profile(kv_dtype=LT_KV_F16), max_ctx=n_prefill + n_decode + 8, hist_cap=4096)
+    # split-K over the context (the declared split order, merged in the attention launch)
+    plan = dr.DecodePlan(model, dr.Profile(kv_dtype=LT_KV_F16, attn_nsplit=C5_ATTN_NSPLIT),
+                         max_ctx=n_prefill + n_decode + 8, hist_cap=4096)
     prompt = M.random_prompt(cfg, n_prefill, seed=17)
     # warm the prefill kernels on a short prompt, then rewind
     dr.forward_prefill(plan, prompt[:8])

@@ -126,6 +126,7 @@ LT_API int lt_kv_append_incr(lt_ctx* ctx, void* kc, const float* k, void* vc, co
 LT_API int lt_attn_decode(lt_ctx* ctx, const float* q, const void* kc, const void* vc, const int* len,
                    float* out, int batch, int nh, int nkv, int hd, float scale, int maxt,
                    int nsplit, int kv_dtype, void* ws, size_t ws_bytes);
+/* Bytes of split-K workspace (0 for nsplit == 1). */
 LT_API size_t lt_attn_workspace_size(int batch, int nh, int hd, int nsplit);
 
 /* Greedy argmax over n logits, ties to the lowest index (k_argmax_s1/_s2,
@@ -209,10 +210,13 @@ LT_API size_t lt_q8_gemv_argmax_workspace_size(int N);
  * bpd/lib/dev_residency.py:1396-1425).  qkv = [q (nh*hd) | k (nkv*hd) | v (nkv*hd)] before
  * RoPE (bias included); the new token is position L = *len; K/V row L is written to the
  * cache and attention runs over L+1 positions.  *len is not changed here (see
- * lt_q8_gemv_attn_out).  nsplit == 1 writes the output fp32 into out[nh*hd] (if non-null)
- * and quantized into xq[nh*hd] / xd[nh*hd/32] (if non-null; hd % 32 == 0); nsplit > 1
- * writes split partials into ws (lt_attn_workspace_size(1, nh, hd, nsplit) bytes) for
- * lt_q8_gemv_attn_out. */
+ * lt_q8_gemv_attn_out).  The output goes to out[nh*hd] fp32 (if non-null) and quantized to
+ * xq[nh*hd] / xd[nh*hd/32] (if non-null; hd % 32 == 0).  nsplit > 1 (<= 128) splits the
+ * context into contiguous ceil((L+1)/nsplit) ranges; each split's partials go to ws
+ * (lt_attn_workspace_size(1, nh, hd, nsplit) bytes) and a second launch merges them in
+ * ascending split order (the declared combine,
+ * bpd/kernelgen/experimental/attn_decode_split.cu:37-91), so the output is final either
+ * way; lt_q8_gemv_attn_out then takes it with nsplit = 1. */
 LT_API int lt_attn_step(lt_ctx* ctx, const float* qkv, const float* freqs, void* kc, void* vc, const int* len,
                         float* out, int8_t* xq, uint16_t* xd, int nh, int nkv, int hd, float scale, int maxt,
                         int nsplit, int kv_dtype, void* ws, size_t ws_bytes);

@@ -229,7 +229,7 @@ extern "C" {
 
 size_t lt_attn_workspace_size(int batch, int nh, int hd, int nsplit) {
   if (nsplit <= 1 || batch <= 0 || nh <= 0 || hd <= 0) return 0;
-  return (size_t)batch * nh * nsplit * (size_t)(2 + hd) * sizeof(float) + 256;
+  return lt_attn_ws_bytes(batch * nh, hd, nsplit);
 }
 
 static int attn_impl(lt_ctx* ctx, const float* q, const void* kc, const void* vc, const int* len,
@@ -259,11 +259,10 @@ static int attn_impl(lt_ctx* ctx, const float* q, const void* kc, const void* vc
     LT_REQUIRE(ws != nullptr, "lt_attn_decode: nsplit=%d needs a workspace", nsplit);
     if (ws_bytes < need) return lt_fail(LT_ENOMEM, "lt_attn_decode: workspace %zu < %zu bytes", ws_bytes, need);
     LT_REQUIRE(lt_aligned(ws, 16), "lt_attn_decode: workspace must be 16-byte aligned");
-    size_t nrow = (size_t)batch * nh * nsplit;
-    wsm = (float*)ws;
-    wsz = wsm + nrow;
-    wso = wsz + nrow;
-    wso = (float*)(((uintptr_t)wso + 15) & ~(uintptr_t)15);
+    const AttnWs w = lt_attn_ws_layout(ws, batch * nh, hd, nsplit);
+    wsm = w.m;
+    wsz = w.z;
+    wso = w.o;
   }
   hipError_t e;
   const bool f16 = kv_dtype == LT_KV_F16;

@@ -641,18 +641,24 @@ __global__ __launch_bounds__(256) void k_attn_step(
     for (int u = 0; u < kKU; u++)
       if (u < upr) __builtin_memcpy(&kraw[u], (const uint16_t*)kc + head_base + (size_t)tid * kvrow + u * kEpu, 16);
   }
-  const int cn0 = n < cpos ? n : cpos;
-  u32x4 vraw[kUpt];
+  // V rows through a buffer resource: rows past the range (and row L, which comes from
+  // registers) read as zeros without touching memory, so every load is unconditional
+  const __amdgpu_buffer_rsrc_t vrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      vc, 0, (int)((size_t)maxt * kvrow * (kF16 ? 2 : 4)), 0x00020000);
+  auto load_vchunk = [&](int c0, u32x4* dst) {
+    const int cn = n - c0 < cpos ? n - c0 : cpos;
 #pragma unroll
-  for (int k = 0; k < kUpt; k++) {
-    const int u = tid + 256 * k;
-    const int t = u / upr;
-    if (t < cn0 && p0 + t != L) {
-      const size_t e = head_base + (size_t)t * kvrow + (size_t)(u - t * upr) * kEpu;
-      if (kF16) __builtin_memcpy(&vraw[k], (const uint16_t*)vc + e, 16);
-      else __builtin_memcpy(&vraw[k], (const float*)vc + e, 16);
+    for (int k = 0; k < kUpt; k++) {
+      const int u = tid + 256 * k;
+      const int t = u / upr;
+      const bool real = t < cn && p0 + c0 + t != L;
+      const size_t e = head_base + (size_t)(c0 + t) * kvrow + (size_t)(u - t * upr) * kEpu;
+      const int off = real ? (int)(e * (kF16 ? 2 : 4)) : (int)kNoBlock;
+      dst[k] = __builtin_amdgcn_raw_buffer_load_b128(vrsrc, off, 0, 0);
     }
-  }
+  };
+  u32x4 vraw[kUpt];
+  load_vchunk(0, vraw);
 
   // RoPE (the arithmetic of k_rope) of the q heads and of the group's k; v rounded
   const float pos = (float)(valid ? L : 0);
@@ -782,19 +788,7 @@ __global__ __launch_bounds__(256) void k_attn_step(
   float acc0 = 0.0f, acc1 = 0.0f;   // thread handles outputs tid and tid + 256
   for (int c0 = 0; c0 < n; c0 += cpos) {
     const int cn = n - c0 < cpos ? n - c0 : cpos;
-    if (c0 > 0) {
-      __syncthreads();
-#pragma unroll
-      for (int k = 0; k < kUpt; k++) {
-        const int u = tid + 256 * k;
-        const int t = u / upr;
-        if (t < cn && p0 + c0 + t != L) {
-          const size_t e = head_base + (size_t)(c0 + t) * kvrow + (size_t)(u - t * upr) * kEpu;
-          if (kF16) __builtin_memcpy(&vraw[k], (const uint16_t*)vc + e, 16);
-          else __builtin_memcpy(&vraw[k], (const float*)vc + e, 16);
-        }
-      }
-    }
+    if (c0 > 0) __syncthreads();   // the previous chunk's readers are done with svt
 #pragma unroll
     for (int k = 0; k < kUpt; k++) {
       const int u = tid + 256 * k;
@@ -820,6 +814,8 @@ __global__ __launch_bounds__(256) void k_attn_step(
         }
       }
     }
+    // the next chunk's loads fly under this chunk's chains
+    if (c0 + cpos < n) load_vchunk(c0 + cpos, vraw);
     __syncthreads();
     if (tid < nout) {
       const int r = tid / hd, d = tid - r * hd;
@@ -848,13 +844,16 @@ __global__ __launch_bounds__(256) void k_attn_step(
       wso[((size_t)h * nsplit + sp) * hd + d] = a;
     }
   }
-  if (nsplit > 1 && tid < HPW) {
-    const int h = h0 + tid;
-    wsm[(size_t)h * nsplit + sp] = s_mx[tid];
-    wsz[(size_t)h * nsplit + sp] = s_z[tid];
+  if (nsplit > 1) {
+    if (tid < HPW) {
+      const int h = h0 + tid;
+      wsm[(size_t)h * nsplit + sp] = s_mx[tid];
+      wsz[(size_t)h * nsplit + sp] = s_z[tid];
+    }
+    return;   // k_attn_merge combines the partials
   }
   // @phase attn 5
-  if (nsplit == 1 && oq) {
+  if (oq) {
     // the workgroup's heads are whole 32-element blocks of the attention vector: quantize
     // them for the O projection (k_quant_q8's quantizer)
     __syncthreads();
@@ -864,6 +863,70 @@ __global__ __launch_bounds__(256) void k_attn_step(
       quant_block_hw(svt[b * 32 + lane], lane, oq + o0 + b * 32, od + (o0 >> 5) + b);
   }
   // @phase attn 6
+}
+
+// Split-K merge, one workgroup per query head (the declared combine, ascending split
+// order, bpd/kernelgen/experimental/attn_decode_split.cu:37-91): M = max m_s,
+// w_s = exp(m_s - M), Z = sum fma(w_s, Z_s), O_d = sum fma(w_s, O_s,d), out = O/Z; then
+// the quant of the head's hd/32 blocks.  Every partial is fetched by independent buffer
+// loads issued at the start (one memory round trip); the exps run one per thread.
+constexpr int kMergeQ = 16;   // split outputs prefetched per thread
+
+__global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ wsm, const float* __restrict__ wsz,
+                                                    const float* __restrict__ wso, const int* __restrict__ len,
+                                                    int maxt, float* __restrict__ out, int8_t* __restrict__ oq,
+                                                    uint16_t* __restrict__ od, int hd, int nsplit) {
+  __shared__ float sm[128], sz[128], sw[128], sout[256];
+  __shared__ float s_Z;
+  const int h = blockIdx.x;
+  const int tid = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t orsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(wso + (size_t)h * nsplit * hd), 0, nsplit * hd * 4, 0x00020000);
+  float po[kMergeQ];
+  auto load_po = [&](int q0) {
+#pragma unroll
+    for (int q = 0; q < kMergeQ; q++) {
+      const int off = (tid < hd && q0 + q < nsplit) ? ((q0 + q) * hd + tid) * 4 : (int)kNoBlock;
+      po[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(orsrc, off, 0, 0));
+    }
+  };
+  load_po(0);
+  if (tid < nsplit) {
+    sm[tid] = wsm[(size_t)h * nsplit + tid];
+    sz[tid] = wsz[(size_t)h * nsplit + tid];
+  }
+  const int L = *len;
+  const bool valid = L >= 0 && L < maxt;
+  __syncthreads();
+  float M = -1e30f;
+  for (int q = 0; q < nsplit; q++) M = fmaxf(M, sm[q]);
+  if (tid < nsplit) sw[tid] = lt_expf(sm[tid] - M);
+  __syncthreads();
+  if (tid == 0) {
+    float Z = 0.0f;
+    for (int q = 0; q < nsplit; q++) Z = fmaf(sw[q], sz[q], Z);
+    s_Z = Z;
+  }
+  float a = 0.0f;
+  for (int q0 = 0; q0 < nsplit; q0 += kMergeQ) {
+    if (q0 > 0) load_po(q0);
+#pragma unroll
+    for (int q = 0; q < kMergeQ; q++)
+      if (q0 + q < nsplit) a = fmaf(sw[q0 + q], po[q], a);
+  }
+  __syncthreads();
+  if (tid < hd) {
+    const float v = valid ? a / s_Z : 0.0f;
+    if (out) out[(size_t)h * hd + tid] = v;
+    sout[tid] = v;
+  }
+  if (oq) {
+    __syncthreads();
+    const int lane = tid & 31;
+    const size_t o0 = (size_t)h * hd;
+    for (int b = tid >> 5; b < hd / 32; b += 8)
+      quant_block_hw(sout[b * 32 + lane], lane, oq + o0 + b * 32, od + (o0 >> 5) + b);
+  }
 }
 
 inline int grid_for(long n, int per) { return (int)((n + per - 1) / per); }
@@ -1035,10 +1098,10 @@ int lt_q8_gemv_attn_out(lt_ctx* ctx, const int8_t* xq, const uint16_t* xd, const
     const size_t need = lt_attn_workspace_size(1, nh, hd, nsplit);
     LT_REQUIRE(ws && lt_aligned(ws, 16), "lt_q8_gemv_attn_out: nsplit=%d needs a 16-byte aligned workspace", nsplit);
     if (ws_bytes < need) return lt_fail(LT_ENOMEM, "lt_q8_gemv_attn_out: workspace %zu < %zu bytes", ws_bytes, need);
-    const size_t nrow = (size_t)nh * nsplit;
-    P.wsm = (const float*)ws;
-    P.wsz = P.wsm + nrow;
-    P.wso = (const float*)(((uintptr_t)(P.wsz + nrow) + 15) & ~(uintptr_t)15);
+    const AttnWs w = lt_attn_ws_layout(const_cast<void*>(ws), nh, hd, nsplit);
+    P.wsm = w.m;
+    P.wsz = w.z;
+    P.wso = w.o;
   }
   hipError_t e = resid ? launch_gemv<PRO_MERGE, EPI_RESID>(P, ctx, nullptr)
                        : launch_gemv<PRO_MERGE, EPI_STORE>(P, ctx, nullptr);
@@ -1106,17 +1169,17 @@ int lt_attn_step(lt_ctx* ctx, const float* qkv, const float* freqs, void* kc, vo
   if (shm > 64 * 1024)
     return lt_fail(LT_EINVAL, "lt_attn_step: %zu bytes of LDS for maxt=%d nsplit=%d; raise nsplit", shm, maxt, nsplit);
   float *wsm = nullptr, *wsz = nullptr, *wso = nullptr;
-  if (nsplit == 1) {
-    LT_REQUIRE(out || xq, "lt_attn_step: nsplit=1 needs out or xq/xd");
-    LT_REQUIRE(!xq || (xd && hd % 32 == 0), "lt_attn_step: quantized output needs xd and hd %% 32 == 0");
-  } else {
+  LT_REQUIRE(out || xq, "lt_attn_step: needs out or xq/xd");
+  LT_REQUIRE(!xq || (xd && hd % 32 == 0), "lt_attn_step: quantized output needs xd and hd %% 32 == 0");
+  if (nsplit > 1) {
+    LT_REQUIRE(nsplit <= 128, "lt_attn_step: nsplit=%d (at most 128)", nsplit);
     const size_t need = lt_attn_workspace_size(1, nh, hd, nsplit);
     LT_REQUIRE(ws && lt_aligned(ws, 16), "lt_attn_step: nsplit=%d needs a 16-byte aligned workspace", nsplit);
     if (ws_bytes < need) return lt_fail(LT_ENOMEM, "lt_attn_step: workspace %zu < %zu bytes", ws_bytes, need);
-    const size_t nrow = (size_t)nh * nsplit;
-    wsm = (float*)ws;
-    wsz = wsm + nrow;
-    wso = (float*)(((uintptr_t)(wsz + nrow) + 15) & ~(uintptr_t)15);
+    const AttnWs w = lt_attn_ws_layout(ws, nh, hd, nsplit);
+    wsm = w.m;
+    wsz = w.z;
+    wso = w.o;
   }
   dim3 grid(nsplit, nh / hpw);
   const bool f16 = kv_dtype == LT_KV_F16;
@@ -1139,6 +1202,11 @@ int lt_attn_step(lt_ctx* ctx, const float* qkv, const float* freqs, void* kc, vo
       return lt_fail(LT_EINVAL, "lt_attn_step: unsupported heads per workgroup %d", hpw);
   }
 #undef LT_STEP_CASE
+  if (nsplit > 1) {
+    LT_CHECK(hipGetLastError());
+    k_attn_merge<<<nh, 256, 0, ctx->stream>>>(wsm, wsz, wso, len, maxt, out, xq, xd, hd, nsplit);
+    return lt_check_launch("k_attn_merge");
+  }
   return lt_check_launch("k_attn_step");
 }
 

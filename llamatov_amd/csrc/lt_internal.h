@@ -32,6 +32,29 @@ int lt_check_launch(const char* kernel);
 
 static inline bool lt_aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
+// Split-K attention workspace for `rows` = batch * nh query heads and nsplit splits:
+// per-split maxima m[rows][nsplit], sums z[rows][nsplit], outputs o[rows][nsplit][hd]
+// (16-byte aligned).
+struct AttnWs {
+  float* m;
+  float* z;
+  float* o;
+};
+
+static inline size_t lt_attn_ws_bytes(int rows, int hd, int nsplit) {
+  const size_t nrow = (size_t)rows * nsplit;
+  return nrow * (size_t)(2 + hd) * sizeof(float) + 256;
+}
+
+static inline AttnWs lt_attn_ws_layout(void* ws, int rows, int hd, int nsplit) {
+  const size_t nrow = (size_t)rows * nsplit;
+  AttnWs w;
+  w.m = (float*)ws;
+  w.z = w.m + nrow;
+  w.o = (float*)(((uintptr_t)(w.z + nrow) + 15) & ~(uintptr_t)15);
+  return w;
+}
+
 // Device helpers shared by the kernel translation units.
 __device__ __forceinline__ float lt_h2f(uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));

@@ -103,6 +103,12 @@ class DevTensor:
         return DevTensor(dev.malloc(n * np.dtype(dtype).itemsize), shape, dtype, True, dev)
 
     @staticmethod
+    def zeros(shape, dtype=np.float32, dev: Device | None = None) -> "DevTensor":
+        t = DevTensor.empty(shape, dtype, dev)
+        t.dev.fill(t.ptr, 0, t.nbytes)
+        return t
+
+    @staticmethod
     def from_host(arr: np.ndarray, dev: Device | None = None) -> "DevTensor":
         a = np.ascontiguousarray(arr)
         t = DevTensor.empty(a.shape, a.dtype, dev)
@@ -523,8 +529,8 @@ class DecodePlan:
         """Five launches per layer (lt_fused.hip), then the vocab GEMV with its argmax:
         the same arithmetic as _enqueue_per_op, bit for bit.
           QKV   rmsnorm -> quant -> GEMV + bias        (layer 0: from the embedding of tok)
-          attn  RoPE -> KV append -> attention -> quant
-          O     [split merge -> quant] -> GEMV + x, length += 1
+          attn  RoPE -> KV append -> attention -> quant (split-K: partials, then a merge launch)
+          O     GEMV + x, length += 1
           FFN1  rmsnorm -> quant -> gate|up GEMV -> SiLU(g)*u -> quant
           FFN2  down GEMV + xres"""
         cfg, m, p = self.cfg, self.model, self.profile
@@ -545,7 +551,7 @@ class DecodePlan:
             call("lt_attn_step", h, self.qkv.vp, m.freqs.vp, cache.k.vp, cache.v.vp, _vp(cache.len_ptr),
                  None, self.xq.vp, self.xd.vp, nh, nkv, hd, ctypes.c_float(self.scale), cache.max_seq,
                  p.attn_nsplit, p.kv_dtype, ws, ws_n)
-            call("lt_q8_gemv_attn_out", h, self.xq.vp, self.xd.vp, ws, ws_n, p.attn_nsplit, nh, hd, L["wo"].t.vp,
+            call("lt_q8_gemv_attn_out", h, self.xq.vp, self.xd.vp, None, 0, 1, nh, hd, L["wo"].t.vp,
                  x.vp, self.xres.vp, E, cfg.q_dim, _vp(cache.len_ptr), cache.max_seq)
             call("lt_q8_gemv_rms_silu", h, self.xres.vp, L["ffn_norm"].vp, eps, L["wgu_il"].t.vp, self.xq.vp,
                  self.xd.vp, F, E)

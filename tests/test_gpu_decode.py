@@ -41,7 +41,8 @@ def bitexact(a, b):
 
 @pytest.mark.parametrize("step", ["fused", "per_op"])
 @pytest.mark.parametrize("kv_dtype,nsplit,fused", [(LT_KV_F32, 1, False), (LT_KV_F16, 1, True),
-                                                   (LT_KV_F32, 4, True), (LT_KV_F16, 2, False)])
+                                                   (LT_KV_F32, 4, True), (LT_KV_F16, 2, False),
+                                                   (LT_KV_F16, 16, False)])
 def test_tiny_stepwise_logits_bitexact(gpu, oracle, step, kv_dtype, nsplit, fused):
     cfg = M.TINY
     case(f"tiny stepwise {step} kv={kv_dtype} nsplit={nsplit} fused_rms={fused}")
@@ -64,15 +65,18 @@ def test_tiny_stepwise_logits_bitexact(gpu, oracle, step, kv_dtype, nsplit, fuse
     plan.free()
 
 
-def test_graph_replay_equals_eager(gpu):
+@pytest.mark.parametrize("nsplit", [1, 8])
+def test_graph_replay_equals_eager(gpu, nsplit):
     """GR gate: graph replay is bit-identical to the eager step, device length advances,
-    and the token chain from replay_tokens equals replay_token one by one."""
+    and the token chain from replay_tokens equals replay_token one by one (also with the
+    split-K attention and its merge launch in the graph)."""
     cfg = M.TINY
-    case("tiny graph vs eager")
+    case(f"tiny graph vs eager nsplit={nsplit}")
     m = resident(cfg, gpu)
     prompt = M.random_prompt(cfg, 5, seed=8)
-    eager = dr.DecodePlan(m)
-    graph = dr.DecodePlan(m)
+    prof = dr.Profile(kv_dtype=LT_KV_F16, attn_nsplit=nsplit)
+    eager = dr.DecodePlan(m, prof)
+    graph = dr.DecodePlan(m, prof)
     dr.forward_pass_resident(eager, prompt)
     gr = dr.GraphRunner(graph)
     gr.seed(prompt)

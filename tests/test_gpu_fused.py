@@ -136,12 +136,13 @@ def test_q8_gemv_attn_out(gpu, oracle):
 
 
 @pytest.mark.parametrize("kv_dtype", [LT_KV_F32, LT_KV_F16])
-@pytest.mark.parametrize("nsplit", [1, 3])
+@pytest.mark.parametrize("nsplit", [1, 3, 16])
 @pytest.mark.parametrize("geom", [(14, 2, 64, 1e6), (32, 8, 128, 5e5)])
 def test_attn_step_then_out(gpu, oracle, kv_dtype, nsplit, geom):
-    """RoPE + append + attention (+ split merge in the O launcher) against the oracle's
+    """RoPE + append + attention (+ the split merge launch) against the oracle's
     rope -> append -> attention -> quant -> GEMV chain, over a length sweep; the new cache
-    row and the length bump are checked too."""
+    row and the length bump are checked too.  With nsplit > 1 the O launcher's own merge of
+    the same partials gives the same O projection."""
     nh, nkv, hd, theta = geom
     f16 = kv_dtype == LT_KV_F16
     rng = np.random.default_rng(26)
@@ -157,7 +158,7 @@ def test_attn_step_then_out(gpu, oracle, kv_dtype, nsplit, geom):
     base_k = rng.standard_normal((maxt, width)).astype(np.float32)
     base_v = rng.standard_normal((maxt, width)).astype(np.float32)
     ws_n = _lib.raw("lt_attn_workspace_size")(1, nh, hd, nsplit)
-    ws = empty((max(ws_n, 16),), np.uint8)
+    ws = dr.DevTensor.zeros((max(ws_n, 16),), np.uint8, gpu)
     scale = float(hd ** -0.5)
     for L in (0, 1, 2, 40, maxt - 1):
         case(f"attn_step nh={nh} hd={hd} kv={kv_dtype} nsplit={nsplit} L={L}")
@@ -193,13 +194,17 @@ def test_attn_step_then_out(gpu, oracle, kv_dtype, nsplit, geom):
         aq, ad = empty((nh * hd,), np.int8), empty((nh * hd // 32,), np.uint16)
         call("lt_attn_step", gpu.handle, up(qkv).vp, dfreq.vp, dk.vp, dv.vp, dlen.vp, datt.vp, aq.vp, ad.vp,
              nh, nkv, hd, ctypes.c_float(scale), maxt, nsplit, kv_dtype, ws.vp, ws.nbytes)
-        if nsplit == 1:
-            assert_bitexact(datt.to_host(), att, "attention output")
-            assert_bitexact(aq.to_host(), xq, "attention quants")
-            assert_bitexact(ad.to_host(), xd, "attention scales")
+        assert_bitexact(datt.to_host(), att, "attention output")
+        assert_bitexact(aq.to_host(), xq, "attention quants")
+        assert_bitexact(ad.to_host(), xd, "attention scales")
         assert int(dlen.to_host()[0]) == L
+        if nsplit > 1:
+            y2 = empty((E,), np.float32)
+            call("lt_q8_gemv_attn_out", gpu.handle, aq.vp, ad.vp, ws.vp, ws.nbytes, nsplit, nh, hd, dW.vp,
+                 up(r).vp, y2.vp, E, nh * hd, None, maxt)
+            assert_bitexact(y2.to_host(), exp, f"O after the launcher's own merge L={L}")
         y = empty((E,), np.float32)
-        call("lt_q8_gemv_attn_out", gpu.handle, aq.vp, ad.vp, ws.vp, ws.nbytes, nsplit, nh, hd, dW.vp, up(r).vp,
+        call("lt_q8_gemv_attn_out", gpu.handle, aq.vp, ad.vp, None, 0, 1, nh, hd, dW.vp, up(r).vp,
              y.vp, E, nh * hd, dlen.vp, maxt)
         assert_bitexact(y.to_host(), exp, f"O after attention L={L}")
         assert int(dlen.to_host()[0]) == L + 1
