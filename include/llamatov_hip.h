@@ -120,9 +120,10 @@ LT_API int lt_kv_append_incr(lt_ctx* ctx, void* kc, const float* k, void* vc, co
  * bpd/lib/ir_param_axes.pl:303-341).
  *   q   [batch][nh*hd] fp32,  out [batch][nh*hd] fp32,
  *   kc, vc  [batch][maxt][nkv*hd] (kv_dtype), len[batch] device ints (valid positions).
- * nsplit == 1: the single-pass order of k_attn_decode_masked.  nsplit > 1: split-K with
- * contiguous ceil(L/nsplit) ranges and an ascending-split combine.  The result does not
- * depend on maxt.  ws must hold lt_attn_workspace_size(...) bytes (0 for nsplit == 1). */
+ * nsplit == 1: the single-pass order of k_attn_decode_masked.  nsplit > 1 (<= 128):
+ * split-K with contiguous ceil(L/nsplit) ranges and an ascending-split combine (a second
+ * launch).  The result does not depend on maxt.  hd % 8 == 0, hd <= 256; each cache below
+ * 2 GiB.  ws must hold lt_attn_workspace_size(...) bytes (0 for nsplit == 1). */
 LT_API int lt_attn_decode(lt_ctx* ctx, const float* q, const void* kc, const void* vc, const int* len,
                    float* out, int batch, int nh, int nkv, int hd, float scale, int maxt,
                    int nsplit, int kv_dtype, void* ws, size_t ws_bytes);

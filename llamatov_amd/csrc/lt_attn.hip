@@ -1,9 +1,11 @@
-// lt_attn.hip -- GQA decode attention over a position-major KV cache, fp32 or fp16.
+// lt_attn.hip -- GQA attention over a position-major KV cache (fp32 or fp16): the decode
+// step's fused RoPE + KV append + attention, batched decode, and causal prefill, all on
+// one workgroup kernel with split-K over the context and a deterministic merge launch.
 //
-// One workgroup per (split, group of HPW query heads sharing one KV head, sequence).
-// A workgroup scores its contiguous range of positions for all HPW heads at once, so
-// each K row is read once for the group; then it folds max and Z per head and the
-// exp-weighted V sum per (head, dim).  The arithmetic of each head is exactly the
+// One workgroup per (split, group of HPW query heads sharing one KV head, sequence or
+// query token).  A workgroup scores its contiguous range of positions for all HPW heads
+// at once, so each K row is read once for the group; then it folds max and Z per head and
+// the exp-weighted V sum per (head, dim).  The arithmetic of each head is exactly the
 // reference's:
 //   score  s_t = (sequential fma over i of q_i*K_t,i) * scale
 //            (bpd/lib/dev_residency.py:1987-1991);
@@ -14,61 +16,62 @@
 //   O_d    sequential fma fold over the range in ascending t.
 // nsplit == 1 writes out = O/Z directly: the single-pass k_attn_decode_masked order
 // (positions >= L contribute exactly nothing there, so maxt does not enter the result).
-// nsplit > 1 writes per-split (m, Z, O) and k_attn_combine merges them in ascending
-// split order, the declared order attn_decode_split (bpd/lib/ir_param_axes.pl:303-341,
+// nsplit > 1 splits the context into contiguous ceil(L/nsplit) ranges, writes per-split
+// (m, Z, O), and k_attn_merge combines them in ascending split order, the declared order
+// attn_decode_split (bpd/lib/ir_param_axes.pl:303-341,
 // bpd/kernelgen/experimental/attn_decode_split.cu:37-91).
-#include "lt_internal.h"
+//
+// Latency structure: the thread's K row and the first V chunk are loaded before any
+// arithmetic; V is staged through LDS in chunks (double-buffered through registers) so
+// the sequential per-dimension chains read LDS; every load of a row that may lie past
+// the range is a buffer load (out-of-range offsets read zeros), so loads never sit
+// behind branches.
+#include "lt_q8_device.h"
 
 namespace {
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+using namespace lt;
+
+constexpr uint32_t kNoRow = 0x80000000u;   // out-of-range buffer offset: reads zeros
+constexpr int kVChunkFloats = 8192;        // 32 KB of staged V per chunk
+
+enum AttnMode { AM_STEP = 0, AM_DECODE = 1, AM_PREFILL = 2 };
+
+struct AttnArgs {
+  const float* qkv;     // AM_STEP: q|k|v of the new token (q, k un-roped)
+  const float* freqs;   // AM_STEP: RoPE frequencies [hd/2]
+  const float* q;       // AM_DECODE / AM_PREFILL: query rows, q_stride floats apart
+  int q_stride;
+  void* kc;
+  void* vc;
+  const int* len;       // STEP: *len = position of the new token; DECODE: len[b]; PREFILL: len[0]
+  float* out;           // [rows][nh*hd] (optional for STEP)
+  int8_t* oq;           // AM_STEP: quantized output (optional)
+  uint16_t* od;
+  float* wsm;           // nsplit > 1: partials
+  float* wsz;
+  float* wso;
+  int nh, nkv, hd;
+  float scale;
+  int maxt, nsplit, per_max;
+};
 
 template <bool kF16>
-__device__ __forceinline__ void load8(const void* base, size_t idx, float v[8]) {
-  if (kF16) {
-    u32x4 w;
-    __builtin_memcpy(&w, (const uint16_t*)base + idx, 16);
-    uint32_t a[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      v[2 * i] = lt_h2f((uint16_t)(a[i] & 0xFFFFu));
-      v[2 * i + 1] = lt_h2f((uint16_t)(a[i] >> 16));
-    }
-  } else {
-    u32x4 w0, w1;
-    __builtin_memcpy(&w0, (const float*)base + idx, 16);
-    __builtin_memcpy(&w1, (const float*)base + idx + 4, 16);
-    uint32_t a[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = __builtin_bit_cast(float, a[i]);
-  }
+__device__ __forceinline__ float kv_round(float v) {
+  return kF16 ? lt_half_to_float_bits(lt_float_to_half_bits(v)) : v;
 }
 
-template <bool kF16>
-__device__ __forceinline__ void load2(const void* base, size_t idx, float& a, float& b) {
-  if (kF16) {
-    uint32_t w;
-    __builtin_memcpy(&w, (const uint16_t*)base + idx, 4);
-    a = lt_h2f((uint16_t)(w & 0xFFFFu));
-    b = lt_h2f((uint16_t)(w >> 16));
-  } else {
-    const float* p = (const float*)base + idx;
-    a = p[0];
-    b = p[1];
-  }
-}
-
-// prefill != 0: the batch is T query tokens of one sequence sharing one cache, query b
-// attending *len + b + 1 positions (causal); q rows are q_stride floats apart.
-template <bool kF16, bool kSplit, int HPW>
-__global__ __launch_bounds__(256) void k_attn_decode(
-    const float* __restrict__ q, const void* __restrict__ kc, const void* __restrict__ vc,
-    const int* __restrict__ len, float* __restrict__ out, float* __restrict__ wsm,
-    float* __restrict__ wsz, float* __restrict__ wso, int nh, int nkv, int hd, float scale,
-    int maxt, int nsplit, int per_max, int q_stride, int prefill) {
+template <bool kF16, int HPW, int MODE>
+__global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
-  float* sq = lds;             // [HPW][hd]
-  float* se = lds + HPW * hd;  // [HPW][per_max]
+  const int hd = A.hd;
+  const int per_max = A.per_max;
+  const int nsplit = A.nsplit;
+  float* sq = lds;                      // [HPW][hd] q (roped in STEP mode)
+  float* sk = sq + HPW * hd;            // [hd] STEP: new k (roped, cache-rounded)
+  float* sv = sk + hd;                  // [hd] STEP: new v (cache-rounded)
+  float* se = sv + hd;                  // [HPW][per_max] scores, then exps
+  float* svt = se + HPW * per_max;      // [kVChunkFloats] staged V (then the output)
   __shared__ float s_mx[HPW];
   __shared__ float s_z[HPW];
 
@@ -76,151 +79,463 @@ __global__ __launch_bounds__(256) void k_attn_decode(
   const int sp = blockIdx.x;
   const int h0 = blockIdx.y * HPW;
   const int b = blockIdx.z;
-  const int rep = nh / nkv;
+  const int rep = A.nh / A.nkv;
   const int g = h0 / rep;
+  const int half = hd >> 1;
+  const int qd = A.nh * hd;
+  const int kvd = A.nkv * hd;
+  const size_t kvrow = (size_t)kvd;
+  constexpr int kEpu = kF16 ? 8 : 4;               // elements per 16-byte unit
+  constexpr int kUpt = kVChunkFloats / kEpu / 256;  // V units per thread per chunk
+  constexpr int kKU = 16;                           // K units prefetched per thread
+  const int upr = hd / kEpu;                        // units per position row
+  const int cpos = kVChunkFloats / hd;              // positions per V chunk
 
-  int L = prefill ? len[0] + b + 1 : len[b];
-  L = L < 0 ? 0 : (L > maxt ? maxt : L);
-  const int per = (L + nsplit - 1) / nsplit;
+  // @phase attn 0
+  // the inputs that do not depend on the length first
+  const int nrope = (HPW + 1) * half;
+  float x1 = 0.0f, x2 = 0.0f, vnew = 0.0f, fr = 0.0f;
+  if (MODE == AM_STEP) {
+    if (tid < nrope) {
+      const int r = tid / half;
+      const int j = tid - r * half;
+      const float* src = r < HPW ? A.qkv + (size_t)(h0 + r) * hd : A.qkv + qd + (size_t)g * hd;
+      x1 = src[j];
+      x2 = src[j + half];
+      fr = A.freqs[j];
+    }
+    if (tid < hd) vnew = A.qkv[qd + kvd + (size_t)g * hd + tid];
+  }
+  // DECODE / PREFILL: the q rows into registers now, into LDS after the K/V loads issue
+  constexpr int kQpt = (HPW * 256 + 255) / 256;   // q values per thread (hd <= 256)
+  float qreg[kQpt];
+  if (MODE != AM_STEP) {
+    const float* qs = A.q + (size_t)b * A.q_stride + (size_t)h0 * hd;
+#pragma unroll
+    for (int k = 0; k < kQpt; k++) qreg[k] = tid + 256 * k < HPW * hd ? qs[tid + 256 * k] : 0.0f;
+  }
+
+  // context: positions [0, nctx); position Lnew (STEP only) comes from registers
+  int Lnew = -1, nctx;
+  bool valid = true;
+  if (MODE == AM_STEP) {
+    Lnew = *A.len;
+    valid = Lnew >= 0 && Lnew < A.maxt;
+    nctx = valid ? Lnew + 1 : 0;
+  } else {
+    const int L = MODE == AM_PREFILL ? A.len[0] + b + 1 : A.len[b];
+    nctx = L < 0 ? 0 : (L > A.maxt ? A.maxt : L);
+  }
+  const int per = (nctx + nsplit - 1) / nsplit;
   const int p0 = sp * per;
   int p1 = p0 + per;
-  if (p1 > L) p1 = L;
+  if (p1 > nctx) p1 = nctx;
   const int n = p1 > p0 ? p1 - p0 : 0;
-
-  const size_t kvrow = (size_t)nkv * hd;
-  const size_t seq_base = prefill ? 0 : (size_t)b * (size_t)maxt * kvrow;
+  const size_t seq_base = MODE == AM_DECODE ? (size_t)b * (size_t)A.maxt * kvrow : 0;
   const size_t head_base = seq_base + (size_t)p0 * kvrow + (size_t)g * hd;
+  const int cache_rows = MODE == AM_DECODE ? (int)gridDim.z * A.maxt : A.maxt;
+  const int ebytes = kF16 ? 2 : 4;
+  const __amdgpu_buffer_rsrc_t krsrc =
+      __builtin_amdgcn_make_buffer_rsrc(A.kc, 0, (int)((size_t)cache_rows * kvrow * ebytes), 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrsrc =
+      __builtin_amdgcn_make_buffer_rsrc(A.vc, 0, (int)((size_t)cache_rows * kvrow * ebytes), 0x00020000);
 
-  for (int i = tid; i < HPW * hd; i += 256) sq[i] = q[(size_t)b * q_stride + (size_t)h0 * hd + i];
+  // @phase attn 1
+  // this thread's first K row and the first V chunk, under the prologue's arithmetic
+  const bool kpre = upr <= kKU;
+  u32x4 kraw[kKU];
+  if (kpre) {
+    const bool real = tid < n && p0 + tid != Lnew;
+#pragma unroll
+    for (int u = 0; u < kKU; u++) {
+      const int off = (real && u < upr) ? (int)((head_base + (size_t)tid * kvrow + u * kEpu) * ebytes) : (int)kNoRow;
+      kraw[u] = __builtin_amdgcn_raw_buffer_load_b128(krsrc, off, 0, 0);
+    }
+  }
+  auto load_vchunk = [&](int c0, u32x4* dst) {
+    const int cn = n - c0 < cpos ? n - c0 : cpos;
+#pragma unroll
+    for (int k = 0; k < kUpt; k++) {
+      const int u = tid + 256 * k;
+      const int t = u / upr;
+      const bool real = t < cn && p0 + c0 + t != Lnew;
+      const size_t e = head_base + (size_t)(c0 + t) * kvrow + (size_t)(u - t * upr) * kEpu;
+      dst[k] = __builtin_amdgcn_raw_buffer_load_b128(vrsrc, real ? (int)(e * ebytes) : (int)kNoRow, 0, 0);
+    }
+  };
+  u32x4 vraw[kUpt];
+  load_vchunk(0, vraw);
+
+  if (MODE == AM_STEP) {
+    // RoPE (the arithmetic of k_rope, rope_from_facts.pl:40-69) of the q heads and of the
+    // group's k; v rounded through the cache's type
+    const float pos = (float)(valid ? Lnew : 0);
+    for (int i = tid; i < nrope; i += 256) {
+      const int r = i / half;
+      const int j = i - r * half;
+      if (i != tid) {
+        const float* src = r < HPW ? A.qkv + (size_t)(h0 + r) * hd : A.qkv + qd + (size_t)g * hd;
+        x1 = src[j];
+        x2 = src[j + half];
+        fr = A.freqs[j];
+      }
+      float s, c;
+      lt_sincosf(pos * fr, &s, &c);
+      const float o1 = fmaf(x1, c, -(x2 * s));
+      const float o2 = fmaf(x1, s, x2 * c);
+      if (r < HPW) {
+        sq[r * hd + j] = o1;
+        sq[r * hd + j + half] = o2;
+      } else {
+        sk[j] = kv_round<kF16>(o1);
+        sk[j + half] = kv_round<kF16>(o2);
+      }
+    }
+    if (tid < hd) sv[tid] = kv_round<kF16>(vnew);
+  } else {
+#pragma unroll
+    for (int k = 0; k < kQpt; k++)
+      if (tid + 256 * k < HPW * hd) sq[tid + 256 * k] = qreg[k];
+  }
   __syncthreads();
+  // @phase attn 2
 
-  // scores: thread per position, HPW sequential-fma chains over i
+  if (MODE == AM_STEP && valid && sp == 0 && (h0 % rep) == 0 && tid < hd) {
+    // the new row into the cache (k_append_kv_incr, dev_residency.py:303-315)
+    const size_t off = (size_t)Lnew * kvrow + (size_t)g * hd + tid;
+    if (kF16) {
+      ((uint16_t*)A.kc)[off] = lt_float_to_half_bits(sk[tid]);
+      ((uint16_t*)A.vc)[off] = lt_float_to_half_bits(sv[tid]);
+    } else {
+      ((float*)A.kc)[off] = sk[tid];
+      ((float*)A.vc)[off] = sv[tid];
+    }
+  }
+
+  // scores: thread per position, HPW sequential fma chains over i
   for (int t = tid; t < n; t += 256) {
     float acc[HPW];
 #pragma unroll
     for (int r = 0; r < HPW; r++) acc[r] = 0.0f;
-    const size_t rowi = head_base + (size_t)t * kvrow;
-    for (int i0 = 0; i0 < hd; i0 += 8) {
-      float kv[8];
-      load8<kF16>(kc, rowi + i0, kv);
+    const bool fresh = p0 + t == Lnew;
+    if (fresh) {
+      for (int i = 0; i < hd; i++) {
+        const float kv = sk[i];
 #pragma unroll
-      for (int ii = 0; ii < 8; ii++)
+        for (int r = 0; r < HPW; r++) acc[r] = fmaf(sq[r * hd + i], kv, acc[r]);
+      }
+    } else if (kpre) {
+      u32x4 kr[kKU];
+      if (t == tid) {
 #pragma unroll
-        for (int r = 0; r < HPW; r++) acc[r] = fmaf(sq[r * hd + i0 + ii], kv[ii], acc[r]);
+        for (int u = 0; u < kKU; u++) kr[u] = kraw[u];
+      } else {   // positions past the first 256: loaded here, all 16 pieces at once
+#pragma unroll
+        for (int u = 0; u < kKU; u++) {
+          const int off = (u < upr) ? (int)((head_base + (size_t)t * kvrow + u * kEpu) * ebytes) : (int)kNoRow;
+          kr[u] = __builtin_amdgcn_raw_buffer_load_b128(krsrc, off, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kKU; u++) {
+        if (u < upr) {
+          const uint32_t a[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
+          if (kF16) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              const float k0 = lt_h2f((uint16_t)(a[q] & 0xFFFFu));
+              const float k1 = lt_h2f((uint16_t)(a[q] >> 16));
+              const int i = u * 8 + 2 * q;
+#pragma unroll
+              for (int r = 0; r < HPW; r++) {
+                acc[r] = fmaf(sq[r * hd + i], k0, acc[r]);
+                acc[r] = fmaf(sq[r * hd + i + 1], k1, acc[r]);
+              }
+            }
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              const float k0 = __builtin_bit_cast(float, a[q]);
+              const int i = u * 4 + q;
+#pragma unroll
+              for (int r = 0; r < HPW; r++) acc[r] = fmaf(sq[r * hd + i], k0, acc[r]);
+            }
+          }
+        }
+      }
+    } else {
+      // rows wider than the prefetch (fp32 with hd > 64): 16-byte pieces in order
+      const size_t rowi = head_base + (size_t)t * kvrow;
+      for (int u = 0; u < upr; u++) {
+        const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(krsrc, (int)((rowi + u * kEpu) * ebytes), 0, 0);
+        const uint32_t a[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const float k0 = __builtin_bit_cast(float, a[q]);
+          const int i = u * 4 + q;
+#pragma unroll
+          for (int r = 0; r < HPW; r++) acc[r] = fmaf(sq[r * hd + i], k0, acc[r]);
+        }
+      }
     }
 #pragma unroll
-    for (int r = 0; r < HPW; r++) se[r * per_max + t] = acc[r] * scale;
+    for (int r = 0; r < HPW; r++) se[r * per_max + t] = acc[r] * A.scale;
   }
   __syncthreads();
 
-  const int wave = tid >> 6, lane = tid & 63;
+  // @phase attn 3
+  const int wave = tid >> 6, wl = tid & 63;
   for (int r = wave; r < HPW; r += 4) {
     float m = -1e30f;
-    for (int t = lane; t < n; t += 64) m = fmaxf(m, se[r * per_max + t]);
-#pragma unroll
-    for (int s = 32; s > 0; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
-    if (lane == 0) s_mx[r] = m;
+    for (int t = wl; t < n; t += 64) m = fmaxf(m, se[r * per_max + t]);
+    m = wave_max(m);
+    if (wl == 0) s_mx[r] = m;
   }
   __syncthreads();
-
   for (int r = 0; r < HPW; r++) {
     const float m = s_mx[r];
     for (int t = tid; t < n; t += 256) se[r * per_max + t] = lt_expf(se[r * per_max + t] - m);
   }
   __syncthreads();
-
   for (int r = wave; r < HPW; r += 4) {
     float ls = 0.0f;
-    for (int t = lane; t < n; t += 64) ls = ls + se[r * per_max + t];
-#pragma unroll
-    for (int s = 32; s > 0; s >>= 1) ls = ls + __shfl_down(ls, s, 64);
-    if (lane == 0) s_z[r] = ls;
+    for (int t = wl; t < n; t += 64) ls = ls + se[r * per_max + t];
+    ls = wave_tree_dpp(ls);   // the frozen 64-lane tree, s = 32 .. 1
+    if (wl == 0) s_z[r] = ls;
   }
-  __syncthreads();
 
-  // O: thread per (head, dim pair); two independent sequential chains over t
-  const int hpairs = hd >> 1;
-  for (int idx = tid; idx < HPW * hpairs; idx += 256) {
-    const int r = idx / hpairs;
-    const int d = (idx - r * hpairs) * 2;
-    const float* e = se + r * per_max;
-    float a0 = 0.0f, a1 = 0.0f;
-    int t = 0;
-    for (; t + 8 <= n; t += 8) {
-      float v0[8], v1[8];
+  // @phase attn 4
+  // O: thread per (head, dim); each a sequential fma chain over t, V staged in LDS in
+  // chunks of cpos positions, the next chunk's loads in flight under this chunk's chains
+  const int nout = HPW * hd;
+  float acc0 = 0.0f, acc1 = 0.0f;   // thread handles outputs tid and tid + 256
+  for (int c0 = 0; c0 < n; c0 += cpos) {
+    const int cn = n - c0 < cpos ? n - c0 : cpos;
+    if (c0 > 0) __syncthreads();   // the previous chunk's readers are done with svt
 #pragma unroll
-      for (int u = 0; u < 8; u++) load2<kF16>(vc, head_base + (size_t)(t + u) * kvrow + d, v0[u], v1[u]);
+    for (int k = 0; k < kUpt; k++) {
+      const int u = tid + 256 * k;
+      const int t = u / upr;
+      if (t < cn) {
+        const int c = u - t * upr;
+        float* dst = svt + t * hd + c * kEpu;
+        if (p0 + c0 + t == Lnew) {
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
-        a0 = fmaf(e[t + u], v0[u], a0);
-        a1 = fmaf(e[t + u], v1[u], a1);
+          for (int q = 0; q < kEpu; q++) dst[q] = sv[c * kEpu + q];
+        } else {
+          const uint32_t a[4] = {vraw[k].x, vraw[k].y, vraw[k].z, vraw[k].w};
+          if (kF16) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              dst[2 * q] = lt_h2f((uint16_t)(a[q] & 0xFFFFu));
+              dst[2 * q + 1] = lt_h2f((uint16_t)(a[q] >> 16));
+            }
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; q++) dst[q] = __builtin_bit_cast(float, a[q]);
+          }
+        }
       }
     }
-    for (; t < n; t++) {
-      float x0, x1;
-      load2<kF16>(vc, head_base + (size_t)t * kvrow + d, x0, x1);
-      a0 = fmaf(e[t], x0, a0);
-      a1 = fmaf(e[t], x1, a1);
+    if (c0 + cpos < n) load_vchunk(c0 + cpos, vraw);
+    __syncthreads();
+    if (tid < nout) {
+      const int r = tid / hd, d = tid - r * hd;
+      const float* e = se + r * per_max + c0;
+      for (int t = 0; t < cn; t++) acc0 = fmaf(e[t], svt[t * hd + d], acc0);
     }
-    const size_t hrow = (size_t)b * nh + h0 + r;
-    if (!kSplit) {
-      out[hrow * hd + d] = a0 / s_z[r];
-      out[hrow * hd + d + 1] = a1 / s_z[r];
+    if (tid + 256 < nout) {
+      const int o = tid + 256;
+      const int r = o / hd, d = o - r * hd;
+      const float* e = se + r * per_max + c0;
+      for (int t = 0; t < cn; t++) acc1 = fmaf(e[t], svt[t * hd + d], acc1);
+    }
+  }
+  __syncthreads();
+  const size_t hrow0 = (size_t)b * A.nh + h0;   // output / partial row of head h0
+  for (int k = 0; k < 2; k++) {
+    const int o = tid + 256 * k;
+    if (o >= nout) break;
+    const int r = o / hd, d = o - r * hd;
+    const float a = k ? acc1 : acc0;
+    if (nsplit == 1) {
+      const float v = valid ? a / s_z[r] : 0.0f;
+      if (A.out) A.out[hrow0 * hd + o] = v;
+      svt[o] = v;
     } else {
-      float* o = wso + (hrow * nsplit + sp) * hd + d;
-      o[0] = a0;
-      o[1] = a1;
+      A.wso[((hrow0 + r) * nsplit + sp) * hd + d] = a;
     }
   }
-  if (kSplit && tid < HPW) {
-    const size_t hrow = (size_t)b * nh + h0 + tid;
-    wsm[hrow * nsplit + sp] = s_mx[tid];
-    wsz[hrow * nsplit + sp] = s_z[tid];
+  if (nsplit > 1) {
+    if (tid < HPW) {
+      A.wsm[(hrow0 + tid) * nsplit + sp] = s_mx[tid];
+      A.wsz[(hrow0 + tid) * nsplit + sp] = s_z[tid];
+    }
+    return;   // k_attn_merge combines the partials
   }
+  // @phase attn 5
+  if (MODE == AM_STEP && A.oq) {
+    // the workgroup's heads are whole 32-element blocks of the attention vector: quantize
+    // them for the O projection (k_quant_q8's quantizer)
+    __syncthreads();
+    const int lane = tid & 31;
+    const size_t o0 = (size_t)h0 * hd;
+    for (int q = tid >> 5; q < nout / 32; q += 8)
+      quant_block_hw(svt[q * 32 + lane], lane, A.oq + o0 + q * 32, A.od + (o0 >> 5) + q);
+  }
+  // @phase attn 6
 }
 
-__global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ wsm,
-                                                      const float* __restrict__ wsz,
-                                                      const float* __restrict__ wso,
-                                                      float* __restrict__ out, int nh, int hd,
-                                                      int nsplit) {
+// Split-K merge, one workgroup per (query head, row): the declared combine in ascending
+// split order (attn_decode_split.cu:37-91): M = max m_s, w_s = exp(m_s - M),
+// Z = sum fma(w_s, Z_s), O_d = sum fma(w_s, O_s,d), out = O/Z; optionally the quant of
+// the head's hd/32 blocks.  Every partial is fetched by independent buffer loads issued at
+// the start (one memory round trip); the exps run one per thread.  len (STEP) marks an
+// out-of-range position: the output is then 0, as in the single pass.
+constexpr int kMergeQ = 16;   // split outputs prefetched per thread
+
+__global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ wsm, const float* __restrict__ wsz,
+                                                    const float* __restrict__ wso, const int* __restrict__ len,
+                                                    int maxt, float* __restrict__ out, int8_t* __restrict__ oq,
+                                                    uint16_t* __restrict__ od, int nh, int hd, int nsplit) {
+  __shared__ float sm[128], sz[128], sw[128], sout[256];
+  __shared__ float s_Z;
   const size_t hrow = (size_t)blockIdx.y * nh + blockIdx.x;
-  const float* m = wsm + hrow * nsplit;
-  const float* z = wsz + hrow * nsplit;
-  float M = -1e30f;
-  for (int s = 0; s < nsplit; s++) M = fmaxf(M, m[s]);
-  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-    float Z = 0.0f, acc = 0.0f;
-    for (int s = 0; s < nsplit; s++) {
-      const float w = lt_expf(m[s] - M);
-      Z = fmaf(w, z[s], Z);
-      acc = fmaf(w, wso[(hrow * nsplit + s) * hd + d], acc);
+  const int tid = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t orsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(wso + hrow * nsplit * hd), 0, nsplit * hd * 4, 0x00020000);
+  float po[kMergeQ];
+  auto load_po = [&](int q0) {
+#pragma unroll
+    for (int q = 0; q < kMergeQ; q++) {
+      const int off = (tid < hd && q0 + q < nsplit) ? ((q0 + q) * hd + tid) * 4 : (int)kNoRow;
+      po[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(orsrc, off, 0, 0));
     }
-    out[hrow * hd + d] = acc / Z;
+  };
+  load_po(0);
+  if (tid < nsplit) {
+    sm[tid] = wsm[hrow * nsplit + tid];
+    sz[tid] = wsz[hrow * nsplit + tid];
+  }
+  bool valid = true;
+  if (len) {
+    const int L = *len;
+    valid = L >= 0 && L < maxt;
+  }
+  __syncthreads();
+  float M = -1e30f;
+  for (int q = 0; q < nsplit; q++) M = fmaxf(M, sm[q]);
+  if (tid < nsplit) sw[tid] = lt_expf(sm[tid] - M);
+  __syncthreads();
+  if (tid == 0) {
+    float Z = 0.0f;
+    for (int q = 0; q < nsplit; q++) Z = fmaf(sw[q], sz[q], Z);
+    s_Z = Z;
+  }
+  float a = 0.0f;
+  for (int q0 = 0; q0 < nsplit; q0 += kMergeQ) {
+    if (q0 > 0) load_po(q0);
+#pragma unroll
+    for (int q = 0; q < kMergeQ; q++)
+      if (q0 + q < nsplit) a = fmaf(sw[q0 + q], po[q], a);
+  }
+  __syncthreads();
+  if (tid < hd) {
+    const float v = valid ? a / s_Z : 0.0f;
+    if (out) out[hrow * hd + tid] = v;
+    sout[tid] = v;
+  }
+  if (oq) {
+    __syncthreads();
+    const int lane = tid & 31;
+    const size_t o0 = hrow * hd;
+    for (int q = tid >> 5; q < hd / 32; q += 8)
+      quant_block_hw(sout[q * 32 + lane], lane, oq + o0 + q * 32, od + (o0 >> 5) + q);
   }
 }
 
-template <bool kF16, bool kSplit>
-hipError_t launch_attn(int hpw, dim3 grid, size_t shm, hipStream_t st, const float* q, const void* kc,
-                       const void* vc, const int* len, float* out, float* wsm, float* wsz, float* wso,
-                       int nh, int nkv, int hd, float scale, int maxt, int nsplit, int per_max,
-                       int q_stride, int prefill) {
-#define LT_ATTN_CASE(H)                                                                      \
-  case H:                                                                                    \
-    k_attn_decode<kF16, kSplit, H><<<grid, 256, shm, st>>>(q, kc, vc, len, out, wsm, wsz, wso, \
-                                                           nh, nkv, hd, scale, maxt, nsplit,  \
-                                                           per_max, q_stride, prefill);       \
+template <bool kF16, int MODE>
+hipError_t launch_attn_k(int hpw, dim3 grid, size_t shm, hipStream_t st, const AttnArgs& A) {
+#define LT_ATTN_CASE(H)                                    \
+  case H:                                                  \
+    k_attn<kF16, H, MODE><<<grid, 256, shm, st>>>(A);      \
     break;
   switch (hpw) {
     LT_ATTN_CASE(1)
     LT_ATTN_CASE(2)
     LT_ATTN_CASE(4)
+    LT_ATTN_CASE(7)
     LT_ATTN_CASE(8)
     default:
       return hipErrorInvalidValue;
   }
 #undef LT_ATTN_CASE
   return hipGetLastError();
+}
+
+// Launches the attention (and the merge when nsplit > 1) for `rows` query rows with hpw
+// heads per workgroup.
+int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, void* ws, size_t ws_bytes,
+                const char* what) {
+  if (A.nsplit > 1) {
+    LT_REQUIRE(A.nsplit <= 128, "%s: nsplit=%d (at most 128)", what, A.nsplit);
+    const size_t need = lt_attn_ws_bytes(rows * A.nh, A.hd, A.nsplit);
+    LT_REQUIRE(ws && lt_aligned(ws, 16), "%s: nsplit=%d needs a 16-byte aligned workspace", what, A.nsplit);
+    if (ws_bytes < need) return lt_fail(LT_ENOMEM, "%s: workspace %zu < %zu bytes", what, ws_bytes, need);
+    const AttnWs w = lt_attn_ws_layout(ws, rows * A.nh, A.hd, A.nsplit);
+    A.wsm = w.m;
+    A.wsz = w.z;
+    A.wso = w.o;
+  }
+  A.per_max = (A.maxt + A.nsplit - 1) / A.nsplit;
+  const size_t shm = ((size_t)hpw * A.hd + 2 * A.hd + (size_t)hpw * A.per_max + kVChunkFloats) * sizeof(float);
+  if (shm > 64 * 1024)
+    return lt_fail(LT_EINVAL, "%s: %zu bytes of LDS for maxt=%d nsplit=%d; raise nsplit", what, shm, A.maxt,
+                   A.nsplit);
+  const dim3 grid(A.nsplit, A.nh / hpw, rows);
+  hipError_t e;
+  if (mode == AM_STEP)
+    e = f16 ? launch_attn_k<true, AM_STEP>(hpw, grid, shm, ctx->stream, A)
+            : launch_attn_k<false, AM_STEP>(hpw, grid, shm, ctx->stream, A);
+  else if (mode == AM_DECODE)
+    e = f16 ? launch_attn_k<true, AM_DECODE>(hpw, grid, shm, ctx->stream, A)
+            : launch_attn_k<false, AM_DECODE>(hpw, grid, shm, ctx->stream, A);
+  else
+    e = f16 ? launch_attn_k<true, AM_PREFILL>(hpw, grid, shm, ctx->stream, A)
+            : launch_attn_k<false, AM_PREFILL>(hpw, grid, shm, ctx->stream, A);
+  if (e != hipSuccess) return lt_fail_hip(e, what, __FILE__, __LINE__);
+  if (A.nsplit > 1) {
+    k_attn_merge<<<dim3(A.nh, rows), 256, 0, ctx->stream>>>(A.wsm, A.wsz, A.wso, mode == AM_STEP ? A.len : nullptr,
+                                                            A.maxt, A.out, A.oq, A.od, A.nh, A.hd, A.nsplit);
+    return lt_check_launch("k_attn_merge");
+  }
+  return lt_check_launch("k_attn");
+}
+
+// Heads per workgroup: short caches are latency-bound (one head per workgroup keeps each
+// thread's chains short); large caches are bandwidth-bound (the heads of a KV group share
+// one workgroup so every K/V row is read once).
+int pick_hpw(int nh, int nkv, int hd, size_t cache_bytes) {
+  const int rep = nh / nkv;
+  if (cache_bytes > ((size_t)4 << 20))
+    for (int c : {8, 7, 4, 2})
+      if (rep % c == 0 && c * hd <= 512) return c;
+  return 1;
+}
+
+int check_common(int nh, int nkv, int hd, int maxt, int nsplit, int kv_dtype, const void* kc, const void* vc,
+                 size_t cache_bytes, const char* what) {
+  LT_REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0, "%s: nh=%d nkv=%d", what, nh, nkv);
+  LT_REQUIRE(hd > 0 && hd % 8 == 0 && hd <= 256, "%s: hd=%d (multiple of 8, <= 256)", what, hd);
+  LT_REQUIRE(maxt > 0 && nsplit >= 1 && nsplit <= maxt, "%s: maxt=%d nsplit=%d", what, maxt, nsplit);
+  LT_REQUIRE(kv_dtype == LT_KV_F32 || kv_dtype == LT_KV_F16, "%s: kv_dtype=%d", what, kv_dtype);
+  LT_REQUIRE(lt_aligned(kc, 16) && lt_aligned(vc, 16), "%s: K/V caches must be 16-byte aligned", what);
+  LT_REQUIRE(cache_bytes < ((size_t)1 << 31), "%s: %zu bytes of K (or V) cache (at most 2 GiB)", what, cache_bytes);
+  return LT_OK;
+}
+
+size_t cache_bytes_of(int rows, int maxt, int nkv, int hd, int kv_dtype) {
+  return (size_t)rows * maxt * nkv * hd * (kv_dtype == LT_KV_F16 ? 2 : 4);
 }
 
 }  // namespace
@@ -232,66 +547,49 @@ size_t lt_attn_workspace_size(int batch, int nh, int hd, int nsplit) {
   return lt_attn_ws_bytes(batch * nh, hd, nsplit);
 }
 
-static int attn_impl(lt_ctx* ctx, const float* q, const void* kc, const void* vc, const int* len,
-                     float* out, int batch, int nh, int nkv, int hd, float scale, int maxt, int nsplit,
-                     int kv_dtype, void* ws, size_t ws_bytes, int q_stride, int prefill) {
-  LT_REQUIRE(ctx && q && kc && vc && len && out, "lt_attn_decode: null argument");
-  LT_REQUIRE(q_stride >= nh * hd, "lt_attn: q_stride=%d < nh*hd", q_stride);
-  LT_REQUIRE(batch > 0 && nh > 0 && nkv > 0 && nh % nkv == 0, "lt_attn_decode: batch=%d nh=%d nkv=%d", batch, nh, nkv);
-  LT_REQUIRE(hd > 0 && hd % 8 == 0 && hd <= 512, "lt_attn_decode: hd=%d (multiple of 8, <= 512)", hd);
-  LT_REQUIRE(maxt > 0 && nsplit >= 1 && nsplit <= maxt, "lt_attn_decode: maxt=%d nsplit=%d", maxt, nsplit);
-  LT_REQUIRE(kv_dtype == LT_KV_F32 || kv_dtype == LT_KV_F16, "lt_attn_decode: kv_dtype=%d", kv_dtype);
-  LT_REQUIRE(lt_aligned(kc, 16) && lt_aligned(vc, 16), "lt_attn_decode: K/V caches must be 16-byte aligned");
-  const int rep = nh / nkv;
-  int hpw = 1;
-  if (nsplit > 1) {
-    for (int c : {8, 4, 2})
-      if (rep % c == 0) { hpw = c; break; }
-  }
-  const int per_max = (maxt + nsplit - 1) / nsplit;
-  const size_t shm = (size_t)hpw * (hd + per_max) * sizeof(float);
-  if (shm > 64 * 1024)
-    return lt_fail(LT_EINVAL, "lt_attn_decode: %zu bytes of LDS for maxt=%d nsplit=%d; raise nsplit", shm, maxt, nsplit);
-  dim3 grid(nsplit, nh / hpw, batch);
-  float *wsm = nullptr, *wsz = nullptr, *wso = nullptr;
-  if (nsplit > 1) {
-    size_t need = lt_attn_workspace_size(batch, nh, hd, nsplit);
-    LT_REQUIRE(ws != nullptr, "lt_attn_decode: nsplit=%d needs a workspace", nsplit);
-    if (ws_bytes < need) return lt_fail(LT_ENOMEM, "lt_attn_decode: workspace %zu < %zu bytes", ws_bytes, need);
-    LT_REQUIRE(lt_aligned(ws, 16), "lt_attn_decode: workspace must be 16-byte aligned");
-    const AttnWs w = lt_attn_ws_layout(ws, batch * nh, hd, nsplit);
-    wsm = w.m;
-    wsz = w.z;
-    wso = w.o;
-  }
-  hipError_t e;
-  const bool f16 = kv_dtype == LT_KV_F16;
-  if (nsplit == 1)
-    e = f16 ? launch_attn<true, false>(hpw, grid, shm, ctx->stream, q, kc, vc, len, out, wsm, wsz, wso, nh, nkv, hd, scale, maxt, nsplit, per_max, q_stride, prefill)
-            : launch_attn<false, false>(hpw, grid, shm, ctx->stream, q, kc, vc, len, out, wsm, wsz, wso, nh, nkv, hd, scale, maxt, nsplit, per_max, q_stride, prefill);
-  else
-    e = f16 ? launch_attn<true, true>(hpw, grid, shm, ctx->stream, q, kc, vc, len, out, wsm, wsz, wso, nh, nkv, hd, scale, maxt, nsplit, per_max, q_stride, prefill)
-            : launch_attn<false, true>(hpw, grid, shm, ctx->stream, q, kc, vc, len, out, wsm, wsz, wso, nh, nkv, hd, scale, maxt, nsplit, per_max, q_stride, prefill);
-  if (e != hipSuccess) return lt_fail_hip(e, "k_attn_decode launch", __FILE__, __LINE__);
-  if (nsplit > 1) {
-    k_attn_combine<<<dim3(nh, batch), hd < 256 ? hd : 256, 0, ctx->stream>>>(wsm, wsz, wso, out, nh, hd, nsplit);
-    return lt_check_launch("k_attn_combine");
-  }
-  return LT_OK;
-}
-
 int lt_attn_decode(lt_ctx* ctx, const float* q, const void* kc, const void* vc, const int* len,
                    float* out, int batch, int nh, int nkv, int hd, float scale, int maxt, int nsplit,
                    int kv_dtype, void* ws, size_t ws_bytes) {
-  return attn_impl(ctx, q, kc, vc, len, out, batch, nh, nkv, hd, scale, maxt, nsplit, kv_dtype, ws, ws_bytes,
-                   nh * hd, 0);
+  LT_REQUIRE(ctx && q && kc && vc && len && out, "lt_attn_decode: null argument");
+  LT_REQUIRE(batch > 0, "lt_attn_decode: batch=%d", batch);
+  const size_t cb = cache_bytes_of(batch, maxt, nkv, hd, kv_dtype);
+  if (int rc = check_common(nh, nkv, hd, maxt, nsplit, kv_dtype, kc, vc, cb, "lt_attn_decode")) return rc;
+  AttnArgs A = {};
+  A.q = q; A.q_stride = nh * hd; A.kc = (void*)kc; A.vc = (void*)vc; A.len = len; A.out = out;
+  A.nh = nh; A.nkv = nkv; A.hd = hd; A.scale = scale; A.maxt = maxt; A.nsplit = nsplit;
+  return launch_attn(ctx, AM_DECODE, kv_dtype == LT_KV_F16, pick_hpw(nh, nkv, hd, cb / batch), batch, A, ws,
+                     ws_bytes, "lt_attn_decode");
 }
 
 int lt_attn_prefill(lt_ctx* ctx, const float* q, int q_stride, const void* kc, const void* vc, const int* len0,
                     float* out, int T, int nh, int nkv, int hd, float scale, int maxt, int nsplit, int kv_dtype,
                     void* ws, size_t ws_bytes) {
-  return attn_impl(ctx, q, kc, vc, len0, out, T, nh, nkv, hd, scale, maxt, nsplit, kv_dtype, ws, ws_bytes,
-                   q_stride, 1);
+  LT_REQUIRE(ctx && q && kc && vc && len0 && out, "lt_attn_prefill: null argument");
+  LT_REQUIRE(T > 0 && q_stride >= nh * hd, "lt_attn_prefill: T=%d q_stride=%d", T, q_stride);
+  const size_t cb = cache_bytes_of(1, maxt, nkv, hd, kv_dtype);
+  if (int rc = check_common(nh, nkv, hd, maxt, nsplit, kv_dtype, kc, vc, cb, "lt_attn_prefill")) return rc;
+  AttnArgs A = {};
+  A.q = q; A.q_stride = q_stride; A.kc = (void*)kc; A.vc = (void*)vc; A.len = len0; A.out = out;
+  A.nh = nh; A.nkv = nkv; A.hd = hd; A.scale = scale; A.maxt = maxt; A.nsplit = nsplit;
+  // the T query rows of one sequence re-read the same rows: the heads of a KV group share
+  // each workgroup whenever the group divides
+  return launch_attn(ctx, AM_PREFILL, kv_dtype == LT_KV_F16, pick_hpw(nh, nkv, hd, (size_t)1 << 30), T, A, ws,
+                     ws_bytes, "lt_attn_prefill");
+}
+
+int lt_attn_step(lt_ctx* ctx, const float* qkv, const float* freqs, void* kc, void* vc, const int* len,
+                 float* out, int8_t* xq, uint16_t* xd, int nh, int nkv, int hd, float scale, int maxt, int nsplit,
+                 int kv_dtype, void* ws, size_t ws_bytes) {
+  LT_REQUIRE(ctx && qkv && freqs && kc && vc && len, "lt_attn_step: null argument");
+  const size_t cb = cache_bytes_of(1, maxt, nkv, hd, kv_dtype);
+  if (int rc = check_common(nh, nkv, hd, maxt, nsplit, kv_dtype, kc, vc, cb, "lt_attn_step")) return rc;
+  LT_REQUIRE(out || xq, "lt_attn_step: needs out or xq/xd");
+  LT_REQUIRE(!xq || (xd && hd % 32 == 0), "lt_attn_step: quantized output needs xd and hd %% 32 == 0");
+  AttnArgs A = {};
+  A.qkv = qkv; A.freqs = freqs; A.kc = kc; A.vc = vc; A.len = len; A.out = out; A.oq = xq; A.od = xd;
+  A.nh = nh; A.nkv = nkv; A.hd = hd; A.scale = scale; A.maxt = maxt; A.nsplit = nsplit;
+  return launch_attn(ctx, AM_STEP, kv_dtype == LT_KV_F16, pick_hpw(nh, nkv, hd, cb), 1, A, ws, ws_bytes,
+                     "lt_attn_step");
 }
 
 }  // extern "C"

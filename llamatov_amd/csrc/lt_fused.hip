@@ -106,58 +106,62 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t f32_rsrc(const float* p, int n
 //  - strided: slot s of thread t holds element s*256 + t (the rms_ss order's lanes);
 //  - vector:  group v of thread t holds elements 4t + 1024v .. +3, so a 32-element block
 //    lives on 8 consecutive lanes (quant4 / q4_to_rec).
-// KS = ceil(K/256) strided slots; KV vector groups are held at once (all of them for
-// K <= 4096, else the groups are processed KV at a time).
-template <int KS>
+// KS = ceil(K/256) strided slots (held by the first 256 threads); a workgroup of NT
+// threads covers 4*NT elements per vector group; KV groups are held at once (all of them
+// up to 4), the rest are processed KV at a time.
+template <int KS, int NT = kThreads>
 struct Slots {
-  static constexpr int KV = KS >= 16 ? 4 : 1;
-  static constexpr int NV = KS >= 16 ? KS / 4 : 1;   // vector groups in all
+  static constexpr int NV = (KS * 256 + 4 * NT - 1) / (4 * NT);   // vector groups in all
+  static constexpr int KV = NV < 4 ? NV : 4;
   float s[KS];       // strided x (sum of squares only)
   f32x4 x[KV];       // vector x
   f32x4 w[KV];       // vector norm weight
 };
 
-template <int KS>
+template <int KS, int NT>
 __device__ __forceinline__ void load_vgroups(const float* __restrict__ x, const float* __restrict__ w, int K,
-                                             int v0, Slots<KS>& S) {
+                                             int v0, Slots<KS, NT>& S) {
   const __amdgpu_buffer_rsrc_t rx = f32_rsrc(x, K);
   const int t = threadIdx.x;
 #pragma unroll
-  for (int v = 0; v < Slots<KS>::KV; v++)
-    S.x[v] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (t + kThreads * (v0 + v)) * 16, 0, 0));
+  for (int v = 0; v < Slots<KS, NT>::KV; v++)
+    S.x[v] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (t + NT * (v0 + v)) * 16, 0, 0));
   if (w) {
     const __amdgpu_buffer_rsrc_t rw = f32_rsrc(w, K);
 #pragma unroll
-    for (int v = 0; v < Slots<KS>::KV; v++)
-      S.w[v] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (t + kThreads * (v0 + v)) * 16, 0, 0));
+    for (int v = 0; v < Slots<KS, NT>::KV; v++)
+      S.w[v] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (t + NT * (v0 + v)) * 16, 0, 0));
   }
 }
 
-// kStrided: also load the strided copy of x for the sum of squares.
-template <int KS, bool kStrided>
+// kStrided: also load the strided copy of x for the sum of squares (threads < 256).
+template <int KS, bool kStrided, int NT = kThreads>
 __device__ __forceinline__ void load_slots(const float* __restrict__ x, const float* __restrict__ w, int K,
-                                           Slots<KS>& S) {
+                                           Slots<KS, NT>& S) {
   if (kStrided) {
     const __amdgpu_buffer_rsrc_t rx = f32_rsrc(x, K);
+    const int t = threadIdx.x;
 #pragma unroll
-    for (int s = 0; s < KS; s++)
-      S.s[s] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, (s * kThreads + (int)threadIdx.x) * 4, 0, 0));
+    for (int s = 0; s < KS; s++) {
+      const int off = (NT == 256 || t < 256) ? (s * 256 + t) * 4 : (int)0x80000000;
+      S.s[s] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, off, 0, 0));
+    }
   }
-  load_vgroups<KS>(x, w, K, 0, S);
+  load_vgroups<KS, NT>(x, w, K, 0, S);
 }
 
 // Quantize the vector groups into records (optionally normalized: y = (x*inv)*w).  The
-// groups past the first KV are loaded here (K > 4096).
-template <int KS, bool kNorm>
-__device__ __forceinline__ void slots_to_rec(Slots<KS>& S, const float* __restrict__ x, const float* __restrict__ w,
-                                             float inv, int K, uint32_t* rec) {
+// groups past the first KV are loaded here (K > 16*NT).
+template <int KS, bool kNorm, int NT = kThreads>
+__device__ __forceinline__ void slots_to_rec(Slots<KS, NT>& S, const float* __restrict__ x,
+                                             const float* __restrict__ w, float inv, int K, uint32_t* rec) {
   const int t = threadIdx.x;
   const int j = t & 7;
   const int nb = K >> 5;
-  constexpr int KV = Slots<KS>::KV;
+  constexpr int KV = Slots<KS, NT>::KV;
 #pragma unroll
-  for (int v0 = 0; v0 < Slots<KS>::NV; v0 += KV) {
-    if (v0 > 0) load_vgroups<KS>(x, kNorm ? w : nullptr, K, v0, S);
+  for (int v0 = 0; v0 < Slots<KS, NT>::NV; v0 += KV) {
+    if (v0 > 0) load_vgroups<KS, NT>(x, kNorm ? w : nullptr, K, v0, S);
     uint32_t p[KV];
     QScale sc[KV];
 #pragma unroll
@@ -173,7 +177,7 @@ __device__ __forceinline__ void slots_to_rec(Slots<KS>& S, const float* __restri
     }
 #pragma unroll
     for (int v = 0; v < KV; v++) {
-      const int b = (t >> 3) + 32 * (v0 + v);
+      const int b = (t >> 3) + (NT / 8) * (v0 + v);
       q4_to_rec(p[v], sc[v].dq, j, b < nb, rec + b * kRecDwords);
     }
   }
@@ -200,13 +204,13 @@ __device__ __forceinline__ void lds_slots(const float* xrow, const float* __rest
 // rms_ss order (norm_softmax_from_facts.pl:49, 83-108): thread t folds x[t], x[t+256], ...
 // by fma, then the pairwise tree 128..1; inv = rsqrt(ss/N + eps).  Slots past K hold
 // zeros, which leave the fold unchanged (p + 0*0 == p for p >= 0).
-template <int KS>
-__device__ __forceinline__ float rms_inv(const Slots<KS>& S, int K, float eps, float* red, float* sinv) {
+template <int KS, int NT>
+__device__ __forceinline__ float rms_inv(const Slots<KS, NT>& S, int K, float eps, float* red, float* sinv) {
   const int t = threadIdx.x;
   float p = 0.0f;
 #pragma unroll
   for (int s = 0; s < KS; s++) p = fmaf(S.s[s], S.s[s], p);
-  red[t] = p;
+  if (NT == 256 || t < 256) red[t] = p;
   __syncthreads();
   if (t < 64) {
     float a = red[t] + red[t + 128];
@@ -243,37 +247,42 @@ __device__ __forceinline__ void pro_merge_quant(const GemvParams& P, uint32_t* r
 }
 
 // Staged int8 quants + fp16 scales: copied through LDS, then laid out as records.
-constexpr int kStageChunks = 4;   // 16-byte chunks of xq per thread (K <= 16384)
+constexpr int kStageChunks = 4;   // 16-byte chunks of xq per thread of a 256-thread workgroup (K <= 16384)
 
+template <int NT = kThreads>
 struct StageRegs {
-  u32x4 c[kStageChunks];
-  uint16_t d[2];
+  static constexpr int C = kStageChunks * 256 / NT;   // chunks per thread
+  static constexpr int DS = 2 * 256 / NT > 0 ? 2 * 256 / NT : 1;   // scales per thread
+  u32x4 c[C];
+  uint16_t d[DS];
 };
 
+template <int NT = kThreads>
 __device__ __forceinline__ void load_stage(const int8_t* __restrict__ xq, const uint16_t* __restrict__ xd,
-                                           int K, StageRegs& R) {
+                                           int K, StageRegs<NT>& R) {
   // buffer loads: chunks past K and scales past K/32 read zeros, with no branches
   const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)xq, 0, K, 0x00020000);
   const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc((void*)xd, 0, (K / 32) * 2, 0x00020000);
 #pragma unroll
-  for (int k = 0; k < kStageChunks; k++)
-    R.c[k] = __builtin_amdgcn_raw_buffer_load_b128(rq, (threadIdx.x + kThreads * k) * 16, 0, 0);
+  for (int k = 0; k < StageRegs<NT>::C; k++)
+    R.c[k] = __builtin_amdgcn_raw_buffer_load_b128(rq, (threadIdx.x + NT * k) * 16, 0, 0);
 #pragma unroll
-  for (int k = 0; k < 2; k++)
-    R.d[k] = __builtin_amdgcn_raw_buffer_load_b16(rd, (threadIdx.x + kThreads * k) * 2, 0, 0);
+  for (int k = 0; k < StageRegs<NT>::DS; k++)
+    R.d[k] = __builtin_amdgcn_raw_buffer_load_b16(rd, (threadIdx.x + NT * k) * 2, 0, 0);
 }
 
-__device__ __forceinline__ void stage_to_rec(const StageRegs& R, int K, uint8_t* sxq, uint32_t* rec) {
+template <int NT = kThreads>
+__device__ __forceinline__ void stage_to_rec(const StageRegs<NT>& R, int K, uint8_t* sxq, uint32_t* rec) {
   u32x4* dst = (u32x4*)sxq;
 #pragma unroll
-  for (int k = 0; k < kStageChunks; k++) {
-    const int i = threadIdx.x + kThreads * k;
+  for (int k = 0; k < StageRegs<NT>::C; k++) {
+    const int i = threadIdx.x + NT * k;
     if (i < K / 16) dst[i] = R.c[k];
   }
   __syncthreads();
   const uint32_t* X = (const uint32_t*)sxq;   // 8 dwords per block
   const int nb = K >> 5;
-  for (int i = threadIdx.x; i < nb * 9; i += kThreads) {
+  for (int i = threadIdx.x; i < nb * 9; i += NT) {
     const int b = i / 9;
     const int j = i - b * 9;
     uint32_t* r = rec + b * kRecDwords;
@@ -283,8 +292,8 @@ __device__ __forceinline__ void stage_to_rec(const StageRegs& R, int K, uint8_t*
     r[kRecPhase + j] = lo;
   }
 #pragma unroll
-  for (int k = 0; k < 2; k++) {
-    const int b = threadIdx.x + kThreads * k;
+  for (int k = 0; k < StageRegs<NT>::DS; k++) {
+    const int b = threadIdx.x + NT * k;
     if (b < nb) {
       const uint32_t xdf = __builtin_bit_cast(uint32_t, lt_h2f(R.d[k]));
       rec[b * kRecDwords + 9] = xdf;
@@ -295,8 +304,9 @@ __device__ __forceinline__ void stage_to_rec(const StageRegs& R, int K, uint8_t*
 
 // ---- the fused GEMV ----------------------------------------------------------------
 //
-// Half-wave hw (0..7) of workgroup w takes rows w*row0 + hw + step*i (i < max_rows): 8
-// contiguous rows per workgroup pass, or workgroups striding over groups of 8 rows.  Each
+// Half-wave hw (0..7) of workgroup w takes rows w*row0 + hw + step*i (i < max_rows): one
+// group of 8 rows per workgroup, or (large N) a contiguous block of row0 rows per
+// workgroup, walked 8 rows at a time.  Each
 // row is the canonical Q8_0 dot: lane L folds blocks L, L+32, ... by fma, then the 5-level
 // shfl_down tree (q8_0_from_facts.pl:466-516).
 //
@@ -327,7 +337,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
 
   // (1) the prologue's global inputs
   Slots<KS> S;
-  StageRegs SR;
+  StageRegs<> SR;
   int tok = 0;
   if constexpr (PRO == PRO_RMS) load_slots<KS, true>(P.x, P.nw, K, S);
   else if constexpr (PRO == PRO_QUANT) load_slots<KS, false>(P.x, nullptr, K, S);
@@ -554,381 +564,6 @@ __global__ __launch_bounds__(kFinThreads) void k_argmax_finalize(const float* __
   }
 }
 
-// ---- fused RoPE + KV append + attention --------------------------------------------
-//
-// One workgroup per (split, group of HPW query heads sharing a KV head).  The new token
-// sits at position L = *len.  Every workgroup ropes its own q heads and the group's new
-// k row (rope_from_facts.pl:40-69, the arithmetic of k_rope), rounds k and v through
-// fp16 when the cache is fp16, and uses those values for position L directly; the one
-// workgroup with split 0 and the group's first head stores the row into the cache
-// (k_append_kv_incr, dev_residency.py:303-315).  Positions < L are read from the cache.
-// The attention arithmetic is lt_attn.hip's (the reference's masked single pass, or the
-// declared split-K partials when nsplit > 1).  V is staged through LDS in chunks so the
-// sequential per-dimension fma chains read LDS, not HBM.
-constexpr int kVChunkFloats = 8192;   // 32 KB of staged V per chunk
-
-template <bool kF16>
-__device__ __forceinline__ float kv_at(const void* base, size_t idx) {
-  return kF16 ? lt_h2f(((const uint16_t*)base)[idx]) : ((const float*)base)[idx];
-}
-
-template <bool kF16>
-__device__ __forceinline__ float kv_round(float v) {
-  return kF16 ? lt_half_to_float_bits(lt_float_to_half_bits(v)) : v;
-}
-
-template <bool kF16, int HPW>
-__global__ __launch_bounds__(256) void k_attn_step(
-    const float* __restrict__ qkv, const float* __restrict__ freqs, void* __restrict__ kc,
-    void* __restrict__ vc, const int* __restrict__ len, float* __restrict__ out,
-    int8_t* __restrict__ oq, uint16_t* __restrict__ od, float* __restrict__ wsm,
-    float* __restrict__ wsz, float* __restrict__ wso, int nh, int nkv, int hd, float scale, int maxt,
-    int nsplit, int per_max) {
-  extern __shared__ __attribute__((aligned(16))) float lds[];
-  float* sq = lds;                      // [HPW][hd] roped q
-  float* sk = sq + HPW * hd;            // [hd] new k (roped, cache-rounded)
-  float* sv = sk + hd;                  // [hd] new v (cache-rounded)
-  float* se = sv + hd;                  // [HPW][per_max] scores, then exps
-  float* svt = se + HPW * per_max;      // [kVChunkFloats] staged V (then the output)
-  __shared__ float s_mx[HPW];
-  __shared__ float s_z[HPW];
-
-  const int tid = threadIdx.x;
-  const int sp = blockIdx.x;
-  const int h0 = blockIdx.y * HPW;
-  const int rep = nh / nkv;
-  const int g = h0 / rep;
-  const int half = hd >> 1;
-  const int qd = nh * hd;
-  const int kvd = nkv * hd;
-  const size_t kvrow = (size_t)kvd;
-  constexpr int kEpu = kF16 ? 8 : 4;               // elements per 16-byte unit
-  constexpr int kUpt = kVChunkFloats / kEpu / 256;  // V units per thread per chunk
-  constexpr int kKU = HPW <= 2 ? 16 : 1;            // K units prefetched per thread (fp16, hd <= 128)
-  const int upr = hd / kEpu;                        // units per position row
-  const int cpos = kVChunkFloats / hd;              // positions per V chunk
-
-  // @phase attn 0
-  // RoPE inputs do not depend on the length: load them first
-  const int nrope = (HPW + 1) * half;
-  float x1 = 0.0f, x2 = 0.0f, vnew = 0.0f, fr = 0.0f;
-  if (tid < nrope) {
-    const int r = tid / half;
-    const int j = tid - r * half;
-    const float* src = r < HPW ? qkv + (size_t)(h0 + r) * hd : qkv + qd + (size_t)g * hd;
-    x1 = src[j];
-    x2 = src[j + half];
-    fr = freqs[j];
-  }
-  if (tid < hd) vnew = qkv[qd + kvd + (size_t)g * hd + tid];
-
-  const int L = *len;
-  const bool valid = L >= 0 && L < maxt;
-  const int nctx = valid ? L + 1 : 0;
-  const int per = (nctx + nsplit - 1) / nsplit;
-  const int p0 = sp * per;
-  int p1 = p0 + per;
-  if (p1 > nctx) p1 = nctx;
-  const int n = p1 > p0 ? p1 - p0 : 0;
-  const size_t head_base = (size_t)p0 * kvrow + (size_t)g * hd;
-
-  // @phase attn 1
-  // issue this thread's first K row and the first V chunk now, under the RoPE work
-  const bool kpre = kF16 && upr <= kKU && tid < n && p0 + tid != L;
-  u32x4 kraw[kKU];
-  if (kpre) {
-#pragma unroll
-    for (int u = 0; u < kKU; u++)
-      if (u < upr) __builtin_memcpy(&kraw[u], (const uint16_t*)kc + head_base + (size_t)tid * kvrow + u * kEpu, 16);
-  }
-  // V rows through a buffer resource: rows past the range (and row L, which comes from
-  // registers) read as zeros without touching memory, so every load is unconditional
-  const __amdgpu_buffer_rsrc_t vrsrc = __builtin_amdgcn_make_buffer_rsrc(
-      vc, 0, (int)((size_t)maxt * kvrow * (kF16 ? 2 : 4)), 0x00020000);
-  auto load_vchunk = [&](int c0, u32x4* dst) {
-    const int cn = n - c0 < cpos ? n - c0 : cpos;
-#pragma unroll
-    for (int k = 0; k < kUpt; k++) {
-      const int u = tid + 256 * k;
-      const int t = u / upr;
-      const bool real = t < cn && p0 + c0 + t != L;
-      const size_t e = head_base + (size_t)(c0 + t) * kvrow + (size_t)(u - t * upr) * kEpu;
-      const int off = real ? (int)(e * (kF16 ? 2 : 4)) : (int)kNoBlock;
-      dst[k] = __builtin_amdgcn_raw_buffer_load_b128(vrsrc, off, 0, 0);
-    }
-  };
-  u32x4 vraw[kUpt];
-  load_vchunk(0, vraw);
-
-  // RoPE (the arithmetic of k_rope) of the q heads and of the group's k; v rounded
-  const float pos = (float)(valid ? L : 0);
-  for (int i = tid; i < nrope; i += 256) {
-    const int r = i / half;
-    const int j = i - r * half;
-    if (i != tid) {
-      const float* src = r < HPW ? qkv + (size_t)(h0 + r) * hd : qkv + qd + (size_t)g * hd;
-      x1 = src[j];
-      x2 = src[j + half];
-      fr = freqs[j];
-    }
-    float s, c;
-    lt_sincosf(pos * fr, &s, &c);
-    const float o1 = fmaf(x1, c, -(x2 * s));
-    const float o2 = fmaf(x1, s, x2 * c);
-    if (r < HPW) {
-      sq[r * hd + j] = o1;
-      sq[r * hd + j + half] = o2;
-    } else {
-      sk[j] = kv_round<kF16>(o1);
-      sk[j + half] = kv_round<kF16>(o2);
-    }
-  }
-  if (tid < hd) sv[tid] = kv_round<kF16>(vnew);
-  __syncthreads();
-  // @phase attn 2
-
-  if (valid && sp == 0 && (h0 % rep) == 0 && tid < hd) {
-    const size_t off = (size_t)L * kvrow + (size_t)g * hd + tid;
-    if (kF16) {
-      ((uint16_t*)kc)[off] = lt_float_to_half_bits(sk[tid]);
-      ((uint16_t*)vc)[off] = lt_float_to_half_bits(sv[tid]);
-    } else {
-      ((float*)kc)[off] = sk[tid];
-      ((float*)vc)[off] = sv[tid];
-    }
-  }
-
-  // scores: thread per position, HPW sequential fma chains over i
-  for (int t = tid; t < n; t += 256) {
-    float acc[HPW];
-#pragma unroll
-    for (int r = 0; r < HPW; r++) acc[r] = 0.0f;
-    if (p0 + t == L) {
-      for (int i = 0; i < hd; i++) {
-        const float kv = sk[i];
-#pragma unroll
-        for (int r = 0; r < HPW; r++) acc[r] = fmaf(sq[r * hd + i], kv, acc[r]);
-      }
-    } else if (kpre && t == tid) {
-#pragma unroll
-      for (int u = 0; u < kKU; u++) {
-        if (u < upr) {
-          const uint32_t a[4] = {kraw[u].x, kraw[u].y, kraw[u].z, kraw[u].w};
-#pragma unroll
-          for (int q = 0; q < 4; q++) {
-            const float k0 = lt_h2f((uint16_t)(a[q] & 0xFFFFu));
-            const float k1 = lt_h2f((uint16_t)(a[q] >> 16));
-            const int i = u * 8 + 2 * q;
-#pragma unroll
-            for (int r = 0; r < HPW; r++) {
-              acc[r] = fmaf(sq[r * hd + i], k0, acc[r]);
-              acc[r] = fmaf(sq[r * hd + i + 1], k1, acc[r]);
-            }
-          }
-        }
-      }
-    } else {
-      const size_t rowi = head_base + (size_t)t * kvrow;
-      for (int i0 = 0; i0 < hd; i0 += 8) {
-        float kv[8];
-        if (kF16) {
-          u32x4 w;
-          __builtin_memcpy(&w, (const uint16_t*)kc + rowi + i0, 16);
-          const uint32_t a[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-          for (int q = 0; q < 4; q++) {
-            kv[2 * q] = lt_h2f((uint16_t)(a[q] & 0xFFFFu));
-            kv[2 * q + 1] = lt_h2f((uint16_t)(a[q] >> 16));
-          }
-        } else {
-          u32x4 w0, w1;
-          __builtin_memcpy(&w0, (const float*)kc + rowi + i0, 16);
-          __builtin_memcpy(&w1, (const float*)kc + rowi + i0 + 4, 16);
-          const uint32_t a[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-          for (int q = 0; q < 8; q++) kv[q] = __builtin_bit_cast(float, a[q]);
-        }
-#pragma unroll
-        for (int ii = 0; ii < 8; ii++)
-#pragma unroll
-          for (int r = 0; r < HPW; r++) acc[r] = fmaf(sq[r * hd + i0 + ii], kv[ii], acc[r]);
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < HPW; r++) se[r * per_max + t] = acc[r] * scale;
-  }
-  __syncthreads();
-
-  // @phase attn 3
-  const int wave = tid >> 6, wl = tid & 63;
-  for (int r = wave; r < HPW; r += 4) {
-    float m = -1e30f;
-    for (int t = wl; t < n; t += 64) m = fmaxf(m, se[r * per_max + t]);
-    m = wave_max(m);
-    if (wl == 0) s_mx[r] = m;
-  }
-  __syncthreads();
-  for (int r = 0; r < HPW; r++) {
-    const float m = s_mx[r];
-    for (int t = tid; t < n; t += 256) se[r * per_max + t] = lt_expf(se[r * per_max + t] - m);
-  }
-  __syncthreads();
-  for (int r = wave; r < HPW; r += 4) {
-    float ls = 0.0f;
-    for (int t = wl; t < n; t += 64) ls = ls + se[r * per_max + t];
-    ls = wave_tree_dpp(ls);   // the frozen 64-lane tree, s = 32 .. 1
-    if (wl == 0) s_z[r] = ls;
-  }
-
-  // @phase attn 4
-  // O: thread per (head, dim); each a sequential fma chain over t, V staged in LDS in
-  // chunks of cpos positions (16-byte loads, all issued before the stores; chunk 0 was
-  // issued at the top)
-  const int nout = HPW * hd;
-  float acc0 = 0.0f, acc1 = 0.0f;   // thread handles outputs tid and tid + 256
-  for (int c0 = 0; c0 < n; c0 += cpos) {
-    const int cn = n - c0 < cpos ? n - c0 : cpos;
-    if (c0 > 0) __syncthreads();   // the previous chunk's readers are done with svt
-#pragma unroll
-    for (int k = 0; k < kUpt; k++) {
-      const int u = tid + 256 * k;
-      const int t = u / upr;
-      if (t < cn) {
-        const int c = u - t * upr;
-        float* dst = svt + t * hd + c * kEpu;
-        if (p0 + c0 + t == L) {
-#pragma unroll
-          for (int q = 0; q < kEpu; q++) dst[q] = sv[c * kEpu + q];
-        } else {
-          const uint32_t a[4] = {vraw[k].x, vraw[k].y, vraw[k].z, vraw[k].w};
-          if (kF16) {
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-              dst[2 * q] = lt_h2f((uint16_t)(a[q] & 0xFFFFu));
-              dst[2 * q + 1] = lt_h2f((uint16_t)(a[q] >> 16));
-            }
-          } else {
-#pragma unroll
-            for (int q = 0; q < 4; q++) dst[q] = __builtin_bit_cast(float, a[q]);
-          }
-        }
-      }
-    }
-    // the next chunk's loads fly under this chunk's chains
-    if (c0 + cpos < n) load_vchunk(c0 + cpos, vraw);
-    __syncthreads();
-    if (tid < nout) {
-      const int r = tid / hd, d = tid - r * hd;
-      const float* e = se + r * per_max + c0;
-      for (int t = 0; t < cn; t++) acc0 = fmaf(e[t], svt[t * hd + d], acc0);
-    }
-    if (tid + 256 < nout) {
-      const int o = tid + 256;
-      const int r = o / hd, d = o - r * hd;
-      const float* e = se + r * per_max + c0;
-      for (int t = 0; t < cn; t++) acc1 = fmaf(e[t], svt[t * hd + d], acc1);
-    }
-  }
-  __syncthreads();
-  for (int k = 0; k < 2; k++) {
-    const int o = tid + 256 * k;
-    if (o >= nout) break;
-    const int r = o / hd, d = o - r * hd;
-    const float a = k ? acc1 : acc0;
-    const int h = h0 + r;
-    if (nsplit == 1) {
-      const float v = valid ? a / s_z[r] : 0.0f;
-      if (out) out[(size_t)h * hd + d] = v;
-      svt[o] = v;
-    } else {
-      wso[((size_t)h * nsplit + sp) * hd + d] = a;
-    }
-  }
-  if (nsplit > 1) {
-    if (tid < HPW) {
-      const int h = h0 + tid;
-      wsm[(size_t)h * nsplit + sp] = s_mx[tid];
-      wsz[(size_t)h * nsplit + sp] = s_z[tid];
-    }
-    return;   // k_attn_merge combines the partials
-  }
-  // @phase attn 5
-  if (oq) {
-    // the workgroup's heads are whole 32-element blocks of the attention vector: quantize
-    // them for the O projection (k_quant_q8's quantizer)
-    __syncthreads();
-    const int lane = tid & 31;
-    const size_t o0 = (size_t)h0 * hd;
-    for (int b = tid >> 5; b < nout / 32; b += 8)
-      quant_block_hw(svt[b * 32 + lane], lane, oq + o0 + b * 32, od + (o0 >> 5) + b);
-  }
-  // @phase attn 6
-}
-
-// Split-K merge, one workgroup per query head (the declared combine, ascending split
-// order, bpd/kernelgen/experimental/attn_decode_split.cu:37-91): M = max m_s,
-// w_s = exp(m_s - M), Z = sum fma(w_s, Z_s), O_d = sum fma(w_s, O_s,d), out = O/Z; then
-// the quant of the head's hd/32 blocks.  Every partial is fetched by independent buffer
-// loads issued at the start (one memory round trip); the exps run one per thread.
-constexpr int kMergeQ = 16;   // split outputs prefetched per thread
-
-__global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ wsm, const float* __restrict__ wsz,
-                                                    const float* __restrict__ wso, const int* __restrict__ len,
-                                                    int maxt, float* __restrict__ out, int8_t* __restrict__ oq,
-                                                    uint16_t* __restrict__ od, int hd, int nsplit) {
-  __shared__ float sm[128], sz[128], sw[128], sout[256];
-  __shared__ float s_Z;
-  const int h = blockIdx.x;
-  const int tid = threadIdx.x;
-  const __amdgpu_buffer_rsrc_t orsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(wso + (size_t)h * nsplit * hd), 0, nsplit * hd * 4, 0x00020000);
-  float po[kMergeQ];
-  auto load_po = [&](int q0) {
-#pragma unroll
-    for (int q = 0; q < kMergeQ; q++) {
-      const int off = (tid < hd && q0 + q < nsplit) ? ((q0 + q) * hd + tid) * 4 : (int)kNoBlock;
-      po[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(orsrc, off, 0, 0));
-    }
-  };
-  load_po(0);
-  if (tid < nsplit) {
-    sm[tid] = wsm[(size_t)h * nsplit + tid];
-    sz[tid] = wsz[(size_t)h * nsplit + tid];
-  }
-  const int L = *len;
-  const bool valid = L >= 0 && L < maxt;
-  __syncthreads();
-  float M = -1e30f;
-  for (int q = 0; q < nsplit; q++) M = fmaxf(M, sm[q]);
-  if (tid < nsplit) sw[tid] = lt_expf(sm[tid] - M);
-  __syncthreads();
-  if (tid == 0) {
-    float Z = 0.0f;
-    for (int q = 0; q < nsplit; q++) Z = fmaf(sw[q], sz[q], Z);
-    s_Z = Z;
-  }
-  float a = 0.0f;
-  for (int q0 = 0; q0 < nsplit; q0 += kMergeQ) {
-    if (q0 > 0) load_po(q0);
-#pragma unroll
-    for (int q = 0; q < kMergeQ; q++)
-      if (q0 + q < nsplit) a = fmaf(sw[q0 + q], po[q], a);
-  }
-  __syncthreads();
-  if (tid < hd) {
-    const float v = valid ? a / s_Z : 0.0f;
-    if (out) out[(size_t)h * hd + tid] = v;
-    sout[tid] = v;
-  }
-  if (oq) {
-    __syncthreads();
-    const int lane = tid & 31;
-    const size_t o0 = (size_t)h * hd;
-    for (int b = tid >> 5; b < hd / 32; b += 8)
-      quant_block_hw(sout[b * 32 + lane], lane, oq + o0 + b * 32, od + (o0 >> 5) + b);
-  }
-}
-
 inline int grid_for(long n, int per) { return (int)((n + per - 1) / per); }
 
 // Row mapping.  The gate|up GEMV takes 64 contiguous rows per workgroup (one quant block
@@ -979,8 +614,12 @@ hipError_t launch_gemv_k(GemvParams P, size_t shm, hipStream_t st, int num_cus, 
       P.row0 = 8; P.step = 8; P.max_rows = 1;
       grid = groups;
     } else {
-      grid = cap;
-      P.row0 = 8; P.step = 8 * cap; P.max_rows = 0x7FFFFFFF;
+      // workgroups walking contiguous blocks of rows (their half-waves 8 rows apart), about
+      // half a resident wave of them: every workgroup streams one region of the matrix
+      const int wgs = cap / 2 > 0 ? cap / 2 : 1;
+      const int per = (P.N + wgs - 1) / wgs;
+      P.row0 = (per + 7) & ~7; P.step = 8; P.max_rows = P.row0 / 8;
+      grid = (P.N + P.row0 - 1) / P.row0;
     }
   }
   if (grid_out) *grid_out = grid;
@@ -1004,9 +643,10 @@ hipError_t launch_gemv(const GemvParams& P, lt_ctx* ctx, int* grid_out) {
     return shallow ? launch_gemv_k<1, PRO, EPI, 2>(P, shm, st, ncu, grid_out)
                    : launch_gemv_k<1, PRO, EPI, 8>(P, shm, st, ncu, grid_out);
   } else {
-    if (P.K <= 1024)
+    if (P.K <= 1024) {
       return shallow ? launch_gemv_k<4, PRO, EPI, 2>(P, shm, st, ncu, grid_out)
                      : launch_gemv_k<4, PRO, EPI, 8>(P, shm, st, ncu, grid_out);
+    }
     if (P.K <= 4096) return launch_gemv_k<16, PRO, EPI, 8>(P, shm, st, ncu, grid_out);
     if constexpr (PRO == PRO_EMBED_RMS) return hipErrorInvalidValue;   // K <= 4096 (entry check)
     else return launch_gemv_k<64, PRO, EPI, 4>(P, shm, st, ncu, grid_out);
@@ -1144,70 +784,6 @@ int lt_q8_gemv_rms_argmax(lt_ctx* ctx, const float* x, const float* nw, float ep
   if (int rc = finish(launch_gemv<PRO_RMS, EPI_ARGMAX>(P, ctx, &grid), "k_gemv_fused<rms,argmax>")) return rc;
   k_argmax_finalize<<<1, kFinThreads, 0, ctx->stream>>>(P.pval, P.pidx, grid, out, hist, count, cap);
   return lt_check_launch("k_argmax_finalize");
-}
-
-int lt_attn_step(lt_ctx* ctx, const float* qkv, const float* freqs, void* kc, void* vc, const int* len,
-                 float* out, int8_t* xq, uint16_t* xd, int nh, int nkv, int hd, float scale, int maxt, int nsplit,
-                 int kv_dtype, void* ws, size_t ws_bytes) {
-  LT_REQUIRE(ctx && qkv && freqs && kc && vc && len, "lt_attn_step: null argument");
-  LT_REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0, "lt_attn_step: nh=%d nkv=%d", nh, nkv);
-  LT_REQUIRE(hd > 0 && hd % 8 == 0 && hd <= 256, "lt_attn_step: hd=%d (multiple of 8, <= 256)", hd);
-  LT_REQUIRE(maxt > 0 && nsplit >= 1 && nsplit <= maxt, "lt_attn_step: maxt=%d nsplit=%d", maxt, nsplit);
-  LT_REQUIRE(kv_dtype == LT_KV_F32 || kv_dtype == LT_KV_F16, "lt_attn_step: kv_dtype=%d", kv_dtype);
-  LT_REQUIRE(lt_aligned(kc, 16) && lt_aligned(vc, 16), "lt_attn_step: K/V caches must be 16-byte aligned");
-  // Short caches are latency-bound: one head per workgroup keeps each thread's sequential
-  // chains short.  Large caches are bandwidth-bound: the heads of a KV group share one
-  // workgroup so every K/V row is read once.
-  const int rep = nh / nkv;
-  const size_t cache_bytes = (size_t)maxt * nkv * hd * (kv_dtype == LT_KV_F16 ? 2 : 4);
-  int hpw = 1;
-  if (cache_bytes > ((size_t)4 << 20))
-    for (int c : {8, 7, 4, 2})
-      if (rep % c == 0 && c * hd <= 512) { hpw = c; break; }
-  const int per_max = (maxt + nsplit - 1) / nsplit;
-  const size_t shm = ((size_t)hpw * hd + 2 * hd + (size_t)hpw * per_max + kVChunkFloats) * sizeof(float);
-  if (shm > 64 * 1024)
-    return lt_fail(LT_EINVAL, "lt_attn_step: %zu bytes of LDS for maxt=%d nsplit=%d; raise nsplit", shm, maxt, nsplit);
-  float *wsm = nullptr, *wsz = nullptr, *wso = nullptr;
-  LT_REQUIRE(out || xq, "lt_attn_step: needs out or xq/xd");
-  LT_REQUIRE(!xq || (xd && hd % 32 == 0), "lt_attn_step: quantized output needs xd and hd %% 32 == 0");
-  if (nsplit > 1) {
-    LT_REQUIRE(nsplit <= 128, "lt_attn_step: nsplit=%d (at most 128)", nsplit);
-    const size_t need = lt_attn_workspace_size(1, nh, hd, nsplit);
-    LT_REQUIRE(ws && lt_aligned(ws, 16), "lt_attn_step: nsplit=%d needs a 16-byte aligned workspace", nsplit);
-    if (ws_bytes < need) return lt_fail(LT_ENOMEM, "lt_attn_step: workspace %zu < %zu bytes", ws_bytes, need);
-    const AttnWs w = lt_attn_ws_layout(ws, nh, hd, nsplit);
-    wsm = w.m;
-    wsz = w.z;
-    wso = w.o;
-  }
-  dim3 grid(nsplit, nh / hpw);
-  const bool f16 = kv_dtype == LT_KV_F16;
-#define LT_STEP_CASE(H)                                                                                   \
-  case H:                                                                                                 \
-    if (f16) k_attn_step<true, H><<<grid, 256, shm, ctx->stream>>>(qkv, freqs, kc, vc, len, out, xq, xd,   \
-                                                                  wsm, wsz, wso, nh, nkv, hd, scale, maxt, \
-                                                                  nsplit, per_max);                        \
-    else k_attn_step<false, H><<<grid, 256, shm, ctx->stream>>>(qkv, freqs, kc, vc, len, out, xq, xd,     \
-                                                               wsm, wsz, wso, nh, nkv, hd, scale, maxt,    \
-                                                               nsplit, per_max);                           \
-    break;
-  switch (hpw) {
-    LT_STEP_CASE(1)
-    LT_STEP_CASE(2)
-    LT_STEP_CASE(4)
-    LT_STEP_CASE(7)
-    LT_STEP_CASE(8)
-    default:
-      return lt_fail(LT_EINVAL, "lt_attn_step: unsupported heads per workgroup %d", hpw);
-  }
-#undef LT_STEP_CASE
-  if (nsplit > 1) {
-    LT_CHECK(hipGetLastError());
-    k_attn_merge<<<nh, 256, 0, ctx->stream>>>(wsm, wsz, wso, len, maxt, out, xq, xd, hd, nsplit);
-    return lt_check_launch("k_attn_merge");
-  }
-  return lt_check_launch("k_attn_step");
 }
 
 }  // extern "C"
