@@ -54,7 +54,10 @@ struct AttnArgs {
   int nh, nkv, hd;
   float scale;
   int maxt, nsplit, per_max;
+  int inwg;             // 1: this workgroup computes all nsplit splits of its row and merges them
 };
+
+constexpr int kMaxInWgSplits = 16;   // splits one workgroup can hold (partial outputs in registers)
 
 template <bool kF16>
 __device__ __forceinline__ float kv_round(float v) {
@@ -72,8 +75,9 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
   float* sv = sk + hd;                  // [hd] STEP: new v (cache-rounded)
   float* se = sv + hd;                  // [HPW][per_max] scores, then exps
   float* svt = se + HPW * per_max;      // [kVChunkFloats] staged V (then the output)
-  __shared__ float s_mx[HPW];
-  __shared__ float s_z[HPW];
+  __shared__ float s_ms[HPW * kMaxInWgSplits];   // per (head, split): max, then exp weight
+  __shared__ float s_zs[HPW * kMaxInWgSplits];   // per (head, split): Z
+  __shared__ float s_z[HPW];                     // per head: the final Z
 
   const int tid = threadIdx.x;
   const int sp = blockIdx.x;
@@ -126,7 +130,9 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
     const int L = MODE == AM_PREFILL ? A.len[0] + b + 1 : A.len[b];
     nctx = L < 0 ? 0 : (L > A.maxt ? A.maxt : L);
   }
-  const int per = (nctx + nsplit - 1) / nsplit;
+  const bool inwg = MODE == AM_PREFILL && A.inwg != 0;
+  const int nsub = inwg ? nsplit : 1;            // splits inside this workgroup's range
+  const int per = inwg ? nctx : (nctx + nsplit - 1) / nsplit;
   const int p0 = sp * per;
   int p1 = p0 + per;
   if (p1 > nctx) p1 = nctx;
@@ -284,24 +290,29 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
   __syncthreads();
 
   // @phase attn 3
+  // softmax of each split (the whole range, or nsub splits of length spl inside it)
   const int wave = tid >> 6, wl = tid & 63;
-  for (int r = wave; r < HPW; r += 4) {
+  const int spl = nsub > 1 ? ((n + nsub - 1) / nsub > 0 ? (n + nsub - 1) / nsub : 1) : (n > 0 ? n : 1);
+  for (int q = wave; q < HPW * nsub; q += 4) {
+    const int r = q / nsub, sub = q - r * nsub;
+    const int t0 = sub * spl, t1 = t0 + spl < n ? t0 + spl : n;
     float m = -1e30f;
-    for (int t = wl; t < n; t += 64) m = fmaxf(m, se[r * per_max + t]);
+    for (int t = t0 + wl; t < t1; t += 64) m = fmaxf(m, se[r * per_max + t]);
     m = wave_max(m);
-    if (wl == 0) s_mx[r] = m;
+    if (wl == 0) s_ms[q] = m;
   }
   __syncthreads();
-  for (int r = 0; r < HPW; r++) {
-    const float m = s_mx[r];
-    for (int t = tid; t < n; t += 256) se[r * per_max + t] = lt_expf(se[r * per_max + t] - m);
-  }
+  for (int r = 0; r < HPW; r++)
+    for (int t = tid; t < n; t += 256)
+      se[r * per_max + t] = lt_expf(se[r * per_max + t] - s_ms[r * nsub + t / spl]);
   __syncthreads();
-  for (int r = wave; r < HPW; r += 4) {
+  for (int q = wave; q < HPW * nsub; q += 4) {
+    const int r = q / nsub, sub = q - r * nsub;
+    const int t0 = sub * spl, t1 = t0 + spl < n ? t0 + spl : n;
     float ls = 0.0f;
-    for (int t = wl; t < n; t += 64) ls = ls + se[r * per_max + t];
+    for (int t = t0 + wl; t < t1; t += 64) ls = ls + se[r * per_max + t];
     ls = wave_tree_dpp(ls);   // the frozen 64-lane tree, s = 32 .. 1
-    if (wl == 0) s_z[r] = ls;
+    if (wl == 0) s_zs[q] = ls;
   }
 
   // @phase attn 4
@@ -309,6 +320,9 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
   // chunks of cpos positions, the next chunk's loads in flight under this chunk's chains
   const int nout = HPW * hd;
   float acc0 = 0.0f, acc1 = 0.0f;   // thread handles outputs tid and tid + 256
+  float po0[kMaxInWgSplits], po1[kMaxInWgSplits];   // in-workgroup splits' outputs
+#pragma unroll
+  for (int i = 0; i < kMaxInWgSplits; i++) { po0[i] = 0.0f; po1[i] = 0.0f; }
   for (int c0 = 0; c0 < n; c0 += cpos) {
     const int cn = n - c0 < cpos ? n - c0 : cpos;
     if (c0 > 0) __syncthreads();   // the previous chunk's readers are done with svt
@@ -339,17 +353,70 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
     }
     if (c0 + cpos < n) load_vchunk(c0 + cpos, vraw);
     __syncthreads();
-    if (tid < nout) {
-      const int r = tid / hd, d = tid - r * hd;
-      const float* e = se + r * per_max + c0;
-      for (int t = 0; t < cn; t++) acc0 = fmaf(e[t], svt[t * hd + d], acc0);
+    // ascending t; where an inner split ends the chain is saved as that split's O and
+    // restarts from 0
+    for (int t = 0; t < cn;) {
+      int tend = cn;
+      if (nsub > 1) {
+        const int nextb = ((c0 + t) / spl + 1) * spl;   // the next split boundary
+        if (nextb - c0 < cn) tend = nextb - c0;
+      }
+      if (tid < nout) {
+        const int r = tid / hd, d = tid - r * hd;
+        const float* e = se + r * per_max + c0;
+        for (int u = t; u < tend; u++) acc0 = fmaf(e[u], svt[u * hd + d], acc0);
+      }
+      if (tid + 256 < nout) {
+        const int o = tid + 256;
+        const int r = o / hd, d = o - r * hd;
+        const float* e = se + r * per_max + c0;
+        for (int u = t; u < tend; u++) acc1 = fmaf(e[u], svt[u * hd + d], acc1);
+      }
+      t = tend;
+      const int g1 = c0 + t;   // positions folded so far
+      if (nsub > 1 && g1 % spl == 0 && g1 < n) {   // an inner boundary: split g1/spl - 1 ends
+        const int ended = g1 / spl - 1;
+#pragma unroll
+        for (int i = 0; i < kMaxInWgSplits; i++)
+          if (i == ended) { po0[i] = acc0; po1[i] = acc1; }
+        acc0 = 0.0f;
+        acc1 = 0.0f;
+      }
     }
-    if (tid + 256 < nout) {
-      const int o = tid + 256;
-      const int r = o / hd, d = o - r * hd;
-      const float* e = se + r * per_max + c0;
-      for (int t = 0; t < cn; t++) acc1 = fmaf(e[t], svt[t * hd + d], acc1);
+  }
+  if (nsub > 1) {
+    // the last nonempty split ends at n; then merge the splits in ascending order (the
+    // declared combine, attn_decode_split.cu:37-91)
+    const int last = n > 0 ? (n - 1) / spl : 0;
+#pragma unroll
+    for (int i = 0; i < kMaxInWgSplits; i++)
+      if (i == last && n > 0) { po0[i] = acc0; po1[i] = acc1; }
+    __syncthreads();   // s_ms / s_zs complete
+    if (tid < HPW) {
+      float M = -1e30f;
+      for (int q = 0; q < nsub; q++) M = fmaxf(M, s_ms[tid * nsub + q]);
+      float Z = 0.0f;
+      for (int q = 0; q < nsub; q++) {
+        const float w = lt_expf(s_ms[tid * nsub + q] - M);
+        s_ms[tid * nsub + q] = w;
+        Z = fmaf(w, s_zs[tid * nsub + q], Z);
+      }
+      s_z[tid] = Z;
     }
+    __syncthreads();
+    acc0 = 0.0f;
+    acc1 = 0.0f;
+    const int r0 = (tid < nout ? tid : 0) / hd;
+    const int r1 = (tid + 256 < nout ? tid + 256 : 0) / hd;
+#pragma unroll
+    for (int i = 0; i < kMaxInWgSplits; i++) {
+      if (i < nsub) {
+        acc0 = fmaf(s_ms[r0 * nsub + i], po0[i], acc0);
+        acc1 = fmaf(s_ms[r1 * nsub + i], po1[i], acc1);
+      }
+    }
+  } else if (tid < HPW) {
+    s_z[tid] = s_zs[tid];
   }
   __syncthreads();
   const size_t hrow0 = (size_t)b * A.nh + h0;   // output / partial row of head h0
@@ -358,7 +425,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
     if (o >= nout) break;
     const int r = o / hd, d = o - r * hd;
     const float a = k ? acc1 : acc0;
-    if (nsplit == 1) {
+    if (nsplit == 1 || inwg) {
       const float v = valid ? a / s_z[r] : 0.0f;
       if (A.out) A.out[hrow0 * hd + o] = v;
       svt[o] = v;
@@ -366,9 +433,9 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
       A.wso[((hrow0 + r) * nsplit + sp) * hd + d] = a;
     }
   }
-  if (nsplit > 1) {
+  if (nsplit > 1 && !inwg) {
     if (tid < HPW) {
-      A.wsm[(hrow0 + tid) * nsplit + sp] = s_mx[tid];
+      A.wsm[(hrow0 + tid) * nsplit + sp] = s_ms[tid];
       A.wsz[(hrow0 + tid) * nsplit + sp] = s_z[tid];
     }
     return;   // k_attn_merge combines the partials
@@ -477,8 +544,10 @@ hipError_t launch_attn_k(int hpw, dim3 grid, size_t shm, hipStream_t st, const A
 // heads per workgroup.
 int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, void* ws, size_t ws_bytes,
                 const char* what) {
-  if (A.nsplit > 1) {
-    LT_REQUIRE(A.nsplit <= 128, "%s: nsplit=%d (at most 128)", what, A.nsplit);
+  LT_REQUIRE(A.nsplit <= 128, "%s: nsplit=%d (at most 128)", what, A.nsplit);
+  if (A.nsplit > 1 && !(mode == AM_PREFILL && A.nsplit <= kMaxInWgSplits &&
+                        ((size_t)hpw * A.hd + 2 * A.hd + (size_t)hpw * A.maxt + kVChunkFloats) * sizeof(float) <=
+                            64 * 1024)) {
     const size_t need = lt_attn_ws_bytes(rows * A.nh, A.hd, A.nsplit);
     LT_REQUIRE(ws && lt_aligned(ws, 16), "%s: nsplit=%d needs a 16-byte aligned workspace", what, A.nsplit);
     if (ws_bytes < need) return lt_fail(LT_ENOMEM, "%s: workspace %zu < %zu bytes", what, ws_bytes, need);
@@ -487,12 +556,17 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
     A.wsz = w.z;
     A.wso = w.o;
   }
-  A.per_max = (A.maxt + A.nsplit - 1) / A.nsplit;
-  const size_t shm = ((size_t)hpw * A.hd + 2 * A.hd + (size_t)hpw * A.per_max + kVChunkFloats) * sizeof(float);
+  auto shm_for = [&](int per_max) {
+    return ((size_t)hpw * A.hd + 2 * A.hd + (size_t)hpw * per_max + kVChunkFloats) * sizeof(float);
+  };
+  // prefill: every query row's splits inside one workgroup when they fit (no merge launch)
+  A.inwg = mode == AM_PREFILL && A.nsplit > 1 && A.nsplit <= kMaxInWgSplits && shm_for(A.maxt) <= 64 * 1024;
+  A.per_max = A.inwg ? A.maxt : (A.maxt + A.nsplit - 1) / A.nsplit;
+  const size_t shm = shm_for(A.per_max);
   if (shm > 64 * 1024)
     return lt_fail(LT_EINVAL, "%s: %zu bytes of LDS for maxt=%d nsplit=%d; raise nsplit", what, shm, A.maxt,
                    A.nsplit);
-  const dim3 grid(A.nsplit, A.nh / hpw, rows);
+  const dim3 grid(A.inwg ? 1 : A.nsplit, A.nh / hpw, rows);
   hipError_t e;
   if (mode == AM_STEP)
     e = f16 ? launch_attn_k<true, AM_STEP>(hpw, grid, shm, ctx->stream, A)
@@ -504,7 +578,7 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
     e = f16 ? launch_attn_k<true, AM_PREFILL>(hpw, grid, shm, ctx->stream, A)
             : launch_attn_k<false, AM_PREFILL>(hpw, grid, shm, ctx->stream, A);
   if (e != hipSuccess) return lt_fail_hip(e, what, __FILE__, __LINE__);
-  if (A.nsplit > 1) {
+  if (A.nsplit > 1 && !A.inwg) {
     k_attn_merge<<<dim3(A.nh, rows), 256, 0, ctx->stream>>>(A.wsm, A.wsz, A.wso, mode == AM_STEP ? A.len : nullptr,
                                                             A.maxt, A.out, A.oq, A.od, A.nh, A.hd, A.nsplit);
     return lt_check_launch("k_attn_merge");

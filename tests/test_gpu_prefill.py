@@ -81,7 +81,8 @@ def weights(cfg):
 
 @pytest.mark.parametrize("cfg_name,n_prompt,kv_dtype,nsplit", [
     ("tiny", 9, LT_KV_F32, 1), ("tiny", 40, LT_KV_F16, 2), ("small-qwen-arch", 32, LT_KV_F16, 1),
-    ("small-qwen-arch", 33, LT_KV_F32, 4)])
+    ("small-qwen-arch", 33, LT_KV_F32, 4), ("small-qwen-arch", 70, LT_KV_F16, 16),
+    ("tiny", 40, LT_KV_F32, 32)])
 def test_prefill_equals_stepwise(gpu, oracle, cfg_name, n_prompt, kv_dtype, nsplit):
     cfg = M.CONFIGS[cfg_name]
     case(f"prefill vs stepwise {cfg_name} T={n_prompt} kv={kv_dtype} nsplit={nsplit}")
