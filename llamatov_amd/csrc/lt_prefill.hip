@@ -19,10 +19,12 @@ using namespace lt;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int kGemmWaves = 4;                  // waves per workgroup: 4 x 32 tokens share 32 rows
 constexpr int kGemmTokens = 32 * kGemmWaves;   // tokens per workgroup
 constexpr int kDepth = 4;                      // blocks in flight per wave
+constexpr uint32_t kNoBlk = 0x80000000u;       // out-of-range buffer offset: reads zeros
 
 enum GemmEpi { GE_STORE = 0, GE_BIAS = 1, GE_RESID = 2, GE_SILU = 3 };
 
@@ -44,7 +46,7 @@ __device__ __forceinline__ int c_row(int r, int h) { return 8 * (r >> 2) + 4 * h
 
 template <GemmEpi EPI>
 __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
-  __shared__ __attribute__((aligned(16))) float s_wd[kGemmWaves][32];
+  __shared__ float s_st4[kGemmWaves][16 * 64];   // tree level 4 of each wave's 32 x 32 tile
   const int wave = threadIdx.x >> 6;
   const int l = threadIdx.x & 63;
   const int h = l >> 5;
@@ -69,51 +71,52 @@ __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)P.W, 0, (int)((mat_bytes + 3u) & ~3u), 0x00020000);
   // B lane: token t0 + c (clamped)
   const int btok = t0 + c < P.T ? t0 + c : P.T - 1;
-  const int8_t* xrow = P.Xq + (size_t)btok * P.K + 16 * h;
-  const uint16_t* xdrow = P.Xd + (size_t)btok * nb;
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)P.Xq, 0, (int)((size_t)P.T * P.K), 0x00020000);
+  const __amdgpu_buffer_rsrc_t xdr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)P.Xd, 0, (int)(((size_t)P.T * nb * 2 + 3) & ~(size_t)3), 0x00020000);
+  const uint32_t xrow_off = (uint32_t)btok * (uint32_t)P.K + 16u * (uint32_t)h;
+  const uint32_t xd_off = (uint32_t)btok * (uint32_t)nb * 2u;
 
-  // Operands of one block, prefetched: the A lane's 16 quant bytes (realigned), its row's
-  // scale, and the B lane's 16 quant bytes and scale.
+  // Operands of one block, raw as loaded (so the loads stay in flight until the block is
+  // folded): the A lane's 5 dwords around its 16 quant bytes, the dword holding its row's
+  // scale, the B lane's 16 quant bytes and the dword holding its token's scale.  Every load
+  // is unconditional: past the last block the offsets are out of range and read zeros.
   struct Ops {
-    v4i a, bq;
-    float wd, xd;
+    v4i w03, bq;
+    uint32_t w4, wdw, xdw;
   };
-  auto load_ops = [&](int b, Ops& o) {
+  auto load_ops = [&](int b, bool real, Ops& o) {
     const uint32_t off = row_off + (uint32_t)b * (uint32_t)kBlockBytes;
-    const uint32_t start = off + 2u + 16u * (uint32_t)h;
-    const uint32_t base = start & ~3u;
-    const uint32_t sh = start & 3u;   // 0 or 2
-    const v4i w03 = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)base, 0, 0));
-    const uint32_t w4 = __builtin_amdgcn_raw_buffer_load_b32(wr, (int)(base + 16u), 0, 0);
-    o.a.x = (int)__builtin_amdgcn_alignbyte((uint32_t)w03.y, (uint32_t)w03.x, sh);
-    o.a.y = (int)__builtin_amdgcn_alignbyte((uint32_t)w03.z, (uint32_t)w03.y, sh);
-    o.a.z = (int)__builtin_amdgcn_alignbyte((uint32_t)w03.w, (uint32_t)w03.z, sh);
-    o.a.w = (int)__builtin_amdgcn_alignbyte(w4, (uint32_t)w03.w, sh);
-    __builtin_memcpy(&o.bq, xrow + 32 * b, 16);
-    o.xd = lt_h2f(xdrow[b]);
-    o.wd = lt_h2f(*(const uint16_t*)(P.W + off));
+    const uint32_t base = real ? (off + 2u + 16u * (uint32_t)h) & ~3u : kNoBlk;
+    o.w03 = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)base, 0, 0));
+    o.w4 = __builtin_amdgcn_raw_buffer_load_b32(wr, (int)(base + 16u), 0, 0);
+    o.wdw = __builtin_amdgcn_raw_buffer_load_b32(wr, real ? (int)(off & ~3u) : (int)kNoBlk, 0, 0);
+    o.bq = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                       xr, real ? (int)(xrow_off + 32u * (uint32_t)b) : (int)kNoBlk, 0, 0));
+    o.xdw = __builtin_amdgcn_raw_buffer_load_b32(xdr, real ? (int)((xd_off + 2u * (uint32_t)b) & ~3u) : (int)kNoBlk,
+                                                 0, 0);
   };
-  // fold one block into the leaf's 16 running sums: exact MFMA dots, then
-  // v = fma(wd*xd, isum, v) per element (the row scales reach the C rows through LDS)
-  auto fold_ops = [&](const Ops& o, float (&v)[16]) {
+  // fold block b into the leaf's 16 running sums: exact MFMA dots isum, the exact scale
+  // products wd*xd as an fp32 MFMA outer product (A lane: its row's wd in k = 0, zero in
+  // k = 1; B lane: its token's xd in k = 0, zero in k = 1; a product of two fp16 values is
+  // exact in fp32 and the zero terms add nothing), then v = fma(wd*xd, isum, v) per element
+  auto fold_ops = [&](const Ops& o, int b, float (&v)[16]) {
+    const uint32_t off = row_off + (uint32_t)b * (uint32_t)kBlockBytes;
+    const uint32_t sh = (off + 2u + 16u * (uint32_t)h) & 3u;   // 0 or 2
+    v4i a;
+    a.x = (int)__builtin_amdgcn_alignbyte((uint32_t)o.w03.y, (uint32_t)o.w03.x, sh);
+    a.y = (int)__builtin_amdgcn_alignbyte((uint32_t)o.w03.z, (uint32_t)o.w03.y, sh);
+    a.z = (int)__builtin_amdgcn_alignbyte((uint32_t)o.w03.w, (uint32_t)o.w03.z, sh);
+    a.w = (int)__builtin_amdgcn_alignbyte(o.w4, (uint32_t)o.w03.w, sh);
+    const float wd = lt_h2f((uint16_t)((off & 2u) ? (o.wdw >> 16) : (o.wdw & 0xFFFFu)));
+    const float xd = lt_h2f((uint16_t)(((xd_off + 2u * (uint32_t)b) & 2u) ? (o.xdw >> 16) : (o.xdw & 0xFFFFu)));
     const v16i z = {};
-    const v16i isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, o.bq, z, 0, 0, 0);
-    if (h == 0) s_wd[wave][c] = o.wd;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    float wd[16];
+    const v16i isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, o.bq, z, 0, 0, 0);
+    const v16f zf = {};
+    const v16f sc = __builtin_amdgcn_mfma_f32_32x32x2f32(h == 0 ? wd : 0.0f, h == 0 ? xd : 0.0f, zf, 0, 0, 0);
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-      float4 v4;
-      __builtin_memcpy(&v4, &s_wd[wave][8 * q + 4 * h], 16);
-      wd[4 * q + 0] = v4.x; wd[4 * q + 1] = v4.y; wd[4 * q + 2] = v4.z; wd[4 * q + 3] = v4.w;
-    }
-    // the scales are read before the next block's writes (LDS keeps a wave's order)
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int r = 0; r < 16; r++) v[r] = fmaf(wd[r] * o.xd, (float)isum[r], v[r]);
+    for (int r = 0; r < 16; r++) v[r] = fmaf(sc[r], (float)isum[r], v[r]);
   };
 
   // The blocks in post-order: leaf i (0..31) is lane L = bitrev5(i) and holds blocks
@@ -122,8 +125,8 @@ __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
   auto leaf_lane = [](int i) { return (int)(__builtin_bitreverse32((uint32_t)i) >> 27); };
   int pi = 0, pb = 0;   // producer: leaf, next block (pb = -1: done)
   auto produce = [&](Ops& o) {
+    load_ops(pb >= 0 ? pb : 0, pb >= 0, o);
     if (pb >= 0) {
-      load_ops(pb, o);
       pb += 32;
       while (pb >= nb) {           // next non-empty leaf
         if (++pi == 32) { pb = -1; break; }
@@ -135,47 +138,67 @@ __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
 #pragma unroll
   for (int d = 0; d < kDepth; d++) produce(ring[d]);
 
-  float st[5][16];   // pending partial sums of the tree, one per level
-  float v[16], res[16];
+  float st[4][16];   // pending partial sums of the tree, levels 0..3 (level 4: s_st4)
+  float v[16];
 #pragma unroll
   for (int r = 0; r < 16; r++) {
     v[r] = 0.0f;
-    res[r] = 0.0f;
   }
 #pragma unroll
-  for (int l2 = 0; l2 < 5; l2++)
+  for (int l2 = 0; l2 < 4; l2++)
 #pragma unroll
     for (int r = 0; r < 16; r++) st[l2][r] = 0.0f;
-  // combine leaf i into the stack: it closes every level whose bit is set in i (i is
-  // uniform and the register indices are static, so the stack stays in registers)
+  // combine leaf i into the stack: it closes every level whose bit is set in i (its
+  // trailing ones: left subtree st[lvl] + right subtree v, the reference tree's pairing)
+  // and parks the sum at the first clear level.  i is uniform, so these are scalar
+  // branches around static register indices.
   auto close_leaf = [&](int i) {
-    // branch-free selects on static levels: leaf i adds into levels 0.. while their bit
-    // is set and parks its sum at the first clear one
-    bool carry = true;
+    const int t1 = __builtin_ctz(~(unsigned)i);   // trailing ones, 0..5
 #pragma unroll
-    for (int lvl = 0; lvl < 5; lvl++) {
-      const bool bit = ((i >> lvl) & 1) != 0;
-      const bool comb = carry && bit;
-      const bool park = carry && !bit;
+    for (int lvl = 0; lvl < 4; lvl++) {
+      if (lvl < t1) {
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const float sum = st[lvl][r] + v[r];
-        st[lvl][r] = park ? v[r] : st[lvl][r];
-        v[r] = comb ? sum : v[r];
+        for (int r = 0; r < 16; r++) v[r] = st[lvl][r] + v[r];
       }
-      carry = comb;
     }
-    const bool last = i == 31;     // the last leaf closes every level: v is the row value
+    if (t1 == 5) {   // level 4 (parked by leaf 15) lives in LDS
 #pragma unroll
-    for (int r = 0; r < 16; r++) res[r] = last ? v[r] : res[r];
+      for (int r = 0; r < 16; r++) v[r] = s_st4[wave][r * 64 + l] + v[r];
+    }
+    switch (t1) {
+      case 0:
+#pragma unroll
+        for (int r = 0; r < 16; r++) st[0][r] = v[r];
+        break;
+      case 1:
+#pragma unroll
+        for (int r = 0; r < 16; r++) st[1][r] = v[r];
+        break;
+      case 2:
+#pragma unroll
+        for (int r = 0; r < 16; r++) st[2][r] = v[r];
+        break;
+      case 3:
+#pragma unroll
+        for (int r = 0; r < 16; r++) st[3][r] = v[r];
+        break;
+      case 4:
+#pragma unroll
+        for (int r = 0; r < 16; r++) s_st4[wave][r * 64 + l] = v[r];
+        break;
+      default:   // i == 31: every level closed, v is the row value (kept in v)
+        break;
+    }
   };
   int ci = 0, cb = 0;   // consumer: leaf, block
   for (int s0 = 0; s0 < nb; s0 += kDepth) {
 #pragma unroll
     for (int d = 0; d < kDepth; d++) {
+      // every slot folds and refills (loads on all paths keep the load counters exact):
+      // past the last block a slot holds zeros, and v + 0*0 leaves v unchanged
+      fold_ops(ring[d], cb, v);
+      produce(ring[d]);
       if (s0 + d < nb) {
-        fold_ops(ring[d], v);
-        produce(ring[d]);
         cb += 32;
         if (cb >= nb) {            // leaf ci is complete; close it and any empty leaves after it
           close_leaf(ci);
@@ -184,8 +207,10 @@ __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
             for (int r = 0; r < 16; r++) v[r] = 0.0f;
             close_leaf(ci);
           }
+          if (ci < 32) {           // after leaf 31, v holds the row values
 #pragma unroll
-          for (int r = 0; r < 16; r++) v[r] = 0.0f;
+            for (int r = 0; r < 16; r++) v[r] = 0.0f;
+          }
         }
       }
     }
@@ -199,14 +224,14 @@ __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
 #pragma unroll
     for (int r = 0; r < 16; r += 2) {
       const int n = n0 + c_row(r, h);
-      if (n < P.N) P.Y[(size_t)t * F + (n >> 1)] = lt_silu_mul(res[r], res[r + 1]);
+      if (n < P.N) P.Y[(size_t)t * F + (n >> 1)] = lt_silu_mul(v[r], v[r + 1]);
     }
   } else {
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const int n = n0 + c_row(r, h);
       if (n < P.N) {
-        float o = res[r];
+        float o = v[r];
         if constexpr (EPI == GE_BIAS) o = o + P.bias[n];
         if constexpr (EPI == GE_RESID) o = o + P.resid[(size_t)t * P.N + n];
         P.Y[(size_t)t * P.N + n] = o;
