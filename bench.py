@@ -89,9 +89,15 @@ def gemv_roofline(dev, w_embd: np.ndarray, N: int, K: int, eps: float, launches:
     avg_s = ms / 1e3 / launches
     alg_bytes = N * (K // 32) * 34 + 8 * K + 4 * N
     achieved = alg_bytes / avg_s / 1e9
-    return {"kernel": "k_gemv_fused<4, PRO_RMS, EPI_STORE, 4> (lt_q8_gemv_rms, vocab projection)",
+    traffic = None   # HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE counter runs
+    tf = ROOT / "profiles" / "gemv_vocab_c2_traffic.txt"
+    if tf.exists():
+        import re
+        m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", tf.read_text(), flags=re.M)
+        traffic = int(m.group(1)) if m else None
+    return {"kernel": "k_gemv_fused<4, PRO_RMS, EPI_STORE, 8> (lt_q8_gemv_rms, vocab projection)",
             "shape": [N, K], "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "bytes_per_launch": alg_bytes, "avg_launch_us": round(avg_s * 1e6, 3),
             "weight_copies": copies}
 
@@ -278,6 +284,9 @@ def main() -> int:
     ap.add_argument("--per-op", action="store_true",
                     help="thirteen per-op launches per layer (the reference's kernel-per-op chain) "
                          "instead of the five fused launches")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the GEMV roofline leg, plus a device copy of one weight matrix (the known-size "
+                         "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE); for counter runs")
     ap.add_argument("--eager", action="store_true",
                     help="launch the step's kernels directly instead of replaying the captured graph "
                          "(same kernels; for profilers that cannot trace graph launches)")
@@ -293,6 +302,17 @@ def main() -> int:
     from llamatov_amd._lib import LT_KV_F16, LT_KV_F32
 
     cfg = M.QWEN25_05B
+    if args.roofline_only:
+        w = M.synth_weights(cfg, seed=1234)
+        dev = dr.get_device()
+        emb = w["token_embd.weight"]
+        rf = gemv_roofline(dev, emb, cfg.vocab, cfg.n_embd, cfg.norm_eps, launches=20)
+        src = dr.DevTensor.from_host(emb, dev)
+        dst = dr.DevTensor.empty(src.shape, src.dtype, dev)
+        dev.d2d(dst.ptr, src.ptr, src.nbytes)   # calibration: a plain copy of known size
+        dev.sync()
+        print(json.dumps({"roofline": rf, "calibration_copy_bytes": int(src.nbytes)}), flush=True)
+        return 0
     if args.prompt + args.steps > cfg.max_ctx or args.prompt + args.warmup > cfg.max_ctx:
         print("bench.py: prompt + steps exceeds the 1024-position KV cache", file=sys.stderr)
         return 2
