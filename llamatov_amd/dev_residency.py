@@ -420,10 +420,28 @@ class ResidentModel:
         for kind, owner, key, slot, N, K in staged:
             owner[key] = Q8Weight(None, K, t=slot[0], N=N) if kind == "q8" else slot[0]
         self.arena = arena
+        self.load_report = None
         self.tok_embd = top["tok_embd"]
         self.output = top.get("output", self.tok_embd)
         self.output_norm = top["output_norm"]
         self.freqs = top["freqs"]
+
+    @classmethod
+    def from_gguf(cls, path, dev: Device | None = None, layouts: str = "both",
+                  max_ctx: int = 1024) -> "ResidentModel":
+        """Upload a Q8_0 GGUF file (the reference's load_model + first-use residency,
+        decode_fact.py:39-51, fact_dispatch.py:255-299): Q8_0 blocks go from the mapped file
+        to the device without a float32 copy.  `load_report` says how many tensors were used
+        verbatim, canonicalized or quantized from another type."""
+        from . import gguf
+        cfg, w, reader, report = gguf.load_q8_model(path, max_ctx=max_ctx)
+        try:
+            m = cls(cfg, w, dev, layouts)
+        finally:
+            del w
+            reader.close()
+        m.load_report = report
+        return m
 
     def free(self) -> None:
         self.arena.free()
@@ -781,3 +799,40 @@ class GraphRunner:
         if self.captured:
             call("lt_graph_free", self.graph)
             self.captured = False
+
+
+def generate(model, input_ids, n_tokens: int, profile: Profile = PRODUCTION_PROFILE,
+             batched_prefill: bool = True, max_ctx: int | None = None) -> list[int]:
+    """Greedy generation of n_tokens after input_ids, the reference's decode loop
+    (decode_fact.py:54-111 semantics; GraphRunner seed -> capture -> replay,
+    dev_residency.py:1626-1818): the prompt is prefilled, the first token is its greedy
+    argmax, and every further token comes from one replay of the captured step.
+
+    `model` is a ResidentModel or the path of a Q8_0 GGUF file (loaded and freed here)."""
+    own = not isinstance(model, ResidentModel)
+    m = ResidentModel.from_gguf(model, max_ctx=max_ctx or 1024) if own else model
+    plan = gr = None
+    try:
+        ids = [int(t) for t in np.asarray(input_ids).reshape(-1)]
+        if not ids:
+            raise ValueError("generate: empty prompt")
+        if n_tokens < 1:
+            return []
+        plan = DecodePlan(m, profile, max_ctx=max_ctx, hist_cap=max(4096, n_tokens))
+        if len(ids) + n_tokens - 1 > plan.max_ctx:
+            raise ValueError(f"generate: {len(ids)} prompt + {n_tokens - 1} decode positions exceed "
+                             f"the {plan.max_ctx}-position KV cache")
+        gr = GraphRunner(plan)
+        gr.seed(ids, batched=batched_prefill and "wgu_il" in m.layers[0])
+        out = [plan.read_token()]
+        if n_tokens > 1:
+            gr.capture()
+            out += gr.replay_tokens(n_tokens - 1)
+        return out
+    finally:
+        if gr is not None:
+            gr.free()
+        if plan is not None:
+            plan.free()
+        if own:
+            m.free()

@@ -1,0 +1,86 @@
+"""A model loaded from a GGUF file decodes exactly as the same weights held in memory and as
+the oracle, through every stage of the path: file -> mapped Q8_0 blocks -> device arena ->
+fused decode step / batched prefill / graph replay.
+
+The reference's one known answer (Qwen2.5-0.5B-Instruct Q8_0, prompt [1, 415, 6557] ->
+greedy 310, 470, 895, 280, 286, 456; bpd/decode_referee.py:189) runs when the file is
+supplied through LLAMATOV_QWEN25_05B_GGUF; the container and the GPU box do not hold it."""
+import os
+
+import numpy as np
+import pytest
+
+from llamatov_amd import dev_residency as dr
+from llamatov_amd import gguf as G
+from llamatov_amd import model as M
+from llamatov_amd._lib import LT_KV_F16, LT_KV_F32
+
+pytestmark = pytest.mark.gpu
+
+
+def case(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def bitexact(a, b):
+    return np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
+
+
+@pytest.fixture(scope="module")
+def tiny_file(tmp_path_factory):
+    cfg = M.TINY
+    w = M.synth_weights(cfg, seed=4321)
+    p = tmp_path_factory.mktemp("gguf") / "tiny.gguf"
+    G.save_q8_model(p, cfg, w)
+    return cfg, w, p
+
+
+def test_gguf_model_steps_like_memory_and_oracle(gpu, oracle, tiny_file):
+    cfg, w, path = tiny_file
+    case("gguf tiny stepwise vs in-memory vs oracle")
+    mf = dr.ResidentModel.from_gguf(path, gpu, max_ctx=cfg.max_ctx)
+    mm = dr.ResidentModel(cfg, w, gpu)
+    assert mf.load_report.verbatim == sum(1 for _, k, _ in M.weight_specs(cfg) if k == "q8")
+    assert mf.arena.nbytes == mm.arena.nbytes
+    prof = dr.Profile(kv_dtype=LT_KV_F16, attn_nsplit=2)
+    pf, pm = dr.DecodePlan(mf, prof), dr.DecodePlan(mm, prof)
+    orc = oracle.OracleModel(mf.cfg, w, kv_f16=True, attn_nsplit=2)
+    toks = M.random_prompt(cfg, 5, seed=12)
+    try:
+        for i in range(16):
+            t = toks[i] if i < len(toks) else int(np.argmax(exp))
+            pf.step(t)
+            pm.step(t)
+            got, ref = pf.read_logits(), pm.read_logits()
+            exp = orc.step(t)
+            assert bitexact(got, ref), f"step {i}: file vs memory"
+            assert bitexact(got, exp), f"step {i}: file vs oracle, max |d| {np.abs(got - exp).max()}"
+    finally:
+        pf.free(); pm.free(); mf.free(); mm.free()
+
+
+@pytest.mark.parametrize("kv_dtype,batched", [(LT_KV_F32, True), (LT_KV_F16, False)])
+def test_generate_from_path(gpu, oracle, tiny_file, kv_dtype, batched):
+    cfg, w, path = tiny_file
+    case(f"gguf generate kv={kv_dtype} batched={batched}")
+    prof = dr.Profile(kv_dtype=kv_dtype, attn_nsplit=1)
+    prompt = M.random_prompt(cfg, 7, seed=2)
+    got = dr.generate(str(path), prompt, 20, prof, batched_prefill=batched, max_ctx=cfg.max_ctx)
+    orc = oracle.OracleModel(cfg, w, kv_f16=kv_dtype == LT_KV_F16, attn_nsplit=1)
+    for t in prompt:
+        logits = orc.step(t)
+    exp = []
+    for _ in range(20):
+        nxt = oracle.argmax(logits)
+        exp.append(nxt)
+        logits = orc.step(nxt)
+    assert got == exp
+
+
+def test_known_answer_qwen25_05b(gpu):
+    path = os.environ.get("LLAMATOV_QWEN25_05B_GGUF")
+    if not path or not os.path.exists(path):
+        pytest.skip("Qwen2.5-0.5B-Instruct Q8_0 GGUF not supplied (LLAMATOV_QWEN25_05B_GGUF)")
+    case("known answer qwen2.5-0.5b")
+    prof = dr.Profile(kv_dtype=LT_KV_F32, attn_nsplit=1)
+    assert dr.generate(path, [1, 415, 6557], 6, prof) == [310, 470, 895, 280, 286, 456]
