@@ -26,6 +26,8 @@
 // the sequential per-dimension chains read LDS; every load of a row that may lie past
 // the range is a buffer load (out-of-range offsets read zeros), so loads never sit
 // behind branches.
+#include <cstdlib>
+
 #include "lt_q8_device.h"
 
 namespace {
@@ -453,6 +455,241 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
   // @phase attn 6
 }
 
+// Batched decode over long caches: one wave per workgroup, (split, HPW heads of one KV
+// group, sequence).  The same per-split arithmetic as k_attn, laid out so nothing waits on
+// a barrier or on LDS-staged V:
+//   scores   lane l takes positions l, l+64, ... of the split, HPW sequential fma chains
+//            over i, times scale, into LDS position-major [t][HPW];
+//   max      per head over the lanes (fmax, order-free);
+//   Z        lane l folds e_t over its own positions in ascending order, then the 64-lane
+//            tree (the frozen strided order);
+//   O        lane l owns dims [l*DPL, l*DPL + DPL) of every head: HPW*DPL sequential fma
+//            chains over t ascending, reading V rows straight from HBM (a wave reads one
+//            whole row per load) and the HPW exps of row t by one broadcast LDS read.
+// Loads run as rings: each K unit and each V row slot is refilled with the next round's
+// data as soon as it is consumed, so a wave keeps a round of K and kVRing rows of V in
+// flight without a second register buffer.  Every load is unconditional (past the range
+// the buffer offset reads zeros) and tails are masked by selects, so waits stay partial.
+// Every K/V row is read once per KV group.  Bit-identical to k_attn's AM_DECODE results.
+constexpr int kVRing = 32;
+
+template <bool kF16, int HPW, int DPL>
+__global__ __launch_bounds__(64) void k_attn_w1(AttnArgs A) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  constexpr int HD = 64 * DPL;
+  constexpr int kEb = kF16 ? 2 : 4;                 // bytes per cache element
+  constexpr int KU = HD * kEb / 16;                 // 16-byte units per K row
+  constexpr int VD = DPL * kEb / 4;                 // V dwords per lane per row (1, 2 or 4)
+  constexpr int OPL = DPL;                          // outputs per lane per head
+  static_assert(VD >= 1 && KU <= 32, "k_attn_w1: unsupported head size / cache type");
+  float* sq = lds;                                  // [HPW][HD]
+  float* se = lds + HPW * HD;                       // [per_max + 2][HPW]: rows, spare, zeros
+  const int l = threadIdx.x;
+  const int sp = blockIdx.x;
+  const int h0 = blockIdx.y * HPW;
+  const int b = blockIdx.z;
+  const int g = h0 / (A.nh / A.nkv);
+  const int kvrow = A.nkv * HD;                     // elements per cache position
+
+  const int L = A.len[b];
+  const int nctx = L < 0 ? 0 : (L > A.maxt ? A.maxt : L);
+  const int per = (nctx + A.nsplit - 1) / A.nsplit;
+  const int p0 = sp * per;
+  const int p1 = p0 + per < nctx ? p0 + per : nctx;
+  const int n = p1 > p0 ? p1 - p0 : 0;
+  const uint32_t rows = (uint32_t)gridDim.z * (uint32_t)A.maxt;
+  const __amdgpu_buffer_rsrc_t krsrc =
+      __builtin_amdgcn_make_buffer_rsrc(A.kc, 0, (int)(rows * (uint32_t)kvrow * kEb), 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrsrc =
+      __builtin_amdgcn_make_buffer_rsrc(A.vc, 0, (int)(rows * (uint32_t)kvrow * kEb), 0x00020000);
+  // byte offset of (position p0 of this split, head group g) and the row pitch
+  const uint32_t base = ((uint32_t)b * (uint32_t)A.maxt + (uint32_t)p0) * (uint32_t)kvrow * kEb + (uint32_t)g * HD * kEb;
+  const uint32_t pitch = (uint32_t)kvrow * kEb;
+
+  auto k_off = [&](int t) { return t < n ? (int)(base + (uint32_t)t * pitch) : (int)kNoRow; };
+  auto v_off = [&](int t) { return t < n ? (int)(base + (uint32_t)t * pitch + (uint32_t)l * VD * 4) : (int)kNoRow; };
+  auto load_v = [&](int t, uint32_t* dst) {
+    const int off = v_off(t);
+    if (VD == 1) {
+      dst[0] = __builtin_amdgcn_raw_buffer_load_b32(vrsrc, off, 0, 0);
+    } else if (VD == 2) {
+      const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(vrsrc, off, 0, 0);
+      dst[0] = w.x; dst[1] = w.y;
+    } else {
+      const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(vrsrc, off, 0, 0);
+      dst[0] = w.x; dst[1] = w.y; dst[2] = w.z; dst[3] = w.w;
+    }
+  };
+
+  // @phase attn 0
+  // first K row of this lane and the first kVRing V rows: in flight before anything else
+  u32x4 kr[KU];
+  {
+    const int off = k_off(l);
+#pragma unroll
+    for (int u = 0; u < KU; u++) kr[u] = __builtin_amdgcn_raw_buffer_load_b128(krsrc, off + u * 16, 0, 0);
+  }
+  uint32_t v[kVRing][VD];
+#pragma unroll
+  for (int k = 0; k < kVRing; k++) load_v(k, v[k]);
+  {
+    const float* qs = A.q + (size_t)b * A.q_stride + (size_t)h0 * HD;
+#pragma unroll
+    for (int k = 0; k < HPW * DPL; k++) sq[l + 64 * k] = qs[l + 64 * k];
+    if (l < HPW) se[(A.per_max + 1) * HPW + l] = 0.0f;   // the zero row
+  }
+  __syncthreads();
+
+  // @phase attn 1
+  // scores; unit u of the next round's row is requested right after unit u is consumed
+  float m[HPW];
+#pragma unroll
+  for (int r = 0; r < HPW; r++) m[r] = -1e30f;
+  for (int t = l; t - l < n; t += 64) {
+    const int noff = k_off(t + 64);
+    float acc[HPW];
+#pragma unroll
+    for (int r = 0; r < HPW; r++) acc[r] = 0.0f;
+    // q of unit u (kQu dims per head) is read one unit ahead of its use
+    constexpr int kQu = kF16 ? 8 : 4;
+    float qc[HPW][kQu], qn[HPW][kQu];
+#pragma unroll
+    for (int r = 0; r < HPW; r++)
+#pragma unroll
+      for (int i = 0; i < kQu; i++) qc[r][i] = sq[r * HD + i];
+#pragma unroll
+    for (int u = 0; u < KU; u++) {
+      uint32_t a[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
+      // unit u is consumed here and no earlier: keeps one unit's conversions live at a
+      // time, and its refill behind its use
+      asm volatile("" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]) : : "memory");
+      kr[u] = __builtin_amdgcn_raw_buffer_load_b128(krsrc, noff + u * 16, 0, 0);
+      if (u + 1 < KU) {
+#pragma unroll
+        for (int r = 0; r < HPW; r++)
+#pragma unroll
+          for (int i = 0; i < kQu; i++) qn[r][i] = sq[r * HD + (u + 1) * kQu + i];
+      }
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        if (kF16) {
+          const float k0 = lt_h2f((uint16_t)(a[c] & 0xFFFFu));
+          const float k1 = lt_h2f((uint16_t)(a[c] >> 16));
+#pragma unroll
+          for (int r = 0; r < HPW; r++) {
+            acc[r] = fmaf(qc[r][2 * c], k0, acc[r]);
+            acc[r] = fmaf(qc[r][2 * c + 1], k1, acc[r]);
+          }
+        } else {
+          const float k0 = __builtin_bit_cast(float, a[c]);
+#pragma unroll
+          for (int r = 0; r < HPW; r++) acc[r] = fmaf(qc[r][c], k0, acc[r]);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < HPW; r++)
+#pragma unroll
+        for (int i = 0; i < kQu; i++) qc[r][i] = qn[r][i];
+    }
+    // stored unconditionally (lanes past the range write the spare row per_max), so the
+    // chains are computed in place rather than sunk into per-head branches
+    const bool in = t < n;
+    const int ts = in ? t : A.per_max;
+#pragma unroll
+    for (int r = 0; r < HPW; r++) {
+      const float s = acc[r] * A.scale;
+      se[ts * HPW + r] = s;
+      m[r] = fmaxf(m[r], in ? s : -1e30f);
+    }
+  }
+  // @phase attn 2
+  // max, exps and Z
+  float zs[HPW];
+#pragma unroll
+  for (int r = 0; r < HPW; r++) {
+    m[r] = wave_max(m[r]);
+    zs[r] = 0.0f;
+  }
+  for (int t = l; t < n; t += 64) {
+#pragma unroll
+    for (int r = 0; r < HPW; r++) {
+      const float e = lt_expf(se[t * HPW + r] - m[r]);
+      se[t * HPW + r] = e;
+      zs[r] = zs[r] + e;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < HPW; r++) zs[r] = wave_tree_dpp(zs[r]);   // lane 0: Z of head r
+  __syncthreads();
+
+  // @phase attn 3
+  // O: ascending t; row slot k is refilled with row t + kVRing once row t is folded.  Past
+  // n the exps come from the zero row and the rows read zeros, so fma(0, 0, o) leaves o
+  // unchanged (o is never -0: it starts at +0 and +0 + -0 = +0).
+  float o[HPW][OPL];
+#pragma unroll
+  for (int r = 0; r < HPW; r++)
+#pragma unroll
+    for (int k = 0; k < OPL; k++) o[r][k] = 0.0f;
+  for (int t0 = 0; t0 < n; t0 += kVRing) {
+#pragma unroll
+    for (int k = 0; k < kVRing; k++) {
+      const int t = t0 + k;
+      const int ti = t < n ? t : A.per_max + 1;   // past the range: the zero row
+      uint32_t x[VD];
+#pragma unroll
+      for (int w = 0; w < VD; w++) x[w] = v[k][w];
+      // row t is consumed here: its exps are read and its slot refilled no earlier
+      if (VD == 1) asm volatile("" : "+v"(x[0]) : : "memory");
+      else if (VD == 2) asm volatile("" : "+v"(x[0]), "+v"(x[1]) : : "memory");
+      else asm volatile("" : "+v"(x[0]), "+v"(x[1]), "+v"(x[VD > 2 ? 2 : 0]), "+v"(x[VD > 3 ? 3 : 0]) : : "memory");
+      float e[HPW];
+#pragma unroll
+      for (int r = 0; r < HPW; r++) e[r] = se[ti * HPW + r];
+      load_v(t + kVRing, v[k]);
+#pragma unroll
+      for (int w = 0; w < VD; w++) {
+        if (kF16) {
+          const float x0 = lt_h2f((uint16_t)(x[w] & 0xFFFFu));
+          const float x1 = lt_h2f((uint16_t)(x[w] >> 16));
+#pragma unroll
+          for (int r = 0; r < HPW; r++) {
+            o[r][2 * w] = fmaf(e[r], x0, o[r][2 * w]);
+            o[r][2 * w + 1] = fmaf(e[r], x1, o[r][2 * w + 1]);
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < HPW; r++) o[r][w] = fmaf(e[r], __builtin_bit_cast(float, x[w]), o[r][w]);
+        }
+      }
+    }
+  }
+
+  // @phase attn 4
+  // outputs: dims [l*OPL, l*OPL + OPL) of each head
+  const size_t hrow0 = (size_t)b * A.nh + h0;
+  if (A.nsplit == 1) {
+#pragma unroll
+    for (int r = 0; r < HPW; r++) {
+      const float z = __shfl(zs[r], 0, 64);
+#pragma unroll
+      for (int k = 0; k < OPL; k++) A.out[(hrow0 + r) * HD + l * OPL + k] = o[r][k] / z;
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < HPW; r++)
+#pragma unroll
+      for (int k = 0; k < OPL; k++) A.wso[((hrow0 + r) * A.nsplit + sp) * HD + l * OPL + k] = o[r][k];
+    if (l == 0) {
+#pragma unroll
+      for (int r = 0; r < HPW; r++) {
+        A.wsm[(hrow0 + r) * A.nsplit + sp] = m[r];
+        A.wsz[(hrow0 + r) * A.nsplit + sp] = zs[r];
+      }
+    }
+  }
+}
+
 // Split-K merge, one workgroup per (query head, row): the declared combine in ascending
 // split order (attn_decode_split.cu:37-91): M = max m_s, w_s = exp(m_s - M),
 // Z = sum fma(w_s, Z_s), O_d = sum fma(w_s, O_s,d), out = O/Z; optionally the quant of
@@ -540,6 +777,33 @@ hipError_t launch_attn_k(int hpw, dim3 grid, size_t shm, hipStream_t st, const A
   return hipGetLastError();
 }
 
+template <bool kF16>
+hipError_t launch_w1(int hpw, int dpl, dim3 grid, size_t shm, hipStream_t st, const AttnArgs& A) {
+#define LT_W1_CASE(H, D)                                            \
+  if (hpw == H && dpl == D) {                                       \
+    k_attn_w1<kF16, H, D><<<grid, 64, shm, st>>>(A);                \
+    return hipGetLastError();                                       \
+  }
+  if constexpr (!kF16) {
+    LT_W1_CASE(1, 1) LT_W1_CASE(2, 1) LT_W1_CASE(4, 1) LT_W1_CASE(8, 1)
+  }
+  LT_W1_CASE(1, 2) LT_W1_CASE(2, 2) LT_W1_CASE(4, 2) LT_W1_CASE(8, 2)
+  if constexpr (kF16) {
+    LT_W1_CASE(1, 4) LT_W1_CASE(2, 4) LT_W1_CASE(4, 4) LT_W1_CASE(8, 4)
+  }
+#undef LT_W1_CASE
+  return hipErrorInvalidValue;
+}
+
+// LT_ATTN_W1=0 keeps batched decode on k_attn (for comparisons); the default is k_attn_w1.
+bool use_w1() {
+  static const bool on = [] {
+    const char* s = getenv("LT_ATTN_W1");
+    return !(s && s[0] == '0');
+  }();
+  return on;
+}
+
 // Launches the attention (and the merge when nsplit > 1) for `rows` query rows with hpw
 // heads per workgroup.
 int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, void* ws, size_t ws_bytes,
@@ -555,6 +819,28 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
     A.wsm = w.m;
     A.wsz = w.z;
     A.wso = w.o;
+  }
+  if (mode == AM_DECODE && use_w1()) {
+    // the single-wave kernel: all heads of a KV group share its K/V reads
+    const int rep = A.nh / A.nkv;
+    const int h = rep % 8 == 0 ? 8 : rep % 4 == 0 ? 4 : rep % 2 == 0 ? 2 : 1;
+    const int dpl = A.hd / 64;
+    const int per_max = (A.maxt + A.nsplit - 1) / A.nsplit;
+    const size_t shm = ((size_t)h * A.hd + (size_t)(per_max + 2) * h) * sizeof(float);
+    // fp16: 128 or 256 dims; fp32: 64 or 128 (a K row of at most 32 16-byte units)
+    if (A.hd % 64 == 0 && (f16 ? (dpl == 2 || dpl == 4) : (dpl == 1 || dpl == 2)) && shm <= 64 * 1024) {
+      A.per_max = per_max;
+      const dim3 grid(A.nsplit, A.nh / h, rows);
+      hipError_t e = f16 ? launch_w1<true>(h, dpl, grid, shm, ctx->stream, A)
+                         : launch_w1<false>(h, dpl, grid, shm, ctx->stream, A);
+      if (e != hipSuccess) return lt_fail_hip(e, what, __FILE__, __LINE__);
+      if (A.nsplit > 1) {
+        k_attn_merge<<<dim3(A.nh, rows), 256, 0, ctx->stream>>>(A.wsm, A.wsz, A.wso, nullptr, A.maxt, A.out,
+                                                                nullptr, nullptr, A.nh, A.hd, A.nsplit);
+        return lt_check_launch("k_attn_merge");
+      }
+      return lt_check_launch("k_attn_w1");
+    }
   }
   auto shm_for = [&](int per_max) {
     return ((size_t)hpw * A.hd + 2 * A.hd + (size_t)hpw * per_max + kVChunkFloats) * sizeof(float);

@@ -13,6 +13,7 @@
 namespace lt {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // 16-byte vector with 4-byte alignment: global_load_dwordx4 needs only dword alignment.
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 

@@ -213,6 +213,32 @@ def test_attention_masked_poison_and_length_sweep(gpu, oracle, kv_dtype, nsplit,
         assert_bitexact(out.to_host(), exp, f"attn L={L}")
 
 
+@pytest.mark.parametrize("kv_dtype,hd", [(LT_KV_F16, 128), (LT_KV_F16, 256), (LT_KV_F32, 64),
+                                         (LT_KV_F32, 128)])
+@pytest.mark.parametrize("nh,nkv", [(8, 8), (16, 8), (32, 8), (16, 2)])
+def test_attention_decode_geometries(gpu, oracle, kv_dtype, hd, nh, nkv):
+    """Batched decode across head sizes, GQA group sizes (1, 2, 4, 8 heads per KV head) and
+    cache types, NaN past each sequence's length, split counts that leave ragged and empty
+    splits (L = 3 with 4 splits), and the single-split path that divides in-kernel."""
+    f16 = kv_dtype == LT_KV_F16
+    rng = np.random.default_rng(hd + nh)
+    B, maxt = 3, 300
+    for nsplit, lens in ((1, [300, 129, 1]), (4, [3, 64, 65]), (7, [300, 200, 77])):
+        case(f"attn decode hd={hd} nh={nh} nkv={nkv} f16={f16} nsplit={nsplit} lens={lens}")
+        q = rng.standard_normal((B, nh * hd)).astype(np.float32)
+        k, v = _attn_setup(rng, B, maxt, nkv, hd, kv_dtype, lens, np.nan)
+        ws_n = _lib.raw("lt_attn_workspace_size")(B, nh, hd, nsplit)
+        ws = empty((max(ws_n, 1),), np.uint8)
+        out = empty((B, nh * hd), np.float32)
+        scale = float(hd ** -0.5)
+        call("lt_attn_decode", gpu.handle, up(q).vp, up(k).vp, up(v).vp, up(np.array(lens, np.int32)).vp,
+             out.vp, B, nh, nkv, hd, ctypes.c_float(scale), maxt, nsplit, kv_dtype, ws.vp, ws.nbytes)
+        got = out.to_host()
+        for b in range(B):
+            exp = oracle.attn_decode(q[b], k[b], v[b], lens[b], nh, nkv, hd, scale, f16, nsplit)
+            assert_bitexact(got[b], exp, f"attn b={b} L={lens[b]}")
+
+
 @pytest.mark.parametrize("B,L,nsplit", [(1, 4096, 32), (8, 4096, 32), (1, 16384, 64), (2, 32768, 128)])
 def test_attention_long_context_batched(gpu, oracle, B, L, nsplit):
     """BASELINE config 4 geometry: 32 Q heads, 8 KV heads, hd 128, fp16 KV."""
