@@ -474,7 +474,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
 constexpr int kVRing = 32;
 
 template <bool kF16, int HPW, int DPL>
-__global__ __launch_bounds__(64) void k_attn_w1(AttnArgs A) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((kF16 ? DPL * 8 : DPL * 16) <= 16 ? 3 : 1))) void k_attn_w1(AttnArgs A) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   constexpr int HD = 64 * DPL;
   constexpr int kEb = kF16 ? 2 : 4;                 // bytes per cache element
@@ -483,7 +483,8 @@ __global__ __launch_bounds__(64) void k_attn_w1(AttnArgs A) {
   constexpr int OPL = DPL;                          // outputs per lane per head
   static_assert(VD >= 1 && KU <= 32, "k_attn_w1: unsupported head size / cache type");
   float* sq = lds;                                  // [HPW][HD]
-  float* se = lds + HPW * HD;                       // [per_max + 2][HPW]: rows, spare, zeros
+  u32x4* sk = (u32x4*)(lds + HPW * HD);             // [64][KU] one round of K rows, swizzled
+  float* se = lds + HPW * HD + 64 * KU * 4;         // [per_max + 2][HPW]: rows, spare, zeros
   const int l = threadIdx.x;
   const int sp = blockIdx.x;
   const int h0 = blockIdx.y * HPW;
@@ -506,7 +507,6 @@ __global__ __launch_bounds__(64) void k_attn_w1(AttnArgs A) {
   const uint32_t base = ((uint32_t)b * (uint32_t)A.maxt + (uint32_t)p0) * (uint32_t)kvrow * kEb + (uint32_t)g * HD * kEb;
   const uint32_t pitch = (uint32_t)kvrow * kEb;
 
-  auto k_off = [&](int t) { return t < n ? (int)(base + (uint32_t)t * pitch) : (int)kNoRow; };
   auto v_off = [&](int t) { return t < n ? (int)(base + (uint32_t)t * pitch + (uint32_t)l * VD * 4) : (int)kNoRow; };
   auto load_v = [&](int t, uint32_t* dst) {
     const int off = v_off(t);
@@ -522,16 +522,26 @@ __global__ __launch_bounds__(64) void k_attn_w1(AttnArgs A) {
   };
 
   // @phase attn 0
-  // first K row of this lane and the first kVRing V rows: in flight before anything else
-  u32x4 kr[KU];
-  {
-    const int off = k_off(l);
+  // K rounds are read coalesced: load i of a round brings rows i*(64/KU) + l/KU, unit
+  // l%KU (whole rows per instruction); they pass through LDS, where row r's unit u sits at
+  // slot (u + r) % KU of row r, so the lane-per-row reads below are bank-conflict free
+  constexpr int kRpi = 64 / KU;                     // rows per load instruction
+  const int kl_row = l / KU, kl_unit = l % KU;
+  u32x4 kb[KU];
+  // Rows past the split's end are clamped to its last row: their scores only reach the
+  // spare LDS row and are masked out of the max (V rows past the end read zeros instead).
+  const int nlast = n > 0 ? n - 1 : 0;
+  const uint32_t k_last = base + (uint32_t)nlast * pitch + (uint32_t)kl_unit * 16;
+  auto load_round = [&](int t0) {
+    uint32_t off = base + (uint32_t)(t0 + kl_row) * pitch + (uint32_t)kl_unit * 16;
 #pragma unroll
-    for (int u = 0; u < KU; u++) kr[u] = __builtin_amdgcn_raw_buffer_load_b128(krsrc, off + u * 16, 0, 0);
-  }
-  uint32_t v[kVRing][VD];
-#pragma unroll
-  for (int k = 0; k < kVRing; k++) load_v(k, v[k]);
+    for (int i = 0; i < KU; i++) {
+      kb[i] = __builtin_amdgcn_raw_buffer_load_b128(krsrc, (int)(off < k_last ? off : k_last), 0, 0);
+      off += kRpi * pitch;
+    }
+  };
+  // the first K round: in flight before anything else
+  load_round(0);
   {
     const float* qs = A.q + (size_t)b * A.q_stride + (size_t)h0 * HD;
 #pragma unroll
@@ -546,50 +556,64 @@ __global__ __launch_bounds__(64) void k_attn_w1(AttnArgs A) {
 #pragma unroll
   for (int r = 0; r < HPW; r++) m[r] = -1e30f;
   for (int t = l; t - l < n; t += 64) {
-    const int noff = k_off(t + 64);
+    // this round's rows into LDS (the previous round's reads were issued before these
+    // writes, and one wave's LDS operations complete in order), then the next round's loads
+#pragma unroll
+    for (int i = 0; i < KU; i++) {
+      const int r = i * kRpi + kl_row;
+      sk[r * KU + ((kl_unit + r) % KU)] = kb[i];
+    }
+    asm volatile("" ::: "memory");
+    load_round(t - l + 64);
+    // passes of kHg heads over this lane's K row in LDS; within a pass, K unit u and q of
+    // unit u (kQu dims per head) are read one unit ahead of their use, and the fence keeps
+    // the compiler from hoisting more
+    constexpr int kHg = HPW < 2 ? HPW : 2;
+    constexpr int kQu = kF16 ? 8 : 4;
     float acc[HPW];
 #pragma unroll
-    for (int r = 0; r < HPW; r++) acc[r] = 0.0f;
-    // q of unit u (kQu dims per head) is read one unit ahead of its use
-    constexpr int kQu = kF16 ? 8 : 4;
-    float qc[HPW][kQu], qn[HPW][kQu];
+    for (int g0 = 0; g0 < HPW; g0 += kHg) {
+      float qc[kHg][kQu], qn[kHg][kQu];
+      u32x4 kc = sk[l * KU + (l % KU)], kn;
 #pragma unroll
-    for (int r = 0; r < HPW; r++)
+      for (int r = 0; r < kHg; r++) {
+        acc[g0 + r] = 0.0f;
 #pragma unroll
-      for (int i = 0; i < kQu; i++) qc[r][i] = sq[r * HD + i];
-#pragma unroll
-    for (int u = 0; u < KU; u++) {
-      uint32_t a[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
-      // unit u is consumed here and no earlier: keeps one unit's conversions live at a
-      // time, and its refill behind its use
-      asm volatile("" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]) : : "memory");
-      kr[u] = __builtin_amdgcn_raw_buffer_load_b128(krsrc, noff + u * 16, 0, 0);
-      if (u + 1 < KU) {
-#pragma unroll
-        for (int r = 0; r < HPW; r++)
-#pragma unroll
-          for (int i = 0; i < kQu; i++) qn[r][i] = sq[r * HD + (u + 1) * kQu + i];
+        for (int i = 0; i < kQu; i++) qc[r][i] = sq[(g0 + r) * HD + i];
       }
 #pragma unroll
-      for (int c = 0; c < 4; c++) {
-        if (kF16) {
-          const float k0 = lt_h2f((uint16_t)(a[c] & 0xFFFFu));
-          const float k1 = lt_h2f((uint16_t)(a[c] >> 16));
+      for (int u = 0; u < KU; u++) {
+        asm volatile("" ::: "memory");
+        uint32_t a[4] = {kc.x, kc.y, kc.z, kc.w};
+        if (u + 1 < KU) {
+          kn = sk[l * KU + ((u + 1 + l) % KU)];
 #pragma unroll
-          for (int r = 0; r < HPW; r++) {
-            acc[r] = fmaf(qc[r][2 * c], k0, acc[r]);
-            acc[r] = fmaf(qc[r][2 * c + 1], k1, acc[r]);
-          }
-        } else {
-          const float k0 = __builtin_bit_cast(float, a[c]);
+          for (int r = 0; r < kHg; r++)
 #pragma unroll
-          for (int r = 0; r < HPW; r++) acc[r] = fmaf(qc[r][c], k0, acc[r]);
+            for (int i = 0; i < kQu; i++) qn[r][i] = sq[(g0 + r) * HD + (u + 1) * kQu + i];
         }
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          if (kF16) {
+            const float k0 = lt_h2f((uint16_t)(a[c] & 0xFFFFu));
+            const float k1 = lt_h2f((uint16_t)(a[c] >> 16));
+#pragma unroll
+            for (int r = 0; r < kHg; r++) {
+              acc[g0 + r] = fmaf(qc[r][2 * c], k0, acc[g0 + r]);
+              acc[g0 + r] = fmaf(qc[r][2 * c + 1], k1, acc[g0 + r]);
+            }
+          } else {
+            const float k0 = __builtin_bit_cast(float, a[c]);
+#pragma unroll
+            for (int r = 0; r < kHg; r++) acc[g0 + r] = fmaf(qc[r][c], k0, acc[g0 + r]);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < kHg; r++)
+#pragma unroll
+          for (int i = 0; i < kQu; i++) qc[r][i] = qn[r][i];
+        kc = kn;
       }
-#pragma unroll
-      for (int r = 0; r < HPW; r++)
-#pragma unroll
-        for (int i = 0; i < kQu; i++) qc[r][i] = qn[r][i];
     }
     // stored unconditionally (lanes past the range write the spare row per_max), so the
     // chains are computed in place rather than sunk into per-head branches
@@ -603,6 +627,10 @@ __global__ __launch_bounds__(64) void k_attn_w1(AttnArgs A) {
     }
   }
   // @phase attn 2
+  // the first kVRing V rows go out now, under the softmax
+  uint32_t v[kVRing][VD];
+#pragma unroll
+  for (int k = 0; k < kVRing; k++) load_v(k, v[k]);
   // max, exps and Z
   float zs[HPW];
 #pragma unroll
@@ -694,10 +722,9 @@ __global__ __launch_bounds__(64) void k_attn_w1(AttnArgs A) {
 // split order (attn_decode_split.cu:37-91): M = max m_s, w_s = exp(m_s - M),
 // Z = sum fma(w_s, Z_s), O_d = sum fma(w_s, O_s,d), out = O/Z; optionally the quant of
 // the head's hd/32 blocks.  Every partial is fetched by independent buffer loads issued at
-// the start (one memory round trip); the exps run one per thread.  len (STEP) marks an
-// out-of-range position: the output is then 0, as in the single pass.
-constexpr int kMergeQ = 16;   // split outputs prefetched per thread
-
+// the start (kMergeQ >= nsplit: one memory round trip); the exps run one per thread.  len
+// (STEP) marks an out-of-range position: the output is then 0, as in the single pass.
+template <int kMergeQ>   // split outputs prefetched per thread
 __global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ wsm, const float* __restrict__ wsz,
                                                     const float* __restrict__ wso, const int* __restrict__ len,
                                                     int maxt, float* __restrict__ out, int8_t* __restrict__ oq,
@@ -708,12 +735,15 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ ws
   const int tid = threadIdx.x;
   const __amdgpu_buffer_rsrc_t orsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)(wso + hrow * nsplit * hd), 0, nsplit * hd * 4, 0x00020000);
+  // every load in range and unconditional (dim clamped to hd-1, split to nsplit-1; the
+  // surplus values are never folded), so no load waits behind a branch
   float po[kMergeQ];
+  const int dcl = tid < hd ? tid : hd - 1;
   auto load_po = [&](int q0) {
 #pragma unroll
     for (int q = 0; q < kMergeQ; q++) {
-      const int off = (tid < hd && q0 + q < nsplit) ? ((q0 + q) * hd + tid) * 4 : (int)kNoRow;
-      po[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(orsrc, off, 0, 0));
+      const int sq_ = q0 + q < nsplit ? q0 + q : nsplit - 1;
+      po[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(orsrc, dcl * 4, sq_ * hd * 4, 0));
     }
   };
   load_po(0);
@@ -777,6 +807,19 @@ hipError_t launch_attn_k(int hpw, dim3 grid, size_t shm, hipStream_t st, const A
   return hipGetLastError();
 }
 
+// The merge with a prefetch depth covering nsplit (<= 128, checked by the callers).
+void launch_merge(dim3 grid, hipStream_t st, const float* wsm, const float* wsz, const float* wso, const int* len,
+                  int maxt, float* out, int8_t* oq, uint16_t* od, int nh, int hd, int nsplit) {
+  if (nsplit <= 16)
+    k_attn_merge<16><<<grid, 256, 0, st>>>(wsm, wsz, wso, len, maxt, out, oq, od, nh, hd, nsplit);
+  else if (nsplit <= 32)
+    k_attn_merge<32><<<grid, 256, 0, st>>>(wsm, wsz, wso, len, maxt, out, oq, od, nh, hd, nsplit);
+  else if (nsplit <= 64)
+    k_attn_merge<64><<<grid, 256, 0, st>>>(wsm, wsz, wso, len, maxt, out, oq, od, nh, hd, nsplit);
+  else
+    k_attn_merge<128><<<grid, 256, 0, st>>>(wsm, wsz, wso, len, maxt, out, oq, od, nh, hd, nsplit);
+}
+
 template <bool kF16>
 hipError_t launch_w1(int hpw, int dpl, dim3 grid, size_t shm, hipStream_t st, const AttnArgs& A) {
 #define LT_W1_CASE(H, D)                                            \
@@ -826,7 +869,8 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
     const int h = rep % 8 == 0 ? 8 : rep % 4 == 0 ? 4 : rep % 2 == 0 ? 2 : 1;
     const int dpl = A.hd / 64;
     const int per_max = (A.maxt + A.nsplit - 1) / A.nsplit;
-    const size_t shm = ((size_t)h * A.hd + (size_t)(per_max + 2) * h) * sizeof(float);
+    const size_t ku = (size_t)A.hd * (f16 ? 2 : 4) / 16;
+    const size_t shm = ((size_t)h * A.hd + 64 * ku * 4 + (size_t)(per_max + 2) * h) * sizeof(float);
     // fp16: 128 or 256 dims; fp32: 64 or 128 (a K row of at most 32 16-byte units)
     if (A.hd % 64 == 0 && (f16 ? (dpl == 2 || dpl == 4) : (dpl == 1 || dpl == 2)) && shm <= 64 * 1024) {
       A.per_max = per_max;
@@ -835,8 +879,8 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
                          : launch_w1<false>(h, dpl, grid, shm, ctx->stream, A);
       if (e != hipSuccess) return lt_fail_hip(e, what, __FILE__, __LINE__);
       if (A.nsplit > 1) {
-        k_attn_merge<<<dim3(A.nh, rows), 256, 0, ctx->stream>>>(A.wsm, A.wsz, A.wso, nullptr, A.maxt, A.out,
-                                                                nullptr, nullptr, A.nh, A.hd, A.nsplit);
+        launch_merge(dim3(A.nh, rows), ctx->stream, A.wsm, A.wsz, A.wso, nullptr, A.maxt, A.out, nullptr, nullptr,
+                     A.nh, A.hd, A.nsplit);
         return lt_check_launch("k_attn_merge");
       }
       return lt_check_launch("k_attn_w1");
@@ -865,8 +909,8 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
             : launch_attn_k<false, AM_PREFILL>(hpw, grid, shm, ctx->stream, A);
   if (e != hipSuccess) return lt_fail_hip(e, what, __FILE__, __LINE__);
   if (A.nsplit > 1 && !A.inwg) {
-    k_attn_merge<<<dim3(A.nh, rows), 256, 0, ctx->stream>>>(A.wsm, A.wsz, A.wso, mode == AM_STEP ? A.len : nullptr,
-                                                            A.maxt, A.out, A.oq, A.od, A.nh, A.hd, A.nsplit);
+    launch_merge(dim3(A.nh, rows), ctx->stream, A.wsm, A.wsz, A.wso, mode == AM_STEP ? A.len : nullptr, A.maxt,
+                 A.out, A.oq, A.od, A.nh, A.hd, A.nsplit);
     return lt_check_launch("k_attn_merge");
   }
   return lt_check_launch("k_attn");
