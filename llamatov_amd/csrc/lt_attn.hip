@@ -471,7 +471,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
 // flight without a second register buffer.  Every load is unconditional (past the range
 // the buffer offset reads zeros) and tails are masked by selects, so waits stay partial.
 // Every K/V row is read once per KV group.  Bit-identical to k_attn's AM_DECODE results.
-constexpr int kVRing = 32;
+constexpr int kVRingDw = 32;   // V dwords in flight per lane (rows = kVRingDw / VD)
 
 template <bool kF16, int HPW, int DPL>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((kF16 ? DPL * 8 : DPL * 16) <= 16 ? 3 : 1))) void k_attn_w1(AttnArgs A) {
@@ -481,10 +481,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((kF16 ? DPL 
   constexpr int KU = HD * kEb / 16;                 // 16-byte units per K row
   constexpr int VD = DPL * kEb / 4;                 // V dwords per lane per row (1, 2 or 4)
   constexpr int OPL = DPL;                          // outputs per lane per head
+  constexpr int kVRing = kVRingDw / VD;             // V rows in flight
   static_assert(VD >= 1 && KU <= 32, "k_attn_w1: unsupported head size / cache type");
   float* sq = lds;                                  // [HPW][HD]
-  u32x4* sk = (u32x4*)(lds + HPW * HD);             // [64][KU] one round of K rows, swizzled
-  float* se = lds + HPW * HD + 64 * KU * 4;         // [per_max + 2][HPW]: rows, spare, zeros
+  u32x4* sk = (u32x4*)(lds + HPW * HD);             // [kPR][KU + 1] one round of K rows, padded
+  float* se = lds + HPW * HD + (HPW >= 2 ? 32 : 64) * (KU + 1) * 4;   // [per_max + 2][HPW]: rows, spare, zeros
   const int l = threadIdx.x;
   const int sp = blockIdx.x;
   const int h0 = blockIdx.y * HPW;
@@ -522,26 +523,35 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((kF16 ? DPL 
   };
 
   // @phase attn 0
-  // K rounds are read coalesced: load i of a round brings rows i*(64/KU) + l/KU, unit
-  // l%KU (whole rows per instruction); they pass through LDS, where row r's unit u sits at
-  // slot (u + r) % KU of row r, so the lane-per-row reads below are bank-conflict free
+  // Scores run in rounds of kPR positions.  With HPW >= 2 the two half-waves take half of
+  // the heads each for the same 32 positions (lane l: position t0 + l%32, heads
+  // hb .. hb+kHL-1), which halves a round's K footprint; with HPW = 1 a round is 64
+  // positions.  K rounds are read coalesced: load i of a round brings rows
+  // i*(64/KU) + l/KU, unit l%KU (whole rows per instruction); they pass through LDS rows
+  // padded by one 16-byte unit, so the lane-per-row reads below (lanes 4 banks apart) are
+  // bank-conflict free and every LDS address is a base plus an immediate.
+  constexpr int kPR = HPW >= 2 ? 32 : 64;           // positions per round
+  constexpr int kHL = HPW >= 2 ? HPW / 2 : 1;       // heads per lane
   constexpr int kRpi = 64 / KU;                     // rows per load instruction
+  constexpr int kNI = kPR * KU / 64;                // load instructions per round
+  const int lr = l % kPR;                           // this lane's row within a round
+  const int hb = HPW >= 2 ? (l / 32) * kHL : 0;     // this lane's first head
   const int kl_row = l / KU, kl_unit = l % KU;
-  u32x4 kb[KU];
+  u32x4 kb[kNI];
   // Rows past the split's end are clamped to its last row: their scores only reach the
-  // spare LDS row and are masked out of the max (V rows past the end read zeros instead).
+  // spare LDS row, which no later pass reads (V rows past the end read zeros instead).
   const int nlast = n > 0 ? n - 1 : 0;
   const uint32_t k_last = base + (uint32_t)nlast * pitch + (uint32_t)kl_unit * 16;
-  auto load_round = [&](int t0) {
+  auto load_round = [&](int t0, u32x4* dst) {
     uint32_t off = base + (uint32_t)(t0 + kl_row) * pitch + (uint32_t)kl_unit * 16;
 #pragma unroll
-    for (int i = 0; i < KU; i++) {
-      kb[i] = __builtin_amdgcn_raw_buffer_load_b128(krsrc, (int)(off < k_last ? off : k_last), 0, 0);
+    for (int i = 0; i < kNI; i++) {
+      dst[i] = __builtin_amdgcn_raw_buffer_load_b128(krsrc, (int)(off < k_last ? off : k_last), 0, 0);
       off += kRpi * pitch;
     }
   };
   // the first K round: in flight before anything else
-  load_round(0);
+  load_round(0, kb);
   {
     const float* qs = A.q + (size_t)b * A.q_stride + (size_t)h0 * HD;
 #pragma unroll
@@ -551,46 +561,44 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((kF16 ? DPL 
   __syncthreads();
 
   // @phase attn 1
-  // scores; unit u of the next round's row is requested right after unit u is consumed
-  float m[HPW];
-#pragma unroll
-  for (int r = 0; r < HPW; r++) m[r] = -1e30f;
-  for (int t = l; t - l < n; t += 64) {
+  auto score_round = [&](int t0, u32x4* buf) {
     // this round's rows into LDS (the previous round's reads were issued before these
-    // writes, and one wave's LDS operations complete in order), then the next round's loads
+    // writes, and one wave's LDS operations complete in order), then the next round's
+    // loads into the same registers
 #pragma unroll
-    for (int i = 0; i < KU; i++) {
-      const int r = i * kRpi + kl_row;
-      sk[r * KU + ((kl_unit + r) % KU)] = kb[i];
-    }
+    for (int i = 0; i < kNI; i++) sk[(i * kRpi + kl_row) * (KU + 1) + kl_unit] = buf[i];
     asm volatile("" ::: "memory");
-    load_round(t - l + 64);
+    load_round(t0 + kPR, buf);
     // passes of kHg heads over this lane's K row in LDS; within a pass, K unit u and q of
     // unit u (kQu dims per head) are read one unit ahead of their use, and the fence keeps
     // the compiler from hoisting more
-    constexpr int kHg = HPW < 2 ? HPW : 2;
+    constexpr int kHg = kHL < 2 ? kHL : 2;
     constexpr int kQu = kF16 ? 8 : 4;
-    float acc[HPW];
+    // stored unconditionally (lanes past the range write the spare row per_max), so the
+    // chains are computed in place rather than sunk into branches
+    const int t = t0 + lr;
+    const int ts = t < n ? t : A.per_max;
 #pragma unroll
-    for (int g0 = 0; g0 < HPW; g0 += kHg) {
+    for (int g0 = 0; g0 < kHL; g0 += kHg) {
+      float acc[kHg];
       float qc[kHg][kQu], qn[kHg][kQu];
-      u32x4 kc = sk[l * KU + (l % KU)], kn;
+      u32x4 kc = sk[lr * (KU + 1)], kn;
 #pragma unroll
       for (int r = 0; r < kHg; r++) {
-        acc[g0 + r] = 0.0f;
+        acc[r] = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kQu; i++) qc[r][i] = sq[(g0 + r) * HD + i];
+        for (int i = 0; i < kQu; i++) qc[r][i] = sq[(hb + g0 + r) * HD + i];
       }
 #pragma unroll
       for (int u = 0; u < KU; u++) {
         asm volatile("" ::: "memory");
         uint32_t a[4] = {kc.x, kc.y, kc.z, kc.w};
         if (u + 1 < KU) {
-          kn = sk[l * KU + ((u + 1 + l) % KU)];
+          kn = sk[lr * (KU + 1) + u + 1];
 #pragma unroll
           for (int r = 0; r < kHg; r++)
 #pragma unroll
-            for (int i = 0; i < kQu; i++) qn[r][i] = sq[(g0 + r) * HD + (u + 1) * kQu + i];
+            for (int i = 0; i < kQu; i++) qn[r][i] = sq[(hb + g0 + r) * HD + (u + 1) * kQu + i];
         }
 #pragma unroll
         for (int c = 0; c < 4; c++) {
@@ -599,13 +607,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((kF16 ? DPL 
             const float k1 = lt_h2f((uint16_t)(a[c] >> 16));
 #pragma unroll
             for (int r = 0; r < kHg; r++) {
-              acc[g0 + r] = fmaf(qc[r][2 * c], k0, acc[g0 + r]);
-              acc[g0 + r] = fmaf(qc[r][2 * c + 1], k1, acc[g0 + r]);
+              acc[r] = fmaf(qc[r][2 * c], k0, acc[r]);
+              acc[r] = fmaf(qc[r][2 * c + 1], k1, acc[r]);
             }
           } else {
             const float k0 = __builtin_bit_cast(float, a[c]);
 #pragma unroll
-            for (int r = 0; r < kHg; r++) acc[g0 + r] = fmaf(qc[r][c], k0, acc[g0 + r]);
+            for (int r = 0; r < kHg; r++) acc[r] = fmaf(qc[r][c], k0, acc[r]);
           }
         }
 #pragma unroll
@@ -614,25 +622,25 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((kF16 ? DPL 
           for (int i = 0; i < kQu; i++) qc[r][i] = qn[r][i];
         kc = kn;
       }
-    }
-    // stored unconditionally (lanes past the range write the spare row per_max), so the
-    // chains are computed in place rather than sunk into per-head branches
-    const bool in = t < n;
-    const int ts = in ? t : A.per_max;
 #pragma unroll
-    for (int r = 0; r < HPW; r++) {
-      const float s = acc[r] * A.scale;
-      se[ts * HPW + r] = s;
-      m[r] = fmaxf(m[r], in ? s : -1e30f);
+      for (int r = 0; r < kHg; r++) se[ts * HPW + hb + g0 + r] = acc[r] * A.scale;
     }
-  }
+  };
+  for (int t0 = 0; t0 < n; t0 += kPR) score_round(t0, kb);
   // @phase attn 2
   // the first kVRing V rows go out now, under the softmax
   uint32_t v[kVRing][VD];
 #pragma unroll
   for (int k = 0; k < kVRing; k++) load_v(k, v[k]);
-  // max, exps and Z
-  float zs[HPW];
+  // max (order-free: from the stored scores), exps and Z
+  __syncthreads();
+  float m[HPW], zs[HPW];
+#pragma unroll
+  for (int r = 0; r < HPW; r++) m[r] = -1e30f;
+  for (int t = l; t < n; t += 64) {
+#pragma unroll
+    for (int r = 0; r < HPW; r++) m[r] = fmaxf(m[r], se[t * HPW + r]);
+  }
 #pragma unroll
   for (int r = 0; r < HPW; r++) {
     m[r] = wave_max(m[r]);
@@ -870,7 +878,8 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
     const int dpl = A.hd / 64;
     const int per_max = (A.maxt + A.nsplit - 1) / A.nsplit;
     const size_t ku = (size_t)A.hd * (f16 ? 2 : 4) / 16;
-    const size_t shm = ((size_t)h * A.hd + 64 * ku * 4 + (size_t)(per_max + 2) * h) * sizeof(float);
+    const size_t kpr = h >= 2 ? 32 : 64;              // positions per score round
+    const size_t shm = ((size_t)h * A.hd + kpr * (ku + 1) * 4 + (size_t)(per_max + 2) * h) * sizeof(float);
     // fp16: 128 or 256 dims; fp32: 64 or 128 (a K row of at most 32 16-byte units)
     if (A.hd % 64 == 0 && (f16 ? (dpl == 2 || dpl == 4) : (dpl == 1 || dpl == 2)) && shm <= 64 * 1024) {
       A.per_max = per_max;
