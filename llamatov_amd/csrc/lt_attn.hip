@@ -455,65 +455,111 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
   // @phase attn 6
 }
 
-// Batched decode over long caches: one wave per workgroup, (split, HPW heads of one KV
-// group, sequence).  The same per-split arithmetic as k_attn, laid out so nothing waits on
-// a barrier or on LDS-staged V:
-//   scores   lane l takes positions l, l+64, ... of the split, HPW sequential fma chains
-//            over i, times scale, into LDS position-major [t][HPW];
-//   max      per head over the lanes (fmax, order-free);
-//   Z        lane l folds e_t over its own positions in ascending order, then the 64-lane
-//            tree (the frozen strided order);
+// Single-wave attention for batched decode (AM_DECODE) and for the decode step (AM_STEP:
+// RoPE of q and the new k, the KV append and the quantized output fused in, as k_attn
+// does): one wave per workgroup, (split, HPW heads of one KV group, sequence).  The same
+// per-split arithmetic as k_attn, laid out so nothing waits on a barrier or on LDS-staged V:
+//   scores   one lane per position (K row from LDS), the heads' sequential fma chains over
+//            i, times scale, into LDS position-major [t][HPW];
+//   max      per head over the split (fmax, order-free);
+//   Z        lane l folds e_t over its positions l, l+64, ... in ascending order, then the
+//            64-lane tree (the frozen strided order);
 //   O        lane l owns dims [l*DPL, l*DPL + DPL) of every head: HPW*DPL sequential fma
 //            chains over t ascending, reading V rows straight from HBM (a wave reads one
 //            whole row per load) and the HPW exps of row t by one broadcast LDS read.
-// Loads run as rings: each K unit and each V row slot is refilled with the next round's
-// data as soon as it is consumed, so a wave keeps a round of K and kVRing rows of V in
-// flight without a second register buffer.  Every load is unconditional (past the range
-// the buffer offset reads zeros) and tails are masked by selects, so waits stay partial.
-// Every K/V row is read once per KV group.  Bit-identical to k_attn's AM_DECODE results.
-constexpr int kVRingDw = 32;   // V dwords in flight per lane (rows = kVRingDw / VD)
+// In a step the new position's K and V rows come from the RoPE'd registers (rounded
+// through the cache's type): they replace the loaded rows in the LDS K round and in the V
+// ring, so no workgroup depends on another's append.
+// Loads run as rings: each V row slot is refilled with the next row as soon as it is
+// consumed, and a K round is in flight while the previous one is scored.  Every load is
+// unconditional (past the range a buffer offset reads zeros, or the row is clamped) and
+// tails are masked by selects, so waits stay partial.  Every K/V row is read once per KV
+// group.  Bit-identical to k_attn's results.
+constexpr int kVRingDw = 32;   // V dwords in flight per lane
 
-template <bool kF16, int HPW, int DPL>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((kF16 ? DPL * 8 : DPL * 16) <= 16 ? 3 : 1))) void k_attn_w1(AttnArgs A) {
+template <bool kF16, int HPW, int DPL, int MODE>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(MODE != AM_STEP && (kF16 ? DPL * 8 : DPL * 16) <= 16 ? 3 : 1))) void k_attn_w1(AttnArgs A) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
+  constexpr bool kStep = MODE == AM_STEP;
   constexpr int HD = 64 * DPL;
   constexpr int kEb = kF16 ? 2 : 4;                 // bytes per cache element
   constexpr int KU = HD * kEb / 16;                 // 16-byte units per K row
-  constexpr int VD = DPL * kEb / 4;                 // V dwords per lane per row (1, 2 or 4)
+  constexpr int kVB = DPL * kEb;                    // V bytes per lane per row (2 .. 16)
+  constexpr int VD = kVB < 4 ? 1 : kVB / 4;         // registers per V row
   constexpr int OPL = DPL;                          // outputs per lane per head
   constexpr int kVRing = kVRingDw / VD;             // V rows in flight
-  static_assert(VD >= 1 && KU <= 32, "k_attn_w1: unsupported head size / cache type");
-  float* sq = lds;                                  // [HPW][HD]
+  constexpr int kEg = 8;                            // exps read per group in the O loop
+  const int per_up = (A.per_max + kVRing - 1) / kVRing * kVRing;   // per_max rounded to whole rings
+  const int srow = per_up + kEg;                    // the spare score row
+  constexpr int kPR = HPW >= 2 ? 32 : 64;           // positions per score round
+  static_assert(KU >= 8 && KU <= 32, "k_attn_w1: unsupported head size / cache type");
+  float* sq = lds;                                  // [HPW][HD] q (roped in a step); then the outputs
   u32x4* sk = (u32x4*)(lds + HPW * HD);             // [kPR][KU + 1] one round of K rows, padded
-  float* se = lds + HPW * HD + (HPW >= 2 ? 32 : 64) * (KU + 1) * 4;   // [per_max + 2][HPW]: rows, spare, zeros
+  u32x4* sfk = sk + kPR * (KU + 1);                 // step: the new K row, then the new V row (cache format)
+  float* se = (float*)(sfk + (kStep ? 2 * KU : 0)); // [per_up + kEg + 1][HPW]: rows (zero past n), spare
   const int l = threadIdx.x;
   const int sp = blockIdx.x;
   const int h0 = blockIdx.y * HPW;
   const int b = blockIdx.z;
-  const int g = h0 / (A.nh / A.nkv);
+  const int rep = A.nh / A.nkv;
+  const int g = h0 / rep;
   const int kvrow = A.nkv * HD;                     // elements per cache position
 
-  const int L = A.len[b];
-  const int nctx = L < 0 ? 0 : (L > A.maxt ? A.maxt : L);
+  // the step's length first, then the new token's inputs: waiting for the length (which
+  // places the cache reads) does not wait for the inputs, and waiting for the inputs
+  // never waits for cache rows
+  const int len0 = kStep ? *A.len : A.len[b];
+  constexpr int kHalf = HD / 2;
+  constexpr int kRopeIt = ((HPW + 1) * kHalf + 63) / 64;
+  float rx1[kRopeIt], rx2[kRopeIt], rfr[kRopeIt], rv[DPL];
+  if (kStep) {
+#pragma unroll
+    for (int it = 0; it < kRopeIt; it++) {
+      const int i0 = l + 64 * it < (HPW + 1) * kHalf ? l + 64 * it : 0;
+      const int r = i0 / kHalf, j = i0 - r * kHalf;
+      const float* src = r < HPW ? A.qkv + (size_t)(h0 + r) * HD : A.qkv + (size_t)A.nh * HD + (size_t)g * HD;
+      rx1[it] = src[j];
+      rx2[it] = src[j + kHalf];
+      rfr[it] = A.freqs[j];
+    }
+#pragma unroll
+    for (int k = 0; k < DPL; k++) rv[k] = A.qkv[(size_t)A.nh * HD + kvrow + (size_t)g * HD + l + 64 * k];
+  }
+
+  int Lnew = -1, nctx;
+  bool valid = true;
+  if (kStep) {
+    Lnew = len0;
+    valid = Lnew >= 0 && Lnew < A.maxt;
+    nctx = valid ? Lnew + 1 : 0;
+  } else {
+    nctx = len0 < 0 ? 0 : (len0 > A.maxt ? A.maxt : len0);
+  }
   const int per = (nctx + A.nsplit - 1) / A.nsplit;
   const int p0 = sp * per;
   const int p1 = p0 + per < nctx ? p0 + per : nctx;
   const int n = p1 > p0 ? p1 - p0 : 0;
+  const int tnew = kStep ? Lnew - p0 : -1;          // the new position within this split (if 0 <= tnew < n)
   const uint32_t rows = (uint32_t)gridDim.z * (uint32_t)A.maxt;
   const __amdgpu_buffer_rsrc_t krsrc =
       __builtin_amdgcn_make_buffer_rsrc(A.kc, 0, (int)(rows * (uint32_t)kvrow * kEb), 0x00020000);
-  const __amdgpu_buffer_rsrc_t vrsrc =
-      __builtin_amdgcn_make_buffer_rsrc(A.vc, 0, (int)(rows * (uint32_t)kvrow * kEb), 0x00020000);
   // byte offset of (position p0 of this split, head group g) and the row pitch
   const uint32_t base = ((uint32_t)b * (uint32_t)A.maxt + (uint32_t)p0) * (uint32_t)kvrow * kEb + (uint32_t)g * HD * kEb;
   const uint32_t pitch = (uint32_t)kvrow * kEb;
+  // The V rows read from the cache are the split's first nv rows (a step's new row, the
+  // split's last, is folded from registers): a buffer that ends right after them makes
+  // every later row read zeros with no per-row test.
+  const int nv = kStep && n > 0 && tnew == n - 1 ? n - 1 : n;
+  const __amdgpu_buffer_rsrc_t vrsrc =
+      __builtin_amdgcn_make_buffer_rsrc(A.vc, 0, (int)(base + (uint32_t)nv * pitch), 0x00020000);
 
-  auto v_off = [&](int t) { return t < n ? (int)(base + (uint32_t)t * pitch + (uint32_t)l * VD * 4) : (int)kNoRow; };
   auto load_v = [&](int t, uint32_t* dst) {
-    const int off = v_off(t);
-    if (VD == 1) {
+    const int off = (int)(base + (uint32_t)t * pitch + (uint32_t)l * kVB);
+    if (kVB == 2) {
+      dst[0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(vrsrc, off, 0, 0);
+    } else if (kVB == 4) {
       dst[0] = __builtin_amdgcn_raw_buffer_load_b32(vrsrc, off, 0, 0);
-    } else if (VD == 2) {
+    } else if (kVB == 8) {
       const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(vrsrc, off, 0, 0);
       dst[0] = w.x; dst[1] = w.y;
     } else {
@@ -530,7 +576,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((kF16 ? DPL 
   // i*(64/KU) + l/KU, unit l%KU (whole rows per instruction); they pass through LDS rows
   // padded by one 16-byte unit, so the lane-per-row reads below (lanes 4 banks apart) are
   // bank-conflict free and every LDS address is a base plus an immediate.
-  constexpr int kPR = HPW >= 2 ? 32 : 64;           // positions per round
   constexpr int kHL = HPW >= 2 ? HPW / 2 : 1;       // heads per lane
   constexpr int kRpi = 64 / KU;                     // rows per load instruction
   constexpr int kNI = kPR * KU / 64;                // load instructions per round
@@ -550,23 +595,77 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((kF16 ? DPL 
       off += kRpi * pitch;
     }
   };
-  // the first K round: in flight before anything else
+  // the first K round: in flight before anything else (a step: and the V ring)
   load_round(0, kb);
-  {
+  uint32_t v[kVRing][VD];
+  if (kStep) {
+#pragma unroll
+    for (int k = 0; k < kVRing; k++) load_v(k, v[k]);
+  }
+  uint32_t fv[VD];                                  // step: this lane's part of the new V row
+  if (kStep) {
+    // RoPE (the arithmetic of k_rope, rope_from_facts.pl:40-69) of the q heads and the
+    // group's k; k and v rounded through the cache's type
+    const float pos = (float)(valid ? Lnew : 0);
+#pragma unroll
+    for (int it = 0; it < kRopeIt; it++) {
+      const int i = l + 64 * it;
+      if (i < (HPW + 1) * kHalf) {
+        const int r = i / kHalf, j = i - r * kHalf;
+        float sn, cs;
+        lt_sincosf(pos * rfr[it], &sn, &cs);
+        const float o1 = fmaf(rx1[it], cs, -(rx2[it] * sn));
+        const float o2 = fmaf(rx1[it], sn, rx2[it] * cs);
+        if (r < HPW) {
+          sq[r * HD + j] = o1;
+          sq[r * HD + j + kHalf] = o2;
+        } else if (kF16) {
+          ((uint16_t*)sfk)[j] = lt_float_to_half_bits(o1);
+          ((uint16_t*)sfk)[j + kHalf] = lt_float_to_half_bits(o2);
+        } else {
+          ((float*)sfk)[j] = o1;
+          ((float*)sfk)[j + kHalf] = o2;
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < DPL; k++) {
+      if (kF16) ((uint16_t*)(sfk + KU))[l + 64 * k] = lt_float_to_half_bits(rv[k]);
+      else ((float*)(sfk + KU))[l + 64 * k] = rv[k];
+    }
+  } else {
     const float* qs = A.q + (size_t)b * A.q_stride + (size_t)h0 * HD;
 #pragma unroll
     for (int k = 0; k < HPW * DPL; k++) sq[l + 64 * k] = qs[l + 64 * k];
-    if (l < HPW) se[(A.per_max + 1) * HPW + l] = 0.0f;   // the zero row
   }
   __syncthreads();
+  if (kStep) {
+    // this lane's dims of the new V row, in the V ring's register format
+    const uint32_t* fvr = (const uint32_t*)(sfk + KU);
+    if (kVB == 2) fv[0] = ((const uint16_t*)(sfk + KU))[l];
+    else {
+#pragma unroll
+      for (int w = 0; w < VD; w++) fv[w] = fvr[l * VD + w];
+    }
+    if (valid && sp == 0 && h0 % rep == 0 && l < KU) {
+      // the new row into the cache (k_append_kv_incr, dev_residency.py:303-315)
+      const size_t off = ((size_t)Lnew * kvrow + (size_t)g * HD) * kEb;
+      *(u32x4*)((char*)A.kc + off + l * 16) = sfk[l];
+      *(u32x4*)((char*)A.vc + off + l * 16) = sfk[KU + l];
+    }
+  }
 
   // @phase attn 1
   auto score_round = [&](int t0, u32x4* buf) {
     // this round's rows into LDS (the previous round's reads were issued before these
-    // writes, and one wave's LDS operations complete in order), then the next round's
-    // loads into the same registers
+    // writes, and one wave's LDS operations complete in order), the new row over its
+    // loaded copy, then the next round's loads into the same registers
 #pragma unroll
     for (int i = 0; i < kNI; i++) sk[(i * kRpi + kl_row) * (KU + 1) + kl_unit] = buf[i];
+    if (kStep) {
+      const int tr = tnew - t0;
+      if (tr >= 0 && tr < kPR && l < KU) sk[tr * (KU + 1) + l] = sfk[l];
+    }
     asm volatile("" ::: "memory");
     load_round(t0 + kPR, buf);
     // passes of kHg heads over this lane's K row in LDS; within a pass, K unit u and q of
@@ -574,10 +673,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((kF16 ? DPL 
     // the compiler from hoisting more
     constexpr int kHg = kHL < 2 ? kHL : 2;
     constexpr int kQu = kF16 ? 8 : 4;
-    // stored unconditionally (lanes past the range write the spare row per_max), so the
+    // stored unconditionally (lanes past the range write the spare row), so the
     // chains are computed in place rather than sunk into branches
     const int t = t0 + lr;
-    const int ts = t < n ? t : A.per_max;
+    const int ts = t < n ? t : srow;
 #pragma unroll
     for (int g0 = 0; g0 < kHL; g0 += kHg) {
       float acc[kHg];
@@ -628,10 +727,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((kF16 ? DPL 
   };
   for (int t0 = 0; t0 < n; t0 += kPR) score_round(t0, kb);
   // @phase attn 2
-  // the first kVRing V rows go out now, under the softmax
-  uint32_t v[kVRing][VD];
+  // batched decode: the first kVRing V rows go out now, under the softmax
+  if (!kStep) {
 #pragma unroll
-  for (int k = 0; k < kVRing; k++) load_v(k, v[k]);
+    for (int k = 0; k < kVRing; k++) load_v(k, v[k]);
+  }
   // max (order-free: from the stored scores), exps and Z
   __syncthreads();
   float m[HPW], zs[HPW];
@@ -656,6 +756,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((kF16 ? DPL 
   }
 #pragma unroll
   for (int r = 0; r < HPW; r++) zs[r] = wave_tree_dpp(zs[r]);   // lane 0: Z of head r
+  // exps of 0 up to the O loop's last ring (those rows read zeros from V)
+  {
+    const int n_up = (n + kVRing - 1) / kVRing * kVRing;
+    for (int i = n * HPW + l; i < n_up * HPW; i += 64) se[i] = 0.0f;
+  }
   __syncthreads();
 
   // @phase attn 3
@@ -667,22 +772,21 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((kF16 ? DPL 
   for (int r = 0; r < HPW; r++)
 #pragma unroll
     for (int k = 0; k < OPL; k++) o[r][k] = 0.0f;
-  for (int t0 = 0; t0 < n; t0 += kVRing) {
+  // The exps of a group of kEg rows are read one group ahead (the per-row fence below keeps
+  // the ring in registers and would otherwise make every row wait for its LDS read).
+  static_assert(kVRing % kEg == 0, "k_attn_w1: ring of whole exp groups");
+  auto read_e = [&](int t, float (*dst)[HPW]) {
 #pragma unroll
-    for (int k = 0; k < kVRing; k++) {
-      const int t = t0 + k;
-      const int ti = t < n ? t : A.per_max + 1;   // past the range: the zero row
-      uint32_t x[VD];
+    for (int j = 0; j < kEg; j++)
 #pragma unroll
-      for (int w = 0; w < VD; w++) x[w] = v[k][w];
-      // row t is consumed here: its exps are read and its slot refilled no earlier
-      if (VD == 1) asm volatile("" : "+v"(x[0]) : : "memory");
-      else if (VD == 2) asm volatile("" : "+v"(x[0]), "+v"(x[1]) : : "memory");
-      else asm volatile("" : "+v"(x[0]), "+v"(x[1]), "+v"(x[VD > 2 ? 2 : 0]), "+v"(x[VD > 3 ? 3 : 0]) : : "memory");
-      float e[HPW];
+      for (int r = 0; r < HPW; r++) dst[j][r] = se[(t + j) * HPW + r];
+  };
+  auto fold_row = [&](const float* e, const uint32_t* x) {
+    if (kF16 && kVB == 2) {
+      const float x0 = lt_h2f((uint16_t)(x[0] & 0xFFFFu));
 #pragma unroll
-      for (int r = 0; r < HPW; r++) e[r] = se[ti * HPW + r];
-      load_v(t + kVRing, v[k]);
+      for (int r = 0; r < HPW; r++) o[r][0] = fmaf(e[r], x0, o[r][0]);
+    } else {
 #pragma unroll
       for (int w = 0; w < VD; w++) {
         if (kF16) {
@@ -699,6 +803,38 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((kF16 ? DPL 
         }
       }
     }
+  };
+  float ec[kEg][HPW], en[kEg][HPW];
+  read_e(0, ec);
+  for (int t0 = 0; t0 < n; t0 += kVRing) {
+#pragma unroll
+    for (int k0 = 0; k0 < kVRing; k0 += kEg) {
+      read_e(t0 + k0 + kEg, en);
+#pragma unroll
+      for (int j = 0; j < kEg; j++) {
+        const int k = k0 + j;
+        uint32_t x[VD];
+#pragma unroll
+        for (int w = 0; w < VD; w++) x[w] = v[k][w];
+        // row t0+k is consumed here: its slot is refilled no earlier
+        if (VD == 1) asm volatile("" : "+v"(x[0]) : : "memory");
+        else if (VD == 2) asm volatile("" : "+v"(x[0]), "+v"(x[1]) : : "memory");
+        else asm volatile("" : "+v"(x[0]), "+v"(x[1]), "+v"(x[VD > 2 ? 2 : 0]), "+v"(x[VD > 3 ? 3 : 0]) : : "memory");
+        load_v(t0 + k + kVRing, v[k]);
+        fold_row(ec[j], x);
+      }
+#pragma unroll
+      for (int j = 0; j < kEg; j++)
+#pragma unroll
+        for (int r = 0; r < HPW; r++) ec[j][r] = en[j][r];
+    }
+  }
+  if (kStep && nv < n) {
+    // the new row, last in its split
+    float e[HPW];
+#pragma unroll
+    for (int r = 0; r < HPW; r++) e[r] = se[(n - 1) * HPW + r];
+    fold_row(e, fv);
   }
 
   // @phase attn 4
@@ -709,7 +845,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((kF16 ? DPL 
     for (int r = 0; r < HPW; r++) {
       const float z = __shfl(zs[r], 0, 64);
 #pragma unroll
-      for (int k = 0; k < OPL; k++) A.out[(hrow0 + r) * HD + l * OPL + k] = o[r][k] / z;
+      for (int k = 0; k < OPL; k++) {
+        const float val = valid ? o[r][k] / z : 0.0f;
+        if (A.out) A.out[(hrow0 + r) * HD + l * OPL + k] = val;
+        if (kStep) sq[r * HD + l * OPL + k] = val;
+      }
+    }
+    if (kStep && A.oq) {
+      // the workgroup's heads are whole 32-element blocks of the attention vector: quantize
+      // them for the O projection (k_quant_q8's quantizer)
+      __syncthreads();
+      const int lane = l & 31;
+      const size_t o0 = (size_t)h0 * HD;
+      for (int qb = l >> 5; qb < HPW * HD / 32; qb += 2)
+        quant_block_hw(sq[qb * 32 + lane], lane, A.oq + o0 + qb * 32, A.od + (o0 >> 5) + qb);
     }
   } else {
 #pragma unroll
@@ -828,16 +977,14 @@ void launch_merge(dim3 grid, hipStream_t st, const float* wsm, const float* wsz,
     k_attn_merge<128><<<grid, 256, 0, st>>>(wsm, wsz, wso, len, maxt, out, oq, od, nh, hd, nsplit);
 }
 
-template <bool kF16>
+template <bool kF16, int MODE>
 hipError_t launch_w1(int hpw, int dpl, dim3 grid, size_t shm, hipStream_t st, const AttnArgs& A) {
 #define LT_W1_CASE(H, D)                                            \
   if (hpw == H && dpl == D) {                                       \
-    k_attn_w1<kF16, H, D><<<grid, 64, shm, st>>>(A);                \
+    k_attn_w1<kF16, H, D, MODE><<<grid, 64, shm, st>>>(A);          \
     return hipGetLastError();                                       \
   }
-  if constexpr (!kF16) {
-    LT_W1_CASE(1, 1) LT_W1_CASE(2, 1) LT_W1_CASE(4, 1) LT_W1_CASE(8, 1)
-  }
+  LT_W1_CASE(1, 1) LT_W1_CASE(2, 1) LT_W1_CASE(4, 1) LT_W1_CASE(8, 1)
   LT_W1_CASE(1, 2) LT_W1_CASE(2, 2) LT_W1_CASE(4, 2) LT_W1_CASE(8, 2)
   if constexpr (kF16) {
     LT_W1_CASE(1, 4) LT_W1_CASE(2, 4) LT_W1_CASE(4, 4) LT_W1_CASE(8, 4)
@@ -846,7 +993,8 @@ hipError_t launch_w1(int hpw, int dpl, dim3 grid, size_t shm, hipStream_t st, co
   return hipErrorInvalidValue;
 }
 
-// LT_ATTN_W1=0 keeps batched decode on k_attn (for comparisons); the default is k_attn_w1.
+// LT_ATTN_W1=0 keeps decode and the decode step on k_attn (for comparisons); the default is
+// k_attn_w1 wherever its head sizes apply.
 bool use_w1() {
   static const bool on = [] {
     const char* s = getenv("LT_ATTN_W1");
@@ -871,7 +1019,7 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
     A.wsz = w.z;
     A.wso = w.o;
   }
-  if (mode == AM_DECODE && use_w1()) {
+  if ((mode == AM_DECODE || mode == AM_STEP) && use_w1()) {
     // the single-wave kernel: all heads of a KV group share its K/V reads
     const int rep = A.nh / A.nkv;
     const int h = rep % 8 == 0 ? 8 : rep % 4 == 0 ? 4 : rep % 2 == 0 ? 2 : 1;
@@ -879,17 +1027,27 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
     const int per_max = (A.maxt + A.nsplit - 1) / A.nsplit;
     const size_t ku = (size_t)A.hd * (f16 ? 2 : 4) / 16;
     const size_t kpr = h >= 2 ? 32 : 64;              // positions per score round
-    const size_t shm = ((size_t)h * A.hd + kpr * (ku + 1) * 4 + (size_t)(per_max + 2) * h) * sizeof(float);
-    // fp16: 128 or 256 dims; fp32: 64 or 128 (a K row of at most 32 16-byte units)
-    if (A.hd % 64 == 0 && (f16 ? (dpl == 2 || dpl == 4) : (dpl == 1 || dpl == 2)) && shm <= 64 * 1024) {
+    const int vb = dpl * (f16 ? 2 : 4);               // V bytes per lane per row
+    const int ring = kVRingDw / (vb < 4 ? 1 : vb / 4);  // V rows in flight
+    const size_t per_up = (size_t)(per_max + ring - 1) / ring * ring;
+    const size_t shm = ((size_t)h * A.hd + (kpr * (ku + 1) + (mode == AM_STEP ? 2 * ku : 0)) * 4 +
+                        (per_up + 8 + 1) * h) * sizeof(float);
+    // fp16: 64, 128 or 256 dims; fp32: 64 or 128 (a K row of 8 to 32 16-byte units)
+    if (A.hd % 64 == 0 && (f16 ? (dpl == 1 || dpl == 2 || dpl == 4) : (dpl == 1 || dpl == 2)) &&
+        shm <= 64 * 1024) {
       A.per_max = per_max;
       const dim3 grid(A.nsplit, A.nh / h, rows);
-      hipError_t e = f16 ? launch_w1<true>(h, dpl, grid, shm, ctx->stream, A)
-                         : launch_w1<false>(h, dpl, grid, shm, ctx->stream, A);
+      hipError_t e;
+      if (mode == AM_STEP)
+        e = f16 ? launch_w1<true, AM_STEP>(h, dpl, grid, shm, ctx->stream, A)
+                : launch_w1<false, AM_STEP>(h, dpl, grid, shm, ctx->stream, A);
+      else
+        e = f16 ? launch_w1<true, AM_DECODE>(h, dpl, grid, shm, ctx->stream, A)
+                : launch_w1<false, AM_DECODE>(h, dpl, grid, shm, ctx->stream, A);
       if (e != hipSuccess) return lt_fail_hip(e, what, __FILE__, __LINE__);
       if (A.nsplit > 1) {
-        launch_merge(dim3(A.nh, rows), ctx->stream, A.wsm, A.wsz, A.wso, nullptr, A.maxt, A.out, nullptr, nullptr,
-                     A.nh, A.hd, A.nsplit);
+        launch_merge(dim3(A.nh, rows), ctx->stream, A.wsm, A.wsz, A.wso, mode == AM_STEP ? A.len : nullptr, A.maxt,
+                     A.out, A.oq, A.od, A.nh, A.hd, A.nsplit);
         return lt_check_launch("k_attn_merge");
       }
       return lt_check_launch("k_attn_w1");
