@@ -27,6 +27,7 @@
 // the range is a buffer load (out-of-range offsets read zeros), so loads never sit
 // behind branches.
 #include <cstdlib>
+#include <type_traits>
 
 #include "lt_q8_device.h"
 
@@ -475,7 +476,8 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
 // unconditional (past the range a buffer offset reads zeros, or the row is clamped) and
 // tails are masked by selects, so waits stay partial.  Every K/V row is read once per KV
 // group.  Bit-identical to k_attn's results.
-constexpr int kVRingDw = 32;   // V dwords in flight per lane
+constexpr int kVRingDw = 32;       // V dwords in flight per lane, batched decode (many waves)
+constexpr int kVRingDwStep = 56;   // the decode step (few waves): a deep ring (under the 63 loads a wave can count), issued before the scores
 
 template <bool kF16, int HPW, int DPL, int MODE>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(MODE != AM_STEP && (kF16 ? DPL * 8 : DPL * 16) <= 16 ? 3 : 1))) void k_attn_w1(AttnArgs A) {
@@ -487,8 +489,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(MODE != AM_S
   constexpr int kVB = DPL * kEb;                    // V bytes per lane per row (2 .. 16)
   constexpr int VD = kVB < 4 ? 1 : kVB / 4;         // registers per V row
   constexpr int OPL = DPL;                          // outputs per lane per head
-  constexpr int kVRing = kVRingDw / VD;             // V rows in flight
   constexpr int kEg = 8;                            // exps read per group in the O loop
+  constexpr int kVRing = (kStep ? kVRingDwStep : kVRingDw) / VD / kEg * kEg;   // V rows in flight
   const int per_up = (A.per_max + kVRing - 1) / kVRing * kVRing;   // per_max rounded to whole rings
   const int srow = per_up + kEg;                    // the spare score row
   constexpr int kPR = HPW >= 2 ? 32 : 64;           // positions per score round
@@ -553,11 +555,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(MODE != AM_S
   const __amdgpu_buffer_rsrc_t vrsrc =
       __builtin_amdgcn_make_buffer_rsrc(A.vc, 0, (int)(base + (uint32_t)nv * pitch), 0x00020000);
 
+  // 2 bytes per lane (fp16, 64 dims): lanes 2i and 2i+1 load the same dword of the row and
+  // take its low / high half
   auto load_v = [&](int t, uint32_t* dst) {
-    const int off = (int)(base + (uint32_t)t * pitch + (uint32_t)l * kVB);
-    if (kVB == 2) {
-      dst[0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(vrsrc, off, 0, 0);
-    } else if (kVB == 4) {
+    const int off = (int)(base + (uint32_t)t * pitch + (kVB == 2 ? (uint32_t)(l >> 1) * 4 : (uint32_t)l * kVB));
+    if (kVB == 2 || kVB == 4) {
       dst[0] = __builtin_amdgcn_raw_buffer_load_b32(vrsrc, off, 0, 0);
     } else if (kVB == 8) {
       const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(vrsrc, off, 0, 0);
@@ -595,13 +597,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(MODE != AM_S
       off += kRpi * pitch;
     }
   };
-  // the first K round: in flight before anything else (a step: and the V ring)
-  load_round(0, kb);
+  // a step's V ring, then the first K round: in flight before anything else (the ring's
+  // loads are the oldest, so waiting for a ring row never waits for K)
+  // (the fences keep the ring's loads in the order its rows are consumed, so each row
+  // waits for its own load only)
   uint32_t v[kVRing][VD];
   if (kStep) {
 #pragma unroll
-    for (int k = 0; k < kVRing; k++) load_v(k, v[k]);
+    for (int k = 0; k < kVRing; k++) {
+      load_v(k, v[k]);
+      asm volatile("" ::: "memory");
+    }
   }
+  load_round(0, kb);
   uint32_t fv[VD];                                  // step: this lane's part of the new V row
   if (kStep) {
     // RoPE (the arithmetic of k_rope, rope_from_facts.pl:40-69) of the q heads and the
@@ -642,7 +650,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(MODE != AM_S
   if (kStep) {
     // this lane's dims of the new V row, in the V ring's register format
     const uint32_t* fvr = (const uint32_t*)(sfk + KU);
-    if (kVB == 2) fv[0] = ((const uint16_t*)(sfk + KU))[l];
+    if (kVB == 2) fv[0] = fvr[l >> 1];
     else {
 #pragma unroll
       for (int w = 0; w < VD; w++) fv[w] = fvr[l * VD + w];
@@ -656,7 +664,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(MODE != AM_S
   }
 
   // @phase attn 1
-  auto score_round = [&](int t0, u32x4* buf) {
+  auto score_round = [&](int t0, u32x4* buf, auto prefetch) {
     // this round's rows into LDS (the previous round's reads were issued before these
     // writes, and one wave's LDS operations complete in order), the new row over its
     // loaded copy, then the next round's loads into the same registers
@@ -667,7 +675,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(MODE != AM_S
       if (tr >= 0 && tr < kPR && l < KU) sk[tr * (KU + 1) + l] = sfk[l];
     }
     asm volatile("" ::: "memory");
-    load_round(t0 + kPR, buf);
+    if constexpr (decltype(prefetch)::value) load_round(t0 + kPR, buf);
     // passes of kHg heads over this lane's K row in LDS; within a pass, K unit u and q of
     // unit u (kQu dims per head) are read one unit ahead of their use, and the fence keeps
     // the compiler from hoisting more
@@ -725,12 +733,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(MODE != AM_S
       for (int r = 0; r < kHg; r++) se[ts * HPW + hb + g0 + r] = acc[r] * A.scale;
     }
   };
-  for (int t0 = 0; t0 < n; t0 += kPR) score_round(t0, kb);
+  // the last round loads nothing ahead: loads still pending when the O loop reuses their
+  // registers would make it wait for them
+  int t0s = 0;
+  for (; t0s + kPR < n; t0s += kPR) score_round(t0s, kb, std::true_type{});
+  if (n > 0) score_round(t0s, kb, std::false_type{});
   // @phase attn 2
   // batched decode: the first kVRing V rows go out now, under the softmax
   if (!kStep) {
 #pragma unroll
-    for (int k = 0; k < kVRing; k++) load_v(k, v[k]);
+    for (int k = 0; k < kVRing; k++) {
+      load_v(k, v[k]);
+      asm volatile("" ::: "memory");
+    }
   }
   // max (order-free: from the stored scores), exps and Z
   __syncthreads();
@@ -783,7 +798,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(MODE != AM_S
   };
   auto fold_row = [&](const float* e, const uint32_t* x) {
     if (kF16 && kVB == 2) {
-      const float x0 = lt_h2f((uint16_t)(x[0] & 0xFFFFu));
+      const float x0 = lt_h2f((uint16_t)(l & 1 ? x[0] >> 16 : x[0] & 0xFFFFu));
 #pragma unroll
       for (int r = 0; r < HPW; r++) o[r][0] = fmaf(e[r], x0, o[r][0]);
     } else {
@@ -816,12 +831,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(MODE != AM_S
         uint32_t x[VD];
 #pragma unroll
         for (int w = 0; w < VD; w++) x[w] = v[k][w];
-        // row t0+k is consumed here: its slot is refilled no earlier
+        // row t0+k is consumed here
         if (VD == 1) asm volatile("" : "+v"(x[0]) : : "memory");
         else if (VD == 2) asm volatile("" : "+v"(x[0]), "+v"(x[1]) : : "memory");
         else asm volatile("" : "+v"(x[0]), "+v"(x[1]), "+v"(x[VD > 2 ? 2 : 0]), "+v"(x[VD > 3 ? 3 : 0]) : : "memory");
-        load_v(t0 + k + kVRing, v[k]);
+        // the refill after the fold: the fenced value is dead by then, so the new row can
+        // land in the same registers and the ring needs no copies at the loop's back edge
         fold_row(ec[j], x);
+        load_v(t0 + k + kVRing, v[k]);
       }
 #pragma unroll
       for (int j = 0; j < kEg; j++)
@@ -1028,7 +1045,7 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
     const size_t ku = (size_t)A.hd * (f16 ? 2 : 4) / 16;
     const size_t kpr = h >= 2 ? 32 : 64;              // positions per score round
     const int vb = dpl * (f16 ? 2 : 4);               // V bytes per lane per row
-    const int ring = kVRingDw / (vb < 4 ? 1 : vb / 4);  // V rows in flight
+    const int ring = (mode == AM_STEP ? kVRingDwStep : kVRingDw) / (vb < 4 ? 1 : vb / 4) / 8 * 8;   // V rows in flight
     const size_t per_up = (size_t)(per_max + ring - 1) / ring * ring;
     const size_t shm = ((size_t)h * A.hd + (kpr * (ku + 1) + (mode == AM_STEP ? 2 * ku : 0)) * 4 +
                         (per_up + 8 + 1) * h) * sizeof(float);
