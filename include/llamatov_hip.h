@@ -241,6 +241,24 @@ LT_API int lt_q8_gemm(lt_ctx* ctx, const void* W, const int8_t* Xq, const uint16
 LT_API int lt_q8_gemm_silu(lt_ctx* ctx, const void* Wgu, const int8_t* Xq, const uint16_t* Xd, float* V, int T,
                            int F, int K);
 
+/* The coalesced layouts of the prefill GEMM (no reference counterpart; same results):
+ * - the tile-major copy of a Q8_0 matrix W [N][K/32] (GGUF blocks): Wt[rt][b][r] is row
+ *   32*rt + r's block b, 34 bytes, rows past N zero; lt_q8_tiles_bytes(N, K) bytes, built on
+ *   the device by lt_q8_tiles (Wt 16-byte aligned);
+ * - block-major activation quants: lt_quant_q8_bm writes token t's block b of x [T][K] (the
+ *   lt_quant_q8 quantizer) to Xq[b][t][32] and Xd[b][t]. */
+LT_API size_t lt_q8_tiles_bytes(int N, int K);
+LT_API int lt_q8_tiles(lt_ctx* ctx, const void* W, void* Wt, int N, int K);
+LT_API int lt_quant_q8_bm(lt_ctx* ctx, const float* x, int8_t* xq, uint16_t* xd, int T, int K);
+
+/* lt_q8_gemm / lt_q8_gemm_silu on those layouts (Wt from lt_q8_tiles, Xq/Xd from
+ * lt_quant_q8_bm): every block's operands are contiguous runs, so each element is the same
+ * bits with far fewer cache lines touched per block.  The tile copy must be below 2 GiB. */
+LT_API int lt_q8_gemm_t(lt_ctx* ctx, const void* Wt, const int8_t* Xq, const uint16_t* Xd, const float* bias,
+                        const float* resid, float* Y, int T, int N, int K);
+LT_API int lt_q8_gemm_silu_t(lt_ctx* ctx, const void* Wgut, const int8_t* Xq, const uint16_t* Xd, float* V, int T,
+                             int F, int K);
+
 /* RoPE (lt_rope_qk's arithmetic) of T rows of q|k, row t at position *pos0 + t; rows are
  * row_stride floats apart and hold nheads contiguous heads of hd. */
 LT_API int lt_rope_batch(lt_ctx* ctx, float* qk, int T, int row_stride, const int* pos0, int nheads, int hd,

@@ -29,9 +29,9 @@ constexpr uint32_t kNoBlk = 0x80000000u;       // out-of-range buffer offset: re
 enum GemmEpi { GE_STORE = 0, GE_BIAS = 1, GE_RESID = 2, GE_SILU = 3 };
 
 struct GemmParams {
-  const uint8_t* W;      // Q8_0 blocks [N][K/32]
-  const int8_t* Xq;      // [T][K]
-  const uint16_t* Xd;    // [T][K/32] fp16 bits
+  const uint8_t* W;      // Q8_0 blocks [N][K/32]; tiled: [ceil(N/32)][K/32][32 rows][34 B]
+  const int8_t* Xq;      // [T][K]; tiled: block-major [K/32][T][32]
+  const uint16_t* Xd;    // [T][K/32] fp16 bits; tiled: [K/32][T]
   const float* bias;     // [N] (GE_BIAS)
   const float* resid;    // [T][N] (GE_RESID)
   float* Y;              // [T][N], or [T][N/2] for GE_SILU
@@ -44,7 +44,11 @@ struct GemmParams {
 // 16*(l/32) .. +16 of the block (the same half of k for A and B).
 __device__ __forceinline__ int c_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 
-template <GemmEpi EPI>
+// kTiled: the weights in the tile-major copy (a 32-row tile's block b is 1088 contiguous
+// bytes) and the activations block-major (block b of 32 consecutive tokens is 1 KB
+// contiguous), so both operands of a block are coalesced loads; the arithmetic and the
+// order are the same.
+template <GemmEpi EPI, bool kTiled>
 __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
   __shared__ float s_st4[kGemmWaves][16 * 64];   // tree level 4 of each wave's 32 x 32 tile
   const int wave = threadIdx.x >> 6;
@@ -62,10 +66,14 @@ __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
   const int t0 = tt * kGemmTokens + wave * 32;
   const int nb = P.K >> 5;
 
-  // A lane: weight row n0 + c (clamped; results of clamped rows are discarded)
+  // A lane: weight row n0 + c (clamped; results of clamped rows are discarded).  Block b of
+  // the lane's row starts at row_off + b * a_step.
   const int arow = n0 + c < P.N ? n0 + c : P.N - 1;
-  const uint32_t row_off = (uint32_t)arow * (uint32_t)nb * (uint32_t)kBlockBytes;
-  const uint32_t mat_bytes = (uint32_t)P.N * (uint32_t)nb * (uint32_t)kBlockBytes;
+  const uint32_t row_off = kTiled ? (uint32_t)rt * (uint32_t)nb * 32u * (uint32_t)kBlockBytes + (uint32_t)c * kBlockBytes
+                                  : (uint32_t)arow * (uint32_t)nb * (uint32_t)kBlockBytes;
+  const uint32_t a_step = kTiled ? 32u * kBlockBytes : (uint32_t)kBlockBytes;
+  const uint32_t mat_bytes = kTiled ? (uint32_t)P.nrt * (uint32_t)nb * 32u * (uint32_t)kBlockBytes
+                                    : (uint32_t)P.N * (uint32_t)nb * (uint32_t)kBlockBytes;
   // the 16 quant bytes of a block half begin 2 bytes into the block; the 5th dword can lie
   // past the matrix: buffer loads bound it (out-of-range dwords read as zero)
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)P.W, 0, (int)((mat_bytes + 3u) & ~3u), 0x00020000);
@@ -75,8 +83,16 @@ __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
       __builtin_amdgcn_make_buffer_rsrc((void*)P.Xq, 0, (int)((size_t)P.T * P.K), 0x00020000);
   const __amdgpu_buffer_rsrc_t xdr =
       __builtin_amdgcn_make_buffer_rsrc((void*)P.Xd, 0, (int)(((size_t)P.T * nb * 2 + 3) & ~(size_t)3), 0x00020000);
+  // B lane: its token's block b at xq_of(b) (16-byte aligned) and scale at xd_of(b)
   const uint32_t xrow_off = (uint32_t)btok * (uint32_t)P.K + 16u * (uint32_t)h;
   const uint32_t xd_off = (uint32_t)btok * (uint32_t)nb * 2u;
+  auto xq_of = [&](int b) {
+    return kTiled ? ((uint32_t)b * (uint32_t)P.T + (uint32_t)btok) * 32u + 16u * (uint32_t)h
+                  : xrow_off + 32u * (uint32_t)b;
+  };
+  auto xd_of = [&](int b) {
+    return kTiled ? ((uint32_t)b * (uint32_t)P.T + (uint32_t)btok) * 2u : xd_off + 2u * (uint32_t)b;
+  };
 
   // Operands of one block, raw as loaded (so the loads stay in flight until the block is
   // folded): the A lane's 5 dwords around its 16 quant bytes, the dword holding its row's
@@ -87,22 +103,20 @@ __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
     uint32_t w4, wdw, xdw;
   };
   auto load_ops = [&](int b, bool real, Ops& o) {
-    const uint32_t off = row_off + (uint32_t)b * (uint32_t)kBlockBytes;
+    const uint32_t off = row_off + (uint32_t)b * a_step;
     const uint32_t base = real ? (off + 2u + 16u * (uint32_t)h) & ~3u : kNoBlk;
     o.w03 = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)base, 0, 0));
     o.w4 = __builtin_amdgcn_raw_buffer_load_b32(wr, (int)(base + 16u), 0, 0);
     o.wdw = __builtin_amdgcn_raw_buffer_load_b32(wr, real ? (int)(off & ~3u) : (int)kNoBlk, 0, 0);
-    o.bq = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
-                                       xr, real ? (int)(xrow_off + 32u * (uint32_t)b) : (int)kNoBlk, 0, 0));
-    o.xdw = __builtin_amdgcn_raw_buffer_load_b32(xdr, real ? (int)((xd_off + 2u * (uint32_t)b) & ~3u) : (int)kNoBlk,
-                                                 0, 0);
+    o.bq = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, real ? (int)xq_of(b) : (int)kNoBlk, 0, 0));
+    o.xdw = __builtin_amdgcn_raw_buffer_load_b32(xdr, real ? (int)(xd_of(b) & ~3u) : (int)kNoBlk, 0, 0);
   };
   // fold block b into the leaf's 16 running sums: exact MFMA dots isum, the exact scale
   // products wd*xd as an fp32 MFMA outer product (A lane: its row's wd in k = 0, zero in
   // k = 1; B lane: its token's xd in k = 0, zero in k = 1; a product of two fp16 values is
   // exact in fp32 and the zero terms add nothing), then v = fma(wd*xd, isum, v) per element
   auto fold_ops = [&](const Ops& o, int b, float (&v)[16]) {
-    const uint32_t off = row_off + (uint32_t)b * (uint32_t)kBlockBytes;
+    const uint32_t off = row_off + (uint32_t)b * a_step;
     const uint32_t sh = (off + 2u + 16u * (uint32_t)h) & 3u;   // 0 or 2
     v4i a;
     a.x = (int)__builtin_amdgcn_alignbyte((uint32_t)o.w03.y, (uint32_t)o.w03.x, sh);
@@ -110,7 +124,7 @@ __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
     a.z = (int)__builtin_amdgcn_alignbyte((uint32_t)o.w03.w, (uint32_t)o.w03.z, sh);
     a.w = (int)__builtin_amdgcn_alignbyte(o.w4, (uint32_t)o.w03.w, sh);
     const float wd = lt_h2f((uint16_t)((off & 2u) ? (o.wdw >> 16) : (o.wdw & 0xFFFFu)));
-    const float xd = lt_h2f((uint16_t)(((xd_off + 2u * (uint32_t)b) & 2u) ? (o.xdw >> 16) : (o.xdw & 0xFFFFu)));
+    const float xd = lt_h2f((uint16_t)((xd_of(b) & 2u) ? (o.xdw >> 16) : (o.xdw & 0xFFFFu)));
     const v16i z = {};
     const v16i isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, o.bq, z, 0, 0, 0);
     const v16f zf = {};
@@ -310,6 +324,33 @@ __global__ void k_len_add(int* __restrict__ len, int T, int maxt) {
   }
 }
 
+// The tile-major copy of a Q8_0 matrix: tile rt, block b holds rows 32*rt .. 32*rt+31 of
+// block b, 34 bytes each (rows past N are zero).  One 2-byte unit per thread, written in
+// order.
+__global__ __launch_bounds__(256) void k_q8_tiles(const uint16_t* __restrict__ W, uint16_t* __restrict__ Wt, int N,
+                                                  int nb, uint32_t units) {
+  constexpr uint32_t kUnits = kBlockBytes / 2;             // 17 per block
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < units; i += gridDim.x * 256u) {
+    const uint32_t chunk = i / (32u * kUnits), j = i - chunk * 32u * kUnits;
+    const uint32_t rt = chunk / (uint32_t)nb, b = chunk - rt * (uint32_t)nb;
+    const uint32_t r = j / kUnits, u = j - r * kUnits;
+    const uint32_t row = rt * 32u + r;
+    Wt[i] = row < (uint32_t)N ? W[((size_t)row * nb + b) * kUnits + u] : (uint16_t)0;
+  }
+}
+
+// Block-major activation quants: block b of token t goes to slot b*T + t (lt_quant_q8's
+// quantizer on each 32-element block of x [T][K]); a half-wave per output block, in order.
+__global__ __launch_bounds__(256) void k_quant_q8_bm(const float* __restrict__ x, int8_t* __restrict__ xq,
+                                                     uint16_t* __restrict__ xd, int T, int nbk) {
+  const long ob = (long)blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int lane = threadIdx.x & 31;
+  if (ob >= (long)T * nbk) return;   // uniform per half-wave
+  const int b = (int)(ob / T), t = (int)(ob - (long)b * T);
+  const float v = x[((size_t)t * nbk + b) * 32 + lane];
+  quant_block_hw(v, lane, xq + ob * 32, xd + ob);
+}
+
 int check_gemm(const char* fn, const void* W, const int8_t* Xq, const uint16_t* Xd, const float* Y, int T, int N,
                int K) {
   LT_REQUIRE(W && Xq && Xd && Y, "%s: null argument", fn);
@@ -320,13 +361,42 @@ int check_gemm(const char* fn, const void* W, const int8_t* Xq, const uint16_t* 
   return LT_OK;
 }
 
-template <GemmEpi EPI>
+template <GemmEpi EPI, bool kTiled>
 int launch_gemm(lt_ctx* ctx, GemmParams P) {
   P.nrt = (P.N + 31) / 32;
   P.ntt = (P.T + kGemmTokens - 1) / kGemmTokens;
   const long grid = (long)((P.nrt + 7) / 8) * 8 * P.ntt;
-  k_q8_gemm<EPI><<<(unsigned)grid, 256, 0, ctx->stream>>>(P);
+  k_q8_gemm<EPI, kTiled><<<(unsigned)grid, 256, 0, ctx->stream>>>(P);
   return lt_check_launch("k_q8_gemm");
+}
+
+size_t tiles_bytes(int N, int K) { return (size_t)((N + 31) / 32) * 32 * (size_t)(K / 32) * kBlockBytes; }
+
+template <bool kTiled>
+int gemm_entry(const char* fn, lt_ctx* ctx, const void* W, const int8_t* Xq, const uint16_t* Xd, const float* bias,
+               const float* resid, float* Y, int T, int N, int K) {
+  LT_REQUIRE(ctx, "%s: null ctx", fn);
+  if (int rc = check_gemm(fn, W, Xq, Xd, Y, T, N, K)) return rc;
+  LT_REQUIRE(!(bias && resid), "%s: give bias or resid, not both", fn);
+  if (kTiled) LT_REQUIRE(tiles_bytes(N, K) < ((size_t)1 << 31), "%s: tile copy of %d x %d above 2 GiB", fn, N, K);
+  GemmParams P{};
+  P.W = (const uint8_t*)W; P.Xq = Xq; P.Xd = Xd; P.bias = bias; P.resid = resid; P.Y = Y;
+  P.T = T; P.N = N; P.K = K;
+  if (bias) return launch_gemm<GE_BIAS, kTiled>(ctx, P);
+  if (resid) return launch_gemm<GE_RESID, kTiled>(ctx, P);
+  return launch_gemm<GE_STORE, kTiled>(ctx, P);
+}
+
+template <bool kTiled>
+int gemm_silu_entry(const char* fn, lt_ctx* ctx, const void* Wgu, const int8_t* Xq, const uint16_t* Xd, float* V,
+                    int T, int F, int K) {
+  LT_REQUIRE(ctx && F > 0, "%s: null ctx or F=%d", fn, F);
+  if (int rc = check_gemm(fn, Wgu, Xq, Xd, V, T, 2 * F, K)) return rc;
+  if (kTiled) LT_REQUIRE(tiles_bytes(2 * F, K) < ((size_t)1 << 31), "%s: tile copy above 2 GiB", fn);
+  GemmParams P{};
+  P.W = (const uint8_t*)Wgu; P.Xq = Xq; P.Xd = Xd; P.Y = V;
+  P.T = T; P.N = 2 * F; P.K = K;
+  return launch_gemm<GE_SILU, kTiled>(ctx, P);
 }
 
 }  // namespace
@@ -335,25 +405,47 @@ extern "C" {
 
 int lt_q8_gemm(lt_ctx* ctx, const void* W, const int8_t* Xq, const uint16_t* Xd, const float* bias,
                const float* resid, float* Y, int T, int N, int K) {
-  LT_REQUIRE(ctx, "lt_q8_gemm: null ctx");
-  if (int rc = check_gemm("lt_q8_gemm", W, Xq, Xd, Y, T, N, K)) return rc;
-  LT_REQUIRE(!(bias && resid), "lt_q8_gemm: give bias or resid, not both");
-  GemmParams P{};
-  P.W = (const uint8_t*)W; P.Xq = Xq; P.Xd = Xd; P.bias = bias; P.resid = resid; P.Y = Y;
-  P.T = T; P.N = N; P.K = K;
-  if (bias) return launch_gemm<GE_BIAS>(ctx, P);
-  if (resid) return launch_gemm<GE_RESID>(ctx, P);
-  return launch_gemm<GE_STORE>(ctx, P);
+  return gemm_entry<false>("lt_q8_gemm", ctx, W, Xq, Xd, bias, resid, Y, T, N, K);
 }
 
 int lt_q8_gemm_silu(lt_ctx* ctx, const void* Wgu, const int8_t* Xq, const uint16_t* Xd, float* V, int T, int F,
                     int K) {
-  LT_REQUIRE(ctx && F > 0, "lt_q8_gemm_silu: null ctx or F=%d", F);
-  if (int rc = check_gemm("lt_q8_gemm_silu", Wgu, Xq, Xd, V, T, 2 * F, K)) return rc;
-  GemmParams P{};
-  P.W = (const uint8_t*)Wgu; P.Xq = Xq; P.Xd = Xd; P.Y = V;
-  P.T = T; P.N = 2 * F; P.K = K;
-  return launch_gemm<GE_SILU>(ctx, P);
+  return gemm_silu_entry<false>("lt_q8_gemm_silu", ctx, Wgu, Xq, Xd, V, T, F, K);
+}
+
+size_t lt_q8_tiles_bytes(int N, int K) {
+  if (N <= 0 || K <= 0 || K % 32) return 0;
+  return tiles_bytes(N, K);
+}
+
+int lt_q8_tiles(lt_ctx* ctx, const void* W, void* Wt, int N, int K) {
+  LT_REQUIRE(ctx && W && Wt, "lt_q8_tiles: null argument");
+  LT_REQUIRE(N > 0 && K > 0 && K % 32 == 0, "lt_q8_tiles: N=%d K=%d", N, K);
+  LT_REQUIRE(lt_aligned(W, 4) && lt_aligned(Wt, 16), "lt_q8_tiles: misaligned argument");
+  const size_t units = tiles_bytes(N, K) / 2;
+  LT_REQUIRE(units < ((size_t)1 << 32), "lt_q8_tiles: %d x %d too large", N, K);
+  const unsigned grid = (unsigned)(units / 256 < 65536 ? (units + 255) / 256 : 65536);
+  k_q8_tiles<<<grid, 256, 0, ctx->stream>>>((const uint16_t*)W, (uint16_t*)Wt, N, K / 32, (uint32_t)units);
+  return lt_check_launch("k_q8_tiles");
+}
+
+int lt_quant_q8_bm(lt_ctx* ctx, const float* x, int8_t* xq, uint16_t* xd, int T, int K) {
+  LT_REQUIRE(ctx && x && xq && xd, "lt_quant_q8_bm: null argument");
+  LT_REQUIRE(T > 0 && K > 0 && K % 32 == 0, "lt_quant_q8_bm: T=%d K=%d", T, K);
+  LT_REQUIRE(lt_aligned(xq, 16) && lt_aligned(xd, 2), "lt_quant_q8_bm: misaligned argument");
+  const long nblk = (long)T * (K / 32);
+  k_quant_q8_bm<<<(unsigned)((nblk + 7) / 8), 256, 0, ctx->stream>>>(x, xq, xd, T, K / 32);
+  return lt_check_launch("k_quant_q8_bm");
+}
+
+int lt_q8_gemm_t(lt_ctx* ctx, const void* Wt, const int8_t* Xq, const uint16_t* Xd, const float* bias,
+                 const float* resid, float* Y, int T, int N, int K) {
+  return gemm_entry<true>("lt_q8_gemm_t", ctx, Wt, Xq, Xd, bias, resid, Y, T, N, K);
+}
+
+int lt_q8_gemm_silu_t(lt_ctx* ctx, const void* Wgut, const int8_t* Xq, const uint16_t* Xd, float* V, int T, int F,
+                      int K) {
+  return gemm_silu_entry<true>("lt_q8_gemm_silu_t", ctx, Wgut, Xq, Xd, V, T, F, K);
 }
 
 int lt_rope_batch(lt_ctx* ctx, float* qk, int T, int row_stride, const int* pos0, int nheads, int hd,

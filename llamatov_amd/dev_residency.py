@@ -421,6 +421,7 @@ class ResidentModel:
             owner[key] = Q8Weight(None, K, t=slot[0], N=N) if kind == "q8" else slot[0]
         self.arena = arena
         self.load_report = None
+        self.tiles = None   # the prefill GEMM's tile-major copies (prefill_tiles)
         self.tok_embd = top["tok_embd"]
         self.output = top.get("output", self.tok_embd)
         self.output_norm = top["output_norm"]
@@ -443,7 +444,36 @@ class ResidentModel:
         m.load_report = report
         return m
 
+    def prefill_tiles(self) -> None:
+        """Tile-major copies of the prefill GEMM's matrices (q|k|v, o, interleaved gate|up,
+        down), built on the device from the resident blocks at the first batched prefill:
+        one allocation, lt_q8_tiles per matrix.  The decode path keeps reading the GGUF-layout
+        blocks; the copies cost one more copy of those weights in HBM."""
+        if self.tiles is not None:
+            return
+        if "wgu_il" not in self.layers[0]:
+            raise ValueError("prefill needs the fused gate|up layout (ResidentModel layouts 'fused' or 'both')")
+        nbytes = _lib.raw("lt_q8_tiles_bytes")
+        names = ("wqkv", "wo", "wgu_il", "wdown")
+        plan = []
+        total = 0
+        for L in self.layers:
+            for k in names:
+                W = L[k]
+                n = int(nbytes(W.N, W.K))
+                plan.append((L, k, W, total, n))
+                total += (n + 255) // 256 * 256
+        base = self.dev.malloc(total)
+        for L, k, W, off, n in plan:
+            t = DevTensor(base + off, (n,), np.uint8, owns=False, dev=self.dev)
+            call("lt_q8_tiles", self.dev.handle, W.t.vp, t.vp, W.N, W.K)
+            L[k + "_t"] = Q8Weight(None, W.K, t=t, N=W.N)
+        self.tiles = base
+
     def free(self) -> None:
+        if self.tiles is not None:
+            self.dev.free(self.tiles)
+            self.tiles = None
         self.arena.free()
 
 
@@ -672,10 +702,12 @@ class PrefillBuffers:
 
 def forward_prefill(plan: DecodePlan, tokens) -> None:
     """Batched prefill of a prompt: every linear layer runs once over all T tokens through
-    the tiled int8-MFMA Q8_0 GEMM (lt_q8_gemm), with batched RMSNorm/quant/RoPE/KV append and
-    causal attention.  It is device-uniform with the single-token path the reference uses
-    (bpd/lib/dev_residency.py:1338-1356): the KV cache, the last token's logits and the
-    greedy token it leaves on the device are bit-identical to forward_pass_resident's."""
+    the int8-MFMA Q8_0 GEMM on the coalesced layouts (tile-major weight copies from
+    ResidentModel.prefill_tiles, block-major activation quants; lt_q8_gemm_t), with batched
+    RMSNorm/RoPE/KV append and causal attention.  It is device-uniform with the single-token
+    path the reference uses (bpd/lib/dev_residency.py:1338-1356): the KV cache, the last
+    token's logits and the greedy token it leaves on the device are bit-identical to
+    forward_pass_resident's."""
     toks = np.asarray([int(t) for t in np.asarray(tokens).reshape(-1)], np.int32)
     T = int(toks.size)
     if T == 0:
@@ -685,6 +717,7 @@ def forward_prefill(plan: DecodePlan, tokens) -> None:
         raise ValueError(f"prefill of {T} tokens overflows the {plan.max_ctx}-position KV cache")
     if "wgu_il" not in m.layers[0]:
         raise ValueError("forward_prefill needs the fused gate|up layout (ResidentModel layouts 'fused' or 'both')")
+    m.prefill_tiles()
     B = plan.prefill_buffers(T)
     h = D.handle
     E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
@@ -697,21 +730,21 @@ def forward_prefill(plan: DecodePlan, tokens) -> None:
         cache = plan.caches[il]
         lp = _vp(cache.len_ptr)
         call("lt_rmsnorm", h, B.x.vp, L["attn_norm"].vp, B.h.vp, T, E, eps)
-        call("lt_quant_q8", h, B.h.vp, B.xq.vp, B.xd.vp, T * E)
-        call("lt_q8_gemm", h, L["wqkv"].t.vp, B.xq.vp, B.xd.vp, _vp(L["bqkv"]), None, B.qkv.vp, T, NQ, E)
+        call("lt_quant_q8_bm", h, B.h.vp, B.xq.vp, B.xd.vp, T, E)
+        call("lt_q8_gemm_t", h, L["wqkv_t"].t.vp, B.xq.vp, B.xd.vp, _vp(L["bqkv"]), None, B.qkv.vp, T, NQ, E)
         call("lt_rope_batch", h, B.qkv.vp, T, NQ, lp, nh + nkv, hd, m.freqs.vp)
         call("lt_kv_append_batch", h, cache.k.vp, cache.v.vp, B.qkv.vp, NQ, QD, QD + KD, T, lp, KD,
              cache.max_seq, p.kv_dtype)
         call("lt_attn_prefill", h, B.qkv.vp, NQ, cache.k.vp, cache.v.vp, lp, B.att.vp, T, nh, nkv, hd,
              ctypes.c_float(plan.scale), cache.max_seq, p.attn_nsplit, p.kv_dtype, ws, ws_n)
         call("lt_len_add", h, lp, T, cache.max_seq)
-        call("lt_quant_q8", h, B.att.vp, B.xq.vp, B.xd.vp, T * QD)
-        call("lt_q8_gemm", h, L["wo"].t.vp, B.xq.vp, B.xd.vp, None, B.x.vp, B.xres.vp, T, E, QD)
+        call("lt_quant_q8_bm", h, B.att.vp, B.xq.vp, B.xd.vp, T, QD)
+        call("lt_q8_gemm_t", h, L["wo_t"].t.vp, B.xq.vp, B.xd.vp, None, B.x.vp, B.xres.vp, T, E, QD)
         call("lt_rmsnorm", h, B.xres.vp, L["ffn_norm"].vp, B.h.vp, T, E, eps)
-        call("lt_quant_q8", h, B.h.vp, B.xq.vp, B.xd.vp, T * E)
-        call("lt_q8_gemm_silu", h, L["wgu_il"].t.vp, B.xq.vp, B.xd.vp, B.v.vp, T, F, E)
-        call("lt_quant_q8", h, B.v.vp, B.xq.vp, B.xd.vp, T * F)
-        call("lt_q8_gemm", h, L["wdown"].t.vp, B.xq.vp, B.xd.vp, None, B.xres.vp, B.x.vp, T, E, F)
+        call("lt_quant_q8_bm", h, B.h.vp, B.xq.vp, B.xd.vp, T, E)
+        call("lt_q8_gemm_silu_t", h, L["wgu_il_t"].t.vp, B.xq.vp, B.xd.vp, B.v.vp, T, F, E)
+        call("lt_quant_q8_bm", h, B.v.vp, B.xq.vp, B.xd.vp, T, F)
+        call("lt_q8_gemm_t", h, L["wdown_t"].t.vp, B.xq.vp, B.xd.vp, None, B.xres.vp, B.x.vp, T, E, F)
         cache.length += T
     # the last token's logits and greedy token, as the decode step computes them
     D.d2d(plan.carry.ptr, B.x.ptr + (T - 1) * E * 4, E * 4)

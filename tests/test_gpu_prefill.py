@@ -70,6 +70,96 @@ def test_q8_gemm_silu(gpu, oracle, F, K, T):
         assert np.array_equal(bits(got[t]), bits(oracle.silu_mul(g, u))), f"token {t}"
 
 
+def tiles_host(W, N, K):
+    """The tile-major layout restated on the host: Wt[rt][b][r] = row 32*rt + r's block b."""
+    nb = K // 32
+    nt = (N + 31) // 32
+    pad = np.zeros((nt * 32, nb * 34), np.uint8)
+    pad[:N] = W
+    return pad.reshape(nt, 32, nb, 34).transpose(0, 2, 1, 3).copy()
+
+
+@pytest.mark.parametrize("N,K", [(1152, 896), (100, 96), (33, 4864), (32, 32)])
+def test_q8_tiles_layout(gpu, N, K):
+    case(f"q8_tiles N={N} K={K}")
+    from llamatov_amd._lib import raw
+    rng = np.random.default_rng(N + K)
+    W = rng.integers(0, 256, (N, K // 32 * 34), dtype=np.uint8)
+    n = int(raw("lt_q8_tiles_bytes")(N, K))
+    assert n == (N + 31) // 32 * 32 * (K // 32) * 34
+    Wt = dr.DevTensor.empty((n,), np.uint8)
+    Wt.dev.fill(Wt.ptr, 0xA5, Wt.nbytes)
+    call("lt_q8_tiles", gpu.handle, up(W).vp, Wt.vp, N, K)
+    assert np.array_equal(Wt.to_host(), tiles_host(W, N, K).reshape(-1))
+
+
+@pytest.mark.parametrize("T,K", [(37, 896), (1, 32), (130, 4864)])
+def test_quant_q8_block_major(gpu, oracle, T, K):
+    case(f"quant_q8_bm T={T} K={K}")
+    rng = np.random.default_rng(T * K)
+    X = rng.standard_normal((T, K)).astype(np.float32)
+    X[0, :32] = 0.0
+    X[-1, 32 * (K // 64):32 * (K // 64) + 32] *= 1e-30
+    xq = dr.DevTensor.empty((K // 32, T, 32), np.int8)
+    xd = dr.DevTensor.empty((K // 32, T), np.uint16)
+    call("lt_quant_q8_bm", gpu.handle, up(X).vp, xq.vp, xd.vp, T, K)
+    gq, gd = xq.to_host(), xd.to_host()
+    for t in range(T):
+        q, d = oracle.quant_q8(X[t])
+        assert np.array_equal(gq[:, t, :].reshape(-1), q), f"token {t} quants"
+        assert np.array_equal(gd[:, t], d), f"token {t} scales"
+
+
+@pytest.mark.parametrize("N,K,T,epi", [(1152, 896, 37, "bias"), (896, 4864, 130, "resid"), (100, 96, 5, "store"),
+                                       (64, 1024, 129, "store"), (4096, 4096, 33, "store"), (40, 14336, 3, "resid")])
+def test_q8_gemm_tiled_matches_gemv_per_token(gpu, oracle, N, K, T, epi):
+    case(f"q8_gemm_t N={N} K={K} T={T} {epi}")
+    rng = np.random.default_rng(33)
+    W = hq8.quantize_rows((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    X = (rng.standard_normal((T, K))).astype(np.float32)
+    X[0, :64] = 0.0
+    xq = np.empty((T, K), np.int8)
+    xd = np.empty((T, K // 32), np.uint16)
+    for t in range(T):
+        xq[t], xd[t] = oracle.quant_q8(X[t])
+    xq_bm = np.ascontiguousarray(xq.reshape(T, K // 32, 32).transpose(1, 0, 2))
+    xd_bm = np.ascontiguousarray(xd.T)
+    bias = (rng.standard_normal(N) * 0.02).astype(np.float32) if epi == "bias" else None
+    resid = rng.standard_normal((T, N)).astype(np.float32) if epi == "resid" else None
+    Y = dr.DevTensor.empty((T, N), np.float32)
+    call("lt_q8_gemm_t", gpu.handle, up(tiles_host(W, N, K)).vp, up(xq_bm).vp, up(xd_bm).vp,
+         up(bias).vp if bias is not None else None, up(resid).vp if resid is not None else None, Y.vp, T, N, K)
+    got = Y.to_host()
+    for t in range(T):
+        r = bias if bias is not None else (resid[t] if resid is not None else None)
+        exp = oracle.q8_gemv(W, xq[t], xd[t], K, r)
+        assert np.array_equal(bits(got[t]), bits(exp)), f"token {t}: {np.flatnonzero(bits(got[t]) != bits(exp))[:5]}"
+
+
+@pytest.mark.parametrize("F,K,T", [(4864, 896, 40), (64, 128, 7), (48, 96, 70)])
+def test_q8_gemm_silu_tiled(gpu, oracle, F, K, T):
+    case(f"q8_gemm_silu_t F={F} K={K} T={T}")
+    rng = np.random.default_rng(34)
+    Wg = hq8.quantize_rows((rng.standard_normal((F, K)) * 0.02).astype(np.float32))
+    Wu = hq8.quantize_rows((rng.standard_normal((F, K)) * 0.02).astype(np.float32))
+    X = rng.standard_normal((T, K)).astype(np.float32)
+    xq = np.empty((T, K), np.int8)
+    xd = np.empty((T, K // 32), np.uint16)
+    for t in range(T):
+        xq[t], xd[t] = oracle.quant_q8(X[t])
+    xq_bm = np.ascontiguousarray(xq.reshape(T, K // 32, 32).transpose(1, 0, 2))
+    xd_bm = np.ascontiguousarray(xd.T)
+    V = dr.DevTensor.empty((T, F), np.float32)
+    Wgu = M.interleave_gateup(Wg, Wu)
+    call("lt_q8_gemm_silu_t", gpu.handle, up(tiles_host(Wgu, 2 * F, K)).vp, up(xq_bm).vp, up(xd_bm).vp, V.vp,
+         T, F, K)
+    got = V.to_host()
+    for t in range(T):
+        g = oracle.q8_gemv(Wg, xq[t], xd[t], K)
+        u = oracle.q8_gemv(Wu, xq[t], xd[t], K)
+        assert np.array_equal(bits(got[t]), bits(oracle.silu_mul(g, u))), f"token {t}"
+
+
 _W = {}
 
 
