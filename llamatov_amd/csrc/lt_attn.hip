@@ -456,9 +456,11 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
   // @phase attn 6
 }
 
-// Single-wave attention for batched decode (AM_DECODE) and for the decode step (AM_STEP:
-// RoPE of q and the new k, the KV append and the quantized output fused in, as k_attn
-// does): one wave per workgroup, (split, HPW heads of one KV group, sequence).  The same
+// Single-wave attention for batched decode (AM_DECODE), causal prefill (AM_PREFILL: query
+// row b of one sequence is a decode of *len + b + 1 positions of the shared cache) and the
+// decode step (AM_STEP: RoPE of q and the new k, the KV append and the quantized output
+// fused in, as k_attn does): one wave per workgroup, (split, HPW heads of one KV group,
+// sequence or query row).  The same
 // per-split arithmetic as k_attn, laid out so nothing waits on a barrier or on LDS-staged V:
 //   scores   one lane per position (K row from LDS), the heads' sequential fma chains over
 //            i, times scale, into LDS position-major [t][HPW];
@@ -480,7 +482,11 @@ constexpr int kVRingDw = 32;       // V dwords in flight per lane, batched decod
 constexpr int kVRingDwStep = 56;   // the decode step (few waves): a deep ring (under the 63 loads a wave can count), issued before the scores
 
 template <bool kF16, int HPW, int DPL, int MODE>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(MODE != AM_STEP && (kF16 ? DPL * 8 : DPL * 16) <= 16 ? 3 : 1))) void k_attn_w1(AttnArgs A) {
+// (occupancy hint: 3 waves per SIMD where a K row is at most 16 units and at most 4 heads
+// share the wave, else 2 -- 8 heads' exps and outputs need the registers -- and 1 for the
+// step's deep ring)
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
+    MODE == AM_STEP ? 1 : (kF16 ? DPL * 8 : DPL * 16) <= 16 && HPW <= 4 ? 3 : 2))) void k_attn_w1(AttnArgs A) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   constexpr bool kStep = MODE == AM_STEP;
   constexpr int HD = 64 * DPL;
@@ -510,7 +516,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(MODE != AM_S
   // the step's length first, then the new token's inputs: waiting for the length (which
   // places the cache reads) does not wait for the inputs, and waiting for the inputs
   // never waits for cache rows
-  const int len0 = kStep ? *A.len : A.len[b];
+  const int len0 = kStep ? *A.len : MODE == AM_PREFILL ? A.len[0] + b + 1 : A.len[b];
   constexpr int kHalf = HD / 2;
   constexpr int kRopeIt = ((HPW + 1) * kHalf + 63) / 64;
   float rx1[kRopeIt], rx2[kRopeIt], rfr[kRopeIt], rv[DPL];
@@ -542,11 +548,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(MODE != AM_S
   const int p1 = p0 + per < nctx ? p0 + per : nctx;
   const int n = p1 > p0 ? p1 - p0 : 0;
   const int tnew = kStep ? Lnew - p0 : -1;          // the new position within this split (if 0 <= tnew < n)
-  const uint32_t rows = (uint32_t)gridDim.z * (uint32_t)A.maxt;
+  const uint32_t rows = MODE == AM_DECODE ? (uint32_t)gridDim.z * (uint32_t)A.maxt : (uint32_t)A.maxt;
   const __amdgpu_buffer_rsrc_t krsrc =
       __builtin_amdgcn_make_buffer_rsrc(A.kc, 0, (int)(rows * (uint32_t)kvrow * kEb), 0x00020000);
   // byte offset of (position p0 of this split, head group g) and the row pitch
-  const uint32_t base = ((uint32_t)b * (uint32_t)A.maxt + (uint32_t)p0) * (uint32_t)kvrow * kEb + (uint32_t)g * HD * kEb;
+  const uint32_t seq0 = MODE == AM_DECODE ? (uint32_t)b * (uint32_t)A.maxt : 0u;   // the sequence's first row
+  const uint32_t base = (seq0 + (uint32_t)p0) * (uint32_t)kvrow * kEb + (uint32_t)g * HD * kEb;
   const uint32_t pitch = (uint32_t)kvrow * kEb;
   // The V rows read from the cache are the split's first nv rows (a step's new row, the
   // split's last, is folded from registers): a buffer that ends right after them makes
@@ -1010,8 +1017,8 @@ hipError_t launch_w1(int hpw, int dpl, dim3 grid, size_t shm, hipStream_t st, co
   return hipErrorInvalidValue;
 }
 
-// LT_ATTN_W1=0 keeps decode and the decode step on k_attn (for comparisons); the default is
-// k_attn_w1 wherever its head sizes apply.
+// LT_ATTN_W1=0 keeps every mode on k_attn (for comparisons); the default is k_attn_w1
+// wherever its head sizes and LDS budget apply.
 bool use_w1() {
   static const bool on = [] {
     const char* s = getenv("LT_ATTN_W1");
@@ -1025,9 +1032,24 @@ bool use_w1() {
 int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, void* ws, size_t ws_bytes,
                 const char* what) {
   LT_REQUIRE(A.nsplit <= 128, "%s: nsplit=%d (at most 128)", what, A.nsplit);
-  if (A.nsplit > 1 && !(mode == AM_PREFILL && A.nsplit <= kMaxInWgSplits &&
-                        ((size_t)hpw * A.hd + 2 * A.hd + (size_t)hpw * A.maxt + kVChunkFloats) * sizeof(float) <=
-                            64 * 1024)) {
+  // the single-wave kernel (every mode): all heads of a KV group share its K/V reads
+  const int rep = A.nh / A.nkv;
+  const int h = rep % 8 == 0 ? 8 : rep % 4 == 0 ? 4 : rep % 2 == 0 ? 2 : 1;
+  const int dpl = A.hd / 64;
+  const int per_max = (A.maxt + A.nsplit - 1) / A.nsplit;
+  const size_t ku = (size_t)A.hd * (f16 ? 2 : 4) / 16;
+  const size_t kpr = h >= 2 ? 32 : 64;              // positions per score round
+  const int vb = dpl * (f16 ? 2 : 4);               // V bytes per lane per row
+  const int ring = (mode == AM_STEP ? kVRingDwStep : kVRingDw) / (vb < 4 ? 1 : vb / 4) / 8 * 8;   // V rows in flight
+  const size_t per_up = (size_t)(per_max + ring - 1) / ring * ring;
+  const size_t w1_shm = ((size_t)h * A.hd + (kpr * (ku + 1) + (mode == AM_STEP ? 2 * ku : 0)) * 4 +
+                         (per_up + 8 + 1) * h) * sizeof(float);
+  // fp16: 64, 128 or 256 dims; fp32: 64 or 128 (a K row of 8 to 32 16-byte units)
+  const bool w1 = use_w1() && A.hd % 64 == 0 &&
+                  (f16 ? (dpl == 1 || dpl == 2 || dpl == 4) : (dpl == 1 || dpl == 2)) && w1_shm <= 64 * 1024;
+  if (A.nsplit > 1 && (w1 || !(mode == AM_PREFILL && A.nsplit <= kMaxInWgSplits &&
+                               ((size_t)hpw * A.hd + 2 * A.hd + (size_t)hpw * A.maxt + kVChunkFloats) *
+                                       sizeof(float) <= 64 * 1024))) {
     const size_t need = lt_attn_ws_bytes(rows * A.nh, A.hd, A.nsplit);
     LT_REQUIRE(ws && lt_aligned(ws, 16), "%s: nsplit=%d needs a 16-byte aligned workspace", what, A.nsplit);
     if (ws_bytes < need) return lt_fail(LT_ENOMEM, "%s: workspace %zu < %zu bytes", what, ws_bytes, need);
@@ -1036,39 +1058,26 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
     A.wsz = w.z;
     A.wso = w.o;
   }
-  if ((mode == AM_DECODE || mode == AM_STEP) && use_w1()) {
-    // the single-wave kernel: all heads of a KV group share its K/V reads
-    const int rep = A.nh / A.nkv;
-    const int h = rep % 8 == 0 ? 8 : rep % 4 == 0 ? 4 : rep % 2 == 0 ? 2 : 1;
-    const int dpl = A.hd / 64;
-    const int per_max = (A.maxt + A.nsplit - 1) / A.nsplit;
-    const size_t ku = (size_t)A.hd * (f16 ? 2 : 4) / 16;
-    const size_t kpr = h >= 2 ? 32 : 64;              // positions per score round
-    const int vb = dpl * (f16 ? 2 : 4);               // V bytes per lane per row
-    const int ring = (mode == AM_STEP ? kVRingDwStep : kVRingDw) / (vb < 4 ? 1 : vb / 4) / 8 * 8;   // V rows in flight
-    const size_t per_up = (size_t)(per_max + ring - 1) / ring * ring;
-    const size_t shm = ((size_t)h * A.hd + (kpr * (ku + 1) + (mode == AM_STEP ? 2 * ku : 0)) * 4 +
-                        (per_up + 8 + 1) * h) * sizeof(float);
-    // fp16: 64, 128 or 256 dims; fp32: 64 or 128 (a K row of 8 to 32 16-byte units)
-    if (A.hd % 64 == 0 && (f16 ? (dpl == 1 || dpl == 2 || dpl == 4) : (dpl == 1 || dpl == 2)) &&
-        shm <= 64 * 1024) {
-      A.per_max = per_max;
-      const dim3 grid(A.nsplit, A.nh / h, rows);
-      hipError_t e;
-      if (mode == AM_STEP)
-        e = f16 ? launch_w1<true, AM_STEP>(h, dpl, grid, shm, ctx->stream, A)
-                : launch_w1<false, AM_STEP>(h, dpl, grid, shm, ctx->stream, A);
-      else
-        e = f16 ? launch_w1<true, AM_DECODE>(h, dpl, grid, shm, ctx->stream, A)
-                : launch_w1<false, AM_DECODE>(h, dpl, grid, shm, ctx->stream, A);
-      if (e != hipSuccess) return lt_fail_hip(e, what, __FILE__, __LINE__);
-      if (A.nsplit > 1) {
-        launch_merge(dim3(A.nh, rows), ctx->stream, A.wsm, A.wsz, A.wso, mode == AM_STEP ? A.len : nullptr, A.maxt,
-                     A.out, A.oq, A.od, A.nh, A.hd, A.nsplit);
-        return lt_check_launch("k_attn_merge");
-      }
-      return lt_check_launch("k_attn_w1");
+  if (w1) {
+    A.per_max = per_max;
+    const dim3 grid(A.nsplit, A.nh / h, rows);
+    hipError_t e;
+    if (mode == AM_STEP)
+      e = f16 ? launch_w1<true, AM_STEP>(h, dpl, grid, w1_shm, ctx->stream, A)
+              : launch_w1<false, AM_STEP>(h, dpl, grid, w1_shm, ctx->stream, A);
+    else if (mode == AM_DECODE)
+      e = f16 ? launch_w1<true, AM_DECODE>(h, dpl, grid, w1_shm, ctx->stream, A)
+              : launch_w1<false, AM_DECODE>(h, dpl, grid, w1_shm, ctx->stream, A);
+    else
+      e = f16 ? launch_w1<true, AM_PREFILL>(h, dpl, grid, w1_shm, ctx->stream, A)
+              : launch_w1<false, AM_PREFILL>(h, dpl, grid, w1_shm, ctx->stream, A);
+    if (e != hipSuccess) return lt_fail_hip(e, what, __FILE__, __LINE__);
+    if (A.nsplit > 1) {
+      launch_merge(dim3(A.nh, rows), ctx->stream, A.wsm, A.wsz, A.wso, mode == AM_STEP ? A.len : nullptr, A.maxt,
+                   A.out, A.oq, A.od, A.nh, A.hd, A.nsplit);
+      return lt_check_launch("k_attn_merge");
     }
+    return lt_check_launch("k_attn_w1");
   }
   auto shm_for = [&](int per_max) {
     return ((size_t)hpw * A.hd + 2 * A.hd + (size_t)hpw * per_max + kVChunkFloats) * sizeof(float);

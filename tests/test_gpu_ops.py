@@ -239,6 +239,32 @@ def test_attention_decode_geometries(gpu, oracle, kv_dtype, hd, nh, nkv):
             assert_bitexact(got[b], exp, f"attn b={b} L={lens[b]}")
 
 
+@pytest.mark.parametrize("kv_dtype,nh,nkv,hd", [(LT_KV_F16, 14, 2, 64), (LT_KV_F32, 14, 2, 64),
+                                                 (LT_KV_F16, 32, 8, 128), (LT_KV_F32, 16, 2, 128),
+                                                 (LT_KV_F16, 8, 8, 256)])
+@pytest.mark.parametrize("len0,T,nsplit", [(0, 37, 1), (5, 40, 4), (0, 70, 16), (200, 33, 7)])
+def test_attention_prefill(gpu, oracle, kv_dtype, nh, nkv, hd, len0, T, nsplit):
+    """Causal prefill attention: query t of T attends the first len0 + t + 1 rows of one
+    cache, each exactly as a decode of that length (split layout per query, empty splits for
+    short queries), NaN past len0 + T."""
+    f16 = kv_dtype == LT_KV_F16
+    case(f"attn prefill nh={nh} nkv={nkv} hd={hd} f16={f16} len0={len0} T={T} nsplit={nsplit}")
+    rng = np.random.default_rng(nh * hd + T)
+    maxt = 300
+    q = rng.standard_normal((T, nh * hd)).astype(np.float32)
+    k, v = _attn_setup(rng, 1, maxt, nkv, hd, kv_dtype, [len0 + T], np.nan)
+    ws_n = _lib.raw("lt_attn_workspace_size")(T, nh, hd, nsplit)
+    ws = empty((max(ws_n, 1),), np.uint8)
+    out = empty((T, nh * hd), np.float32)
+    scale = float(hd ** -0.5)
+    call("lt_attn_prefill", gpu.handle, up(q).vp, nh * hd, up(k).vp, up(v).vp, up(np.array([len0], np.int32)).vp,
+         out.vp, T, nh, nkv, hd, ctypes.c_float(scale), maxt, nsplit, kv_dtype, ws.vp, ws.nbytes)
+    got = out.to_host()
+    for t in range(T):
+        exp = oracle.attn_decode(q[t], k[0], v[0], len0 + t + 1, nh, nkv, hd, scale, f16, nsplit)
+        assert_bitexact(got[t], exp, f"query {t} L={len0 + t + 1}")
+
+
 @pytest.mark.parametrize("B,L,nsplit", [(1, 4096, 32), (8, 4096, 32), (1, 16384, 64), (2, 32768, 128)])
 def test_attention_long_context_batched(gpu, oracle, B, L, nsplit):
     """BASELINE config 4 geometry: 32 Q heads, 8 KV heads, hd 128, fp16 KV."""
