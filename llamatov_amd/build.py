@@ -29,6 +29,9 @@ HIP_FLAGS = [
     "-ffp-contract=off",
     "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results straight into VGPRs: the prefill GEMM folds every MFMA result with VALU
+    # arithmetic, which would otherwise first copy each of them out of the AGPRs
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-command-line-argument",
 ]
 

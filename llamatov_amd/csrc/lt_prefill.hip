@@ -102,14 +102,31 @@ __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
     v4i w03, bq;
     uint32_t w4, wdw, xdw;
   };
+  // Tiled: a block's offsets are a per-block part common to the wave (the 1088-byte tile
+  // block, the 32T-byte activation block; a multiple of 4, so every lane keeps its
+  // alignment) plus a per-lane constant, and the scales are 16-bit loads.  Past the last
+  // block the common part is kNoBlk, which puts every lane out of range.
+  const uint32_t a_lane = (row_off + 2u + 16u * (uint32_t)h) & ~3u;   // the A lane's first dword
+  const uint32_t a_sh = (row_off + 2u + 16u * (uint32_t)h) & 3u;      // its byte shift (0 or 2)
   auto load_ops = [&](int b, bool real, Ops& o) {
-    const uint32_t off = row_off + (uint32_t)b * a_step;
-    const uint32_t base = real ? (off + 2u + 16u * (uint32_t)h) & ~3u : kNoBlk;
-    o.w03 = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)base, 0, 0));
-    o.w4 = __builtin_amdgcn_raw_buffer_load_b32(wr, (int)(base + 16u), 0, 0);
-    o.wdw = __builtin_amdgcn_raw_buffer_load_b32(wr, real ? (int)(off & ~3u) : (int)kNoBlk, 0, 0);
-    o.bq = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, real ? (int)xq_of(b) : (int)kNoBlk, 0, 0));
-    o.xdw = __builtin_amdgcn_raw_buffer_load_b32(xdr, real ? (int)(xd_of(b) & ~3u) : (int)kNoBlk, 0, 0);
+    if constexpr (kTiled) {
+      const uint32_t sa = real ? (uint32_t)b * a_step : kNoBlk;
+      const uint32_t sq = real ? (uint32_t)b * (uint32_t)P.T * 32u : kNoBlk;
+      const uint32_t sd = real ? (uint32_t)b * (uint32_t)P.T * 2u : kNoBlk;
+      o.w03 = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)(sa + a_lane), 0, 0));
+      o.w4 = __builtin_amdgcn_raw_buffer_load_b32(wr, (int)(sa + a_lane + 16u), 0, 0);
+      o.wdw = __builtin_amdgcn_raw_buffer_load_b16(wr, (int)(sa + row_off), 0, 0);
+      o.bq = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)(sq + xq_of(0)), 0, 0));
+      o.xdw = __builtin_amdgcn_raw_buffer_load_b16(xdr, (int)(sd + xd_of(0)), 0, 0);
+    } else {
+      const uint32_t off = row_off + (uint32_t)b * a_step;
+      const uint32_t base = real ? (off + 2u + 16u * (uint32_t)h) & ~3u : kNoBlk;
+      o.w03 = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)base, 0, 0));
+      o.w4 = __builtin_amdgcn_raw_buffer_load_b32(wr, (int)(base + 16u), 0, 0);
+      o.wdw = __builtin_amdgcn_raw_buffer_load_b32(wr, real ? (int)(off & ~3u) : (int)kNoBlk, 0, 0);
+      o.bq = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, real ? (int)xq_of(b) : (int)kNoBlk, 0, 0));
+      o.xdw = __builtin_amdgcn_raw_buffer_load_b32(xdr, real ? (int)(xd_of(b) & ~3u) : (int)kNoBlk, 0, 0);
+    }
   };
   // fold block b into the leaf's 16 running sums: exact MFMA dots isum, the exact scale
   // products wd*xd as an fp32 MFMA outer product (A lane: its row's wd in k = 0, zero in
@@ -117,14 +134,15 @@ __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
   // exact in fp32 and the zero terms add nothing), then v = fma(wd*xd, isum, v) per element
   auto fold_ops = [&](const Ops& o, int b, float (&v)[16]) {
     const uint32_t off = row_off + (uint32_t)b * a_step;
-    const uint32_t sh = (off + 2u + 16u * (uint32_t)h) & 3u;   // 0 or 2
+    const uint32_t sh = kTiled ? a_sh : (off + 2u + 16u * (uint32_t)h) & 3u;   // 0 or 2
     v4i a;
     a.x = (int)__builtin_amdgcn_alignbyte((uint32_t)o.w03.y, (uint32_t)o.w03.x, sh);
     a.y = (int)__builtin_amdgcn_alignbyte((uint32_t)o.w03.z, (uint32_t)o.w03.y, sh);
     a.z = (int)__builtin_amdgcn_alignbyte((uint32_t)o.w03.w, (uint32_t)o.w03.z, sh);
     a.w = (int)__builtin_amdgcn_alignbyte(o.w4, (uint32_t)o.w03.w, sh);
-    const float wd = lt_h2f((uint16_t)((off & 2u) ? (o.wdw >> 16) : (o.wdw & 0xFFFFu)));
-    const float xd = lt_h2f((uint16_t)((xd_of(b) & 2u) ? (o.xdw >> 16) : (o.xdw & 0xFFFFu)));
+    const float wd = kTiled ? lt_h2f((uint16_t)o.wdw) : lt_h2f((uint16_t)((off & 2u) ? (o.wdw >> 16) : (o.wdw & 0xFFFFu)));
+    const float xd = kTiled ? lt_h2f((uint16_t)o.xdw)
+                            : lt_h2f((uint16_t)((xd_of(b) & 2u) ? (o.xdw >> 16) : (o.xdw & 0xFFFFu)));
     const v16i z = {};
     const v16i isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, o.bq, z, 0, 0, 0);
     const v16f zf = {};
@@ -357,6 +375,8 @@ int check_gemm(const char* fn, const void* W, const int8_t* Xq, const uint16_t* 
   LT_REQUIRE(T > 0 && N > 0 && K > 0 && K % 32 == 0, "%s: T=%d N=%d K=%d (K multiple of 32)", fn, T, N, K);
   LT_REQUIRE((uint64_t)N * (uint64_t)(K / 32) * 34u < ((uint64_t)1 << 31),
              "%s: a %d x %d Q8_0 matrix must be below 2 GiB (split it by rows)", fn, N, K);
+  LT_REQUIRE((uint64_t)T * (uint64_t)K < ((uint64_t)1 << 31), "%s: T=%d x K=%d activation quants above 2 GiB", fn, T,
+             K);
   LT_REQUIRE(lt_aligned(W, 4) && lt_aligned(Xq, 16) && lt_aligned(Xd, 2), "%s: misaligned argument", fn);
   return LT_OK;
 }
