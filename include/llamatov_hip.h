@@ -242,9 +242,10 @@ LT_API int lt_q8_gemm_silu(lt_ctx* ctx, const void* Wgu, const int8_t* Xq, const
                            int F, int K);
 
 /* The coalesced layouts of the prefill GEMM (no reference counterpart; same results):
- * - the tile-major copy of a Q8_0 matrix W [N][K/32] (GGUF blocks): Wt[rt][b][r] is row
- *   32*rt + r's block b, 34 bytes, rows past N zero; lt_q8_tiles_bytes(N, K) bytes, built on
- *   the device by lt_q8_tiles (Wt 16-byte aligned);
+ * - the tile-major copy of a Q8_0 matrix W [N][K/32] (GGUF blocks): the 1088-byte tile
+ *   block (rt, b) at Wt + (rt*K/32 + b)*1088 holds the 32 quant bytes of rows 32*rt + r,
+ *   r = 0..31, at 32*r, then their fp16 scales at 1024 + 2*r; rows past N are zero.
+ *   lt_q8_tiles_bytes(N, K) bytes, built on the device by lt_q8_tiles (Wt 16-byte aligned);
  * - block-major activation quants: lt_quant_q8_bm writes token t's block b of x [T][K] (the
  *   lt_quant_q8 quantizer) to Xq[b][t][32] and Xd[b][t]. */
 LT_API size_t lt_q8_tiles_bytes(int N, int K);

@@ -44,10 +44,18 @@ struct GemmParams {
 // 16*(l/32) .. +16 of the block (the same half of k for A and B).
 __device__ __forceinline__ int c_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 
-// kTiled: the weights in the tile-major copy (a 32-row tile's block b is 1088 contiguous
-// bytes) and the activations block-major (block b of 32 consecutive tokens is 1 KB
-// contiguous), so both operands of a block are coalesced loads; the arithmetic and the
-// order are the same.
+// The tile-major copy's 1088-byte tile block: the 32 rows' quants, 32 bytes each (row r at
+// 32r), then the 32 rows' fp16 scales (row r at kTileQ + 2r).
+constexpr uint32_t kTileQ = 32u * 32u;
+constexpr uint32_t kTileBlk = kTileQ + 64u;
+static_assert(kTileBlk == 32u * kBlockBytes, "a tile block holds 32 Q8_0 blocks");
+
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+
+// kTiled: the weights in the tile-major copy and the activations block-major (block b of
+// 32 consecutive tokens is 1 KB of quants and 64 bytes of scales, each contiguous), so
+// both operands of a block are coalesced, aligned loads; the arithmetic and the order are
+// those of the row-major layouts.
 template <GemmEpi EPI, bool kTiled>
 __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
   __shared__ float s_st4[kGemmWaves][16 * 64];   // tree level 4 of each wave's 32 x 32 tile
@@ -65,88 +73,99 @@ __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
   const int n0 = rt * 32;
   const int t0 = tt * kGemmTokens + wave * 32;
   const int nb = P.K >> 5;
-
-  // A lane: weight row n0 + c (clamped; results of clamped rows are discarded).  Block b of
-  // the lane's row starts at row_off + b * a_step.
-  const int arow = n0 + c < P.N ? n0 + c : P.N - 1;
-  const uint32_t row_off = kTiled ? (uint32_t)rt * (uint32_t)nb * 32u * (uint32_t)kBlockBytes + (uint32_t)c * kBlockBytes
-                                  : (uint32_t)arow * (uint32_t)nb * (uint32_t)kBlockBytes;
-  const uint32_t a_step = kTiled ? 32u * kBlockBytes : (uint32_t)kBlockBytes;
-  const uint32_t mat_bytes = kTiled ? (uint32_t)P.nrt * (uint32_t)nb * 32u * (uint32_t)kBlockBytes
-                                    : (uint32_t)P.N * (uint32_t)nb * (uint32_t)kBlockBytes;
-  // the 16 quant bytes of a block half begin 2 bytes into the block; the 5th dword can lie
-  // past the matrix: buffer loads bound it (out-of-range dwords read as zero)
-  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)P.W, 0, (int)((mat_bytes + 3u) & ~3u), 0x00020000);
-  // B lane: token t0 + c (clamped)
+  // B lane: token t0 + c (clamped; results of clamped tokens are discarded)
   const int btok = t0 + c < P.T ? t0 + c : P.T - 1;
-  const __amdgpu_buffer_rsrc_t xr =
-      __builtin_amdgcn_make_buffer_rsrc((void*)P.Xq, 0, (int)((size_t)P.T * P.K), 0x00020000);
-  const __amdgpu_buffer_rsrc_t xdr =
-      __builtin_amdgcn_make_buffer_rsrc((void*)P.Xd, 0, (int)(((size_t)P.T * nb * 2 + 3) & ~(size_t)3), 0x00020000);
-  // B lane: its token's block b at xq_of(b) (16-byte aligned) and scale at xd_of(b)
-  const uint32_t xrow_off = (uint32_t)btok * (uint32_t)P.K + 16u * (uint32_t)h;
-  const uint32_t xd_off = (uint32_t)btok * (uint32_t)nb * 2u;
-  auto xq_of = [&](int b) {
-    return kTiled ? ((uint32_t)b * (uint32_t)P.T + (uint32_t)btok) * 32u + 16u * (uint32_t)h
-                  : xrow_off + 32u * (uint32_t)b;
-  };
-  auto xd_of = [&](int b) {
-    return kTiled ? ((uint32_t)b * (uint32_t)P.T + (uint32_t)btok) * 2u : xd_off + 2u * (uint32_t)b;
-  };
 
   // Operands of one block, raw as loaded (so the loads stay in flight until the block is
-  // folded): the A lane's 5 dwords around its 16 quant bytes, the dword holding its row's
-  // scale, the B lane's 16 quant bytes and the dword holding its token's scale.  Every load
-  // is unconditional: past the last block the offsets are out of range and read zeros.
+  // folded).  Every load is unconditional: past the last block they read zeros.
+  //   row-major: the A lane's 5 dwords around its 16 quant bytes (a block's quants begin 2
+  //     bytes in), the dword holding its row's scale, the B lane's 16 quant bytes and the
+  //     dword holding its token's scale;
+  //   tiled: the A and B lanes' 16 quant bytes and (lanes of the first k half) the row's
+  //     and the token's scale as 16-bit loads; the block's part of each offset is the
+  //     wave-uniform soffset, the lane's part a constant.
   struct Ops {
     v4i w03, bq;
     uint32_t w4, wdw, xdw;
   };
-  // Tiled: a block's offsets are a per-block part common to the wave (the 1088-byte tile
-  // block, the 32T-byte activation block; a multiple of 4, so every lane keeps its
-  // alignment) plus a per-lane constant, and the scales are 16-bit loads.  Past the last
-  // block the common part is kNoBlk, which puts every lane out of range.
-  const uint32_t a_lane = (row_off + 2u + 16u * (uint32_t)h) & ~3u;   // the A lane's first dword
-  const uint32_t a_sh = (row_off + 2u + 16u * (uint32_t)h) & 3u;      // its byte shift (0 or 2)
+  // row-major addressing: block b of the A lane's row (clamped) at row_off + 34b, of the
+  // B lane's token at xrow_off + 32b, its scale at xd_off + 2b
+  const int arow = n0 + c < P.N ? n0 + c : P.N - 1;
+  const uint32_t row_off = (uint32_t)arow * (uint32_t)nb * (uint32_t)kBlockBytes;
+  const uint32_t xrow_off = (uint32_t)btok * (uint32_t)P.K + 16u * (uint32_t)h;
+  const uint32_t xd_off = (uint32_t)btok * (uint32_t)nb * 2u;
+  // the 5th dword can lie past the matrix: buffer loads bound it (out-of-range dwords read
+  // as zero)
+  const uint32_t mat_bytes = kTiled ? (uint32_t)nb * kTileBlk : (uint32_t)P.N * (uint32_t)nb * (uint32_t)kBlockBytes;
+  // tiled: the resources cover this row tile's blocks; lanes of the second k half aim their
+  // scale loads out of range (the scale MFMA's k = 4..7 terms must be zero)
+  const uint8_t* wbase = kTiled ? P.W + (size_t)rt * (size_t)nb * kTileBlk : P.W;
+  const uint32_t aq_v = (uint32_t)c * 32u + 16u * (uint32_t)h;
+  const uint32_t ad_v = h ? kNoBlk : kTileQ + 2u * (uint32_t)c;
+  const uint32_t bq_v = (uint32_t)btok * 32u + 16u * (uint32_t)h;
+  const uint32_t bd_v = h ? kNoBlk : (uint32_t)btok * 2u;
+  const uint32_t x_bytes = (uint32_t)P.T * (uint32_t)P.K;
+  const uint32_t xd_bytes = (uint32_t)P.T * (uint32_t)nb * 2u;
   auto load_ops = [&](int b, bool real, Ops& o) {
     if constexpr (kTiled) {
-      const uint32_t sa = real ? (uint32_t)b * a_step : kNoBlk;
-      const uint32_t sq = real ? (uint32_t)b * (uint32_t)P.T * 32u : kNoBlk;
-      const uint32_t sd = real ? (uint32_t)b * (uint32_t)P.T * 2u : kNoBlk;
-      o.w03 = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)(sa + a_lane), 0, 0));
-      o.w4 = __builtin_amdgcn_raw_buffer_load_b32(wr, (int)(sa + a_lane + 16u), 0, 0);
-      o.wdw = __builtin_amdgcn_raw_buffer_load_b16(wr, (int)(sa + row_off), 0, 0);
-      o.bq = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)(sq + xq_of(0)), 0, 0));
-      o.xdw = __builtin_amdgcn_raw_buffer_load_b16(xdr, (int)(sd + xd_of(0)), 0, 0);
+      // past the last block: resources of no records (every load reads zeros)
+      const __amdgpu_buffer_rsrc_t wr =
+          __builtin_amdgcn_make_buffer_rsrc((void*)wbase, 0, real ? (int)mat_bytes : 0, 0x00020000);
+      const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)P.Xq, 0, real ? (int)x_bytes : 0, 0x00020000);
+      const __amdgpu_buffer_rsrc_t xdr =
+          __builtin_amdgcn_make_buffer_rsrc((void*)P.Xd, 0, real ? (int)((xd_bytes + 3u) & ~3u) : 0, 0x00020000);
+      const int bb = real ? b : 0;
+      const int sa = (int)((uint32_t)bb * kTileBlk);
+      const int sq = (int)((uint32_t)bb * (uint32_t)P.T * 32u);
+      const int sd = (int)((uint32_t)bb * (uint32_t)P.T * 2u);
+      o.w03 = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)aq_v, sa, 0));
+      o.wdw = __builtin_amdgcn_raw_buffer_load_b16(wr, (int)ad_v, sa, 0);
+      o.bq = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)bq_v, sq, 0));
+      o.xdw = __builtin_amdgcn_raw_buffer_load_b16(xdr, (int)bd_v, sd, 0);
     } else {
-      const uint32_t off = row_off + (uint32_t)b * a_step;
+      const __amdgpu_buffer_rsrc_t wr =
+          __builtin_amdgcn_make_buffer_rsrc((void*)P.W, 0, (int)((mat_bytes + 3u) & ~3u), 0x00020000);
+      const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)P.Xq, 0, (int)x_bytes, 0x00020000);
+      const __amdgpu_buffer_rsrc_t xdr =
+          __builtin_amdgcn_make_buffer_rsrc((void*)P.Xd, 0, (int)((xd_bytes + 3u) & ~3u), 0x00020000);
+      const uint32_t off = row_off + (uint32_t)b * kBlockBytes;
       const uint32_t base = real ? (off + 2u + 16u * (uint32_t)h) & ~3u : kNoBlk;
       o.w03 = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)base, 0, 0));
       o.w4 = __builtin_amdgcn_raw_buffer_load_b32(wr, (int)(base + 16u), 0, 0);
       o.wdw = __builtin_amdgcn_raw_buffer_load_b32(wr, real ? (int)(off & ~3u) : (int)kNoBlk, 0, 0);
-      o.bq = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, real ? (int)xq_of(b) : (int)kNoBlk, 0, 0));
-      o.xdw = __builtin_amdgcn_raw_buffer_load_b32(xdr, real ? (int)(xd_of(b) & ~3u) : (int)kNoBlk, 0, 0);
+      o.bq = __builtin_bit_cast(
+          v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, real ? (int)(xrow_off + 32u * (uint32_t)b) : (int)kNoBlk, 0, 0));
+      o.xdw = __builtin_amdgcn_raw_buffer_load_b32(
+          xdr, real ? (int)((xd_off + 2u * (uint32_t)b) & ~3u) : (int)kNoBlk, 0, 0);
     }
   };
   // fold block b into the leaf's 16 running sums: exact MFMA dots isum, the exact scale
-  // products wd*xd as an fp32 MFMA outer product (A lane: its row's wd in k = 0, zero in
-  // k = 1; B lane: its token's xd in k = 0, zero in k = 1; a product of two fp16 values is
-  // exact in fp32 and the zero terms add nothing), then v = fma(wd*xd, isum, v) per element
+  // products wd*xd as an MFMA outer product (A lane: its row's wd in k = 0, zero in the
+  // other k; B lane: its token's xd in k = 0; a product of two fp16 values is exact in fp32
+  // and the zero terms add nothing), then v = fma(wd*xd, isum, v) per element
   auto fold_ops = [&](const Ops& o, int b, float (&v)[16]) {
-    const uint32_t off = row_off + (uint32_t)b * a_step;
-    const uint32_t sh = kTiled ? a_sh : (off + 2u + 16u * (uint32_t)h) & 3u;   // 0 or 2
-    v4i a;
-    a.x = (int)__builtin_amdgcn_alignbyte((uint32_t)o.w03.y, (uint32_t)o.w03.x, sh);
-    a.y = (int)__builtin_amdgcn_alignbyte((uint32_t)o.w03.z, (uint32_t)o.w03.y, sh);
-    a.z = (int)__builtin_amdgcn_alignbyte((uint32_t)o.w03.w, (uint32_t)o.w03.z, sh);
-    a.w = (int)__builtin_amdgcn_alignbyte(o.w4, (uint32_t)o.w03.w, sh);
-    const float wd = kTiled ? lt_h2f((uint16_t)o.wdw) : lt_h2f((uint16_t)((off & 2u) ? (o.wdw >> 16) : (o.wdw & 0xFFFFu)));
-    const float xd = kTiled ? lt_h2f((uint16_t)o.xdw)
-                            : lt_h2f((uint16_t)((xd_of(b) & 2u) ? (o.xdw >> 16) : (o.xdw & 0xFFFFu)));
     const v16i z = {};
-    const v16i isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, o.bq, z, 0, 0, 0);
     const v16f zf = {};
-    const v16f sc = __builtin_amdgcn_mfma_f32_32x32x2f32(h == 0 ? wd : 0.0f, h == 0 ? xd : 0.0f, zf, 0, 0, 0);
+    v16i isum;
+    v16f sc;
+    if constexpr (kTiled) {
+      isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.w03, o.bq, z, 0, 0, 0);
+      // the 16-bit loads zero-extend: {scale, 0, 0, 0} as fp16 (zeros in the other k half)
+      const u32x2 aw = {o.wdw, 0u}, bw = {o.xdw, 0u};
+      sc = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(h4, aw), __builtin_bit_cast(h4, bw), zf, 0, 0, 0);
+    } else {
+      const uint32_t off = row_off + (uint32_t)b * kBlockBytes;
+      const uint32_t sh = (off + 2u + 16u * (uint32_t)h) & 3u;   // 0 or 2
+      v4i a;
+      a.x = (int)__builtin_amdgcn_alignbyte((uint32_t)o.w03.y, (uint32_t)o.w03.x, sh);
+      a.y = (int)__builtin_amdgcn_alignbyte((uint32_t)o.w03.z, (uint32_t)o.w03.y, sh);
+      a.z = (int)__builtin_amdgcn_alignbyte((uint32_t)o.w03.w, (uint32_t)o.w03.z, sh);
+      a.w = (int)__builtin_amdgcn_alignbyte(o.w4, (uint32_t)o.w03.w, sh);
+      const float wd = lt_h2f((uint16_t)((off & 2u) ? (o.wdw >> 16) : (o.wdw & 0xFFFFu)));
+      const float xd = lt_h2f((uint16_t)(((xd_off + 2u * (uint32_t)b) & 2u) ? (o.xdw >> 16) : (o.xdw & 0xFFFFu)));
+      isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, o.bq, z, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(h == 0 ? wd : 0.0f, h == 0 ? xd : 0.0f, zf, 0, 0, 0);
+    }
 #pragma unroll
     for (int r = 0; r < 16; r++) v[r] = fmaf(sc[r], (float)isum[r], v[r]);
   };
@@ -342,23 +361,24 @@ __global__ void k_len_add(int* __restrict__ len, int T, int maxt) {
   }
 }
 
-// The tile-major copy of a Q8_0 matrix: tile rt, block b holds rows 32*rt .. 32*rt+31 of
-// block b, 34 bytes each (rows past N are zero).  One 2-byte unit per thread, written in
-// order.
+// The tile-major copy of a Q8_0 matrix: tile rt, block b holds the quants of rows
+// 32*rt .. 32*rt+31 of block b (32 bytes each), then their fp16 scales (rows past N are
+// zero).  One 2-byte unit per thread, written in order.
 __global__ __launch_bounds__(256) void k_q8_tiles(const uint16_t* __restrict__ W, uint16_t* __restrict__ Wt, int N,
                                                   int nb, uint32_t units) {
   constexpr uint32_t kUnits = kBlockBytes / 2;             // 17 per block
+  constexpr uint32_t kTileUnits = kTileBlk / 2;            // 544 per tile block
   for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < units; i += gridDim.x * 256u) {
-    const uint32_t chunk = i / (32u * kUnits), j = i - chunk * 32u * kUnits;
+    const uint32_t chunk = i / kTileUnits, j = i - chunk * kTileUnits;
     const uint32_t rt = chunk / (uint32_t)nb, b = chunk - rt * (uint32_t)nb;
-    const uint32_t r = j / kUnits, u = j - r * kUnits;
+    // units 0..511: row j/16's quant pair j%16 (block unit 1 + j%16); 512..543: the scale
+    // of row j-512 (block unit 0)
+    const uint32_t r = j < 512u ? j >> 4 : j - 512u;
+    const uint32_t u = j < 512u ? 1u + (j & 15u) : 0u;
     const uint32_t row = rt * 32u + r;
     Wt[i] = row < (uint32_t)N ? W[((size_t)row * nb + b) * kUnits + u] : (uint16_t)0;
   }
 }
-
-// Block-major activation quants: block b of token t goes to slot b*T + t (lt_quant_q8's
-// quantizer on each 32-element block of x [T][K]); a half-wave per output block, in order.
 __global__ __launch_bounds__(256) void k_quant_q8_bm(const float* __restrict__ x, int8_t* __restrict__ xq,
                                                      uint16_t* __restrict__ xd, int T, int nbk) {
   const long ob = (long)blockIdx.x * 8 + (threadIdx.x >> 5);

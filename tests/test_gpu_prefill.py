@@ -71,12 +71,14 @@ def test_q8_gemm_silu(gpu, oracle, F, K, T):
 
 
 def tiles_host(W, N, K):
-    """The tile-major layout restated on the host: Wt[rt][b][r] = row 32*rt + r's block b."""
+    """The tile-major layout restated on the host: tile block (rt, b) = the 32 quant bytes of
+    rows 32*rt .. 32*rt+31 of block b, then their 32 fp16 scales (1088 bytes)."""
     nb = K // 32
     nt = (N + 31) // 32
     pad = np.zeros((nt * 32, nb * 34), np.uint8)
     pad[:N] = W
-    return pad.reshape(nt, 32, nb, 34).transpose(0, 2, 1, 3).copy()
+    blk = pad.reshape(nt, 32, nb, 34).transpose(0, 2, 1, 3)          # [rt][b][r][34]
+    return np.concatenate([blk[..., 2:].reshape(nt, nb, 1024), blk[..., :2].reshape(nt, nb, 64)], axis=2)
 
 
 @pytest.mark.parametrize("N,K", [(1152, 896), (100, 96), (33, 4864), (32, 32)])
@@ -110,8 +112,21 @@ def test_quant_q8_block_major(gpu, oracle, T, K):
         assert np.array_equal(gd[:, t], d), f"token {t} scales"
 
 
+def subnormal_scales(rng, W, xd, frac=0.25):
+    """Replaces a fraction of the weight and activation scales by fp16 subnormals (bits
+    0x0001 .. 0x03FF, either sign): the scale products must stay exact."""
+    nb = xd.shape[1]
+    sc = W.reshape(W.shape[0], nb, 34)[..., :2].copy().view(np.uint16)[..., 0]
+    m = rng.random(sc.shape) < frac
+    sc[m] = rng.integers(1, 0x400, m.sum()).astype(np.uint16) | (rng.integers(0, 2, m.sum()) << 15).astype(np.uint16)
+    W.reshape(W.shape[0], nb, 34)[..., :2] = sc[..., None].view(np.uint8).reshape(W.shape[0], nb, 2)
+    m = rng.random(xd.shape) < frac
+    xd[m] = rng.integers(1, 0x400, m.sum()).astype(np.uint16)
+
+
 @pytest.mark.parametrize("N,K,T,epi", [(1152, 896, 37, "bias"), (896, 4864, 130, "resid"), (100, 96, 5, "store"),
-                                       (64, 1024, 129, "store"), (4096, 4096, 33, "store"), (40, 14336, 3, "resid")])
+                                       (64, 1024, 129, "store"), (4096, 4096, 33, "store"), (40, 14336, 3, "resid"),
+                                       (96, 256, 70, "subnormal")])
 def test_q8_gemm_tiled_matches_gemv_per_token(gpu, oracle, N, K, T, epi):
     case(f"q8_gemm_t N={N} K={K} T={T} {epi}")
     rng = np.random.default_rng(33)
@@ -122,6 +137,9 @@ def test_q8_gemm_tiled_matches_gemv_per_token(gpu, oracle, N, K, T, epi):
     xd = np.empty((T, K // 32), np.uint16)
     for t in range(T):
         xq[t], xd[t] = oracle.quant_q8(X[t])
+    if epi == "subnormal":
+        subnormal_scales(rng, W, xd)
+        epi = "store"
     xq_bm = np.ascontiguousarray(xq.reshape(T, K // 32, 32).transpose(1, 0, 2))
     xd_bm = np.ascontiguousarray(xd.T)
     bias = (rng.standard_normal(N) * 0.02).astype(np.float32) if epi == "bias" else None
