@@ -20,6 +20,7 @@
 #include "lt_q8_device.h"
 
 #include <cstdlib>
+#include <mutex>
 
 namespace {
 
@@ -318,8 +319,19 @@ __device__ __forceinline__ void stage_to_rec(const StageRegs<NT>& R, int K, uint
 // zeros without touching memory, so the loop issues every load unconditionally (the
 // compiler's load counters stay exact and the loads pipeline).
 constexpr uint32_t kNoBlock = 0x80000000u;
+// Staged streaming (kStg): a workgroup whose 64 rows are contiguous and one 32-block item
+// each (K <= 1024) reads its whole region -- at most 64 x 32 blocks -- as coalesced
+// non-temporal 16-byte loads (kStgLoads per thread, issued before the prologue), parks it
+// in LDS, and every half-wave then folds its rows' blocks from there: the same raw dwords
+// and arithmetic as the per-lane block loads, with whole cache lines per load instruction.
+// It is used when the whole grid is resident at once (the 0.5B gate|up GEMV: every load
+// of the launch is in flight from its start); a grid of several rounds (the vocab GEMV)
+// streams better through the per-lane ring, which overlaps loads and folds.
+constexpr int kStgRows = 64;
+constexpr int kStgLoads = (kStgRows * 32 * (int)kBlockBytes + 4095) / 4096;   // 17
+constexpr uint32_t kStgBytes = (uint32_t)kStgLoads * 4096u + 16u;   // + the last block's 9th dword
 
-template <int KS, Pro PRO, Epi EPI, int D>
+template <int KS, Pro PRO, Epi EPI, int D, bool kStg = false>
 __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int K = P.K;
@@ -366,6 +378,18 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
   const __amdgpu_buffer_rsrc_t wrsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)P.W, 0, (int)((mat_bytes + 3u) & ~3u), 0x00020000);
 
+  // staged: the workgroup's region (rows past N read zeros)
+  u32x4 stg[kStg ? kStgLoads : 1];
+  if constexpr (kStg) {
+    const int r0 = blockIdx.x * kStgRows;
+    const int nr = P.N - r0 < kStgRows ? P.N - r0 : kStgRows;
+    const uint32_t region = (uint32_t)nr * (uint32_t)nb * (uint32_t)kBlockBytes;
+    const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(P.W + (size_t)r0 * (size_t)nb * kBlockBytes), 0, (int)((region + 3u) & ~3u), 0x00020000);
+#pragma unroll
+    for (int i = 0; i < kStgLoads; i++)
+      stg[i] = __builtin_amdgcn_raw_buffer_load_b128(srsrc, (int)(threadIdx.x * 16u + (uint32_t)i * 4096u), 0, 2);
+  }
   RawBlock ring[D];
   int is = 0, ik = 0;                                                   // next item to issue
   uint32_t issue_row = (uint32_t)rbase * (uint32_t)nb * (uint32_t)kBlockBytes;
@@ -381,8 +405,10 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
     is++;
     if (++ik == nk) { ik = 0; issue_row += row_step_bytes; }
   };
+  if constexpr (!kStg) {
 #pragma unroll
-  for (int d = 0; d < D; d++) issue(ring[d]);
+    for (int d = 0; d < D; d++) issue(ring[d]);
+  }
   // the epilogue's residuals, fetched with the weights
   float rpre[kResidPre];
   if constexpr (EPI == EPI_RESID) {
@@ -432,6 +458,16 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
     const float inv = rms_inv<KS>(S, K, P.eps, red, sinv);
     slots_to_rec<KS, true>(S, nullptr, P.nw, inv, K, rec);
   }
+  // staged: the region into LDS, after the prologue's buffers (the host sizes the launch's
+  // LDS the same way)
+  const uint32_t stage_off = (uint32_t)(kThreads + 4) * 4u + (uint32_t)((nb * kRecDwords + 3) & ~3) * 4u +
+                             ((PRO == PRO_STAGE || PRO == PRO_MERGE) ? (uint32_t)((K + 15) & ~15) : 0u) +
+                             (PRO == PRO_EMBED_RMS ? (uint32_t)((K + 15) & ~15) + (uint32_t)K * 4u : 0u);
+  const uint32_t* stage = (const uint32_t*)(smem + stage_off);
+  if constexpr (kStg) {
+#pragma unroll
+    for (int i = 0; i < kStgLoads; i++) *(u32x4*)(smem + stage_off + threadIdx.x * 16u + (uint32_t)i * 4096u) = stg[i];
+  }
   __syncthreads();
   // @phase gemv 2
 
@@ -441,50 +477,70 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
   float acc = 0.0f;
   int fm = 0, fi = 0, fk = 0;         // item being folded: index, row, slot
   uint32_t fold_row = (uint32_t)rbase * (uint32_t)nb * (uint32_t)kBlockBytes;
-  // all trips but the last refill the ring; the last one only drains it
-  auto fold_item = [&](RawBlock& r, bool refill) {
-    const int b = lane + 32 * fk;
-    const bool odd = ((fold_row + lane_bytes + (uint32_t)fk * kSlotBytes) & 2u) != 0;
-    const float folded = fold_raw(r, odd, rec + (b < nb ? b : 0) * kRecDwords, acc);
-    acc = (fm < total && b < nb) ? folded : acc;
-    if (refill) issue(r);
-    fm++;
-    if (++fk == nk) {                   // row end: the same item for both half-waves
-      const float v = halfwave_tree_dpp(acc);   // the row value, on lane 0 of the half-wave
-      const int row = rbase + step * fi;
-      if (lane == 0 && fi < nrows) {
-        if constexpr (EPI == EPI_SILU) {
-          s_rows[row - blockIdx.x * kSiluRows] = v;
-        } else {
-          float o = v;
-          if constexpr (EPI == EPI_RESID) {
-            float rv = 0.0f;
-            if (fi < kResidPre) {
+  // a finished row: the tree (the row value lands on lane 0 of the half-wave), then the
+  // epilogue for row rbase + step * fi
+  auto finish_row = [&](float a, int ri) {
+    const float v = halfwave_tree_dpp(a);
+    const int row = rbase + step * ri;
+    if (lane == 0 && ri < nrows) {
+      if constexpr (EPI == EPI_SILU) {
+        s_rows[row - blockIdx.x * kSiluRows] = v;
+      } else {
+        float o = v;
+        if constexpr (EPI == EPI_RESID) {
+          float rv = 0.0f;
+          if (ri < kResidPre) {
 #pragma unroll
-              for (int i = 0; i < kResidPre; i++)   // static indices keep rpre in registers
-                if (fi == i) rv = rpre[i];
-            } else {
-              rv = P.resid[row];
-            }
-            o = v + rv;
+            for (int i = 0; i < kResidPre; i++)   // static indices keep rpre in registers
+              if (ri == i) rv = rpre[i];
+          } else {
+            rv = P.resid[row];
           }
-          P.y[row] = o;
-          if (EPI == EPI_ARGMAX && am_better(o, row, bv, bi)) { bv = o; bi = row; }
+          o = v + rv;
         }
+        P.y[row] = o;
+        if (EPI == EPI_ARGMAX && am_better(o, row, bv, bi)) { bv = o; bi = row; }
       }
-      acc = 0.0f;
-      fk = 0;
-      fi++;
-      fold_row += row_step_bytes;
     }
   };
-  for (int t = 0; t + 1 < trips; t++) {
+  if constexpr (kStg) {
+    // row hw + 8i of the region: lane L folds block L from LDS (lanes past nb fold lane 0's
+    // block and discard it)
+    const int lb = lane < nb ? lane : 0;
 #pragma unroll
-    for (int d = 0; d < D; d++) fold_item(ring[d], true);
-  }
-  if (trips > 0) {
+    for (int i = 0; i < kStgRows / 8; i++) {
+      const uint32_t off = (uint32_t)(hw + 8 * i) * (uint32_t)nb * (uint32_t)kBlockBytes + (uint32_t)lb * kBlockBytes;
+      RawBlock r;
 #pragma unroll
-    for (int d = 0; d < D; d++) fold_item(ring[d], false);
+      for (int k = 0; k < 9; k++) r.w[k] = stage[(off >> 2) + k];
+      const float folded = fold_raw(r, (off & 2u) != 0, rec + lb * kRecDwords, 0.0f);
+      finish_row(lane < nb ? folded : 0.0f, i);
+    }
+  } else {
+    // all trips but the last refill the ring; the last one only drains it
+    auto fold_item = [&](RawBlock& r, bool refill) {
+      const int b = lane + 32 * fk;
+      const bool odd = ((fold_row + lane_bytes + (uint32_t)fk * kSlotBytes) & 2u) != 0;
+      const float folded = fold_raw(r, odd, rec + (b < nb ? b : 0) * kRecDwords, acc);
+      acc = (fm < total && b < nb) ? folded : acc;
+      if (refill) issue(r);
+      fm++;
+      if (++fk == nk) {                   // row end: the same item for both half-waves
+        finish_row(acc, fi);
+        acc = 0.0f;
+        fk = 0;
+        fi++;
+        fold_row += row_step_bytes;
+      }
+    };
+    for (int t = 0; t + 1 < trips; t++) {
+#pragma unroll
+      for (int d = 0; d < D; d++) fold_item(ring[d], true);
+    }
+    if (trips > 0) {
+#pragma unroll
+      for (int d = 0; d < D; d++) fold_item(ring[d], false);
+    }
   }
 
   // @phase gemv 3
@@ -582,29 +638,47 @@ int env_rows() {
   return env;
 }
 
+// Resident workgroups of a kernel at an LDS size, cached per (kernel, LDS size).
 template <typename Kern>
 int resident_wgs(Kern kern, size_t shm, int num_cus) {
-  static size_t cached_shm[8];
-  static int cached_n[8];
+  constexpr int kCache = 32;
+  static const void* cached_k[kCache];
+  static size_t cached_shm[kCache];
+  static int cached_n[kCache];
   static int used = 0;
+  static std::mutex mu;   // launches may come from several host threads
+  std::lock_guard<std::mutex> lock(mu);
+  const void* key = (const void*)kern;
   for (int i = 0; i < used; i++)
-    if (cached_shm[i] == shm) return cached_n[i];
+    if (cached_k[i] == key && cached_shm[i] == shm) return cached_n[i];
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, shm) != hipSuccess || per_cu < 1)
     per_cu = 1;
   const int n = per_cu * (num_cus > 0 ? num_cus : 1);
-  if (used < 8) { cached_shm[used] = shm; cached_n[used] = n; used++; }
+  if (used < kCache) { cached_k[used] = key; cached_shm[used] = shm; cached_n[used] = n; used++; }
   return n;
+}
+
+// LT_GEMV_STAGE=0 keeps the 64-row mapping on per-lane block loads (for comparisons).
+bool use_stage() {
+  static const bool on = [] {
+    const char* s = getenv("LT_GEMV_STAGE");
+    return !(s && s[0] == '0');
+  }();
+  return on;
 }
 
 template <int KS, Pro PRO, Epi EPI, int D>
 hipError_t launch_gemv_k(GemvParams P, size_t shm, hipStream_t st, int num_cus, int* grid_out) {
   auto kern = k_gemv_fused<KS, PRO, EPI, D>;
   const int groups = (P.N + 7) / 8;
+  const bool one_item = (P.K / 32 + 31) / 32 == 1;
   int grid;
+  bool stg = false;   // the 64-row mapping with one item per row: staged streaming
   if (EPI == EPI_SILU) {
     P.row0 = kSiluRows; P.step = 8; P.max_rows = kSiluRows / 8;
     grid = P.N / kSiluRows;
+    stg = one_item;
   } else if (env_rows() > 0) {
     const int R = env_rows();
     P.row0 = R; P.step = 8; P.max_rows = R / 8;
@@ -614,11 +688,11 @@ hipError_t launch_gemv_k(GemvParams P, size_t shm, hipStream_t st, int num_cus, 
     if (groups <= cap) {
       P.row0 = 8; P.step = 8; P.max_rows = 1;
       grid = groups;
-    } else if ((P.K / 32 + 31) / 32 == 1) {
-      // rows of one item (K <= 1024): 64 contiguous rows per workgroup (measured best for
-      // the 151936 x 896 vocab GEMV: 5.5-5.65 TB/s, against 5.0-5.2 with fewer, longer blocks)
-      P.row0 = 64; P.step = 8; P.max_rows = 8;
-      grid = (P.N + 63) / 64;
+    } else if (one_item) {
+      // rows of one item (K <= 1024): 64 contiguous rows per workgroup, streamed staged
+      P.row0 = kStgRows; P.step = 8; P.max_rows = kStgRows / 8;
+      grid = (P.N + kStgRows - 1) / kStgRows;
+      stg = true;
     } else {
       // workgroups walking contiguous blocks of rows (their half-waves 8 rows apart), about
       // half a resident wave of them: every workgroup streams one region of the matrix
@@ -629,6 +703,15 @@ hipError_t launch_gemv_k(GemvParams P, size_t shm, hipStream_t st, int num_cus, 
     }
   }
   if (grid_out) *grid_out = grid;
+  if constexpr (D == 8 && KS <= 4) {
+    if (stg && use_stage()) {
+      auto skern = k_gemv_fused<KS, PRO, EPI, D, true>;
+      if (grid <= resident_wgs(skern, shm + kStgBytes, num_cus)) {
+        skern<<<grid, kThreads, shm + kStgBytes, st>>>(P);
+        return hipGetLastError();
+      }
+    }
+  }
   kern<<<grid, kThreads, shm, st>>>(P);
   return hipGetLastError();
 }
