@@ -57,8 +57,8 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 // both operands of a block are coalesced, aligned loads; the arithmetic and the order are
 // those of the row-major layouts.
 template <GemmEpi EPI, bool kTiled>
-__global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
-  __shared__ float s_st4[kGemmWaves][16 * 64];   // tree level 4 of each wave's 32 x 32 tile
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_q8_gemm(GemmParams P) {
+  __shared__ float s_st[kGemmWaves][3][16 * 64];   // tree levels 2..4 of each wave's 32 x 32 tile
   const int wave = threadIdx.x >> 6;
   const int l = threadIdx.x & 63;
   const int h = l >> 5;
@@ -189,32 +189,37 @@ __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
 #pragma unroll
   for (int d = 0; d < kDepth; d++) produce(ring[d]);
 
-  float st[4][16];   // pending partial sums of the tree, levels 0..3 (level 4: s_st4)
+  // pending partial sums of the tree: levels 0 and 1 in registers; levels 2..4, parked at
+  // most once per 4 leaves, in LDS
+  float st[2][16];
   float v[16];
 #pragma unroll
   for (int r = 0; r < 16; r++) {
     v[r] = 0.0f;
   }
 #pragma unroll
-  for (int l2 = 0; l2 < 4; l2++)
+  for (int l2 = 0; l2 < 2; l2++)
 #pragma unroll
     for (int r = 0; r < 16; r++) st[l2][r] = 0.0f;
   // combine leaf i into the stack: it closes every level whose bit is set in i (its
-  // trailing ones: left subtree st[lvl] + right subtree v, the reference tree's pairing)
-  // and parks the sum at the first clear level.  i is uniform, so these are scalar
-  // branches around static register indices.
+  // trailing ones: left subtree (the parked sum) + right subtree v, the reference tree's
+  // pairing, level by level from the bottom) and parks the sum at the first clear level.
+  // i is uniform, so these are scalar branches around static register indices.
   auto close_leaf = [&](int i) {
     const int t1 = __builtin_ctz(~(unsigned)i);   // trailing ones, 0..5
 #pragma unroll
-    for (int lvl = 0; lvl < 4; lvl++) {
+    for (int lvl = 0; lvl < 2; lvl++) {
       if (lvl < t1) {
 #pragma unroll
         for (int r = 0; r < 16; r++) v[r] = st[lvl][r] + v[r];
       }
     }
-    if (t1 == 5) {   // level 4 (parked by leaf 15) lives in LDS
 #pragma unroll
-      for (int r = 0; r < 16; r++) v[r] = s_st4[wave][r * 64 + l] + v[r];
+    for (int lvl = 2; lvl < 5; lvl++) {
+      if (lvl < t1) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) v[r] = s_st[wave][lvl - 2][r * 64 + l] + v[r];
+      }
     }
     switch (t1) {
       case 0:
@@ -226,28 +231,49 @@ __global__ __launch_bounds__(256) void k_q8_gemm(GemmParams P) {
         for (int r = 0; r < 16; r++) st[1][r] = v[r];
         break;
       case 2:
-#pragma unroll
-        for (int r = 0; r < 16; r++) st[2][r] = v[r];
-        break;
       case 3:
-#pragma unroll
-        for (int r = 0; r < 16; r++) st[3][r] = v[r];
-        break;
       case 4:
 #pragma unroll
-        for (int r = 0; r < 16; r++) s_st4[wave][r * 64 + l] = v[r];
+        for (int r = 0; r < 16; r++) s_st[wave][t1 - 2][r * 64 + l] = v[r];
         break;
       default:   // i == 31: every level closed, v is the row value (kept in v)
         break;
     }
   };
   int ci = 0, cb = 0;   // consumer: leaf, block
+  // tiled: the MFMAs run one block ahead of the fold (two result sets, A and B, alternate
+  // with the slot's parity, so nothing is copied), and a fold never waits for its own MFMAs
+  static_assert(kDepth % 2 == 0, "k_q8_gemm: the A/B result sets alternate over an even ring");
+  v16i isA, isB;
+  v16f scA, scB;
+  auto mfma_tiled = [&](const Ops& o, v16i& isum, v16f& sc) {
+    const v16i z = {};
+    const v16f zf = {};
+    isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.w03, o.bq, z, 0, 0, 0);
+    // the 16-bit loads zero-extend: {scale, 0, 0, 0} as fp16 (zeros in the other k half)
+    const u32x2 aw = {o.wdw, 0u}, bw = {o.xdw, 0u};
+    sc = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(h4, aw), __builtin_bit_cast(h4, bw), zf, 0, 0, 0);
+  };
+  if constexpr (kTiled) mfma_tiled(ring[0], isA, scA);
   for (int s0 = 0; s0 < nb; s0 += kDepth) {
 #pragma unroll
     for (int d = 0; d < kDepth; d++) {
       // every slot folds and refills (loads on all paths keep the load counters exact):
       // past the last block a slot holds zeros, and v + 0*0 leaves v unchanged
-      fold_ops(ring[d], cb, v);
+      if constexpr (kTiled) {
+        // slot d + 1 holds the next block (slot 0 was refilled with it at d = 0)
+        if (d % 2 == 0) {
+          mfma_tiled(ring[(d + 1) % kDepth], isB, scB);
+#pragma unroll
+          for (int r = 0; r < 16; r++) v[r] = fmaf(scA[r], (float)isA[r], v[r]);
+        } else {
+          mfma_tiled(ring[(d + 1) % kDepth], isA, scA);
+#pragma unroll
+          for (int r = 0; r < 16; r++) v[r] = fmaf(scB[r], (float)isB[r], v[r]);
+        }
+      } else {
+        fold_ops(ring[d], cb, v);
+      }
       produce(ring[d]);
       if (s0 + d < nb) {
         cb += 32;
