@@ -499,12 +499,21 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   constexpr int kVRing = (kStep ? kVRingDwStep : kVRingDw) / VD / kEg * kEg;   // V rows in flight
   const int per_up = (A.per_max + kVRing - 1) / kVRing * kVRing;   // per_max rounded to whole rings
   const int srow = per_up + kEg;                    // the spare score row
+  // The step with 64 fp16 dims (a V row is 128 bytes): V streams in chunks of kCR rows, one
+  // 16-byte load per lane (8 lanes per row), kNC chunks in flight, and each chunk passes
+  // through 1 KB of LDS to the lanes' dims -- 8x fewer load instructions than a row per
+  // load, so a whole short context is in flight at once.
+  constexpr bool kChunk = kStep && kF16 && DPL == 1;
+  constexpr int kCR = 8;                            // rows per chunk (one exp group)
+  constexpr int kNC = 24;                           // chunks in flight
+  static_assert(!kChunk || kCR == kEg, "k_attn_w1: a V chunk is one exp group");
   constexpr int kPR = HPW >= 2 ? 32 : 64;           // positions per score round
   static_assert(KU >= 8 && KU <= 32, "k_attn_w1: unsupported head size / cache type");
   float* sq = lds;                                  // [HPW][HD] q (roped in a step); then the outputs
   u32x4* sk = (u32x4*)(lds + HPW * HD);             // [kPR][KU + 1] one round of K rows, padded
   u32x4* sfk = sk + kPR * (KU + 1);                 // step: the new K row, then the new V row (cache format)
   float* se = (float*)(sfk + (kStep ? 2 * KU : 0)); // [per_up + kEg + 1][HPW]: rows (zero past n), spare
+  uint32_t* sv = (uint32_t*)(se + ((per_up + kEg + 1) * HPW + 3) / 4 * 4);   // kChunk: 2 x 1 KB
   const int l = threadIdx.x;
   const int sp = blockIdx.x;
   const int h0 = blockIdx.y * HPW;
@@ -577,6 +586,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     }
   };
 
+  // chunk c: rows c*kCR + l/8, bytes (l%8)*16 of each (rows past nv read zeros)
+  auto load_chunk = [&](int c, u32x4& dst) {
+    const uint32_t off = base + (uint32_t)(c * kCR + (l >> 3)) * pitch + (uint32_t)(l & 7) * 16u;
+    dst = __builtin_amdgcn_raw_buffer_load_b128(vrsrc, (int)off, 0, 0);
+  };
+
   // @phase attn 0
   // Scores run in rounds of kPR positions.  With HPW >= 2 the two half-waves take half of
   // the heads each for the same 32 positions (lane l: position t0 + l%32, heads
@@ -609,7 +624,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   // (the fences keep the ring's loads in the order its rows are consumed, so each row
   // waits for its own load only)
   uint32_t v[kVRing][VD];
-  if (kStep) {
+  u32x4 vch[kChunk ? kNC : 1];
+  if (kChunk) {
+#pragma unroll
+    for (int k = 0; k < kNC; k++) {
+      load_chunk(k, vch[k]);
+      asm volatile("" ::: "memory");
+    }
+  } else if (kStep) {
 #pragma unroll
     for (int k = 0; k < kVRing; k++) {
       load_v(k, v[k]);
@@ -828,6 +850,38 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   };
   float ec[kEg][HPW], en[kEg][HPW];
   read_e(0, ec);
+  if constexpr (kChunk) {
+    // chunk c: through LDS buffer c % 2 (a wave's LDS operations complete in order, so a
+    // buffer is rewritten only after the reads of the chunk before), its kCR rows folded
+    // in order, its register slot refilled with chunk c + kNC.  (Writing and reading chunk
+    // c + 1 during chunk c's fold measured slower: its conditional stage makes the load
+    // waits conservative.)
+    const int nch = (n + kCR - 1) / kCR;
+    for (int c0 = 0; c0 < nch; c0 += kNC) {
+#pragma unroll
+      for (int k = 0; k < kNC; k++) {
+        const int c = c0 + k;
+        if (c >= nch) break;
+        read_e((c + 1) * kCR, en);
+        u32x4 x = vch[k];
+        asm volatile("" : "+v"(x.x), "+v"(x.y), "+v"(x.z), "+v"(x.w) : : "memory");
+        uint32_t* buf = sv + (k & 1) * 256;
+        *(u32x4*)&buf[l * 4] = x;
+        load_chunk(c + kNC, vch[k]);
+        const uint16_t* b16 = (const uint16_t*)buf;
+#pragma unroll
+        for (int j = 0; j < kCR; j++) {
+          const float x0 = lt_h2f(b16[j * 64 + l]);
+#pragma unroll
+          for (int r = 0; r < HPW; r++) o[r][0] = fmaf(ec[j][r], x0, o[r][0]);
+        }
+#pragma unroll
+        for (int j = 0; j < kEg; j++)
+#pragma unroll
+          for (int r = 0; r < HPW; r++) ec[j][r] = en[j][r];
+      }
+    }
+  } else
   for (int t0 = 0; t0 < n; t0 += kVRing) {
 #pragma unroll
     for (int k0 = 0; k0 < kVRing; k0 += kEg) {
@@ -1043,7 +1097,8 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
   const int ring = (mode == AM_STEP ? kVRingDwStep : kVRingDw) / (vb < 4 ? 1 : vb / 4) / 8 * 8;   // V rows in flight
   const size_t per_up = (size_t)(per_max + ring - 1) / ring * ring;
   const size_t w1_shm = ((size_t)h * A.hd + (kpr * (ku + 1) + (mode == AM_STEP ? 2 * ku : 0)) * 4 +
-                         (per_up + 8 + 1) * h) * sizeof(float);
+                         ((per_up + 8 + 1) * h + 3) / 4 * 4) * sizeof(float) +
+                        (mode == AM_STEP && f16 && dpl == 1 ? 2048 : 0);   // the step's V chunk buffers
   // fp16: 64, 128 or 256 dims; fp32: 64 or 128 (a K row of 8 to 32 16-byte units)
   const bool w1 = use_w1() && A.hd % 64 == 0 &&
                   (f16 ? (dpl == 1 || dpl == 2 || dpl == 4) : (dpl == 1 || dpl == 2)) && w1_shm <= 64 * 1024;
