@@ -216,6 +216,44 @@ def test_attn_step_then_out(gpu, oracle, kv_dtype, nsplit, geom):
         assert np.array_equal(gk[:L].view(np.uint8), kc_host[:L].view(np.uint8))
 
 
+@pytest.mark.parametrize("nsplit", [1, 3])
+@pytest.mark.parametrize("nh,nkv", [(14, 2), (8, 1)])
+def test_attn_step_long_context(gpu, oracle, nsplit, nh, nkv):
+    """The step with 64 fp16 dims streams V in 8-row chunks, 24 chunks in flight: lengths
+    around one ring (192 rows), ragged chunk tails and refills up to the cache's end, with
+    poison past the new row."""
+    hd, theta, maxt = 64, 1e6, 1024
+    rng = np.random.default_rng(29)
+    width = nkv * hd
+    freqs = up(oracle.rope_freqs(hd, theta))
+    base_k = rng.standard_normal((maxt, width)).astype(np.float16).view(np.uint16)
+    base_v = rng.standard_normal((maxt, width)).astype(np.float16).view(np.uint16)
+    ws_n = _lib.raw("lt_attn_workspace_size")(1, nh, hd, nsplit)
+    ws = dr.DevTensor.zeros((max(ws_n, 16),), np.uint8, gpu)
+    scale = float(hd ** -0.5)
+    for L in (190, 191, 192, 193, 200, 383, 577, 1023):
+        case(f"attn_step long nh={nh} nkv={nkv} nsplit={nsplit} L={L}")
+        kc, vc = base_k.copy(), base_v.copy()
+        kc[L:] = 0x7E00
+        vc[L:] = 0x7E00
+        qkv = rng.standard_normal(nh * hd + 2 * width).astype(np.float32)
+        roped = oracle.rope(qkv[: (nh + nkv) * hd], L, nh + nkv, hd, theta)
+        ek, ev = kc.copy(), vc.copy()
+        ek[L] = roped[nh * hd:].astype(np.float16).view(np.uint16)
+        ev[L] = qkv[(nh + nkv) * hd:].astype(np.float16).view(np.uint16)
+        att = oracle.attn_decode(roped[: nh * hd], ek, ev, L + 1, nh, nkv, hd, scale, True, nsplit)
+        xq, xd = oracle.quant_q8(att)
+        dk, dv = up(kc), up(vc)
+        datt = empty((nh * hd,), np.float32)
+        aq, ad = empty((nh * hd,), np.int8), empty((nh * hd // 32,), np.uint16)
+        call("lt_attn_step", gpu.handle, up(qkv).vp, freqs.vp, dk.vp, dv.vp, up(np.array([L], np.int32)).vp,
+             datt.vp, aq.vp, ad.vp, nh, nkv, hd, ctypes.c_float(scale), maxt, nsplit, LT_KV_F16, ws.vp, ws.nbytes)
+        assert_bitexact(datt.to_host(), att, f"attention output L={L}")
+        assert_bitexact(aq.to_host(), xq, f"attention quants L={L}")
+        assert_bitexact(ad.to_host(), xd, f"attention scales L={L}")
+        assert np.array_equal(dv.to_host()[L], ev[L]) and np.array_equal(dk.to_host()[L], ek[L])
+
+
 def test_q8_gemv_rms_argmax(gpu, oracle):
     rng = np.random.default_rng(27)
     N, K = 151936, 896
