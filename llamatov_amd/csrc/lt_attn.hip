@@ -854,8 +854,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     // chunk c: through LDS buffer c % 2 (a wave's LDS operations complete in order, so a
     // buffer is rewritten only after the reads of the chunk before), its kCR rows folded
     // in order, its register slot refilled with chunk c + kNC.  (Writing and reading chunk
-    // c + 1 during chunk c's fold measured slower: its conditional stage makes the load
-    // waits conservative.)
+    // c + 1 during chunk c's fold measured slower, with the look-ahead conditional or not.)
     const int nch = (n + kCR - 1) / kCR;
     for (int c0 = 0; c0 < nch; c0 += kNC) {
 #pragma unroll
