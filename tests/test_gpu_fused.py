@@ -216,13 +216,13 @@ def test_attn_step_then_out(gpu, oracle, kv_dtype, nsplit, geom):
         assert np.array_equal(gk[:L].view(np.uint8), kc_host[:L].view(np.uint8))
 
 
-@pytest.mark.parametrize("nsplit", [1, 3])
-@pytest.mark.parametrize("nh,nkv", [(14, 2), (8, 1)])
-def test_attn_step_long_context(gpu, oracle, nsplit, nh, nkv):
-    """The step with 64 fp16 dims streams V in 8-row chunks, 24 chunks in flight: lengths
-    around one ring (192 rows), ragged chunk tails and refills up to the cache's end, with
-    poison past the new row."""
-    hd, theta, maxt = 64, 1e6, 1024
+@pytest.mark.parametrize("nsplit", [1, 3, 16])
+@pytest.mark.parametrize("nh,nkv,hd", [(14, 2, 64), (8, 1, 64), (32, 8, 128), (16, 2, 128)])
+def test_attn_step_long_context(gpu, oracle, nsplit, nh, nkv, hd):
+    """The fp16 step with 64 or 128 dims streams V in 8-row chunks (24 or 12 in flight):
+    lengths around one ring (192 / 96 rows), ragged chunk tails, refills up to the cache's
+    end, splits of a few rows, with poison past the new row."""
+    theta, maxt = 1e6, 1024
     rng = np.random.default_rng(29)
     width = nkv * hd
     freqs = up(oracle.rope_freqs(hd, theta))
@@ -231,7 +231,7 @@ def test_attn_step_long_context(gpu, oracle, nsplit, nh, nkv):
     ws_n = _lib.raw("lt_attn_workspace_size")(1, nh, hd, nsplit)
     ws = dr.DevTensor.zeros((max(ws_n, 16),), np.uint8, gpu)
     scale = float(hd ** -0.5)
-    for L in (190, 191, 192, 193, 200, 383, 577, 1023):
+    for L in (0, 5, 95, 96, 97, 190, 191, 192, 193, 200, 383, 577, 1023):
         case(f"attn_step long nh={nh} nkv={nkv} nsplit={nsplit} L={L}")
         kc, vc = base_k.copy(), base_v.copy()
         kc[L:] = 0x7E00
