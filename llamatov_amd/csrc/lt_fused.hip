@@ -629,12 +629,11 @@ inline int grid_for(long n, int per) { return (int)((n + per - 1) / per); }
 // about half a resident wave of workgroups covers the matrix (LT_GEMV_ROWS=R forces R
 // contiguous rows per workgroup, for tuning sweeps).
 int env_rows() {
-  static int env = -1;
-  if (env < 0) {
+  static const int env = [] {   // read once (thread-safe initialization)
     const char* s = getenv("LT_GEMV_ROWS");
-    env = s ? atoi(s) : 0;
-    if (env < 0 || env % 8) env = 0;
-  }
+    const int r = s ? atoi(s) : 0;
+    return r < 0 || r % 8 ? 0 : r;
+  }();
   return env;
 }
 
