@@ -218,6 +218,16 @@ def c5_leg(dev, n_prefill: int = 512, n_decode: int = 256, eager: bool = False) 
     pre_ms = ev.stop_ms()
     macs = n_prefill * cfg.n_layers * (cfg.n_qkv * cfg.n_embd + cfg.n_embd * cfg.q_dim + 2 * cfg.n_ff * cfg.n_embd
                                       + cfg.n_embd * cfg.n_ff)
+    res = {"model": cfg.name, "prefill_tokens": n_prefill, "prefill_ms": round(pre_ms, 3),
+           "prefill_tok_s": round(n_prefill / (pre_ms / 1e3), 1),
+           "prefill_mfma_util": round(2 * macs / (pre_ms / 1e3) / (INT8_PEAK_TOPS * 1e12), 4),
+           "prefill_gemm_macs": int(macs)}
+    if n_decode <= 4:   # prefill only (counter runs)
+        log(f"C5: prefill {pre_ms:.1f} ms ({res['prefill_mfma_util'] * 100:.1f}% of int8 MFMA peak)")
+        ev.free()
+        plan.free()
+        model.free()
+        return res
     runner = dr.GraphRunner(plan)
     one = plan.step if eager else runner._launch
     if not eager:
@@ -232,12 +242,9 @@ def c5_leg(dev, n_prefill: int = 512, n_decode: int = 256, eager: bool = False) 
     tok_s = (n_decode - 4) / (dec_ms / 1e3)
     kv_bytes = sum(cfg.n_layers * 2 * (n_prefill + i + 1) * cfg.kv_dim * 2 for i in range(n_decode)) / n_decode
     step_bytes = cfg.weight_bytes() + kv_bytes
-    res = {"model": cfg.name, "prefill_tokens": n_prefill, "prefill_ms": round(pre_ms, 3),
-           "prefill_tok_s": round(n_prefill / (pre_ms / 1e3), 1),
-           "prefill_mfma_util": round(2 * macs / (pre_ms / 1e3) / (INT8_PEAK_TOPS * 1e12), 4),
-           "prefill_gemm_macs": int(macs), "decode_tokens": n_decode, "decode_tok_s": round(tok_s, 2),
-           "decode_ms_per_token": round(dec_ms / (n_decode - 4), 4), "decode_step_bytes": int(step_bytes),
-           "decode_roofline_frac": round(step_bytes * tok_s / (HBM_PEAK_GBS * 1e9), 4)}
+    res.update({"decode_tokens": n_decode, "decode_tok_s": round(tok_s, 2),
+                "decode_ms_per_token": round(dec_ms / (n_decode - 4), 4), "decode_step_bytes": int(step_bytes),
+                "decode_roofline_frac": round(step_bytes * tok_s / (HBM_PEAK_GBS * 1e9), 4)})
     log(f"C5: prefill {pre_ms:.1f} ms ({res['prefill_mfma_util'] * 100:.1f}% of int8 MFMA peak), "
         f"decode {tok_s:.1f} tok/s")
     ev.free()
@@ -279,6 +286,8 @@ def main() -> int:
     ap.add_argument("--c4", action="store_true", help="also time BASELINE config 4 attention (adds c4_attention)")
     ap.add_argument("--c5", action="store_true",
                     help="also run BASELINE config 5 (Llama-3-8B arch: 512-token MFMA prefill + 256 decode; adds c5)")
+    ap.add_argument("--c5-decode", type=int, default=256,
+                    help="C5 decode tokens (at most 4: prefill only, for counter runs)")
     ap.add_argument("--gemv-sweep", action="store_true",
                     help="also time the Q8_0 GEMV on the BASELINE config 1/3 shapes (adds gemv_sweep)")
     ap.add_argument("--per-op", action="store_true",
@@ -431,7 +440,7 @@ def main() -> int:
         plan.free()
         model.free()
         log("C5 leg")
-        result["c5"] = c5_leg(dev, eager=args.eager)
+        result["c5"] = c5_leg(dev, n_decode=args.c5_decode, eager=args.eager)
     print(json.dumps(result), flush=True)
     return 0
 
