@@ -528,7 +528,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   const int len0 = kStep ? *A.len : MODE == AM_PREFILL ? A.len[0] + b + 1 : A.len[b];
   constexpr int kHalf = HD / 2;
   constexpr int kRopeIt = ((HPW + 1) * kHalf + 63) / 64;
-  float rx1[kRopeIt], rx2[kRopeIt], rfr[kRopeIt], rv[DPL];
+  // Lane l's rotary pair index in RoPE iteration it is (l + 64·it) mod kHalf: with kHalf
+  // = 32 or 64 always the same, with 128 one of two -- so each lane evaluates sin/cos for
+  // kJ angles only, shared by every head it rotates (the same function of the same value)
+  constexpr int kJ = kHalf <= 64 ? 1 : kHalf / 64;
+  float rx1[kRopeIt], rx2[kRopeIt], rfq[kJ], rv[DPL];
   if (kStep) {
 #pragma unroll
     for (int it = 0; it < kRopeIt; it++) {
@@ -537,8 +541,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
       const float* src = r < HPW ? A.qkv + (size_t)(h0 + r) * HD : A.qkv + (size_t)A.nh * HD + (size_t)g * HD;
       rx1[it] = src[j];
       rx2[it] = src[j + kHalf];
-      rfr[it] = A.freqs[j];
     }
+#pragma unroll
+    for (int q = 0; q < kJ; q++) rfq[q] = A.freqs[(l % kHalf) + 64 * q];
 #pragma unroll
     for (int k = 0; k < DPL; k++) rv[k] = A.qkv[(size_t)A.nh * HD + kvrow + (size_t)g * HD + l + 64 * k];
   }
@@ -644,13 +649,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     // RoPE (the arithmetic of k_rope, rope_from_facts.pl:40-69) of the q heads and the
     // group's k; k and v rounded through the cache's type
     const float pos = (float)(valid ? Lnew : 0);
+    float snq[kJ], csq[kJ];
+#pragma unroll
+    for (int q = 0; q < kJ; q++) lt_sincosf(pos * rfq[q], &snq[q], &csq[q]);
 #pragma unroll
     for (int it = 0; it < kRopeIt; it++) {
       const int i = l + 64 * it;
       if (i < (HPW + 1) * kHalf) {
         const int r = i / kHalf, j = i - r * kHalf;
-        float sn, cs;
-        lt_sincosf(pos * rfr[it], &sn, &cs);
+        const float sn = snq[kJ == 1 ? 0 : it % kJ], cs = csq[kJ == 1 ? 0 : it % kJ];
         const float o1 = fmaf(rx1[it], cs, -(rx2[it] * sn));
         const float o2 = fmaf(rx1[it], sn, rx2[it] * cs);
         if (r < HPW) {
@@ -1087,9 +1094,22 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
   LT_REQUIRE(A.nsplit <= 128, "%s: nsplit=%d (at most 128)", what, A.nsplit);
   // the single-wave kernel (every mode): all heads of a KV group share its K/V reads
   const int rep = A.nh / A.nkv;
-  const int h = rep % 8 == 0 ? 8 : rep % 4 == 0 ? 4 : rep % 2 == 0 ? 2 : 1;
-  const int dpl = A.hd / 64;
+  int h = rep % 8 == 0 ? 8 : rep % 4 == 0 ? 4 : rep % 2 == 0 ? 2 : 1;
   const int per_max = (A.maxt + A.nsplit - 1) / A.nsplit;
+  if (mode == AM_STEP) {
+    // A step is one token: with splits of at most 256 rows its single-wave workgroups are
+    // bound by their own serial work (RoPE, scores, exps and the O chains of HPW heads), so
+    // one head per wave (rep workgroups per KV group, each re-reading the group's rows from
+    // L2) is fastest (8B decode 432 -> 450 tok/s); longer splits keep the heads together.
+    // LT_ATTN_STEP_HPW=H caps the heads per wave instead (sweeps).
+    static const int cap = [] {
+      const char* s = getenv("LT_ATTN_STEP_HPW");
+      return s ? atoi(s) : 0;
+    }();
+    const int c = cap > 0 ? cap : per_max <= 256 ? 1 : 8;
+    while (h > c && h > 1) h /= 2;
+  }
+  const int dpl = A.hd / 64;
   const size_t ku = (size_t)A.hd * (f16 ? 2 : 4) / 16;
   const size_t kpr = h >= 2 ? 32 : 64;              // positions per score round
   const int vb = dpl * (f16 ? 2 : 4);               // V bytes per lane per row
