@@ -13,6 +13,9 @@
 // stack of 5 partial sums per element replays the pairing with every addition in place.
 #include "lt_q8_device.h"
 
+#include <cstdlib>
+#include <type_traits>
+
 namespace {
 
 using namespace lt;
@@ -56,8 +59,14 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 // 32 consecutive tokens is 1 KB of quants and 64 bytes of scales, each contiguous), so
 // both operands of a block are coalesced, aligned loads; the arithmetic and the order are
 // those of the row-major layouts.
-template <GemmEpi EPI, bool kTiled>
+// kSL: how the tiled kernel walks the leaves.  0: one dynamic loop over the block sequence
+// (any K).  1: K a multiple of 2048 (an even number of blocks per leaf) -- leaves in groups of
+// 4 with the group's structure static: the tree's levels 0 and 1 are the accumulators
+// themselves (no parking copies), the ring slot indices are static, and only the group's last
+// leaf closes levels 2..4 (in LDS) with a short dynamic loop.
+template <GemmEpi EPI, bool kTiled, int kSL = 0>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_q8_gemm(GemmParams P) {
+  static_assert(kSL == 0 || kTiled, "k_q8_gemm: grouped leaves use the tiled layouts");
   __shared__ float s_st[kGemmWaves][3][16 * 64];   // tree levels 2..4 of each wave's 32 x 32 tile
   const int wave = threadIdx.x >> 6;
   const int l = threadIdx.x & 63;
@@ -185,6 +194,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
       }
     }
   };
+  float v[16];   // the tile's row values once every leaf is folded
+  if constexpr (kSL == 0) {
   Ops ring[kDepth];
 #pragma unroll
   for (int d = 0; d < kDepth; d++) produce(ring[d]);
@@ -192,7 +203,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
   // pending partial sums of the tree: levels 0 and 1 in registers; levels 2..4, parked at
   // most once per 4 leaves, in LDS
   float st[2][16];
-  float v[16];
 #pragma unroll
   for (int r = 0; r < 16; r++) {
     v[r] = 0.0f;
@@ -291,6 +301,72 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
         }
       }
     }
+  }
+
+  } else {
+    // groups of 4 leaves (post-order leaf i = 4g + j holds blocks bitrev5(i) + 32k, k < bpl):
+    //   j = 0 -> va (parked at level 0 as it is);  j = 1 -> vb, closes level 0 (va + vb) and
+    //   parks at level 1;  j = 2 -> va (level 0);  j = 3 -> vc, closes levels 0 (va + vc),
+    //   1 (vb + vc) and 2 .. t1-1 from LDS, parks at t1 = 2 + ctz(~g) (leaf 31: the row value)
+    // The block at sequence position p lives in ring slot p % 2 (every leaf starts at an even
+    // position); a slot is refilled with position p + 2 once its MFMAs are issued.
+    const int bpl = nb >> 5;
+    Ops ring[2];
+    load_ops(0, true, ring[0]);    // leaf 0: blocks 0 and 32
+    load_ops(32, true, ring[1]);
+    const v16i z = {};
+    const v16f zf = {};
+    // one block from ring slot sl, which is then refilled with the block two positions on
+    auto step = [&](auto S, float (&acc)[16], int rb, bool rreal) {
+      constexpr int sl = decltype(S)::value;
+      const Ops& o = ring[sl];
+      const v16i isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.w03, o.bq, z, 0, 0, 0);
+      const u32x2 aw = {o.wdw, 0u}, bw = {o.xdw, 0u};
+      const v16f sc =
+          __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(h4, aw), __builtin_bit_cast(h4, bw), zf, 0, 0, 0);
+      load_ops(rb, rreal, ring[sl]);
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[r] = fmaf(sc[r], (float)isum[r], acc[r]);
+    };
+    auto leaf = [&](int i, float (&acc)[16]) {
+      const int L = leaf_lane(i);
+      const int Ln = i < 31 ? leaf_lane(i + 1) : 0;
+      // position (i, k) + 2: the same leaf or the next one (past leaf 31: zeros)
+      auto ref = [&](int k, auto S) {
+        const bool same = k + 2 < bpl;
+        step(S, acc, same ? L + 32 * (k + 2) : Ln + 32 * (k + 2 - bpl), same || i < 31);
+      };
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+      for (int k = 0; k < bpl; k += 2) {
+        ref(k, std::integral_constant<int, 0>{});
+        ref(k + 1, std::integral_constant<int, 1>{});
+      }
+    };
+    float va[16], vb[16], vc[16];
+    for (int g = 0; g < 8; g++) {
+      leaf(4 * g, va);
+      leaf(4 * g + 1, vb);
+#pragma unroll
+      for (int r = 0; r < 16; r++) vb[r] = va[r] + vb[r];
+      leaf(4 * g + 2, va);
+      leaf(4 * g + 3, vc);
+#pragma unroll
+      for (int r = 0; r < 16; r++) vc[r] = va[r] + vc[r];
+#pragma unroll
+      for (int r = 0; r < 16; r++) vc[r] = vb[r] + vc[r];
+      const int t1 = 2 + __builtin_ctz(~(unsigned)g);   // 2 .. 5
+      for (int lvl = 2; lvl < t1; lvl++) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) vc[r] = s_st[wave][lvl - 2][r * 64 + l] + vc[r];
+      }
+      if (t1 < 5) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) s_st[wave][t1 - 2][r * 64 + l] = vc[r];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) v[r] = vc[r];
   }
 
   const int t = t0 + c;
@@ -432,6 +508,19 @@ int launch_gemm(lt_ctx* ctx, GemmParams P) {
   P.nrt = (P.N + 31) / 32;
   P.ntt = (P.T + kGemmTokens - 1) / kGemmTokens;
   const long grid = (long)((P.nrt + 7) / 8) * 8 * P.ntt;
+  if constexpr (kTiled) {
+    // grouped leaves (an even number of blocks per leaf) when the launch holds 3 or more
+    // waves per SIMD: their 2-block load ring leans on the other waves to hide latency (with 2
+    // per SIMD, the 8B O and down GEMMs, the 4-deep dynamic ring measured faster)
+    // (LT_GEMM_GROUPED=1 / 0 forces the choice where K allows it, read at every launch)
+    const long waves = (long)P.nrt * ((P.T + 31) / 32);
+    const char* force = getenv("LT_GEMM_GROUPED");
+    const bool big = waves >= 12L * (ctx->num_cus > 0 ? ctx->num_cus : 256);
+    if (P.K % 2048 == 0 && (force ? force[0] == '1' : big)) {
+      k_q8_gemm<EPI, true, 1><<<(unsigned)grid, 256, 0, ctx->stream>>>(P);
+      return lt_check_launch("k_q8_gemm");
+    }
+  }
   k_q8_gemm<EPI, kTiled><<<(unsigned)grid, 256, 0, ctx->stream>>>(P);
   return lt_check_launch("k_q8_gemm");
 }

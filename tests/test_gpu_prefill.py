@@ -126,9 +126,14 @@ def subnormal_scales(rng, W, xd, frac=0.25):
 
 @pytest.mark.parametrize("N,K,T,epi", [(1152, 896, 37, "bias"), (896, 4864, 130, "resid"), (100, 96, 5, "store"),
                                        (64, 1024, 129, "store"), (4096, 4096, 33, "store"), (40, 14336, 3, "resid"),
-                                       (96, 256, 70, "subnormal")])
-def test_q8_gemm_tiled_matches_gemv_per_token(gpu, oracle, N, K, T, epi):
-    case(f"q8_gemm_t N={N} K={K} T={T} {epi}")
+                                       (96, 256, 70, "subnormal"), (64, 2048, 45, "bias"), (72, 6144, 130, "resid"),
+                                       (33, 4096, 7, "subnormal")])
+@pytest.mark.parametrize("grouped", ["1", "0"])
+def test_q8_gemm_tiled_matches_gemv_per_token(gpu, oracle, N, K, T, epi, grouped, monkeypatch):
+    """Both leaf walks of the tiled kernel (grouped leaves where K % 2048 == 0, forced
+    on and off with LT_GEMM_GROUPED) against the oracle's GEMV per token."""
+    monkeypatch.setenv("LT_GEMM_GROUPED", grouped)
+    case(f"q8_gemm_t N={N} K={K} T={T} {epi} grouped={grouped}")
     rng = np.random.default_rng(33)
     W = hq8.quantize_rows((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
     X = (rng.standard_normal((T, K))).astype(np.float32)
@@ -154,9 +159,11 @@ def test_q8_gemm_tiled_matches_gemv_per_token(gpu, oracle, N, K, T, epi):
         assert np.array_equal(bits(got[t]), bits(exp)), f"token {t}: {np.flatnonzero(bits(got[t]) != bits(exp))[:5]}"
 
 
-@pytest.mark.parametrize("F,K,T", [(4864, 896, 40), (64, 128, 7), (48, 96, 70)])
-def test_q8_gemm_silu_tiled(gpu, oracle, F, K, T):
-    case(f"q8_gemm_silu_t F={F} K={K} T={T}")
+@pytest.mark.parametrize("F,K,T", [(4864, 896, 40), (64, 128, 7), (48, 96, 70), (128, 6144, 33), (96, 4096, 140)])
+@pytest.mark.parametrize("grouped", ["1", "0"])
+def test_q8_gemm_silu_tiled(gpu, oracle, F, K, T, grouped, monkeypatch):
+    monkeypatch.setenv("LT_GEMM_GROUPED", grouped)
+    case(f"q8_gemm_silu_t F={F} K={K} T={T} grouped={grouped}")
     rng = np.random.default_rng(34)
     Wg = hq8.quantize_rows((rng.standard_normal((F, K)) * 0.02).astype(np.float32))
     Wu = hq8.quantize_rows((rng.standard_normal((F, K)) * 0.02).astype(np.float32))
