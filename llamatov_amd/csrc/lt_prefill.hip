@@ -60,12 +60,14 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 // both operands of a block are coalesced, aligned loads; the arithmetic and the order are
 // those of the row-major layouts.
 // kSL: how the tiled kernel walks the leaves.  0: one dynamic loop over the block sequence
-// (any K).  1: K a multiple of 2048 (an even number of blocks per leaf) -- leaves in groups of
-// 4 with the group's structure static: the tree's levels 0 and 1 are the accumulators
-// themselves (no parking copies), the ring slot indices are static, and only the group's last
-// leaf closes levels 2..4 (in LDS) with a short dynamic loop.
+// (any K).  1..3: K a multiple of 2048 (an even number bpl of blocks per leaf) -- leaves in
+// groups of 4 with the group's structure static: the tree's levels 0 and 1 are the
+// accumulators themselves (no parking copies), the ring slot indices are static, and only the
+// group's last leaf closes levels 2..4 (in LDS) with a short dynamic loop.  1: a 2-slot load
+// ring (3 waves per SIMD); 2: a 4-slot ring with the MFMAs one block ahead of the fold (up to
+// 256 registers, 2 waves per SIMD; bpl % 4 == 0 -- with bpl % 4 == 2 the allocation spills).
 template <GemmEpi EPI, bool kTiled, int kSL = 0>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_q8_gemm(GemmParams P) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSL >= 2 ? 2 : 3))) void k_q8_gemm(GemmParams P) {
   static_assert(kSL == 0 || kTiled, "k_q8_gemm: grouped leaves use the tiled layouts");
   __shared__ float s_st[kGemmWaves][3][16 * 64];   // tree levels 2..4 of each wave's 32 x 32 tile
   const int wave = threadIdx.x >> 6;
@@ -308,49 +310,82 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     //   j = 0 -> va (parked at level 0 as it is);  j = 1 -> vb, closes level 0 (va + vb) and
     //   parks at level 1;  j = 2 -> va (level 0);  j = 3 -> vc, closes levels 0 (va + vc),
     //   1 (vb + vc) and 2 .. t1-1 from LDS, parks at t1 = 2 + ctz(~g) (leaf 31: the row value)
-    // The block at sequence position p lives in ring slot p % 2 (every leaf starts at an even
-    // position); a slot is refilled with position p + 2 once its MFMAs are issued.
+    // The block at sequence position p lives in ring slot p % kRD (a leaf starts at position
+    // i·bpl, slot (i·bpl) % kRD); a slot is refilled with position p + kRD once its MFMAs are
+    // issued.  With kRD = 4 the MFMAs of position p + 1 run before position p's fold (result
+    // sets A / B by the parity of p).
+    constexpr int kRD = kSL == 1 ? 2 : 4;
     const int bpl = nb >> 5;
-    Ops ring[2];
-    load_ops(0, true, ring[0]);    // leaf 0: blocks 0 and 32
-    load_ops(32, true, ring[1]);
+    Ops ring[kRD];
+#pragma unroll
+    for (int d = 0; d < kRD; d++) load_ops(32 * d, true, ring[d]);   // leaf 0's first kRD blocks
     const v16i z = {};
     const v16f zf = {};
-    // one block from ring slot sl, which is then refilled with the block two positions on
+    auto mfma_t = [&](const Ops& o, v16i& isum, v16f& sc) {
+      isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.w03, o.bq, z, 0, 0, 0);
+      const u32x2 aw = {o.wdw, 0u}, bw = {o.xdw, 0u};
+      sc = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(h4, aw), __builtin_bit_cast(h4, bw), zf, 0, 0, 0);
+    };
+    v16i isA, isB;
+    v16f scA, scB;
+    if constexpr (kRD == 4) mfma_t(ring[0], isA, scA);
+    // one block from ring slot sl, which is then refilled with the block kRD positions on
     auto step = [&](auto S, float (&acc)[16], int rb, bool rreal) {
       constexpr int sl = decltype(S)::value;
-      const Ops& o = ring[sl];
-      const v16i isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.w03, o.bq, z, 0, 0, 0);
-      const u32x2 aw = {o.wdw, 0u}, bw = {o.xdw, 0u};
-      const v16f sc =
-          __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(h4, aw), __builtin_bit_cast(h4, bw), zf, 0, 0, 0);
-      load_ops(rb, rreal, ring[sl]);
+      if constexpr (kRD == 2) {
+        v16i isum;
+        v16f sc;
+        mfma_t(ring[sl], isum, sc);
+        load_ops(rb, rreal, ring[sl]);
 #pragma unroll
-      for (int r = 0; r < 16; r++) acc[r] = fmaf(sc[r], (float)isum[r], acc[r]);
+        for (int r = 0; r < 16; r++) acc[r] = fmaf(sc[r], (float)isum[r], acc[r]);
+      } else if constexpr ((sl & 1) == 0) {
+        mfma_t(ring[(sl + 1) & 3], isB, scB);
+        load_ops(rb, rreal, ring[sl]);
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[r] = fmaf(scA[r], (float)isA[r], acc[r]);
+      } else {
+        mfma_t(ring[(sl + 1) & 3], isA, scA);
+        load_ops(rb, rreal, ring[sl]);
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[r] = fmaf(scB[r], (float)isB[r], acc[r]);
+      }
     };
-    auto leaf = [&](int i, float (&acc)[16]) {
+    auto leaf = [&](auto J, int i, float (&acc)[16]) {
+      constexpr int j = decltype(J)::value;
+      static_assert(j >= 0 && j < 4, "k_q8_gemm: leaf within a group");   // (i·bpl) % kRD == 0
       const int L = leaf_lane(i);
       const int Ln = i < 31 ? leaf_lane(i + 1) : 0;
-      // position (i, k) + 2: the same leaf or the next one (past leaf 31: zeros)
+      // position (i, k) + kRD: the same leaf or the next one (past leaf 31: zeros)
       auto ref = [&](int k, auto S) {
-        const bool same = k + 2 < bpl;
-        step(S, acc, same ? L + 32 * (k + 2) : Ln + 32 * (k + 2 - bpl), same || i < 31);
+        const bool same = k + kRD < bpl;
+        step(S, acc, same ? L + 32 * (k + kRD) : Ln + 32 * (k + kRD - bpl), same || i < 31);
       };
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[r] = 0.0f;
-      for (int k = 0; k < bpl; k += 2) {
-        ref(k, std::integral_constant<int, 0>{});
-        ref(k + 1, std::integral_constant<int, 1>{});
+      if constexpr (kRD == 2) {
+        for (int k = 0; k < bpl; k += 2) {
+          ref(k, std::integral_constant<int, 0>{});
+          ref(k + 1, std::integral_constant<int, 1>{});
+        }
+      } else {
+        int k = 0;
+        for (; k + 4 <= bpl; k += 4) {
+          ref(k, std::integral_constant<int, 0>{});
+          ref(k + 1, std::integral_constant<int, 1>{});
+          ref(k + 2, std::integral_constant<int, 2>{});
+          ref(k + 3, std::integral_constant<int, 3>{});
+        }
       }
     };
     float va[16], vb[16], vc[16];
     for (int g = 0; g < 8; g++) {
-      leaf(4 * g, va);
-      leaf(4 * g + 1, vb);
+      leaf(std::integral_constant<int, 0>{}, 4 * g, va);
+      leaf(std::integral_constant<int, 1>{}, 4 * g + 1, vb);
 #pragma unroll
       for (int r = 0; r < 16; r++) vb[r] = va[r] + vb[r];
-      leaf(4 * g + 2, va);
-      leaf(4 * g + 3, vc);
+      leaf(std::integral_constant<int, 2>{}, 4 * g + 2, va);
+      leaf(std::integral_constant<int, 3>{}, 4 * g + 3, vc);
 #pragma unroll
       for (int r = 0; r < 16; r++) vc[r] = va[r] + vc[r];
 #pragma unroll
@@ -509,16 +544,25 @@ int launch_gemm(lt_ctx* ctx, GemmParams P) {
   P.ntt = (P.T + kGemmTokens - 1) / kGemmTokens;
   const long grid = (long)((P.nrt + 7) / 8) * 8 * P.ntt;
   if constexpr (kTiled) {
-    // grouped leaves (an even number of blocks per leaf) when the launch holds 3 or more
-    // waves per SIMD: their 2-block load ring leans on the other waves to hide latency (with 2
-    // per SIMD, the 8B O and down GEMMs, the 4-deep dynamic ring measured faster)
-    // (LT_GEMM_GROUPED=1 / 0 forces the choice where K allows it, read at every launch)
-    const long waves = (long)P.nrt * ((P.T + 31) / 32);
-    const char* force = getenv("LT_GEMM_GROUPED");
-    const bool big = waves >= 12L * (ctx->num_cus > 0 ? ctx->num_cus : 256);
-    if (P.K % 2048 == 0 && (force ? force[0] == '1' : big)) {
-      k_q8_gemm<EPI, true, 1><<<(unsigned)grid, 256, 0, ctx->stream>>>(P);
-      return lt_check_launch("k_q8_gemm");
+    // K a multiple of 2048 (an even number of blocks per leaf, bpl): grouped leaves -- with a
+    // 2-slot ring when the launch holds 3 or more waves per SIMD (the other waves hide the
+    // latency), else (bpl % 4 == 0) with a 4-slot ring and pipelined MFMAs in 256 registers.
+    // LT_GEMM_GROUPED=0 / 1 / 2 forces the dynamic walk / the 2-slot / the 4-slot walk where
+    // K allows it (read at every launch).
+    if (P.K % 2048 == 0) {
+      const int bpl = P.K / 1024;
+      const long waves = (long)P.nrt * ((P.T + 31) / 32);
+      const bool big = waves >= 12L * (ctx->num_cus > 0 ? ctx->num_cus : 256);
+      const char* force = getenv("LT_GEMM_GROUPED");
+      const int walk = force ? atoi(force) : big ? 1 : bpl % 4 == 0 ? 2 : 0;
+      if (walk == 1) {
+        k_q8_gemm<EPI, true, 1><<<(unsigned)grid, 256, 0, ctx->stream>>>(P);
+        return lt_check_launch("k_q8_gemm");
+      }
+      if (walk == 2 && bpl % 4 == 0) {
+        k_q8_gemm<EPI, true, 2><<<(unsigned)grid, 256, 0, ctx->stream>>>(P);
+        return lt_check_launch("k_q8_gemm");
+      }
     }
   }
   k_q8_gemm<EPI, kTiled><<<(unsigned)grid, 256, 0, ctx->stream>>>(P);

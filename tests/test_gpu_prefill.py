@@ -128,10 +128,11 @@ def subnormal_scales(rng, W, xd, frac=0.25):
                                        (64, 1024, 129, "store"), (4096, 4096, 33, "store"), (40, 14336, 3, "resid"),
                                        (96, 256, 70, "subnormal"), (64, 2048, 45, "bias"), (72, 6144, 130, "resid"),
                                        (33, 4096, 7, "subnormal")])
-@pytest.mark.parametrize("grouped", ["1", "0"])
+@pytest.mark.parametrize("grouped", ["2", "1", "0"])
 def test_q8_gemm_tiled_matches_gemv_per_token(gpu, oracle, N, K, T, epi, grouped, monkeypatch):
-    """Both leaf walks of the tiled kernel (grouped leaves where K % 2048 == 0, forced
-    on and off with LT_GEMM_GROUPED) against the oracle's GEMV per token."""
+    """Every leaf walk of the tiled kernel (grouped leaves with a 4- or 2-slot ring where K
+    allows them, the dynamic walk; forced with LT_GEMM_GROUPED) against the oracle's GEMV
+    per token."""
     monkeypatch.setenv("LT_GEMM_GROUPED", grouped)
     case(f"q8_gemm_t N={N} K={K} T={T} {epi} grouped={grouped}")
     rng = np.random.default_rng(33)
@@ -160,7 +161,7 @@ def test_q8_gemm_tiled_matches_gemv_per_token(gpu, oracle, N, K, T, epi, grouped
 
 
 @pytest.mark.parametrize("F,K,T", [(4864, 896, 40), (64, 128, 7), (48, 96, 70), (128, 6144, 33), (96, 4096, 140)])
-@pytest.mark.parametrize("grouped", ["1", "0"])
+@pytest.mark.parametrize("grouped", ["2", "1", "0"])
 def test_q8_gemm_silu_tiled(gpu, oracle, F, K, T, grouped, monkeypatch):
     monkeypatch.setenv("LT_GEMM_GROUPED", grouped)
     case(f"q8_gemm_silu_t F={F} K={K} T={T} grouped={grouped}")
