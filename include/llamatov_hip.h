@@ -251,6 +251,10 @@ LT_API int lt_q8_gemm_silu(lt_ctx* ctx, const void* Wgu, const int8_t* Xq, const
 LT_API size_t lt_q8_tiles_bytes(int N, int K);
 LT_API int lt_q8_tiles(lt_ctx* ctx, const void* W, void* Wt, int N, int K);
 LT_API int lt_quant_q8_bm(lt_ctx* ctx, const float* x, int8_t* xq, uint16_t* xd, int T, int K);
+/* lt_rmsnorm of T rows of x [T][N] followed by lt_quant_q8_bm of the result, in one launch
+ * (the same arithmetic; the normalized rows are not stored). */
+LT_API int lt_rmsnorm_quant_bm(lt_ctx* ctx, const float* x, const float* w, int8_t* xq, uint16_t* xd, int T,
+                               int N, float eps);
 
 /* lt_q8_gemm / lt_q8_gemm_silu on those layouts (Wt from lt_q8_tiles, Xq/Xd from
  * lt_quant_q8_bm): every block's operands are contiguous runs, so each element is the same

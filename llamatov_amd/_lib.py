@@ -64,6 +64,7 @@ _SIGS = {
     "lt_q8_tiles_bytes": (c_size_t, [c_int, c_int]),
     "lt_q8_tiles": (c_int, [_P, _P, _P, c_int, c_int]),
     "lt_quant_q8_bm": (c_int, [_P, _P, _P, _P, c_int, c_int]),
+    "lt_rmsnorm_quant_bm": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_float]),
     "lt_q8_gemm_t": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int]),
     "lt_q8_gemm_silu_t": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int]),
     "lt_rope_batch": (c_int, [_P, _P, c_int, c_int, _P, c_int, c_int, _P]),

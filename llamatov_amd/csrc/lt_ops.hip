@@ -102,6 +102,29 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__
     quant_block_hw(ybuf[b * 32 + lane], lane, xq + b * 32, xd + b);
 }
 
+// k_rmsnorm_quant over T rows with block-major output (the prefill GEMM's activation layout):
+// row t's block b goes to xq[(b*T + t)*32 ..], xd[b*T + t].  The same arithmetic as
+// k_rmsnorm followed by k_quant_q8 per row.
+__global__ __launch_bounds__(256) void k_rmsnorm_quant_bm(const float* __restrict__ x,
+                                                          const float* __restrict__ w,
+                                                          int8_t* __restrict__ xq,
+                                                          uint16_t* __restrict__ xd, int T, int N,
+                                                          float eps) {
+  extern __shared__ float ybuf[];  // [N]
+  __shared__ float red[256];
+  __shared__ float sinv;
+  const int t = blockIdx.x;
+  const float* xr = x + (size_t)t * N;
+  float inv = rms_inv_block256(xr, N, eps, red, &sinv);
+  for (int j = threadIdx.x; j < N; j += 256) ybuf[j] = (xr[j] * inv) * w[j];
+  __syncthreads();
+  int lane = threadIdx.x & 31;
+  for (int b = threadIdx.x >> 5; b < N / 32; b += 8) {
+    const size_t ob = (size_t)b * T + t;
+    quant_block_hw(ybuf[b * 32 + lane], lane, xq + ob * 32, xd + ob);
+  }
+}
+
 // ---------------------------------------------------------------------------------
 // Per-(row, block) int32 dots of the GEMV arithmetic (a debug hook; the GEMV itself is
 // k_gemv_fused in lt_fused.hip).
@@ -348,6 +371,16 @@ int lt_rmsnorm_quant(lt_ctx* ctx, const float* x, const float* w, int8_t* xq, ui
   LT_REQUIRE(N > 0 && N % 32 == 0 && N <= 16384, "lt_rmsnorm_quant: N=%d (multiple of 32, <= 16384)", N);
   k_rmsnorm_quant<<<1, 256, (size_t)N * sizeof(float), ctx->stream>>>(x, w, xq, xd, N, eps);
   return lt_check_launch("k_rmsnorm_quant");
+}
+
+int lt_rmsnorm_quant_bm(lt_ctx* ctx, const float* x, const float* w, int8_t* xq, uint16_t* xd, int T, int N,
+                        float eps) {
+  LT_REQUIRE(ctx && x && w && xq && xd, "lt_rmsnorm_quant_bm: null argument");
+  LT_REQUIRE(T > 0 && N > 0 && N % 32 == 0 && N <= 16384, "lt_rmsnorm_quant_bm: T=%d N=%d (N multiple of 32, <= 16384)",
+             T, N);
+  LT_REQUIRE(lt_aligned(xq, 16) && lt_aligned(xd, 2), "lt_rmsnorm_quant_bm: misaligned argument");
+  k_rmsnorm_quant_bm<<<T, 256, (size_t)N * sizeof(float), ctx->stream>>>(x, w, xq, xd, T, N, eps);
+  return lt_check_launch("k_rmsnorm_quant_bm");
 }
 
 int lt_q8_gemv_isums(lt_ctx* ctx, const void* W, const int8_t* xq, int32_t* isum, int N, int K) {

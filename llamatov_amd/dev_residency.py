@@ -684,7 +684,6 @@ class PrefillBuffers:
         self.T = T
         self.toks = DevTensor.empty((T,), np.int32, D)
         self.x = DevTensor.empty((T, E), np.float32, D)
-        self.h = DevTensor.empty((T, E), np.float32, D)
         self.xres = DevTensor.empty((T, E), np.float32, D)
         self.qkv = DevTensor.empty((T, cfg.n_qkv), np.float32, D)
         self.att = DevTensor.empty((T, cfg.q_dim), np.float32, D)
@@ -695,7 +694,7 @@ class PrefillBuffers:
         self.ws = DevTensor.empty((aw,), np.uint8, D) if aw else None
 
     def free(self) -> None:
-        for t in (self.toks, self.x, self.h, self.xres, self.qkv, self.att, self.v, self.xq, self.xd, self.ws):
+        for t in (self.toks, self.x, self.xres, self.qkv, self.att, self.v, self.xq, self.xd, self.ws):
             if t is not None:
                 t.free()
 
@@ -729,8 +728,7 @@ def forward_prefill(plan: DecodePlan, tokens) -> None:
     for il, L in enumerate(m.layers):
         cache = plan.caches[il]
         lp = _vp(cache.len_ptr)
-        call("lt_rmsnorm", h, B.x.vp, L["attn_norm"].vp, B.h.vp, T, E, eps)
-        call("lt_quant_q8_bm", h, B.h.vp, B.xq.vp, B.xd.vp, T, E)
+        call("lt_rmsnorm_quant_bm", h, B.x.vp, L["attn_norm"].vp, B.xq.vp, B.xd.vp, T, E, eps)
         call("lt_q8_gemm_t", h, L["wqkv_t"].t.vp, B.xq.vp, B.xd.vp, _vp(L["bqkv"]), None, B.qkv.vp, T, NQ, E)
         call("lt_rope_batch", h, B.qkv.vp, T, NQ, lp, nh + nkv, hd, m.freqs.vp)
         call("lt_kv_append_batch", h, cache.k.vp, cache.v.vp, B.qkv.vp, NQ, QD, QD + KD, T, lp, KD,
@@ -740,8 +738,7 @@ def forward_prefill(plan: DecodePlan, tokens) -> None:
         call("lt_len_add", h, lp, T, cache.max_seq)
         call("lt_quant_q8_bm", h, B.att.vp, B.xq.vp, B.xd.vp, T, QD)
         call("lt_q8_gemm_t", h, L["wo_t"].t.vp, B.xq.vp, B.xd.vp, None, B.x.vp, B.xres.vp, T, E, QD)
-        call("lt_rmsnorm", h, B.xres.vp, L["ffn_norm"].vp, B.h.vp, T, E, eps)
-        call("lt_quant_q8_bm", h, B.h.vp, B.xq.vp, B.xd.vp, T, E)
+        call("lt_rmsnorm_quant_bm", h, B.xres.vp, L["ffn_norm"].vp, B.xq.vp, B.xd.vp, T, E, eps)
         call("lt_q8_gemm_silu_t", h, L["wgu_il_t"].t.vp, B.xq.vp, B.xd.vp, B.v.vp, T, F, E)
         call("lt_quant_q8_bm", h, B.v.vp, B.xq.vp, B.xd.vp, T, F)
         call("lt_q8_gemm_t", h, L["wdown_t"].t.vp, B.xq.vp, B.xd.vp, None, B.xres.vp, B.x.vp, T, E, F)

@@ -26,6 +26,25 @@ def bits(a):
     return a.view(np.uint32) if a.dtype == np.float32 else a
 
 
+@pytest.mark.parametrize("T,K", [(37, 896), (1, 4096), (130, 4096), (9, 14336)])
+def test_rmsnorm_quant_block_major(gpu, T, K):
+    """One launch of RMSNorm + block-major quant equals lt_rmsnorm followed by lt_quant_q8_bm."""
+    case(f"rmsnorm_quant_bm T={T} K={K}")
+    rng = np.random.default_rng(T + K)
+    X = (2.0 * rng.standard_normal((T, K))).astype(np.float32)
+    X[0, :64] = 0.0
+    w = (0.5 * rng.standard_normal(K) + 1.0).astype(np.float32)
+    dx, dw = up(X), up(w)
+    h = dr.DevTensor.empty((T, K), np.float32)
+    q1, d1 = dr.DevTensor.empty((K // 32, T, 32), np.int8), dr.DevTensor.empty((K // 32, T), np.uint16)
+    q2, d2 = dr.DevTensor.empty((K // 32, T, 32), np.int8), dr.DevTensor.empty((K // 32, T), np.uint16)
+    call("lt_rmsnorm", gpu.handle, dx.vp, dw.vp, h.vp, T, K, 1e-5)
+    call("lt_quant_q8_bm", gpu.handle, h.vp, q1.vp, d1.vp, T, K)
+    call("lt_rmsnorm_quant_bm", gpu.handle, dx.vp, dw.vp, q2.vp, d2.vp, T, K, 1e-5)
+    assert np.array_equal(q1.to_host(), q2.to_host())
+    assert np.array_equal(d1.to_host(), d2.to_host())
+
+
 @pytest.mark.parametrize("N,K,T,epi", [(1152, 896, 37, "bias"), (896, 4864, 130, "resid"), (100, 96, 5, "store"),
                                        (64, 1024, 129, "store"), (4096, 4096, 33, "store"), (40, 14336, 3, "resid")])
 def test_q8_gemm_matches_gemv_per_token(gpu, oracle, N, K, T, epi):
