@@ -38,7 +38,9 @@ using namespace lt;
 constexpr uint32_t kNoRow = 0x80000000u;   // out-of-range buffer offset: reads zeros
 constexpr int kVChunkFloats = 8192;        // 32 KB of staged V per chunk
 
-enum AttnMode { AM_STEP = 0, AM_DECODE = 1, AM_PREFILL = 2 };
+// AM_PREFILL_RM (k_attn_w1 only): a causal prefill row whose nsplit splits are all computed
+// by one wave and merged in registers (no partials, no merge launch)
+enum AttnMode { AM_STEP = 0, AM_DECODE = 1, AM_PREFILL = 2, AM_PREFILL_RM = 3 };
 
 struct AttnArgs {
   const float* qkv;     // AM_STEP: q|k|v of the new token (q, k un-roped)
@@ -489,6 +491,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     MODE == AM_STEP ? 1 : (kF16 ? DPL * 8 : DPL * 16) <= 16 && HPW <= 4 ? 3 : 2))) void k_attn_w1(AttnArgs A) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   constexpr bool kStep = MODE == AM_STEP;
+  constexpr bool kRM = MODE == AM_PREFILL_RM;
   constexpr int HD = 64 * DPL;
   constexpr int kEb = kF16 ? 2 : 4;                 // bytes per cache element
   constexpr int KU = HD * kEb / 16;                 // 16-byte units per K row
@@ -512,12 +515,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   float* sq = lds;                                  // [HPW][HD] q (roped in a step); then the outputs
   u32x4* sk = (u32x4*)(lds + HPW * HD);             // [kPR][KU + 1] one round of K rows, padded
   u32x4* sfk = sk + kPR * (KU + 1);                 // step: the new K row, then the new V row (cache format)
-  float* se = (float*)(sfk + (kStep ? 2 * KU : 0)); // [per_up + kEg + 1][HPW]: rows (zero past n), spare
-  uint32_t* sv = (uint32_t*)(se + ((per_up + kEg + 1) * HPW + 3) / 4 * 4);   // kChunk: 2 x 1 KB
+  // [per_up + kEg + 1 (+ 64 in kRM: the Z trees' reads past a split)][HPW]: rows (zero past n), spare
+  float* se = (float*)(sfk + (kStep ? 2 * KU : 0));
+  constexpr int kRmPad = kRM ? 64 : 0;
+  uint32_t* sv = (uint32_t*)(se + ((per_up + kEg + 1 + kRmPad) * HPW + 3) / 4 * 4);   // kChunk: 2 x 1 KB
+  float* srm = (float*)sv;                          // kRM: [3][nsplit*HPW] m_s, Z_s, w_s; then [HPW] Z
   const int l = threadIdx.x;
   const int sp = blockIdx.x;
   const int h0 = blockIdx.y * HPW;
-  const int b = blockIdx.z;
+  // kRM: the longest rows first (a row's work grows with its position)
+  const int b = kRM ? (int)(gridDim.z - 1 - blockIdx.z) : (int)blockIdx.z;
   const int rep = A.nh / A.nkv;
   const int g = h0 / rep;
   const int kvrow = A.nkv * HD;                     // elements per cache position
@@ -525,7 +532,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   // the step's length first, then the new token's inputs: waiting for the length (which
   // places the cache reads) does not wait for the inputs, and waiting for the inputs
   // never waits for cache rows
-  const int len0 = kStep ? *A.len : MODE == AM_PREFILL ? A.len[0] + b + 1 : A.len[b];
+  const int len0 = kStep ? *A.len : MODE == AM_PREFILL || kRM ? A.len[0] + b + 1 : A.len[b];
   constexpr int kHalf = HD / 2;
   constexpr int kRopeIt = ((HPW + 1) * kHalf + 63) / 64;
   // Lane l's rotary pair index in RoPE iteration it is (l + 64·it) mod kHalf: with kHalf
@@ -557,7 +564,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   } else {
     nctx = len0 < 0 ? 0 : (len0 > A.maxt ? A.maxt : len0);
   }
-  const int per = (nctx + A.nsplit - 1) / A.nsplit;
+  const int per = kRM ? nctx : (nctx + A.nsplit - 1) / A.nsplit;   // kRM: the whole row, split later
   const int p0 = sp * per;
   const int p1 = p0 + per < nctx ? p0 + per : nctx;
   const int n = p1 > p0 ? p1 - p0 : 0;
@@ -783,9 +790,52 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
       asm volatile("" ::: "memory");
     }
   }
-  // max (order-free: from the stored scores), exps and Z
   __syncthreads();
   float m[HPW], zs[HPW];
+  const int rm_np = A.nsplit * HPW;                 // kRM: (split, head) pairs
+  const int rm_per = kRM ? (n + A.nsplit - 1) / A.nsplit : 0;   // kRM: positions per split (<= 64)
+  if constexpr (kRM) {
+    // One lane per (split s, head r), the arithmetic of a split's workgroup and of
+    // k_attn_merge: m_s = max of the split's scores, its exps in place, Z_s = the lane fold
+    // (one position per lane: 0 + e_j = e_j) through the 64-lane tree of wave_tree_dpp
+    // evaluated serially (b_j = z_j + z_{j+32}, then halves 16 .. 1), then
+    // w_s = exp(m_s - M) with M = max m_s, and Z = sum over s ascending of fma(w_s, Z_s).
+    for (int pi = l; pi < rm_np; pi += 64) {
+      const int s_ = pi / HPW, r = pi - s_ * HPW;
+      const int q0 = s_ * rm_per;
+      const int ns = q0 < n ? (q0 + rm_per < n ? rm_per : n - q0) : 0;
+      float* e = se + (ns > 0 ? q0 : 0) * HPW + r;
+      float mx = -1e30f;
+      for (int t = 0; t < ns; t++) mx = fmaxf(mx, e[t * HPW]);
+      for (int t = 0; t < ns; t++) e[t * HPW] = lt_expf(e[t * HPW] - mx);
+      float bt[32];
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        const float lo = e[j * HPW], hi = e[(j + 32) * HPW];
+        bt[j] = (j < ns ? lo : 0.0f) + (j + 32 < ns ? hi : 0.0f);
+      }
+#pragma unroll
+      for (int w = 16; w >= 1; w /= 2)
+#pragma unroll
+        for (int j = 0; j < w; j++) bt[j] = bt[j] + bt[j + w];
+      srm[pi] = mx;
+      srm[rm_np + pi] = bt[0];
+    }
+    __syncthreads();
+    for (int pi = l; pi < rm_np; pi += 64) {
+      const int r = pi % HPW;
+      float M = -1e30f;
+      for (int q = 0; q < A.nsplit; q++) M = fmaxf(M, srm[q * HPW + r]);
+      srm[2 * rm_np + pi] = lt_expf(srm[pi] - M);
+    }
+    __syncthreads();
+    if (l < HPW) {
+      float Z = 0.0f;
+      for (int q = 0; q < A.nsplit; q++) Z = fmaf(srm[2 * rm_np + q * HPW + l], srm[rm_np + q * HPW + l], Z);
+      srm[3 * rm_np + l] = Z;
+    }
+  } else {
+  // max (order-free: from the stored scores), exps and Z
 #pragma unroll
   for (int r = 0; r < HPW; r++) m[r] = -1e30f;
   for (int t = l; t < n; t += 64) {
@@ -807,6 +857,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   }
 #pragma unroll
   for (int r = 0; r < HPW; r++) zs[r] = wave_tree_dpp(zs[r]);   // lane 0: Z of head r
+  }
   // exps of 0 up to the O loop's last ring (those rows read zeros from V)
   {
     const int n_up = (n + kVRing - 1) / kVRing * kVRing;
@@ -823,6 +874,28 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   for (int r = 0; r < HPW; r++)
 #pragma unroll
     for (int k = 0; k < OPL; k++) o[r][k] = 0.0f;
+  // kRM: a[r][k] = sum over splits s ascending of fma(w_s, O_s), each split's chain O_s
+  // restarting from 0 at its first row (the trailing empty splits add fma(0, 0, a) = a);
+  // rm_nb = rows folded when the current split rm_s ends (-1 after the last)
+  float a[kRM ? HPW : 1][kRM ? OPL : 1];
+#pragma unroll
+  for (int r = 0; r < (kRM ? HPW : 1); r++)
+#pragma unroll
+    for (int k = 0; k < (kRM ? OPL : 1); k++) a[r][k] = 0.0f;
+  int rm_s = 0, rm_nb = kRM ? (n < rm_per ? n : rm_per) : -1;
+  auto rm_merge = [&]() {
+#pragma unroll
+    for (int r = 0; r < (kRM ? HPW : 1); r++) {
+      const float w = srm[2 * rm_np + rm_s * HPW + r];
+#pragma unroll
+      for (int k = 0; k < (kRM ? OPL : 1); k++) {
+        a[r][k] = fmaf(w, o[r][k], a[r][k]);
+        o[r][k] = 0.0f;
+      }
+    }
+    rm_s++;
+    rm_nb = rm_nb == n ? -1 : (rm_nb + rm_per < n ? rm_nb + rm_per : n);
+  };
   // The exps of a group of kEg rows are read one group ahead (the per-row fence below keeps
   // the ring in registers and would otherwise make every row wait for its LDS read).
   static_assert(kVRing % kEg == 0, "k_attn_w1: ring of whole exp groups");
@@ -906,6 +979,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
         // land in the same registers and the ring needs no copies at the loop's back edge
         fold_row(ec[j], x);
         load_v(t0 + k + kVRing, v[k]);
+        if constexpr (kRM) {
+          if (t0 + k + 1 == rm_nb) rm_merge();
+        }
       }
 #pragma unroll
       for (int j = 0; j < kEg; j++)
@@ -924,7 +1000,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   // @phase attn 4
   // outputs: dims [l*OPL, l*OPL + OPL) of each head
   const size_t hrow0 = (size_t)b * A.nh + h0;
-  if (A.nsplit == 1) {
+  if constexpr (kRM) {
+#pragma unroll
+    for (int r = 0; r < HPW; r++) {
+      const float z = srm[3 * rm_np + r];
+#pragma unroll
+      for (int k = 0; k < OPL; k++) A.out[(hrow0 + r) * HD + l * OPL + k] = a[r][k] / z;
+    }
+  } else if (A.nsplit == 1) {
 #pragma unroll
     for (int r = 0; r < HPW; r++) {
       const float z = __shfl(zs[r], 0, 64);
@@ -1077,6 +1160,16 @@ hipError_t launch_w1(int hpw, int dpl, dim3 grid, size_t shm, hipStream_t st, co
   return hipErrorInvalidValue;
 }
 
+// LT_ATTN_PREFILL_RM=0 keeps a prefill with splits on partials + k_attn_merge (for
+// comparisons); the default merges each row's splits in its own wave where they fit.
+bool use_rm() {
+  static const bool on = [] {
+    const char* s = getenv("LT_ATTN_PREFILL_RM");
+    return !(s && s[0] == '0');
+  }();
+  return on;
+}
+
 // LT_ATTN_W1=0 keeps every mode on k_attn (for comparisons); the default is k_attn_w1
 // wherever its head sizes and LDS budget apply.
 bool use_w1() {
@@ -1121,6 +1214,19 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
   // fp16: 64, 128 or 256 dims; fp32: 64 or 128 (a K row of 8 to 32 16-byte units)
   const bool w1 = use_w1() && A.hd % 64 == 0 &&
                   (f16 ? (dpl == 1 || dpl == 2 || dpl == 4) : (dpl == 1 || dpl == 2)) && w1_shm <= 64 * 1024;
+  // a prefill row's splits in one wave (AM_PREFILL_RM): at most 64 positions per split (each
+  // lane of a split's Z tree then holds one position) and the whole row's scores in LDS
+  const size_t per_up_rm = (size_t)(A.maxt + ring - 1) / ring * ring;
+  const size_t rm_shm = ((size_t)h * A.hd + kpr * (ku + 1) * 4 + ((per_up_rm + 8 + 1 + 64) * h + 3) / 4 * 4 +
+                         3 * (size_t)A.nsplit * h + h) * sizeof(float);
+  if (w1 && mode == AM_PREFILL && A.nsplit > 1 && per_max <= 64 && rm_shm <= 64 * 1024 && use_rm()) {
+    A.per_max = A.maxt;
+    const dim3 grid(1, A.nh / h, rows);
+    const hipError_t e = f16 ? launch_w1<true, AM_PREFILL_RM>(h, dpl, grid, rm_shm, ctx->stream, A)
+                             : launch_w1<false, AM_PREFILL_RM>(h, dpl, grid, rm_shm, ctx->stream, A);
+    if (e != hipSuccess) return lt_fail_hip(e, what, __FILE__, __LINE__);
+    return lt_check_launch("k_attn_w1");
+  }
   if (A.nsplit > 1 && (w1 || !(mode == AM_PREFILL && A.nsplit <= kMaxInWgSplits &&
                                ((size_t)hpw * A.hd + 2 * A.hd + (size_t)hpw * A.maxt + kVChunkFloats) *
                                        sizeof(float) <= 64 * 1024))) {

@@ -242,7 +242,8 @@ def test_attention_decode_geometries(gpu, oracle, kv_dtype, hd, nh, nkv):
 @pytest.mark.parametrize("kv_dtype,nh,nkv,hd", [(LT_KV_F16, 14, 2, 64), (LT_KV_F32, 14, 2, 64),
                                                  (LT_KV_F16, 32, 8, 128), (LT_KV_F32, 16, 2, 128),
                                                  (LT_KV_F16, 8, 8, 256)])
-@pytest.mark.parametrize("len0,T,nsplit", [(0, 37, 1), (5, 40, 4), (0, 70, 16), (200, 33, 7)])
+@pytest.mark.parametrize("len0,T,nsplit", [(0, 37, 1), (5, 40, 4), (0, 70, 16), (200, 33, 7), (250, 50, 5),
+                                            (0, 300, 16), (3, 61, 64)])
 def test_attention_prefill(gpu, oracle, kv_dtype, nh, nkv, hd, len0, T, nsplit):
     """Causal prefill attention: query t of T attends the first len0 + t + 1 rows of one
     cache, each exactly as a decode of that length (split layout per query, empty splits for
