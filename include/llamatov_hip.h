@@ -247,7 +247,7 @@ LT_API int lt_q8_gemm_silu(lt_ctx* ctx, const void* Wgu, const int8_t* Xq, const
  *   r = 0..31, at 32*r, then their fp16 scales at 1024 + 2*r; rows past N are zero.
  *   lt_q8_tiles_bytes(N, K) bytes, built on the device by lt_q8_tiles (Wt 16-byte aligned);
  * - block-major activation quants: lt_quant_q8_bm writes token t's block b of x [T][K] (the
- *   lt_quant_q8 quantizer) to Xq[b][t][32] and Xd[b][t]. */
+ *   lt_quant_q8 quantizer) to Xq[b][t][32] and Xd[b][t] (x 16-byte aligned, Xq 16, Xd 2). */
 LT_API size_t lt_q8_tiles_bytes(int N, int K);
 LT_API int lt_q8_tiles(lt_ctx* ctx, const void* W, void* Wt, int N, int K);
 LT_API int lt_quant_q8_bm(lt_ctx* ctx, const float* x, int8_t* xq, uint16_t* xd, int T, int K);

@@ -104,7 +104,10 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__
 
 // k_rmsnorm_quant over T rows with block-major output (the prefill GEMM's activation layout):
 // row t's block b goes to xq[(b*T + t)*32 ..], xd[b*T + t].  The same arithmetic as
-// k_rmsnorm followed by k_quant_q8 per row.
+// k_rmsnorm followed by k_quant_q8 per row: thread j's elements j, j+256, ... (NPT at most)
+// are loaded at once into registers, with the weights, and folded in that order, then the
+// block tree of rms_inv_block256.
+template <int NPT>
 __global__ __launch_bounds__(256) void k_rmsnorm_quant_bm(const float* __restrict__ x,
                                                           const float* __restrict__ w,
                                                           int8_t* __restrict__ xq,
@@ -113,13 +116,37 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant_bm(const float* __restric
   extern __shared__ float ybuf[];  // [N]
   __shared__ float red[256];
   __shared__ float sinv;
-  const int t = blockIdx.x;
+  const int t = blockIdx.x, tid = threadIdx.x;
   const float* xr = x + (size_t)t * N;
-  float inv = rms_inv_block256(xr, N, eps, red, &sinv);
-  for (int j = threadIdx.x; j < N; j += 256) ybuf[j] = (xr[j] * inv) * w[j];
+  float xv[NPT], wv[NPT];
+#pragma unroll
+  for (int i = 0; i < NPT; i++) {
+    const int j = tid + 256 * i;
+    xv[i] = j < N ? xr[j] : 0.0f;
+    wv[i] = j < N ? w[j] : 0.0f;
+  }
+  float p = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NPT; i++)
+    if (tid + 256 * i < N) p = fmaf(xv[i], xv[i], p);
+  red[tid] = p;
   __syncthreads();
-  int lane = threadIdx.x & 31;
-  for (int b = threadIdx.x >> 5; b < N / 32; b += 8) {
+  if (tid < 64) {
+    float a = red[tid] + red[tid + 128];
+    float b = red[tid + 64] + red[tid + 192];
+    float c = a + b;
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) c = c + __shfl_down(c, s, 64);
+    if (tid == 0) sinv = lt_rsqrtf(c / (float)N + eps);
+  }
+  __syncthreads();
+  const float inv = sinv;
+#pragma unroll
+  for (int i = 0; i < NPT; i++)
+    if (tid + 256 * i < N) ybuf[tid + 256 * i] = (xv[i] * inv) * wv[i];
+  __syncthreads();
+  int lane = tid & 31;
+  for (int b = tid >> 5; b < N / 32; b += 8) {
     const size_t ob = (size_t)b * T + t;
     quant_block_hw(ybuf[b * 32 + lane], lane, xq + ob * 32, xd + ob);
   }
@@ -379,7 +406,10 @@ int lt_rmsnorm_quant_bm(lt_ctx* ctx, const float* x, const float* w, int8_t* xq,
   LT_REQUIRE(T > 0 && N > 0 && N % 32 == 0 && N <= 16384, "lt_rmsnorm_quant_bm: T=%d N=%d (N multiple of 32, <= 16384)",
              T, N);
   LT_REQUIRE(lt_aligned(xq, 16) && lt_aligned(xd, 2), "lt_rmsnorm_quant_bm: misaligned argument");
-  k_rmsnorm_quant_bm<<<T, 256, (size_t)N * sizeof(float), ctx->stream>>>(x, w, xq, xd, T, N, eps);
+  const size_t shm = (size_t)N * sizeof(float);
+  if (N <= 1024) k_rmsnorm_quant_bm<4><<<T, 256, shm, ctx->stream>>>(x, w, xq, xd, T, N, eps);
+  else if (N <= 4096) k_rmsnorm_quant_bm<16><<<T, 256, shm, ctx->stream>>>(x, w, xq, xd, T, N, eps);
+  else k_rmsnorm_quant_bm<64><<<T, 256, shm, ctx->stream>>>(x, w, xq, xd, T, N, eps);
   return lt_check_launch("k_rmsnorm_quant_bm");
 }
 

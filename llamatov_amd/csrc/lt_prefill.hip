@@ -518,12 +518,17 @@ __global__ __launch_bounds__(256) void k_q8_tiles(const uint16_t* __restrict__ W
 }
 __global__ __launch_bounds__(256) void k_quant_q8_bm(const float* __restrict__ x, int8_t* __restrict__ xq,
                                                      uint16_t* __restrict__ xd, int T, int nbk) {
-  const long ob = (long)blockIdx.x * 8 + (threadIdx.x >> 5);
-  const int lane = threadIdx.x & 31;
-  if (ob >= (long)T * nbk) return;   // uniform per half-wave
+  // 8 lanes per output block (4 consecutive elements each, one 16-byte load), 32 blocks
+  // per workgroup; consecutive blocks of the output are consecutive tokens of one block column
+  const long ob = (long)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const int j = threadIdx.x & 7;
+  if (ob >= (long)T * nbk) return;   // uniform per 8-lane group
   const int b = (int)(ob / T), t = (int)(ob - (long)b * T);
-  const float v = x[((size_t)t * nbk + b) * 32 + lane];
-  quant_block_hw(v, lane, xq + ob * 32, xd + ob);
+  const float4 v = *(const float4*)(x + ((size_t)t * nbk + b) * 32 + 4 * j);
+  QScale s;
+  const uint32_t p = quant4(v.x, v.y, v.z, v.w, s);
+  ((uint32_t*)(xq + ob * 32))[j] = p;
+  if (j == 0) xd[ob] = s.h;
 }
 
 int check_gemm(const char* fn, const void* W, const int8_t* Xq, const uint16_t* Xd, const float* Y, int T, int N,
@@ -633,7 +638,8 @@ int lt_quant_q8_bm(lt_ctx* ctx, const float* x, int8_t* xq, uint16_t* xd, int T,
   LT_REQUIRE(T > 0 && K > 0 && K % 32 == 0, "lt_quant_q8_bm: T=%d K=%d", T, K);
   LT_REQUIRE(lt_aligned(xq, 16) && lt_aligned(xd, 2), "lt_quant_q8_bm: misaligned argument");
   const long nblk = (long)T * (K / 32);
-  k_quant_q8_bm<<<(unsigned)((nblk + 7) / 8), 256, 0, ctx->stream>>>(x, xq, xd, T, K / 32);
+  LT_REQUIRE(lt_aligned(x, 16), "lt_quant_q8_bm: x must be 16-byte aligned");
+  k_quant_q8_bm<<<(unsigned)((nblk + 31) / 32), 256, 0, ctx->stream>>>(x, xq, xd, T, K / 32);
   return lt_check_launch("k_quant_q8_bm");
 }
 

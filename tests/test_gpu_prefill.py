@@ -114,7 +114,7 @@ def test_q8_tiles_layout(gpu, N, K):
     assert np.array_equal(Wt.to_host(), tiles_host(W, N, K).reshape(-1))
 
 
-@pytest.mark.parametrize("T,K", [(37, 896), (1, 32), (130, 4864)])
+@pytest.mark.parametrize("T,K", [(37, 896), (1, 32), (130, 4864), (67, 14336)])
 def test_quant_q8_block_major(gpu, oracle, T, K):
     case(f"quant_q8_bm T={T} K={K}")
     rng = np.random.default_rng(T * K)
