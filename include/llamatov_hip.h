@@ -278,6 +278,16 @@ LT_API int lt_kv_append_batch(lt_ctx* ctx, void* kc, void* vc, const float* src,
 /* *len += T, capped at maxt. */
 LT_API int lt_len_add(lt_ctx* ctx, int* len, int T, int maxt);
 
+/* lt_rope_batch of the nh q and nkv k heads of T rows of q|k|v (row_stride floats apart),
+ * then lt_kv_append_batch of their k and v (k_off = nh*hd, v_off = (nh+nkv)*hd, width
+ * nkv*hd), in one launch (no reference counterpart; the same q rows and cache rows).  The
+ * roped k is written to the cache only, not back into the rows.  hd even, at most 256. */
+LT_API int lt_rope_append_batch(lt_ctx* ctx, float* qkv, int T, int row_stride, const int* len, int nh, int nkv,
+                                int hd, const float* freqs, void* kc, void* vc, int maxt, int kv_dtype);
+/* lt_len_add of len[0 .. n-1] in one launch (the prefill's per-layer lengths after its last
+ * layer; no reference counterpart). */
+LT_API int lt_len_add_n(lt_ctx* ctx, int* len, int n, int T, int maxt);
+
 /* Causal attention of T query tokens of one sequence over its cache (k_attn_decode_masked's
  * order per query): query t (q + t*q_stride) attends *len0 + t + 1 positions; out [T][nh*hd].
  * nsplit and ws as lt_attn_decode with batch = T. */

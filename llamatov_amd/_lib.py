@@ -70,6 +70,8 @@ _SIGS = {
     "lt_rope_batch": (c_int, [_P, _P, c_int, c_int, _P, c_int, c_int, _P]),
     "lt_kv_append_batch": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, _P, c_int, c_int, c_int]),
     "lt_len_add": (c_int, [_P, _P, c_int, c_int]),
+    "lt_rope_append_batch": (c_int, [_P, _P, c_int, c_int, _P, c_int, c_int, c_int, _P, _P, _P, c_int, c_int]),
+    "lt_len_add_n": (c_int, [_P, _P, c_int, c_int, c_int]),
     "lt_attn_prefill": (c_int, [_P, _P, c_int, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float, c_int,
                                 c_int, c_int, _P, c_size_t]),
     "lt_embed_q8_batch": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _P]),

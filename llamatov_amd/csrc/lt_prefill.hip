@@ -491,6 +491,58 @@ __global__ __launch_bounds__(256) void k_embed_batch(const uint8_t* __restrict__
   x[(size_t)t * E + i] = v;
 }
 
+// k_rope_batch of the q and k heads of one row of q|k|v, then k_kv_append_batch of its k
+// and v, in one workgroup per token: the hd/2 angles of the row's position are evaluated
+// once (lt_sincosf of the same products) into LDS and shared by every head.  The roped k
+// goes to the cache only (not back into the row).
+template <bool kF16>
+__global__ __launch_bounds__(256) void k_rope_append_batch(float* __restrict__ qkv, int row_stride,
+                                                           const int* __restrict__ len, int nh, int nkv, int hd,
+                                                           const float* __restrict__ freqs, void* __restrict__ kc,
+                                                           void* __restrict__ vc, int maxt) {
+  __shared__ float s_sn[128], s_cs[128];
+  const int t = blockIdx.x;
+  const int half = hd >> 1;
+  const int pos = *len + t;
+  for (int j = threadIdx.x; j < half; j += 256) lt_sincosf((float)pos * freqs[j], &s_sn[j], &s_cs[j]);
+  __syncthreads();
+  float* row = qkv + (size_t)t * row_stride;
+  const bool app = pos >= 0 && pos < maxt;
+  const int width = nkv * hd;
+  auto put = [&](void* c, size_t off, float v) {
+    if (kF16) ((uint16_t*)c)[off] = lt_float_to_half_bits(v);
+    else ((float*)c)[off] = v;
+  };
+  for (int i = threadIdx.x; i < (nh + nkv) * half; i += 256) {
+    const int hh = i / half, j = i - hh * half;
+    float* base = row + (size_t)hh * hd;
+    const float x1 = base[j], x2 = base[j + half];
+    const float sn = s_sn[j], cs = s_cs[j];
+    const float o1 = fmaf(x1, cs, -(x2 * sn));
+    const float o2 = fmaf(x1, sn, x2 * cs);
+    if (hh < nh) {
+      base[j] = o1;
+      base[j + half] = o2;
+    } else if (app) {
+      const size_t off = (size_t)pos * width + (size_t)(hh - nh) * hd + j;
+      put(kc, off, o1);
+      put(kc, off + half, o2);
+    }
+  }
+  if (app) {
+    const float* v = row + (size_t)(nh + nkv) * hd;
+    for (int i = threadIdx.x; i < width; i += 256) put(vc, (size_t)pos * width + i, v[i]);
+  }
+}
+
+// n consecutive lengths each advanced by T (clamped to maxt)
+__global__ void k_len_add_n(int* __restrict__ len, int n, int T, int maxt) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const int L = len[i] + T;
+    len[i] = L < maxt ? L : maxt;
+  }
+}
+
 __global__ void k_len_add(int* __restrict__ len, int T, int maxt) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
     const int L = *len + T;
@@ -680,6 +732,26 @@ int lt_embed_q8_batch(lt_ctx* ctx, const void* emb, const int* toks, float* x, i
   LT_REQUIRE(T > 0 && E > 0 && E % 32 == 0 && vocab > 0, "lt_embed_q8_batch: T=%d E=%d vocab=%d", T, E, vocab);
   k_embed_batch<<<dim3((E + 255) / 256, T), 256, 0, ctx->stream>>>((const uint8_t*)emb, toks, x, E, vocab, err);
   return lt_check_launch("k_embed_batch");
+}
+
+int lt_rope_append_batch(lt_ctx* ctx, float* qkv, int T, int row_stride, const int* len, int nh, int nkv, int hd,
+                         const float* freqs, void* kc, void* vc, int maxt, int kv_dtype) {
+  LT_REQUIRE(ctx && qkv && len && freqs && kc && vc, "lt_rope_append_batch: null argument");
+  LT_REQUIRE(T > 0 && nh > 0 && nkv > 0 && hd > 0 && hd % 2 == 0 && hd <= 256 && maxt > 0 &&
+                 row_stride >= (nh + 2 * nkv) * hd,
+             "lt_rope_append_batch: T=%d nh=%d nkv=%d hd=%d row_stride=%d maxt=%d", T, nh, nkv, hd, row_stride, maxt);
+  LT_REQUIRE(kv_dtype == LT_KV_F32 || kv_dtype == LT_KV_F16, "lt_rope_append_batch: kv_dtype=%d", kv_dtype);
+  if (kv_dtype == LT_KV_F16)
+    k_rope_append_batch<true><<<T, 256, 0, ctx->stream>>>(qkv, row_stride, len, nh, nkv, hd, freqs, kc, vc, maxt);
+  else
+    k_rope_append_batch<false><<<T, 256, 0, ctx->stream>>>(qkv, row_stride, len, nh, nkv, hd, freqs, kc, vc, maxt);
+  return lt_check_launch("k_rope_append_batch");
+}
+
+int lt_len_add_n(lt_ctx* ctx, int* len, int n, int T, int maxt) {
+  LT_REQUIRE(ctx && len && n > 0 && T >= 0 && maxt > 0, "lt_len_add_n: bad argument");
+  k_len_add_n<<<1, 256, 0, ctx->stream>>>(len, n, T, maxt);
+  return lt_check_launch("k_len_add_n");
 }
 
 int lt_len_add(lt_ctx* ctx, int* len, int T, int maxt) {

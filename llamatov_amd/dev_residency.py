@@ -725,17 +725,21 @@ def forward_prefill(plan: DecodePlan, tokens) -> None:
     D.h2d(B.toks.ptr, toks)
     call("lt_embed_q8_batch", h, m.tok_embd.t.vp, B.toks.vp, B.x.vp, T, E, cfg.vocab, plan.err.vp)
     ws, ws_n = _vp(B.ws), (B.ws.nbytes if B.ws is not None else 0)
+    # the layers' lengths sit in one array (each layer's attention reads only its own, so
+    # they can all advance after the last layer) when the plan allocated them together
+    lens_joint = all(c.len_ptr == plan.lens.ptr + 4 * il and c.max_seq == plan.caches[0].max_seq
+                     for il, c in enumerate(plan.caches))
     for il, L in enumerate(m.layers):
         cache = plan.caches[il]
         lp = _vp(cache.len_ptr)
         call("lt_rmsnorm_quant_bm", h, B.x.vp, L["attn_norm"].vp, B.xq.vp, B.xd.vp, T, E, eps)
         call("lt_q8_gemm_t", h, L["wqkv_t"].t.vp, B.xq.vp, B.xd.vp, _vp(L["bqkv"]), None, B.qkv.vp, T, NQ, E)
-        call("lt_rope_batch", h, B.qkv.vp, T, NQ, lp, nh + nkv, hd, m.freqs.vp)
-        call("lt_kv_append_batch", h, cache.k.vp, cache.v.vp, B.qkv.vp, NQ, QD, QD + KD, T, lp, KD,
+        call("lt_rope_append_batch", h, B.qkv.vp, T, NQ, lp, nh, nkv, hd, m.freqs.vp, cache.k.vp, cache.v.vp,
              cache.max_seq, p.kv_dtype)
         call("lt_attn_prefill", h, B.qkv.vp, NQ, cache.k.vp, cache.v.vp, lp, B.att.vp, T, nh, nkv, hd,
              ctypes.c_float(plan.scale), cache.max_seq, p.attn_nsplit, p.kv_dtype, ws, ws_n)
-        call("lt_len_add", h, lp, T, cache.max_seq)
+        if not lens_joint:
+            call("lt_len_add", h, lp, T, cache.max_seq)
         call("lt_quant_q8_bm", h, B.att.vp, B.xq.vp, B.xd.vp, T, QD)
         call("lt_q8_gemm_t", h, L["wo_t"].t.vp, B.xq.vp, B.xd.vp, None, B.x.vp, B.xres.vp, T, E, QD)
         call("lt_rmsnorm_quant_bm", h, B.xres.vp, L["ffn_norm"].vp, B.xq.vp, B.xd.vp, T, E, eps)
@@ -743,6 +747,8 @@ def forward_prefill(plan: DecodePlan, tokens) -> None:
         call("lt_quant_q8_bm", h, B.v.vp, B.xq.vp, B.xd.vp, T, F)
         call("lt_q8_gemm_t", h, L["wdown_t"].t.vp, B.xq.vp, B.xd.vp, None, B.xres.vp, B.x.vp, T, E, F)
         cache.length += T
+    if lens_joint:   # every layer's length, after the last attention that reads one
+        call("lt_len_add_n", h, _vp(plan.lens.ptr), len(m.layers), T, plan.caches[0].max_seq)
     # the last token's logits and greedy token, as the decode step computes them
     D.d2d(plan.carry.ptr, B.x.ptr + (T - 1) * E * 4, E * 4)
     call("lt_q8_gemv_rms_argmax", h, plan.carry.vp, m.output_norm.vp, eps, m.output.t.vp, plan.logits.vp,

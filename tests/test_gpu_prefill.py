@@ -45,6 +45,36 @@ def test_rmsnorm_quant_block_major(gpu, T, K):
     assert np.array_equal(d1.to_host(), d2.to_host())
 
 
+@pytest.mark.parametrize("kv_dtype,nh,nkv,hd,T,len0,maxt", [(LT_KV_F16, 32, 8, 128, 77, 5, 100),
+                                                             (LT_KV_F32, 14, 2, 64, 40, 0, 64),
+                                                             (LT_KV_F16, 8, 8, 256, 9, 3, 10),
+                                                             (LT_KV_F32, 4, 1, 128, 6, -2, 8)])
+def test_rope_append_batch(gpu, kv_dtype, nh, nkv, hd, T, len0, maxt):
+    """One launch of RoPE + KV append equals lt_rope_batch followed by lt_kv_append_batch: the
+    same q rows and cache rows, rows at positions outside [0, maxt) roped but not stored."""
+    case(f"rope_append_batch kv={kv_dtype} nh={nh} nkv={nkv} hd={hd} T={T} len0={len0} maxt={maxt}")
+    rng = np.random.default_rng(nh * T + hd)
+    NQ = (nh + 2 * nkv) * hd
+    X = (3.0 * rng.standard_normal((T, NQ))).astype(np.float32)
+    freqs = (1e4 ** (-np.arange(hd // 2) * 2.0 / hd)).astype(np.float32)
+    et = np.float16 if kv_dtype == LT_KV_F16 else np.float32
+    fill = np.full((maxt, nkv * hd), 7, et)
+    x1, x2, fr, ln = up(X), up(X), up(freqs), up(np.array([len0], np.int32))
+    k1, v1, k2, v2 = up(fill), up(fill), up(fill), up(fill)
+    call("lt_rope_batch", gpu.handle, x1.vp, T, NQ, ln.vp, nh + nkv, hd, fr.vp)
+    call("lt_kv_append_batch", gpu.handle, k1.vp, v1.vp, x1.vp, NQ, nh * hd, (nh + nkv) * hd, T, ln.vp, nkv * hd,
+         maxt, kv_dtype)
+    call("lt_rope_append_batch", gpu.handle, x2.vp, T, NQ, ln.vp, nh, nkv, hd, fr.vp, k2.vp, v2.vp, maxt, kv_dtype)
+    a, b = x1.to_host(), x2.to_host()
+    assert bits(a[:, :nh * hd]).tobytes() == bits(b[:, :nh * hd]).tobytes(), "q rows"
+    assert np.array_equal(a[:, (nh + nkv) * hd:], b[:, (nh + nkv) * hd:]), "v rows untouched"
+    for c1, c2, what in ((k1, k2, "K"), (v1, v2, "V")):
+        assert c1.to_host().tobytes() == c2.to_host().tobytes(), f"{what} cache"
+    lens = up(np.array([0, 5, maxt - 1, maxt], np.int32))
+    call("lt_len_add_n", gpu.handle, lens.vp, 3, T, maxt)
+    assert lens.to_host().tolist() == [min(T, maxt), min(5 + T, maxt), maxt, maxt]
+
+
 @pytest.mark.parametrize("N,K,T,epi", [(1152, 896, 37, "bias"), (896, 4864, 130, "resid"), (100, 96, 5, "store"),
                                        (64, 1024, 129, "store"), (4096, 4096, 33, "store"), (40, 14336, 3, "resid")])
 def test_q8_gemm_matches_gemv_per_token(gpu, oracle, N, K, T, epi):
