@@ -1201,6 +1201,13 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
     }();
     const int c = cap > 0 ? cap : per_max <= 256 ? 1 : 8;
     while (h > c && h > 1) h /= 2;
+  } else if (mode == AM_PREFILL) {
+    // LT_ATTN_PREFILL_HPW=H caps a prefill's heads per wave (sweeps)
+    static const int pcap = [] {
+      const char* s = getenv("LT_ATTN_PREFILL_HPW");
+      return s ? atoi(s) : 0;
+    }();
+    while (pcap > 0 && h > pcap && h > 1) h /= 2;
   }
   const int dpl = A.hd / 64;
   const size_t ku = (size_t)A.hd * (f16 ? 2 : 4) / 16;
