@@ -113,7 +113,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant_bm(const float* __restric
                                                           int8_t* __restrict__ xq,
                                                           uint16_t* __restrict__ xd, int T, int N,
                                                           float eps) {
-  extern __shared__ float ybuf[];  // [N]
+  extern __shared__ __attribute__((aligned(16))) float ybuf[];  // [N]
   __shared__ float red[256];
   __shared__ float sinv;
   const int t = blockIdx.x, tid = threadIdx.x;
@@ -145,10 +145,15 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant_bm(const float* __restric
   for (int i = 0; i < NPT; i++)
     if (tid + 256 * i < N) ybuf[tid + 256 * i] = (xv[i] * inv) * wv[i];
   __syncthreads();
-  int lane = tid & 31;
-  for (int b = tid >> 5; b < N / 32; b += 8) {
+  // 8 lanes per block, 4 elements each (quant4: the quantizer of quant_block_hw)
+  const int j = tid & 7;
+  for (int b = tid >> 3; b < N / 32; b += 32) {
     const size_t ob = (size_t)b * T + t;
-    quant_block_hw(ybuf[b * 32 + lane], lane, xq + ob * 32, xd + ob);
+    const float4 v = *(const float4*)(ybuf + b * 32 + 4 * j);
+    QScale sc;
+    const uint32_t p = quant4(v.x, v.y, v.z, v.w, sc);
+    ((uint32_t*)(xq + ob * 32))[j] = p;
+    if (j == 0) xd[ob] = sc.h;
   }
 }
 

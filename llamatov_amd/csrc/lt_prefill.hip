@@ -493,8 +493,9 @@ __global__ __launch_bounds__(256) void k_embed_batch(const uint8_t* __restrict__
 
 // k_rope_batch of the q and k heads of one row of q|k|v, then k_kv_append_batch of its k
 // and v, in one workgroup per token: the hd/2 angles of the row's position are evaluated
-// once (lt_sincosf of the same products) into LDS and shared by every head.  The roped k
-// goes to the cache only (not back into the row).
+// once (lt_sincosf of the same products) into LDS and shared by every head; gridDim.y
+// workgroups share a token's pairs and V elements.  The roped k goes to the cache only (not
+// back into the row).
 template <bool kF16>
 __global__ __launch_bounds__(256) void k_rope_append_batch(float* __restrict__ qkv, int row_stride,
                                                            const int* __restrict__ len, int nh, int nkv, int hd,
@@ -513,7 +514,8 @@ __global__ __launch_bounds__(256) void k_rope_append_batch(float* __restrict__ q
     if (kF16) ((uint16_t*)c)[off] = lt_float_to_half_bits(v);
     else ((float*)c)[off] = v;
   };
-  for (int i = threadIdx.x; i < (nh + nkv) * half; i += 256) {
+  const int i0 = threadIdx.x + 256 * blockIdx.y, istep = 256 * gridDim.y;
+  for (int i = i0; i < (nh + nkv) * half; i += istep) {
     const int hh = i / half, j = i - hh * half;
     float* base = row + (size_t)hh * hd;
     const float x1 = base[j], x2 = base[j + half];
@@ -531,7 +533,7 @@ __global__ __launch_bounds__(256) void k_rope_append_batch(float* __restrict__ q
   }
   if (app) {
     const float* v = row + (size_t)(nh + nkv) * hd;
-    for (int i = threadIdx.x; i < width; i += 256) put(vc, (size_t)pos * width + i, v[i]);
+    for (int i = i0; i < width; i += istep) put(vc, (size_t)pos * width + i, v[i]);
   }
 }
 
@@ -742,9 +744,11 @@ int lt_rope_append_batch(lt_ctx* ctx, float* qkv, int T, int row_stride, const i
              "lt_rope_append_batch: T=%d nh=%d nkv=%d hd=%d row_stride=%d maxt=%d", T, nh, nkv, hd, row_stride, maxt);
   LT_REQUIRE(kv_dtype == LT_KV_F32 || kv_dtype == LT_KV_F16, "lt_rope_append_batch: kv_dtype=%d", kv_dtype);
   if (kv_dtype == LT_KV_F16)
-    k_rope_append_batch<true><<<T, 256, 0, ctx->stream>>>(qkv, row_stride, len, nh, nkv, hd, freqs, kc, vc, maxt);
+    k_rope_append_batch<true><<<dim3(T, 4), 256, 0, ctx->stream>>>(qkv, row_stride, len, nh, nkv, hd, freqs, kc, vc,
+                                                                    maxt);
   else
-    k_rope_append_batch<false><<<T, 256, 0, ctx->stream>>>(qkv, row_stride, len, nh, nkv, hd, freqs, kc, vc, maxt);
+    k_rope_append_batch<false><<<dim3(T, 4), 256, 0, ctx->stream>>>(qkv, row_stride, len, nh, nkv, hd, freqs, kc, vc,
+                                                                     maxt);
   return lt_check_launch("k_rope_append_batch");
 }
 
