@@ -25,7 +25,6 @@ HIP_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-ffp-contract=off",
     "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -56,15 +55,30 @@ def hipcc() -> str:
     raise RuntimeError(f"hipcc not found under {rocm}; ROCm is required to build {LIB_NAME}")
 
 
-def build(verbose: bool = True) -> Path:
-    """Compile every HIP source into llamatov_amd/libllamatov_hip.so (always recompiles)."""
-    out_tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIP_FLAGS, *map(str, sources()), "-o", str(out_tmp)]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print("[build]", " ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed ({r.returncode}):\n{r.stdout}\n{r.stderr}")
+
+
+def build(verbose: bool = True, jobs: int | None = None) -> Path:
+    """Compile every HIP source into llamatov_amd/libllamatov_hip.so (always recompiles):
+    one object per source, compiled in parallel, then one shared-library link."""
+    from concurrent.futures import ThreadPoolExecutor
+    import tempfile
+
+    out_tmp = LIB_PATH.with_suffix(".so.tmp")
+    srcs = sources()
+    with tempfile.TemporaryDirectory(prefix="lt_build_") as tmp:
+        objs = [Path(tmp) / (s.stem + ".o") for s in srcs]
+        n = jobs or min(len(srcs), max(1, min(8, len(os.sched_getaffinity(0)))))
+        with ThreadPoolExecutor(max_workers=n) as ex:
+            list(ex.map(lambda so: _run([hipcc(), *HIP_FLAGS, "-c", str(so[0]), "-o", str(so[1])], verbose),
+                        zip(srcs, objs)))
+        _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(out_tmp)],
+             verbose)
     os.replace(out_tmp, LIB_PATH)
     (PKG_DIR / (LIB_NAME + ".sha256")).write_text(source_digest() + "\n")
     return LIB_PATH

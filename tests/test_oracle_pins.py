@@ -315,3 +315,33 @@ def test_argmax_ties_lowest_index(oracle):
     assert oracle.argmax(x) == int(np.argmax(x))
     x[1000] = x[50000] = np.float32(100.0)
     assert oracle.argmax(x) == 1000
+
+
+def test_attention_z_fold_order_is_pinned(oracle):
+    """Z is a 64-lane strided fold plus a pairwise tree (bpd/lib/dev_residency.py:1968-2008),
+    not a sequential sum.  Scores 0 at t = 0 and -17.5 elsewhere give e_0 = 1 and 63 values
+    e ~ 2.5e-8, each below half an ulp of 1: a sequential sum drops every one of them (Z = 1),
+    while the tree first adds them among themselves and its last levels add 4e..32e to lane
+    0 (Z ~ 1 + 60e).  With V = 1 at t = 0 (dim 0) and 0 elsewhere, out = 1 / Z."""
+    hd, L = 64, 64
+    q = np.zeros(hd, np.float32)
+    q[0] = 8.0
+    k = np.zeros((L, hd), np.float32)
+    k[1:, 0] = -17.5                  # s_t = 8 * k * 0.125 = k
+    v = np.zeros((L, hd), np.float32)
+    v[0, 0] = 1.0
+    out = oracle.attn_decode(q, k, v, L, 1, 1, hd, 0.125, False)
+    e = np.float32(oracle.expf(-17.5))
+    assert np.float32(1.0) + e == np.float32(1.0)          # each alone is lost against 1
+    # the declared tree, evaluated by hand: lane t (t < 64) holds e_t; s = 32, 16, ..., 1
+    lanes = [np.float32(1.0)] + [e] * 63
+    s = 32
+    while s >= 1:
+        for t in range(s):
+            lanes[t] = np.float32(lanes[t] + lanes[t + s])
+        s //= 2
+    z_tree = lanes[0]
+    assert z_tree > np.float32(1.0)
+    assert out[0] == np.float32(np.float32(1.0) / z_tree)
+    assert out[0] != np.float32(1.0)                        # the sequential-sum result
+    assert np.all(out[1:] == 0.0)
