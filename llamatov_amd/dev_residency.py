@@ -654,8 +654,16 @@ class DecodePlan:
             call("lt_rmsnorm", h, x.vp, w.vp, self.h.vp, 1, E, eps)
             call("lt_quant_q8", h, self.h.vp, self.xq.vp, self.xd.vp, E)
 
+    def check_room(self, n: int = 1) -> None:
+        """Refuse n more positions when the KV caches cannot hold them: past max_ctx the step
+        kernels would attend over an empty context and drop the new row."""
+        if self.caches[0].length + n > self.max_ctx:
+            raise ValueError(f"KV cache full: {self.caches[0].length} + {n} positions exceed "
+                             f"max_ctx {self.max_ctx}")
+
     def step(self, tok: int | None = None) -> None:
         """Eager step (tok=None: use the device token left by the previous argmax)."""
+        self.check_room(1)
         if tok is not None:
             self.set_token(tok)
         self.enqueue_step()
@@ -716,6 +724,11 @@ def forward_prefill(plan: DecodePlan, tokens) -> None:
         raise ValueError(f"prefill of {T} tokens overflows the {plan.max_ctx}-position KV cache")
     if "wgu_il" not in m.layers[0]:
         raise ValueError("forward_prefill needs the fused gate|up layout (ResidentModel layouts 'fused' or 'both')")
+    # every layer's length sits in the plan's one array, so all of them advance in one launch
+    # after the last layer's attention (each layer's attention reads only its own)
+    if not all(c.len_ptr == plan.lens.ptr + 4 * il and c.max_seq == plan.max_ctx
+               for il, c in enumerate(plan.caches)):
+        raise ValueError("forward_prefill needs the DecodePlan's joint length array")
     m.prefill_tiles()
     B = plan.prefill_buffers(T)
     h = D.handle
@@ -725,10 +738,6 @@ def forward_prefill(plan: DecodePlan, tokens) -> None:
     D.h2d(B.toks.ptr, toks)
     call("lt_embed_q8_batch", h, m.tok_embd.t.vp, B.toks.vp, B.x.vp, T, E, cfg.vocab, plan.err.vp)
     ws, ws_n = _vp(B.ws), (B.ws.nbytes if B.ws is not None else 0)
-    # the layers' lengths sit in one array (each layer's attention reads only its own, so
-    # they can all advance after the last layer) when the plan allocated them together
-    lens_joint = all(c.len_ptr == plan.lens.ptr + 4 * il and c.max_seq == plan.caches[0].max_seq
-                     for il, c in enumerate(plan.caches))
     for il, L in enumerate(m.layers):
         cache = plan.caches[il]
         lp = _vp(cache.len_ptr)
@@ -738,17 +747,15 @@ def forward_prefill(plan: DecodePlan, tokens) -> None:
              cache.max_seq, p.kv_dtype)
         call("lt_attn_prefill", h, B.qkv.vp, NQ, cache.k.vp, cache.v.vp, lp, B.att.vp, T, nh, nkv, hd,
              ctypes.c_float(plan.scale), cache.max_seq, p.attn_nsplit, p.kv_dtype, ws, ws_n)
-        if not lens_joint:
-            call("lt_len_add", h, lp, T, cache.max_seq)
         call("lt_quant_q8_bm", h, B.att.vp, B.xq.vp, B.xd.vp, T, QD)
         call("lt_q8_gemm_t", h, L["wo_t"].t.vp, B.xq.vp, B.xd.vp, None, B.x.vp, B.xres.vp, T, E, QD)
         call("lt_rmsnorm_quant_bm", h, B.xres.vp, L["ffn_norm"].vp, B.xq.vp, B.xd.vp, T, E, eps)
         call("lt_q8_gemm_silu_t", h, L["wgu_il_t"].t.vp, B.xq.vp, B.xd.vp, B.v.vp, T, F, E)
         call("lt_quant_q8_bm", h, B.v.vp, B.xq.vp, B.xd.vp, T, F)
         call("lt_q8_gemm_t", h, L["wdown_t"].t.vp, B.xq.vp, B.xd.vp, None, B.xres.vp, B.x.vp, T, E, F)
+    call("lt_len_add_n", h, _vp(plan.lens.ptr), len(m.layers), T, plan.max_ctx)
+    for cache in plan.caches:   # the host mirror advances with the device lengths
         cache.length += T
-    if lens_joint:   # every layer's length, after the last attention that reads one
-        call("lt_len_add_n", h, _vp(plan.lens.ptr), len(m.layers), T, plan.caches[0].max_seq)
     # the last token's logits and greedy token, as the decode step computes them
     D.d2d(plan.carry.ptr, B.x.ptr + (T - 1) * E * 4, E * 4)
     call("lt_q8_gemv_rms_argmax", h, plan.carry.vp, m.output_norm.vp, eps, m.output.t.vp, plan.logits.vp,
@@ -804,6 +811,7 @@ class GraphRunner:
     def _launch(self) -> None:
         if not self.captured:
             raise RuntimeError("call capture() before replay")
+        self.plan.check_room(1)
         call("lt_graph_launch", self.dev.handle, self.graph)
         for c in self.plan.caches:
             c.length += 1
@@ -827,6 +835,7 @@ class GraphRunner:
         start = self.plan.history_count()
         if start + n > self.plan.hist_cap:
             raise ValueError(f"token history capacity {self.plan.hist_cap} exceeded")
+        self.plan.check_room(n)
         for _ in range(n):
             self._launch()
         return self.plan.history()[start:start + n]
@@ -854,7 +863,9 @@ def generate(model, input_ids, n_tokens: int, profile: Profile = PRODUCTION_PROF
             raise ValueError("generate: empty prompt")
         if n_tokens < 1:
             return []
-        plan = DecodePlan(m, profile, max_ctx=max_ctx, hist_cap=max(4096, n_tokens))
+        # the history records one entry per token through the step's argmax: the prompt's
+        # (when it is fed token by token) and every generated one
+        plan = DecodePlan(m, profile, max_ctx=max_ctx, hist_cap=len(ids) + n_tokens)
         if len(ids) + n_tokens - 1 > plan.max_ctx:
             raise ValueError(f"generate: {len(ids)} prompt + {n_tokens - 1} decode positions exceed "
                              f"the {plan.max_ctx}-position KV cache")

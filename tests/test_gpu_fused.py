@@ -42,7 +42,8 @@ def rand_weight(rng, N, K):
 @pytest.mark.parametrize("N,K,bias", [(1152, 896, True), (896, 896, False), (6144, 4096, False),
                                       (40, 4864, True), (151936, 896, False), (24, 14336, True),
                                       (100003, 896, True), (50001, 640, False), (70001, 1024, True),
-                                      (20003, 896, True), (30000, 512, False), (17000, 1024, False)])
+                                      (20003, 896, True), (30000, 512, False), (17000, 1024, False),
+                                      (128256, 4096, False)])
 def test_q8_gemv_rms(gpu, oracle, N, K, bias):
     case(f"gemv_rms N={N} K={K} bias={bias}")
     rng = np.random.default_rng(21)

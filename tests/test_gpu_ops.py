@@ -110,7 +110,7 @@ def _rand_gemv(rng, N, K):
 
 
 GEMV_SHAPES = [(64, 256), (896, 4864), (896, 896), (1152, 896), (9728, 896), (151936, 896),
-               (4864, 896), (4096, 4096), (14336, 4096), (4096, 14336), (7, 96), (33, 32)]
+               (4864, 896), (4096, 4096), (14336, 4096), (4096, 14336), (128256, 4096), (7, 96), (33, 32)]
 
 
 @pytest.mark.parametrize("N,K", GEMV_SHAPES)
@@ -179,8 +179,8 @@ def test_kv_append_incr(gpu, kv_dtype):
 
 
 def _attn_setup(rng, B, maxt, nkv, hd, kv_dtype, L_list, poison):
-    k = rng.standard_normal((B, maxt, nkv * hd)).astype(np.float32)
-    v = rng.standard_normal((B, maxt, nkv * hd)).astype(np.float32)
+    k = rng.standard_normal((B, maxt, nkv * hd), dtype=np.float32)
+    v = rng.standard_normal((B, maxt, nkv * hd), dtype=np.float32)
     for b, L in enumerate(L_list):
         k[b, L:] = poison
         v[b, L:] = poison
@@ -266,7 +266,8 @@ def test_attention_prefill(gpu, oracle, kv_dtype, nh, nkv, hd, len0, T, nsplit):
         assert_bitexact(got[t], exp, f"query {t} L={len0 + t + 1}")
 
 
-@pytest.mark.parametrize("B,L,nsplit", [(1, 4096, 32), (8, 4096, 32), (1, 16384, 64), (2, 32768, 128)])
+@pytest.mark.parametrize("B,L,nsplit", [(1, 4096, 32), (8, 4096, 32), (1, 16384, 64), (2, 32768, 128),
+                                         (8, 16384, 64), (8, 32768, 128)])
 def test_attention_long_context_batched(gpu, oracle, B, L, nsplit):
     """BASELINE config 4 geometry: 32 Q heads, 8 KV heads, hd 128, fp16 KV."""
     case(f"attn C4 B={B} L={L} nsplit={nsplit}")

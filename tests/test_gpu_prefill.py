@@ -284,3 +284,74 @@ def test_prefill_equals_stepwise(gpu, oracle, cfg_name, n_prompt, kv_dtype, nspl
     a.free()
     b.free()
     model.free()
+
+
+@pytest.mark.parametrize("cfg_name,kv_dtype,nsplit", [("tiny", LT_KV_F32, 1), ("small-qwen-arch", LT_KV_F16, 4),
+                                                      ("tiny", LT_KV_F16, 16)])
+def test_prefill_into_non_empty_cache(gpu, oracle, cfg_name, kv_dtype, nsplit):
+    """A batched prefill that starts from a non-empty cache: chunk A, then chunk B, then three
+    decode steps, then chunk C.  RoPE positions, the causal attention over the rows already
+    cached and the shared length update all start at the current length; the result equals
+    the single-token path over the same tokens (KV rows, lengths, logits, greedy token) and
+    the oracle's logits."""
+    cfg = M.CONFIGS[cfg_name]
+    case(f"prefill non-empty {cfg_name} kv={kv_dtype} nsplit={nsplit}")
+    model = dr.ResidentModel(cfg, weights(cfg), gpu, layouts="fused")
+    prof = dr.Profile(kv_dtype=kv_dtype, attn_nsplit=nsplit)
+    toks = M.random_prompt(cfg, 40, seed=21)
+    A, B, C = toks[:11], toks[11:24], toks[24:37]
+    a = dr.DecodePlan(model, prof)
+    b = dr.DecodePlan(model, prof)
+    orc = oracle.OracleModel(cfg, weights(cfg), kv_f16=kv_dtype == LT_KV_F16, attn_nsplit=nsplit)
+    dr.forward_prefill(b, A)
+    dr.forward_prefill(b, B)
+    seq = list(A) + list(B)
+    for _ in range(3):
+        t = b.read_token()
+        seq.append(t)
+        b.step()
+    dr.forward_prefill(b, C)
+    seq += list(C)
+    la = dr.forward_pass_resident(a, seq)
+    lb = b.read_logits()
+    exp = None
+    for t in seq:
+        exp = orc.step(t)
+    assert np.array_equal(bits(la), bits(lb))
+    assert np.array_equal(bits(lb), bits(exp))
+    assert a.read_token() == b.read_token()
+    n = len(seq)
+    assert list(a.lengths()) == list(b.lengths()) == [n] * cfg.n_layers
+    assert all(c.length == n for c in b.caches)
+    for il in range(cfg.n_layers):
+        for w in "kv":
+            assert np.array_equal(a.caches[il].rows_host(w, n).view(np.uint8),
+                                  b.caches[il].rows_host(w, n).view(np.uint8)), (il, w)
+    a.free()
+    b.free()
+    model.free()
+
+
+def test_capacity_is_refused_on_the_host(gpu):
+    """Steps, replays and prefills that would pass max_ctx raise before launching anything."""
+    cfg = M.TINY
+    case("capacity refusal")
+    model = dr.ResidentModel(cfg, weights(cfg), gpu, layouts="fused")
+    plan = dr.DecodePlan(model, dr.Profile(), max_ctx=8, hist_cap=16)
+    dr.forward_prefill(plan, M.random_prompt(cfg, 6, seed=2))
+    with pytest.raises(ValueError):
+        dr.forward_prefill(plan, [1, 2, 3])
+    gr = dr.GraphRunner(plan)
+    gr.capture()
+    with pytest.raises(ValueError):
+        gr.replay_tokens(3)
+    gr.replay_tokens(2)
+    assert list(plan.lengths()) == [8] * cfg.n_layers
+    with pytest.raises(ValueError):
+        gr.replay_token()
+    with pytest.raises(ValueError):
+        plan.step(1)
+    assert list(plan.lengths()) == [8] * cfg.n_layers
+    gr.free()
+    plan.free()
+    model.free()
