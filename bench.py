@@ -65,7 +65,7 @@ def gemv_roofline(dev, w_embd: np.ndarray, N: int, K: int, eps: float, launches:
     151936 x 896 Q8_0 GEMV; lt_q8_gemv_rms, the step's launch without its argmax epilogue),
     timed with HIP events on the library's stream over rotated weight copies (>= 512 MB, so
     the 256 MB Infinity Cache cannot serve it)."""
-    from llamatov_amd import dev_residency as dr
+    from llamatov_amd import engine as dr
     from llamatov_amd._lib import call
     blk_bytes = w_embd.nbytes
     copies = max(2, int(np.ceil(600e6 / blk_bytes)))
@@ -110,7 +110,7 @@ def gemv_sweep(dev, launches: int = 40) -> list[dict]:
     """Q8_0 GEMV bandwidth (BASELINE configs 1 and 3, plus the 0.5B vocab projection):
     lt_q8_gemv on random blocks, rotating >= 600 MB of weight copies so the MALL cannot
     serve them, timed with HIP events on the library's stream."""
-    from llamatov_amd import dev_residency as dr
+    from llamatov_amd import engine as dr
     from llamatov_amd._lib import call
     out = []
     rng = np.random.default_rng(5)
@@ -154,7 +154,7 @@ def attention_sweep(dev, reps: int = 20) -> list[dict]:
     N(0,1), one query token per sequence, L in {4k, 16k, 32k}, batch 1 and 8 (split-K over
     context with the ascending-split merge).  Algorithmic bytes: the K and V rows read plus
     q and out."""
-    from llamatov_amd import dev_residency as dr
+    from llamatov_amd import engine as dr
     from llamatov_amd._lib import LT_KV_F16, call, raw
     out = []
     nh, nkv, hd = 32, 8, 128
@@ -194,7 +194,7 @@ def c5_leg(dev, n_prefill: int = 512, n_decode: int = 256, eager: bool = False) 
     """random-init Llama-3-8B-architecture Q8_0 model (N(0,0.02) weights
     quantized with the engine quantizer), a 512-token prefill of random ids through the
     tiled int8-MFMA GEMM, then 256 greedy decode tokens (graph replay) with an fp16 KV cache."""
-    from llamatov_amd import dev_residency as dr
+    from llamatov_amd import engine as dr
     from llamatov_amd import model as M
     from llamatov_amd._lib import LT_KV_F16
     cfg = M.LLAMA3_8B
@@ -228,7 +228,7 @@ def c5_leg(dev, n_prefill: int = 512, n_decode: int = 256, eager: bool = False) 
         plan.free()
         model.free()
         return res
-    runner = dr.GraphRunner(plan)
+    runner = dr.StepGraph(plan)
     one = plan.step if eager else runner._launch
     if not eager:
         runner.capture()
@@ -306,7 +306,7 @@ def main() -> int:
               "(the hot path is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
         return 2
 
-    from llamatov_amd import dev_residency as dr
+    from llamatov_amd import engine as dr
     from llamatov_amd import model as M
     from llamatov_amd._lib import LT_KV_F16, LT_KV_F32
 
@@ -333,7 +333,7 @@ def main() -> int:
     dev = dr.get_device()
     model = dr.ResidentModel(cfg, w, dev, layouts="per_op" if args.per_op else "fused")
     plan = dr.DecodePlan(model, dr.Profile(kv_dtype=kv_dtype, fused_step=not args.per_op), hist_cap=4096)
-    runner = dr.GraphRunner(plan)
+    runner = dr.StepGraph(plan)
     prompt = M.random_prompt(cfg, args.prompt, seed=7)
 
     log("prefill (eager) + capture")

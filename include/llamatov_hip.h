@@ -74,6 +74,13 @@ LT_API int lt_quant_q8(lt_ctx* ctx, const float* x, int8_t* xq, uint16_t* xd, in
  * v = (g/(1+exp(-g)))*u then lt_quant_q8's quantizer.  K % 32 == 0. */
 LT_API int lt_silu_mul_quant(lt_ctx* ctx, const float* g, const float* u, int8_t* xq, uint16_t* xd, int K);
 
+/* k_silu_mul (bpd/lib/dev_residency.py:545-551, silu_mul_dev :632-637):
+ * y = (g/(1+exp(-g)))*u elementwise, n elements. */
+LT_API int lt_silu_mul(lt_ctx* ctx, const float* g, const float* u, float* y, int n);
+
+/* k_add (bpd/lib/dev_residency.py:552-555, add_dev :639-642): y = a + b elementwise. */
+LT_API int lt_add(lt_ctx* ctx, const float* a, const float* b, float* y, int n);
+
 /* k_rmsnorm block_row over M rows of N (norm_softmax_from_facts.pl:83-108, launcher
  * rms_norm_dev bpd/lib/dev_residency.py:746-781): 256-lane strided fma sum of squares,
  * pairwise tree, inv = rsqrt(ss/N + eps), y = (x*inv)*w.  eps is an argument here

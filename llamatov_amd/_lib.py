@@ -34,6 +34,8 @@ _SIGS = {
     "lt_sync": (c_int, [_P]),
     "lt_quant_q8": (c_int, [_P, _P, _P, _P, c_int]),
     "lt_silu_mul_quant": (c_int, [_P, _P, _P, _P, _P, c_int]),
+    "lt_silu_mul": (c_int, [_P, _P, _P, _P, c_int]),
+    "lt_add": (c_int, [_P, _P, _P, _P, c_int]),
     "lt_rmsnorm": (c_int, [_P, _P, _P, _P, c_int, c_int, c_float]),
     "lt_rmsnorm_quant": (c_int, [_P, _P, _P, _P, _P, c_int, c_float]),
     "lt_q8_gemv": (c_int, [_P, _P, _P, _P, _P, _P, c_int, c_int]),

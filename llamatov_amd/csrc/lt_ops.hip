@@ -50,6 +50,22 @@ __global__ __launch_bounds__(256) void k_silu_mul_quant(const float* __restrict_
 }
 
 // ---------------------------------------------------------------------------------
+// Elementwise SiLU(g)*u and a + b (k_silu_mul / k_add, bpd/lib/dev_residency.py:545-555):
+// the per-element expressions of the fused kernels, for callers that keep fp32 vectors.
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_silu_mul(const float* __restrict__ g, const float* __restrict__ u,
+                                                  float* __restrict__ y, int n) {
+  int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) y[i] = lt_silu_mul(g[i], u[i]);
+}
+
+__global__ __launch_bounds__(256) void k_add(const float* __restrict__ a, const float* __restrict__ b,
+                                             float* __restrict__ y, int n) {
+  int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) y[i] = a[i] + b[i];
+}
+
+// ---------------------------------------------------------------------------------
 // RMSNorm, order rms_ss lanes(256) strided + pairwise tree (norm_softmax_from_facts.pl:
 // 49, 83-108).  Thread t of the 256-thread block is reference lane t.  The tree's first
 // two levels (s = 128, 64) are formed explicitly from LDS by wave 0, the last six
@@ -388,6 +404,20 @@ int lt_silu_mul_quant(lt_ctx* ctx, const float* g, const float* u, int8_t* xq, u
   int nb = K / 32;
   k_silu_mul_quant<<<grid_for(nb, 8), 256, 0, ctx->stream>>>(g, u, xq, xd, nb);
   return lt_check_launch("k_silu_mul_quant");
+}
+
+int lt_silu_mul(lt_ctx* ctx, const float* g, const float* u, float* y, int n) {
+  LT_REQUIRE(ctx && g && u && y, "lt_silu_mul: null argument");
+  LT_REQUIRE(n > 0, "lt_silu_mul: n=%d", n);
+  k_silu_mul<<<(n + 255) / 256, 256, 0, ctx->stream>>>(g, u, y, n);
+  return lt_check_launch("k_silu_mul");
+}
+
+int lt_add(lt_ctx* ctx, const float* a, const float* b, float* y, int n) {
+  LT_REQUIRE(ctx && a && b && y, "lt_add: null argument");
+  LT_REQUIRE(n > 0, "lt_add: n=%d", n);
+  k_add<<<(n + 255) / 256, 256, 0, ctx->stream>>>(a, b, y, n);
+  return lt_check_launch("k_add");
 }
 
 int lt_rmsnorm(lt_ctx* ctx, const float* x, const float* w, float* y, int M, int N, float eps) {

@@ -1,885 +1,668 @@
-"""Device-resident Q8_0 decode on MI355X: the host surface of the reference's
-bpd/lib/dev_residency.py, driving libllamatov_hip.so through ctypes.
+"""The reference's device-resident host surface (bpd/lib/dev_residency.py) with its own
+names, arguments, results and errors, running on libllamatov_hip.so through the engine in
+llamatov_amd.engine.
 
-Names mirror the reference so callers read the same:
-  DevTensor (dev_residency.py:387-415), DeviceKVCache (:418-541), rms_norm_dev (:746-781),
-  q8_linear_dev (:905-985), q8_linear_add_residual_dev (:988-1045), q8_linear_dev_bias
-  (:1177-1193), rope_dev_qk_fused (:722-741), attn_decode_from_cache_masked (:2016-2031),
-  argmax_dev (:1074-1110), forward_pass_resident (:1328-1593), GraphRunner (:1626-1818),
-  PRODUCTION_PROFILE / attest_profile / assert_certified_composition (:1209-1281).
+A caller of the reference switches by importing this module in place of the reference's:
 
-Design differences (MI355X-first; results are the same bits):
-  * Q8_0 weights are the GGUF 34-byte blocks, uploaded once at load (ResidentModel); the
-    reference dequantizes to fp32 on the host and re-quantizes at first use.
-  * Every buffer a decode step touches is allocated up front in a DecodePlan, so the
-    step is capturable without a slab arena and graph pointers never move.
-  * The token id lives on the device: the step gathers its embedding from the Q8_0
-    token_embd and the argmax writes the next id back into the same buffer, so greedy
-    decoding can replay the graph back to back with no host round trip per token.
+    from llamatov_amd import dev_residency as dr       # was: import dev_residency as dr
+    kv = [None] * cfg['n_layers']
+    gr = dr.GraphRunner(w, cfg, kv)
+    logits = gr.seed(torch.tensor(prompt), torch.arange(len(prompt)))
+    gr.capture(torch.tensor([t]), torch.tensor([len(prompt)]))
+    t = gr.replay_token(torch.tensor([t]))
+
+`w` is the reference's weight dict (bpd/llamatov_run.py:lt(): fp32 tensors, linear weights
+[K, N] in GGUF [ne0, ne1] orientation, token_embd [n_embd, vocab]) and `cfg` its config dict
+(n_layers, n_head, n_head_kv, n_embd, rope_theta, norm_eps).  Weights are quantized to Q8_0
+with the engine quantizer at first use and cached on the device, as the reference does
+(fact_dispatch.py:255-299); a Q8_0 GGUF's weights round-trip to the same blocks.
+
+What differs, and why:
+  * Kernel-selection flags (_QFUSED, _FUSE_QKV, _RMS_BLOCKROW, ...) are accepted, listed by
+    PRODUCTION_PROFILE and attested, but do not select kernels: the engine always runs its
+    five fused launches per layer, which are bit-identical to every certified ensemble of the
+    reference's per-op kernels.  Flags that would ask for a host island or a lossy transform
+    (_KV_QUANT_Q8, device paths turned off) are refused by assert_certified_composition.
+  * The KV cache is the engine's (fp32 by default, the reference's elem_bytes=4; elem_bytes=2
+    selects fp16), allocated for _KV_MAX_SEQ positions on the first forward.
+  * Positions must equal the cache length (the reference's capture path ignores `positions`
+    and uses the device length; a mismatch is refused here rather than silently ignored).
+  * A multi-token forward_pass_resident runs the batched prefill, bit-identical to the
+    reference's one-token-at-a-time recursion (dev_residency.py:1338-1356).
+  * Logits come back as a torch tensor [1, 1, vocab] when torch is importable (as the
+    reference returns them), else as a numpy array of that shape.
+  * Pointers are accepted as ctypes.c_void_p, int, or any object with a .ptr.
+
+Every entry point fails loudly (ImportError / LtError) when the HIP library is missing; there
+is no CPU fallback.
 """
 from __future__ import annotations
 
 import ctypes
-import dataclasses
-import math
-from dataclasses import dataclass
+import os
 
 import numpy as np
 
 from . import _lib
+from . import engine
+from . import q8
 from ._lib import LT_KV_F16, LT_KV_F32, call
-from .model import ModelConfig, fused_layer_tensors, interleave_gateup
+from .model import ModelConfig
+
+# ----------------------------------------------------------------------------------
+# Module flags (the reference's names; bpd/lib/dev_residency.py:1209-1229)
+# ----------------------------------------------------------------------------------
+_DEVICE_KV_CACHE = True
+_DEVICE_ATTN = True
+_MASKED_ATTN = True
+_GRAPH_PREP = True
+_KV_MAX_SEQ = int(os.environ.get("BPD_KV_MAX_SEQ", "256"))
+_ATTN_SPLIT_K = False
+_ATTN_NSPLIT = 16            # split count when _ATTN_SPLIT_K (the declared split order)
+_KV_ELEM_BYTES = 4           # 4: fp32 cache (the reference's); 2: fp16 cache
+_DEVICE_LOGITS = True
+_QFUSED = False
+_GEMV_TILED_V4_QFUSED = False
+_KV_QUANT_Q8 = False
+_ADDRES_FUSED = True
+_BIAS_FOLD = True
+_RMS_BLOCKROW = True
+_GEMV_TILED = True
+_GEMV_TILED_V4 = True
+_GEMV_TILED_BM = 16
+_QUANT_PAR = True
+_ARGMAX2 = True
+_FUSE_QKV = True
+_FUSE_GATEUP = True
+_APPEND_KV_FUSED = True
+_APPEND_INCR_FUSED = True
+_RESID_CARRY_FUSED = True
+_ROPE_QK_FUSED = True
+_SILU_QUANT_FUSED = True
+_RMS_QUANT_FUSED = False
+
+PRODUCTION_PROFILE = {
+    "_DEVICE_KV_CACHE": True, "_DEVICE_ATTN": True, "_MASKED_ATTN": True,
+    "_GRAPH_PREP": True, "_KV_MAX_SEQ": 256, "_ATTN_SPLIT_K": False,
+    "_DEVICE_LOGITS": True, "_QFUSED": False, "_GEMV_TILED_V4_QFUSED": False, "_KV_QUANT_Q8": False,
+    "_ADDRES_FUSED": True, "_BIAS_FOLD": True, "_RMS_BLOCKROW": True,
+    "_GEMV_TILED": True, "_GEMV_TILED_V4": True, "_GEMV_TILED_BM": 16,
+    "_QUANT_PAR": True, "_ARGMAX2": True, "_FUSE_QKV": True, "_FUSE_GATEUP": True,
+    "_APPEND_KV_FUSED": True, "_APPEND_INCR_FUSED": True, "_RESID_CARRY_FUSED": True,
+    "_ROPE_QK_FUSED": True, "_SILU_QUANT_FUSED": True,
+}
+
+_UNCERTIFIED_COMPOSITIONS = [
+    (lambda f: f.get("_QFUSED") and (f.get("_BIAS_FOLD") or f.get("_APPEND_KV_FUSED")
+                                     or f.get("_APPEND_INCR_FUSED")),
+     "QFUSED=True with a fusion toggle (BIAS_FOLD / APPEND_KV_FUSED / APPEND_INCR_FUSED) is the "
+     "reference's refused composition (dev_residency.py:1259-1266)"),
+    (lambda f: f.get("_KV_QUANT_Q8"),
+     "_KV_QUANT_Q8 (the lossy kv_quantize_q8 transform) is not part of this build"),
+    (lambda f: not (f.get("_DEVICE_KV_CACHE") and f.get("_DEVICE_ATTN") and f.get("_MASKED_ATTN")
+                    and f.get("_GRAPH_PREP") and f.get("_DEVICE_LOGITS")),
+     "the host-island paths (device KV cache / attention / logits / graph prep off) are not part "
+     "of this build: every step runs on the device"),
+]
+
+
+def apply_production_profile() -> dict:
+    """Set the certified production flags (reference dev_residency.py:1231-1239)."""
+    g = globals()
+    for k, v in PRODUCTION_PROFILE.items():
+        g[k] = v
+    return dict(PRODUCTION_PROFILE)
+
+
+def attest_profile() -> dict:
+    """The live values of every production-profile flag (reference :1241-1248)."""
+    g = globals()
+    live = {k: g.get(k) for k in PRODUCTION_PROFILE}
+    live["_KV_ELEM_BYTES"] = _KV_ELEM_BYTES
+    live["_ATTN_NSPLIT"] = _ATTN_NSPLIT
+    return live
+
+
+def assert_certified_composition() -> None:
+    """Refuse uncertified flag compositions loudly (reference :1268-1281)."""
+    live = attest_profile()
+    for fires, reason in _UNCERTIFIED_COMPOSITIONS:
+        if fires(live):
+            raise RuntimeError("UNCERTIFIED COMPOSITION REFUSED: " + reason)
+    if _KV_ELEM_BYTES not in (2, 4):
+        raise RuntimeError(f"UNCERTIFIED COMPOSITION REFUSED: _KV_ELEM_BYTES={_KV_ELEM_BYTES} (2 or 4)")
+    engine.assert_certified_composition(_engine_profile())
+
+
+def _engine_profile() -> engine.Profile:
+    return engine.Profile(kv_dtype=LT_KV_F16 if _KV_ELEM_BYTES == 2 else LT_KV_F32,
+                          attn_nsplit=_ATTN_NSPLIT if _ATTN_SPLIT_K else 1)
 
 
 # ----------------------------------------------------------------------------------
-# Device context and tensors
+# Tensors and pointers
 # ----------------------------------------------------------------------------------
-class Device:
-    """One lt_ctx (one HIP device + one stream).  The reference's fact_dispatch._ctx()."""
-
-    def __init__(self, index: int = 0):
-        _lib.load()
-        h = ctypes.c_void_p()
-        call("lt_init", index, ctypes.byref(h))
-        self.handle = h
-        self.index = index
-        self.capturing = False
-
-    def malloc(self, nbytes: int) -> int:
-        p = ctypes.c_void_p()
-        call("lt_malloc", self.handle, ctypes.byref(p), max(int(nbytes), 1))
-        return int(p.value)
-
-    def free(self, ptr: int) -> None:
-        if ptr:
-            call("lt_free", self.handle, ctypes.c_void_p(ptr))
-
-    def h2d(self, ptr: int, arr: np.ndarray) -> None:
-        a = np.ascontiguousarray(arr)
-        call("lt_memcpy_h2d", self.handle, ctypes.c_void_p(ptr), a.ctypes.data_as(ctypes.c_void_p), a.nbytes)
-
-    def d2h(self, arr: np.ndarray, ptr: int) -> np.ndarray:
-        assert arr.flags.c_contiguous
-        call("lt_memcpy_d2h", self.handle, arr.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(ptr), arr.nbytes)
-        return arr
-
-    def d2d(self, dst: int, src: int, nbytes: int) -> None:
-        call("lt_memcpy_d2d", self.handle, ctypes.c_void_p(dst), ctypes.c_void_p(src), int(nbytes))
-
-    def fill(self, ptr: int, value: int, nbytes: int) -> None:
-        call("lt_fill_u8", self.handle, ctypes.c_void_p(ptr), value, int(nbytes))
-
-    def sync(self) -> None:
-        call("lt_sync", self.handle)
+def _dev() -> engine.Device:
+    return engine.get_device()
 
 
-_DEVICE: Device | None = None
-
-
-def get_device() -> Device:
-    global _DEVICE
-    if _DEVICE is None:
-        _DEVICE = Device(0)
-    return _DEVICE
+def _addr(p) -> int:
+    return int(engine._vp(p).value or 0)
 
 
 class DevTensor:
-    """A device buffer: raw pointer + shape + numpy dtype (reference DevTensor is fp32-only)."""
-    __slots__ = ("ptr", "shape", "dtype", "n", "nbytes", "_owns", "dev")
+    """A device-resident fp32 activation: a pointer + shape (reference :387-415).  .ptr is
+    a ctypes.c_void_p, as the reference's."""
+    __slots__ = ("ptr", "shape", "n", "nbytes", "_owns")
 
-    def __init__(self, ptr: int, shape, dtype=np.float32, owns: bool = True, dev: Device | None = None):
-        self.ptr = int(ptr)
+    def __init__(self, ptr, shape, owns: bool = True):
+        self.ptr = ptr if isinstance(ptr, ctypes.c_void_p) else ctypes.c_void_p(_addr(ptr))
         self.shape = tuple(int(s) for s in shape)
-        self.dtype = np.dtype(dtype)
         self.n = int(np.prod(self.shape)) if self.shape else 1
-        self.nbytes = self.n * self.dtype.itemsize
+        self.nbytes = self.n * 4
         self._owns = owns
-        self.dev = dev or get_device()
 
     @staticmethod
-    def empty(shape, dtype=np.float32, dev: Device | None = None) -> "DevTensor":
-        dev = dev or get_device()
+    def from_host(arr) -> "DevTensor":
+        a = np.ascontiguousarray(np.asarray(arr, np.float32))
+        t = DevTensor.empty(a.shape)
+        _dev().h2d(t.ptr.value, a)
+        return t
+
+    @staticmethod
+    def empty(shape) -> "DevTensor":
+        shape = tuple(shape) if not isinstance(shape, int) else (shape,)
         n = int(np.prod(shape)) if shape else 1
-        return DevTensor(dev.malloc(n * np.dtype(dtype).itemsize), shape, dtype, True, dev)
-
-    @staticmethod
-    def zeros(shape, dtype=np.float32, dev: Device | None = None) -> "DevTensor":
-        t = DevTensor.empty(shape, dtype, dev)
-        t.dev.fill(t.ptr, 0, t.nbytes)
-        return t
-
-    @staticmethod
-    def from_host(arr: np.ndarray, dev: Device | None = None) -> "DevTensor":
-        a = np.ascontiguousarray(arr)
-        t = DevTensor.empty(a.shape, a.dtype, dev)
-        t.dev.h2d(t.ptr, a)
-        return t
-
-    def view(self, offset_elems: int, shape, dtype=None) -> "DevTensor":
-        dt = np.dtype(dtype) if dtype is not None else self.dtype
-        return DevTensor(self.ptr + offset_elems * self.dtype.itemsize, shape, dt, False, self.dev)
+        return DevTensor(_dev().malloc(n * 4), shape)
 
     def to_host(self) -> np.ndarray:
-        self.dev.sync()
-        out = np.empty(self.shape, self.dtype)
-        return self.dev.d2h(out, self.ptr)
-
-    def upload(self, arr: np.ndarray) -> None:
-        a = np.ascontiguousarray(arr, dtype=self.dtype)
-        if a.nbytes != self.nbytes:
-            raise ValueError(f"upload of {a.nbytes} bytes into a {self.nbytes}-byte tensor")
-        self.dev.h2d(self.ptr, a)
+        d = _dev()
+        d.sync()
+        out = np.empty(self.shape, np.float32)
+        return d.d2h(out, self.ptr.value)
 
     def free(self) -> None:
-        if self._owns and self.ptr:
-            self.dev.free(self.ptr)
-            self.ptr = 0
-
-    @property
-    def vp(self) -> ctypes.c_void_p:
-        return ctypes.c_void_p(self.ptr)
+        if self._owns and self.ptr and self.ptr.value:
+            _dev().free(self.ptr.value)
+            self.ptr = None
 
 
-def _vp(x) -> ctypes.c_void_p:
-    if x is None:
-        return ctypes.c_void_p(0)
-    if isinstance(x, DevTensor):
-        return x.vp
-    return ctypes.c_void_p(int(x))
+def _empty_dev(shape) -> DevTensor:
+    return DevTensor.empty(shape)
+
+
+def _slice_dev(t: DevTensor, start: int, length: int) -> DevTensor:
+    """A device view of t[start:start+length] (reference :1308-1311)."""
+    return DevTensor(ctypes.c_void_p(_addr(t) + start * 4), (length,), owns=False)
+
+
+def _np(x) -> np.ndarray:
+    if hasattr(x, "detach"):
+        x = x.detach().cpu().numpy()
+    return np.asarray(x)
+
+
+def _ids(x) -> list[int]:
+    return [int(v) for v in _np(x).reshape(-1)]
+
+
+_DEV_CONST: dict = {}
+
+
+def _sample_key(a: np.ndarray) -> tuple:
+    f = a.reshape(-1)
+    n = f.size
+    return (a.shape, n) + ((float(f[0]), float(f[n // 3]), float(f[n // 2]), float(f[-1])) if n >= 4
+                          else (float(f.sum()),))
+
+
+def _dev_const(arr) -> ctypes.c_void_p:
+    """A constant fp32 vector on the device, cached by content sample (reference :785-792)."""
+    a = np.ascontiguousarray(np.asarray(_np(arr), np.float32)).reshape(-1)
+    key = _sample_key(a)
+    p = _DEV_CONST.get(key)
+    if p is None:
+        p = ctypes.c_void_p(_dev().malloc(a.nbytes))
+        _dev().h2d(p.value, a)
+        _DEV_CONST[key] = p
+    return p
+
+
+_Q8_WEIGHT_CACHE: dict = {}
+
+
+def _q8_weight(weight2d) -> engine.Q8Weight:
+    """An fp32 weight [K, N] quantized to Q8_0 rows (the N outputs) with the engine
+    quantizer and uploaded once (reference fact_dispatch._quantize_weight_q8_0 + _dev_weight,
+    fact_dispatch.py:255-299), cached by shape and a content sample."""
+    W = np.asarray(_np(weight2d), np.float32)
+    if W.ndim != 2:
+        raise ValueError(f"q8 linear weight must be 2-D [K, N], got {W.shape}")
+    key = _sample_key(W)
+    hit = _Q8_WEIGHT_CACHE.get(key)
+    if hit is None:
+        K, N = W.shape
+        if K % 32:
+            raise ValueError(f"q8 linear: K={K} is not a multiple of 32")
+        hit = engine.Q8Weight(q8.quantize_rows(np.ascontiguousarray(W.T)), K, _dev())
+        _Q8_WEIGHT_CACHE[key] = hit
+    return hit
+
+
+_SCRATCH: dict = {}
+
+
+def _quant_scratch(K: int):
+    """Fixed quantized-activation buffers (int8 [K], fp16 [K/32]) per K, reused across calls
+    (the reference takes them from its slab arena)."""
+    s = _SCRATCH.get(K)
+    if s is None:
+        d = _dev()
+        s = (ctypes.c_void_p(d.malloc(K)), ctypes.c_void_p(d.malloc(K // 32 * 2)))
+        _SCRATCH[K] = s
+    return s
+
+
+def free_scratch() -> None:
+    """No-op: scratch buffers here are fixed per size (reference :139-146 frees slab tensors)."""
 
 
 # ----------------------------------------------------------------------------------
-# Op launchers (thin mirrors of the reference op functions)
+# Op functions (reference :632-1193, 1308-1326, 2016-2031)
 # ----------------------------------------------------------------------------------
-class Q8Weight:
-    """A Q8_0 weight resident on the device as GGUF blocks [N][K/32]: uploads its own copy,
-    or wraps a slice of a DeviceArena (t=...)."""
-    __slots__ = ("t", "N", "K")
-
-    def __init__(self, blocks: np.ndarray | None, K: int, dev: Device | None = None,
-                 t: "DevTensor | None" = None, N: int | None = None):
-        if t is not None:
-            self.t, self.N, self.K = t, int(N), K
-            return
-        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
-        N = blocks.shape[0]
-        if blocks.shape[1] != K // 32 * 34:
-            raise ValueError(f"Q8Weight: {blocks.shape} is not [N, {K // 32 * 34}]")
-        self.t = DevTensor.from_host(blocks, dev)
-        self.N, self.K = N, K
+def silu_mul_dev(g: DevTensor, u: DevTensor) -> DevTensor:
+    y = DevTensor.empty(g.shape)
+    call("lt_silu_mul", _dev().handle, engine._vp(g), engine._vp(u), y.ptr, g.n)
+    return y
 
 
-class DeviceArena:
-    """One device allocation holding a model's tensors back to back (256-byte aligned
-    slices, 2 MiB-aligned base): a single mapping with large pages, so streaming the
-    weights of a decode step never walks more page tables than it has to.  The slices
-    are non-owning DevTensor views; free() releases the whole arena."""
-    ALIGN = 256
-    BASE_ALIGN = 2 << 20
-
-    def __init__(self, dev: Device | None = None):
-        self.dev = dev or get_device()
-        self.items: list[tuple[np.ndarray, list]] = []
-        self.ptr = 0
-
-    def add(self, arr: np.ndarray) -> list:
-        """Stage an array; the returned one-element list receives its DevTensor at commit()."""
-        slot: list = []
-        self.items.append((np.ascontiguousarray(arr), slot))
-        return slot
-
-    def commit(self) -> None:
-        offs, total = [], 0
-        for a, _ in self.items:
-            offs.append(total)
-            total += (a.nbytes + self.ALIGN - 1) // self.ALIGN * self.ALIGN
-        self.ptr = self.dev.malloc(total + self.BASE_ALIGN)
-        base = (self.ptr + self.BASE_ALIGN - 1) // self.BASE_ALIGN * self.BASE_ALIGN
-        for (a, slot), off in zip(self.items, offs):
-            t = DevTensor(base + off, a.shape, a.dtype, owns=False, dev=self.dev)
-            self.dev.h2d(t.ptr, a)
-            slot.append(t)
-        self.nbytes = total
-        self.items = []
-
-    def free(self) -> None:
-        if self.ptr:
-            self.dev.free(self.ptr)
-            self.ptr = 0
+def add_dev(a: DevTensor, b: DevTensor) -> DevTensor:
+    y = DevTensor.empty(a.shape)
+    call("lt_add", _dev().handle, engine._vp(a), engine._vp(b), y.ptr, a.n)
+    return y
 
 
-def quant_q8_dev(x: DevTensor, xq: DevTensor, xd: DevTensor, K: int | None = None) -> None:
-    K = K or x.n
-    call("lt_quant_q8", x.dev.handle, x.vp, xq.vp, xd.vp, K)
-
-
-def rms_norm_dev(x: DevTensor, w: DevTensor, eps: float, out: DevTensor) -> DevTensor:
-    """k_rmsnorm block_row into `out` (reference rms_norm_dev / rms_norm_dev_into)."""
+def rms_norm_dev_into(x, weight_np, eps, out):
     N = x.shape[-1]
     M = x.n // N
-    call("lt_rmsnorm", x.dev.handle, x.vp, w.vp, out.vp, M, N, ctypes.c_float(eps))
+    call("lt_rmsnorm", _dev().handle, engine._vp(x), _dev_const(weight_np), engine._vp(out), M, N,
+         ctypes.c_float(eps))
     return out
 
 
-def q8_gemv_dev(W: Q8Weight, xq: DevTensor, xd: DevTensor, out: DevTensor,
-                resid: DevTensor | None = None) -> DevTensor:
-    call("lt_q8_gemv", out.dev.handle, W.t.vp, xq.vp, xd.vp, _vp(resid), out.vp, W.N, W.K)
-    return out
+def rms_norm_dev(x: DevTensor, weight_np, eps: float = 1e-6) -> DevTensor:
+    """Row-wise RMSNorm of x (any leading shape) with weight_np (reference :746-781)."""
+    return rms_norm_dev_into(x, weight_np, eps, DevTensor.empty(x.shape))
 
 
-def q8_linear_dev(x: DevTensor, W: Q8Weight, out: DevTensor, xq: DevTensor, xd: DevTensor) -> DevTensor:
-    """quant + GEMV (reference q8_linear_dev / q8_linear_dev_into)."""
-    quant_q8_dev(x, xq, xd, W.K)
-    return q8_gemv_dev(W, xq, xd, out)
-
-
-def q8_linear_add_residual_dev(x: DevTensor, W: Q8Weight, resid: DevTensor, out: DevTensor,
-                               xq: DevTensor, xd: DevTensor, silu_src=None) -> DevTensor:
-    """quant (or SiLU*mul+quant when silu_src=(g, u)) + GEMV with the residual added at the
-    store (reference q8_linear_add_residual_dev, :988-1045)."""
+def _quantize_input(x, K, rms_src=None, silu_src=None, xq=None, xd=None):
+    d = _dev()
+    if xq is None or xd is None:
+        xq, xd = _quant_scratch(K)
     if silu_src is not None:
         g, u = silu_src
-        call("lt_silu_mul_quant", out.dev.handle, g.vp, u.vp, xq.vp, xd.vp, W.K)
+        call("lt_silu_mul_quant", d.handle, engine._vp(g), engine._vp(u), engine._vp(xq), engine._vp(xd), K)
+    elif rms_src is not None:
+        x_raw, nw_ptr, eps = rms_src
+        call("lt_rmsnorm_quant", d.handle, engine._vp(x_raw), engine._vp(nw_ptr), engine._vp(xq), engine._vp(xd),
+             K, ctypes.c_float(eps))
     else:
-        quant_q8_dev(x, xq, xd, W.K)
-    return q8_gemv_dev(W, xq, xd, out, resid)
+        call("lt_quant_q8", d.handle, engine._vp(x), engine._vp(xq), engine._vp(xd), K)
+    return xq, xd
 
 
-def q8_linear_dev_bias(x: DevTensor, W: Q8Weight, bias: DevTensor | None, out: DevTensor,
-                       xq: DevTensor, xd: DevTensor) -> DevTensor:
-    """Bias folded into the GEMV store (reference q8_linear_dev_bias, :1177-1193)."""
-    if bias is None:
-        return q8_linear_dev(x, W, out, xq, xd)
-    return q8_linear_add_residual_dev(x, W, bias, out, xq, xd)
-
-
-def rope_dev_qk_fused(qk: DevTensor, pos_ptr: int, nh: int, nkv: int, hd: int, freqs: DevTensor) -> None:
-    call("lt_rope_qk", qk.dev.handle, qk.vp, _vp(pos_ptr), nh + nkv, hd, freqs.vp)
-
-
-def attn_decode_from_cache_masked(q: DevTensor, cache: "DeviceKVCache", nh: int, scale: float,
-                                  len_ptr: int, out: DevTensor, nsplit: int = 1,
-                                  ws: DevTensor | None = None) -> DevTensor:
-    call("lt_attn_decode", q.dev.handle, q.vp, cache.k.vp, cache.v.vp, _vp(len_ptr), out.vp, 1, nh,
-         cache.nkv, cache.hd, ctypes.c_float(scale), cache.max_seq, nsplit, cache.kv_dtype,
-         _vp(ws), ws.nbytes if ws is not None else 0)
+def q8_linear_dev_into(x, weight_np, out, mode: str = "dp4a", xq=None, xd=None):
+    """y = x @ W into `out` (reference :1139-1172).  `mode` is accepted for the reference's
+    signature; there is one GEMV kernel family here."""
+    W = _q8_weight(weight_np)
+    xq, xd = _quantize_input(x, W.K, xq=xq, xd=xd)
+    call("lt_q8_gemv", _dev().handle, W.t.vp, engine._vp(xq), engine._vp(xd), None, engine._vp(out), W.N, W.K)
     return out
 
 
-def argmax_dev(logits: DevTensor, n: int, out_ptr: int, ws: DevTensor) -> int:
+def q8_linear_dev(x, weight_np, mode: str = "dp4a", rms_src=None) -> DevTensor:
+    """y = x @ W with W an fp32 [K, N] weight (quantized to Q8_0 once), x quantized on the
+    device; rms_src=(x_raw, norm_weight_ptr, eps) quantizes rms_norm(x_raw)*w instead of x
+    (reference :905-985)."""
+    W = _q8_weight(weight_np)
+    xq, xd = _quantize_input(x, W.K, rms_src=rms_src)
+    y = DevTensor.empty((W.N,))
+    call("lt_q8_gemv", _dev().handle, W.t.vp, engine._vp(xq), engine._vp(xd), None, y.ptr, W.N, W.K)
+    return y
+
+
+def q8_linear_add_residual_dev(x, weight_np, resid, mode: str = "dp4a", out=None, silu_src=None) -> DevTensor:
+    """y = (x @ W) + resid with the add at the GEMV's store; out= writes into a given buffer;
+    silu_src=(g, u) quantizes silu(g)*u instead of x (reference :988-1045)."""
+    W = _q8_weight(weight_np)
+    xq, xd = _quantize_input(x, W.K, silu_src=silu_src)
+    y = out if out is not None else DevTensor.empty((W.N,))
+    call("lt_q8_gemv", _dev().handle, W.t.vp, engine._vp(xq), engine._vp(xd), engine._vp(resid), engine._vp(y),
+         W.N, W.K)
+    return y
+
+
+def q8_linear_dev_bias(x, weight_np, bias_t=None) -> DevTensor:
+    """q8 linear with the bias folded into the GEMV store (reference :1177-1193)."""
+    if bias_t is None or isinstance(bias_t, int):
+        return q8_linear_dev(x, weight_np)
+    b = np.asarray(_np(bias_t), np.float32)
+    bd = DevTensor(_dev_const(b), (b.shape[0],), owns=False)
+    return q8_linear_add_residual_dev(x, weight_np, bd)
+
+
+_FUSED_W_CACHE: dict = {}
+
+
+def _fused_qkv_weight(w, p):
+    key = (p, "qkv", id(w))
+    hit = _FUSED_W_CACHE.get(key)
+    if hit is None:
+        Wq, Wk, Wv = (np.asarray(_np(w[f"{p}.attn_{n}.weight"]), np.float32) for n in "qkv")
+        Wcat = np.ascontiguousarray(np.concatenate([Wq, Wk, Wv], axis=1))
+        bias = None
+        if f"{p}.attn_q.bias" in w:
+            bias = np.concatenate([np.asarray(_np(w[f"{p}.attn_{n}.bias"]), np.float32) for n in "qkv"])
+        hit = (Wcat, bias, (Wq.shape[1], Wk.shape[1], Wv.shape[1]))
+        _FUSED_W_CACHE[key] = hit
+    return hit
+
+
+def _fused_gateup_weight(w, p):
+    key = (p, "gateup", id(w))
+    hit = _FUSED_W_CACHE.get(key)
+    if hit is None:
+        Wg = np.asarray(_np(w[f"{p}.ffn_gate.weight"]), np.float32)
+        Wu = np.asarray(_np(w[f"{p}.ffn_up.weight"]), np.float32)
+        hit = (np.ascontiguousarray(np.concatenate([Wg, Wu], axis=1)), None, (Wg.shape[1], Wu.shape[1]))
+        _FUSED_W_CACHE[key] = hit
+    return hit
+
+
+def qkv_fused_dev(x, w, p):
+    """One GEMV over concat(Wq, Wk, Wv) (+ biases); (q, k, v) device views (reference :1313-1319)."""
+    Wcat, bcat, (nq, nk, nv) = _fused_qkv_weight(w, p)
+    y = q8_linear_dev_bias(x, Wcat, bcat)
+    return _slice_dev(y, 0, nq), _slice_dev(y, nq, nk), _slice_dev(y, nq + nk, nv)
+
+
+def gateup_fused_dev(x, w, p, rms_src=None):
+    """One GEMV over concat(Wgate, Wup); (g, u) device views (reference :1321-1326)."""
+    Wcat, _, (ng, nu) = _fused_gateup_weight(w, p)
+    y = q8_linear_dev(x, Wcat, rms_src=rms_src)
+    return _slice_dev(y, 0, ng), _slice_dev(y, ng, nu)
+
+
+_FREQS: dict = {}
+
+
+def _freqs(hd: int, theta: float) -> ctypes.c_void_p:
+    key = (int(hd), float(theta))
+    p = _FREQS.get(key)
+    if p is None:
+        f = engine.rope_freqs(hd, theta)
+        p = ctypes.c_void_p(_dev().malloc(f.nbytes))
+        _dev().h2d(p.value, f)
+        _FREQS[key] = p
+    return p
+
+
+def rope_dev_inplace_devpos(x_dev, pos_dev_ptr, n_head, hd, theta):
+    """NeoX RoPE of n_head heads in place at the device position *pos (reference :701-720)."""
+    call("lt_rope_qk", _dev().handle, engine._vp(x_dev), engine._vp(pos_dev_ptr), int(n_head), int(hd),
+         _freqs(hd, theta))
+    return x_dev
+
+
+def rope_dev_inplace(x_dev, pos_int, n_head, hd, theta):
+    """RoPE at a host position (reference :676-699)."""
+    d = _dev()
+    p = d.malloc(4)
+    d.h2d(p, np.array([int(pos_int)], np.int32))
+    rope_dev_inplace_devpos(x_dev, p, n_head, hd, theta)
+    d.sync()
+    d.free(p)
+    return x_dev
+
+
+def rope_dev_qk_fused(qk_dev_ptr, pos_dev_ptr, nh, nkv, hd, theta):
+    """RoPE of the nh q heads and nkv k heads in one launch (reference :722-741)."""
+    call("lt_rope_qk", _dev().handle, engine._vp(qk_dev_ptr), engine._vp(pos_dev_ptr), int(nh + nkv), int(hd),
+         _freqs(hd, theta))
+
+
+class DeviceKVCache(engine.KVCache):
+    """Device KV cache of one layer, [max_seq, nkv*hd] K and V with a device length
+    (reference :418-541).  elem_bytes 4: fp32 (the reference's); 2: fp16 (RNE on store)."""
+
+    def __init__(self, max_seq, nkv, hd, elem_bytes: int = 4):
+        if int(elem_bytes) not in (2, 4):
+            raise ValueError(f"DeviceKVCache: elem_bytes={elem_bytes} (2 = fp16, 4 = fp32)")
+        super().__init__(max_seq, nkv, hd, LT_KV_F16 if int(elem_bytes) == 2 else LT_KV_F32, dev=_dev())
+
+
+def attn_decode_from_cache_masked(q_dev_ptr, cache, nh, scale, len_dev_ptr, maxt) -> DevTensor:
+    """Masked decode attention of the nh query heads over the first *len rows of the cache
+    (reference :2016-2031).  maxt is the cache capacity the reference sizes its launch for."""
+    if int(maxt) > cache.max_seq:
+        raise ValueError(f"attn_decode_from_cache_masked: maxt={maxt} exceeds the cache's {cache.max_seq} rows")
+    out = DevTensor.empty((nh * cache.hd,))
+    call("lt_attn_decode", _dev().handle, engine._vp(q_dev_ptr), cache.k.vp, cache.v.vp, engine._vp(len_dev_ptr),
+         out.ptr, 1, int(nh), cache.nkv, cache.hd, ctypes.c_float(scale), cache.max_seq, 1, cache.kv_dtype,
+         None, 0)
+    return out
+
+
+def attn_decode_from_cache(q_dev_ptr, cache, nh, scale) -> DevTensor:
+    """Decode attention over the cache's host length (reference :2033-2060)."""
+    lp = cache._ensure_len_ptr(seed=True)
+    return attn_decode_from_cache_masked(q_dev_ptr, cache, nh, scale, lp, cache.max_seq)
+
+
+_ARGMAX_BUF = None
+_ARGMAX_WS = None
+
+
+def argmax_dev(logits_ptr, n, out_ptr=None):
+    """Index of the largest of n logits, lowest index on ties, into the device int out_ptr
+    (reference :1074-1110); returns out_ptr."""
+    global _ARGMAX_BUF, _ARGMAX_WS
     if n <= 0:
-        raise ValueError(f"argmax_dev: n={n} (must be > 0)")
-    call("lt_argmax", logits.dev.handle, logits.vp, n, _vp(out_ptr), ws.vp, ws.nbytes)
+        raise AssertionError(f"argmax_dev: n={n} (must be >0)")
+    d = _dev()
+    if _ARGMAX_WS is None:
+        wn = int(_lib.raw("lt_argmax_workspace_size")())
+        _ARGMAX_WS = (ctypes.c_void_p(d.malloc(wn)), wn)
+    if out_ptr is None:
+        if _ARGMAX_BUF is None:
+            _ARGMAX_BUF = ctypes.c_void_p(d.malloc(4))
+        out_ptr = _ARGMAX_BUF
+    call("lt_argmax", d.handle, engine._vp(logits_ptr), int(n), engine._vp(out_ptr), _ARGMAX_WS[0], _ARGMAX_WS[1])
     return out_ptr
 
 
-def rope_freqs(hd: int, theta: float) -> np.ndarray:
-    f = np.empty(hd // 2, dtype=np.float32)
-    call("lt_rope_freqs", hd, ctypes.c_float(theta), f.ctypes.data_as(ctypes.c_void_p))
-    return f
-
-
 # ----------------------------------------------------------------------------------
-# KV cache
+# The model behind (w, cfg): Q8_0 residency and one decode plan per kv_cache list
 # ----------------------------------------------------------------------------------
-class DeviceKVCache:
-    """Device KV cache for one layer: position-major [max_seq][nkv*hd] K and V and a device
-    int length (reference DeviceKVCache, bpd/lib/dev_residency.py:418-541).  kv_dtype
-    LT_KV_F32 (the reference's elem_bytes=4) or LT_KV_F16."""
-
-    def __init__(self, max_seq: int, nkv: int, hd: int, kv_dtype: int = LT_KV_F32,
-                 len_ptr: int | None = None, dev: Device | None = None):
-        self.dev = dev or get_device()
-        self.max_seq, self.nkv, self.hd = int(max_seq), int(nkv), int(hd)
-        self.width = self.nkv * self.hd
-        self.kv_dtype = kv_dtype
-        self.elem_bytes = 2 if kv_dtype == LT_KV_F16 else 4
-        dt = np.uint16 if kv_dtype == LT_KV_F16 else np.float32
-        self.k = DevTensor.empty((self.max_seq, self.width), dt, self.dev)
-        self.v = DevTensor.empty((self.max_seq, self.width), dt, self.dev)
-        self._len_owned = len_ptr is None
-        self.len_ptr = self.dev.malloc(4) if len_ptr is None else int(len_ptr)
-        self.length = 0
-        self.set_length(0)
-
-    def set_length(self, n: int) -> None:
-        self.length = int(n)
-        self.dev.h2d(self.len_ptr, np.array([n], dtype=np.int32))
-
-    def device_length(self) -> int:
-        out = np.zeros(1, np.int32)
-        self.dev.sync()
-        self.dev.d2h(out, self.len_ptr)
-        return int(out[0])
-
-    def append_at_len_incr(self, k: DevTensor, v: DevTensor) -> None:
-        call("lt_kv_append_incr", self.dev.handle, self.k.vp, k.vp, self.v.vp, v.vp,
-             _vp(self.len_ptr), self.width, self.max_seq, self.kv_dtype)
-
-    def rows_host(self, which: str, n: int | None = None) -> np.ndarray:
-        n = self.length if n is None else n
-        t = self.k if which == "k" else self.v
-        out = np.empty((self.max_seq, self.width), t.dtype)
-        self.dev.sync()
-        self.dev.d2h(out, t.ptr)
-        return out[:n]
-
-    def free(self) -> None:
-        self.k.free()
-        self.v.free()
-        if self._len_owned:
-            self.dev.free(self.len_ptr)
+def _engine_cfg(cfg: dict, w) -> ModelConfig:
+    nh = int(cfg["n_head"])
+    E = int(cfg["n_embd"])
+    hd = cfg.get("head_dim")
+    if hd is not None and int(hd) != E // nh:
+        raise ValueError(f"head_dim={hd} differs from n_embd/n_head={E // nh}; the decode path takes "
+                         "head_dim = n_embd / n_head (dev_residency.py:1337)")
+    vocab = int(_embedding_rows(w, E).shape[0])
+    return ModelConfig(name=str(cfg.get("arch", "gguf")), n_layers=int(cfg["n_layers"]), n_embd=E,
+                       n_ff=int(np.asarray(w["blk.0.ffn_gate.weight"].shape)[1]), n_head=nh,
+                       n_head_kv=int(cfg.get("n_head_kv", nh)), vocab=vocab,
+                       rope_theta=float(cfg["rope_theta"]), norm_eps=float(cfg["norm_eps"]),
+                       tied="output.weight" not in w, qkv_bias="blk.0.attn_q.bias" in w,
+                       max_ctx=int(_KV_MAX_SEQ))
 
 
-# ----------------------------------------------------------------------------------
-# Production profile (a frozen config object instead of the reference's env flags)
-# ----------------------------------------------------------------------------------
-@dataclass(frozen=True)
-class Profile:
-    """The certified ensemble.  Every variant below is bit-identical to the reference's
-    per-op chain; the fields select kernels, not numerics, except attn_nsplit (> 1 selects
-    the split-K declared order) and kv_dtype."""
-    kv_dtype: int = LT_KV_F32
-    attn_nsplit: int = 1
-    fused_step: bool = True         # five fused launches per layer (lt_fused.hip)
-    fused_rms_quant: bool = False   # per-op path only: k_rms_quant instead of k_rmsnorm + k_quant_q8
-    graph: bool = True
+def _embedding_rows(w, E: int) -> np.ndarray:
+    """token_embd as [vocab, n_embd] rows (the reference gathers emb.T[tok] when the tensor is
+    [n_embd, vocab], :1357-1358)."""
+    emb = np.asarray(_np(w["token_embd.weight"]), np.float32)
+    return emb.T if emb.shape[0] == E and emb.shape[1] != E else emb
 
 
-PRODUCTION_PROFILE = Profile()
-_CERTIFIED_NSPLIT = {1, 2, 4, 8, 16, 32, 64, 128}
-
-
-def attest_profile(p: Profile) -> dict:
-    return dataclasses.asdict(p)
-
-
-def assert_certified_composition(p: Profile) -> None:
-    """Refuse uncertified ensembles (reference dev_residency.py:1268-1281)."""
-    if p.kv_dtype not in (LT_KV_F32, LT_KV_F16):
-        raise RuntimeError(f"uncertified kv_dtype {p.kv_dtype}")
-    if p.attn_nsplit not in _CERTIFIED_NSPLIT:
-        raise RuntimeError(f"uncertified attn_nsplit {p.attn_nsplit}")
-
-
-# ----------------------------------------------------------------------------------
-# Resident model and the fixed-buffer decode plan
-# ----------------------------------------------------------------------------------
-class ResidentModel:
-    """All weights on the device, uploaded once: Q8_0 blocks verbatim, q|k|v and gate|up
-    concatenated at load (the reference concatenates at first use, dev_residency.py:1283-1326),
-    tied lm_head sharing token_embd's blocks.
-
-    layouts selects the gate|up layouts uploaded: "fused" (rows interleaved gate j, up j, for
-    lt_q8_gemv_rms_silu), "per_op" (gate rows then up rows, the reference's concatenation,
-    for lt_q8_gemv + lt_silu_mul_quant) or "both"."""
-
-    def __init__(self, cfg: ModelConfig, weights: dict, dev: Device | None = None, layouts: str = "both"):
-        if layouts not in ("fused", "per_op", "both"):
-            raise ValueError(f"layouts={layouts!r}")
-        self.cfg = cfg
-        self.dev = dev or get_device()
-        self.layouts = layouts
-        E, F = cfg.n_embd, cfg.n_ff
-        arena = DeviceArena(self.dev)
-        staged = []   # (kind, owner dict, key, slot, N, K)
-
-        def q8(owner, key, blocks, K):
-            staged.append(("q8", owner, key, arena.add(blocks), blocks.shape[0], K))
-
-        def vec(owner, key, arr):
-            if arr is None:
-                owner[key] = None
-                return
-            staged.append(("vec", owner, key, arena.add(np.asarray(arr, np.float32)), 0, 0))
-
-        top: dict = {}
-        q8(top, "tok_embd", weights["token_embd.weight"], E)
-        if not cfg.tied:
-            q8(top, "output", weights["output.weight"], E)
-        vec(top, "output_norm", weights["output_norm.weight"])
-        vec(top, "freqs", rope_freqs(cfg.head_dim, cfg.rope_theta))
-        self.layers = []
-        for il in range(cfg.n_layers):
-            t = fused_layer_tensors(cfg, weights, il)
-            L: dict = {}
-            vec(L, "attn_norm", t["attn_norm"])
-            q8(L, "wqkv", t["wqkv"], E)
-            vec(L, "bqkv", t["bqkv"])
-            q8(L, "wo", t["wo"], cfg.q_dim)
-            vec(L, "ffn_norm", t["ffn_norm"])
-            q8(L, "wdown", t["wdown"], F)
-            if layouts in ("per_op", "both"):
-                q8(L, "wgu", t["wgu"], E)
-            if layouts in ("fused", "both"):
-                p = f"blk.{il}"
-                q8(L, "wgu_il", interleave_gateup(weights[f"{p}.ffn_gate.weight"],
-                                                  weights[f"{p}.ffn_up.weight"]), E)
-            self.layers.append(L)
-        arena.commit()
-        for kind, owner, key, slot, N, K in staged:
-            owner[key] = Q8Weight(None, K, t=slot[0], N=N) if kind == "q8" else slot[0]
-        self.arena = arena
-        self.load_report = None
-        self.tiles = None   # the prefill GEMM's tile-major copies (prefill_tiles)
-        self.tok_embd = top["tok_embd"]
-        self.output = top.get("output", self.tok_embd)
-        self.output_norm = top["output_norm"]
-        self.freqs = top["freqs"]
-
-    @classmethod
-    def from_gguf(cls, path, dev: Device | None = None, layouts: str = "both",
-                  max_ctx: int = 1024) -> "ResidentModel":
-        """Upload a Q8_0 GGUF file (the reference's load_model + first-use residency,
-        decode_fact.py:39-51, fact_dispatch.py:255-299): Q8_0 blocks go from the mapped file
-        to the device without a float32 copy.  `load_report` says how many tensors were used
-        verbatim, canonicalized or quantized from another type."""
-        from . import gguf
-        cfg, w, reader, report = gguf.load_q8_model(path, max_ctx=max_ctx)
-        try:
-            m = cls(cfg, w, dev, layouts)
-        finally:
-            del w
-            reader.close()
-        m.load_report = report
-        return m
-
-    def prefill_tiles(self) -> None:
-        """Tile-major copies of the prefill GEMM's matrices (q|k|v, o, interleaved gate|up,
-        down), built on the device from the resident blocks at the first batched prefill:
-        one allocation, lt_q8_tiles per matrix.  The decode path keeps reading the GGUF-layout
-        blocks; the copies cost one more copy of those weights in HBM."""
-        if self.tiles is not None:
-            return
-        if "wgu_il" not in self.layers[0]:
-            raise ValueError("prefill needs the fused gate|up layout (ResidentModel layouts 'fused' or 'both')")
-        nbytes = _lib.raw("lt_q8_tiles_bytes")
-        names = ("wqkv", "wo", "wgu_il", "wdown")
-        plan = []
-        total = 0
-        for L in self.layers:
-            for k in names:
-                W = L[k]
-                n = int(nbytes(W.N, W.K))
-                plan.append((L, k, W, total, n))
-                total += (n + 255) // 256 * 256
-        base = self.dev.malloc(total)
-        for L, k, W, off, n in plan:
-            t = DevTensor(base + off, (n,), np.uint8, owns=False, dev=self.dev)
-            call("lt_q8_tiles", self.dev.handle, W.t.vp, t.vp, W.N, W.K)
-            L[k + "_t"] = Q8Weight(None, W.K, t=t, N=W.N)
-        self.tiles = base
-
-    def free(self) -> None:
-        if self.tiles is not None:
-            self.dev.free(self.tiles)
-            self.tiles = None
-        self.arena.free()
-
-
-class DecodePlan:
-    """Fixed device buffers and the launch sequence of one decode token."""
-
-    def __init__(self, model: ResidentModel, profile: Profile = PRODUCTION_PROFILE,
-                 max_ctx: int | None = None, hist_cap: int = 4096):
-        assert_certified_composition(profile)
-        need = "fused" if profile.fused_step else "per_op"
-        if model.layouts not in (need, "both"):
-            raise ValueError(f"DecodePlan: profile needs the {need!r} gate|up layout, model has {model.layouts!r}")
-        self.model, self.cfg, self.profile = model, model.cfg, profile
-        self.dev = model.dev
-        cfg = self.cfg
-        E, F, hd = cfg.n_embd, cfg.n_ff, cfg.head_dim
-        self.max_ctx = int(max_ctx or cfg.max_ctx)
-        kmax = max(E, F, cfg.q_dim)
-        D = self.dev
-        self.tok = DevTensor.empty((1,), np.int32, D)
-        self.err = DevTensor.empty((1,), np.int32, D)
-        self.hist = DevTensor.empty((hist_cap,), np.int32, D)
-        self.hist_count = DevTensor.empty((1,), np.int32, D)
-        self.hist_cap = hist_cap
-        self.lens = DevTensor.empty((cfg.n_layers,), np.int32, D)
-        self.resid_in = DevTensor.empty((E,), np.float32, D)
-        self.carry = DevTensor.empty((E,), np.float32, D)
-        self.xres = DevTensor.empty((E,), np.float32, D)
-        self.h = DevTensor.empty((E,), np.float32, D)
-        self.qkv = DevTensor.empty((cfg.n_qkv,), np.float32, D)
-        self.att = DevTensor.empty((cfg.q_dim,), np.float32, D)
-        self.gu = DevTensor.empty((2 * F,), np.float32, D)
-        self.v = DevTensor.empty((F,), np.float32, D)
-        self.logits = DevTensor.empty((cfg.vocab,), np.float32, D)
-        self.xq = DevTensor.empty((kmax,), np.int8, D)
-        self.xd = DevTensor.empty((kmax // 32,), np.uint16, D)
-        ws_n = max(_lib.raw("lt_argmax_workspace_size")(), _lib.raw("lt_q8_gemv_argmax_workspace_size")(cfg.vocab))
-        self.am_ws = DevTensor.empty((ws_n,), np.uint8, D)
-        aw = _lib.raw("lt_attn_workspace_size")(1, cfg.n_head, hd, profile.attn_nsplit)
-        self.attn_ws = DevTensor.empty((aw,), np.uint8, D) if aw else None
-        self.caches = [DeviceKVCache(self.max_ctx, cfg.n_head_kv, hd, profile.kv_dtype,
-                                     len_ptr=self.lens.ptr + 4 * il, dev=D)
-                       for il in range(cfg.n_layers)]
-        self.scale = float(hd ** -0.5)
-        self._prefill: PrefillBuffers | None = None
-        self.reset()
-
-    def prefill_buffers(self, T: int) -> "PrefillBuffers":
-        if self._prefill is None or self._prefill.T < T:
-            if self._prefill is not None:
-                self.dev.sync()
-                self._prefill.free()
-            self._prefill = PrefillBuffers(self, max(T, 32))
-        return self._prefill
-
-    # -- state --------------------------------------------------------------------
-    def reset(self) -> None:
-        """Empty caches (length 0), zero token history."""
-        self.dev.h2d(self.lens.ptr, np.zeros(self.cfg.n_layers, np.int32))
-        for c in self.caches:
-            c.length = 0
-        self.dev.h2d(self.hist_count.ptr, np.zeros(1, np.int32))
-        self.dev.h2d(self.err.ptr, np.zeros(1, np.int32))
-
-    def set_token(self, tok: int) -> None:
-        self.dev.h2d(self.tok.ptr, np.array([tok], np.int32))
-
-    def read_token(self) -> int:
-        out = np.zeros(1, np.int32)
-        self.dev.d2h(out, self.tok.ptr)
-        return int(out[0])
-
-    def read_logits(self) -> np.ndarray:
-        return self.logits.to_host()
-
-    def history_count(self) -> int:
-        out = np.zeros(1, np.int32)
-        self.dev.d2h(out, self.hist_count.ptr)
-        return int(out[0])
-
-    def history(self) -> list[int]:
-        n = self.history_count()
-        out = np.zeros(self.hist_cap, np.int32)
-        self.dev.d2h(out, self.hist.ptr)
-        return [int(t) for t in out[:n]]
-
-    def lengths(self) -> np.ndarray:
-        out = np.zeros(self.cfg.n_layers, np.int32)
-        self.dev.sync()
-        return self.dev.d2h(out, self.lens.ptr)
-
-    # -- the step ----------------------------------------------------------------
-    def enqueue_step(self) -> None:
-        """Launch one decode token (fused or per-op, as the profile says)."""
-        if self.profile.fused_step:
-            self._enqueue_fused()
+def _engine_weights(w, cfg: ModelConfig) -> dict:
+    """The engine's GGUF-named tensors: Q8_0 rows of every matrix the decode path reads
+    (fp32 [K, N] -> N rows of K, quantized with the engine quantizer), fp32 vectors."""
+    from .model import weight_specs
+    out = {}
+    for name, kind, shape in weight_specs(cfg):
+        if name not in w:
+            raise KeyError(f"weight {name!r} is missing")
+        if name == "token_embd.weight":
+            a = _embedding_rows(w, cfg.n_embd)
         else:
-            self._enqueue_per_op()
-
-    def _enqueue_fused(self) -> None:
-        """Five launches per layer (lt_fused.hip), then the vocab GEMV with its argmax:
-        the same arithmetic as _enqueue_per_op, bit for bit.
-          QKV   rmsnorm -> quant -> GEMV + bias        (layer 0: from the embedding of tok)
-          attn  RoPE -> KV append -> attention -> quant (split-K: partials, then a merge launch)
-          O     GEMV + x, length += 1
-          FFN1  rmsnorm -> quant -> gate|up GEMV -> SiLU(g)*u -> quant
-          FFN2  down GEMV + xres"""
-        cfg, m, p = self.cfg, self.model, self.profile
-        h = self.dev.handle
-        E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
-        eps = ctypes.c_float(cfg.norm_eps)
-        ws, ws_n = _vp(self.attn_ws), (self.attn_ws.nbytes if self.attn_ws is not None else 0)
-        for il, L in enumerate(m.layers):
-            cache = self.caches[il]
-            x = self.resid_in if il == 0 else self.carry
-            if il == 0:
-                call("lt_q8_gemv_embed_rms", h, m.tok_embd.t.vp, self.tok.vp, cfg.vocab, self.resid_in.vp,
-                     self.err.vp, L["attn_norm"].vp, eps, L["wqkv"].t.vp, _vp(L["bqkv"]), self.qkv.vp,
-                     cfg.n_qkv, E)
-            else:
-                call("lt_q8_gemv_rms", h, x.vp, L["attn_norm"].vp, eps, L["wqkv"].t.vp, _vp(L["bqkv"]),
-                     self.qkv.vp, cfg.n_qkv, E)
-            call("lt_attn_step", h, self.qkv.vp, m.freqs.vp, cache.k.vp, cache.v.vp, _vp(cache.len_ptr),
-                 None, self.xq.vp, self.xd.vp, nh, nkv, hd, ctypes.c_float(self.scale), cache.max_seq,
-                 p.attn_nsplit, p.kv_dtype, ws, ws_n)
-            call("lt_q8_gemv_attn_out", h, self.xq.vp, self.xd.vp, None, 0, 1, nh, hd, L["wo"].t.vp,
-                 x.vp, self.xres.vp, E, cfg.q_dim, _vp(cache.len_ptr), cache.max_seq)
-            call("lt_q8_gemv_rms_silu", h, self.xres.vp, L["ffn_norm"].vp, eps, L["wgu_il"].t.vp, self.xq.vp,
-                 self.xd.vp, F, E)
-            call("lt_q8_gemv", h, L["wdown"].t.vp, self.xq.vp, self.xd.vp, self.xres.vp, self.carry.vp, E, F)
-        call("lt_q8_gemv_rms_argmax", h, self.carry.vp, m.output_norm.vp, eps, m.output.t.vp, self.logits.vp,
-             cfg.vocab, E, self.tok.vp, self.hist.vp, self.hist_count.vp, self.hist_cap,
-             self.am_ws.vp, self.am_ws.nbytes)
-
-    def _enqueue_per_op(self) -> None:
-        """Launch one token: embed(tok) -> layers -> logits -> argmax -> tok.
-        The launch order is forward_pass_resident's fully-device branch
-        (bpd/lib/dev_residency.py:1365-1477) followed by _compute_folded_logits (:1596-1623)
-        and the device argmax of replay_token (:1795-1818)."""
-        cfg, m, p = self.cfg, self.model, self.profile
-        h = self.dev.handle
-        E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
-        eps = ctypes.c_float(cfg.norm_eps)
-        call("lt_embed_q8", h, m.tok_embd.t.vp, self.tok.vp, self.resid_in.vp, E, cfg.vocab, self.err.vp)
-        x = self.resid_in
-        for il, L in enumerate(m.layers):
-            cache = self.caches[il]
-            self._rms_quant(x, L["attn_norm"], E, eps)
-            q8_gemv_dev(L["wqkv"], self.xq, self.xd, self.qkv, L["bqkv"])
-            call("lt_rope_qk", h, self.qkv.vp, _vp(cache.len_ptr), nh + nkv, hd, m.freqs.vp)
-            k = self.qkv.view(cfg.q_dim, (cfg.kv_dim,))
-            v = self.qkv.view(cfg.q_dim + cfg.kv_dim, (cfg.kv_dim,))
-            cache.append_at_len_incr(k, v)
-            call("lt_attn_decode", h, self.qkv.vp, cache.k.vp, cache.v.vp, _vp(cache.len_ptr),
-                 self.att.vp, 1, nh, nkv, hd, ctypes.c_float(self.scale), cache.max_seq,
-                 p.attn_nsplit, p.kv_dtype, _vp(self.attn_ws),
-                 self.attn_ws.nbytes if self.attn_ws is not None else 0)
-            quant_q8_dev(self.att, self.xq, self.xd, cfg.q_dim)
-            q8_gemv_dev(L["wo"], self.xq, self.xd, self.xres, x)
-            self._rms_quant(self.xres, L["ffn_norm"], E, eps)
-            q8_gemv_dev(L["wgu"], self.xq, self.xd, self.gu)
-            g = self.gu.view(0, (F,))
-            u = self.gu.view(F, (F,))
-            call("lt_silu_mul_quant", h, g.vp, u.vp, self.xq.vp, self.xd.vp, F)
-            q8_gemv_dev(L["wdown"], self.xq, self.xd, self.carry, self.xres)
-            x = self.carry
-        self._rms_quant(x, m.output_norm, E, eps)
-        call("lt_q8_gemv", h, m.output.t.vp, self.xq.vp, self.xd.vp, None, self.logits.vp,
-             m.output.N, m.output.K)
-        call("lt_argmax_record", h, self.logits.vp, cfg.vocab, self.tok.vp, self.hist.vp,
-             self.hist_count.vp, self.hist_cap, self.am_ws.vp, self.am_ws.nbytes)
-
-    def _rms_quant(self, x: DevTensor, w: DevTensor, E: int, eps) -> None:
-        h = self.dev.handle
-        if self.profile.fused_rms_quant:
-            call("lt_rmsnorm_quant", h, x.vp, w.vp, self.xq.vp, self.xd.vp, E, eps)
+            a = np.asarray(_np(w[name]), np.float32)
+            if kind == "q8":
+                a = a.T
+        if kind == "q8":
+            if a.shape != shape:
+                raise ValueError(f"{name}: {a.shape} rows x inputs, expected {shape}")
+            out[name] = q8.quantize_rows(np.ascontiguousarray(a))
         else:
-            call("lt_rmsnorm", h, x.vp, w.vp, self.h.vp, 1, E, eps)
-            call("lt_quant_q8", h, self.h.vp, self.xq.vp, self.xd.vp, E)
-
-    def check_room(self, n: int = 1) -> None:
-        """Refuse n more positions when the KV caches cannot hold them: past max_ctx the step
-        kernels would attend over an empty context and drop the new row."""
-        if self.caches[0].length + n > self.max_ctx:
-            raise ValueError(f"KV cache full: {self.caches[0].length} + {n} positions exceed "
-                             f"max_ctx {self.max_ctx}")
-
-    def step(self, tok: int | None = None) -> None:
-        """Eager step (tok=None: use the device token left by the previous argmax)."""
-        self.check_room(1)
-        if tok is not None:
-            self.set_token(tok)
-        self.enqueue_step()
-        for c in self.caches:
-            c.length += 1
-
-    def free(self) -> None:
-        if self._prefill is not None:
-            self._prefill.free()
-        for c in self.caches:
-            c.free()
-        for t in (self.tok, self.err, self.hist, self.hist_count, self.lens, self.resid_in, self.carry,
-                  self.xres, self.h, self.qkv, self.att, self.gu, self.v, self.logits, self.xq, self.xd,
-                  self.am_ws, self.attn_ws):
-            if t is not None:
-                t.free()
+            out[name] = np.ascontiguousarray(a.reshape(-1))
+    return out
 
 
-class PrefillBuffers:
-    """Device buffers of a batched prefill of up to T tokens."""
-
-    def __init__(self, plan: "DecodePlan", T: int):
-        cfg, D = plan.cfg, plan.dev
-        E, F = cfg.n_embd, cfg.n_ff
-        kmax = max(E, F, cfg.q_dim)
-        self.T = T
-        self.toks = DevTensor.empty((T,), np.int32, D)
-        self.x = DevTensor.empty((T, E), np.float32, D)
-        self.xres = DevTensor.empty((T, E), np.float32, D)
-        self.qkv = DevTensor.empty((T, cfg.n_qkv), np.float32, D)
-        self.att = DevTensor.empty((T, cfg.q_dim), np.float32, D)
-        self.v = DevTensor.empty((T, F), np.float32, D)
-        self.xq = DevTensor.empty((T * kmax,), np.int8, D)
-        self.xd = DevTensor.empty((T * kmax // 32,), np.uint16, D)
-        aw = _lib.raw("lt_attn_workspace_size")(T, cfg.n_head, cfg.head_dim, plan.profile.attn_nsplit)
-        self.ws = DevTensor.empty((aw,), np.uint8, D) if aw else None
-
-    def free(self) -> None:
-        for t in (self.toks, self.x, self.xres, self.qkv, self.att, self.v, self.xq, self.xd, self.ws):
-            if t is not None:
-                t.free()
+_MODELS: dict = {}
 
 
-def forward_prefill(plan: DecodePlan, tokens) -> None:
-    """Batched prefill of a prompt: every linear layer runs once over all T tokens through
-    the int8-MFMA Q8_0 GEMM on the coalesced layouts (tile-major weight copies from
-    ResidentModel.prefill_tiles, block-major activation quants; lt_q8_gemm_t), with batched
-    RMSNorm/RoPE/KV append and causal attention.  It is device-uniform with the single-token
-    path the reference uses (bpd/lib/dev_residency.py:1338-1356): the KV cache, the last
-    token's logits and the greedy token it leaves on the device are bit-identical to
-    forward_pass_resident's."""
-    toks = np.asarray([int(t) for t in np.asarray(tokens).reshape(-1)], np.int32)
-    T = int(toks.size)
-    if T == 0:
-        return
-    cfg, m, p, D = plan.cfg, plan.model, plan.profile, plan.dev
-    if plan.caches[0].length + T > plan.max_ctx:
-        raise ValueError(f"prefill of {T} tokens overflows the {plan.max_ctx}-position KV cache")
-    if "wgu_il" not in m.layers[0]:
-        raise ValueError("forward_prefill needs the fused gate|up layout (ResidentModel layouts 'fused' or 'both')")
-    # every layer's length sits in the plan's one array, so all of them advance in one launch
-    # after the last layer's attention (each layer's attention reads only its own)
-    if not all(c.len_ptr == plan.lens.ptr + 4 * il and c.max_seq == plan.max_ctx
-               for il, c in enumerate(plan.caches)):
-        raise ValueError("forward_prefill needs the DecodePlan's joint length array")
-    m.prefill_tiles()
-    B = plan.prefill_buffers(T)
-    h = D.handle
-    E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
-    QD, KD, NQ = cfg.q_dim, cfg.kv_dim, cfg.n_qkv
-    eps = ctypes.c_float(cfg.norm_eps)
-    D.h2d(B.toks.ptr, toks)
-    call("lt_embed_q8_batch", h, m.tok_embd.t.vp, B.toks.vp, B.x.vp, T, E, cfg.vocab, plan.err.vp)
-    ws, ws_n = _vp(B.ws), (B.ws.nbytes if B.ws is not None else 0)
-    for il, L in enumerate(m.layers):
-        cache = plan.caches[il]
-        lp = _vp(cache.len_ptr)
-        call("lt_rmsnorm_quant_bm", h, B.x.vp, L["attn_norm"].vp, B.xq.vp, B.xd.vp, T, E, eps)
-        call("lt_q8_gemm_t", h, L["wqkv_t"].t.vp, B.xq.vp, B.xd.vp, _vp(L["bqkv"]), None, B.qkv.vp, T, NQ, E)
-        call("lt_rope_append_batch", h, B.qkv.vp, T, NQ, lp, nh, nkv, hd, m.freqs.vp, cache.k.vp, cache.v.vp,
-             cache.max_seq, p.kv_dtype)
-        call("lt_attn_prefill", h, B.qkv.vp, NQ, cache.k.vp, cache.v.vp, lp, B.att.vp, T, nh, nkv, hd,
-             ctypes.c_float(plan.scale), cache.max_seq, p.attn_nsplit, p.kv_dtype, ws, ws_n)
-        call("lt_quant_q8_bm", h, B.att.vp, B.xq.vp, B.xd.vp, T, QD)
-        call("lt_q8_gemm_t", h, L["wo_t"].t.vp, B.xq.vp, B.xd.vp, None, B.x.vp, B.xres.vp, T, E, QD)
-        call("lt_rmsnorm_quant_bm", h, B.xres.vp, L["ffn_norm"].vp, B.xq.vp, B.xd.vp, T, E, eps)
-        call("lt_q8_gemm_silu_t", h, L["wgu_il_t"].t.vp, B.xq.vp, B.xd.vp, B.v.vp, T, F, E)
-        call("lt_quant_q8_bm", h, B.v.vp, B.xq.vp, B.xd.vp, T, F)
-        call("lt_q8_gemm_t", h, L["wdown_t"].t.vp, B.xq.vp, B.xd.vp, None, B.xres.vp, B.x.vp, T, E, F)
-    call("lt_len_add_n", h, _vp(plan.lens.ptr), len(m.layers), T, plan.max_ctx)
-    for cache in plan.caches:   # the host mirror advances with the device lengths
-        cache.length += T
-    # the last token's logits and greedy token, as the decode step computes them
-    D.d2d(plan.carry.ptr, B.x.ptr + (T - 1) * E * 4, E * 4)
-    call("lt_q8_gemv_rms_argmax", h, plan.carry.vp, m.output_norm.vp, eps, m.output.t.vp, plan.logits.vp,
-         cfg.vocab, E, plan.tok.vp, None, None, 0, plan.am_ws.vp, plan.am_ws.nbytes)
+def _resident(w, cfg: dict):
+    """(ResidentModel, exact_embedding): the model uploaded once per weight dict.  When every
+    token_embd row round-trips through Q8_0 unchanged (any Q8_0 GGUF), the step gathers its
+    input row on the device; otherwise the fp32 host row is written before each step, as
+    the reference does."""
+    E = int(cfg["n_embd"])
+    emb = _embedding_rows(w, E)
+    key = (id(w), len(w), _sample_key(np.asarray(emb[:1], np.float32)), tuple(sorted(cfg.items())))
+    hit = _MODELS.get(key)
+    if hit is None:
+        mc = _engine_cfg(cfg, w)
+        ew = _engine_weights(w, mc)
+        exact = bool(np.array_equal(q8.dequantize_rows(ew["token_embd.weight"], E), np.asarray(emb, np.float32)))
+        hit = (engine.ResidentModel(mc, ew, _dev(), layouts="fused"), exact, emb)
+        _MODELS[key] = hit
+    return hit
 
 
-def forward_pass_resident(plan: DecodePlan, tokens) -> np.ndarray:
-    """Feed tokens one at a time through the single-token device path (the reference's
-    device-uniform prefill, dev_residency.py:1338-1356); return the last token's logits."""
-    toks = [int(t) for t in np.asarray(tokens).reshape(-1)]
-    for t in toks:
-        plan.step(t)
-    return plan.read_logits()
+def _plan_for(w, cfg, kv_cache, create: bool = True) -> engine.DecodePlan:
+    c0 = kv_cache[0]
+    if c0 is not None:
+        plan = getattr(c0, "_plan", None)
+        if plan is None:
+            raise ValueError("kv_cache holds caches this module did not create; pass [None] * n_layers")
+        return plan
+    if not create:
+        raise RuntimeError("call seed() (or forward_pass_resident) first: the KV caches do not exist yet")
+    model, exact, _ = _resident(w, cfg)
+    plan = engine.DecodePlan(model, _engine_profile(), max_ctx=int(_KV_MAX_SEQ),
+                             hist_cap=int(_KV_MAX_SEQ) + 1, host_embed=not exact)
+    if len(kv_cache) != len(plan.caches):
+        raise ValueError(f"kv_cache has {len(kv_cache)} entries for a {len(plan.caches)}-layer model")
+    for il, c in enumerate(plan.caches):
+        c._plan = plan
+        kv_cache[il] = c
+    plan._emb = _resident(w, cfg)[2]
+    return plan
+
+
+def _rows(plan, toks):
+    return np.ascontiguousarray(plan._emb[toks], np.float32) if plan.host_embed else None
+
+
+def _as_logits(x: np.ndarray):
+    x = np.ascontiguousarray(x, np.float32).reshape(1, 1, -1)
+    try:
+        import torch
+    except ImportError:
+        return x
+    return torch.from_numpy(x.copy())
+
+
+def forward_pass_resident(w, cfg, tok, positions, kv_cache):
+    """Forward of one or more tokens through the device decode path; returns the last
+    token's logits [1, 1, vocab] (reference :1328-1593).  kv_cache is a list of per-layer
+    entries, None before the first call (the caches are created here and kept in it)."""
+    assert_certified_composition()
+    toks, poss = _ids(tok), _ids(positions)
+    if not toks:
+        raise ValueError("forward_pass_resident: no tokens")
+    plan = _plan_for(w, cfg, kv_cache)
+    L = plan.caches[0].length
+    if poss != list(range(L, L + len(toks))):
+        raise ValueError(f"positions {poss[:4]}... must continue the cache at {L} (the device path "
+                         "takes each token's position from the cache length)")
+    if len(toks) > 1:
+        engine.forward_prefill(plan, toks, _rows(plan, toks))
+    else:
+        plan.step(toks[0], None if not plan.host_embed else _rows(plan, toks)[0])
+    return _as_logits(plan.read_logits())
 
 
 class GraphRunner:
-    """Capture one decode step into a HIP graph and replay it per token
-    (reference GraphRunner, bpd/lib/dev_residency.py:1626-1818)."""
+    """Capture one decode step into a HIP graph and replay it per token (reference
+    :1626-1818): seed() prefills and fixes every buffer, capture() records the step,
+    replay_logits() / replay_token() run it for a token."""
 
-    def __init__(self, plan: DecodePlan):
-        self.plan = plan
-        self.dev = plan.dev
-        self.graph = ctypes.c_void_p()
+    def __init__(self, w, cfg, kv_cache):
+        self.w, self.cfg, self.kv = w, cfg, kv_cache
+        self.E = int(cfg["n_embd"])
         self.captured = False
+        self._graph = None
 
-    def seed(self, prompt, batched: bool = False) -> np.ndarray:
-        """Eager prefill over the prompt (fixed buffers, all kernels loaded); returns the
-        last prompt token's logits.  The device token then holds the first greedy token.
-        batched=True runs forward_prefill (the int8-MFMA GEMM path; bit-identical)."""
-        if batched:
-            forward_prefill(self.plan, prompt)
-            logits = self.plan.read_logits()
-        else:
-            logits = forward_pass_resident(self.plan, prompt)
-        self.dev.sync()
+    def seed(self, first_tok, first_pos):
+        """Prefill the prompt eagerly (every buffer allocated, every kernel loaded); returns
+        the last prompt token's logits."""
+        if not _GRAPH_PREP:
+            raise AssertionError("GraphRunner requires BPD_GRAPH_PREP semantics")
+        assert_certified_composition()
+        logits = forward_pass_resident(self.w, self.cfg, first_tok, first_pos, self.kv)
+        _dev().sync()
         return logits
 
-    def capture(self) -> None:
+    def capture(self, tok, pos):
+        """Record one decode step.  pos must be the position the first replay will take
+        (the cache length); nothing runs until a replay."""
         if self.captured:
             raise RuntimeError("GraphRunner.capture: already captured")
-        call("lt_graph_begin", self.dev.handle)
-        try:
-            self.plan.enqueue_step()
-        except Exception:
-            g = ctypes.c_void_p()
-            _lib.raw("lt_graph_end")(self.dev.handle, ctypes.byref(g))
-            if g.value:
-                _lib.raw("lt_graph_free")(g)
-            raise
-        call("lt_graph_end", self.dev.handle, ctypes.byref(self.graph))
+        plan = _plan_for(self.w, self.cfg, self.kv, create=False)
+        p = _ids(pos)
+        if len(p) != 1 or p[0] != plan.caches[0].length:
+            raise ValueError(f"capture at position {p} but the cache holds {plan.caches[0].length} rows")
+        self._graph = engine.StepGraph(plan)
+        self._graph.capture()
         self.captured = True
 
-    def _launch(self) -> None:
+    def _input(self, tok):
+        t = _ids(tok)
+        if len(t) != 1:
+            raise ValueError(f"a replay takes one token, got {len(t)}")
+        plan = self._graph.plan
+        return t[0], (_rows(plan, t)[0] if plan.host_embed else None)
+
+    def replay_logits(self, tok):
+        """One replay for token `tok`; returns its logits [1, 1, vocab]."""
         if not self.captured:
-            raise RuntimeError("call capture() before replay")
-        self.plan.check_room(1)
-        call("lt_graph_launch", self.dev.handle, self.graph)
-        for c in self.plan.caches:
-            c.length += 1
+            raise AssertionError("call capture() before replay")
+        t, row = self._input(tok)
+        return _as_logits(self._graph.replay_logits(t, row))
 
-    def replay_logits(self, tok: int) -> np.ndarray:
-        self.plan.set_token(tok)
-        self._launch()
-        return self.plan.read_logits()
-
-    def replay_token(self, tok: int | None = None) -> int:
-        """One graph replay; returns the greedy next token (4 bytes cross to the host)."""
-        if tok is not None:
-            self.plan.set_token(tok)
-        self._launch()
-        return self.plan.read_token()
-
-    def replay_tokens(self, n: int) -> list[int]:
-        """n back-to-back replays continuing from the device token; the host reads the n
-        generated ids once at the end from the device history.  Same tokens as n calls of
-        replay_token()."""
-        start = self.plan.history_count()
-        if start + n > self.plan.hist_cap:
-            raise ValueError(f"token history capacity {self.plan.hist_cap} exceeded")
-        self.plan.check_room(n)
-        for _ in range(n):
-            self._launch()
-        return self.plan.history()[start:start + n]
+    def replay_token(self, tok) -> int:
+        """One replay for token `tok`; the argmax runs on the device and only the chosen
+        index (4 bytes) crosses to the host."""
+        if not self.captured:
+            raise AssertionError("call capture() before replay")
+        t, row = self._input(tok)
+        return self._graph.replay_token(t, row)
 
     def free(self) -> None:
-        if self.captured:
-            call("lt_graph_free", self.graph)
+        if self._graph is not None:
+            self._graph.free()
+            self._graph = None
             self.captured = False
-
-
-def generate(model, input_ids, n_tokens: int, profile: Profile = PRODUCTION_PROFILE,
-             batched_prefill: bool = True, max_ctx: int | None = None) -> list[int]:
-    """Greedy generation of n_tokens after input_ids, the reference's decode loop
-    (decode_fact.py:54-111 semantics; GraphRunner seed -> capture -> replay,
-    dev_residency.py:1626-1818): the prompt is prefilled, the first token is its greedy
-    argmax, and every further token comes from one replay of the captured step.
-
-    `model` is a ResidentModel or the path of a Q8_0 GGUF file (loaded and freed here)."""
-    own = not isinstance(model, ResidentModel)
-    m = ResidentModel.from_gguf(model, max_ctx=max_ctx or 1024) if own else model
-    plan = gr = None
-    try:
-        ids = [int(t) for t in np.asarray(input_ids).reshape(-1)]
-        if not ids:
-            raise ValueError("generate: empty prompt")
-        if n_tokens < 1:
-            return []
-        # the history records one entry per token through the step's argmax: the prompt's
-        # (when it is fed token by token) and every generated one
-        plan = DecodePlan(m, profile, max_ctx=max_ctx, hist_cap=len(ids) + n_tokens)
-        if len(ids) + n_tokens - 1 > plan.max_ctx:
-            raise ValueError(f"generate: {len(ids)} prompt + {n_tokens - 1} decode positions exceed "
-                             f"the {plan.max_ctx}-position KV cache")
-        gr = GraphRunner(plan)
-        gr.seed(ids, batched=batched_prefill and "wgu_il" in m.layers[0])
-        out = [plan.read_token()]
-        if n_tokens > 1:
-            gr.capture()
-            out += gr.replay_tokens(n_tokens - 1)
-        return out
-    finally:
-        if gr is not None:
-            gr.free()
-        if plan is not None:
-            plan.free()
-        if own:
-            m.free()

@@ -1,0 +1,1006 @@
+"""The MI355X decode engine: device-resident Q8_0 weights, a fixed-buffer decode plan whose
+launches are captured into one HIP graph per token, and the batched prefill, all driving
+libllamatov_hip.so through ctypes.
+
+Each piece replaces a part of the reference's bpd/lib/dev_residency.py, with buffers the caller
+owns instead of module globals:
+  DevTensor (dev_residency.py:387-415); KVCache (DeviceKVCache, :418-541); the op launchers
+  rms_norm_into (rms_norm_dev, :746-781), q8_linear_into (q8_linear_dev, :905-985),
+  q8_linear_add_residual_into (:988-1045), q8_linear_bias_into (q8_linear_dev_bias,
+  :1177-1193), rope_qk_into (rope_dev_qk_fused, :722-741), attn_decode_into
+  (attn_decode_from_cache_masked, :2016-2031), argmax_into (argmax_dev, :1074-1110);
+  DecodePlan + forward_tokens (forward_pass_resident, :1328-1593); StepGraph (GraphRunner,
+  :1626-1818); Profile (PRODUCTION_PROFILE / attest_profile / assert_certified_composition,
+  :1209-1281).  llamatov_amd.dev_residency keeps the reference's own signatures on top of it.
+
+Design differences (MI355X-first; results are the same bits):
+  * Q8_0 weights are the GGUF 34-byte blocks, uploaded once at load (ResidentModel); the
+    reference dequantizes to fp32 on the host and re-quantizes at first use.
+  * Every buffer a decode step touches is allocated up front in a DecodePlan, so the
+    step is capturable without a slab arena and graph pointers never move.
+  * The token id lives on the device: the step gathers its embedding from the Q8_0
+    token_embd and the argmax writes the next id back into the same buffer, so greedy
+    decoding can replay the graph back to back with no host round trip per token.
+"""
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from ._lib import LT_KV_F16, LT_KV_F32, call
+from .model import ModelConfig, fused_layer_tensors, interleave_gateup
+
+
+# ----------------------------------------------------------------------------------
+# Device context and tensors
+# ----------------------------------------------------------------------------------
+class Device:
+    """One lt_ctx (one HIP device + one stream).  The reference's fact_dispatch._ctx()."""
+
+    def __init__(self, index: int = 0):
+        _lib.load()
+        h = ctypes.c_void_p()
+        call("lt_init", index, ctypes.byref(h))
+        self.handle = h
+        self.index = index
+        self.capturing = False
+
+    def malloc(self, nbytes: int) -> int:
+        p = ctypes.c_void_p()
+        call("lt_malloc", self.handle, ctypes.byref(p), max(int(nbytes), 1))
+        return int(p.value)
+
+    def free(self, ptr: int) -> None:
+        if ptr:
+            call("lt_free", self.handle, ctypes.c_void_p(ptr))
+
+    def h2d(self, ptr: int, arr: np.ndarray) -> None:
+        a = np.ascontiguousarray(arr)
+        call("lt_memcpy_h2d", self.handle, ctypes.c_void_p(ptr), a.ctypes.data_as(ctypes.c_void_p), a.nbytes)
+
+    def d2h(self, arr: np.ndarray, ptr: int) -> np.ndarray:
+        assert arr.flags.c_contiguous
+        call("lt_memcpy_d2h", self.handle, arr.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(ptr), arr.nbytes)
+        return arr
+
+    def d2d(self, dst: int, src: int, nbytes: int) -> None:
+        call("lt_memcpy_d2d", self.handle, ctypes.c_void_p(dst), ctypes.c_void_p(src), int(nbytes))
+
+    def fill(self, ptr: int, value: int, nbytes: int) -> None:
+        call("lt_fill_u8", self.handle, ctypes.c_void_p(ptr), value, int(nbytes))
+
+    def sync(self) -> None:
+        call("lt_sync", self.handle)
+
+
+_DEVICE: Device | None = None
+
+
+def get_device() -> Device:
+    global _DEVICE
+    if _DEVICE is None:
+        _DEVICE = Device(0)
+    return _DEVICE
+
+
+class DevTensor:
+    """A device buffer: raw pointer + shape + numpy dtype (reference DevTensor is fp32-only)."""
+    __slots__ = ("ptr", "shape", "dtype", "n", "nbytes", "_owns", "dev")
+
+    def __init__(self, ptr: int, shape, dtype=np.float32, owns: bool = True, dev: Device | None = None):
+        self.ptr = int(ptr)
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        self.n = int(np.prod(self.shape)) if self.shape else 1
+        self.nbytes = self.n * self.dtype.itemsize
+        self._owns = owns
+        self.dev = dev or get_device()
+
+    @staticmethod
+    def empty(shape, dtype=np.float32, dev: Device | None = None) -> "DevTensor":
+        dev = dev or get_device()
+        n = int(np.prod(shape)) if shape else 1
+        return DevTensor(dev.malloc(n * np.dtype(dtype).itemsize), shape, dtype, True, dev)
+
+    @staticmethod
+    def zeros(shape, dtype=np.float32, dev: Device | None = None) -> "DevTensor":
+        t = DevTensor.empty(shape, dtype, dev)
+        t.dev.fill(t.ptr, 0, t.nbytes)
+        return t
+
+    @staticmethod
+    def from_host(arr: np.ndarray, dev: Device | None = None) -> "DevTensor":
+        a = np.ascontiguousarray(arr)
+        t = DevTensor.empty(a.shape, a.dtype, dev)
+        t.dev.h2d(t.ptr, a)
+        return t
+
+    def view(self, offset_elems: int, shape, dtype=None) -> "DevTensor":
+        dt = np.dtype(dtype) if dtype is not None else self.dtype
+        return DevTensor(self.ptr + offset_elems * self.dtype.itemsize, shape, dt, False, self.dev)
+
+    def to_host(self) -> np.ndarray:
+        self.dev.sync()
+        out = np.empty(self.shape, self.dtype)
+        return self.dev.d2h(out, self.ptr)
+
+    def upload(self, arr: np.ndarray) -> None:
+        a = np.ascontiguousarray(arr, dtype=self.dtype)
+        if a.nbytes != self.nbytes:
+            raise ValueError(f"upload of {a.nbytes} bytes into a {self.nbytes}-byte tensor")
+        self.dev.h2d(self.ptr, a)
+
+    def free(self) -> None:
+        if self._owns and self.ptr:
+            self.dev.free(self.ptr)
+            self.ptr = 0
+
+    @property
+    def vp(self) -> ctypes.c_void_p:
+        return ctypes.c_void_p(self.ptr)
+
+
+def _vp(x) -> ctypes.c_void_p:
+    """A device pointer as a ctypes argument: None, an int address, a ctypes.c_void_p, a
+    DevTensor, or any object whose .ptr is one of those (the reference's tensors)."""
+    if x is None:
+        return ctypes.c_void_p(0)
+    if isinstance(x, ctypes.c_void_p):
+        return ctypes.c_void_p(x.value or 0)
+    if isinstance(x, DevTensor):
+        return x.vp
+    p = getattr(x, "ptr", None)
+    if p is not None:
+        return _vp(p)
+    return ctypes.c_void_p(int(x))
+
+
+# ----------------------------------------------------------------------------------
+# Op launchers (thin mirrors of the reference op functions)
+# ----------------------------------------------------------------------------------
+class Q8Weight:
+    """A Q8_0 weight resident on the device as GGUF blocks [N][K/32]: uploads its own copy,
+    or wraps a slice of a DeviceArena (t=...)."""
+    __slots__ = ("t", "N", "K")
+
+    def __init__(self, blocks: np.ndarray | None, K: int, dev: Device | None = None,
+                 t: "DevTensor | None" = None, N: int | None = None):
+        if t is not None:
+            self.t, self.N, self.K = t, int(N), K
+            return
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        N = blocks.shape[0]
+        if blocks.shape[1] != K // 32 * 34:
+            raise ValueError(f"Q8Weight: {blocks.shape} is not [N, {K // 32 * 34}]")
+        self.t = DevTensor.from_host(blocks, dev)
+        self.N, self.K = N, K
+
+
+class DeviceArena:
+    """One device allocation holding a model's tensors back to back (256-byte aligned
+    slices, 2 MiB-aligned base): a single mapping with large pages, so streaming the
+    weights of a decode step never walks more page tables than it has to.  The slices
+    are non-owning DevTensor views; free() releases the whole arena."""
+    ALIGN = 256
+    BASE_ALIGN = 2 << 20
+
+    def __init__(self, dev: Device | None = None):
+        self.dev = dev or get_device()
+        self.items: list[tuple[np.ndarray, list]] = []
+        self.ptr = 0
+
+    def add(self, arr: np.ndarray) -> list:
+        """Stage an array; the returned one-element list receives its DevTensor at commit()."""
+        slot: list = []
+        self.items.append((np.ascontiguousarray(arr), slot))
+        return slot
+
+    def commit(self) -> None:
+        offs, total = [], 0
+        for a, _ in self.items:
+            offs.append(total)
+            total += (a.nbytes + self.ALIGN - 1) // self.ALIGN * self.ALIGN
+        self.ptr = self.dev.malloc(total + self.BASE_ALIGN)
+        base = (self.ptr + self.BASE_ALIGN - 1) // self.BASE_ALIGN * self.BASE_ALIGN
+        for (a, slot), off in zip(self.items, offs):
+            t = DevTensor(base + off, a.shape, a.dtype, owns=False, dev=self.dev)
+            self.dev.h2d(t.ptr, a)
+            slot.append(t)
+        self.nbytes = total
+        self.items = []
+
+    def free(self) -> None:
+        if self.ptr:
+            self.dev.free(self.ptr)
+            self.ptr = 0
+
+
+def quant_q8_into(x: DevTensor, xq: DevTensor, xd: DevTensor, K: int | None = None) -> None:
+    K = K or x.n
+    call("lt_quant_q8", x.dev.handle, x.vp, xq.vp, xd.vp, K)
+
+
+def rms_norm_into(x: DevTensor, w: DevTensor, eps: float, out: DevTensor) -> DevTensor:
+    """k_rmsnorm block_row into `out` (reference rms_norm_dev_into, dev_residency.py:1130)."""
+    N = x.shape[-1]
+    M = x.n // N
+    call("lt_rmsnorm", x.dev.handle, x.vp, w.vp, out.vp, M, N, ctypes.c_float(eps))
+    return out
+
+
+def q8_gemv_into(W: Q8Weight, xq: DevTensor, xd: DevTensor, out: DevTensor,
+                resid: DevTensor | None = None) -> DevTensor:
+    call("lt_q8_gemv", out.dev.handle, W.t.vp, xq.vp, xd.vp, _vp(resid), out.vp, W.N, W.K)
+    return out
+
+
+def q8_linear_into(x: DevTensor, W: Q8Weight, out: DevTensor, xq: DevTensor, xd: DevTensor) -> DevTensor:
+    """quant + GEMV into `out` (reference q8_linear_dev_into, dev_residency.py:1139-1172)."""
+    quant_q8_into(x, xq, xd, W.K)
+    return q8_gemv_into(W, xq, xd, out)
+
+
+def q8_linear_add_residual_into(x: DevTensor, W: Q8Weight, resid: DevTensor, out: DevTensor,
+                               xq: DevTensor, xd: DevTensor, silu_src=None) -> DevTensor:
+    """quant (or SiLU*mul+quant when silu_src=(g, u)) + GEMV with the residual added at the
+    store (reference q8_linear_add_residual_dev, dev_residency.py:988-1045)."""
+    if silu_src is not None:
+        g, u = silu_src
+        call("lt_silu_mul_quant", out.dev.handle, g.vp, u.vp, xq.vp, xd.vp, W.K)
+    else:
+        quant_q8_into(x, xq, xd, W.K)
+    return q8_gemv_into(W, xq, xd, out, resid)
+
+
+def q8_linear_bias_into(x: DevTensor, W: Q8Weight, bias: DevTensor | None, out: DevTensor,
+                       xq: DevTensor, xd: DevTensor) -> DevTensor:
+    """Bias folded into the GEMV store (reference q8_linear_dev_bias, :1177-1193)."""
+    if bias is None:
+        return q8_linear_into(x, W, out, xq, xd)
+    return q8_linear_add_residual_into(x, W, bias, out, xq, xd)
+
+
+def rope_qk_into(qk: DevTensor, pos_ptr: int, nh: int, nkv: int, hd: int, freqs: DevTensor) -> None:
+    call("lt_rope_qk", qk.dev.handle, qk.vp, _vp(pos_ptr), nh + nkv, hd, freqs.vp)
+
+
+def attn_decode_into(q: DevTensor, cache: "KVCache", nh: int, scale: float,
+                                  len_ptr: int, out: DevTensor, nsplit: int = 1,
+                                  ws: DevTensor | None = None) -> DevTensor:
+    call("lt_attn_decode", q.dev.handle, q.vp, cache.k.vp, cache.v.vp, _vp(len_ptr), out.vp, 1, nh,
+         cache.nkv, cache.hd, ctypes.c_float(scale), cache.max_seq, nsplit, cache.kv_dtype,
+         _vp(ws), ws.nbytes if ws is not None else 0)
+    return out
+
+
+def argmax_into(logits: DevTensor, n: int, out_ptr: int, ws: DevTensor) -> int:
+    if n <= 0:
+        raise ValueError(f"argmax_into: n={n} (must be > 0)")
+    call("lt_argmax", logits.dev.handle, logits.vp, n, _vp(out_ptr), ws.vp, ws.nbytes)
+    return out_ptr
+
+
+def rope_freqs(hd: int, theta: float) -> np.ndarray:
+    f = np.empty(hd // 2, dtype=np.float32)
+    call("lt_rope_freqs", hd, ctypes.c_float(theta), f.ctypes.data_as(ctypes.c_void_p))
+    return f
+
+
+# ----------------------------------------------------------------------------------
+# KV cache
+# ----------------------------------------------------------------------------------
+class KVCache:
+    """Device KV cache for one layer: position-major [max_seq][nkv*hd] K and V and a device
+    int length (reference DeviceKVCache, bpd/lib/dev_residency.py:418-541).  kv_dtype
+    LT_KV_F32 (the reference's elem_bytes=4) or LT_KV_F16."""
+
+    def __init__(self, max_seq: int, nkv: int, hd: int, kv_dtype: int = LT_KV_F32,
+                 len_ptr: int | None = None, dev: Device | None = None):
+        self.dev = dev or get_device()
+        self.max_seq, self.nkv, self.hd = int(max_seq), int(nkv), int(hd)
+        self.width = self.nkv * self.hd
+        self.kv_dtype = kv_dtype
+        self.elem_bytes = 2 if kv_dtype == LT_KV_F16 else 4
+        dt = np.uint16 if kv_dtype == LT_KV_F16 else np.float32
+        self.k = DevTensor.empty((self.max_seq, self.width), dt, self.dev)
+        self.v = DevTensor.empty((self.max_seq, self.width), dt, self.dev)
+        self._len_owned = len_ptr is None
+        self.len_ptr = self.dev.malloc(4) if len_ptr is None else int(len_ptr)
+        self.length = 0
+        self.set_length(0)
+
+    def set_length(self, n: int) -> None:
+        self.length = int(n)
+        self.dev.h2d(self.len_ptr, np.array([n], dtype=np.int32))
+
+    def device_length(self) -> int:
+        out = np.zeros(1, np.int32)
+        self.dev.sync()
+        self.dev.d2h(out, self.len_ptr)
+        return int(out[0])
+
+    # -- the reference DeviceKVCache interface (bpd/lib/dev_residency.py:418-541) --------
+    @property
+    def k_ptr(self) -> ctypes.c_void_p:
+        return self.k.vp
+
+    @property
+    def v_ptr(self) -> ctypes.c_void_p:
+        return self.v.vp
+
+    def _ensure_len_ptr(self, seed: bool = True) -> ctypes.c_void_p:
+        """The device length; seed=True writes the host mirror into it first (eager use,
+        never under capture)."""
+        if seed:
+            self.set_length(self.length)
+        return ctypes.c_void_p(self.len_ptr)
+
+    def incr_len_dev(self) -> None:
+        """*len += 1 on the device (capturable); the host mirror is the caller's."""
+        call("lt_len_add", self.dev.handle, _vp(self.len_ptr), 1, self.max_seq)
+
+    def append(self, k, v, count: int = 1) -> None:
+        """Copy `count` rows of K and V (device pointers, fp32 rows of width elements) into
+        the cache at the host length, then advance the host length (device len unchanged)."""
+        if self.kv_dtype != LT_KV_F32:
+            raise ValueError("KVCache.append copies raw rows into an fp32 cache; an fp16 cache "
+                             "takes rows through append_at_len / append_at_len_incr")
+        if self.length + count > self.max_seq:
+            raise ValueError(f"KV cache full: {self.length} + {count} > {self.max_seq}")
+        n = count * self.width * 4
+        off = self.length * self.width * 4
+        self.dev.d2d(self.k.ptr + off, _vp(k).value, n)
+        self.dev.d2d(self.v.ptr + off, _vp(v).value, n)
+        self.length += count
+
+    def append_at_len(self, k, v) -> None:
+        """Write one K and V row at the device length *len, leaving *len unchanged
+        (capturable; fp16 caches round to nearest even)."""
+        if getattr(self, "_stage", None) is None:
+            self._stage = DevTensor.empty((2 * self.width,), np.float32, self.dev)
+        st = self._stage
+        self.dev.d2d(st.ptr, _vp(k).value, self.width * 4)
+        self.dev.d2d(st.ptr + self.width * 4, _vp(v).value, self.width * 4)
+        call("lt_kv_append_batch", self.dev.handle, self.k.vp, self.v.vp, st.vp, 0, 0, self.width, 1,
+             _vp(self.len_ptr), self.width, self.max_seq, self.kv_dtype)
+
+    def append_at_len_incr(self, k, v) -> bool:
+        """Write one K and V row at *len and advance *len, in one launch; True (the
+        increment is folded, as the reference's fused path reports)."""
+        call("lt_kv_append_incr", self.dev.handle, self.k.vp, _vp(k), self.v.vp, _vp(v),
+             _vp(self.len_ptr), self.width, self.max_seq, self.kv_dtype)
+        return True
+
+    def _slice_host(self, which: str) -> np.ndarray:
+        rows = self.rows_host(which, self.length)
+        if self.kv_dtype == LT_KV_F16:
+            rows = rows.view(np.float16).astype(np.float32)
+        return np.ascontiguousarray(rows, np.float32).reshape(self.length, self.nkv, self.hd)
+
+    def k_slice_host(self) -> np.ndarray:
+        """The valid K rows [length, nkv, hd] as fp32 on the host."""
+        return self._slice_host("k")
+
+    def v_slice_host(self) -> np.ndarray:
+        return self._slice_host("v")
+
+    def rows_host(self, which: str, n: int | None = None) -> np.ndarray:
+        n = self.length if n is None else n
+        t = self.k if which == "k" else self.v
+        out = np.empty((self.max_seq, self.width), t.dtype)
+        self.dev.sync()
+        self.dev.d2h(out, t.ptr)
+        return out[:n]
+
+    def free(self) -> None:
+        self.k.free()
+        self.v.free()
+        if getattr(self, "_stage", None) is not None:
+            self._stage.free()
+            self._stage = None
+        if self._len_owned:
+            self.dev.free(self.len_ptr)
+
+
+# ----------------------------------------------------------------------------------
+# Production profile (a frozen config object instead of the reference's env flags)
+# ----------------------------------------------------------------------------------
+@dataclass(frozen=True)
+class Profile:
+    """The certified ensemble.  Every variant below is bit-identical to the reference's
+    per-op chain; the fields select kernels, not numerics, except attn_nsplit (> 1 selects
+    the split-K declared order) and kv_dtype."""
+    kv_dtype: int = LT_KV_F32
+    attn_nsplit: int = 1
+    fused_step: bool = True         # five fused launches per layer (lt_fused.hip)
+    fused_rms_quant: bool = False   # per-op path only: k_rms_quant instead of k_rmsnorm + k_quant_q8
+    graph: bool = True
+
+
+PRODUCTION_PROFILE = Profile()
+_CERTIFIED_NSPLIT = {1, 2, 4, 8, 16, 32, 64, 128}
+
+
+def attest_profile(p: Profile) -> dict:
+    return dataclasses.asdict(p)
+
+
+def assert_certified_composition(p: Profile) -> None:
+    """Refuse uncertified ensembles (reference dev_residency.py:1268-1281)."""
+    if p.kv_dtype not in (LT_KV_F32, LT_KV_F16):
+        raise RuntimeError(f"uncertified kv_dtype {p.kv_dtype}")
+    if p.attn_nsplit not in _CERTIFIED_NSPLIT:
+        raise RuntimeError(f"uncertified attn_nsplit {p.attn_nsplit}")
+
+
+# ----------------------------------------------------------------------------------
+# Resident model and the fixed-buffer decode plan
+# ----------------------------------------------------------------------------------
+class ResidentModel:
+    """All weights on the device, uploaded once: Q8_0 blocks verbatim, q|k|v and gate|up
+    concatenated at load (the reference concatenates at first use, dev_residency.py:1283-1326),
+    tied lm_head sharing token_embd's blocks.
+
+    layouts selects the gate|up layouts uploaded: "fused" (rows interleaved gate j, up j, for
+    lt_q8_gemv_rms_silu), "per_op" (gate rows then up rows, the reference's concatenation,
+    for lt_q8_gemv + lt_silu_mul_quant) or "both"."""
+
+    def __init__(self, cfg: ModelConfig, weights: dict, dev: Device | None = None, layouts: str = "both"):
+        if layouts not in ("fused", "per_op", "both"):
+            raise ValueError(f"layouts={layouts!r}")
+        self.cfg = cfg
+        self.dev = dev or get_device()
+        self.layouts = layouts
+        E, F = cfg.n_embd, cfg.n_ff
+        arena = DeviceArena(self.dev)
+        staged = []   # (kind, owner dict, key, slot, N, K)
+
+        def q8(owner, key, blocks, K):
+            staged.append(("q8", owner, key, arena.add(blocks), blocks.shape[0], K))
+
+        def vec(owner, key, arr):
+            if arr is None:
+                owner[key] = None
+                return
+            staged.append(("vec", owner, key, arena.add(np.asarray(arr, np.float32)), 0, 0))
+
+        top: dict = {}
+        q8(top, "tok_embd", weights["token_embd.weight"], E)
+        if not cfg.tied:
+            q8(top, "output", weights["output.weight"], E)
+        vec(top, "output_norm", weights["output_norm.weight"])
+        vec(top, "freqs", rope_freqs(cfg.head_dim, cfg.rope_theta))
+        self.layers = []
+        for il in range(cfg.n_layers):
+            t = fused_layer_tensors(cfg, weights, il)
+            L: dict = {}
+            vec(L, "attn_norm", t["attn_norm"])
+            q8(L, "wqkv", t["wqkv"], E)
+            vec(L, "bqkv", t["bqkv"])
+            q8(L, "wo", t["wo"], cfg.q_dim)
+            vec(L, "ffn_norm", t["ffn_norm"])
+            q8(L, "wdown", t["wdown"], F)
+            if layouts in ("per_op", "both"):
+                q8(L, "wgu", t["wgu"], E)
+            if layouts in ("fused", "both"):
+                p = f"blk.{il}"
+                q8(L, "wgu_il", interleave_gateup(weights[f"{p}.ffn_gate.weight"],
+                                                  weights[f"{p}.ffn_up.weight"]), E)
+            self.layers.append(L)
+        arena.commit()
+        for kind, owner, key, slot, N, K in staged:
+            owner[key] = Q8Weight(None, K, t=slot[0], N=N) if kind == "q8" else slot[0]
+        self.arena = arena
+        self.load_report = None
+        self.tiles = None   # the prefill GEMM's tile-major copies (prefill_tiles)
+        self.tok_embd = top["tok_embd"]
+        self.output = top.get("output", self.tok_embd)
+        self.output_norm = top["output_norm"]
+        self.freqs = top["freqs"]
+
+    @classmethod
+    def from_gguf(cls, path, dev: Device | None = None, layouts: str = "both",
+                  max_ctx: int = 1024) -> "ResidentModel":
+        """Upload a Q8_0 GGUF file (the reference's load_model + first-use residency,
+        decode_fact.py:39-51, fact_dispatch.py:255-299): Q8_0 blocks go from the mapped file
+        to the device without a float32 copy.  `load_report` says how many tensors were used
+        verbatim, canonicalized or quantized from another type."""
+        from . import gguf
+        cfg, w, reader, report = gguf.load_q8_model(path, max_ctx=max_ctx)
+        try:
+            m = cls(cfg, w, dev, layouts)
+        finally:
+            del w
+            reader.close()
+        m.load_report = report
+        return m
+
+    def prefill_tiles(self) -> None:
+        """Tile-major copies of the prefill GEMM's matrices (q|k|v, o, interleaved gate|up,
+        down), built on the device from the resident blocks at the first batched prefill:
+        one allocation, lt_q8_tiles per matrix.  The decode path keeps reading the GGUF-layout
+        blocks; the copies cost one more copy of those weights in HBM."""
+        if self.tiles is not None:
+            return
+        if "wgu_il" not in self.layers[0]:
+            raise ValueError("prefill needs the fused gate|up layout (ResidentModel layouts 'fused' or 'both')")
+        nbytes = _lib.raw("lt_q8_tiles_bytes")
+        names = ("wqkv", "wo", "wgu_il", "wdown")
+        plan = []
+        total = 0
+        for L in self.layers:
+            for k in names:
+                W = L[k]
+                n = int(nbytes(W.N, W.K))
+                plan.append((L, k, W, total, n))
+                total += (n + 255) // 256 * 256
+        base = self.dev.malloc(total)
+        for L, k, W, off, n in plan:
+            t = DevTensor(base + off, (n,), np.uint8, owns=False, dev=self.dev)
+            call("lt_q8_tiles", self.dev.handle, W.t.vp, t.vp, W.N, W.K)
+            L[k + "_t"] = Q8Weight(None, W.K, t=t, N=W.N)
+        self.tiles = base
+
+    def free(self) -> None:
+        if self.tiles is not None:
+            self.dev.free(self.tiles)
+            self.tiles = None
+        self.arena.free()
+
+
+class DecodePlan:
+    """Fixed device buffers and the launch sequence of one decode token."""
+
+    def __init__(self, model: ResidentModel, profile: Profile = PRODUCTION_PROFILE,
+                 max_ctx: int | None = None, hist_cap: int = 4096, host_embed: bool = False):
+        """host_embed: the step reads its input row from resid_in, written by the host before
+        each step (set_embedding), as the reference's replay does with its fp32 host
+        embedding (dev_residency.py:1371-1377, 1769-1772); otherwise the step gathers the
+        row of the device token from the Q8_0 token_embd."""
+        assert_certified_composition(profile)
+        self.host_embed = bool(host_embed)
+        need = "fused" if profile.fused_step else "per_op"
+        if model.layouts not in (need, "both"):
+            raise ValueError(f"DecodePlan: profile needs the {need!r} gate|up layout, model has {model.layouts!r}")
+        self.model, self.cfg, self.profile = model, model.cfg, profile
+        self.dev = model.dev
+        cfg = self.cfg
+        E, F, hd = cfg.n_embd, cfg.n_ff, cfg.head_dim
+        self.max_ctx = int(max_ctx or cfg.max_ctx)
+        kmax = max(E, F, cfg.q_dim)
+        D = self.dev
+        self.tok = DevTensor.empty((1,), np.int32, D)
+        self.err = DevTensor.empty((1,), np.int32, D)
+        self.hist = DevTensor.empty((hist_cap,), np.int32, D)
+        self.hist_count = DevTensor.empty((1,), np.int32, D)
+        self.hist_cap = hist_cap
+        self.lens = DevTensor.empty((cfg.n_layers,), np.int32, D)
+        self.resid_in = DevTensor.empty((E,), np.float32, D)
+        self.carry = DevTensor.empty((E,), np.float32, D)
+        self.xres = DevTensor.empty((E,), np.float32, D)
+        self.h = DevTensor.empty((E,), np.float32, D)
+        self.qkv = DevTensor.empty((cfg.n_qkv,), np.float32, D)
+        self.att = DevTensor.empty((cfg.q_dim,), np.float32, D)
+        self.gu = DevTensor.empty((2 * F,), np.float32, D)
+        self.v = DevTensor.empty((F,), np.float32, D)
+        self.logits = DevTensor.empty((cfg.vocab,), np.float32, D)
+        self.xq = DevTensor.empty((kmax,), np.int8, D)
+        self.xd = DevTensor.empty((kmax // 32,), np.uint16, D)
+        ws_n = max(_lib.raw("lt_argmax_workspace_size")(), _lib.raw("lt_q8_gemv_argmax_workspace_size")(cfg.vocab))
+        self.am_ws = DevTensor.empty((ws_n,), np.uint8, D)
+        aw = _lib.raw("lt_attn_workspace_size")(1, cfg.n_head, hd, profile.attn_nsplit)
+        self.attn_ws = DevTensor.empty((aw,), np.uint8, D) if aw else None
+        self.caches = [KVCache(self.max_ctx, cfg.n_head_kv, hd, profile.kv_dtype,
+                                     len_ptr=self.lens.ptr + 4 * il, dev=D)
+                       for il in range(cfg.n_layers)]
+        self.scale = float(hd ** -0.5)
+        self._prefill: PrefillBuffers | None = None
+        self.reset()
+
+    def prefill_buffers(self, T: int) -> "PrefillBuffers":
+        if self._prefill is None or self._prefill.T < T:
+            if self._prefill is not None:
+                self.dev.sync()
+                self._prefill.free()
+            self._prefill = PrefillBuffers(self, max(T, 32))
+        return self._prefill
+
+    # -- state --------------------------------------------------------------------
+    def reset(self) -> None:
+        """Empty caches (length 0), zero token history."""
+        self.dev.h2d(self.lens.ptr, np.zeros(self.cfg.n_layers, np.int32))
+        for c in self.caches:
+            c.length = 0
+        self.dev.h2d(self.hist_count.ptr, np.zeros(1, np.int32))
+        self.dev.h2d(self.err.ptr, np.zeros(1, np.int32))
+
+    def set_token(self, tok: int) -> None:
+        self.dev.h2d(self.tok.ptr, np.array([tok], np.int32))
+
+    def set_embedding(self, row: np.ndarray) -> None:
+        """The next step's input row (host_embed plans), fp32 [n_embd]."""
+        r = np.ascontiguousarray(row, np.float32).reshape(-1)
+        if r.size != self.cfg.n_embd:
+            raise ValueError(f"embedding row of {r.size} values, expected {self.cfg.n_embd}")
+        self.dev.h2d(self.resid_in.ptr, r)
+
+    def read_token(self) -> int:
+        out = np.zeros(1, np.int32)
+        self.dev.d2h(out, self.tok.ptr)
+        return int(out[0])
+
+    def read_logits(self) -> np.ndarray:
+        return self.logits.to_host()
+
+    def history_count(self) -> int:
+        out = np.zeros(1, np.int32)
+        self.dev.d2h(out, self.hist_count.ptr)
+        return int(out[0])
+
+    def history(self) -> list[int]:
+        n = self.history_count()
+        out = np.zeros(self.hist_cap, np.int32)
+        self.dev.d2h(out, self.hist.ptr)
+        return [int(t) for t in out[:n]]
+
+    def lengths(self) -> np.ndarray:
+        out = np.zeros(self.cfg.n_layers, np.int32)
+        self.dev.sync()
+        return self.dev.d2h(out, self.lens.ptr)
+
+    # -- the step ----------------------------------------------------------------
+    def enqueue_step(self) -> None:
+        """Launch one decode token (fused or per-op, as the profile says)."""
+        if self.profile.fused_step:
+            self._enqueue_fused()
+        else:
+            self._enqueue_per_op()
+
+    def _enqueue_fused(self) -> None:
+        """Five launches per layer (lt_fused.hip), then the vocab GEMV with its argmax:
+        the same arithmetic as _enqueue_per_op, bit for bit.
+          QKV   rmsnorm -> quant -> GEMV + bias        (layer 0: from the embedding of tok)
+          attn  RoPE -> KV append -> attention -> quant (split-K: partials, then a merge launch)
+          O     GEMV + x, length += 1
+          FFN1  rmsnorm -> quant -> gate|up GEMV -> SiLU(g)*u -> quant
+          FFN2  down GEMV + xres"""
+        cfg, m, p = self.cfg, self.model, self.profile
+        h = self.dev.handle
+        E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
+        eps = ctypes.c_float(cfg.norm_eps)
+        ws, ws_n = _vp(self.attn_ws), (self.attn_ws.nbytes if self.attn_ws is not None else 0)
+        for il, L in enumerate(m.layers):
+            cache = self.caches[il]
+            x = self.resid_in if il == 0 else self.carry
+            if il == 0 and not self.host_embed:
+                call("lt_q8_gemv_embed_rms", h, m.tok_embd.t.vp, self.tok.vp, cfg.vocab, self.resid_in.vp,
+                     self.err.vp, L["attn_norm"].vp, eps, L["wqkv"].t.vp, _vp(L["bqkv"]), self.qkv.vp,
+                     cfg.n_qkv, E)
+            else:
+                call("lt_q8_gemv_rms", h, x.vp, L["attn_norm"].vp, eps, L["wqkv"].t.vp, _vp(L["bqkv"]),
+                     self.qkv.vp, cfg.n_qkv, E)
+            call("lt_attn_step", h, self.qkv.vp, m.freqs.vp, cache.k.vp, cache.v.vp, _vp(cache.len_ptr),
+                 None, self.xq.vp, self.xd.vp, nh, nkv, hd, ctypes.c_float(self.scale), cache.max_seq,
+                 p.attn_nsplit, p.kv_dtype, ws, ws_n)
+            call("lt_q8_gemv_attn_out", h, self.xq.vp, self.xd.vp, None, 0, 1, nh, hd, L["wo"].t.vp,
+                 x.vp, self.xres.vp, E, cfg.q_dim, _vp(cache.len_ptr), cache.max_seq)
+            call("lt_q8_gemv_rms_silu", h, self.xres.vp, L["ffn_norm"].vp, eps, L["wgu_il"].t.vp, self.xq.vp,
+                 self.xd.vp, F, E)
+            call("lt_q8_gemv", h, L["wdown"].t.vp, self.xq.vp, self.xd.vp, self.xres.vp, self.carry.vp, E, F)
+        call("lt_q8_gemv_rms_argmax", h, self.carry.vp, m.output_norm.vp, eps, m.output.t.vp, self.logits.vp,
+             cfg.vocab, E, self.tok.vp, self.hist.vp, self.hist_count.vp, self.hist_cap,
+             self.am_ws.vp, self.am_ws.nbytes)
+
+    def _enqueue_per_op(self) -> None:
+        """Launch one token: embed(tok) -> layers -> logits -> argmax -> tok.
+        The launch order is forward_pass_resident's fully-device branch
+        (bpd/lib/dev_residency.py:1365-1477) followed by _compute_folded_logits (:1596-1623)
+        and the device argmax of replay_token (:1795-1818)."""
+        cfg, m, p = self.cfg, self.model, self.profile
+        h = self.dev.handle
+        E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
+        eps = ctypes.c_float(cfg.norm_eps)
+        if not self.host_embed:
+            call("lt_embed_q8", h, m.tok_embd.t.vp, self.tok.vp, self.resid_in.vp, E, cfg.vocab, self.err.vp)
+        x = self.resid_in
+        for il, L in enumerate(m.layers):
+            cache = self.caches[il]
+            self._rms_quant(x, L["attn_norm"], E, eps)
+            q8_gemv_into(L["wqkv"], self.xq, self.xd, self.qkv, L["bqkv"])
+            call("lt_rope_qk", h, self.qkv.vp, _vp(cache.len_ptr), nh + nkv, hd, m.freqs.vp)
+            k = self.qkv.view(cfg.q_dim, (cfg.kv_dim,))
+            v = self.qkv.view(cfg.q_dim + cfg.kv_dim, (cfg.kv_dim,))
+            cache.append_at_len_incr(k, v)
+            call("lt_attn_decode", h, self.qkv.vp, cache.k.vp, cache.v.vp, _vp(cache.len_ptr),
+                 self.att.vp, 1, nh, nkv, hd, ctypes.c_float(self.scale), cache.max_seq,
+                 p.attn_nsplit, p.kv_dtype, _vp(self.attn_ws),
+                 self.attn_ws.nbytes if self.attn_ws is not None else 0)
+            quant_q8_into(self.att, self.xq, self.xd, cfg.q_dim)
+            q8_gemv_into(L["wo"], self.xq, self.xd, self.xres, x)
+            self._rms_quant(self.xres, L["ffn_norm"], E, eps)
+            q8_gemv_into(L["wgu"], self.xq, self.xd, self.gu)
+            g = self.gu.view(0, (F,))
+            u = self.gu.view(F, (F,))
+            call("lt_silu_mul_quant", h, g.vp, u.vp, self.xq.vp, self.xd.vp, F)
+            q8_gemv_into(L["wdown"], self.xq, self.xd, self.carry, self.xres)
+            x = self.carry
+        self._rms_quant(x, m.output_norm, E, eps)
+        call("lt_q8_gemv", h, m.output.t.vp, self.xq.vp, self.xd.vp, None, self.logits.vp,
+             m.output.N, m.output.K)
+        call("lt_argmax_record", h, self.logits.vp, cfg.vocab, self.tok.vp, self.hist.vp,
+             self.hist_count.vp, self.hist_cap, self.am_ws.vp, self.am_ws.nbytes)
+
+    def _rms_quant(self, x: DevTensor, w: DevTensor, E: int, eps) -> None:
+        h = self.dev.handle
+        if self.profile.fused_rms_quant:
+            call("lt_rmsnorm_quant", h, x.vp, w.vp, self.xq.vp, self.xd.vp, E, eps)
+        else:
+            call("lt_rmsnorm", h, x.vp, w.vp, self.h.vp, 1, E, eps)
+            call("lt_quant_q8", h, self.h.vp, self.xq.vp, self.xd.vp, E)
+
+    def check_room(self, n: int = 1) -> None:
+        """Refuse n more positions when the KV caches cannot hold them: past max_ctx the step
+        kernels would attend over an empty context and drop the new row."""
+        if self.caches[0].length + n > self.max_ctx:
+            raise ValueError(f"KV cache full: {self.caches[0].length} + {n} positions exceed "
+                             f"max_ctx {self.max_ctx}")
+
+    def step(self, tok: int | None = None, embedding: np.ndarray | None = None) -> None:
+        """Eager step (tok=None: use the device token left by the previous argmax).  A
+        host_embed plan takes the token's input row as `embedding`."""
+        self.check_room(1)
+        if self.host_embed:
+            if embedding is None:
+                raise ValueError("a host_embed plan steps on a host embedding row")
+            self.set_embedding(embedding)
+        if tok is not None:
+            self.set_token(tok)
+        self.enqueue_step()
+        for c in self.caches:
+            c.length += 1
+
+    def free(self) -> None:
+        if self._prefill is not None:
+            self._prefill.free()
+        for c in self.caches:
+            c.free()
+        for t in (self.tok, self.err, self.hist, self.hist_count, self.lens, self.resid_in, self.carry,
+                  self.xres, self.h, self.qkv, self.att, self.gu, self.v, self.logits, self.xq, self.xd,
+                  self.am_ws, self.attn_ws):
+            if t is not None:
+                t.free()
+
+
+class PrefillBuffers:
+    """Device buffers of a batched prefill of up to T tokens."""
+
+    def __init__(self, plan: "DecodePlan", T: int):
+        cfg, D = plan.cfg, plan.dev
+        E, F = cfg.n_embd, cfg.n_ff
+        kmax = max(E, F, cfg.q_dim)
+        self.T = T
+        self.toks = DevTensor.empty((T,), np.int32, D)
+        self.x = DevTensor.empty((T, E), np.float32, D)
+        self.xres = DevTensor.empty((T, E), np.float32, D)
+        self.qkv = DevTensor.empty((T, cfg.n_qkv), np.float32, D)
+        self.att = DevTensor.empty((T, cfg.q_dim), np.float32, D)
+        self.v = DevTensor.empty((T, F), np.float32, D)
+        self.xq = DevTensor.empty((T * kmax,), np.int8, D)
+        self.xd = DevTensor.empty((T * kmax // 32,), np.uint16, D)
+        aw = _lib.raw("lt_attn_workspace_size")(T, cfg.n_head, cfg.head_dim, plan.profile.attn_nsplit)
+        self.ws = DevTensor.empty((aw,), np.uint8, D) if aw else None
+
+    def free(self) -> None:
+        for t in (self.toks, self.x, self.xres, self.qkv, self.att, self.v, self.xq, self.xd, self.ws):
+            if t is not None:
+                t.free()
+
+
+def forward_prefill(plan: DecodePlan, tokens, embeddings: np.ndarray | None = None) -> None:
+    """Batched prefill of a prompt: every linear layer runs once over all T tokens through
+    the int8-MFMA Q8_0 GEMM on the coalesced layouts (tile-major weight copies from
+    ResidentModel.prefill_tiles, block-major activation quants; lt_q8_gemm_t), with batched
+    RMSNorm/RoPE/KV append and causal attention.  It is device-uniform with the single-token
+    path the reference uses (bpd/lib/dev_residency.py:1338-1356): the KV cache, the last
+    token's logits and the greedy token it leaves on the device are bit-identical to
+    forward_tokens's.  A host_embed plan takes the prompt's input rows as `embeddings`
+    (fp32 [T, n_embd])."""
+    toks = np.asarray([int(t) for t in np.asarray(tokens).reshape(-1)], np.int32)
+    T = int(toks.size)
+    if T == 0:
+        return
+    cfg, m, p, D = plan.cfg, plan.model, plan.profile, plan.dev
+    if plan.caches[0].length + T > plan.max_ctx:
+        raise ValueError(f"prefill of {T} tokens overflows the {plan.max_ctx}-position KV cache")
+    if "wgu_il" not in m.layers[0]:
+        raise ValueError("forward_prefill needs the fused gate|up layout (ResidentModel layouts 'fused' or 'both')")
+    # every layer's length sits in the plan's one array, so all of them advance in one launch
+    # after the last layer's attention (each layer's attention reads only its own)
+    if not all(c.len_ptr == plan.lens.ptr + 4 * il and c.max_seq == plan.max_ctx
+               for il, c in enumerate(plan.caches)):
+        raise ValueError("forward_prefill needs the DecodePlan's joint length array")
+    m.prefill_tiles()
+    B = plan.prefill_buffers(T)
+    h = D.handle
+    E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
+    QD, KD, NQ = cfg.q_dim, cfg.kv_dim, cfg.n_qkv
+    eps = ctypes.c_float(cfg.norm_eps)
+    if plan.host_embed:
+        if embeddings is None:
+            raise ValueError("a host_embed plan prefills from host embedding rows")
+        X = np.ascontiguousarray(embeddings, np.float32).reshape(-1)
+        if X.size != T * E:
+            raise ValueError(f"embeddings hold {X.size} values, expected {T} x {E}")
+        D.h2d(B.x.ptr, X)
+    else:
+        D.h2d(B.toks.ptr, toks)
+        call("lt_embed_q8_batch", h, m.tok_embd.t.vp, B.toks.vp, B.x.vp, T, E, cfg.vocab, plan.err.vp)
+    ws, ws_n = _vp(B.ws), (B.ws.nbytes if B.ws is not None else 0)
+    for il, L in enumerate(m.layers):
+        cache = plan.caches[il]
+        lp = _vp(cache.len_ptr)
+        call("lt_rmsnorm_quant_bm", h, B.x.vp, L["attn_norm"].vp, B.xq.vp, B.xd.vp, T, E, eps)
+        call("lt_q8_gemm_t", h, L["wqkv_t"].t.vp, B.xq.vp, B.xd.vp, _vp(L["bqkv"]), None, B.qkv.vp, T, NQ, E)
+        call("lt_rope_append_batch", h, B.qkv.vp, T, NQ, lp, nh, nkv, hd, m.freqs.vp, cache.k.vp, cache.v.vp,
+             cache.max_seq, p.kv_dtype)
+        call("lt_attn_prefill", h, B.qkv.vp, NQ, cache.k.vp, cache.v.vp, lp, B.att.vp, T, nh, nkv, hd,
+             ctypes.c_float(plan.scale), cache.max_seq, p.attn_nsplit, p.kv_dtype, ws, ws_n)
+        call("lt_quant_q8_bm", h, B.att.vp, B.xq.vp, B.xd.vp, T, QD)
+        call("lt_q8_gemm_t", h, L["wo_t"].t.vp, B.xq.vp, B.xd.vp, None, B.x.vp, B.xres.vp, T, E, QD)
+        call("lt_rmsnorm_quant_bm", h, B.xres.vp, L["ffn_norm"].vp, B.xq.vp, B.xd.vp, T, E, eps)
+        call("lt_q8_gemm_silu_t", h, L["wgu_il_t"].t.vp, B.xq.vp, B.xd.vp, B.v.vp, T, F, E)
+        call("lt_quant_q8_bm", h, B.v.vp, B.xq.vp, B.xd.vp, T, F)
+        call("lt_q8_gemm_t", h, L["wdown_t"].t.vp, B.xq.vp, B.xd.vp, None, B.xres.vp, B.x.vp, T, E, F)
+    call("lt_len_add_n", h, _vp(plan.lens.ptr), len(m.layers), T, plan.max_ctx)
+    for cache in plan.caches:   # the host mirror advances with the device lengths
+        cache.length += T
+    # the last token's logits and greedy token, as the decode step computes them
+    D.d2d(plan.carry.ptr, B.x.ptr + (T - 1) * E * 4, E * 4)
+    call("lt_q8_gemv_rms_argmax", h, plan.carry.vp, m.output_norm.vp, eps, m.output.t.vp, plan.logits.vp,
+         cfg.vocab, E, plan.tok.vp, None, None, 0, plan.am_ws.vp, plan.am_ws.nbytes)
+
+
+def forward_tokens(plan: DecodePlan, tokens, embeddings: np.ndarray | None = None) -> np.ndarray:
+    """Feed tokens one at a time through the single-token device path (the reference's
+    device-uniform prefill, dev_residency.py:1338-1356); return the last token's logits.
+    A host_embed plan takes the tokens' input rows as `embeddings` [T, n_embd]."""
+    toks = [int(t) for t in np.asarray(tokens).reshape(-1)]
+    if plan.host_embed:
+        if embeddings is None:
+            raise ValueError("a host_embed plan steps on host embedding rows")
+        X = np.asarray(embeddings, np.float32).reshape(len(toks), -1)
+        for t, row in zip(toks, X):
+            plan.step(t, row)
+    else:
+        for t in toks:
+            plan.step(t)
+    return plan.read_logits()
+
+
+class StepGraph:
+    """Capture one decode step into a HIP graph and replay it per token
+    (reference GraphRunner, bpd/lib/dev_residency.py:1626-1818)."""
+
+    def __init__(self, plan: DecodePlan):
+        self.plan = plan
+        self.dev = plan.dev
+        self.graph = ctypes.c_void_p()
+        self.captured = False
+
+    def seed(self, prompt, batched: bool = False, embeddings: np.ndarray | None = None) -> np.ndarray:
+        """Eager prefill over the prompt (fixed buffers, all kernels loaded); returns the
+        last prompt token's logits.  The device token then holds the first greedy token.
+        batched=True runs forward_prefill (the int8-MFMA GEMM path; bit-identical)."""
+        if batched:
+            forward_prefill(self.plan, prompt, embeddings)
+            logits = self.plan.read_logits()
+        else:
+            logits = forward_tokens(self.plan, prompt, embeddings)
+        self.dev.sync()
+        return logits
+
+    def capture(self) -> None:
+        if self.captured:
+            raise RuntimeError("StepGraph.capture: already captured")
+        call("lt_graph_begin", self.dev.handle)
+        try:
+            self.plan.enqueue_step()
+        except Exception:
+            g = ctypes.c_void_p()
+            _lib.raw("lt_graph_end")(self.dev.handle, ctypes.byref(g))
+            if g.value:
+                _lib.raw("lt_graph_free")(g)
+            raise
+        call("lt_graph_end", self.dev.handle, ctypes.byref(self.graph))
+        self.captured = True
+
+    def _launch(self) -> None:
+        if not self.captured:
+            raise RuntimeError("call capture() before replay")
+        self.plan.check_room(1)
+        call("lt_graph_launch", self.dev.handle, self.graph)
+        for c in self.plan.caches:
+            c.length += 1
+
+    def _set_input(self, tok, embedding) -> None:
+        if self.plan.host_embed:
+            if embedding is None:
+                raise ValueError("a host_embed plan replays on a host embedding row")
+            self.plan.set_embedding(embedding)
+        if tok is not None:
+            self.plan.set_token(tok)
+
+    def replay_logits(self, tok: int, embedding: np.ndarray | None = None) -> np.ndarray:
+        self._set_input(tok, embedding)
+        self._launch()
+        return self.plan.read_logits()
+
+    def replay_token(self, tok: int | None = None, embedding: np.ndarray | None = None) -> int:
+        """One graph replay; returns the greedy next token (4 bytes cross to the host)."""
+        self._set_input(tok, embedding)
+        self._launch()
+        return self.plan.read_token()
+
+    def replay_tokens(self, n: int) -> list[int]:
+        """n back-to-back replays continuing from the device token; the host reads the n
+        generated ids once at the end from the device history.  Same tokens as n calls of
+        replay_token()."""
+        if self.plan.host_embed:
+            raise ValueError("replay_tokens feeds each argmax back on the device; a host_embed "
+                             "plan takes every input row from the host (replay_token per token)")
+        start = self.plan.history_count()
+        if start + n > self.plan.hist_cap:
+            raise ValueError(f"token history capacity {self.plan.hist_cap} exceeded")
+        self.plan.check_room(n)
+        for _ in range(n):
+            self._launch()
+        return self.plan.history()[start:start + n]
+
+    def free(self) -> None:
+        if self.captured:
+            call("lt_graph_free", self.graph)
+            self.captured = False
+
+
+def generate(model, input_ids, n_tokens: int, profile: Profile = PRODUCTION_PROFILE,
+             batched_prefill: bool = True, max_ctx: int | None = None) -> list[int]:
+    """Greedy generation of n_tokens after input_ids, the reference's decode loop
+    (decode_fact.py:54-111 semantics; GraphRunner seed -> capture -> replay,
+    dev_residency.py:1626-1818): the prompt is prefilled, the first token is its greedy
+    argmax, and every further token comes from one replay of the captured step.
+
+    `model` is a ResidentModel or the path of a Q8_0 GGUF file (loaded and freed here)."""
+    own = not isinstance(model, ResidentModel)
+    m = ResidentModel.from_gguf(model, max_ctx=max_ctx or 1024) if own else model
+    plan = gr = None
+    try:
+        ids = [int(t) for t in np.asarray(input_ids).reshape(-1)]
+        if not ids:
+            raise ValueError("generate: empty prompt")
+        if n_tokens < 1:
+            return []
+        # the history records one entry per token through the step's argmax: the prompt's
+        # (when it is fed token by token) and every generated one
+        plan = DecodePlan(m, profile, max_ctx=max_ctx, hist_cap=len(ids) + n_tokens)
+        if len(ids) + n_tokens - 1 > plan.max_ctx:
+            raise ValueError(f"generate: {len(ids)} prompt + {n_tokens - 1} decode positions exceed "
+                             f"the {plan.max_ctx}-position KV cache")
+        gr = StepGraph(plan)
+        gr.seed(ids, batched=batched_prefill and "wgu_il" in m.layers[0])
+        out = [plan.read_token()]
+        if n_tokens > 1:
+            gr.capture()
+            out += gr.replay_tokens(n_tokens - 1)
+        return out
+    finally:
+        if gr is not None:
+            gr.free()
+        if plan is not None:
+            plan.free()
+        if own:
+            m.free()

@@ -26,7 +26,7 @@ def main(argv=None) -> int:
                     help="prefill one token at a time instead of the batched GEMM (same bits)")
     a = ap.parse_args(argv)
 
-    from . import dev_residency as dr
+    from . import engine as dr
     ids = [int(t) for t in a.ids.split(",") if t.strip()]
     t0 = time.perf_counter()
     model = dr.ResidentModel.from_gguf(a.model, max_ctx=a.max_ctx)

@@ -29,7 +29,7 @@ def _gpu_available() -> bool:
 def gpu():
     """The shared device context; fails (not skips) when the HIP library is missing, so a
     GPU run can never pass on a silent fallback."""
-    from llamatov_amd import dev_residency as dr
+    from llamatov_amd import engine as dr
     if not _gpu_available():
         pytest.fail("no usable gfx950 device / libllamatov_hip.so for a gpu-marked test")
     return dr.get_device()

@@ -72,26 +72,26 @@ def test_oracle_decode_fixture(oracle):
 # ---- GPU: the kernels match the fixtures --------------------------------------------
 @pytest.mark.gpu
 def test_gpu_matches_op_fixtures(gpu):
-    from llamatov_amd import dev_residency as dr
+    from llamatov_amd import engine as dr
     from llamatov_amd._lib import LT_KV_F16, LT_KV_F32, call, raw
     up = lambda a: dr.DevTensor.from_host(np.ascontiguousarray(a))
     print("[gpu-case] golden op fixtures", flush=True)
     g = load("gemv_canonical_64x256.npz")
     W = dr.Q8Weight(g["W"], 256)
     y = dr.DevTensor.empty((64,), np.float32)
-    dr.q8_gemv_dev(W, up(g["xq"]), up(g["xd"]), y)
+    dr.q8_gemv_into(W, up(g["xq"]), up(g["xd"]), y)
     assert same_bits(y.to_host(), g["y"])
-    dr.q8_gemv_dev(W, up(g["xq"]), up(g["xd"]), y, up(g["resid"]))
+    dr.q8_gemv_into(W, up(g["xq"]), up(g["xd"]), y, up(g["resid"]))
     assert same_bits(y.to_host(), g["y_resid"])
 
     q = load("quant_q8_896.npz")
     dq, dd = dr.DevTensor.empty((896,), np.int8), dr.DevTensor.empty((28,), np.uint16)
-    dr.quant_q8_dev(up(q["x"]), dq, dd, 896)
+    dr.quant_q8_into(up(q["x"]), dq, dd, 896)
     assert np.array_equal(dq.to_host(), q["xq"]) and np.array_equal(dd.to_host(), q["xd"])
 
     r = load("rmsnorm_896.npz")
     ry = dr.DevTensor.empty((896,), np.float32)
-    dr.rms_norm_dev(up(r["x"]), up(r["w"]), float(r["eps"]), ry)
+    dr.rms_norm_into(up(r["x"]), up(r["w"]), float(r["eps"]), ry)
     assert same_bits(ry.to_host(), r["y"])
 
     p = load("rope_hd64.npz")
@@ -116,14 +116,14 @@ def test_gpu_matches_op_fixtures(gpu):
 @pytest.mark.gpu
 @pytest.mark.parametrize("kv", ["f32", "f16_split4"])
 def test_gpu_matches_decode_fixture(gpu, kv):
-    from llamatov_amd import dev_residency as dr
+    from llamatov_amd import engine as dr
     from llamatov_amd._lib import LT_KV_F16, LT_KV_F32
     print(f"[gpu-case] golden decode fixture {kv}", flush=True)
     g = load("decode_tiny.npz")
     w = M.synth_weights(M.TINY, seed=99)
     prof = dr.Profile() if kv == "f32" else dr.Profile(kv_dtype=LT_KV_F16, attn_nsplit=4)
     plan = dr.DecodePlan(dr.ResidentModel(M.TINY, w), prof)
-    gr = dr.GraphRunner(plan)
+    gr = dr.StepGraph(plan)
     gr.seed(g["prompt"].tolist())
     first = plan.read_token()
     gr.capture()

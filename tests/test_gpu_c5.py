@@ -13,7 +13,7 @@ hidden 4096, FFN 14336, 32 Q / 8 KV heads, head_dim 128, vocab 128256, untied he
 import numpy as np
 import pytest
 
-from llamatov_amd import dev_residency as dr
+from llamatov_amd import engine as dr
 from llamatov_amd import model as M
 from llamatov_amd._lib import LT_KV_F16
 
@@ -58,7 +58,7 @@ def test_c5_prefill_512_equals_stepwise(gpu, c5_model):
     assert list(plan.lengths()) == [N_PREFILL] * cfg.n_layers
     case("C5 token-by-token 512")
     plan.reset()
-    la = dr.forward_pass_resident(plan, prompt)
+    la = dr.forward_tokens(plan, prompt)
     assert np.array_equal(bits(la), bits(lb))
     assert plan.read_token() == tb == int(np.argmax(la))
     for key, rows in _kv(plan, N_PREFILL, layers).items():
@@ -74,7 +74,7 @@ def test_c5_graph_replay_equals_eager_256(gpu, c5_model):
     case("C5 prefill + 256 graph replays")
     dr.forward_prefill(plan, prompt)
     first = plan.read_token()
-    gr = dr.GraphRunner(plan)
+    gr = dr.StepGraph(plan)
     gr.capture()
     seq_g = [first] + gr.replay_tokens(N_DECODE - 1)
     lg = plan.read_logits().copy()
@@ -113,7 +113,7 @@ def test_c5_truncated_matches_oracle(gpu, oracle):
     for t in prompt:
         exp_logits = orc2.step(t)
     assert np.array_equal(bits(plan.read_logits()), bits(exp_logits))
-    gr = dr.GraphRunner(plan)
+    gr = dr.StepGraph(plan)
     gr.capture()
     for _ in range(4):
         t = got[-1]

@@ -5,7 +5,7 @@ BASELINE configuration 2 geometry."""
 import numpy as np
 import pytest
 
-from llamatov_amd import dev_residency as dr
+from llamatov_amd import engine as dr
 from llamatov_amd import model as M
 from llamatov_amd._lib import LT_KV_F16, LT_KV_F32
 
@@ -77,8 +77,8 @@ def test_graph_replay_equals_eager(gpu, nsplit):
     prof = dr.Profile(kv_dtype=LT_KV_F16, attn_nsplit=nsplit)
     eager = dr.DecodePlan(m, prof)
     graph = dr.DecodePlan(m, prof)
-    dr.forward_pass_resident(eager, prompt)
-    gr = dr.GraphRunner(graph)
+    dr.forward_tokens(eager, prompt)
+    gr = dr.StepGraph(graph)
     gr.seed(prompt)
     gr.capture()
     for i in range(12):
@@ -113,13 +113,13 @@ def test_prefill_kv_equals_incremental(gpu):
     m = resident(cfg, gpu)
     prompt = M.random_prompt(cfg, 4, seed=9)
     inc = dr.DecodePlan(m)
-    dr.forward_pass_resident(inc, prompt)
+    dr.forward_tokens(inc, prompt)
     seq = list(prompt)
     for _ in range(10):
         seq.append(inc.read_token())
         inc.step(seq[-1])
     fresh = dr.DecodePlan(m)
-    lg = dr.forward_pass_resident(fresh, seq)
+    lg = dr.forward_tokens(fresh, seq)
     assert bitexact(lg, inc.read_logits())
     for il in range(cfg.n_layers):
         assert np.array_equal(fresh.caches[il].rows_host("k", len(seq)), inc.caches[il].rows_host("k", len(seq)))
@@ -143,7 +143,7 @@ def test_greedy_tokens_identical(gpu, oracle, cfg_name, n_prompt, n_gen, kv_dtyp
     orc = oracle.OracleModel(cfg, weights(cfg), kv_f16=kv_dtype == LT_KV_F16)
     exp, margins = orc.generate(prompt, n_gen)
     plan = dr.DecodePlan(resident(cfg, gpu), dr.Profile(kv_dtype=kv_dtype, fused_step=step == "fused"))
-    gr = dr.GraphRunner(plan)
+    gr = dr.StepGraph(plan)
     gr.seed(prompt)
     first = plan.read_token()
     gr.capture()

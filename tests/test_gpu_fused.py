@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 from llamatov_amd import _lib
-from llamatov_amd import dev_residency as dr
+from llamatov_amd import engine as dr
 from llamatov_amd import model as M
 from llamatov_amd import q8 as hq8
 from llamatov_amd._lib import LT_KV_F16, LT_KV_F32, call

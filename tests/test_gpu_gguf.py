@@ -10,7 +10,7 @@ import os
 import numpy as np
 import pytest
 
-from llamatov_amd import dev_residency as dr
+from llamatov_amd import engine as dr
 from llamatov_amd import gguf as G
 from llamatov_amd import model as M
 from llamatov_amd._lib import LT_KV_F16, LT_KV_F32

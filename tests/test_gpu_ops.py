@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 from llamatov_amd import _lib
-from llamatov_amd import dev_residency as dr
+from llamatov_amd import engine as dr
 from llamatov_amd import q8 as hq8
 from llamatov_amd._lib import LT_KV_F16, LT_KV_F32, call
 
@@ -52,7 +52,7 @@ def test_quant_q8(gpu, oracle, K):
         x[32:64] = np.float32(1.0) * np.arange(-16, 16, dtype=np.float32) / np.float32(127 / 16.5)
     xq, xd = oracle.quant_q8(x)
     dx, dq, dd = up(x), empty((K,), np.int8), empty((K // 32,), np.uint16)
-    dr.quant_q8_dev(dx, dq, dd, K)
+    dr.quant_q8_into(dx, dq, dd, K)
     assert_bitexact(dq.to_host(), xq, "xq")
     assert_bitexact(dd.to_host(), xd, "xd")
 
@@ -79,7 +79,7 @@ def test_rmsnorm_and_fused_quant(gpu, oracle, N, eps):
     w = (0.5 * rng.standard_normal(N) + 1.0).astype(np.float32)
     exp = oracle.rmsnorm(x, w, eps)
     dx, dw, dy = up(x), up(w), empty((N,), np.float32)
-    dr.rms_norm_dev(dx, dw, eps, dy)
+    dr.rms_norm_into(dx, dw, eps, dy)
     assert_bitexact(dy.to_host(), exp, "rmsnorm")
     if N % 32 == 0:
         xq, xd = oracle.quant_q8(exp)
@@ -95,7 +95,7 @@ def test_rmsnorm_multirow(gpu, oracle):
     x = rng.standard_normal((5, 896)).astype(np.float32)
     w = rng.standard_normal(896).astype(np.float32)
     dy = empty((5, 896), np.float32)
-    dr.rms_norm_dev(up(x), up(w), 1e-6, dy)
+    dr.rms_norm_into(up(x), up(w), 1e-6, dy)
     exp = np.stack([oracle.rmsnorm(x[i], w, 1e-6) for i in range(5)])
     assert_bitexact(dy.to_host(), exp, "rmsnorm rows")
 
@@ -121,11 +121,11 @@ def test_q8_gemv_bitexact(gpu, oracle, N, K):
     exp = oracle.q8_gemv(W, xq, xd, K)
     dW = dr.Q8Weight(W, K)
     dq, dd, dy = up(xq), up(xd), empty((N,), np.float32)
-    dr.q8_gemv_dev(dW, dq, dd, dy)
+    dr.q8_gemv_into(dW, dq, dd, dy)
     assert_bitexact(dy.to_host(), exp, f"gemv {N}x{K}")
     # addres / bias epilogue: one fp32 add at the store
     r = rng.standard_normal(N).astype(np.float32)
-    dr.q8_gemv_dev(dW, dq, dd, dy, up(r))
+    dr.q8_gemv_into(dW, dq, dd, dy, up(r))
     assert_bitexact(dy.to_host(), oracle.q8_gemv(W, xq, xd, K, resid=r), "gemv+resid")
     dW.t.free()
 
@@ -161,7 +161,7 @@ def test_rope_qk(gpu, oracle, hd, nh, nkv, theta):
 def test_kv_append_incr(gpu, kv_dtype):
     case(f"kv_append kv_dtype={kv_dtype}")
     rng = np.random.default_rng(5)
-    cache = dr.DeviceKVCache(8, 2, 64, kv_dtype)
+    cache = dr.KVCache(8, 2, 64, kv_dtype)
     rows = []
     for t in range(9):  # the 9th append hits capacity and must change nothing
         k = rng.standard_normal(128).astype(np.float32)
@@ -298,11 +298,11 @@ def test_argmax_ties(gpu, oracle):
         xx = x.copy()
         if planted:
             xx[list(planted)] = np.float32(50.0)
-        dr.argmax_dev(up(xx), xx.size, out.ptr, ws)
+        dr.argmax_into(up(xx), xx.size, out.ptr, ws)
         assert int(out.to_host()[0]) == oracle.argmax(xx)
     for n in (1, 255, 256, 257, 70000):
         xx = x[:n].copy()
-        dr.argmax_dev(up(xx), n, out.ptr, ws)
+        dr.argmax_into(up(xx), n, out.ptr, ws)
         assert int(out.to_host()[0]) == oracle.argmax(xx)
 
 

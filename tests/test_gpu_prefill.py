@@ -5,7 +5,7 @@ stream bit-identical."""
 import numpy as np
 import pytest
 
-from llamatov_amd import dev_residency as dr
+from llamatov_amd import engine as dr
 from llamatov_amd import model as M
 from llamatov_amd import q8 as hq8
 from llamatov_amd._lib import LT_KV_F16, LT_KV_F32, call
@@ -256,7 +256,7 @@ def test_prefill_equals_stepwise(gpu, oracle, cfg_name, n_prompt, kv_dtype, nspl
     prompt = M.random_prompt(cfg, n_prompt, seed=11)
     a = dr.DecodePlan(model, prof)
     b = dr.DecodePlan(model, prof)
-    la = dr.forward_pass_resident(a, prompt)
+    la = dr.forward_tokens(a, prompt)
     dr.forward_prefill(b, prompt)
     lb = b.read_logits()
     assert np.array_equal(bits(la), bits(lb))
@@ -267,7 +267,7 @@ def test_prefill_equals_stepwise(gpu, oracle, cfg_name, n_prompt, kv_dtype, nspl
             assert np.array_equal(a.caches[il].rows_host(w, n_prompt).view(np.uint8),
                                   b.caches[il].rows_host(w, n_prompt).view(np.uint8)), (il, w)
     # decoding continues identically (graph replay after the batched prefill)
-    gb = dr.GraphRunner(b)
+    gb = dr.StepGraph(b)
     gb.capture()
     seq_b = gb.replay_tokens(6)
     seq_a = []
@@ -312,7 +312,7 @@ def test_prefill_into_non_empty_cache(gpu, oracle, cfg_name, kv_dtype, nsplit):
         b.step()
     dr.forward_prefill(b, C)
     seq += list(C)
-    la = dr.forward_pass_resident(a, seq)
+    la = dr.forward_tokens(a, seq)
     lb = b.read_logits()
     exp = None
     for t in seq:
@@ -341,7 +341,7 @@ def test_capacity_is_refused_on_the_host(gpu):
     dr.forward_prefill(plan, M.random_prompt(cfg, 6, seed=2))
     with pytest.raises(ValueError):
         dr.forward_prefill(plan, [1, 2, 3])
-    gr = dr.GraphRunner(plan)
+    gr = dr.StepGraph(plan)
     gr.capture()
     with pytest.raises(ValueError):
         gr.replay_tokens(3)

@@ -1,0 +1,83 @@
+"""Host-side logic of the reference surface (llamatov_amd.dev_residency, llamatov_run) that
+runs without a GPU: the fp32 -> Q8_0 weight conversion of a reference weight dict, the
+config mapping, the embedding round-trip test that selects host rows, the flag gate."""
+import numpy as np
+import pytest
+
+from llamatov_amd import dev_residency as dr
+from llamatov_amd import model as M
+from llamatov_amd import q8 as hq8
+
+
+def reference_w(cfg, qw):
+    w = {}
+    for name, kind, shape in M.weight_specs(cfg):
+        a = qw[name]
+        if kind == "q8":
+            a = hq8.dequantize_rows(a, shape[1]).T
+        w[name] = np.ascontiguousarray(a, np.float32)
+    return w
+
+
+@pytest.mark.parametrize("cfg", [M.TINY, M.TINY.replace(name="t-untied", tied=False, qkv_bias=False)],
+                         ids=lambda c: c.name)
+def test_reference_weights_convert_to_the_same_blocks(cfg):
+    qw = M.synth_weights(cfg, seed=3)
+    w = reference_w(cfg, qw)
+    mc = dr._engine_cfg(cfg.as_cfg(), w)
+    assert (mc.n_layers, mc.n_embd, mc.n_ff, mc.n_head, mc.n_head_kv, mc.vocab, mc.tied, mc.qkv_bias) == \
+        (cfg.n_layers, cfg.n_embd, cfg.n_ff, cfg.n_head, cfg.n_head_kv, cfg.vocab, cfg.tied, cfg.qkv_bias)
+    ew = dr._engine_weights(w, mc)
+    for name, kind, _ in M.weight_specs(cfg):
+        assert np.array_equal(ew[name], qw[name]), name
+    rows = dr._embedding_rows(w, cfg.n_embd)
+    assert np.array_equal(hq8.dequantize_rows(ew["token_embd.weight"], cfg.n_embd), rows)
+
+
+def test_engine_cfg_refuses_a_decoupled_head_dim():
+    cfg = M.TINY
+    w = reference_w(cfg, M.synth_weights(cfg, seed=3))
+    c = dict(cfg.as_cfg(), head_dim=cfg.head_dim * 2)
+    with pytest.raises(ValueError):
+        dr._engine_cfg(c, w)
+
+
+def test_composition_gate_on_the_host():
+    try:
+        dr.apply_production_profile()
+        dr.assert_certified_composition()
+        dr._QFUSED = True
+        with pytest.raises(RuntimeError):
+            dr.assert_certified_composition()
+        dr.apply_production_profile()
+        dr._DEVICE_ATTN = False
+        with pytest.raises(RuntimeError):
+            dr.assert_certified_composition()
+        dr.apply_production_profile()
+        dr._KV_ELEM_BYTES = 3
+        with pytest.raises(RuntimeError):
+            dr.assert_certified_composition()
+    finally:
+        dr.apply_production_profile()
+        dr._KV_ELEM_BYTES = 4
+    live = dr.attest_profile()
+    assert all(live[k] == v for k, v in dr.PRODUCTION_PROFILE.items())
+
+
+def test_load_model_orientation(tmp_path):
+    from llamatov_amd import gguf
+    from llamatov_amd import llamatov_run as R
+    cfg = M.TINY
+    qw = M.synth_weights(cfg, seed=4)
+    p = tmp_path / "t.gguf"
+    gguf.save_q8_model(p, cfg, qw)
+    c, w = R.load_model(str(p))
+    assert (c["n_layers"], c["n_head"], c["n_head_kv"], c["n_embd"]) == (cfg.n_layers, cfg.n_head,
+                                                                          cfg.n_head_kv, cfg.n_embd)
+    wq = np.asarray(w["blk.0.attn_q.weight"])
+    assert wq.shape == (cfg.n_embd, cfg.q_dim)      # [ne0, ne1] = inputs x outputs
+    assert np.array_equal(wq.T, hq8.dequantize_rows(qw["blk.0.attn_q.weight"], cfg.n_embd))
+    emb = np.asarray(w["token_embd.weight"])
+    assert emb.shape == (cfg.n_embd, cfg.vocab)
+    ew = dr._engine_weights(w, dr._engine_cfg(c, w))
+    assert np.array_equal(ew["token_embd.weight"], qw["token_embd.weight"])

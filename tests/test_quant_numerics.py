@@ -47,13 +47,13 @@ def test_quant_zero_and_infinite_scales(oracle):
 
 @pytest.mark.gpu
 def test_device_quant_special_blocks(gpu, oracle):
-    from llamatov_amd import dev_residency as dr
+    from llamatov_amd import engine as dr
     x = _special_blocks()
     xq, xd = oracle.quant_q8(x)
     dx = dr.DevTensor.from_host(x, gpu)
     dq = dr.DevTensor.empty((x.size,), np.int8, gpu)
     dd = dr.DevTensor.empty((x.size // 32,), np.uint16, gpu)
-    dr.quant_q8_dev(dx, dq, dd, x.size)
+    dr.quant_q8_into(dx, dq, dd, x.size)
     assert np.array_equal(dq.to_host(), xq) and np.array_equal(dd.to_host(), xd)
     for t in (dx, dq, dd):
         t.free()
