@@ -204,6 +204,14 @@ LT_API int lt_q8_gemv_attn_out(lt_ctx* ctx, const int8_t* xq, const uint16_t* xd
 LT_API int lt_q8_gemv_rms_silu(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* Wgu,
                                int8_t* vq, uint16_t* vd, int F, int K);
 
+/* rmsnorm -> quant -> gate|up GEMV -> v = SiLU(g)*u in fp32 (the chain of
+ * lt_q8_gemv_rms_silu without the final quant; the down GEMV quantizes v in its prologue,
+ * lt_q8_gemv_quant).  Wgu holds 2F rows interleaved (row 2j = gate j, row 2j+1 = up j);
+ * v is fp32 [F], each element (g/(1+exp(-g)))*u as k_silu_mul computes it
+ * (bpd/lib/dev_residency.py:545-551, gate|up GEMV :1321-1326).  F % 4 == 0. */
+LT_API int lt_q8_gemv_rms_swiglu(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* Wgu,
+                                 float* v, int F, int K);
+
 /* Final norm -> quant -> vocab GEMV -> greedy argmax (_compute_folded_logits
  * bpd/lib/dev_residency.py:1596-1623 + argmax_dev :1074-1110): writes logits[N], then the
  * index of the maximum (ties to the lowest index) to *out, appending it to hist like

@@ -56,6 +56,7 @@ _SIGS = {
     "lt_q8_gemv_attn_out": (c_int, [_P, _P, _P, _P, c_size_t, c_int, c_int, c_int, _P, _P, _P, c_int, c_int,
                                     _P, c_int]),
     "lt_q8_gemv_rms_silu": (c_int, [_P, _P, _P, c_float, _P, _P, _P, c_int, c_int]),
+    "lt_q8_gemv_rms_swiglu": (c_int, [_P, _P, _P, c_float, _P, _P, c_int, c_int]),
     "lt_q8_gemv_rms_argmax": (c_int, [_P, _P, _P, c_float, _P, _P, c_int, c_int, _P, _P, _P, c_int,
                                       _P, c_size_t]),
     "lt_q8_gemv_argmax_workspace_size": (c_size_t, [c_int]),

@@ -27,7 +27,7 @@ namespace {
 using namespace lt;
 
 enum Pro { PRO_STAGE = 0, PRO_QUANT = 1, PRO_RMS = 2, PRO_EMBED_RMS = 3, PRO_MERGE = 4 };
-enum Epi { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_ARGMAX = 3 };
+enum Epi { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_ARGMAX = 3, EPI_SWIGLU = 4 };
 
 struct GemvParams {
   const uint8_t* W;
@@ -482,6 +482,13 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
   auto finish_row = [&](float a, int ri) {
     const float v = halfwave_tree_dpp(a);
     const int row = rbase + step * ri;
+    if constexpr (EPI == EPI_SWIGLU) {
+      // rows 2j (gate j) and 2j + 1 (up j) sit on the two half-waves of one wave, which
+      // finish them together: lane 0 takes the up value from lane 32
+      const float u = __shfl_xor(v, 32, 64);
+      if ((threadIdx.x & 63) == 0 && ri < nrows) P.y[row >> 1] = lt_silu_mul(v, u);
+      return;
+    }
     if (lane == 0 && ri < nrows) {
       if constexpr (EPI == EPI_SILU) {
         s_rows[row - blockIdx.x * kSiluRows] = v;
@@ -737,6 +744,7 @@ hipError_t launch_gemv(const GemvParams& P, lt_ctx* ctx, int* grid_out) {
     }
     if (P.K <= 4096) return launch_gemv_k<16, PRO, EPI, 8>(P, shm, st, ncu, grid_out);
     if constexpr (PRO == PRO_EMBED_RMS) return hipErrorInvalidValue;   // K <= 4096 (entry check)
+    else if (P.K <= 5120) return launch_gemv_k<20, PRO, EPI, 8>(P, shm, st, ncu, grid_out);
     else return launch_gemv_k<64, PRO, EPI, 4>(P, shm, st, ncu, grid_out);
   }
 }
@@ -844,6 +852,16 @@ int lt_q8_gemv_rms_silu(lt_ctx* ctx, const float* x, const float* nw, float eps,
   GemvParams P{};
   P.W = (const uint8_t*)Wgu; P.N = 2 * F; P.K = K; P.x = x; P.nw = nw; P.eps = eps; P.yq = vq; P.yd = vd;
   return finish(launch_gemv<PRO_RMS, EPI_SILU>(P, ctx, nullptr), "k_gemv_fused<rms,silu>");
+}
+
+int lt_q8_gemv_rms_swiglu(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* Wgu, float* v,
+                          int F, int K) {
+  LT_REQUIRE(ctx && x && nw && v, "lt_q8_gemv_rms_swiglu: null argument");
+  LT_REQUIRE(F > 0 && F % 4 == 0, "lt_q8_gemv_rms_swiglu: F=%d (multiple of 4)", F);
+  if (int rc = check_gemv("lt_q8_gemv_rms_swiglu", Wgu, 2 * F, K)) return rc;
+  GemvParams P{};
+  P.W = (const uint8_t*)Wgu; P.N = 2 * F; P.K = K; P.x = x; P.nw = nw; P.eps = eps; P.y = v;
+  return finish(launch_gemv<PRO_RMS, EPI_SWIGLU>(P, ctx, nullptr), "k_gemv_fused<rms,swiglu>");
 }
 
 size_t lt_q8_gemv_argmax_workspace_size(int N) {

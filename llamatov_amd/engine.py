@@ -418,6 +418,12 @@ class Profile:
     kv_dtype: int = LT_KV_F32
     attn_nsplit: int = 1
     fused_step: bool = True         # five fused launches per layer (lt_fused.hip)
+    # fused step: True = the gate|up GEMV writes fp32 SiLU(g)*u and the down GEMV quantizes it
+    # in its prologue (lt_q8_gemv_rms_swiglu + lt_q8_gemv_quant), so gate|up takes any row
+    # mapping; False = gate|up quantizes in its epilogue, 64 staged rows per workgroup
+    # (lt_q8_gemv_rms_silu).  Same bits; False is faster at C2 (gate|up 6.0 vs 7.6 us, down
+    # 5.1 vs 6.1 us: more workgroups repeat the RMSNorm prologue, whose latency bounds them)
+    swiglu_fp32: bool = False
     fused_rms_quant: bool = False   # per-op path only: k_rms_quant instead of k_rmsnorm + k_quant_q8
     graph: bool = True
 
@@ -667,8 +673,8 @@ class DecodePlan:
           QKV   rmsnorm -> quant -> GEMV + bias        (layer 0: from the embedding of tok)
           attn  RoPE -> KV append -> attention -> quant (split-K: partials, then a merge launch)
           O     GEMV + x, length += 1
-          FFN1  rmsnorm -> quant -> gate|up GEMV -> SiLU(g)*u -> quant
-          FFN2  down GEMV + xres"""
+          FFN1  rmsnorm -> quant -> gate|up GEMV -> SiLU(g)*u (-> quant, swiglu_fp32=False)
+          FFN2  (quant ->) down GEMV + xres"""
         cfg, m, p = self.cfg, self.model, self.profile
         h = self.dev.handle
         E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
@@ -689,9 +695,14 @@ class DecodePlan:
                  p.attn_nsplit, p.kv_dtype, ws, ws_n)
             call("lt_q8_gemv_attn_out", h, self.xq.vp, self.xd.vp, None, 0, 1, nh, hd, L["wo"].t.vp,
                  x.vp, self.xres.vp, E, cfg.q_dim, _vp(cache.len_ptr), cache.max_seq)
-            call("lt_q8_gemv_rms_silu", h, self.xres.vp, L["ffn_norm"].vp, eps, L["wgu_il"].t.vp, self.xq.vp,
-                 self.xd.vp, F, E)
-            call("lt_q8_gemv", h, L["wdown"].t.vp, self.xq.vp, self.xd.vp, self.xres.vp, self.carry.vp, E, F)
+            if p.swiglu_fp32:
+                call("lt_q8_gemv_rms_swiglu", h, self.xres.vp, L["ffn_norm"].vp, eps, L["wgu_il"].t.vp,
+                     self.v.vp, F, E)
+                call("lt_q8_gemv_quant", h, self.v.vp, L["wdown"].t.vp, self.xres.vp, self.carry.vp, E, F)
+            else:
+                call("lt_q8_gemv_rms_silu", h, self.xres.vp, L["ffn_norm"].vp, eps, L["wgu_il"].t.vp,
+                     self.xq.vp, self.xd.vp, F, E)
+                call("lt_q8_gemv", h, L["wdown"].t.vp, self.xq.vp, self.xd.vp, self.xres.vp, self.carry.vp, E, F)
         call("lt_q8_gemv_rms_argmax", h, self.carry.vp, m.output_norm.vp, eps, m.output.t.vp, self.logits.vp,
              cfg.vocab, E, self.tok.vp, self.hist.vp, self.hist_count.vp, self.hist_cap,
              self.am_ws.vp, self.am_ws.nbytes)

@@ -39,7 +39,7 @@ def bitexact(a, b):
     return np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
 
 
-@pytest.mark.parametrize("step", ["fused", "per_op"])
+@pytest.mark.parametrize("step", ["fused", "fused_swiglu_fp32", "per_op"])
 @pytest.mark.parametrize("kv_dtype,nsplit,fused", [(LT_KV_F32, 1, False), (LT_KV_F16, 1, True),
                                                    (LT_KV_F32, 4, True), (LT_KV_F16, 2, False),
                                                    (LT_KV_F16, 16, False)])
@@ -47,7 +47,7 @@ def test_tiny_stepwise_logits_bitexact(gpu, oracle, step, kv_dtype, nsplit, fuse
     cfg = M.TINY
     case(f"tiny stepwise {step} kv={kv_dtype} nsplit={nsplit} fused_rms={fused}")
     prof = dr.Profile(kv_dtype=kv_dtype, attn_nsplit=nsplit, fused_rms_quant=fused,
-                      fused_step=step == "fused")
+                      fused_step=step != "per_op", swiglu_fp32=step == "fused_swiglu_fp32")
     plan = dr.DecodePlan(resident(cfg, gpu), prof)
     orc = oracle.OracleModel(cfg, weights(cfg), kv_f16=kv_dtype == LT_KV_F16, attn_nsplit=nsplit)
     toks = M.random_prompt(cfg, 6, seed=3)
@@ -134,6 +134,7 @@ def test_prefill_kv_equals_incremental(gpu):
     ("qwen2.5-0.5b-arch", 32, 128, LT_KV_F32, "fused"),
     ("qwen2.5-0.5b-arch", 32, 128, LT_KV_F16, "fused"),
     ("qwen2.5-0.5b-arch", 32, 128, LT_KV_F16, "per_op"),
+    ("qwen2.5-0.5b-arch", 32, 128, LT_KV_F16, "fused_swiglu_fp32"),
 ])
 def test_greedy_tokens_identical(gpu, oracle, cfg_name, n_prompt, n_gen, kv_dtype, step):
     """Greedy token identity with the oracle, through the captured graph."""
@@ -142,7 +143,8 @@ def test_greedy_tokens_identical(gpu, oracle, cfg_name, n_prompt, n_gen, kv_dtyp
     prompt = M.random_prompt(cfg, n_prompt, seed=7)
     orc = oracle.OracleModel(cfg, weights(cfg), kv_f16=kv_dtype == LT_KV_F16)
     exp, margins = orc.generate(prompt, n_gen)
-    plan = dr.DecodePlan(resident(cfg, gpu), dr.Profile(kv_dtype=kv_dtype, fused_step=step == "fused"))
+    plan = dr.DecodePlan(resident(cfg, gpu), dr.Profile(kv_dtype=kv_dtype, fused_step=step != "per_op",
+                                                        swiglu_fp32=step == "fused_swiglu_fp32"))
     gr = dr.StepGraph(plan)
     gr.seed(prompt)
     first = plan.read_token()

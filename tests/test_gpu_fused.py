@@ -115,6 +115,34 @@ def test_q8_gemv_rms_silu(gpu, oracle, F, K):
     assert_bitexact(vd.to_host(), ed, "silu*up scales")
 
 
+@pytest.mark.parametrize("F,K", [(4864, 896), (14336, 4096), (64, 128), (12, 96), (16384, 896), (20000, 512),
+                                 (3000, 4864)])
+def test_q8_gemv_rms_swiglu(gpu, oracle, F, K):
+    """gate|up GEMV with the fp32 SiLU(g)*u epilogue (adjacent half-waves hold the gate and
+    up rows of one output), then the down GEMV's quantizing prologue: the same quants as the
+    quantizing epilogue, and the down GEMV's output equal to the oracle's."""
+    case(f"gemv_rms_swiglu F={F} K={K}")
+    rng = np.random.default_rng(25)
+    Wg, Wu = rand_weight(rng, F, K), rand_weight(rng, F, K)
+    x = (2.0 * rng.standard_normal(K)).astype(np.float32)
+    nw = (0.5 * rng.standard_normal(K) + 1.0).astype(np.float32)
+    xq, xd = oracle.quant_q8(oracle.rmsnorm(x, nw, 1e-6))
+    g = oracle.q8_gemv(Wg, xq, xd, K)
+    u = oracle.q8_gemv(Wu, xq, xd, K)
+    v = empty((F,), np.float32)
+    call("lt_q8_gemv_rms_swiglu", gpu.handle, up(x).vp, up(nw).vp, ctypes.c_float(1e-6),
+         up(M.interleave_gateup(Wg, Wu)).vp, v.vp, F, K)
+    assert_bitexact(v.to_host(), oracle.silu_mul(g, u), "silu*up")
+    if F % 32 == 0 and F <= 16384:
+        N = 256
+        Wd = rand_weight(rng, N, F)
+        r = rng.standard_normal(N).astype(np.float32)
+        y = empty((N,), np.float32)
+        call("lt_q8_gemv_quant", gpu.handle, v.vp, up(Wd).vp, up(r).vp, y.vp, N, F)
+        sq, sd = oracle.silu_mul_quant(g, u)
+        assert_bitexact(y.to_host(), oracle.q8_gemv(Wd, sq, sd, F, r), "down after swiglu")
+
+
 def test_q8_gemv_attn_out(gpu, oracle):
     """Single-split O launcher on a quantized attention output (split partials come from
     lt_attn_step and are covered by test_attn_step_then_out)."""
