@@ -137,6 +137,17 @@ LT_API int lt_attn_decode(lt_ctx* ctx, const float* q, const void* kc, const voi
 /* Bytes of split-K workspace (0 for nsplit == 1). */
 LT_API size_t lt_attn_workspace_size(int batch, int nh, int hd, int nsplit);
 
+/* lt_attn_decode without a workspace argument and without allocating: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The split-K partials live in a
+ * file-scope device array of 16 MiB (one per GPU, held until the process ends), so
+ * lt_attn_workspace_size(batch, nh, hd, nsplit) must be at most 16 MiB (else LT_EINVAL, nothing
+ * launched).  Same results as lt_attn_decode, bit for bit.  Calls that overlap on one GPU
+ * (from two contexts' streams) share the array and race; calls on one context are ordered. */
+LT_API int lt_attn_decode_noalloc(lt_ctx* ctx, const float* q, const void* kc, const void* vc, const int* len,
+                                  float* out, int batch, int nh, int nkv, int hd, float scale, int maxt,
+                                  int nsplit, int kv_dtype);
+
 /* Greedy argmax over n logits, ties to the lowest index (k_argmax_s1/_s2,
  * bpd/lib/dev_residency.py:225-273, argmax_dev :1074-1110).  ws must hold
  * lt_argmax_workspace_size() bytes.  out is a device int. */

@@ -46,6 +46,8 @@ _SIGS = {
     "lt_attn_decode": (c_int, [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float,
                                c_int, c_int, c_int, _P, c_size_t]),
     "lt_attn_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "lt_attn_decode_noalloc": (c_int, [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float,
+                                       c_int, c_int, c_int]),
     "lt_argmax": (c_int, [_P, _P, c_int, _P, _P, c_size_t]),
     "lt_argmax_workspace_size": (c_size_t, []),
     "lt_argmax_record": (c_int, [_P, _P, c_int, _P, _P, _P, c_int, _P, c_size_t]),

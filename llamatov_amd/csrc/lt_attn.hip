@@ -1324,6 +1324,24 @@ size_t cache_bytes_of(int rows, int maxt, int nkv, int hd, int kv_dtype) {
 
 }  // namespace
 
+// Scratch of lt_attn_decode_noalloc: the split-K partials (m, Z, O per split) in a
+// file-scope device array instead of a caller workspace.  Each GPU holds its own copy at
+// its own address until the process ends; host code never uses the array's name as an
+// address (it is a host-side stand-in): lt_init looks the device address up once per
+// context, with its device current, and the entry point passes that address.  Every
+// split's partials are written before the merge reads them, so nothing needs clearing.
+// Calls that overlap on one GPU (two contexts' streams) share the array and race.
+constexpr size_t kAttnScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) uint8_t scratch[kAttnScratchBytes];
+
+void lt_attn_scratch_bind(lt_ctx* ctx) {
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  ctx->attn_scratch_err = e;
+  ctx->attn_scratch = e == hipSuccess ? p : nullptr;
+  ctx->attn_scratch_bytes = e == hipSuccess ? kAttnScratchBytes : 0;
+}
+
 extern "C" {
 
 size_t lt_attn_workspace_size(int batch, int nh, int hd, int nsplit) {
@@ -1343,6 +1361,31 @@ int lt_attn_decode(lt_ctx* ctx, const float* q, const void* kc, const void* vc, 
   A.nh = nh; A.nkv = nkv; A.hd = hd; A.scale = scale; A.maxt = maxt; A.nsplit = nsplit;
   return launch_attn(ctx, AM_DECODE, kv_dtype == LT_KV_F16, pick_hpw(nh, nkv, hd, cb / batch), batch, A, ws,
                      ws_bytes, "lt_attn_decode");
+}
+
+int lt_attn_decode_noalloc(lt_ctx* ctx, const float* q, const void* kc, const void* vc, const int* len,
+                           float* out, int batch, int nh, int nkv, int hd, float scale, int maxt, int nsplit,
+                           int kv_dtype) {
+  LT_REQUIRE(ctx && q && kc && vc && len && out, "lt_attn_decode_noalloc: null argument");
+  LT_REQUIRE(batch > 0, "lt_attn_decode_noalloc: batch=%d", batch);
+  const size_t cb = cache_bytes_of(batch, maxt, nkv, hd, kv_dtype);
+  if (int rc = check_common(nh, nkv, hd, maxt, nsplit, kv_dtype, kc, vc, cb, "lt_attn_decode_noalloc")) return rc;
+  const size_t need = lt_attn_workspace_size(batch, nh, hd, nsplit);
+  if (need > 0) {
+    if (!ctx->attn_scratch)
+      return lt_fail(LT_ESTATE, "lt_attn_decode_noalloc: the device scratch is not bound (%s)",
+                     hipGetErrorString(ctx->attn_scratch_err));
+    if (need > ctx->attn_scratch_bytes)
+      return lt_fail(LT_EINVAL,
+                     "lt_attn_decode_noalloc: batch=%d nh=%d hd=%d nsplit=%d needs %zu bytes of split partials, "
+                     "more than the %zu-byte device scratch; lower nsplit or batch, or call lt_attn_decode "
+                     "with a workspace", batch, nh, hd, nsplit, need, ctx->attn_scratch_bytes);
+  }
+  AttnArgs A = {};
+  A.q = q; A.q_stride = nh * hd; A.kc = (void*)kc; A.vc = (void*)vc; A.len = len; A.out = out;
+  A.nh = nh; A.nkv = nkv; A.hd = hd; A.scale = scale; A.maxt = maxt; A.nsplit = nsplit;
+  return launch_attn(ctx, AM_DECODE, kv_dtype == LT_KV_F16, pick_hpw(nh, nkv, hd, cb / batch), batch, A,
+                     ctx->attn_scratch, ctx->attn_scratch_bytes, "lt_attn_decode_noalloc");
 }
 
 int lt_attn_prefill(lt_ctx* ctx, const float* q, int q_stride, const void* kc, const void* vc, const int* len0,

@@ -13,7 +13,17 @@ struct lt_ctx {
   hipStream_t stream = nullptr;
   bool capturing = false;
   int num_cus = 0;
+  // the device address of lt_attn.hip's scratch array on this context's device (bound at
+  // lt_init by lt_attn_scratch_bind), or null with the lookup's error in attn_scratch_err
+  void* attn_scratch = nullptr;
+  size_t attn_scratch_bytes = 0;
+  hipError_t attn_scratch_err = hipSuccess;
 };
+
+// Binds ctx->attn_scratch to the device copy of the attention scratch array (the device
+// must be current).  Never fails the caller: a failed lookup is kept in attn_scratch_err and
+// reported by the entry point that needs the scratch.
+void lt_attn_scratch_bind(lt_ctx* ctx);
 
 int lt_fail(int code, const char* fmt, ...);
 int lt_fail_hip(hipError_t e, const char* what, const char* file, int line);

@@ -63,6 +63,7 @@ int lt_init(int device, lt_ctx** out) {
   hipDeviceProp_t prop;
   LT_CHECK(hipGetDeviceProperties(&prop, device));
   c->num_cus = prop.multiProcessorCount;
+  lt_attn_scratch_bind(c);
   *out = c;
   return LT_OK;
 }
