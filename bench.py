@@ -8,11 +8,13 @@ uniform-random prompt, 128 decoded tokens at batch 1.  A step is one decode toke
 replay of the captured HIP graph (embedding gather -> 24 layers -> logits -> argmax), with
 every weight and the KV cache resident in HBM before the timed region starts.
 
-Printed (one JSON line on stdout): decode tok/s, the roofline of the dominant kernel (the
-Q8_0 GEMV of the vocab projection, 151936 x 896, timed with HIP events on the library's
-stream over rotated weight copies so the 256 MB Infinity Cache cannot serve it), and the
-CPU baseline: the oracle (C restatement of the reference arithmetic, OpenMP over GEMV rows)
-decoding a bounded sample of the same workload on the host cores.
+Printed (one JSON line on stdout): decode tok/s; `step_kernels`, every launch of the step
+timed live with HIP events on the library's stream (a captured graph of back-to-back
+launches over rotated weight copies >= 600 MB, so the 256 MB Infinity Cache cannot serve
+them), with its algorithmic bytes, HBM rate and share of the step's kernel time;
+`roofline`, the largest-share kernel of that table; and the CPU baseline: the oracle (C
+restatement of the reference arithmetic, OpenMP over GEMV rows) decoding a bounded sample of
+the same workload and timing the C1 GEMV on the host cores, all cores and one core.
 """
 from __future__ import annotations
 
@@ -60,46 +62,149 @@ class Events:
         self._lib.call("lt_event_destroy", self.b)
 
 
-def gemv_roofline(dev, w_embd: np.ndarray, N: int, K: int, eps: float, launches: int = 60) -> dict:
-    """The decode step's dominant kernel, the vocab projection (final RMSNorm -> quant ->
-    151936 x 896 Q8_0 GEMV; lt_q8_gemv_rms, the step's launch without its argmax epilogue),
-    timed with HIP events on the library's stream over rotated weight copies (>= 512 MB, so
-    the 256 MB Infinity Cache cannot serve it)."""
-    from llamatov_amd import engine as dr
-    from llamatov_amd._lib import call
-    blk_bytes = w_embd.nbytes
-    copies = max(2, int(np.ceil(600e6 / blk_bytes)))
-    ws = [dr.DevTensor.from_host(w_embd, dev) for _ in range(copies)]
-    rng = np.random.default_rng(3)
-    x = dr.DevTensor.from_host(rng.standard_normal(K).astype(np.float32), dev)
-    nw = dr.DevTensor.from_host(np.ones(K, np.float32), dev)
-    y = dr.DevTensor.empty((N,), np.float32, dev)
-    e = ctypes.c_float(eps)
-    for i in range(copies):  # warm the code path
-        call("lt_q8_gemv_rms", dev.handle, x.vp, nw.vp, e, ws[i].vp, None, y.vp, N, K)
+def graph_us_per_launch(dev, launches, reps: int = 3) -> float:
+    """Average duration of one launch: the launches captured back to back into one graph,
+    replayed `reps` times between two HIP events on the library's stream."""
+    from llamatov_amd import _lib
+    for f in launches:   # warm: code objects loaded, pages mapped
+        f()
+    dev.sync()
+    _lib.call("lt_graph_begin", dev.handle)
+    for f in launches:
+        f()
+    g = ctypes.c_void_p()
+    _lib.call("lt_graph_end", dev.handle, ctypes.byref(g))
+    _lib.call("lt_graph_launch", dev.handle, g)
     dev.sync()
     ev = Events(dev)
     ev.start()
-    for i in range(launches):
-        call("lt_q8_gemv_rms", dev.handle, x.vp, nw.vp, e, ws[i % copies].vp, None, y.vp, N, K)
+    for _ in range(reps):
+        _lib.call("lt_graph_launch", dev.handle, g)
     ms = ev.stop_ms()
     ev.free()
-    for t in ws + [x, nw, y]:
-        t.free()
-    avg_s = ms / 1e3 / launches
-    alg_bytes = N * (K // 32) * 34 + 8 * K + 4 * N
-    achieved = alg_bytes / avg_s / 1e9
-    traffic = None   # HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE counter runs
-    tf = ROOT / "profiles" / "gemv_vocab_c2_traffic.txt"
+    _lib.raw("lt_graph_free")(g)
+    return ms * 1e3 / (reps * len(launches))
+
+
+def rotation(dev, mats, min_bytes: float = 600e6):
+    """The given device matrices plus device copies of them, cycled, until the set holds at
+    least min_bytes (so a back-to-back loop streams from HBM, not the Infinity Cache).
+    Returns (set, extra copies to free)."""
+    from llamatov_amd import engine as dr
+    out, extra, i = list(mats), [], 0
+    while sum(m.nbytes for m in out) < min_bytes:
+        src = mats[i % len(mats)]
+        t = dr.DevTensor.empty(src.shape, src.dtype, dev)
+        dev.d2d(t.ptr, src.ptr, src.nbytes)
+        out.append(t)
+        extra.append(t)
+        i += 1
+    return out, extra
+
+
+def step_kernels(dev, plan, only: str | None = None, attn_len: int | None = None) -> list[dict]:
+    """Every launch of the fused C2 decode step, timed on its own (graph of back-to-back
+    launches over rotated weights), with its algorithmic bytes per launch:
+      qkv     rmsnorm -> quant -> QKV GEMV + bias         N(K/32)34 + 8K + 8N
+      attn    RoPE -> KV append -> attention -> quant      2 (L+1) kv_dim 2 (fp16 rows) + 4 n_qkv + QD + QD/16
+      o       O GEMV + residual                            N(K/32)34 + K + K/16 + 8N
+      gateup  rmsnorm -> quant -> gate|up GEMV -> SiLU*up -> quant   2F(K/32)34 + 8K + F + F/16
+      down    down GEMV + residual                         N(K/32)34 + K + K/16 + 8N
+      vocab   final rmsnorm -> quant -> vocab GEMV -> argmax        V(K/32)34 + 8K + 4V
+    The attention runs at cache length attn_len (default: the plan's current length; the
+    decode bench passes the mean length of its timed tokens), over rows the decode wrote; its
+    launches leave the lengths unchanged."""
+    from llamatov_amd import engine as dr
+    from llamatov_amd._lib import call
+    cfg, m, p = plan.cfg, plan.model, plan.profile
+    if not p.fused_step or p.swiglu_fp32 or p.attn_nsplit != 1:
+        raise ValueError("step_kernels times the default fused step (nsplit 1, quantizing gate|up epilogue)")
+    h = dev.handle
+    E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
+    QD, NQ, V = cfg.q_dim, cfg.n_qkv, cfg.vocab
+    eps = ctypes.c_float(cfg.norm_eps)
+    rb = lambda N, K: N * (K // 32) * 34
+    L = plan.caches[0].length if attn_len is None else int(attn_len)
+    kinds = {
+        "qkv": dict(kernel="k_gemv_fused<4, PRO_RMS, EPI_RESID> (lt_q8_gemv_rms)", shape=[NQ, E],
+                    mats=[Ly["wqkv"].t for Ly in m.layers], count=cfg.n_layers,
+                    bytes=rb(NQ, E) + 8 * E + 8 * NQ,
+                    fn=lambda w, il: call("lt_q8_gemv_rms", h, plan.carry.vp, m.layers[il]["attn_norm"].vp, eps,
+                                          w.vp, dr._vp(m.layers[il]["bqkv"]), plan.qkv.vp, NQ, E)),
+        "attn": dict(kernel="k_attn_w1<f16, STEP> (lt_attn_step)", shape=[nh, nkv, hd, L + 1],
+                     mats=None, count=cfg.n_layers,
+                     bytes=2 * (L + 1) * cfg.kv_dim * 2 + 4 * NQ + QD + QD // 16,
+                     fn=lambda w, il: call("lt_attn_step", h, plan.qkv.vp, m.freqs.vp, plan.caches[il].k.vp,
+                                           plan.caches[il].v.vp, dr._vp(plan.caches[il].len_ptr), None,
+                                           plan.xq.vp, plan.xd.vp, nh, nkv, hd, ctypes.c_float(plan.scale),
+                                           plan.caches[il].max_seq, 1, p.kv_dtype, None, 0)),
+        "o": dict(kernel="k_gemv_fused<1, PRO_MERGE, EPI_RESID> (lt_q8_gemv_attn_out)", shape=[E, QD],
+                  mats=[Ly["wo"].t for Ly in m.layers], count=cfg.n_layers,
+                  bytes=rb(E, QD) + QD + QD // 16 + 8 * E,
+                  fn=lambda w, il: call("lt_q8_gemv_attn_out", h, plan.xq.vp, plan.xd.vp, None, 0, 1, nh, hd, w.vp,
+                                        plan.carry.vp, plan.xres.vp, E, QD, None, 0)),
+        "gateup": dict(kernel="k_gemv_fused<4, PRO_RMS, EPI_SILU, staged> (lt_q8_gemv_rms_silu)", shape=[2 * F, E],
+                       mats=[Ly["wgu_il"].t for Ly in m.layers], count=cfg.n_layers,
+                       bytes=rb(2 * F, E) + 8 * E + F + F // 16,
+                       fn=lambda w, il: call("lt_q8_gemv_rms_silu", h, plan.xres.vp, m.layers[il]["ffn_norm"].vp, eps,
+                                             w.vp, plan.xq.vp, plan.xd.vp, F, E)),
+        "down": dict(kernel="k_gemv_fused<1, PRO_STAGE, EPI_RESID> (lt_q8_gemv)", shape=[E, F],
+                     mats=[Ly["wdown"].t for Ly in m.layers], count=cfg.n_layers,
+                     bytes=rb(E, F) + F + F // 16 + 8 * E,
+                     fn=lambda w, il: call("lt_q8_gemv", h, w.vp, plan.xq.vp, plan.xd.vp, plan.xres.vp, plan.carry.vp,
+                                           E, F)),
+        "vocab": dict(kernel="k_gemv_fused<4, PRO_RMS, EPI_ARGMAX> + k_argmax_finalize (lt_q8_gemv_rms_argmax)",
+                      shape=[V, E], mats=[m.output.t], count=1, bytes=rb(V, E) + 8 * E + 4 * V,
+                      fn=lambda w, il: call("lt_q8_gemv_rms_argmax", h, plan.carry.vp, m.output_norm.vp, eps, w.vp,
+                                            plan.logits.vp, V, E, plan.tok.vp, None, None, 0, plan.am_ws.vp,
+                                            plan.am_ws.nbytes)),
+    }
+    out = []
+    for name, k in kinds.items():
+        if only and name != only:
+            continue
+        extra = []
+        if k["mats"] is None:   # attention: one launch per layer cache, twice over, at length L
+            saved = plan.lengths().copy()
+            dev.h2d(plan.lens.ptr, np.full(cfg.n_layers, L, np.int32))
+            launches = [lambda il=il: k["fn"](None, il) for il in range(cfg.n_layers)] * 2
+        else:
+            mats, extra = rotation(dev, k["mats"])
+            launches = [lambda w=w, i=i: k["fn"](w, i % cfg.n_layers) for i, w in enumerate(mats)]
+        us = graph_us_per_launch(dev, launches)
+        if k["mats"] is None:
+            dev.h2d(plan.lens.ptr, saved)
+        for t in extra:
+            t.free()
+        gbs = k["bytes"] / (us * 1e-6) / 1e9
+        out.append({"name": name, "kernel": k["kernel"], "shape": k["shape"], "launches_per_step": k["count"],
+                    "avg_launch_us": round(us, 3), "bytes_per_launch": int(k["bytes"]), "GB/s": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        log(f"step kernel {name}: {us:.2f} us, {gbs:.0f} GB/s")
+    tot = sum(e["avg_launch_us"] * e["launches_per_step"] for e in out)
+    for e in out:
+        e["share"] = round(e["avg_launch_us"] * e["launches_per_step"] / tot, 4) if tot else None
+    return out
+
+
+def roofline_of(entry: dict) -> dict:
+    """The bench line's roofline object for one step-kernel entry; traffic (HBM bytes per
+    launch) comes from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs of the same
+    kernel when profiles/ holds them (bench.py --roofline-only is the counter command)."""
+    traffic, src = None, None
+    tf = ROOT / "profiles" / f"traffic_{entry['name']}_c2.txt"
     if tf.exists():
         import re
-        m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", tf.read_text(), flags=re.M)
-        traffic = int(m.group(1)) if m else None
-    return {"kernel": "k_gemv_fused<4, PRO_RMS, EPI_STORE, 8> (lt_q8_gemv_rms, vocab projection)",
-            "shape": [N, K], "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "bytes_per_launch": alg_bytes, "avg_launch_us": round(avg_s * 1e6, 3),
-            "weight_copies": copies}
+        mt = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", tf.read_text(), flags=re.M)
+        if mt:
+            traffic, src = int(mt.group(1)), f"profiles/{tf.name} (committed counter run, not this run)"
+    return {"kernel": entry["kernel"], "step_kernel": entry["name"], "shape": entry["shape"], "bound": "hbm",
+            "achieved": entry["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": entry["frac"],
+            "traffic": traffic, "traffic_source": src, "bytes_per_launch": entry["bytes_per_launch"],
+            "avg_launch_us": entry["avg_launch_us"], "launches_per_step": entry["launches_per_step"],
+            "share_of_step_kernel_time": entry["share"],
+            "timing": "HIP events on the library stream around a graph of back-to-back launches over >= 600 MB "
+                      "of rotated weight copies"}
 
 
 GEMV_SWEEP = [("C1 ffn_up 0.5B", 4864, 896), ("C3 q/o 8B", 4096, 4096), ("C3 gate/up 8B", 14336, 4096),
@@ -254,23 +359,66 @@ def c5_leg(dev, n_prefill: int = 512, n_decode: int = 256, eager: bool = False) 
     return res
 
 
-def cpu_baseline(cfg, weights, prompt, n_decode: int, kv_f16: bool) -> tuple[dict, list[int]]:
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(cfg, weights, prompt, n_decode: int, kv_f16: bool, n_decode_1core: int = 12,
+                 gemv_iters: int = 200) -> tuple[dict, list[int]]:
+    """The oracle on the host: C2 greedy decode tok/s over n_decode tokens after the prompt
+    (all cores), the same on one core over the first n_decode_1core of those tokens, and the
+    C1 GEMV (4864 x 896 on rotated weight copies > 512 MB) median over gemv_iters calls."""
     from oracle import oracle as orc
-    m = orc.OracleModel(cfg, weights, kv_f16=kv_f16)
-    logits = None
-    for t in prompt:
-        logits = m.step(t)
-    toks = []
-    t0 = time.perf_counter()
-    for _ in range(n_decode):
-        tok = orc.argmax(logits)
-        toks.append(tok)
-        logits = m.step(tok)
-    dt = time.perf_counter() - t0
     cores = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
-    return ({"value": round(n_decode / dt, 3), "unit": "tok/s", "cores": cores, "kind": "port",
-             "sample": f"C2 model, {len(prompt)}-token prompt prefilled untimed, then {n_decode} greedy "
-                       f"decode steps timed (oracle/lt_oracle.c, OpenMP over GEMV rows)"}, toks)
+
+    def decode(n, threads):
+        orc.set_threads(threads)
+        m = orc.OracleModel(cfg, weights, kv_f16=kv_f16)
+        logits = None
+        for t in prompt:
+            logits = m.step(t)
+        toks = []
+        t0 = time.perf_counter()
+        for _ in range(n):
+            tok = orc.argmax(logits)
+            toks.append(tok)
+            logits = m.step(tok)
+        return n / (time.perf_counter() - t0), toks
+
+    tps, toks = decode(n_decode, cores)
+    tps1, toks1 = decode(n_decode_1core, 1)
+    # C1: 4864 x 896 GEMV on N(0, 0.02) weights and an N(0,1) activation, both quantized
+    rng = np.random.default_rng(11)
+    from llamatov_amd import q8
+    W = q8.quantize_rows((rng.standard_normal((4864, 896), dtype=np.float32) * np.float32(0.02)))
+    copies = [W] + [W.copy() for _ in range(int(np.ceil(512e6 / W.nbytes)))]
+    xq, xd = orc.quant_q8(rng.standard_normal(896, dtype=np.float32))
+    gemv = {}
+    for threads in (cores, 1):
+        orc.set_threads(threads)
+        ts = []
+        for i in range(gemv_iters):
+            t0 = time.perf_counter()
+            orc.q8_gemv(copies[i % len(copies)], xq, xd, 896)
+            ts.append(time.perf_counter() - t0)
+        gemv[threads] = float(np.median(ts)) * 1e6
+    orc.set_threads(cores)
+    c1_bytes = 4864 * 28 * 34 + 896 + 28 * 2 + 4 * 4864
+    return ({"value": round(tps, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+             "value_1core": round(tps1, 3), "cpu_model": _cpu_model(),
+             "c1_gemv_median_us": round(gemv[cores], 2), "c1_gemv_median_us_1core": round(gemv[1], 2),
+             "c1_gemv_GBs": round(c1_bytes / (gemv[cores] * 1e-6) / 1e9, 2),
+             "sample": f"C2 model, {len(prompt)}-token prompt prefilled untimed, then {n_decode} greedy decode "
+                       f"steps timed on {cores} threads and the first {n_decode_1core} on 1 thread "
+                       f"(oracle/lt_oracle.c, OpenMP over GEMV rows); C1 4864x896 GEMV median of {gemv_iters} "
+                       f"calls over {len(copies)} rotated weight copies",
+             "tokens_1core_match": toks1 == toks[:n_decode_1core]}, toks)
 
 
 def main() -> int:
@@ -281,6 +429,7 @@ def main() -> int:
     ap.add_argument("--kv", choices=["f16", "f32"], default="f16")
     ap.add_argument("--prompt", type=int, default=32)
     ap.add_argument("--cpu-tokens", type=int, default=128, help="decode tokens in the CPU baseline sample")
+    ap.add_argument("--cpu-tokens-1core", type=int, default=12, help="decode tokens of the 1-core CPU figure")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--c4", action="store_true", help="also time BASELINE config 4 attention (adds c4_attention)")
@@ -294,8 +443,11 @@ def main() -> int:
                     help="thirteen per-op launches per layer (the reference's kernel-per-op chain) "
                          "instead of the five fused launches")
     ap.add_argument("--roofline-only", action="store_true",
-                    help="only the GEMV roofline leg, plus a device copy of one weight matrix (the known-size "
-                         "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE); for counter runs")
+                    help="only one step kernel's timing loop (--roofline-kernel), plus a device copy of a weight "
+                         "matrix (the known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE); "
+                         "for counter runs")
+    ap.add_argument("--roofline-kernel", default="gateup",
+                    choices=["qkv", "attn", "o", "gateup", "down", "vocab"])
     ap.add_argument("--eager", action="store_true",
                     help="launch the step's kernels directly instead of replaying the captured graph "
                          "(same kernels; for profilers that cannot trace graph launches)")
@@ -314,13 +466,16 @@ def main() -> int:
     if args.roofline_only:
         w = M.synth_weights(cfg, seed=1234)
         dev = dr.get_device()
-        emb = w["token_embd.weight"]
-        rf = gemv_roofline(dev, emb, cfg.vocab, cfg.n_embd, cfg.norm_eps, launches=20)
-        src = dr.DevTensor.from_host(emb, dev)
+        model = dr.ResidentModel(cfg, w, dev, layouts="fused")
+        plan = dr.DecodePlan(model, dr.Profile(kv_dtype=LT_KV_F16))
+        dr.forward_prefill(plan, M.random_prompt(cfg, args.prompt, seed=7))
+        entry = step_kernels(dev, plan, only=args.roofline_kernel)[0]
+        src = model.layers[0]["wgu_il"].t
         dst = dr.DevTensor.empty(src.shape, src.dtype, dev)
         dev.d2d(dst.ptr, src.ptr, src.nbytes)   # calibration: a plain copy of known size
         dev.sync()
-        print(json.dumps({"roofline": rf, "calibration_copy_bytes": int(src.nbytes)}), flush=True)
+        print(json.dumps({"roofline": roofline_of(dict(entry, share=None)),
+                          "calibration_copy_bytes": int(src.nbytes)}), flush=True)
         return 0
     if args.prompt + args.steps > cfg.max_ctx or args.prompt + args.warmup > cfg.max_ctx:
         print("bench.py: prompt + steps exceeds the 1024-position KV cache", file=sys.stderr)
@@ -417,9 +572,11 @@ def main() -> int:
         "step_kernels": "per_op" if args.per_op else "fused",
     }
 
-    if not args.no_roofline:
-        log("GEMV roofline leg")
-        result["roofline"] = gemv_roofline(dev, w["token_embd.weight"], cfg.vocab, cfg.n_embd, cfg.norm_eps)
+    if not args.no_roofline and not args.per_op:
+        log("step kernels")
+        table = step_kernels(dev, plan, attn_len=len(prompt) + args.steps // 2)
+        result["step_kernels"] = table
+        result["roofline"] = roofline_of(max(table, key=lambda e: e["share"]))
 
     if args.gemv_sweep:
         log("GEMV sweep")
@@ -431,7 +588,8 @@ def main() -> int:
     if not args.no_cpu_baseline:
         n_cpu = min(args.cpu_tokens, args.steps)
         log(f"CPU baseline: oracle over {n_cpu} decode tokens")
-        cb, cpu_tokens = cpu_baseline(cfg, w, prompt, n_cpu, kv_dtype == LT_KV_F16)
+        cb, cpu_tokens = cpu_baseline(cfg, w, prompt, n_cpu, kv_dtype == LT_KV_F16,
+                                      n_decode_1core=min(args.cpu_tokens_1core, n_cpu))
         result["cpu_baseline"] = cb
         result["tokens_match_cpu"] = cpu_tokens == tokens[:n_cpu]
 

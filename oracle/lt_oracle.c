@@ -18,6 +18,7 @@
 #include <stdlib.h>
 #include <string.h>
 #include <math.h>
+#include <omp.h>
 #include "../llamatov_amd/csrc/lt_numerics.h"
 
 #define OR_API __attribute__((visibility("default")))
@@ -27,6 +28,10 @@
  * Dequant y = q * d (bpd/llamatov_run.py:184-207).
  * ------------------------------------------------------------------------------- */
 static inline uint16_t blk_scale(const uint8_t* blk) { return (uint16_t)(blk[0] | (blk[1] << 8)); }
+
+/* Thread count of the OpenMP loops (the CPU baseline's 1-core and all-core figures). */
+OR_API void or_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+OR_API int or_max_threads(void) { return omp_get_max_threads(); }
 
 OR_API float or_half_to_float(uint16_t h) { return lt_half_to_float_bits(h); }
 OR_API uint16_t or_float_to_half(float f) { return lt_float_to_half_bits(f); }

@@ -30,6 +30,8 @@ def lib() -> ctypes.CDLL:
         L = ctypes.CDLL(str(LIB))
         P = c_void_p
         sigs = {
+            "or_set_threads": (None, [c_int]),
+            "or_max_threads": (c_int, []),
             "or_half_to_float": (c_float, [ctypes.c_uint16]),
             "or_float_to_half": (ctypes.c_uint16, [c_float]),
             "or_expf": (c_float, [c_float]),
@@ -68,6 +70,14 @@ def _p(a: np.ndarray | None) -> c_void_p:
         return c_void_p(0)
     assert a.flags.c_contiguous
     return a.ctypes.data_as(c_void_p)
+
+
+def set_threads(n: int) -> None:
+    lib().or_set_threads(int(n))
+
+
+def max_threads() -> int:
+    return int(lib().or_max_threads())
 
 
 # ---- scalar numerics ---------------------------------------------------------------
