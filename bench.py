@@ -119,12 +119,39 @@ def step_kernels(dev, plan, only: str | None = None, attn_len: int | None = None
     cfg, m, p = plan.cfg, plan.model, plan.profile
     if not p.fused_step or p.swiglu_fp32 or p.attn_nsplit != 1:
         raise ValueError("step_kernels times the default fused step (nsplit 1, quantizing gate|up epilogue)")
+    four = plan.four_launch_len >= (attn_len if attn_len is not None else plan.caches[0].length) + 1
     h = dev.handle
     E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
     QD, NQ, V = cfg.q_dim, cfg.n_qkv, cfg.vocab
     eps = ctypes.c_float(cfg.norm_eps)
     rb = lambda N, K: N * (K // 32) * 34
     L = plan.caches[0].length if attn_len is None else int(attn_len)
+    # the four-launch step's kernels read (QKV, attention) or bump (gate|up) a length: here a
+    # scratch int holding L, so the plan's own lengths stay as they are
+    lenL = dr.DevTensor.from_host(np.array([L], np.int32), dev)
+    lenB = dr.DevTensor.from_host(np.array([L], np.int32), dev)
+    maxt = plan.caches[0].max_seq
+    kinds4 = {
+        "qkv": dict(kernel="k_gemv_fused<4, PRO_RMS, EPI_ROPE_KV> (lt_q8_gemv_rms_rope_kv)", shape=[NQ, E],
+                    mats=[Ly["wqkv"].t for Ly in m.layers], count=cfg.n_layers,
+                    bytes=rb(NQ, E) + 8 * E + 8 * NQ + 2 * cfg.kv_dim * (2 if p.kv_dtype else 4),
+                    fn=lambda w, il: call("lt_q8_gemv_rms_rope_kv", h, plan.carry.vp, None, None, V, None,
+                                          plan.err.vp, m.layers[il]["attn_norm"].vp, eps, w.vp,
+                                          dr._vp(m.layers[il]["bqkv"]), plan.qkv.vp, E, m.freqs.vp,
+                                          plan.caches[il].k.vp, plan.caches[il].v.vp, lenL.vp, nh, nkv, hd, maxt,
+                                          p.kv_dtype)),
+        "attn_o": dict(kernel="k_attn_o<f16> (lt_q8_gemv_attn_o: attention + quant + O GEMV + residual)",
+                       shape=[E, QD, nh, nkv, hd, L + 1], mats=[Ly["wo"].t for Ly in m.layers], count=cfg.n_layers,
+                       bytes=rb(E, QD) + 2 * (L + 1) * cfg.kv_dim * (2 if p.kv_dtype else 4) + 4 * QD + 8 * E,
+                       fn=lambda w, il: call("lt_q8_gemv_attn_o", h, plan.qkv.vp, plan.caches[il].k.vp,
+                                             plan.caches[il].v.vp, lenL.vp, nh, nkv, hd, ctypes.c_float(plan.scale),
+                                             maxt, p.kv_dtype, w.vp, plan.carry.vp, plan.xres.vp, E)),
+        "gateup": dict(kernel="k_gemv_fused<4, PRO_RMS, EPI_SILU, staged> (lt_q8_gemv_rms_silu_len)",
+                       shape=[2 * F, E], mats=[Ly["wgu_il"].t for Ly in m.layers], count=cfg.n_layers,
+                       bytes=rb(2 * F, E) + 8 * E + F + F // 16,
+                       fn=lambda w, il: call("lt_q8_gemv_rms_silu_len", h, plan.xres.vp, m.layers[il]["ffn_norm"].vp,
+                                             eps, w.vp, plan.xq.vp, plan.xd.vp, F, E, lenB.vp, maxt)),
+    }
     kinds = {
         "qkv": dict(kernel="k_gemv_fused<4, PRO_RMS, EPI_RESID> (lt_q8_gemv_rms)", shape=[NQ, E],
                     mats=[Ly["wqkv"].t for Ly in m.layers], count=cfg.n_layers,
@@ -159,6 +186,9 @@ def step_kernels(dev, plan, only: str | None = None, attn_len: int | None = None
                                             plan.logits.vp, V, E, plan.tok.vp, None, None, 0, plan.am_ws.vp,
                                             plan.am_ws.nbytes)),
     }
+    if four:
+        kinds = {"qkv": kinds4["qkv"], "attn_o": kinds4["attn_o"], "gateup": kinds4["gateup"],
+                 "down": kinds["down"], "vocab": kinds["vocab"]}
     out = []
     for name, k in kinds.items():
         if only and name != only:
@@ -181,6 +211,8 @@ def step_kernels(dev, plan, only: str | None = None, attn_len: int | None = None
                     "avg_launch_us": round(us, 3), "bytes_per_launch": int(k["bytes"]), "GB/s": round(gbs, 1),
                     "frac": round(gbs / HBM_PEAK_GBS, 4)})
         log(f"step kernel {name}: {us:.2f} us, {gbs:.0f} GB/s")
+    lenL.free()
+    lenB.free()
     tot = sum(e["avg_launch_us"] * e["launches_per_step"] for e in out)
     for e in out:
         e["share"] = round(e["avg_launch_us"] * e["launches_per_step"] / tot, 4) if tot else None
@@ -447,7 +479,7 @@ def main() -> int:
                          "matrix (the known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE); "
                          "for counter runs")
     ap.add_argument("--roofline-kernel", default="gateup",
-                    choices=["qkv", "attn", "o", "gateup", "down", "vocab"])
+                    choices=["qkv", "attn", "o", "attn_o", "gateup", "down", "vocab"])
     ap.add_argument("--eager", action="store_true",
                     help="launch the step's kernels directly instead of replaying the captured graph "
                          "(same kernels; for profilers that cannot trace graph launches)")

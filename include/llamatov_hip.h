@@ -223,6 +223,34 @@ LT_API int lt_q8_gemv_rms_silu(lt_ctx* ctx, const float* x, const float* nw, flo
 LT_API int lt_q8_gemv_rms_swiglu(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* Wgu,
                                  float* v, int F, int K);
 
+/* ---- the four-launch step (no reference counterparts: each replaces a run of the
+ * launches above with the same bits) ----------------------------------------------------
+ * lt_q8_gemv_rms_rope_kv: lt_q8_gemv_rms (or lt_q8_gemv_embed_rms when emb is given: x is
+ * then ignored and the embedding row of *tok is written to x_out) of the q|k|v rows
+ * N = (nh + 2*nkv)*hd with the bias, then lt_rope_qk of the q and k heads at position *len
+ * and the k and v rows written into the caches at row *len (what lt_attn_step's append
+ * does), qkv receiving every row (q and k rotated).  *len is read, not changed. */
+LT_API int lt_q8_gemv_rms_rope_kv(lt_ctx* ctx, const float* x, const void* emb, const int* tok, int vocab,
+                                  float* x_out, int* err, const float* nw, float eps, const void* W,
+                                  const float* bias, float* qkv, int K, const float* freqs, void* kc, void* vc,
+                                  const int* len, int nh, int nkv, int hd, int maxt, int kv_dtype);
+
+/* lt_attn_step's masked attention (nsplit 1) over *len + 1 cache rows for the roped q in
+ * qkv, its quant, and the O GEMV + resid (y = O . Q8(attention) + resid), in one launch: every
+ * workgroup recomputes the attention of all heads (k_attn_decode_masked's order,
+ * bpd/lib/dev_residency.py:1955-2031) before folding its 32 O rows.  *len is read, not
+ * changed.  It attends at most lt_attn_o_max_len(nh, nkv, hd, kv_dtype) rows (0: the geometry
+ * is outside the kernel; hd must be 64 and nh*hd <= 1024); a launch that finds more rows
+ * writes NaN rows (callers check the length on the host). */
+LT_API int lt_attn_o_max_len(int nh, int nkv, int hd, int kv_dtype);
+LT_API int lt_q8_gemv_attn_o(lt_ctx* ctx, const float* qkv, const void* kc, const void* vc, const int* len, int nh,
+                             int nkv, int hd, float scale, int maxt, int kv_dtype, const void* W, const float* resid,
+                             float* y, int N);
+
+/* lt_q8_gemv_rms_silu, then *len += 1 (when < maxt) after the layer's attention has read it. */
+LT_API int lt_q8_gemv_rms_silu_len(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* Wgu,
+                                   int8_t* vq, uint16_t* vd, int F, int K, int* len, int maxt);
+
 /* Final norm -> quant -> vocab GEMV -> greedy argmax (_compute_folded_logits
  * bpd/lib/dev_residency.py:1596-1623 + argmax_dev :1074-1110): writes logits[N], then the
  * index of the maximum (ties to the lowest index) to *out, appending it to hist like

@@ -58,6 +58,12 @@ _SIGS = {
     "lt_q8_gemv_attn_out": (c_int, [_P, _P, _P, _P, c_size_t, c_int, c_int, c_int, _P, _P, _P, c_int, c_int,
                                     _P, c_int]),
     "lt_q8_gemv_rms_silu": (c_int, [_P, _P, _P, c_float, _P, _P, _P, c_int, c_int]),
+    "lt_q8_gemv_rms_rope_kv": (c_int, [_P, _P, _P, _P, c_int, _P, _P, _P, c_float, _P, _P, _P, c_int, _P, _P, _P,
+                                       _P, c_int, c_int, c_int, c_int, c_int]),
+    "lt_attn_o_max_len": (c_int, [c_int, c_int, c_int, c_int]),
+    "lt_q8_gemv_attn_o": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_float, c_int, c_int, _P, _P, _P,
+                                  c_int]),
+    "lt_q8_gemv_rms_silu_len": (c_int, [_P, _P, _P, c_float, _P, _P, _P, c_int, c_int, _P, c_int]),
     "lt_q8_gemv_rms_swiglu": (c_int, [_P, _P, _P, c_float, _P, _P, c_int, c_int]),
     "lt_q8_gemv_rms_argmax": (c_int, [_P, _P, _P, c_float, _P, _P, c_int, c_int, _P, _P, _P, c_int,
                                       _P, c_size_t]),

@@ -27,7 +27,7 @@ namespace {
 using namespace lt;
 
 enum Pro { PRO_STAGE = 0, PRO_QUANT = 1, PRO_RMS = 2, PRO_EMBED_RMS = 3, PRO_MERGE = 4 };
-enum Epi { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_ARGMAX = 3, EPI_SWIGLU = 4 };
+enum Epi { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_ARGMAX = 3, EPI_SWIGLU = 4, EPI_ROPE_KV = 5 };
 
 struct GemvParams {
   const uint8_t* W;
@@ -58,6 +58,14 @@ struct GemvParams {
   uint16_t* yd;
   float* pval;             // EPI_ARGMAX per-workgroup partials
   int* pidx;
+  // EPI_ROPE_KV: RoPE of the q and k heads at position *lenr (freqs [hd/2]), the k and v rows
+  // written into the caches at row *lenr (row stride nkv*hd; fp16 when kv_f16)
+  const float* freqs;
+  void* kc;
+  void* vc;
+  const int* lenr;
+  int nkv, kv_f16;
+  int* len_bump;           // any PRO but PRO_MERGE: block 0 bumps *len_bump (when < maxt) at its end
 };
 
 constexpr int kThreads = 256;
@@ -358,7 +366,18 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
   else if constexpr (PRO == PRO_EMBED_RMS) tok = *P.tok;
 
   // (2) the weights
-  const int rbase = blockIdx.x * P.row0 + hw;
+  // EPI_ROPE_KV: workgroup w holds 4 rotation pairs of one head (head w / (hd/8), pairs
+  // 4c .. 4c+3 with c = w % (hd/8)): half-waves 0-3 take rows j, half-waves 4-7 rows j + hd/2
+  auto row_of = [&](int h) {
+    if constexpr (EPI == EPI_ROPE_KV) {
+      const int hq = P.hd >> 3;
+      const int head = blockIdx.x / hq;
+      return head * P.hd + ((h & 4) ? (P.hd >> 1) : 0) + (blockIdx.x - head * hq) * 4 + (h & 3);
+    } else {
+      return blockIdx.x * P.row0 + h;
+    }
+  };
+  const int rbase = row_of(hw);
   const int step = P.step;
   const int nk = (nb + 31) >> 5;
   auto rows_from = [&](int r0) {
@@ -368,7 +387,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
   const int nrows = rows_from(rbase);
   const int total = nrows * nk;
   // the even half-wave of a wave has the most rows: its count makes the loop wave-uniform
-  const int trips = (rows_from(blockIdx.x * P.row0 + (hw & ~1)) * nk + D - 1) / D;
+  const int trips = (rows_from(row_of(hw & ~1)) * nk + D - 1) / D;
   const uint32_t row_step_bytes = (uint32_t)step * (uint32_t)nb * (uint32_t)kBlockBytes;
   constexpr uint32_t kSlotBytes = 32u * kBlockBytes;
   const uint32_t lane_bytes = (uint32_t)lane * (uint32_t)kBlockBytes;
@@ -409,14 +428,29 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
 #pragma unroll
     for (int d = 0; d < D; d++) issue(ring[d]);
   }
-  // the epilogue's residuals, fetched with the weights
+  // the epilogue's residuals (or biases), fetched with the weights
   float rpre[kResidPre];
-  if constexpr (EPI == EPI_RESID) {
-    const __amdgpu_buffer_rsrc_t rres = f32_rsrc(P.resid, P.N);
+  if constexpr (EPI == EPI_RESID || EPI == EPI_ROPE_KV) {
+    const __amdgpu_buffer_rsrc_t rres = f32_rsrc(P.resid, P.resid ? P.N : 0);
 #pragma unroll
     for (int i = 0; i < kResidPre; i++) {   // buffer loads: no branches, exact load counters
       const int off = (lane == 0 && i < nrows) ? (rbase + step * i) * 4 : (int)kNoBlock;
       rpre[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rres, off, 0, 0));
+    }
+  }
+  // EPI_ROPE_KV: the rotation of this workgroup's 4 pairs at position *lenr (k_rope's
+  // arithmetic), evaluated under the weight loads
+  __shared__ float s_rot[8];
+  __shared__ int s_pos;
+  if constexpr (EPI == EPI_ROPE_KV) {
+    if (threadIdx.x < 4) {
+      const int pos = *P.lenr;
+      const int j = (blockIdx.x - (blockIdx.x / (P.hd >> 3)) * (P.hd >> 3)) * 4 + threadIdx.x;
+      float sn, cs;
+      lt_sincosf((float)pos * P.freqs[j], &sn, &cs);
+      s_rot[threadIdx.x] = sn;
+      s_rot[4 + threadIdx.x] = cs;
+      if (threadIdx.x == 0) s_pos = pos;
     }
   }
   // @phase gemv 1
@@ -482,6 +516,10 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
   auto finish_row = [&](float a, int ri) {
     const float v = halfwave_tree_dpp(a);
     const int row = rbase + step * ri;
+    if constexpr (EPI == EPI_ROPE_KV) {   // one row per half-wave: the biased value to LDS
+      if (lane == 0 && ri < nrows) s_rows[hw] = P.resid ? v + rpre[0] : v;
+      return;
+    }
     if constexpr (EPI == EPI_SWIGLU) {
       // rows 2j (gate j) and 2j + 1 (up j) sit on the two half-waves of one wave, which
       // finish them together: lane 0 takes the up value from lane 32
@@ -551,6 +589,50 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
   }
 
   // @phase gemv 3
+  if constexpr (EPI == EPI_ROPE_KV) {
+    // x1 = row j, x2 = row j + hd/2: q and k heads rotate (fma(x1, c, -(x2*s)),
+    // fma(x1, s, x2*c)), v heads pass; all rows go to y; k and v rows also to the caches at
+    // row *lenr (a full cache is left unchanged)
+    __syncthreads();
+    if (threadIdx.x < 4) {
+      const int i = threadIdx.x;
+      const int hq = P.hd >> 3;
+      const int head = blockIdx.x / hq;
+      const int half = P.hd >> 1;
+      const int j = (blockIdx.x - head * hq) * 4 + i;
+      const int r1 = head * P.hd + j;
+      float x1 = s_rows[i], x2 = s_rows[i + 4];
+      if (head < P.nh + P.nkv) {
+        const float sn = s_rot[i], cs = s_rot[4 + i];
+        const float y1 = fmaf(x1, cs, -(x2 * sn));
+        const float y2 = fmaf(x1, sn, x2 * cs);
+        x1 = y1;
+        x2 = y2;
+      }
+      P.y[r1] = x1;
+      P.y[r1 + half] = x2;
+      const int L = s_pos;
+      if (head >= P.nh && L >= 0 && L < P.maxt) {
+        const bool isv = head >= P.nh + P.nkv;
+        const size_t off = (size_t)L * P.nkv * P.hd + (size_t)(head - P.nh - (isv ? P.nkv : 0)) * P.hd + j;
+        if (P.kv_f16) {
+          uint16_t* c = (uint16_t*)(isv ? P.vc : P.kc);
+          c[off] = lt_f2h(x1);
+          c[off + half] = lt_f2h(x2);
+        } else {
+          float* c = (float*)(isv ? P.vc : P.kc);
+          c[off] = x1;
+          c[off + half] = x2;
+        }
+      }
+    }
+  }
+  if constexpr (PRO != PRO_MERGE) {
+    if (P.len_bump && blockIdx.x == 0 && threadIdx.x == 0) {
+      const int L = *P.len_bump;
+      if (L >= 0 && L < P.maxt) *P.len_bump = L + 1;
+    }
+  }
   if constexpr (EPI == EPI_SILU) {
     // the workgroup's 64 rows are the gate/up pairs of one 32-element block: SiLU(g)*u
     // one pair per lane of half-wave 0, then k_silu_mul_quant's quantizer
@@ -575,6 +657,273 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
     }
   }
   // @phase gemv 4
+}
+
+// ---- attention recomputed in the O projection's prologue ----------------------------
+//
+// k_attn_o: one launch for k_attn_decode_masked (nsplit 1) -> quant -> O GEMV + residual
+// (bpd/lib/dev_residency.py:1420-1440), for at most AoLayout::kRows / nkv attended rows, where the
+// attention is a few microseconds of arithmetic: every workgroup computes the attention
+// output of all heads itself (q and the cache rows are small and come from L2), quantizes
+// it into the GEMV's activation records, and folds its 32 rows of the O matrix.  The O
+// weights, q, the length and the first kAoFirstL cache rows of K and V are all requested at
+// kernel start, so the launch waits for memory once (twice past kAoFirstL rows).  Each
+// value is the oracle's: scores are sequential fma chains over the head dims times scale;
+// max and Z are the 64-lane strided folds plus trees; exps by lt_expf; out = (sequential
+// fma chain over positions) / Z; then the engine quantizer and the canonical GEMV order.
+struct AttnOParams {
+  const float* qkv;      // roped q of the nh heads at [0, nh*hd)
+  const void* kc;        // caches [maxt][nkv*hd] (fp16 or fp32); this token's row is at *len
+  const void* vc;
+  const int* len;        // rows before this token's (attention covers *len + 1 rows)
+  int nh, nkv, maxt;
+  int maxL;              // rows the launch can attend: AoLayout::kRows / nkv
+  float scale;
+  const uint8_t* W;      // O projection: N rows of K = nh*hd (K <= 1024: one 32-block item per row)
+  const float* resid;
+  float* y;
+  int N;
+};
+
+constexpr int kAoThreads = 1024;
+constexpr int kAoRows = kAoThreads / 32;   // one O row per half-wave
+constexpr int kAoWaves = kAoThreads / 64;
+constexpr int kAoHd = 64;                  // head size: a wave's lanes are one head's dims
+constexpr int kAoFirstL = 128;             // rows requested before the length is known
+constexpr int kAoMaxHpw = 4;               // heads per thread (scores) and per wave (O chains)
+
+template <bool kF16>
+struct AoLayout {
+  static constexpr int kEsz = kF16 ? 2 : 4;
+  static constexpr int kRows = kF16 ? 512 : 256;    // staged (position, KV group) rows
+  static constexpr int kRowB = kAoHd * kEsz;        // one cache row of one KV group, bytes
+  static constexpr int kKRowB = kRowB + 16;         // staged K row: a 16-byte pad keeps a wave's rows on distinct banks
+  static constexpr size_t kKBytes = (size_t)kRows * kKRowB;   // K, group-major
+  // V position-major, [maxL][nkv][hd]: a wave's 64 lanes read one row's 64 dims at once
+  static __host__ __device__ size_t vbytes(int nkv, int maxL) { return (size_t)nkv * maxL * kRowB; }
+};
+constexpr size_t kAoLdsMax = (size_t)160 * 1024;   // LDS of one gfx950 workgroup
+
+template <bool kF16>
+size_t attn_o_lds_bytes(int nh, int nkv, int maxL) {
+  const int K = nh * kAoHd, nb = K / 32;
+  return (size_t)K * 4 + AoLayout<kF16>::kKBytes + AoLayout<kF16>::vbytes(nkv, maxL) + (size_t)nh * maxL * 4 + 64 +
+         (size_t)((nb * kRecDwords + 3) & ~3) * 4;
+}
+
+template <bool kF16>
+__device__ __forceinline__ float kv_elem(const uint8_t* p) {
+  if constexpr (kF16) return lt_h2f(*(const uint16_t*)p);
+  else return *(const float*)p;
+}
+
+// The cache rows [r0, r1) of K (group-major, padded rows) and V (position-major) into LDS:
+// 16-byte pieces, loaded first and stored after, so every load of the round is in flight.
+// A call stages at most kRows (position, group) rows.
+template <bool kF16>
+__device__ __forceinline__ void ao_stage(const AttnOParams& P, int r0, int r1, uint8_t* sK, uint8_t* sV) {
+  using Lo = AoLayout<kF16>;
+  constexpr int PPR = Lo::kRowB / 16;               // pieces per (position, group) row
+  constexpr int kMaxPer = (Lo::kRows * PPR + kAoThreads - 1) / kAoThreads;   // per thread, per tensor
+  const int nkv = P.nkv;
+  const int npieces = (r1 - r0) * nkv * PPR;
+  const uint8_t* kc = (const uint8_t*)P.kc + (size_t)r0 * nkv * Lo::kRowB;
+  const uint8_t* vc = (const uint8_t*)P.vc + (size_t)r0 * nkv * Lo::kRowB;
+  u32x4 kb[kMaxPer], vb[kMaxPer];
+#pragma unroll
+  for (int k = 0; k < kMaxPer; k++) {
+    const int i = threadIdx.x + k * kAoThreads;
+    if (i < npieces) {
+      kb[k] = *(const u32x4*)(kc + (size_t)i * 16);
+      vb[k] = *(const u32x4*)(vc + (size_t)i * 16);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kMaxPer; k++) {
+    const int i = threadIdx.x + k * kAoThreads;
+    if (i < npieces) {
+      const int rr = i / PPR, pc = i - rr * PPR;      // rr = (t - r0) * nkv + g
+      const int t = r0 + rr / nkv, g = rr - (rr / nkv) * nkv;
+      *(u32x4*)(sK + ((size_t)g * P.maxL + t) * Lo::kKRowB + pc * 16) = kb[k];
+      *(u32x4*)(sV + ((size_t)t * nkv + g) * Lo::kRowB + pc * 16) = vb[k];
+    }
+  }
+}
+
+template <bool kF16>
+__global__ __launch_bounds__(kAoThreads) void k_attn_o(AttnOParams P) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  using Lo = AoLayout<kF16>;
+  constexpr int HD = kAoHd;
+  const int nh = P.nh, nkv = P.nkv, rep = nh / nkv, K = nh * HD, nb = K >> 5, maxt = P.maxt;
+  float* sq = (float*)smem;                                    // [K] roped q
+  const int maxL = P.maxL;
+  uint8_t* sK = (uint8_t*)(sq + K);                            // [nkv][maxL] padded K rows
+  uint8_t* sV = sK + Lo::kKBytes;                              // [maxL][nkv] V rows
+  float* sS = (float*)(sV + Lo::vbytes(nkv, maxL));            // [nh][maxL] scores, then exps
+  float* sZ = sS + (size_t)nh * maxL;                          // [16]
+  uint32_t* rec = (uint32_t*)(sZ + 16);                        // [nb][kRecDwords]
+  __shared__ int s_len;
+  const int tid = threadIdx.x, lane = tid & 31, hw = tid >> 5, wl = tid & 63, wv = tid >> 6;
+
+  // (1) every request that does not depend on the length: this half-wave's O row, its
+  // residual, q, the length, and the first kAoFirstL rows of K and V
+  const int row = blockIdx.x * kAoRows + hw;
+  const uint32_t mat_bytes = (uint32_t)P.N * (uint32_t)nb * (uint32_t)kBlockBytes;
+  const __amdgpu_buffer_rsrc_t wrsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)P.W, 0, (int)((mat_bytes + 3u) & ~3u), 0x00020000);
+  const uint32_t off = (row < P.N && lane < nb) ? (uint32_t)row * (uint32_t)nb * kBlockBytes + (uint32_t)lane * kBlockBytes
+                                                : kNoBlock;
+  RawBlock rw;
+  {
+    const uint32_t o4 = off & ~3u;
+    const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)o4, 0, 0);
+    const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)(o4 + 16u), 0, 0);
+    rw.w[0] = v0.x; rw.w[1] = v0.y; rw.w[2] = v0.z; rw.w[3] = v0.w;
+    rw.w[4] = v1.x; rw.w[5] = v1.y; rw.w[6] = v1.z; rw.w[7] = v1.w;
+    rw.w[8] = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)(o4 + 32u), 0, 0);
+  }
+  const bool odd = (off & 2u) != 0;
+  const __amdgpu_buffer_rsrc_t rres = f32_rsrc(P.resid, P.resid ? P.N : 0);
+  const float rv = __builtin_bit_cast(
+      float, __builtin_amdgcn_raw_buffer_load_b32(rres, (lane == 0 && row < P.N) ? row * 4 : (int)kNoBlock, 0, 0));
+  if (tid == 0) s_len = *P.len;
+  for (int i = tid; i < K; i += kAoThreads) sq[i] = P.qkv[i];
+  int first = maxt < kAoFirstL ? maxt : kAoFirstL;
+  if (first > maxL) first = maxL;
+  ao_stage<kF16>(P, 0, first, sK, sV);
+  __syncthreads();
+  const int len0 = s_len;
+  const int L = len0 < 0 ? 0 : (len0 < maxt ? len0 + 1 : maxt);
+  if (L > maxL) {   // outside the launch's contract (the host checks): poison the rows
+    if (lane == 0 && row < P.N) P.y[row] = __builtin_nanf("");
+    return;
+  }
+  if (L > first) {
+    ao_stage<kF16>(P, first, L, sK, sV);
+    __syncthreads();
+  }
+
+  // (2) scores: thread (t, g, part) takes the K row of position t, group g (each value
+  // converted once) and runs the chains of heads part*hpt .. of the group; a wave's lanes
+  // are 64 positions of one (g, part), so every q read is a broadcast
+  const int parts = kAoThreads / (maxL * nkv) > 0 ? kAoThreads / (maxL * nkv) : 1;
+  const int hpt = (rep + parts - 1) / parts;
+  for (int i = tid; i < maxL * nkv * parts; i += kAoThreads) {
+    const int t = i % maxL, gp = i / maxL;
+    const int g = gp % nkv, part = gp / nkv;
+    const int h0 = g * rep + part * hpt;
+    const int nhh = t < L ? (rep - part * hpt < hpt ? rep - part * hpt : hpt) : 0;
+    if (nhh <= 0) continue;
+    const uint8_t* kr = sK + ((size_t)g * maxL + t) * Lo::kKRowB;
+    float sc[kAoMaxHpw] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int e0 = 0; e0 < HD; e0 += 16) {   // 16 dims at a time; each head's chain ascends
+      float kk[16];
+#pragma unroll
+      for (int u = 0; u < 16 * Lo::kEsz / 16; u++) {   // 16-byte reads of the row
+        const u32x4 w = *(const u32x4*)(kr + e0 * Lo::kEsz + u * 16);
+        if constexpr (kF16) {
+          const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+          for (int j = 0; j < 8; j++) kk[u * 8 + j] = lt_h2f((uint16_t)(ww[j >> 1] >> (16 * (j & 1))));
+        } else {
+          // not __builtin_bit_cast(float, w.y): this hipcc lowers a bit_cast of a vector
+          // element to element 0 (every kk would be w.x)
+          kk[u * 4 + 0] = __uint_as_float(w.x);
+          kk[u * 4 + 1] = __uint_as_float(w.y);
+          kk[u * 4 + 2] = __uint_as_float(w.z);
+          kk[u * 4 + 3] = __uint_as_float(w.w);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kAoMaxHpw; k++) {
+        if (k < nhh) {
+          const float* qh = sq + (h0 + k) * HD + e0;
+#pragma unroll
+          for (int e = 0; e < 16; e += 4) {
+            const f32x4 q4 = *(const f32x4*)(qh + e);
+            sc[k] = fmaf(q4.x, kk[e], sc[k]);
+            sc[k] = fmaf(q4.y, kk[e + 1], sc[k]);
+            sc[k] = fmaf(q4.z, kk[e + 2], sc[k]);
+            sc[k] = fmaf(q4.w, kk[e + 3], sc[k]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kAoMaxHpw; k++)
+      if (k < nhh) sS[(h0 + k) * maxL + t] = sc[k] * P.scale;
+  }
+  __syncthreads();
+
+  // (3) softmax statistics, one wave per head: m and Z folded over lanes t mod 64
+  for (int h = wv; h < nh; h += kAoWaves) {
+    float* sh = sS + h * maxL;
+    float m = -1e30f;
+    for (int t = wl; t < L; t += 64) m = fmaxf(m, sh[t]);
+    m = wave_max(m);
+    float z = 0.0f;
+    for (int t = wl; t < L; t += 64) {
+      const float e = lt_expf(sh[t] - m);
+      sh[t] = e;
+      z = z + e;
+    }
+    z = wave_tree_dpp(z);
+    if (wl == 0) sZ[h] = z;
+  }
+  __syncthreads();
+
+  // (4) O chains: wave (g, part) takes heads part*hpw .. of group g, lane = head dim; the
+  // wave reads one staged V row (64 dims) per position, 8 positions per round, each value
+  // converted once for the wave's heads
+  const int wpg0 = kAoWaves / nkv;
+  const int wpg = wpg0 < rep ? wpg0 : rep;                    // waves per KV group
+  const int hpw = (rep + wpg - 1) / wpg;
+  const int og = wv / wpg, opart = wv - og * wpg;
+  const int oh0 = og * rep + opart * hpw;
+  const int onh = og < nkv ? (rep - opart * hpw < hpw ? rep - opart * hpw : hpw) : 0;
+  float acc[kAoMaxHpw] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (onh > 0) {
+    const uint8_t* vr = sV + (size_t)og * Lo::kRowB + wl * Lo::kEsz;
+    const size_t vstride = (size_t)nkv * Lo::kRowB;
+    int t = 0;
+    for (; t + 8 <= L; t += 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = kv_elem<kF16>(vr + (t + j) * vstride);
+#pragma unroll
+      for (int k = 0; k < kAoMaxHpw; k++)
+        if (k < onh) {
+          const f32x4 e0 = *(const f32x4*)(sS + (oh0 + k) * maxL + t);
+          const f32x4 e1 = *(const f32x4*)(sS + (oh0 + k) * maxL + t + 4);
+          acc[k] = fmaf(e0.x, v[0], acc[k]);
+          acc[k] = fmaf(e0.y, v[1], acc[k]);
+          acc[k] = fmaf(e0.z, v[2], acc[k]);
+          acc[k] = fmaf(e0.w, v[3], acc[k]);
+          acc[k] = fmaf(e1.x, v[4], acc[k]);
+          acc[k] = fmaf(e1.y, v[5], acc[k]);
+          acc[k] = fmaf(e1.z, v[6], acc[k]);
+          acc[k] = fmaf(e1.w, v[7], acc[k]);
+        }
+    }
+    for (; t < L; t++) {
+      const float v = kv_elem<kF16>(vr + t * vstride);
+#pragma unroll
+      for (int k = 0; k < kAoMaxHpw; k++)
+        if (k < onh) acc[k] = fmaf(sS[(oh0 + k) * maxL + t], v, acc[k]);
+    }
+  }
+  // (5) out = O / Z, quantized into the GEMV's records (half-wave = one 32-element block)
+#pragma unroll
+  for (int k = 0; k < kAoMaxHpw; k++)
+    if (k < onh) quant_to_rec(acc[k] / sZ[oh0 + k], lane, rec + (2 * (oh0 + k) + (wl >> 5)) * kRecDwords);
+  __syncthreads();
+
+  // (6) the O row: lane L folds block L, the half-wave tree, + residual
+  const float folded = fold_raw(rw, odd, rec + (lane < nb ? lane : 0) * kRecDwords, 0.0f);
+  const float v = halfwave_tree_dpp(lane < nb ? folded : 0.0f);
+  if (lane == 0 && row < P.N) P.y[row] = P.resid ? v + rv : v;
 }
 
 // Reduce G argmax partials (ties to the lowest index) and publish the token; optionally
@@ -685,6 +1034,9 @@ hipError_t launch_gemv_k(GemvParams P, size_t shm, hipStream_t st, int num_cus, 
     P.row0 = kSiluRows; P.step = 8; P.max_rows = kSiluRows / 8;
     grid = P.N / kSiluRows;
     stg = one_item;
+  } else if (EPI == EPI_ROPE_KV) {
+    P.row0 = 8; P.step = 8; P.max_rows = 1;   // the row mapping is the kernel's own (4 pairs of a head)
+    grid = P.N / 8;
   } else if (env_rows() > 0) {
     const int R = env_rows();
     P.row0 = R; P.step = 8; P.max_rows = R / 8;
@@ -733,7 +1085,8 @@ hipError_t launch_gemv(const GemvParams& P, lt_ctx* ctx, int* grid_out) {
   // ring depth: 2 when a half-wave has at most 2 blocks to stream, else 8 (4 for the
   // register-heavy K > 4096 prologues)
   const int nk = (P.K / 32 + 31) / 32;
-  const bool shallow = EPI != EPI_SILU && env_rows() == 0 && (P.N + 7) / 8 <= 1024 && nk <= 2;
+  const bool shallow = EPI != EPI_SILU && (env_rows() == 0 || EPI == EPI_ROPE_KV) && (P.N + 7) / 8 <= 1024 &&
+                       nk <= 2;
   if constexpr (PRO == PRO_STAGE) {
     return shallow ? launch_gemv_k<1, PRO, EPI, 2>(P, shm, st, ncu, grid_out)
                    : launch_gemv_k<1, PRO, EPI, 8>(P, shm, st, ncu, grid_out);
@@ -756,6 +1109,22 @@ int check_gemv(const char* fn, const void* W, int N, int K) {
              "%s: a %d x %d Q8_0 matrix must be below 4 GiB (split it by rows)", fn, N, K);
   LT_REQUIRE(lt_aligned(W, 4), "%s: W must be 4-byte aligned", fn);
   return LT_OK;
+}
+
+// Rows the fused attention + O launch attends at most (0: the geometry is outside it).
+template <bool kF16>
+int attn_o_max_len(int nh, int nkv, int hd) {
+  using Lo = AoLayout<kF16>;
+  if (nh <= 0 || nkv <= 0 || nh % nkv || hd != kAoHd || nh * hd > 1024) return 0;   // one block item per O row
+  const int rep = nh / nkv;
+  const int maxL = Lo::kRows / nkv / 8 * 8;
+  if (maxL < 8 || attn_o_lds_bytes<kF16>(nh, nkv, maxL) > kAoLdsMax) return 0;
+  const int wpg0 = kAoWaves / nkv;
+  const int wpg = wpg0 < rep ? wpg0 : rep;
+  if (wpg < 1 || (rep + wpg - 1) / wpg > kAoMaxHpw) return 0;
+  const int parts = kAoThreads / (maxL * nkv) > 0 ? kAoThreads / (maxL * nkv) : 1;
+  if ((rep + parts - 1) / parts > kAoMaxHpw) return 0;
+  return maxL;
 }
 
 int finish(hipError_t e, const char* kernel) {
@@ -862,6 +1231,67 @@ int lt_q8_gemv_rms_swiglu(lt_ctx* ctx, const float* x, const float* nw, float ep
   GemvParams P{};
   P.W = (const uint8_t*)Wgu; P.N = 2 * F; P.K = K; P.x = x; P.nw = nw; P.eps = eps; P.y = v;
   return finish(launch_gemv<PRO_RMS, EPI_SWIGLU>(P, ctx, nullptr), "k_gemv_fused<rms,swiglu>");
+}
+
+int lt_q8_gemv_rms_rope_kv(lt_ctx* ctx, const float* x, const void* emb, const int* tok, int vocab, float* x_out,
+                           int* err, const float* nw, float eps, const void* W, const float* bias, float* qkv, int K,
+                           const float* freqs, void* kc, void* vc, const int* len, int nh, int nkv, int hd,
+                           int maxt, int kv_dtype) {
+  LT_REQUIRE(ctx && nw && qkv && freqs && kc && vc && len, "lt_q8_gemv_rms_rope_kv: null argument");
+  LT_REQUIRE(emb ? (tok && x_out && vocab > 0 && K <= 4096) : x != nullptr,
+             "lt_q8_gemv_rms_rope_kv: needs x, or emb + tok + x_out + vocab with K <= 4096");
+  LT_REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && hd > 0 && hd % 8 == 0 && maxt > 0,
+             "lt_q8_gemv_rms_rope_kv: nh=%d nkv=%d hd=%d maxt=%d", nh, nkv, hd, maxt);
+  LT_REQUIRE(kv_dtype == LT_KV_F32 || kv_dtype == LT_KV_F16, "lt_q8_gemv_rms_rope_kv: kv_dtype=%d", kv_dtype);
+  const int N = (nh + 2 * nkv) * hd;
+  if (int rc = check_gemv("lt_q8_gemv_rms_rope_kv", W, N, K)) return rc;
+  GemvParams P{};
+  P.W = (const uint8_t*)W; P.N = N; P.K = K; P.x = x; P.nw = nw; P.eps = eps; P.resid = bias; P.y = qkv;
+  P.emb = (const uint8_t*)emb; P.tok = tok; P.vocab = vocab; P.x_out = x_out; P.err = err;
+  P.freqs = freqs; P.kc = kc; P.vc = vc; P.lenr = len; P.nh = nh; P.nkv = nkv; P.hd = hd; P.maxt = maxt;
+  P.kv_f16 = kv_dtype == LT_KV_F16;
+  hipError_t e = emb ? launch_gemv<PRO_EMBED_RMS, EPI_ROPE_KV>(P, ctx, nullptr)
+                     : launch_gemv<PRO_RMS, EPI_ROPE_KV>(P, ctx, nullptr);
+  return finish(e, "k_gemv_fused<rms,rope_kv>");
+}
+
+int lt_q8_gemv_rms_silu_len(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* Wgu, int8_t* vq,
+                            uint16_t* vd, int F, int K, int* len, int maxt) {
+  LT_REQUIRE(ctx && x && nw && vq && vd && len, "lt_q8_gemv_rms_silu_len: null argument");
+  LT_REQUIRE(F > 0 && F % 32 == 0 && maxt > 0, "lt_q8_gemv_rms_silu_len: F=%d maxt=%d", F, maxt);
+  if (int rc = check_gemv("lt_q8_gemv_rms_silu_len", Wgu, 2 * F, K)) return rc;
+  GemvParams P{};
+  P.W = (const uint8_t*)Wgu; P.N = 2 * F; P.K = K; P.x = x; P.nw = nw; P.eps = eps; P.yq = vq; P.yd = vd;
+  P.len_bump = len; P.maxt = maxt;
+  return finish(launch_gemv<PRO_RMS, EPI_SILU>(P, ctx, nullptr), "k_gemv_fused<rms,silu,len>");
+}
+
+int lt_attn_o_max_len(int nh, int nkv, int hd, int kv_dtype) {
+  if (kv_dtype == LT_KV_F16) return attn_o_max_len<true>(nh, nkv, hd);
+  if (kv_dtype == LT_KV_F32) return attn_o_max_len<false>(nh, nkv, hd);
+  return 0;
+}
+
+int lt_q8_gemv_attn_o(lt_ctx* ctx, const float* qkv, const void* kc, const void* vc, const int* len, int nh, int nkv,
+                      int hd, float scale, int maxt, int kv_dtype, const void* W, const float* resid, float* y,
+                      int N) {
+  LT_REQUIRE(ctx && qkv && kc && vc && len && y, "lt_q8_gemv_attn_o: null argument");
+  LT_REQUIRE(kv_dtype == LT_KV_F32 || kv_dtype == LT_KV_F16, "lt_q8_gemv_attn_o: kv_dtype=%d", kv_dtype);
+  const int maxL = lt_attn_o_max_len(nh, nkv, hd, kv_dtype);
+  LT_REQUIRE(maxL > 0 && maxt > 0,
+             "lt_q8_gemv_attn_o: nh=%d nkv=%d hd=%d kv_dtype=%d is outside the fused kernel (hd 64, nh*hd <= 1024); "
+             "use lt_attn_step + lt_q8_gemv_attn_out", nh, nkv, hd, kv_dtype);
+  LT_REQUIRE(lt_aligned(kc, 16) && lt_aligned(vc, 16), "lt_q8_gemv_attn_o: caches must be 16-byte aligned");
+  if (int rc = check_gemv("lt_q8_gemv_attn_o", W, N, nh * hd)) return rc;
+  AttnOParams P{};
+  P.qkv = qkv; P.kc = kc; P.vc = vc; P.len = len; P.nh = nh; P.nkv = nkv; P.maxt = maxt; P.scale = scale;
+  P.W = (const uint8_t*)W; P.resid = resid; P.y = y; P.N = N; P.maxL = maxL;
+  const int grid = (N + kAoRows - 1) / kAoRows;
+  if (kv_dtype == LT_KV_F16)
+    k_attn_o<true><<<grid, kAoThreads, attn_o_lds_bytes<true>(nh, nkv, maxL), ctx->stream>>>(P);
+  else
+    k_attn_o<false><<<grid, kAoThreads, attn_o_lds_bytes<false>(nh, nkv, maxL), ctx->stream>>>(P);
+  return finish(hipGetLastError(), "k_attn_o");
 }
 
 size_t lt_q8_gemv_argmax_workspace_size(int N) {

@@ -424,6 +424,14 @@ class Profile:
     # (lt_q8_gemv_rms_silu).  Same bits; False is faster at C2 (gate|up 6.0 vs 7.6 us, down
     # 5.1 vs 6.1 us: more workgroups repeat the RMSNorm prologue, whose latency bounds them)
     swiglu_fp32: bool = False
+    # fused step, nsplit 1: four launches per layer while the fused attention kernel applies
+    # (head dim 64, at most lt_attn_o_max_len attended rows): QKV + RoPE + KV append
+    # (lt_q8_gemv_rms_rope_kv), attention recomputed in the O GEMV's prologue
+    # (lt_q8_gemv_attn_o), gate|up + the length bump, down; past that length, and otherwise,
+    # the five launches (same bits).  Off by default: recomputing all heads' attention on
+    # each workgroup's CU measured slower at C2 than the separate attention launch, which
+    # spreads the heads over 14 CUs
+    attn_in_o: bool = False
     fused_rms_quant: bool = False   # per-op path only: k_rms_quant instead of k_rmsnorm + k_quant_q8
     graph: bool = True
 
@@ -660,14 +668,15 @@ class DecodePlan:
         return self.dev.d2h(out, self.lens.ptr)
 
     # -- the step ----------------------------------------------------------------
-    def enqueue_step(self) -> None:
-        """Launch one decode token (fused or per-op, as the profile says)."""
+    def enqueue_step(self, four: bool | None = None) -> None:
+        """Launch one decode token (fused or per-op, as the profile says).  four selects the
+        four-launch fused step (default: when the current length allows it)."""
         if self.profile.fused_step:
-            self._enqueue_fused()
+            self._enqueue_fused(self.four_launch if four is None else four)
         else:
             self._enqueue_per_op()
 
-    def _enqueue_fused(self) -> None:
+    def _enqueue_fused(self, four: bool = False) -> None:
         """Five launches per layer (lt_fused.hip), then the vocab GEMV with its argmax:
         the same arithmetic as _enqueue_per_op, bit for bit.
           QKV   rmsnorm -> quant -> GEMV + bias        (layer 0: from the embedding of tok)
@@ -679,6 +688,11 @@ class DecodePlan:
         h = self.dev.handle
         E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
         eps = ctypes.c_float(cfg.norm_eps)
+        if four:
+            if self.four_launch_len <= 0:
+                raise ValueError("the four-launch step does not apply to this profile or geometry")
+            self._enqueue_four()
+            return
         ws, ws_n = _vp(self.attn_ws), (self.attn_ws.nbytes if self.attn_ws is not None else 0)
         for il, L in enumerate(m.layers):
             cache = self.caches[il]
@@ -703,6 +717,52 @@ class DecodePlan:
                 call("lt_q8_gemv_rms_silu", h, self.xres.vp, L["ffn_norm"].vp, eps, L["wgu_il"].t.vp,
                      self.xq.vp, self.xd.vp, F, E)
                 call("lt_q8_gemv", h, L["wdown"].t.vp, self.xq.vp, self.xd.vp, self.xres.vp, self.carry.vp, E, F)
+        call("lt_q8_gemv_rms_argmax", h, self.carry.vp, m.output_norm.vp, eps, m.output.t.vp, self.logits.vp,
+             cfg.vocab, E, self.tok.vp, self.hist.vp, self.hist_count.vp, self.hist_cap,
+             self.am_ws.vp, self.am_ws.nbytes)
+
+    @property
+    def four_launch_len(self) -> int:
+        """Cache lengths up to which a step runs four launches per layer (the next token's
+        attention covers length + 1 <= this many rows); 0 when the profile or the geometry
+        keeps every step at five launches."""
+        p, cfg = self.profile, self.cfg
+        if not (p.fused_step and p.attn_in_o and p.attn_nsplit == 1 and not p.swiglu_fp32):
+            return 0
+        n = int(_lib.raw("lt_attn_o_max_len")(cfg.n_head, cfg.n_head_kv, cfg.head_dim, p.kv_dtype))
+        return min(n, self.max_ctx) if n > 0 else 0
+
+    @property
+    def four_launch(self) -> bool:
+        """The next step (at the current host length) runs four launches per layer."""
+        return self.caches[0].length + 1 <= self.four_launch_len
+
+    def _enqueue_four(self) -> None:
+        """Four launches per layer, the same bits as the five-launch step:
+          QKV   rmsnorm -> quant -> GEMV + bias -> RoPE(q, k) -> k, v into the caches at *len
+          O     attention over *len + 1 rows (every workgroup) -> quant -> O GEMV + x
+          FFN1  rmsnorm -> quant -> gate|up GEMV -> SiLU(g)*u -> quant; *len += 1
+          FFN2  down GEMV + xres"""
+        cfg, m, p = self.cfg, self.model, self.profile
+        h = self.dev.handle
+        E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
+        eps = ctypes.c_float(cfg.norm_eps)
+        scale = ctypes.c_float(self.scale)
+        for il, L in enumerate(m.layers):
+            cache = self.caches[il]
+            lp = _vp(cache.len_ptr)
+            x = self.resid_in if il == 0 else self.carry
+            gather = il == 0 and not self.host_embed
+            call("lt_q8_gemv_rms_rope_kv", h, None if gather else x.vp,
+                 m.tok_embd.t.vp if gather else None, self.tok.vp if gather else None, cfg.vocab,
+                 self.resid_in.vp if gather else None, self.err.vp, L["attn_norm"].vp, eps, L["wqkv"].t.vp,
+                 _vp(L["bqkv"]), self.qkv.vp, E, m.freqs.vp, cache.k.vp, cache.v.vp, lp, nh, nkv, hd,
+                 cache.max_seq, p.kv_dtype)
+            call("lt_q8_gemv_attn_o", h, self.qkv.vp, cache.k.vp, cache.v.vp, lp, nh, nkv, hd, scale,
+                 cache.max_seq, p.kv_dtype, L["wo"].t.vp, x.vp, self.xres.vp, E)
+            call("lt_q8_gemv_rms_silu_len", h, self.xres.vp, L["ffn_norm"].vp, eps, L["wgu_il"].t.vp,
+                 self.xq.vp, self.xd.vp, F, E, lp, cache.max_seq)
+            call("lt_q8_gemv", h, L["wdown"].t.vp, self.xq.vp, self.xd.vp, self.xres.vp, self.carry.vp, E, F)
         call("lt_q8_gemv_rms_argmax", h, self.carry.vp, m.output_norm.vp, eps, m.output.t.vp, self.logits.vp,
              cfg.vocab, E, self.tok.vp, self.hist.vp, self.hist_count.vp, self.hist_cap,
              self.am_ws.vp, self.am_ws.nbytes)
@@ -900,7 +960,8 @@ class StepGraph:
     def __init__(self, plan: DecodePlan):
         self.plan = plan
         self.dev = plan.dev
-        self.graph = ctypes.c_void_p()
+        self.graph = ctypes.c_void_p()    # the five-launch step (every length)
+        self.graph4 = ctypes.c_void_p()   # the four-launch step (lengths up to plan.four_launch_len)
         self.captured = False
 
     def seed(self, prompt, batched: bool = False, embeddings: np.ndarray | None = None) -> np.ndarray:
@@ -915,26 +976,39 @@ class StepGraph:
         self.dev.sync()
         return logits
 
-    def capture(self) -> None:
-        if self.captured:
-            raise RuntimeError("StepGraph.capture: already captured")
+    def _capture_one(self, out: ctypes.c_void_p, four: bool) -> None:
         call("lt_graph_begin", self.dev.handle)
         try:
-            self.plan.enqueue_step()
+            self.plan.enqueue_step(four=four)
         except Exception:
             g = ctypes.c_void_p()
             _lib.raw("lt_graph_end")(self.dev.handle, ctypes.byref(g))
             if g.value:
                 _lib.raw("lt_graph_free")(g)
             raise
-        call("lt_graph_end", self.dev.handle, ctypes.byref(self.graph))
+        call("lt_graph_end", self.dev.handle, ctypes.byref(out))
+
+    def capture(self) -> None:
+        """Record the step: the five-launch graph, and when the plan has one, the four-launch
+        graph that replays take while the cache is short enough for it."""
+        if self.captured:
+            raise RuntimeError("StepGraph.capture: already captured")
+        self._capture_one(self.graph, False)
+        if self.plan.four_launch_len > 0 and self.plan.profile.fused_step:
+            try:
+                self._capture_one(self.graph4, True)
+            except Exception:
+                _lib.raw("lt_graph_free")(self.graph)
+                self.graph = ctypes.c_void_p()
+                raise
         self.captured = True
 
     def _launch(self) -> None:
         if not self.captured:
             raise RuntimeError("call capture() before replay")
         self.plan.check_room(1)
-        call("lt_graph_launch", self.dev.handle, self.graph)
+        g = self.graph4 if self.graph4.value and self.plan.four_launch else self.graph
+        call("lt_graph_launch", self.dev.handle, g)
         for c in self.plan.caches:
             c.length += 1
 
@@ -975,6 +1049,10 @@ class StepGraph:
     def free(self) -> None:
         if self.captured:
             call("lt_graph_free", self.graph)
+            if self.graph4.value:
+                call("lt_graph_free", self.graph4)
+            self.graph = ctypes.c_void_p()
+            self.graph4 = ctypes.c_void_p()
             self.captured = False
 
 

@@ -65,6 +65,44 @@ def test_tiny_stepwise_logits_bitexact(gpu, oracle, step, kv_dtype, nsplit, fuse
     plan.free()
 
 
+@pytest.mark.parametrize("kv_dtype", [LT_KV_F32, LT_KV_F16])
+@pytest.mark.parametrize("four", [True, False])
+def test_small_qwen_four_launch_step_bitexact(gpu, oracle, kv_dtype, four):
+    """The four-launch step (attention inside the O GEMV, RoPE + KV append in the QKV GEMV)
+    and the five-launch step against the oracle's step, logits and KV rows, over 40 steps
+    (head dim 64: the fused attention applies)."""
+    cfg = M.SMALL_QWEN
+    case(f"small-qwen stepwise four={four} kv={kv_dtype}")
+    plan = dr.DecodePlan(resident(cfg, gpu), dr.Profile(kv_dtype=kv_dtype, attn_in_o=four))
+    assert plan.four_launch == four
+    orc = oracle.OracleModel(cfg, weights(cfg), kv_f16=kv_dtype == LT_KV_F16)
+    toks = M.random_prompt(cfg, 5, seed=13)
+    for i in range(40):
+        t = toks[i] if i < len(toks) else int(np.argmax(exp))
+        plan.step(t)
+        exp = orc.step(t)
+        assert bitexact(plan.read_logits(), exp), f"step {i}"
+    assert list(plan.lengths()) == [40] * cfg.n_layers
+    for il in range(cfg.n_layers):
+        for which in "kv":
+            assert np.array_equal(plan.caches[il].rows_host(which, 40), orc.kv_rows(il, which, 40))
+    # graph replays of the same step continue the oracle's greedy chain, bit for bit (the
+    # four-launch graph while the cache is short enough, the five-launch one after)
+    gr = dr.StepGraph(plan)
+    gr.capture()
+    seq = gr.replay_tokens(6)
+    ref = []
+    t = int(np.argmax(exp))
+    for _ in range(6):
+        exp = orc.step(t)
+        t = int(np.argmax(exp))
+        ref.append(t)
+    assert seq == ref
+    assert bitexact(plan.read_logits(), exp)
+    gr.free()
+    plan.free()
+
+
 @pytest.mark.parametrize("nsplit", [1, 8])
 def test_graph_replay_equals_eager(gpu, nsplit):
     """GR gate: graph replay is bit-identical to the eager step, device length advances,
@@ -152,5 +190,31 @@ def test_greedy_tokens_identical(gpu, oracle, cfg_name, n_prompt, n_gen, kv_dtyp
     got = [first] + gr.replay_tokens(n_gen - 1)
     print(f"[margins] min top1-top2 margin {float(margins.min()):.3e}", flush=True)
     assert got == exp
+    gr.free()
+    plan.free()
+
+
+def test_step_switches_from_four_to_five_launches(gpu, oracle):
+    """A decode that crosses the four-launch step's length limit: the graph replays switch to
+    the five-launch graph there, and every token's logits equal the oracle's."""
+    cfg = M.SMALL_QWEN.replace(max_ctx=512)
+    case("four -> five launch switch")
+    w = weights(M.SMALL_QWEN)
+    plan = dr.DecodePlan(dr.ResidentModel(cfg, w, gpu, layouts="fused"),
+                         dr.Profile(kv_dtype=LT_KV_F16, attn_in_o=True))
+    lim = plan.four_launch_len
+    assert 0 < lim < 400
+    orc = oracle.OracleModel(cfg, w, kv_f16=True)
+    prompt = M.random_prompt(cfg, lim - 5, seed=3)
+    dr.forward_prefill(plan, prompt)
+    for t in prompt:
+        exp = orc.step(t)
+    gr = dr.StepGraph(plan)
+    gr.capture()
+    for i in range(12):     # lengths lim-5 .. lim+6: both graphs
+        t = int(np.argmax(exp))
+        lg = gr.replay_logits(t)
+        exp = orc.step(t)
+        assert bitexact(lg, exp), f"replay {i} at length {plan.caches[0].length}"
     gr.free()
     plan.free()

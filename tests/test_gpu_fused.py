@@ -313,3 +313,111 @@ def test_q8_gemv_rms_argmax(gpu, oracle):
         call("lt_q8_gemv_rms_argmax", gpu.handle, dx.vp, dnw.vp, ctypes.c_float(1e-6), up(W2).vp, logits.vp, N, K,
              out.vp, None, None, 0, ws.vp, ws.nbytes)
         assert int(out.to_host()[0]) == oracle.argmax(e2) == min(lo, hi, oracle.argmax(e2))
+
+
+# ---- the four-launch step's launchers ---------------------------------------------------
+@pytest.mark.parametrize("nh,nkv,hd,E", [(14, 2, 64, 896), (32, 8, 128, 4096), (4, 2, 32, 128), (8, 1, 64, 512)])
+@pytest.mark.parametrize("kv_dtype", [LT_KV_F16, LT_KV_F32])
+@pytest.mark.parametrize("embed", [False, True])
+def test_q8_gemv_rms_rope_kv(gpu, oracle, nh, nkv, hd, E, kv_dtype, embed):
+    """QKV GEMV + bias, RoPE of q and k at position *len, k and v into the caches at row
+    *len: the oracle's rms -> quant -> gemv(+bias) -> rope -> append, bit for bit."""
+    case(f"rms_rope_kv nh={nh} nkv={nkv} hd={hd} E={E} kv={kv_dtype} embed={embed}")
+    rng = np.random.default_rng(nh * hd + E)
+    f16 = kv_dtype == LT_KV_F16
+    N = (nh + 2 * nkv) * hd
+    W = rand_weight(rng, N, E)
+    bias = (rng.standard_normal(N) * 0.5).astype(np.float32) if nh != 8 else None
+    nw = (0.5 * rng.standard_normal(E) + 1.0).astype(np.float32)
+    theta, eps, maxt, pos = 1e6, 1e-6, 64, 37
+    emb = rand_weight(rng, 50, E)
+    tok = 13
+    x = oracle.embed_row(emb, tok, E) if embed else (2.0 * rng.standard_normal(E)).astype(np.float32)
+    xq, xd = oracle.quant_q8(oracle.rmsnorm(x, nw, eps))
+    y = oracle.q8_gemv(W, xq, xd, E, bias)
+    qk = oracle.rope(y[:(nh + nkv) * hd], pos, nh + nkv, hd, theta)
+    exp = np.concatenate([qk, y[(nh + nkv) * hd:]])
+    width = nkv * hd
+    kc0 = rng.standard_normal((maxt, width), dtype=np.float32)
+    vc0 = rng.standard_normal((maxt, width), dtype=np.float32)
+    if f16:
+        kc0, vc0 = kc0.astype(np.float16).view(np.uint16), vc0.astype(np.float16).view(np.uint16)
+    dk, dv, dlen = up(kc0), up(vc0), up(np.array([pos], np.int32))
+    out, xo, err = empty((N,), np.float32), empty((E,), np.float32), up(np.zeros(1, np.int32))
+    freqs = up(dr.rope_freqs(hd, theta))
+    call("lt_q8_gemv_rms_rope_kv", gpu.handle, None if embed else up(x).vp, up(emb).vp if embed else None,
+         up(np.array([tok], np.int32)).vp if embed else None, 50, xo.vp if embed else None, err.vp, up(nw).vp,
+         ctypes.c_float(eps), up(W).vp, up(bias).vp if bias is not None else None, out.vp, E, freqs.vp,
+         dk.vp, dv.vp, dlen.vp, nh, nkv, hd, maxt, kv_dtype)
+    assert_bitexact(out.to_host(), exp, "qkv")
+    ek, ev = kc0.copy(), vc0.copy()
+    krow, vrow = exp[nh * hd:(nh + nkv) * hd], exp[(nh + nkv) * hd:]
+    ek[pos] = krow.astype(np.float16).view(np.uint16) if f16 else krow
+    ev[pos] = vrow.astype(np.float16).view(np.uint16) if f16 else vrow
+    assert np.array_equal(dk.to_host(), ek) and np.array_equal(dv.to_host(), ev)
+    assert dlen.to_host()[0] == pos
+    if embed:
+        assert_bitexact(xo.to_host(), x, "embedding row")
+
+
+@pytest.mark.parametrize("nh,nkv", [(14, 2), (8, 8), (10, 2), (4, 1), (12, 4)])
+@pytest.mark.parametrize("kv_dtype", [LT_KV_F16, LT_KV_F32])
+def test_q8_gemv_attn_o(gpu, oracle, nh, nkv, kv_dtype):
+    """Attention over *len + 1 rows recomputed in the O GEMV's prologue: the oracle's masked
+    attention -> quant -> O GEMV + residual, bit for bit, at lengths across the staging,
+    lane-fold and 8-row boundaries up to the launch's limit, NaN past the length; past the
+    limit the rows come back NaN."""
+    hd, maxt, E = 64, 1024, 768
+    f16 = kv_dtype == LT_KV_F16
+    maxL = _lib.raw("lt_attn_o_max_len")(nh, nkv, hd, kv_dtype)
+    assert maxL >= 32
+    rng = np.random.default_rng(nh * 10 + nkv)
+    K = nh * hd
+    W = rand_weight(rng, E, K)
+    dW = up(W)
+    r = rng.standard_normal(E).astype(np.float32)
+    dr_ = up(r)
+    scale = float(hd ** -0.5)
+    lens = sorted({L for L in (1, 2, 7, 8, 9, 63, 64, 65, 127, 128, 129, 200, maxL - 1, maxL) if 1 <= L <= maxL})
+    for L in lens + [maxL + 1]:
+        case(f"attn_o nh={nh} nkv={nkv} kv={kv_dtype} L={L} (max {maxL})")
+        q = rng.standard_normal(K, dtype=np.float32)
+        kc = rng.standard_normal((maxt, nkv * hd), dtype=np.float32)
+        vc = rng.standard_normal((maxt, nkv * hd), dtype=np.float32)
+        kc[L:] = np.nan
+        vc[L:] = np.nan
+        if f16:
+            kc, vc = kc.astype(np.float16).view(np.uint16), vc.astype(np.float16).view(np.uint16)
+        y = empty((E,), np.float32)
+        dlen = up(np.array([L - 1], np.int32))
+        call("lt_q8_gemv_attn_o", gpu.handle, up(q).vp, up(kc).vp, up(vc).vp, dlen.vp, nh, nkv, hd,
+             ctypes.c_float(scale), maxt, kv_dtype, dW.vp, dr_.vp, y.vp, E)
+        if L > maxL:
+            assert np.all(np.isnan(y.to_host()))
+            continue
+        att = oracle.attn_decode(q, kc, vc, L, nh, nkv, hd, scale, f16)
+        aq, ad = oracle.quant_q8(att)
+        assert_bitexact(y.to_host(), oracle.q8_gemv(W, aq, ad, K, r), f"attn_o L={L}")
+        assert dlen.to_host()[0] == L - 1
+    assert _lib.raw("lt_attn_o_max_len")(14, 2, 128, LT_KV_F16) == 0
+    assert _lib.raw("lt_attn_o_max_len")(32, 2, 64, LT_KV_F16) == 0
+
+
+def test_q8_gemv_rms_silu_len(gpu, oracle):
+    case("rms_silu_len")
+    rng = np.random.default_rng(26)
+    F, K = 4864, 896
+    Wg, Wu = rand_weight(rng, F, K), rand_weight(rng, F, K)
+    x = (2.0 * rng.standard_normal(K)).astype(np.float32)
+    nw = (0.5 * rng.standard_normal(K) + 1.0).astype(np.float32)
+    xq, xd = oracle.quant_q8(oracle.rmsnorm(x, nw, 1e-6))
+    eq, ed = oracle.silu_mul_quant(oracle.q8_gemv(Wg, xq, xd, K), oracle.q8_gemv(Wu, xq, xd, K))
+    Wil = up(M.interleave_gateup(Wg, Wu))
+    for L0, maxt in ((5, 64), (63, 64), (64, 64)):
+        vq, vd = empty((F,), np.int8), empty((F // 32,), np.uint16)
+        dlen = up(np.array([L0], np.int32))
+        call("lt_q8_gemv_rms_silu_len", gpu.handle, up(x).vp, up(nw).vp, ctypes.c_float(1e-6), Wil.vp, vq.vp,
+             vd.vp, F, K, dlen.vp, maxt)
+        assert_bitexact(vq.to_host(), eq, "silu*up quants")
+        assert_bitexact(vd.to_host(), ed, "silu*up scales")
+        assert dlen.to_host()[0] == (L0 + 1 if L0 < maxt else L0)
