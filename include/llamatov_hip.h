@@ -353,6 +353,47 @@ LT_API int lt_attn_prefill(lt_ctx* ctx, const float* q, int q_stride, const void
 LT_API int lt_embed_q8_batch(lt_ctx* ctx, const void* emb, const int* toks, float* x, int T, int E, int vocab,
                              int* err);
 
+/* ---- ggml-compatible numerics (the optional profile; the reference's CPU substrate,
+ *      bpd-substrate/bench/bpd_cpu.c:4005-4446 and bpd_gemm_q8_0_cpu.c:22-258) ----
+ * Quantizer: d16 = fp16_rne(amax / 127.f), id = amax != 0 ? 127.f / amax : 0,
+ * q = rint(x * id) with ties to even (ggml's dispatched AVX quantize_row_q8_0).  Dot orders:
+ * LT_GGML_VEC = ggml_vec_dot_q8_0_q8_0's AVX path (block pairs, 8 lanes, mul then add,
+ * hsum_float_8, scalar odd tail); LT_GGML_LLAMAFILE = llamafile tinyBLAS_Q0_AVX's cell
+ * (per block, 8 lanes of 4 quants, mul then add, hsum_float_8). */
+#define LT_GGML_VEC 0
+#define LT_GGML_LLAMAFILE 1
+
+/* The quantizer into the engine's split layout (xq [K] int8, xd [K/32] fp16 bits), for the
+ * profile's decode step.  No reference counterpart of this layout: bpd_quant_q8_0_cpu's
+ * arithmetic (bpd_cpu.c:4083-4112) with the engine's activation buffers. */
+LT_API int lt_quant_q8_ggml(lt_ctx* ctx, const float* x, int8_t* xq, uint16_t* xd, int K);
+
+/* bpd_quant_q8_0_cpu(x, y, n_elements) (bpd_cpu.c:4083): n_elements fp32 -> n_elements/32
+ * 34-byte Q8_0 blocks at y. */
+LT_API int lt_quant_q8_0_ggml(lt_ctx* ctx, const float* x, uint8_t* y, int n_elements);
+
+/* y[n] = dot(W row n, (xq, xd)) in ggml order `order` (+ resid[n] as one fp32 add, ggml's
+ * separate ADD node), N rows of K.  The row's lane products live in LDS: K <= 40960
+ * (LT_GGML_VEC) or 20480 (LT_GGML_LLAMAFILE).  xq 16-byte aligned, W 4-byte aligned. */
+LT_API int lt_q8_gemv_ggml(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd, const float* resid,
+                           float* y, int N, int K, int order);
+
+/* Workspace of the two qmatmul entries: the quantized activation rows. */
+LT_API size_t lt_qmatmul_q8_0_workspace_size(int M, int K);
+
+/* bpd_qmatmul_q8_0_cpu(W_q8_0, X_f32, out, M, N, K) (bpd_cpu.c:4283-4305): X [M][K] fp32,
+ * out[m][n] = vec_dot(W row n, quantized X row m).  ws 16-byte aligned. */
+LT_API int lt_qmatmul_q8_0_ggml(lt_ctx* ctx, const void* W, const float* X, float* out, int M, int N, int K,
+                                void* ws, size_t ws_bytes);
+
+/* bpd_qmatmul_q8_0_llamafile_cpu(W_q8_0, X_f32, out, m_weight, m_tokens, K)
+ * (bpd_cpu.c:4419-4446 with bpd_gemm_q8_0_cpu.c:209-258): out[token][row] (ldc = m_weight);
+ * tokens grouped 4/2/1 as llamafile's mnpack, the llamafile cell order except for a group of
+ * one token (the last when m_tokens is odd), which takes the vec_dot order -- with ggml's
+ * odd-block tail, which the reference dispatcher's single-token path omits. */
+LT_API int lt_qmatmul_q8_0_llamafile(lt_ctx* ctx, const void* W, const float* X, float* out, int m_weight,
+                                     int m_tokens, int K, void* ws, size_t ws_bytes);
+
 /* ---- numerics self-check (no reference counterpart: a diagnostic of this build) ----
  * Runs on the device and writes 4 counters to host memory: out[0] = non-NaN binary32
  * patterns whose hardware fp16 conversion (the quantizer's scale) differs from

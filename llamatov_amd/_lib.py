@@ -16,6 +16,8 @@ LIB_PATH = Path(os.environ.get("LT_HIP_LIB", _PKG / "libllamatov_hip.so"))
 
 LT_KV_F32 = 0
 LT_KV_F16 = 1
+LT_GGML_VEC = 0
+LT_GGML_LLAMAFILE = 1
 
 _P = c_void_p
 # name -> (restype, argtypes)
@@ -36,6 +38,12 @@ _SIGS = {
     "lt_silu_mul_quant": (c_int, [_P, _P, _P, _P, _P, c_int]),
     "lt_silu_mul": (c_int, [_P, _P, _P, _P, c_int]),
     "lt_add": (c_int, [_P, _P, _P, _P, c_int]),
+    "lt_quant_q8_ggml": (c_int, [_P, _P, _P, _P, c_int]),
+    "lt_quant_q8_0_ggml": (c_int, [_P, _P, _P, c_int]),
+    "lt_q8_gemv_ggml": (c_int, [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int]),
+    "lt_qmatmul_q8_0_workspace_size": (c_size_t, [c_int, c_int]),
+    "lt_qmatmul_q8_0_ggml": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _P, c_size_t]),
+    "lt_qmatmul_q8_0_llamafile": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _P, c_size_t]),
     "lt_rmsnorm": (c_int, [_P, _P, _P, _P, c_int, c_int, c_float]),
     "lt_rmsnorm_quant": (c_int, [_P, _P, _P, _P, _P, c_int, c_float]),
     "lt_q8_gemv": (c_int, [_P, _P, _P, _P, _P, _P, c_int, c_int]),

@@ -32,7 +32,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _lib
-from ._lib import LT_KV_F16, LT_KV_F32, call
+from ._lib import LT_GGML_VEC, LT_KV_F16, LT_KV_F32, call
 from .model import ModelConfig, fused_layer_tensors, interleave_gateup
 
 
@@ -434,9 +434,15 @@ class Profile:
     attn_in_o: bool = False
     fused_rms_quant: bool = False   # per-op path only: k_rms_quant instead of k_rmsnorm + k_quant_q8
     graph: bool = True
+    # "engine": the reference engine's quantizer and canonical GEMV order (every field above);
+    # "ggml": ggml's dispatched quantizer (id = 127/amax, ties to even) and its vec_dot order
+    # for every GEMV of the step (lt_ggml.hip), so that logits compare with llama.cpp on an
+    # AVX1 host; per-op launches only (fused_step=False), prefill token by token
+    numerics: str = "engine"
 
 
 PRODUCTION_PROFILE = Profile()
+GGML_PROFILE = Profile(fused_step=False, numerics="ggml")
 _CERTIFIED_NSPLIT = {1, 2, 4, 8, 16, 32, 64, 128}
 
 
@@ -450,6 +456,11 @@ def assert_certified_composition(p: Profile) -> None:
         raise RuntimeError(f"uncertified kv_dtype {p.kv_dtype}")
     if p.attn_nsplit not in _CERTIFIED_NSPLIT:
         raise RuntimeError(f"uncertified attn_nsplit {p.attn_nsplit}")
+    if p.numerics not in ("engine", "ggml"):
+        raise RuntimeError(f"uncertified numerics {p.numerics!r}")
+    if p.numerics == "ggml" and (p.fused_step or p.fused_rms_quant):
+        raise RuntimeError("the ggml numerics profile runs the per-op step: fused_step=False, "
+                           "fused_rms_quant=False")
 
 
 # ----------------------------------------------------------------------------------
@@ -771,7 +782,8 @@ class DecodePlan:
         """Launch one token: embed(tok) -> layers -> logits -> argmax -> tok.
         The launch order is forward_pass_resident's fully-device branch
         (bpd/lib/dev_residency.py:1365-1477) followed by _compute_folded_logits (:1596-1623)
-        and the device argmax of replay_token (:1795-1818)."""
+        and the device argmax of replay_token (:1795-1818).  Under numerics="ggml" every
+        quantizer and GEMV is ggml's (lt_ggml.hip); the rest of the chain is unchanged."""
         cfg, m, p = self.cfg, self.model, self.profile
         h = self.dev.handle
         E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
@@ -782,7 +794,7 @@ class DecodePlan:
         for il, L in enumerate(m.layers):
             cache = self.caches[il]
             self._rms_quant(x, L["attn_norm"], E, eps)
-            q8_gemv_into(L["wqkv"], self.xq, self.xd, self.qkv, L["bqkv"])
+            self._gemv(L["wqkv"], self.qkv, L["bqkv"])
             call("lt_rope_qk", h, self.qkv.vp, _vp(cache.len_ptr), nh + nkv, hd, m.freqs.vp)
             k = self.qkv.view(cfg.q_dim, (cfg.kv_dim,))
             v = self.qkv.view(cfg.q_dim + cfg.kv_dim, (cfg.kv_dim,))
@@ -791,24 +803,45 @@ class DecodePlan:
                  self.att.vp, 1, nh, nkv, hd, ctypes.c_float(self.scale), cache.max_seq,
                  p.attn_nsplit, p.kv_dtype, _vp(self.attn_ws),
                  self.attn_ws.nbytes if self.attn_ws is not None else 0)
-            quant_q8_into(self.att, self.xq, self.xd, cfg.q_dim)
-            q8_gemv_into(L["wo"], self.xq, self.xd, self.xres, x)
+            self._quant(self.att, cfg.q_dim)
+            self._gemv(L["wo"], self.xres, x)
             self._rms_quant(self.xres, L["ffn_norm"], E, eps)
-            q8_gemv_into(L["wgu"], self.xq, self.xd, self.gu)
+            self._gemv(L["wgu"], self.gu)
             g = self.gu.view(0, (F,))
             u = self.gu.view(F, (F,))
-            call("lt_silu_mul_quant", h, g.vp, u.vp, self.xq.vp, self.xd.vp, F)
-            q8_gemv_into(L["wdown"], self.xq, self.xd, self.carry, self.xres)
+            if p.numerics == "ggml":     # SiLU(g)*u in place over g, then ggml's quantizer
+                call("lt_silu_mul", h, g.vp, u.vp, g.vp, F)
+                self._quant(g, F)
+            else:
+                call("lt_silu_mul_quant", h, g.vp, u.vp, self.xq.vp, self.xd.vp, F)
+            self._gemv(L["wdown"], self.carry, self.xres)
             x = self.carry
         self._rms_quant(x, m.output_norm, E, eps)
-        call("lt_q8_gemv", h, m.output.t.vp, self.xq.vp, self.xd.vp, None, self.logits.vp,
-             m.output.N, m.output.K)
+        self._gemv(m.output, self.logits)
         call("lt_argmax_record", h, self.logits.vp, cfg.vocab, self.tok.vp, self.hist.vp,
              self.hist_count.vp, self.hist_cap, self.am_ws.vp, self.am_ws.nbytes)
 
+    def _quant(self, x: DevTensor, K: int) -> None:
+        """The step's activation quantizer (the engine's, or ggml's under numerics="ggml")."""
+        if self.profile.numerics == "ggml":
+            call("lt_quant_q8_ggml", self.dev.handle, x.vp, self.xq.vp, self.xd.vp, K)
+        else:
+            quant_q8_into(x, self.xq, self.xd, K)
+
+    def _gemv(self, W: Q8Weight, out: DevTensor, resid: DevTensor | None = None) -> None:
+        """out = W . (xq, xd) (+ resid) in the step's GEMV order."""
+        if self.profile.numerics == "ggml":
+            call("lt_q8_gemv_ggml", self.dev.handle, W.t.vp, self.xq.vp, self.xd.vp, _vp(resid), out.vp,
+                 W.N, W.K, LT_GGML_VEC)
+        else:
+            q8_gemv_into(W, self.xq, self.xd, out, resid)
+
     def _rms_quant(self, x: DevTensor, w: DevTensor, E: int, eps) -> None:
         h = self.dev.handle
-        if self.profile.fused_rms_quant:
+        if self.profile.numerics == "ggml":
+            call("lt_rmsnorm", h, x.vp, w.vp, self.h.vp, 1, E, eps)
+            call("lt_quant_q8_ggml", h, self.h.vp, self.xq.vp, self.xd.vp, E)
+        elif self.profile.fused_rms_quant:
             call("lt_rmsnorm_quant", h, x.vp, w.vp, self.xq.vp, self.xd.vp, E, eps)
         else:
             call("lt_rmsnorm", h, x.vp, w.vp, self.h.vp, 1, E, eps)
@@ -880,7 +913,11 @@ def forward_prefill(plan: DecodePlan, tokens, embeddings: np.ndarray | None = No
     path the reference uses (bpd/lib/dev_residency.py:1338-1356): the KV cache, the last
     token's logits and the greedy token it leaves on the device are bit-identical to
     forward_tokens's.  A host_embed plan takes the prompt's input rows as `embeddings`
-    (fp32 [T, n_embd])."""
+    (fp32 [T, n_embd]).  The ggml numerics profile has no batched form (its decode order is
+    ggml's single-token vec_dot): it prefills with forward_tokens."""
+    if plan.profile.numerics != "engine":
+        raise ValueError("forward_prefill runs the engine's numerics; a ggml-numerics plan prefills "
+                         "token by token (forward_tokens)")
     toks = np.asarray([int(t) for t in np.asarray(tokens).reshape(-1)], np.int32)
     T = int(toks.size)
     if T == 0:
@@ -1080,7 +1117,7 @@ def generate(model, input_ids, n_tokens: int, profile: Profile = PRODUCTION_PROF
             raise ValueError(f"generate: {len(ids)} prompt + {n_tokens - 1} decode positions exceed "
                              f"the {plan.max_ctx}-position KV cache")
         gr = StepGraph(plan)
-        gr.seed(ids, batched=batched_prefill and "wgu_il" in m.layers[0])
+        gr.seed(ids, batched=batched_prefill and profile.numerics == "engine" and "wgu_il" in m.layers[0])
         out = [plan.read_token()]
         if n_tokens > 1:
             gr.capture()

@@ -139,6 +139,155 @@ OR_API void or_q8_gemv(const uint8_t* W, const int8_t* xq, const uint16_t* xd, c
   }
 }
 
+/* ---------------------------------------------------------------------------------
+ * ggml-compatible numerics (the optional profile that lets results be compared with
+ * llama.cpp / Ollama): ggml's dispatched AVX quantizer and its two Q8_0 dot orders, as the
+ * reference's CPU substrate restates them (bpd-substrate/bench/bpd_cpu.c:4005-4271,
+ * bpd_gemm_q8_0_cpu.c:22-130; bpd/tests/q8_0_kernel/README.md:28-55).  AVX1 arithmetic:
+ * separate multiply and add (no FMA), as on the reference's Ivy Bridge host.
+ * ------------------------------------------------------------------------------- */
+
+/* quantize_row_q8_0, AVX path (bpd_cpu.c:4083-4112): amax = max |x|; stored scale
+ * d16 = fp16_rne(amax / 127.f); multiplier id = amax != 0 ? 127.f / amax : 0 (one division,
+ * not 1/d); q = rint(x * id), ties to even.  |x * id| <= 127 * (1 + 2^-23) < 127.5, so the
+ * int8 conversion never saturates. */
+OR_API void or_quant_q8_ggml(const float* x, int K, int8_t* xq, uint16_t* xd) {
+  int nb = K / 32;
+  for (int b = 0; b < nb; b++) {
+    float amax = 0.0f;
+    for (int i = 0; i < 32; i++) { float a = fabsf(x[b * 32 + i]); if (a > amax) amax = a; }
+    float d = amax / 127.0f;
+    xd[b] = lt_float_to_half_bits(d);
+    float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    for (int i = 0; i < 32; i++) {
+      float t = x[b * 32 + i] * id;
+      xq[b * 32 + i] = (int8_t)rintf(t);
+    }
+  }
+}
+
+/* The same quantizer writing 34-byte blocks (bpd_quant_q8_0_cpu's output format). */
+OR_API void or_quant_q8_0_ggml_blocks(const float* x, int K, uint8_t* y) {
+  int nb = K / 32;
+  int8_t q[32];
+  uint16_t d;
+  for (int b = 0; b < nb; b++) {
+    or_quant_q8_ggml(x + b * 32, 32, q, &d);
+    y[b * 34] = (uint8_t)(d & 0xFF);
+    y[b * 34 + 1] = (uint8_t)(d >> 8);
+    memcpy(y + b * 34 + 2, q, 32);
+  }
+}
+
+/* hsum_float_8 (bpd_cpu.c:4180-4186): (a4+a0 + a6+a2) + (a5+a1 + a7+a3). */
+static float ggml_hsum8(const float* a) {
+  float r0 = a[4] + a[0], r1 = a[5] + a[1], r2 = a[6] + a[2], r3 = a[7] + a[3];
+  float s0 = r0 + r2, s1 = r1 + r3;
+  return s0 + s1;
+}
+
+/* Sum of the products of quants {4j..4j+3} of one block (exact integer). */
+static int32_t quad_dot(const int8_t* w, const int8_t* x, int j) {
+  int32_t s = 0;
+  for (int i = 0; i < 4; i++) s += (int32_t)w[4 * j + i] * (int32_t)x[4 * j + i];
+  return s;
+}
+
+/* ggml_vec_dot_q8_0_q8_0, AVX path (bpd_cpu.c:4188-4223): blocks in pairs (b, b+1); lane
+ * 4h + j (h = 0, 1 the block of the pair, j = 0..3) holds the int dot of quants
+ * {4j..4j+3} and {16+4j..16+4j+3} of block b+h, times delta = wd*xd of that block, added
+ * to the lane's accumulator (mul, then add); hsum_float_8; an odd last block adds
+ * (float)isum * (wd*xd) to the sum. */
+static float dot_ggml_vec(const uint8_t* wrow, const int8_t* xq, const uint16_t* xd, int nb) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int b = 0;
+  for (; b + 1 < nb; b += 2) {
+    for (int h = 0; h < 2; h++) {
+      const uint8_t* blk = wrow + (size_t)(b + h) * 34;
+      const int8_t* w = (const int8_t*)(blk + 2);
+      const int8_t* x = xq + (size_t)(b + h) * 32;
+      float delta = lt_half_to_float_bits(blk_scale(blk)) * lt_half_to_float_bits(xd[b + h]);
+      for (int j = 0; j < 4; j++) {
+        int32_t s = quad_dot(w, x, j) + quad_dot(w, x, j + 4);
+        float p = delta * (float)s;
+        acc[4 * h + j] = p + acc[4 * h + j];
+      }
+    }
+  }
+  float sum = ggml_hsum8(acc);
+  for (; b < nb; b++) {
+    const uint8_t* blk = wrow + (size_t)b * 34;
+    const int8_t* w = (const int8_t*)(blk + 2);
+    int32_t s = 0;
+    for (int i = 0; i < 32; i++) s += (int32_t)w[i] * (int32_t)xq[(size_t)b * 32 + i];
+    float delta = lt_half_to_float_bits(blk_scale(blk)) * lt_half_to_float_bits(xd[b]);
+    float p = (float)s * delta;
+    sum = sum + p;
+  }
+  return sum;
+}
+
+/* llamafile tinyBLAS_Q0_AVX cell (bpd_cpu.c:4344-4398, bpd_gemm_q8_0_cpu.c:82-130): per
+ * block, lane j (0..7) holds the int dot of quants {4j..4j+3}, times scale = wd*xd, added
+ * to the lane's accumulator (mul, then add); hsum_float_8 at the end. */
+static float dot_ggml_llamafile(const uint8_t* wrow, const int8_t* xq, const uint16_t* xd, int nb) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int b = 0; b < nb; b++) {
+    const uint8_t* blk = wrow + (size_t)b * 34;
+    const int8_t* w = (const int8_t*)(blk + 2);
+    const int8_t* x = xq + (size_t)b * 32;
+    float scale = lt_half_to_float_bits(blk_scale(blk)) * lt_half_to_float_bits(xd[b]);
+    for (int j = 0; j < 8; j++) {
+      float p = scale * (float)quad_dot(w, x, j);
+      acc[j] = p + acc[j];
+    }
+  }
+  return ggml_hsum8(acc);
+}
+
+/* GEMV rows in a ggml order (0 = vec_dot, 1 = llamafile); y = dot (+ resid[row] as one
+ * fp32 add, ggml's separate ADD node for the bias and the residual). */
+OR_API void or_q8_gemv_ggml(const uint8_t* W, const int8_t* xq, const uint16_t* xd, const float* resid,
+                            float* y, int N, int K, int order) {
+  int nb = K / 32;
+#pragma omp parallel for schedule(static)
+  for (int n = 0; n < N; n++) {
+    const uint8_t* wrow = W + (size_t)n * nb * 34;
+    float v = order ? dot_ggml_llamafile(wrow, xq, xd, nb) : dot_ggml_vec(wrow, xq, xd, nb);
+    y[n] = resid ? v + resid[n] : v;
+  }
+}
+
+/* bpd_qmatmul_q8_0_cpu (bpd_cpu.c:4283-4305): X [M][K] fp32 quantized row by row, then
+ * out[m][n] = vec_dot(W row n, X row m). */
+OR_API void or_qmatmul_q8_0_ggml(const uint8_t* W, const float* X, float* out, int M, int N, int K) {
+  int8_t* xq = (int8_t*)malloc((size_t)K);
+  uint16_t* xd = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(K / 32));
+  for (int m = 0; m < M; m++) {
+    or_quant_q8_ggml(X + (size_t)m * K, K, xq, xd);
+    or_q8_gemv_ggml(W, xq, xd, NULL, out + (size_t)m * N, N, K, 0);
+  }
+  free(xq);
+  free(xd);
+}
+
+/* bpd_qmatmul_q8_0_llamafile_cpu (bpd_cpu.c:4419-4446) with its tile dispatcher
+ * (bpd_gemm_q8_0_cpu.c:209-258, llamafile's mnpack): tokens go in groups of 4, then 2,
+ * then 1; a token of a group of 1 (the last one when m_tokens is odd) takes the vec_dot
+ * order, every other token the llamafile cell order.  out[token][row], ldc = m_weight. */
+OR_API void or_qmatmul_q8_0_llamafile(const uint8_t* W, const float* X, float* out, int m_weight, int m_tokens,
+                                      int K) {
+  int8_t* xq = (int8_t*)malloc((size_t)K);
+  uint16_t* xd = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(K / 32));
+  for (int m = 0; m < m_tokens; m++) {
+    int vec = (m_tokens & 1) && m == m_tokens - 1;
+    or_quant_q8_ggml(X + (size_t)m * K, K, xq, xd);
+    or_q8_gemv_ggml(W, xq, xd, NULL, out + (size_t)m * m_weight, m_weight, K, vec ? 0 : 1);
+  }
+  free(xq);
+  free(xd);
+}
+
 /* RMSNorm, reduction_order(rms_ss, lanes(256), strided, tree(pairwise,8))
  * (bpd/kernelgen/emitters/norm_softmax_from_facts.pl:49, block_row :83-108,
  * canonical_serial :117-144): p[t] = fma(x_j, x_j, p[t]) over j = t, t+256, ...;
@@ -335,7 +484,20 @@ typedef struct {
   const float* const* ffn_norm;     /* [n_layers] -> [E] */
   const uint8_t* const* wgu;        /* [n_layers] -> [2F][E/32], gate rows then up rows */
   const uint8_t* const* wdown;      /* [n_layers] -> [E][F/32] */
+  int numerics;                     /* 0 = the engine's quantizer and GEMV order, 1 = ggml's
+                                       (or_quant_q8_ggml, vec_dot order) for every GEMV */
 } or_model;
+
+/* The step's quantizer and GEMV under the model's numerics. */
+static void step_quant(const or_model* m, const float* x, int K, int8_t* xq, uint16_t* xd) {
+  if (m->numerics) or_quant_q8_ggml(x, K, xq, xd);
+  else or_quant_q8(x, K, xq, xd);
+}
+static void step_gemv(const or_model* m, const uint8_t* W, const int8_t* xq, const uint16_t* xd,
+                      const float* resid, float* y, int N, int K) {
+  if (m->numerics) or_q8_gemv_ggml(W, xq, xd, resid, y, N, K, 0);
+  else or_q8_gemv(W, xq, xd, resid, y, N, K);
+}
 
 typedef struct {
   int len;
@@ -392,8 +554,8 @@ OR_API int or_decode_step(const or_model* m, or_state* st, int tok, float* logit
   float scale = (float)pow((double)hd, -0.5);   /* hd ** -0.5 (dev_residency.py:1423) */
   for (int l = 0; l < m->n_layers; l++) {
     or_rmsnorm(x, m->attn_norm[l], h, E, m->eps);
-    or_quant_q8(h, E, xq, xd);
-    or_q8_gemv(m->wqkv[l], xq, xd, m->bqkv ? m->bqkv[l] : NULL, qkv, NQKV, E);
+    step_quant(m, h, E, xq, xd);
+    step_gemv(m, m->wqkv[l], xq, xd, m->bqkv ? m->bqkv[l] : NULL, qkv, NQKV, E);
     or_rope(qkv, pos, nh + nkv, hd, freqs);
     for (int i = 0; i < KD; i++) {
       kv_store(st->kc[l], m->kv_f16, (size_t)pos * KD + i, qkv[QD + i]);
@@ -401,18 +563,19 @@ OR_API int or_decode_step(const or_model* m, or_state* st, int tok, float* logit
     }
     or_attn_decode(qkv, st->kc[l], st->vc[l], pos + 1, att, nh, nkv, hd, scale, m->kv_f16,
                    m->attn_nsplit > 0 ? m->attn_nsplit : 1);
-    or_quant_q8(att, QD, xq, xd);
-    or_q8_gemv(m->wo[l], xq, xd, x, xres, E, QD);
+    step_quant(m, att, QD, xq, xd);
+    step_gemv(m, m->wo[l], xq, xd, x, xres, E, QD);
     or_rmsnorm(xres, m->ffn_norm[l], h, E, m->eps);
-    or_quant_q8(h, E, xq, xd);
-    or_q8_gemv(m->wgu[l], xq, xd, NULL, gu, 2 * F, E);
-    or_silu_mul_quant(gu, gu + F, F, xq, xd);
-    or_q8_gemv(m->wdown[l], xq, xd, xres, x, E, F);
+    step_quant(m, h, E, xq, xd);
+    step_gemv(m, m->wgu[l], xq, xd, NULL, gu, 2 * F, E);
+    or_silu_mul(gu, gu + F, F, gu);
+    step_quant(m, gu, F, xq, xd);
+    step_gemv(m, m->wdown[l], xq, xd, xres, x, E, F);
   }
   st->len = pos + 1;
   or_rmsnorm(x, m->output_norm, h, E, m->eps);
-  or_quant_q8(h, E, xq, xd);
-  or_q8_gemv(m->output, xq, xd, NULL, logits, m->vocab, E);
+  step_quant(m, h, E, xq, xd);
+  step_gemv(m, m->output, xq, xd, NULL, logits, m->vocab, E);
   free(x); free(h); free(xres); free(qkv); free(att); free(gu); free(xq); free(xd); free(freqs);
   return 0;
 }

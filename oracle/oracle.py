@@ -44,6 +44,11 @@ def lib() -> ctypes.CDLL:
             "or_silu_mul": (None, [P, P, c_int, P]),
             "or_q8_block_dots": (None, [P, P, c_int, c_int, P]),
             "or_q8_gemv": (None, [P, P, P, P, P, c_int, c_int]),
+            "or_quant_q8_ggml": (None, [P, c_int, P, P]),
+            "or_quant_q8_0_ggml_blocks": (None, [P, c_int, P]),
+            "or_q8_gemv_ggml": (None, [P, P, P, P, P, c_int, c_int, c_int]),
+            "or_qmatmul_q8_0_ggml": (None, [P, P, P, c_int, c_int, c_int]),
+            "or_qmatmul_q8_0_llamafile": (None, [P, P, P, c_int, c_int, c_int]),
             "or_rmsnorm": (None, [P, P, P, c_int, c_float]),
             "or_rope_freqs": (None, [c_int, c_float, P]),
             "or_rope": (None, [P, c_int, c_int, c_int, P]),
@@ -166,6 +171,51 @@ def q8_gemv(W: np.ndarray, xq: np.ndarray, xd: np.ndarray, K: int, resid: np.nda
     return y
 
 
+# ---- ggml-compatible numerics ----------------------------------------------------------
+GGML_VEC, GGML_LLAMAFILE = 0, 1
+
+
+def quant_q8_ggml(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    x = np.ascontiguousarray(x, np.float32)
+    xq = np.empty(x.size, np.int8)
+    xd = np.empty(x.size // 32, np.uint16)
+    lib().or_quant_q8_ggml(_p(x), x.size, _p(xq), _p(xd))
+    return xq, xd
+
+
+def quant_q8_0_ggml_blocks(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(x.size // 32 * 34, np.uint8)
+    lib().or_quant_q8_0_ggml_blocks(_p(x), x.size, _p(y))
+    return y
+
+
+def q8_gemv_ggml(W: np.ndarray, xq: np.ndarray, xd: np.ndarray, K: int, order: int = GGML_VEC,
+                 resid: np.ndarray | None = None) -> np.ndarray:
+    W = np.ascontiguousarray(W, np.uint8)
+    N = W.size // (K // 32 * 34)
+    y = np.empty(N, np.float32)
+    r = None if resid is None else np.ascontiguousarray(resid, np.float32)
+    lib().or_q8_gemv_ggml(_p(W), _p(np.ascontiguousarray(xq, np.int8)), _p(np.ascontiguousarray(xd, np.uint16)),
+                          _p(r), _p(y), N, K, order)
+    return y
+
+
+def qmatmul_q8_0_ggml(W: np.ndarray, X: np.ndarray, N: int, K: int) -> np.ndarray:
+    X = np.ascontiguousarray(X, np.float32).reshape(-1, K)
+    out = np.empty((X.shape[0], N), np.float32)
+    lib().or_qmatmul_q8_0_ggml(_p(np.ascontiguousarray(W, np.uint8)), _p(X), _p(out), X.shape[0], N, K)
+    return out
+
+
+def qmatmul_q8_0_llamafile(W: np.ndarray, X: np.ndarray, m_weight: int, K: int) -> np.ndarray:
+    X = np.ascontiguousarray(X, np.float32).reshape(-1, K)
+    out = np.empty((X.shape[0], m_weight), np.float32)
+    lib().or_qmatmul_q8_0_llamafile(_p(np.ascontiguousarray(W, np.uint8)), _p(X), _p(out), m_weight,
+                                    X.shape[0], K)
+    return out
+
+
 def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
     x = np.ascontiguousarray(x, np.float32).reshape(-1)
     w = np.ascontiguousarray(w, np.float32).reshape(-1)
@@ -218,7 +268,7 @@ class _OrModel(ctypes.Structure):
         ("tok_embd", c_void_p), ("output", c_void_p), ("output_norm", c_void_p),
         ("attn_norm", POINTER(c_void_p)), ("wqkv", POINTER(c_void_p)), ("bqkv", POINTER(c_void_p)),
         ("wo", POINTER(c_void_p)), ("ffn_norm", POINTER(c_void_p)), ("wgu", POINTER(c_void_p)),
-        ("wdown", POINTER(c_void_p)),
+        ("wdown", POINTER(c_void_p)), ("numerics", c_int),
     ]
 
 
@@ -244,7 +294,7 @@ class OracleModel:
     """The oracle's view of a synthetic model: keeps the numpy arrays alive."""
 
     def __init__(self, cfg, weights: dict, kv_f16: bool = False, attn_nsplit: int = 1,
-                 max_ctx: int | None = None):
+                 max_ctx: int | None = None, numerics: str = "engine"):
         self.cfg = cfg
         self.keep = []
         nl = cfg.n_layers
@@ -279,6 +329,9 @@ class OracleModel:
         m.ffn_norm = ptrs([arr(L["ffn_norm"], np.float32) for L in layers])
         m.wgu = ptrs([arr(L["wgu"], np.uint8) for L in layers])
         m.wdown = ptrs([arr(L["wdown"], np.uint8) for L in layers])
+        if numerics not in ("engine", "ggml"):
+            raise ValueError(f"numerics={numerics!r}")
+        m.numerics = int(numerics == "ggml")
         self.m = m
         self.st = lib().or_state_new(ctypes.byref(m))
 

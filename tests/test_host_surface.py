@@ -64,6 +64,19 @@ def test_composition_gate_on_the_host():
     assert all(live[k] == v for k, v in dr.PRODUCTION_PROFILE.items())
 
 
+def test_engine_profile_refusals():
+    """The engine's Profile gate (the reference's composition gate, dev_residency.py:1268-1281)
+    refuses uncertified splits, cache types and numerics, and a ggml-numerics profile that
+    asks for the fused step."""
+    from llamatov_amd import engine as E
+    E.assert_certified_composition(E.PRODUCTION_PROFILE)
+    E.assert_certified_composition(E.GGML_PROFILE)
+    for bad in (E.Profile(attn_nsplit=3), E.Profile(kv_dtype=2), E.Profile(numerics="fast"),
+                E.Profile(numerics="ggml"), E.Profile(numerics="ggml", fused_step=False, fused_rms_quant=True)):
+        with pytest.raises(RuntimeError):
+            E.assert_certified_composition(bad)
+
+
 def test_load_model_orientation(tmp_path):
     from llamatov_amd import gguf
     from llamatov_amd import llamatov_run as R
