@@ -394,6 +394,37 @@ LT_API int lt_qmatmul_q8_0_ggml(lt_ctx* ctx, const void* W, const float* X, floa
 LT_API int lt_qmatmul_q8_0_llamafile(lt_ctx* ctx, const void* W, const float* X, float* out, int m_weight,
                                      int m_tokens, int K, void* ws, size_t ws_bytes);
 
+/* ---- sampling beyond greedy (temperature, top-k, top-p) on the device ----
+ * The reference's device argmax (k_argmax / replay_token, bpd/lib/dev_residency.py:186-191,
+ * 1795-1818) is the k = 1 case, planned there to extend to top-k/top-p/temperature; there is
+ * no reference signature.  Semantics (exact, reproduced by the CPU restatement): candidates
+ * ranked by logit (ties to the lower index, -0 == +0); the first k = clamp(top_k, 1,
+ * LT_SAMPLE_MAX_K) of them (k = 1 when temperature <= 0); e_i = exp((l_i - l_0) / T) with the
+ * division as one multiply by the fp32 reciprocal; c_i the sequential cumulative sum; n the
+ * smallest count with c_{n-1} >= top_p * c_{k-1} (all k when top_p >= 1); u from
+ * Philox4x32-10 (counter {counter, 0}, key seed): u = (x0 >> 8) * 2^-24; the token is the
+ * first i < n with c_i > u * c_{n-1}.  Every call advances params->counter by one. */
+#define LT_SAMPLE_MAX_K 1024
+
+/* Sampling state, kept in DEVICE memory (8-byte aligned): the host may rewrite it between
+ * launches or graph replays; the kernel reads it and advances counter. */
+typedef struct lt_sample_params {
+  float temperature;
+  int top_k;
+  float top_p;
+  int reserved;
+  unsigned long long seed;
+  unsigned long long counter;
+} lt_sample_params;
+
+/* Workspace of lt_sample for a vocabulary of V (0 when V is outside 1 .. 262144). */
+LT_API size_t lt_sample_workspace_size(int V);
+
+/* Draw one token from logits[V] into *out_tok; with hist, also append it (hist[*count] = id,
+ * *count += 1 while < cap), as lt_argmax_record does.  Two launches, graph-capturable. */
+LT_API int lt_sample(lt_ctx* ctx, const float* logits, int V, lt_sample_params* params, int* out_tok, int* hist,
+                     int* count, int cap, void* ws, size_t ws_bytes);
+
 /* ---- numerics self-check (no reference counterpart: a diagnostic of this build) ----
  * Runs on the device and writes 4 counters to host memory: out[0] = non-NaN binary32
  * patterns whose hardware fp16 conversion (the quantizer's scale) differs from

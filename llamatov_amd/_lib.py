@@ -18,6 +18,7 @@ LT_KV_F32 = 0
 LT_KV_F16 = 1
 LT_GGML_VEC = 0
 LT_GGML_LLAMAFILE = 1
+LT_SAMPLE_MAX_K = 1024
 
 _P = c_void_p
 # name -> (restype, argtypes)
@@ -38,6 +39,8 @@ _SIGS = {
     "lt_silu_mul_quant": (c_int, [_P, _P, _P, _P, _P, c_int]),
     "lt_silu_mul": (c_int, [_P, _P, _P, _P, c_int]),
     "lt_add": (c_int, [_P, _P, _P, _P, c_int]),
+    "lt_sample_workspace_size": (c_size_t, [c_int]),
+    "lt_sample": (c_int, [_P, _P, c_int, _P, _P, _P, _P, c_int, _P, c_size_t]),
     "lt_quant_q8_ggml": (c_int, [_P, _P, _P, _P, c_int]),
     "lt_quant_q8_0_ggml": (c_int, [_P, _P, _P, c_int]),
     "lt_q8_gemv_ggml": (c_int, [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int]),

@@ -32,7 +32,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _lib
-from ._lib import LT_GGML_VEC, LT_KV_F16, LT_KV_F32, call
+from ._lib import LT_GGML_VEC, LT_KV_F16, LT_KV_F32, LT_SAMPLE_MAX_K, call
 from .model import ModelConfig, fused_layer_tensors, interleave_gateup
 
 
@@ -625,6 +625,9 @@ class DecodePlan:
                        for il in range(cfg.n_layers)]
         self.scale = float(hd ** -0.5)
         self._prefill: PrefillBuffers | None = None
+        self.sampling = False
+        self._sample_params: DevTensor | None = None
+        self._sample_ws: DevTensor | None = None
         self.reset()
 
     def prefill_buffers(self, T: int) -> "PrefillBuffers":
@@ -729,8 +732,8 @@ class DecodePlan:
                      self.xq.vp, self.xd.vp, F, E)
                 call("lt_q8_gemv", h, L["wdown"].t.vp, self.xq.vp, self.xd.vp, self.xres.vp, self.carry.vp, E, F)
         call("lt_q8_gemv_rms_argmax", h, self.carry.vp, m.output_norm.vp, eps, m.output.t.vp, self.logits.vp,
-             cfg.vocab, E, self.tok.vp, self.hist.vp, self.hist_count.vp, self.hist_cap,
-             self.am_ws.vp, self.am_ws.nbytes)
+             cfg.vocab, E, self.tok.vp, *self._hist_args(), self.am_ws.vp, self.am_ws.nbytes)
+        self._enqueue_sample_if_on()
 
     @property
     def four_launch_len(self) -> int:
@@ -775,8 +778,8 @@ class DecodePlan:
                  self.xq.vp, self.xd.vp, F, E, lp, cache.max_seq)
             call("lt_q8_gemv", h, L["wdown"].t.vp, self.xq.vp, self.xd.vp, self.xres.vp, self.carry.vp, E, F)
         call("lt_q8_gemv_rms_argmax", h, self.carry.vp, m.output_norm.vp, eps, m.output.t.vp, self.logits.vp,
-             cfg.vocab, E, self.tok.vp, self.hist.vp, self.hist_count.vp, self.hist_cap,
-             self.am_ws.vp, self.am_ws.nbytes)
+             cfg.vocab, E, self.tok.vp, *self._hist_args(), self.am_ws.vp, self.am_ws.nbytes)
+        self._enqueue_sample_if_on()
 
     def _enqueue_per_op(self) -> None:
         """Launch one token: embed(tok) -> layers -> logits -> argmax -> tok.
@@ -818,8 +821,67 @@ class DecodePlan:
             x = self.carry
         self._rms_quant(x, m.output_norm, E, eps)
         self._gemv(m.output, self.logits)
-        call("lt_argmax_record", h, self.logits.vp, cfg.vocab, self.tok.vp, self.hist.vp,
-             self.hist_count.vp, self.hist_cap, self.am_ws.vp, self.am_ws.nbytes)
+        if self.sampling:
+            self._enqueue_sample(record=True)
+        else:
+            call("lt_argmax_record", h, self.logits.vp, cfg.vocab, self.tok.vp, self.hist.vp, self.hist_count.vp,
+                 self.hist_cap, self.am_ws.vp, self.am_ws.nbytes)
+
+    # -- sampling beyond greedy ----------------------------------------------------
+    def set_sampling(self, temperature: float | None, top_k: int = 40, top_p: float = 1.0, seed: int = 0,
+                     counter: int = 0) -> None:
+        """Draw every step's token with lt_sample (temperature, top-k, top-p; Philox stream
+        `seed`, starting at draw `counter`) instead of the greedy argmax; temperature=None
+        returns to greedy.  The parameters live on the device: a captured graph reads them at
+        every replay, so new values apply without re-capture; switching between greedy and
+        sampling changes the launch sequence and needs a new capture."""
+        if temperature is None:
+            self.sampling = False
+            return
+        if not 1 <= int(top_k) <= LT_SAMPLE_MAX_K:
+            raise ValueError(f"top_k={top_k}: 1 .. {LT_SAMPLE_MAX_K}")
+        if self._sample_params is None:
+            n = _lib.raw("lt_sample_workspace_size")(self.cfg.vocab)
+            if n == 0:
+                raise ValueError(f"lt_sample: vocab {self.cfg.vocab} is outside 1 .. 262144")
+            self._sample_params = DevTensor.empty((32,), np.uint8, self.dev)
+            self._sample_ws = DevTensor.empty((n,), np.uint8, self.dev)
+        rec = np.zeros(1, np.dtype([("temperature", "<f4"), ("top_k", "<i4"), ("top_p", "<f4"), ("reserved", "<i4"),
+                                    ("seed", "<u8"), ("counter", "<u8")]))
+        rec["temperature"], rec["top_k"], rec["top_p"] = temperature, int(top_k), top_p
+        rec["seed"], rec["counter"] = int(seed) & (2 ** 64 - 1), int(counter)
+        self.dev.h2d(self._sample_params.ptr, rec.view(np.uint8))
+        self.sampling = True
+
+    def sample_counter(self) -> int:
+        """Draws made so far (the device counter)."""
+        out = np.zeros(4, np.uint64)
+        self.dev.d2h(out, self._sample_params.ptr)
+        return int(out[3])
+
+    def _hist_args(self) -> tuple:
+        """The argmax launch records the token unless the sampler draws (and records) it."""
+        if self.sampling:
+            return (None, None, 0)
+        return (self.hist.vp, self.hist_count.vp, self.hist_cap)
+
+    def _enqueue_sample(self, record: bool) -> None:
+        call("lt_sample", self.dev.handle, self.logits.vp, self.cfg.vocab, self._sample_params.vp, self.tok.vp,
+             self.hist.vp if record else None, self.hist_count.vp if record else None,
+             self.hist_cap if record else 0, self._sample_ws.vp, self._sample_ws.nbytes)
+
+    def _enqueue_sample_if_on(self) -> None:
+        if self.sampling:
+            self._enqueue_sample(record=True)
+
+    def sample_current(self) -> int:
+        """Draw a token from the logits now on the device (after a prefill) into the device
+        token, without recording it in the history; returns it."""
+        if not self.sampling:
+            raise ValueError("sample_current: set_sampling first")
+        self._enqueue_sample(record=False)
+        self.dev.sync()
+        return self.read_token()
 
     def _quant(self, x: DevTensor, K: int) -> None:
         """The step's activation quantizer (the engine's, or ggml's under numerics="ggml")."""
@@ -875,7 +937,7 @@ class DecodePlan:
             c.free()
         for t in (self.tok, self.err, self.hist, self.hist_count, self.lens, self.resid_in, self.carry,
                   self.xres, self.h, self.qkv, self.att, self.gu, self.v, self.logits, self.xq, self.xd,
-                  self.am_ws, self.attn_ws):
+                  self.am_ws, self.attn_ws, self._sample_params, self._sample_ws):
             if t is not None:
                 t.free()
 
@@ -1000,6 +1062,7 @@ class StepGraph:
         self.graph = ctypes.c_void_p()    # the five-launch step (every length)
         self.graph4 = ctypes.c_void_p()   # the four-launch step (lengths up to plan.four_launch_len)
         self.captured = False
+        self.captured_sampling = False
 
     def seed(self, prompt, batched: bool = False, embeddings: np.ndarray | None = None) -> np.ndarray:
         """Eager prefill over the prompt (fixed buffers, all kernels loaded); returns the
@@ -1039,10 +1102,13 @@ class StepGraph:
                 self.graph = ctypes.c_void_p()
                 raise
         self.captured = True
+        self.captured_sampling = self.plan.sampling
 
     def _launch(self) -> None:
         if not self.captured:
             raise RuntimeError("call capture() before replay")
+        if self.plan.sampling != self.captured_sampling:
+            raise RuntimeError("the plan switched between greedy and sampling after capture: capture again")
         self.plan.check_room(1)
         g = self.graph4 if self.graph4.value and self.plan.four_launch else self.graph
         call("lt_graph_launch", self.dev.handle, g)
@@ -1063,7 +1129,8 @@ class StepGraph:
         return self.plan.read_logits()
 
     def replay_token(self, tok: int | None = None, embedding: np.ndarray | None = None) -> int:
-        """One graph replay; returns the greedy next token (4 bytes cross to the host)."""
+        """One graph replay; returns the next token, greedy or drawn by the plan's sampler
+        (4 bytes cross to the host)."""
         self._set_input(tok, embedding)
         self._launch()
         return self.plan.read_token()
@@ -1094,11 +1161,15 @@ class StepGraph:
 
 
 def generate(model, input_ids, n_tokens: int, profile: Profile = PRODUCTION_PROFILE,
-             batched_prefill: bool = True, max_ctx: int | None = None) -> list[int]:
-    """Greedy generation of n_tokens after input_ids, the reference's decode loop
+             batched_prefill: bool = True, max_ctx: int | None = None,
+             sampling: dict | None = None) -> list[int]:
+    """Generation of n_tokens after input_ids, the reference's decode loop
     (decode_fact.py:54-111 semantics; GraphRunner seed -> capture -> replay,
     dev_residency.py:1626-1818): the prompt is prefilled, the first token is its greedy
     argmax, and every further token comes from one replay of the captured step.
+    sampling={temperature, top_k, top_p, seed} draws every generated token with the device
+    sampler instead (DecodePlan.set_sampling, after the prompt: draw i of the sequence is
+    Philox counter i).
 
     `model` is a ResidentModel or the path of a Q8_0 GGUF file (loaded and freed here)."""
     own = not isinstance(model, ResidentModel)
@@ -1118,7 +1189,11 @@ def generate(model, input_ids, n_tokens: int, profile: Profile = PRODUCTION_PROF
                              f"the {plan.max_ctx}-position KV cache")
         gr = StepGraph(plan)
         gr.seed(ids, batched=batched_prefill and profile.numerics == "engine" and "wgu_il" in m.layers[0])
-        out = [plan.read_token()]
+        if sampling:
+            plan.set_sampling(**sampling)
+            out = [plan.sample_current()]
+        else:
+            out = [plan.read_token()]
         if n_tokens > 1:
             gr.capture()
             out += gr.replay_tokens(n_tokens - 1)

@@ -288,6 +288,82 @@ OR_API void or_qmatmul_q8_0_llamafile(const uint8_t* W, const float* X, float* o
   free(xd);
 }
 
+/* ---------------------------------------------------------------------------------
+ * Sampling beyond greedy (the extension the reference plans for its device argmax,
+ * bpd/lib/dev_residency.py:186-191, 1795-1803).  The definition the device sampler
+ * (lt_sample.hip) follows, restated with a full sort instead of its radix selects.
+ * ------------------------------------------------------------------------------- */
+
+/* Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC 2011): 10 rounds, the key bumped by the
+ * Weyl constants before every round but the first. */
+OR_API void or_philox4x32_10(const uint32_t ctr_in[4], const uint32_t key_in[2], uint32_t out[4]) {
+  uint32_t c0 = ctr_in[0], c1 = ctr_in[1], c2 = ctr_in[2], c3 = ctr_in[3], k0 = key_in[0], k1 = key_in[1];
+  for (int r = 0; r < 10; r++) {
+    if (r) { k0 += 0x9E3779B9u; k1 += 0xBB67AE85u; }
+    uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
+    uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0, n1 = (uint32_t)p1;
+    uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1, n3 = (uint32_t)p0;
+    c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+  }
+  out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+static uint32_t sample_order_key(float v) {
+  uint32_t b;
+  memcpy(&b, &v, 4);
+  if ((b << 1) == 0u) return 0x80000000u;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+static int cmp_desc_u64(const void* a, const void* b) {
+  uint64_t x = *(const uint64_t*)a, y = *(const uint64_t*)b;
+  return x < y ? 1 : (x > y ? -1 : 0);
+}
+
+/* Rank by (logit desc, index asc) with -0 == +0; k = clamp(top_k, 1, 1024) (1 when
+ * temperature <= 0), at most V; e_i = lt_expf((l_i - l_0) * (1/T)); c_i sequential;
+ * n = smallest count with c_{n-1} >= top_p * c_{k-1} (k when top_p >= 1);
+ * u = (philox4x32_10({counter, 0}, seed).x >> 8) * 2^-24; first i < n with c_i > u*c_{n-1}. */
+OR_API int or_sample(const float* logits, int V, float temperature, int top_k, float top_p, uint64_t seed,
+                     uint64_t counter) {
+  int k = top_k < 1 ? 1 : (top_k > 1024 ? 1024 : top_k);
+  if (!(temperature > 0.0f)) k = 1;
+  if (k > V) k = V;
+  uint64_t* key = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
+  for (int i = 0; i < V; i++) key[i] = ((uint64_t)sample_order_key(logits[i]) << 32) | (uint32_t)~(uint32_t)i;
+  qsort(key, (size_t)V, sizeof(uint64_t), cmp_desc_u64);
+  int pick = 0;
+  if (k > 1) {
+    float invT = 1.0f / temperature;
+    float l0 = logits[~(uint32_t)key[0]];
+    float* c = (float*)malloc(sizeof(float) * (size_t)k);
+    float acc = 0.0f;
+    for (int i = 0; i < k; i++) {
+      float li = logits[~(uint32_t)key[i]];
+      float ci = (li - l0) * invT;
+      /* -0 and +0 rank as one key; the logit difference only feeds exp, where they agree */
+      acc = acc + lt_expf(ci);
+      c[i] = acc;
+    }
+    int n = k;
+    if (top_p < 1.0f) {
+      float thr = top_p * c[k - 1];
+      for (int i = 0; i < k; i++) if (c[i] >= thr) { n = i + 1; break; }
+    }
+    uint32_t ctr[4] = {(uint32_t)counter, (uint32_t)(counter >> 32), 0u, 0u};
+    uint32_t kk[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)}, out[4];
+    or_philox4x32_10(ctr, kk, out);
+    float u = (float)(out[0] >> 8) * 0x1.0p-24f;
+    float target = u * c[n - 1];
+    pick = n - 1;
+    for (int i = 0; i < n; i++) if (c[i] > target) { pick = i; break; }
+    free(c);
+  }
+  int id = (int)~(uint32_t)key[pick];
+  free(key);
+  return id;
+}
+
 /* RMSNorm, reduction_order(rms_ss, lanes(256), strided, tree(pairwise,8))
  * (bpd/kernelgen/emitters/norm_softmax_from_facts.pl:49, block_row :83-108,
  * canonical_serial :117-144): p[t] = fma(x_j, x_j, p[t]) over j = t, t+256, ...;

@@ -17,8 +17,16 @@ LIB = HERE / "liblt_oracle.so"
 _lib = None
 
 
+REF_SRC = Path("/root/reference/bpd-substrate/bench/bpd_cpu.c")
+
+
 def build() -> Path:
+    """The oracle, and -- where the reference tree is present (not on the GPU box) -- the
+    reference's own CPU substrate into _ref/ (`make ref`), the checker of the ggml numerics."""
     subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    if REF_SRC.exists():
+        subprocess.run(["make", "-s", "-C", str(HERE), "ref"], check=True, stdout=subprocess.DEVNULL,
+                       stderr=subprocess.DEVNULL)
     return LIB
 
 
@@ -45,6 +53,8 @@ def lib() -> ctypes.CDLL:
             "or_q8_block_dots": (None, [P, P, c_int, c_int, P]),
             "or_q8_gemv": (None, [P, P, P, P, P, c_int, c_int]),
             "or_quant_q8_ggml": (None, [P, c_int, P, P]),
+            "or_philox4x32_10": (None, [P, P, P]),
+            "or_sample": (c_int, [P, c_int, c_float, c_int, c_float, ctypes.c_uint64, ctypes.c_uint64]),
             "or_quant_q8_0_ggml_blocks": (None, [P, c_int, P]),
             "or_q8_gemv_ggml": (None, [P, P, P, P, P, c_int, c_int, c_int]),
             "or_qmatmul_q8_0_ggml": (None, [P, P, P, c_int, c_int, c_int]),
@@ -214,6 +224,20 @@ def qmatmul_q8_0_llamafile(W: np.ndarray, X: np.ndarray, m_weight: int, K: int) 
     lib().or_qmatmul_q8_0_llamafile(_p(np.ascontiguousarray(W, np.uint8)), _p(X), _p(out), m_weight,
                                     X.shape[0], K)
     return out
+
+
+# ---- sampling ------------------------------------------------------------------------------
+def philox4x32_10(ctr, key) -> list[int]:
+    c = np.ascontiguousarray(np.asarray(ctr, np.uint32))
+    k = np.ascontiguousarray(np.asarray(key, np.uint32))
+    out = np.zeros(4, np.uint32)
+    lib().or_philox4x32_10(_p(c), _p(k), _p(out))
+    return [int(v) for v in out]
+
+
+def sample(logits: np.ndarray, temperature: float, top_k: int, top_p: float, seed: int, counter: int) -> int:
+    x = np.ascontiguousarray(logits, np.float32).reshape(-1)
+    return int(lib().or_sample(_p(x), x.size, temperature, top_k, top_p, seed, counter))
 
 
 def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:

@@ -1,0 +1,155 @@
+"""The device sampler (lt_sample.hip) against the oracle's sampler (pinned in
+test_oracle_sample.py): every draw's token bit for bit over vocab sizes across the chunk
+boundaries, tied logits, greedy and nucleus settings; the counter and history bookkeeping;
+refusals; and sampled generation through the decode step and its graph against the oracle
+model stepped on the host."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from llamatov_amd import _lib
+from llamatov_amd import engine as dr
+from llamatov_amd import model as M
+from llamatov_amd._lib import call
+
+pytestmark = pytest.mark.gpu
+
+
+def case(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+PARAM_DT = np.dtype([("temperature", "<f4"), ("top_k", "<i4"), ("top_p", "<f4"), ("reserved", "<i4"),
+                     ("seed", "<u8"), ("counter", "<u8")])
+
+
+def params(T, k, p, seed, counter):
+    r = np.zeros(1, PARAM_DT)
+    r["temperature"], r["top_k"], r["top_p"], r["seed"], r["counter"] = T, k, p, seed, counter
+    return r.view(np.uint8)
+
+
+@pytest.mark.parametrize("V", [16, 1000, 8192, 8193, 151936, 262144])
+def test_sample_matches_oracle(gpu, oracle, V):
+    rng = np.random.default_rng(V)
+    ws_n = _lib.raw("lt_sample_workspace_size")(V)
+    ws = dr.DevTensor.empty((ws_n,), np.uint8, gpu)
+    tok = dr.DevTensor.empty((1,), np.int32, gpu)
+    hist = dr.DevTensor.empty((64,), np.int32, gpu)
+    cnt = dr.DevTensor.from_host(np.zeros(1, np.int32), gpu)
+    par = dr.DevTensor.empty((32,), np.uint8, gpu)
+    settings = [(0.0, 40, 1.0), (1.0, 1, 1.0), (0.7, 40, 0.9), (1.0, 1024, 0.95), (1.5, 300, 1.0),
+                (0.9, 1024, 1e-7), (1e30, 64, 1.0)]
+    n_draws = 0
+    for trial in range(3):
+        l = (rng.standard_normal(V) * 3).astype(np.float32)
+        if trial == 1:
+            l = np.round(l, 0).astype(np.float32)            # heavy ties straddling every rank
+        if trial == 2:
+            l[rng.integers(0, V, 5)] = l.max() + 1.0          # a tie at the top
+            l[::7] = -0.0
+        dl = dr.DevTensor.from_host(l, gpu)
+        for T, k, p in settings:
+            seed = 1234 + trial
+            dev_par = params(T, k, p, seed, 5)
+            gpu.h2d(par.ptr, dev_par)
+            for c in range(5, 9):
+                case(f"sample V={V} trial={trial} T={T} k={k} p={p} counter={c}")
+                call("lt_sample", gpu.handle, dl.vp, V, par.vp, tok.vp, hist.vp, cnt.vp, 64, ws.vp, ws_n)
+                got = int(tok.to_host()[0])
+                exp = oracle.sample(l, T, k, p, seed, c)
+                assert got == exp, (V, trial, T, k, p, c, got, exp)
+                n_draws += 1
+            back = par.to_host().view(PARAM_DT)[0]
+            assert int(back["counter"]) == 9
+    h = hist.to_host()
+    assert int(cnt.to_host()[0]) == min(n_draws, 64)
+    assert 0 <= h.min() and h.max() < V
+
+
+def test_sample_refusals(gpu):
+    case("sample refusals")
+    f = _lib.raw("lt_sample")
+    V = 1000
+    ws_n = _lib.raw("lt_sample_workspace_size")(V)
+    ws = dr.DevTensor.empty((ws_n,), np.uint8, gpu)
+    d = dr.DevTensor.empty((V,), np.float32, gpu)
+    par = dr.DevTensor.empty((32,), np.uint8, gpu)
+    tok = dr.DevTensor.empty((1,), np.int32, gpu)
+    assert _lib.raw("lt_sample_workspace_size")(262145) == 0
+    assert f(gpu.handle, d.vp, 262145, par.vp, tok.vp, None, None, 0, ws.vp, ws_n) == -1
+    assert f(gpu.handle, d.vp, V, par.vp, tok.vp, None, None, 0, ws.vp, ws_n - 1) == -1
+    assert f(gpu.handle, d.vp, V, par.vp, tok.vp, tok.vp, None, 4, ws.vp, ws_n) == -1
+
+
+_W = {}
+
+
+def weights(cfg):
+    if cfg.name not in _W:
+        _W[cfg.name] = M.synth_weights(cfg, 1234)
+    return _W[cfg.name]
+
+
+def oracle_sampled(oracle, cfg, w, prompt, n, T, k, p, seed, kv_f16):
+    orc = oracle.OracleModel(cfg, w, kv_f16=kv_f16)
+    for t in prompt:
+        lg = orc.step(t)
+    out = []
+    for i in range(n):
+        t = oracle.sample(lg, T, k, p, seed, i)
+        out.append(t)
+        if i + 1 < n:
+            lg = orc.step(t)
+    return out
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_sampled_generation(gpu, oracle, fused):
+    cfg = M.SMALL_QWEN
+    case(f"sampled generation fused={fused}")
+    w = weights(cfg)
+    model = dr.ResidentModel(cfg, w, gpu)
+    prompt = M.random_prompt(cfg, 7, seed=21)
+    prof = dr.Profile(kv_dtype=dr.LT_KV_F16, fused_step=fused)
+    sp = dict(temperature=0.8, top_k=40, top_p=0.95, seed=77)
+    got = dr.generate(model, prompt, 24, prof, sampling=sp)
+    exp = oracle_sampled(oracle, cfg, w, prompt, 24, 0.8, 40, 0.95, 77, True)
+    assert got == exp
+    # greedy with the same plan machinery is unchanged
+    assert dr.generate(model, prompt, 8, prof) == oracle.OracleModel(cfg, w, kv_f16=True).generate(prompt, 8)[0]
+    model.free()
+
+
+def test_sampling_parameters_change_between_replays(gpu, oracle):
+    cfg = M.TINY
+    case("sampling parameters between replays")
+    w = weights(cfg)
+    model = dr.ResidentModel(cfg, w, gpu)
+    plan = dr.DecodePlan(model, dr.Profile(kv_dtype=dr.LT_KV_F32))
+    prompt = M.random_prompt(cfg, 4, seed=2)
+    gr = dr.StepGraph(plan)
+    gr.seed(prompt)
+    plan.set_sampling(1.0, top_k=20, top_p=1.0, seed=5)
+    orc = oracle.OracleModel(cfg, w)
+    for t in prompt:
+        lg = orc.step(t)
+    t = plan.sample_current()
+    assert t == oracle.sample(lg, 1.0, 20, 1.0, 5, 0)
+    gr.capture()
+    settings = [(1.0, 20, 1.0, 5, 1), (0.5, 3, 0.8, 9, 0), (0.0, 20, 1.0, 9, 0)]
+    for T, k, p, seed, c0 in settings:
+        plan.set_sampling(T, top_k=k, top_p=p, seed=seed, counter=c0)
+        for i in range(4):
+            lg = orc.step(t)
+            t_dev = gr.replay_token()
+            t = oracle.sample(lg, T, k, p, seed, c0 + i)
+            assert t_dev == t
+        assert plan.sample_counter() == c0 + 4
+    plan.set_sampling(None)
+    with pytest.raises(RuntimeError):
+        gr.replay_token()
+    gr.free()
+    plan.free()
+    model.free()
