@@ -453,6 +453,41 @@ def cpu_baseline(cfg, weights, prompt, n_decode: int, kv_f16: bool, n_decode_1co
              "tokens_1core_match": toks1 == toks[:n_decode_1core]}, toks)
 
 
+def batched_leg(dev, model, cfg, kv_dtype, batches, prompt_len: int, steps: int, warmup: int) -> list:
+    """Batched decode (BatchDecodePlan): B sequences with prompt_len-token random prompts,
+    prefilled, then `steps` replays of the captured batched step timed with HIP events;
+    aggregate decode tok/s = B * steps / time.  Not the headline (BASELINE's metric is bs=1)."""
+    from llamatov_amd import engine as dr
+    from llamatov_amd import model as M
+    out = []
+    for B in batches:
+        plan = dr.BatchDecodePlan(model, B, dr.Profile(kv_dtype=kv_dtype), max_ctx=cfg.max_ctx,
+                                  hist_cap=steps + warmup + 1)
+        gr = dr.BatchStepGraph(plan)
+        try:
+            for b in range(B):
+                plan.prefill(b, M.random_prompt(cfg, prompt_len, seed=100 + b))
+            gr.capture()
+            for _ in range(warmup):
+                gr.replay()
+            dev.sync()
+            ev = Events(dev)
+            ev.start()
+            for _ in range(steps):
+                gr.replay()
+            ms = ev.stop_ms()
+            dev.sync()
+            ev.free()
+            out.append({"batch": B, "tok_s": round(B * steps / (ms / 1e3), 1),
+                        "ms_per_step": round(ms / steps, 4), "steps": steps,
+                        "context": f"{prompt_len + warmup} .. {prompt_len + warmup + steps}"})
+            log(f"batched decode B={B}: {out[-1]['tok_s']} tok/s, {out[-1]['ms_per_step']} ms/step")
+        finally:
+            gr.free()
+            plan.free()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -480,6 +515,8 @@ def main() -> int:
                          "for counter runs")
     ap.add_argument("--roofline-kernel", default="gateup",
                     choices=["qkv", "attn", "o", "attn_o", "gateup", "down", "vocab"])
+    ap.add_argument("--batched", default="8,32",
+                    help="batch sizes of the batched-decode leg (adds batched_decode; empty to skip)")
     ap.add_argument("--eager", action="store_true",
                     help="launch the step's kernels directly instead of replaying the captured graph "
                          "(same kernels; for profilers that cannot trace graph launches)")
@@ -626,8 +663,12 @@ def main() -> int:
         result["tokens_match_cpu"] = cpu_tokens == tokens[:n_cpu]
 
     runner.free()
+    plan.free()
+    batches = [int(b) for b in args.batched.split(",") if b.strip()]
+    if batches and not args.per_op:
+        log("batched decode leg")
+        result["batched_decode"] = batched_leg(dev, model, cfg, kv_dtype, batches, len(prompt), 64, 8)
     if args.c5:
-        plan.free()
         model.free()
         log("C5 leg")
         result["c5"] = c5_leg(dev, n_decode=args.c5_decode, eager=args.eager)

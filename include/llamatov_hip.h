@@ -353,6 +353,27 @@ LT_API int lt_attn_prefill(lt_ctx* ctx, const float* q, int q_stride, const void
 LT_API int lt_embed_q8_batch(lt_ctx* ctx, const void* emb, const int* toks, float* x, int T, int E, int vocab,
                              int* err);
 
+/* ---- batched decode (bs > 1): B independent sequences, one token of each per step ----
+ * The reference notes batched decode as future work of its device-uniform prefill
+ * (bpd/lib/dev_residency.py:1344-1350); no reference signature.  The step reuses the
+ * prefill's GEMM (lt_q8_gemm_t over the B rows) and these three per-sequence entries; row b
+ * of every result is bit-identical to sequence b decoded alone. */
+
+/* lt_rope_append_batch with row t the next token of sequence t: position len[t], cache rows
+ * of sequence t at kc/vc + t*maxt*nkv*hd elements ([B][maxt][nkv*hd]). */
+LT_API int lt_rope_append_seqs(lt_ctx* ctx, float* qkv, int B, int row_stride, const int* len, int nh, int nkv,
+                               int hd, const float* freqs, void* kc, void* vc, int maxt, int kv_dtype);
+
+/* lt_attn_decode with the query rows q_stride floats apart (the q|k|v rows of the GEMM
+ * output), same results. */
+LT_API int lt_attn_decode_rows(lt_ctx* ctx, const float* q, int q_stride, const void* kc, const void* vc,
+                               const int* len, float* out, int batch, int nh, int nkv, int hd, float scale, int maxt,
+                               int nsplit, int kv_dtype, void* ws, size_t ws_bytes);
+
+/* out[r] = argmax of row r of x [rows][n] (ties to the lowest index, as lt_argmax); with
+ * hist, also hist[r][count[r]] = out[r], count[r] += 1 while < cap. */
+LT_API int lt_argmax_rows(lt_ctx* ctx, const float* x, int rows, int n, int* out, int* hist, int* count, int cap);
+
 /* ---- ggml-compatible numerics (the optional profile; the reference's CPU substrate,
  *      bpd-substrate/bench/bpd_cpu.c:4005-4446 and bpd_gemm_q8_0_cpu.c:22-258) ----
  * Quantizer: d16 = fp16_rne(amax / 127.f), id = amax != 0 ? 127.f / amax : 0,

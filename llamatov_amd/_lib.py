@@ -39,6 +39,10 @@ _SIGS = {
     "lt_silu_mul_quant": (c_int, [_P, _P, _P, _P, _P, c_int]),
     "lt_silu_mul": (c_int, [_P, _P, _P, _P, c_int]),
     "lt_add": (c_int, [_P, _P, _P, _P, c_int]),
+    "lt_rope_append_seqs": (c_int, [_P, _P, c_int, c_int, _P, c_int, c_int, c_int, _P, _P, _P, c_int, c_int]),
+    "lt_attn_decode_rows": (c_int, [_P, _P, c_int, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float, c_int,
+                                    c_int, c_int, _P, c_size_t]),
+    "lt_argmax_rows": (c_int, [_P, _P, c_int, c_int, _P, _P, _P, c_int]),
     "lt_sample_workspace_size": (c_size_t, [c_int]),
     "lt_sample": (c_int, [_P, _P, c_int, _P, _P, _P, _P, c_int, _P, c_size_t]),
     "lt_quant_q8_ggml": (c_int, [_P, _P, _P, _P, c_int]),

@@ -1363,6 +1363,20 @@ int lt_attn_decode(lt_ctx* ctx, const float* q, const void* kc, const void* vc, 
                      ws_bytes, "lt_attn_decode");
 }
 
+int lt_attn_decode_rows(lt_ctx* ctx, const float* q, int q_stride, const void* kc, const void* vc, const int* len,
+                        float* out, int batch, int nh, int nkv, int hd, float scale, int maxt, int nsplit,
+                        int kv_dtype, void* ws, size_t ws_bytes) {
+  LT_REQUIRE(ctx && q && kc && vc && len && out, "lt_attn_decode_rows: null argument");
+  LT_REQUIRE(batch > 0 && q_stride >= nh * hd, "lt_attn_decode_rows: batch=%d q_stride=%d", batch, q_stride);
+  const size_t cb = cache_bytes_of(batch, maxt, nkv, hd, kv_dtype);
+  if (int rc = check_common(nh, nkv, hd, maxt, nsplit, kv_dtype, kc, vc, cb, "lt_attn_decode_rows")) return rc;
+  AttnArgs A = {};
+  A.q = q; A.q_stride = q_stride; A.kc = (void*)kc; A.vc = (void*)vc; A.len = len; A.out = out;
+  A.nh = nh; A.nkv = nkv; A.hd = hd; A.scale = scale; A.maxt = maxt; A.nsplit = nsplit;
+  return launch_attn(ctx, AM_DECODE, kv_dtype == LT_KV_F16, pick_hpw(nh, nkv, hd, cb / batch), batch, A, ws,
+                     ws_bytes, "lt_attn_decode_rows");
+}
+
 int lt_attn_decode_noalloc(lt_ctx* ctx, const float* q, const void* kc, const void* vc, const int* len,
                            float* out, int batch, int nh, int nkv, int hd, float scale, int maxt, int nsplit,
                            int kv_dtype) {

@@ -332,6 +332,53 @@ __global__ __launch_bounds__(256) void k_argmax_s2(const float* __restrict__ pva
   }
 }
 
+// Row-wise argmax of a [rows][n] matrix (the batched decode step's vocab rows): one
+// 1024-thread workgroup per row, 8 loads in flight per thread, the same total order (value,
+// then lowest index) as the single-row argmax; optional per-row histories hist[r][cap].
+__global__ __launch_bounds__(1024) void k_argmax_rows(const float* __restrict__ x, int n, int* __restrict__ out,
+                                                      int* __restrict__ hist, int* __restrict__ count, int cap) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  const int r = blockIdx.x;
+  const float* xr = x + (size_t)r * n;
+  float bv = -__builtin_inff();
+  int bi = 0x7FFFFFFF;
+  for (int base = 0; base < n; base += 1024 * 8) {
+    float v[8];
+    int ix[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int i = base + k * 1024 + (int)threadIdx.x;
+      v[k] = i < n ? xr[i] : -__builtin_inff();
+      ix[k] = i < n ? i : 0x7FFFFFFF;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+      if (am_better(v[k], ix[k], bv, bi)) { bv = v[k]; bi = ix[k]; }
+  }
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) {
+    const float ov = __shfl_xor(bv, m, 64);
+    const int oi = __shfl_xor(bi, m, 64);
+    if (am_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { sv[w] = bv; si[w] = bi; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < 16; k++)
+      if (am_better(sv[k], si[k], bv, bi)) { bv = sv[k]; bi = si[k]; }
+    out[r] = bi;
+    if (hist) {
+      const int c = count[r];
+      if (c >= 0 && c < cap) {
+        hist[(size_t)r * cap + c] = bi;
+        count[r] = c + 1;
+      }
+    }
+  }
+}
+
 inline int grid_for(long n, int per) { return (int)((n + per - 1) / per); }
 
 // ---- numerics self-check (lt_selftest_numerics) ---------------------------------------
@@ -518,6 +565,14 @@ int lt_argmax_record(lt_ctx* ctx, const float* x, int n, int* out, int* hist, in
                      void* ws, size_t ws_bytes) {
   LT_REQUIRE(hist && count && cap > 0, "lt_argmax_record: null history or cap=%d", cap);
   return argmax_impl(ctx, x, n, out, hist, count, cap, ws, ws_bytes);
+}
+
+int lt_argmax_rows(lt_ctx* ctx, const float* x, int rows, int n, int* out, int* hist, int* count, int cap) {
+  LT_REQUIRE(ctx && x && out, "lt_argmax_rows: null argument");
+  LT_REQUIRE(rows > 0 && n > 0, "lt_argmax_rows: rows=%d n=%d", rows, n);
+  LT_REQUIRE(!hist || (count && cap > 0), "lt_argmax_rows: a history needs count and cap > 0");
+  k_argmax_rows<<<rows, 1024, 0, ctx->stream>>>(x, n, out, hist, count, cap);
+  return lt_check_launch("k_argmax_rows");
 }
 
 int lt_selftest_numerics(lt_ctx* ctx, unsigned long long* out) {

@@ -495,8 +495,9 @@ __global__ __launch_bounds__(256) void k_embed_batch(const uint8_t* __restrict__
 // and v, in one workgroup per token: the hd/2 angles of the row's position are evaluated
 // once (lt_sincosf of the same products) into LDS and shared by every head; gridDim.y
 // workgroups share a token's pairs and V elements.  The roped k goes to the cache only (not
-// back into the row).
-template <bool kF16>
+// back into the row).  kSeqs: row t is the next token of sequence t -- position len[t], cache
+// rows of sequence t at [t][maxt][nkv*hd] -- instead of token t of one sequence at *len + t.
+template <bool kF16, bool kSeqs>
 __global__ __launch_bounds__(256) void k_rope_append_batch(float* __restrict__ qkv, int row_stride,
                                                            const int* __restrict__ len, int nh, int nkv, int hd,
                                                            const float* __restrict__ freqs, void* __restrict__ kc,
@@ -504,7 +505,12 @@ __global__ __launch_bounds__(256) void k_rope_append_batch(float* __restrict__ q
   __shared__ float s_sn[128], s_cs[128];
   const int t = blockIdx.x;
   const int half = hd >> 1;
-  const int pos = *len + t;
+  const int pos = kSeqs ? len[t] : *len + t;
+  if (kSeqs) {
+    const size_t seq = (size_t)t * maxt * nkv * hd * (kF16 ? 2 : 4);
+    kc = (uint8_t*)kc + seq;
+    vc = (uint8_t*)vc + seq;
+  }
   for (int j = threadIdx.x; j < half; j += 256) lt_sincosf((float)pos * freqs[j], &s_sn[j], &s_cs[j]);
   __syncthreads();
   float* row = qkv + (size_t)t * row_stride;
@@ -744,12 +750,28 @@ int lt_rope_append_batch(lt_ctx* ctx, float* qkv, int T, int row_stride, const i
              "lt_rope_append_batch: T=%d nh=%d nkv=%d hd=%d row_stride=%d maxt=%d", T, nh, nkv, hd, row_stride, maxt);
   LT_REQUIRE(kv_dtype == LT_KV_F32 || kv_dtype == LT_KV_F16, "lt_rope_append_batch: kv_dtype=%d", kv_dtype);
   if (kv_dtype == LT_KV_F16)
-    k_rope_append_batch<true><<<dim3(T, 4), 256, 0, ctx->stream>>>(qkv, row_stride, len, nh, nkv, hd, freqs, kc, vc,
-                                                                    maxt);
+    k_rope_append_batch<true, false><<<dim3(T, 4), 256, 0, ctx->stream>>>(qkv, row_stride, len, nh, nkv, hd, freqs,
+                                                                           kc, vc, maxt);
   else
-    k_rope_append_batch<false><<<dim3(T, 4), 256, 0, ctx->stream>>>(qkv, row_stride, len, nh, nkv, hd, freqs, kc, vc,
-                                                                     maxt);
+    k_rope_append_batch<false, false><<<dim3(T, 4), 256, 0, ctx->stream>>>(qkv, row_stride, len, nh, nkv, hd, freqs,
+                                                                            kc, vc, maxt);
   return lt_check_launch("k_rope_append_batch");
+}
+
+int lt_rope_append_seqs(lt_ctx* ctx, float* qkv, int B, int row_stride, const int* len, int nh, int nkv, int hd,
+                        const float* freqs, void* kc, void* vc, int maxt, int kv_dtype) {
+  LT_REQUIRE(ctx && qkv && len && freqs && kc && vc, "lt_rope_append_seqs: null argument");
+  LT_REQUIRE(B > 0 && nh > 0 && nkv > 0 && hd > 0 && hd % 2 == 0 && hd <= 256 && maxt > 0 &&
+                 row_stride >= (nh + 2 * nkv) * hd,
+             "lt_rope_append_seqs: B=%d nh=%d nkv=%d hd=%d row_stride=%d maxt=%d", B, nh, nkv, hd, row_stride, maxt);
+  LT_REQUIRE(kv_dtype == LT_KV_F32 || kv_dtype == LT_KV_F16, "lt_rope_append_seqs: kv_dtype=%d", kv_dtype);
+  if (kv_dtype == LT_KV_F16)
+    k_rope_append_batch<true, true><<<dim3(B, 4), 256, 0, ctx->stream>>>(qkv, row_stride, len, nh, nkv, hd, freqs,
+                                                                          kc, vc, maxt);
+  else
+    k_rope_append_batch<false, true><<<dim3(B, 4), 256, 0, ctx->stream>>>(qkv, row_stride, len, nh, nkv, hd, freqs,
+                                                                           kc, vc, maxt);
+  return lt_check_launch("k_rope_append_batch<seqs>");
 }
 
 int lt_len_add_n(lt_ctx* ctx, int* len, int n, int T, int maxt) {

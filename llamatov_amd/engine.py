@@ -523,6 +523,7 @@ class ResidentModel:
         self.arena = arena
         self.load_report = None
         self.tiles = None   # the prefill GEMM's tile-major copies (prefill_tiles)
+        self.output_t: Q8Weight | None = None   # the lm_head's tile-major copy (head_tiles)
         self.tok_embd = top["tok_embd"]
         self.output = top.get("output", self.tok_embd)
         self.output_norm = top["output_norm"]
@@ -571,10 +572,24 @@ class ResidentModel:
             L[k + "_t"] = Q8Weight(None, W.K, t=t, N=W.N)
         self.tiles = base
 
+    def head_tiles(self) -> Q8Weight:
+        """Tile-major copy of the lm_head (the batched decode step's vocab GEMM), built on the
+        device at first use."""
+        if self.output_t is None:
+            W = self.output
+            n = int(_lib.raw("lt_q8_tiles_bytes")(W.N, W.K))
+            t = DevTensor.empty((n,), np.uint8, self.dev)
+            call("lt_q8_tiles", self.dev.handle, W.t.vp, t.vp, W.N, W.K)
+            self.output_t = Q8Weight(None, W.K, t=t, N=W.N)
+        return self.output_t
+
     def free(self) -> None:
         if self.tiles is not None:
             self.dev.free(self.tiles)
             self.tiles = None
+        if self.output_t is not None:
+            self.output_t.t.free()
+            self.output_t = None
         self.arena.free()
 
 
@@ -1010,22 +1025,8 @@ def forward_prefill(plan: DecodePlan, tokens, embeddings: np.ndarray | None = No
     else:
         D.h2d(B.toks.ptr, toks)
         call("lt_embed_q8_batch", h, m.tok_embd.t.vp, B.toks.vp, B.x.vp, T, E, cfg.vocab, plan.err.vp)
-    ws, ws_n = _vp(B.ws), (B.ws.nbytes if B.ws is not None else 0)
-    for il, L in enumerate(m.layers):
-        cache = plan.caches[il]
-        lp = _vp(cache.len_ptr)
-        call("lt_rmsnorm_quant_bm", h, B.x.vp, L["attn_norm"].vp, B.xq.vp, B.xd.vp, T, E, eps)
-        call("lt_q8_gemm_t", h, L["wqkv_t"].t.vp, B.xq.vp, B.xd.vp, _vp(L["bqkv"]), None, B.qkv.vp, T, NQ, E)
-        call("lt_rope_append_batch", h, B.qkv.vp, T, NQ, lp, nh, nkv, hd, m.freqs.vp, cache.k.vp, cache.v.vp,
-             cache.max_seq, p.kv_dtype)
-        call("lt_attn_prefill", h, B.qkv.vp, NQ, cache.k.vp, cache.v.vp, lp, B.att.vp, T, nh, nkv, hd,
-             ctypes.c_float(plan.scale), cache.max_seq, p.attn_nsplit, p.kv_dtype, ws, ws_n)
-        call("lt_quant_q8_bm", h, B.att.vp, B.xq.vp, B.xd.vp, T, QD)
-        call("lt_q8_gemm_t", h, L["wo_t"].t.vp, B.xq.vp, B.xd.vp, None, B.x.vp, B.xres.vp, T, E, QD)
-        call("lt_rmsnorm_quant_bm", h, B.xres.vp, L["ffn_norm"].vp, B.xq.vp, B.xd.vp, T, E, eps)
-        call("lt_q8_gemm_silu_t", h, L["wgu_il_t"].t.vp, B.xq.vp, B.xd.vp, B.v.vp, T, F, E)
-        call("lt_quant_q8_bm", h, B.v.vp, B.xq.vp, B.xd.vp, T, F)
-        call("lt_q8_gemm_t", h, L["wdown_t"].t.vp, B.xq.vp, B.xd.vp, None, B.xres.vp, B.x.vp, T, E, F)
+    _prefill_layers(m, p, B, T, [(c.k.vp, c.v.vp, _vp(c.len_ptr)) for c in plan.caches], plan.max_ctx,
+                    plan.scale)
     call("lt_len_add_n", h, _vp(plan.lens.ptr), len(m.layers), T, plan.max_ctx)
     for cache in plan.caches:   # the host mirror advances with the device lengths
         cache.length += T
@@ -1033,6 +1034,30 @@ def forward_prefill(plan: DecodePlan, tokens, embeddings: np.ndarray | None = No
     D.d2d(plan.carry.ptr, B.x.ptr + (T - 1) * E * 4, E * 4)
     call("lt_q8_gemv_rms_argmax", h, plan.carry.vp, m.output_norm.vp, eps, m.output.t.vp, plan.logits.vp,
          cfg.vocab, E, plan.tok.vp, None, None, 0, plan.am_ws.vp, plan.am_ws.nbytes)
+
+
+def _prefill_layers(m: ResidentModel, p: Profile, B: PrefillBuffers, T: int, caches: list, maxt: int,
+                    scale: float) -> None:
+    """The layers of a batched prefill of the T rows in B.x, one sequence: caches[il] =
+    (k, v, len) device pointers of layer il's cache and its length (read, not advanced)."""
+    cfg, h = m.cfg, m.dev.handle
+    E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
+    QD, NQ = cfg.q_dim, cfg.n_qkv
+    eps = ctypes.c_float(cfg.norm_eps)
+    ws, ws_n = _vp(B.ws), (B.ws.nbytes if B.ws is not None else 0)
+    for il, L in enumerate(m.layers):
+        kp, vp, lp = caches[il]
+        call("lt_rmsnorm_quant_bm", h, B.x.vp, L["attn_norm"].vp, B.xq.vp, B.xd.vp, T, E, eps)
+        call("lt_q8_gemm_t", h, L["wqkv_t"].t.vp, B.xq.vp, B.xd.vp, _vp(L["bqkv"]), None, B.qkv.vp, T, NQ, E)
+        call("lt_rope_append_batch", h, B.qkv.vp, T, NQ, lp, nh, nkv, hd, m.freqs.vp, kp, vp, maxt, p.kv_dtype)
+        call("lt_attn_prefill", h, B.qkv.vp, NQ, kp, vp, lp, B.att.vp, T, nh, nkv, hd, ctypes.c_float(scale), maxt,
+             p.attn_nsplit, p.kv_dtype, ws, ws_n)
+        call("lt_quant_q8_bm", h, B.att.vp, B.xq.vp, B.xd.vp, T, QD)
+        call("lt_q8_gemm_t", h, L["wo_t"].t.vp, B.xq.vp, B.xd.vp, None, B.x.vp, B.xres.vp, T, E, QD)
+        call("lt_rmsnorm_quant_bm", h, B.xres.vp, L["ffn_norm"].vp, B.xq.vp, B.xd.vp, T, E, eps)
+        call("lt_q8_gemm_silu_t", h, L["wgu_il_t"].t.vp, B.xq.vp, B.xd.vp, B.v.vp, T, F, E)
+        call("lt_quant_q8_bm", h, B.v.vp, B.xq.vp, B.xd.vp, T, F)
+        call("lt_q8_gemm_t", h, L["wdown_t"].t.vp, B.xq.vp, B.xd.vp, None, B.xres.vp, B.x.vp, T, E, F)
 
 
 def forward_tokens(plan: DecodePlan, tokens, embeddings: np.ndarray | None = None) -> np.ndarray:
@@ -1158,6 +1183,271 @@ class StepGraph:
             self.graph = ctypes.c_void_p()
             self.graph4 = ctypes.c_void_p()
             self.captured = False
+
+
+# ----------------------------------------------------------------------------------
+# Batched decode (bs > 1): B independent sequences, one token of each per step
+# ----------------------------------------------------------------------------------
+class BatchDecodePlan:
+    """B sequences decoded together (the reference's future-work note on batching its
+    device-uniform path, bpd/lib/dev_residency.py:1344-1350).  Each step takes the next token
+    of every sequence: the linear layers run once over the B rows through the prefill's
+    int8-MFMA GEMM (each weight byte read once per step, not once per sequence), RoPE and the
+    KV append per sequence at its own length, the batched decode attention over each
+    sequence's own cache, and a row-wise argmax.  Row b is bit-identical to sequence b
+    decoded alone by DecodePlan (the GEMM is device-uniform with the GEMV).
+
+    Device state: per layer one K and one V cache of [B][max_ctx][n_kv*head_dim]; lens =
+    [pos[0..B), attn[0..B)] with pos[b] the length of sequence b (shared by its layers) and
+    attn[b] = pos[b] + 1 the rows its next step attends; toks[b]; histories hist[b][cap]."""
+
+    def __init__(self, model: ResidentModel, batch: int, profile: Profile = PRODUCTION_PROFILE,
+                 max_ctx: int | None = None, hist_cap: int = 4096):
+        assert_certified_composition(profile)
+        if profile.numerics != "engine":
+            raise ValueError("batched decode runs the engine's numerics")
+        if "wgu_il" not in model.layers[0]:
+            raise ValueError("batched decode needs the fused gate|up layout (layouts 'fused' or 'both')")
+        if batch < 1:
+            raise ValueError(f"batch={batch}")
+        self.model, self.cfg, self.profile, self.dev = model, model.cfg, profile, model.dev
+        self.B = int(batch)
+        cfg, D = self.cfg, self.dev
+        E, F, B = cfg.n_embd, cfg.n_ff, self.B
+        self.max_ctx = int(max_ctx or cfg.max_ctx)
+        model.prefill_tiles()
+        self.head = model.head_tiles()
+        esz = 2 if profile.kv_dtype == LT_KV_F16 else 4
+        self.slot_bytes = self.max_ctx * cfg.kv_dim * esz
+        self.k = [DevTensor.empty((B * self.slot_bytes,), np.uint8, D) for _ in range(cfg.n_layers)]
+        self.v = [DevTensor.empty((B * self.slot_bytes,), np.uint8, D) for _ in range(cfg.n_layers)]
+        self.lens = DevTensor.empty((2 * B,), np.int32, D)
+        self.toks = DevTensor.empty((B,), np.int32, D)
+        self.err = DevTensor.empty((1,), np.int32, D)
+        self.hist_cap = int(hist_cap)
+        self.hist = DevTensor.empty((B, self.hist_cap), np.int32, D)
+        self.hist_count = DevTensor.empty((B,), np.int32, D)
+        kmax = max(E, F, cfg.q_dim)
+        self.x = DevTensor.empty((B, E), np.float32, D)
+        self.xres = DevTensor.empty((B, E), np.float32, D)
+        self.qkv = DevTensor.empty((B, cfg.n_qkv), np.float32, D)
+        self.att = DevTensor.empty((B, cfg.q_dim), np.float32, D)
+        self.vbuf = DevTensor.empty((B, F), np.float32, D)
+        self.xq = DevTensor.empty((B * kmax,), np.int8, D)
+        self.xd = DevTensor.empty((B * kmax // 32,), np.uint16, D)
+        self.logits = DevTensor.empty((B, cfg.vocab), np.float32, D)
+        aw = _lib.raw("lt_attn_workspace_size")(B, cfg.n_head, cfg.head_dim, profile.attn_nsplit)
+        self.attn_ws = DevTensor.empty((aw,), np.uint8, D) if aw else None
+        self.scale = float(cfg.head_dim ** -0.5)
+        self._prefill: PrefillBuffers | None = None
+        self.length = [0] * B
+        self.reset()
+
+    # -- state --------------------------------------------------------------------
+    def reset(self, b: int | None = None) -> None:
+        """Empty every sequence (or sequence b): length 0, history cleared."""
+        seqs = range(self.B) if b is None else [b]
+        for i in seqs:
+            self.length[i] = 0
+        self._push_lengths()
+        cnt = np.zeros(self.B, np.int32)
+        if b is not None:
+            self.dev.d2h(cnt, self.hist_count.ptr)
+            cnt[b] = 0
+        self.dev.h2d(self.hist_count.ptr, cnt)
+        self.dev.h2d(self.err.ptr, np.zeros(1, np.int32))
+
+    def _push_lengths(self) -> None:
+        pos = np.asarray(self.length, np.int32)
+        self.dev.h2d(self.lens.ptr, np.concatenate([pos, np.minimum(pos + 1, self.max_ctx)]).astype(np.int32))
+
+    def set_tokens(self, toks) -> None:
+        t = np.asarray([int(x) for x in toks], np.int32)
+        if t.size != self.B:
+            raise ValueError(f"{t.size} tokens for a batch of {self.B}")
+        self.dev.h2d(self.toks.ptr, t)
+
+    def read_tokens(self) -> list[int]:
+        out = np.zeros(self.B, np.int32)
+        self.dev.d2h(out, self.toks.ptr)
+        return [int(v) for v in out]
+
+    def read_logits(self) -> np.ndarray:
+        out = np.zeros((self.B, self.cfg.vocab), np.float32)
+        self.dev.d2h(out, self.logits.ptr)
+        return out
+
+    def history(self) -> list[list[int]]:
+        cnt = np.zeros(self.B, np.int32)
+        self.dev.d2h(cnt, self.hist_count.ptr)
+        h = np.zeros((self.B, self.hist_cap), np.int32)
+        self.dev.d2h(h, self.hist.ptr)
+        return [[int(v) for v in h[b, :cnt[b]]] for b in range(self.B)]
+
+    def check_room(self, n: int = 1) -> None:
+        full = [b for b in range(self.B) if self.length[b] + n > self.max_ctx]
+        if full:
+            raise ValueError(f"KV cache full for sequences {full} (max_ctx {self.max_ctx})")
+
+    # -- prefill of one sequence ----------------------------------------------------
+    def prefill(self, b: int, tokens) -> None:
+        """Batched prefill of sequence b's prompt (continuing at its current length): its KV
+        rows, its length, and -- from the last prompt token -- its logits row and greedy token
+        (not recorded in the history), bit-identical to forward_prefill of a lone sequence."""
+        toks = np.asarray([int(t) for t in np.asarray(tokens).reshape(-1)], np.int32)
+        T = int(toks.size)
+        if not 0 <= b < self.B:
+            raise ValueError(f"sequence {b} of a batch of {self.B}")
+        if T == 0:
+            return
+        if self.length[b] + T > self.max_ctx:
+            raise ValueError(f"prefill of {T} tokens overflows sequence {b}'s {self.max_ctx}-position cache")
+        cfg, m, D = self.cfg, self.model, self.dev
+        h, E = D.handle, cfg.n_embd
+        if self._prefill is None or self._prefill.T < T:
+            if self._prefill is not None:
+                D.sync()
+                self._prefill.free()
+            self._prefill = PrefillBuffers(self, max(T, 32))
+        Bf = self._prefill
+        D.h2d(Bf.toks.ptr, toks)
+        call("lt_embed_q8_batch", h, m.tok_embd.t.vp, Bf.toks.vp, Bf.x.vp, T, E, cfg.vocab, self.err.vp)
+        lp = self.lens.ptr + 4 * b
+        off = b * self.slot_bytes
+        _prefill_layers(m, self.profile, Bf, T, [(self.k[il].ptr + off, self.v[il].ptr + off, lp)
+                                                 for il in range(cfg.n_layers)], self.max_ctx, self.scale)
+        call("lt_len_add", h, _vp(lp), T, self.max_ctx)
+        call("lt_len_add", h, _vp(self.lens.ptr + 4 * (self.B + b)), T, self.max_ctx)
+        self.length[b] += T
+        call("lt_rmsnorm_quant_bm", h, Bf.x.ptr + (T - 1) * E * 4, m.output_norm.vp, Bf.xq.vp, Bf.xd.vp, 1, E,
+             ctypes.c_float(cfg.norm_eps))
+        call("lt_q8_gemm_t", h, self.head.t.vp, Bf.xq.vp, Bf.xd.vp, None, None, self.logits.ptr + b * cfg.vocab * 4,
+             1, cfg.vocab, E)
+        call("lt_argmax_rows", h, self.logits.ptr + b * cfg.vocab * 4, 1, cfg.vocab, self.toks.ptr + 4 * b, None,
+             None, 0)
+        D.sync()
+
+    # -- the batched step -----------------------------------------------------------
+    def enqueue_step(self) -> None:
+        """Launch one token of every sequence: embed -> layers -> vocab GEMM -> row argmax."""
+        cfg, m, p, B = self.cfg, self.model, self.profile, self.B
+        h = self.dev.handle
+        E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
+        QD, NQ, V = cfg.q_dim, cfg.n_qkv, cfg.vocab
+        eps = ctypes.c_float(cfg.norm_eps)
+        pos, attn = _vp(self.lens.ptr), _vp(self.lens.ptr + 4 * B)
+        ws, ws_n = _vp(self.attn_ws), (self.attn_ws.nbytes if self.attn_ws is not None else 0)
+        call("lt_embed_q8_batch", h, m.tok_embd.t.vp, self.toks.vp, self.x.vp, B, E, cfg.vocab, self.err.vp)
+        for il, L in enumerate(m.layers):
+            kp, vp = self.k[il].vp, self.v[il].vp
+            call("lt_rmsnorm_quant_bm", h, self.x.vp, L["attn_norm"].vp, self.xq.vp, self.xd.vp, B, E, eps)
+            call("lt_q8_gemm_t", h, L["wqkv_t"].t.vp, self.xq.vp, self.xd.vp, _vp(L["bqkv"]), None, self.qkv.vp,
+                 B, NQ, E)
+            call("lt_rope_append_seqs", h, self.qkv.vp, B, NQ, pos, nh, nkv, hd, m.freqs.vp, kp, vp, self.max_ctx,
+                 p.kv_dtype)
+            call("lt_attn_decode_rows", h, self.qkv.vp, NQ, kp, vp, attn, self.att.vp, B, nh, nkv, hd,
+                 ctypes.c_float(self.scale), self.max_ctx, p.attn_nsplit, p.kv_dtype, ws, ws_n)
+            call("lt_quant_q8_bm", h, self.att.vp, self.xq.vp, self.xd.vp, B, QD)
+            call("lt_q8_gemm_t", h, L["wo_t"].t.vp, self.xq.vp, self.xd.vp, None, self.x.vp, self.xres.vp, B, E, QD)
+            call("lt_rmsnorm_quant_bm", h, self.xres.vp, L["ffn_norm"].vp, self.xq.vp, self.xd.vp, B, E, eps)
+            call("lt_q8_gemm_silu_t", h, L["wgu_il_t"].t.vp, self.xq.vp, self.xd.vp, self.vbuf.vp, B, F, E)
+            call("lt_quant_q8_bm", h, self.vbuf.vp, self.xq.vp, self.xd.vp, B, F)
+            call("lt_q8_gemm_t", h, L["wdown_t"].t.vp, self.xq.vp, self.xd.vp, None, self.xres.vp, self.x.vp, B, E, F)
+        call("lt_len_add_n", h, _vp(self.lens.ptr), 2 * B, 1, self.max_ctx)
+        call("lt_rmsnorm_quant_bm", h, self.x.vp, m.output_norm.vp, self.xq.vp, self.xd.vp, B, E, eps)
+        call("lt_q8_gemm_t", h, self.head.t.vp, self.xq.vp, self.xd.vp, None, None, self.logits.vp, B, V, E)
+        call("lt_argmax_rows", h, self.logits.vp, B, V, self.toks.vp, self.hist.vp, self.hist_count.vp,
+             self.hist_cap)
+
+    def step(self, toks=None) -> None:
+        """Eager step (toks=None: each sequence continues from its device token)."""
+        self.check_room(1)
+        if toks is not None:
+            self.set_tokens(toks)
+        self.enqueue_step()
+        self.dev.sync()
+        self.length = [n + 1 for n in self.length]
+
+    def free(self) -> None:
+        self.dev.sync()
+        if self._prefill is not None:
+            self._prefill.free()
+        for t in [*self.k, *self.v, self.lens, self.toks, self.err, self.hist, self.hist_count, self.x, self.xres,
+                  self.qkv, self.att, self.vbuf, self.xq, self.xd, self.logits, self.attn_ws]:
+            if t is not None:
+                t.free()
+
+
+class BatchStepGraph:
+    """The batched step captured once and replayed per token (all sequences advance)."""
+
+    def __init__(self, plan: BatchDecodePlan):
+        self.plan, self.dev = plan, plan.dev
+        self.graph = ctypes.c_void_p()
+
+    def capture(self) -> None:
+        if self.graph.value:
+            raise RuntimeError("BatchStepGraph.capture: already captured")
+        call("lt_graph_begin", self.dev.handle)
+        try:
+            self.plan.enqueue_step()
+        except Exception:
+            g = ctypes.c_void_p()
+            _lib.raw("lt_graph_end")(self.dev.handle, ctypes.byref(g))
+            if g.value:
+                _lib.raw("lt_graph_free")(g)
+            raise
+        call("lt_graph_end", self.dev.handle, ctypes.byref(self.graph))
+
+    def replay(self) -> None:
+        if not self.graph.value:
+            raise RuntimeError("call capture() before replay")
+        self.plan.check_room(1)
+        call("lt_graph_launch", self.dev.handle, self.graph)
+        self.plan.length = [n + 1 for n in self.plan.length]
+
+    def replay_tokens(self, n: int) -> list[list[int]]:
+        """n back-to-back replays; the generated ids of every sequence, read once at the end."""
+        before = [len(h) for h in self.plan.history()]
+        if max(before) + n > self.plan.hist_cap:
+            raise ValueError(f"token history capacity {self.plan.hist_cap} exceeded")
+        self.plan.check_room(n)
+        for _ in range(n):
+            self.replay()
+        return [h[s:s + n] for h, s in zip(self.plan.history(), before)]
+
+    def free(self) -> None:
+        if self.graph.value:
+            call("lt_graph_free", self.graph)
+            self.graph = ctypes.c_void_p()
+
+
+def batch_generate(model: ResidentModel, prompts, n_tokens: int, profile: Profile = PRODUCTION_PROFILE,
+                   max_ctx: int | None = None) -> list[list[int]]:
+    """Greedy generation of n_tokens after each of len(prompts) prompts, decoded together:
+    each prompt prefilled (batched GEMM), the first token its greedy argmax, then n_tokens - 1
+    replays of the captured batched step.  Sequence b's tokens equal generate(model,
+    prompts[b], n_tokens)."""
+    prompts = [[int(t) for t in np.asarray(pr).reshape(-1)] for pr in prompts]
+    if not prompts or any(not pr for pr in prompts):
+        raise ValueError("batch_generate: every prompt needs at least one token")
+    if n_tokens < 1:
+        return [[] for _ in prompts]
+    need = max(len(pr) for pr in prompts) + n_tokens - 1
+    plan = BatchDecodePlan(model, len(prompts), profile, max_ctx=max(max_ctx or 0, need, 1), hist_cap=n_tokens)
+    gr = BatchStepGraph(plan)
+    try:
+        for b, pr in enumerate(prompts):
+            plan.prefill(b, pr)
+        out = [[t] for t in plan.read_tokens()]
+        if n_tokens > 1:
+            gr.capture()
+            for o, more in zip(out, gr.replay_tokens(n_tokens - 1)):
+                o.extend(more)
+        return out
+    finally:
+        gr.free()
+        plan.free()
 
 
 def generate(model, input_ids, n_tokens: int, profile: Profile = PRODUCTION_PROFILE,
