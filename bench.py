@@ -488,6 +488,83 @@ def batched_leg(dev, model, cfg, kv_dtype, batches, prompt_len: int, steps: int,
     return out
 
 
+def sampled_leg(dev, plan, prompt, steps: int) -> dict:
+    """The C2 decode with the device sampler drawing every token (temperature 0.8, top-k 40,
+    top-p 0.95): one graph replay per token, timed with HIP events, plus the sampler's own
+    launch pair (lt_sample on the 151936 logits) timed back to back."""
+    from llamatov_amd import engine as dr
+    from llamatov_amd import _lib
+    cfg = plan.cfg
+    dev.h2d(plan.lens.ptr, np.full(cfg.n_layers, len(prompt), np.int32))
+    for c in plan.caches:
+        c.length = len(prompt)
+    plan.set_sampling(0.8, top_k=40, top_p=0.95, seed=1)
+    gr = dr.StepGraph(plan)
+    try:
+        gr.capture()
+        for _ in range(4):
+            gr._launch()
+        dev.sync()
+        dev.h2d(plan.lens.ptr, np.full(cfg.n_layers, len(prompt), np.int32))
+        for c in plan.caches:
+            c.length = len(prompt)
+        ev = Events(dev)
+        ev.start()
+        for _ in range(steps):
+            gr._launch()
+        ms = ev.stop_ms()
+        dev.sync()
+        ev.free()
+        us = graph_us_per_launch(dev, [lambda: plan._enqueue_sample(record=False)], reps=20)
+    finally:
+        gr.free()
+        plan.set_sampling(None)
+    return {"tok_s": round(steps / (ms / 1e3), 1), "ms_per_step": round(ms / steps, 4),
+            "settings": "temperature 0.8, top_k 40, top_p 0.95", "sampler_us": round(us, 2)}
+
+
+def ggml_leg(dev, model, prompt, steps: int) -> dict:
+    """The ggml-compatible numerics profile: its per-op decode step at C2 (graph replays, HIP
+    events) and its GEMV (vec_dot order) on the C1 and vocab shapes over rotated weights."""
+    from llamatov_amd import engine as dr
+    from llamatov_amd._lib import LT_GGML_VEC, LT_KV_F16, call
+    cfg = model.cfg
+    plan = dr.DecodePlan(model, dr.Profile(kv_dtype=LT_KV_F16, fused_step=False, numerics="ggml"))
+    gr = dr.StepGraph(plan)
+    out = {}
+    try:
+        gr.seed(prompt)
+        gr.capture()
+        for _ in range(4):
+            gr._launch()
+        dev.sync()
+        ev = Events(dev)
+        ev.start()
+        for _ in range(steps):
+            gr._launch()
+        ms = ev.stop_ms()
+        dev.sync()
+        ev.free()
+        out["decode_tok_s"] = round(steps / (ms / 1e3), 1)
+        h = dev.handle
+        for name, W in (("c1_4864x896", model.layers[0]["wgu"]), ("vocab_151936x896", model.output)):
+            N, K = W.N, W.K
+            if name.startswith("c1"):
+                N = 4864
+            mats, extra = rotation(dev, [W.t])
+            fns = [lambda t=t, N=N, K=K: call("lt_q8_gemv_ggml", h, t.vp, plan.xq.vp, plan.xd.vp, None,
+                                               plan.logits.vp, N, K, LT_GGML_VEC) for t in mats]
+            us = graph_us_per_launch(dev, fns)
+            nbytes = N * (K // 32) * 34 + K + K // 16 + 4 * N
+            out[name] = {"us": round(us, 2), "GB/s": round(nbytes / us / 1e3, 1)}
+            for t in extra:
+                t.free()
+    finally:
+        gr.free()
+        plan.free()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -517,6 +594,9 @@ def main() -> int:
                     choices=["qkv", "attn", "o", "attn_o", "gateup", "down", "vocab"])
     ap.add_argument("--batched", default="8,32",
                     help="batch sizes of the batched-decode leg (adds batched_decode; empty to skip)")
+    ap.add_argument("--no-sampled", action="store_true", help="skip the sampled-decode leg")
+    ap.add_argument("--ggml", action="store_true",
+                    help="also run the ggml-compatible numerics profile (adds ggml_numerics)")
     ap.add_argument("--eager", action="store_true",
                     help="launch the step's kernels directly instead of replaying the captured graph "
                          "(same kernels; for profilers that cannot trace graph launches)")
@@ -537,7 +617,9 @@ def main() -> int:
         dev = dr.get_device()
         model = dr.ResidentModel(cfg, w, dev, layouts="fused")
         plan = dr.DecodePlan(model, dr.Profile(kv_dtype=LT_KV_F16))
-        dr.forward_prefill(plan, M.random_prompt(cfg, args.prompt, seed=7))
+        # the cache as the timed decode sees it on average (prompt + half the steps), so the
+        # attention runs at the length of the main bench line's step table
+        dr.forward_prefill(plan, M.random_prompt(cfg, args.prompt + args.steps // 2, seed=7))
         entry = step_kernels(dev, plan, only=args.roofline_kernel)[0]
         src = model.layers[0]["wgu_il"].t
         dst = dr.DevTensor.empty(src.shape, src.dtype, dev)
@@ -555,7 +637,7 @@ def main() -> int:
     w = M.synth_weights(cfg, seed=1234)
     log(f"weights ready in {time.perf_counter() - t0:.1f}s; uploading")
     dev = dr.get_device()
-    model = dr.ResidentModel(cfg, w, dev, layouts="per_op" if args.per_op else "fused")
+    model = dr.ResidentModel(cfg, w, dev, layouts="per_op" if args.per_op else ("both" if args.ggml else "fused"))
     plan = dr.DecodePlan(model, dr.Profile(kv_dtype=kv_dtype, fused_step=not args.per_op), hist_cap=4096)
     runner = dr.StepGraph(plan)
     prompt = M.random_prompt(cfg, args.prompt, seed=7)
@@ -663,7 +745,13 @@ def main() -> int:
         result["tokens_match_cpu"] = cpu_tokens == tokens[:n_cpu]
 
     runner.free()
+    if not args.no_sampled and not args.eager:
+        log("sampled decode leg")
+        result["sampled_decode"] = sampled_leg(dev, plan, prompt, 64)
     plan.free()
+    if args.ggml:
+        log("ggml numerics leg")
+        result["ggml_numerics"] = ggml_leg(dev, model, prompt, 64)
     batches = [int(b) for b in args.batched.split(",") if b.strip()]
     if batches and not args.per_op:
         log("batched decode leg")

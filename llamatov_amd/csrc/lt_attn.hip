@@ -60,6 +60,7 @@ struct AttnArgs {
   float scale;
   int maxt, nsplit, per_max;
   int inwg;             // 1: this workgroup computes all nsplit splits of its row and merges them
+  int xcd_groups;       // k_attn_w1, one split, one row: workgroup i serves KV group i % 8 (slot i / 8)
 };
 
 constexpr int kMaxInWgSplits = 16;   // splits one workgroup can hold (partial outputs in registers)
@@ -522,7 +523,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   float* srm = (float*)sv;                          // kRM: [3][nsplit*HPW] m_s, Z_s, w_s; then [HPW] Z
   const int l = threadIdx.x;
   const int sp = blockIdx.x;
-  const int h0 = blockIdx.y * HPW;
+  // xcd_groups: workgroups are dealt to the 8 XCDs round-robin by id, so id i runs on XCD
+  // i % 8; giving XCD g all the workgroups of KV group g keeps the group's K/V rows in one L2
+  // (fetched from HBM once, not once per head); ids whose XCD has no group exit at once
+  int h0 = blockIdx.y * HPW;
+  if (A.xcd_groups) {
+    const int x = (int)(blockIdx.y & 7u), k = (int)(blockIdx.y >> 3);
+    if (x >= A.nkv) return;
+    h0 = x * (A.nh / A.nkv) + k * HPW;
+  }
   // kRM: the longest rows first (a row's work grows with its position)
   const int b = kRM ? (int)(gridDim.z - 1 - blockIdx.z) : (int)blockIdx.z;
   const int rep = A.nh / A.nkv;
@@ -1247,7 +1256,17 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
   }
   if (w1) {
     A.per_max = per_max;
-    const dim3 grid(A.nsplit, A.nh / h, rows);
+    dim3 grid(A.nsplit, A.nh / h, rows);
+    // one step row, one split, several workgroups per KV group, at most 8 groups: place each
+    // group's workgroups on one XCD (LT_ATTN_XCD=0 keeps the plain order, for comparison)
+    static const bool xcd = [] {
+      const char* s = getenv("LT_ATTN_XCD");
+      return !(s && s[0] == '0');
+    }();
+    if (xcd && mode == AM_STEP && A.nsplit == 1 && rows == 1 && A.nkv <= 8 && A.nh / A.nkv > h) {
+      A.xcd_groups = 1;
+      grid.y = 8 * (A.nh / A.nkv / h);
+    }
     hipError_t e;
     if (mode == AM_STEP)
       e = f16 ? launch_w1<true, AM_STEP>(h, dpl, grid, w1_shm, ctx->stream, A)
