@@ -305,7 +305,7 @@ def attention_sweep(dev, reps: int = 20) -> list[dict]:
             q = dr.DevTensor.from_host(rng.standard_normal(B * nh * hd).astype(np.float32), dev)
             lens = dr.DevTensor.from_host(np.full(B, L, np.int32), dev)
             o = dr.DevTensor.empty((B * nh * hd,), np.float32, dev)
-            nsplit = max(1, min(128, (L + 255) // 256))   # ~256 positions per split
+            nsplit = dr.attn_nsplit_for(B, L, nkv)   # 8 workgroups per CU, 64 .. 512 rows per split
             wsn = raw("lt_attn_workspace_size")(B, nh, hd, nsplit)
             ws = dr.DevTensor.empty((max(wsn, 16),), np.uint8, dev)
             args = (dev.handle, q.vp, kc.vp, vc.vp, lens.vp, o.vp, B, nh, nkv, hd, ctypes.c_float(hd ** -0.5), L,
@@ -592,7 +592,7 @@ def main() -> int:
                          "for counter runs")
     ap.add_argument("--roofline-kernel", default="gateup",
                     choices=["qkv", "attn", "o", "attn_o", "gateup", "down", "vocab"])
-    ap.add_argument("--batched", default="8,32",
+    ap.add_argument("--batched", default="8,64",
                     help="batch sizes of the batched-decode leg (adds batched_decode; empty to skip)")
     ap.add_argument("--no-sampled", action="store_true", help="skip the sampled-decode leg")
     ap.add_argument("--ggml", action="store_true",

@@ -370,6 +370,22 @@ LT_API int lt_attn_decode_rows(lt_ctx* ctx, const float* q, int q_stride, const 
                                const int* len, float* out, int batch, int nh, int nkv, int hd, float scale, int maxt,
                                int nsplit, int kv_dtype, void* ws, size_t ws_bytes);
 
+/* lt_rmsnorm_quant over T rows with row-major output (xq [T][N], xd [T][N/32]): row t is
+ * bit-identical to lt_rmsnorm_quant of that row alone. */
+LT_API int lt_rmsnorm_quant_rows(lt_ctx* ctx, const float* x, const float* w, int8_t* xq, uint16_t* xd, int T,
+                                 int N, float eps);
+
+/* The Q8_0 GEMV over T tokens at once (W [N][K/32] GGUF blocks; row-major quants xq [T][K],
+ * xd [T][K/32]): each weight block read once per group of up to 8 tokens; y[t][row] is
+ * bit-identical to lt_q8_gemv of token t.  epi: LT_MULTI_STORE (y [T][N], plus add[row] when
+ * add is given: a bias), LT_MULTI_RESID (y = v + add[t][row]), LT_MULTI_SILU (rows 2j / 2j+1
+ * are gate j / up j: y[t][j] = SiLU(g)*u, y [T][N/2]). */
+#define LT_MULTI_STORE 0
+#define LT_MULTI_RESID 1
+#define LT_MULTI_SILU 2
+LT_API int lt_q8_gemv_multi(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd, int T,
+                            const float* add, float* y, int N, int K, int epi);
+
 /* out[r] = argmax of row r of x [rows][n] (ties to the lowest index, as lt_argmax); with
  * hist, also hist[r][count[r]] = out[r], count[r] += 1 while < cap. */
 LT_API int lt_argmax_rows(lt_ctx* ctx, const float* x, int rows, int n, int* out, int* hist, int* count, int cap);

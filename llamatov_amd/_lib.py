@@ -19,6 +19,7 @@ LT_KV_F16 = 1
 LT_GGML_VEC = 0
 LT_GGML_LLAMAFILE = 1
 LT_SAMPLE_MAX_K = 1024
+LT_MULTI_STORE, LT_MULTI_RESID, LT_MULTI_SILU = 0, 1, 2
 
 _P = c_void_p
 # name -> (restype, argtypes)
@@ -43,6 +44,8 @@ _SIGS = {
     "lt_attn_decode_rows": (c_int, [_P, _P, c_int, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float, c_int,
                                     c_int, c_int, _P, c_size_t]),
     "lt_argmax_rows": (c_int, [_P, _P, c_int, c_int, _P, _P, _P, c_int]),
+    "lt_rmsnorm_quant_rows": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_float]),
+    "lt_q8_gemv_multi": (c_int, [_P, _P, _P, _P, c_int, _P, _P, c_int, c_int, c_int]),
     "lt_sample_workspace_size": (c_size_t, [c_int]),
     "lt_sample": (c_int, [_P, _P, c_int, _P, _P, _P, _P, c_int, _P, c_size_t]),
     "lt_quant_q8_ggml": (c_int, [_P, _P, _P, _P, c_int]),

@@ -1,0 +1,164 @@
+// lt_multi.hip -- the Q8_0 GEMV over several tokens at once, for the batched decode step at
+// small batch: each weight block is read once and folded against every token's quantized
+// activation, so a step of B tokens streams each weight matrix once per 8 tokens (the prefill
+// GEMM streams it once too, but it is tuned for hundreds of tokens and takes 5x the
+// single-token time at B = 8).
+//
+// Per (row, token) the arithmetic is the single-token GEMV's, bit for bit: lane L of the
+// row's half-wave folds blocks L, L+32, ... with acc = fma(wd*xd, (float)isum, acc) (exact
+// int32 block dot by v_dot4), then the 5-level half-wave tree (the reference's lanes(32)
+// strided accum(fma) tree(shfl_down,5), q8_0_from_facts.pl:466-476).
+//
+// Layout: row-major activation quants xq [T][K], xd [T][K/32] (lt_quant_q8 /
+// lt_rmsnorm_quant_rows over the T rows); a workgroup of 8 half-waves takes 8 consecutive rows
+// and NT tokens (gridDim.y covers T in groups of NT), stages the NT tokens' quants in LDS once
+// (coalesced 16-byte loads, all in flight), and every half-wave streams its row's blocks --
+// each re-aligned to dwords once (load_q8_block) -- against all of them (fold_block, the same
+// fma as fold_raw).
+#include "lt_internal.h"
+#include "lt_q8_device.h"
+
+using namespace lt;
+
+namespace {
+
+constexpr int kMtThreads = 256;
+constexpr int kMtRows = kMtThreads / 32;
+constexpr size_t kMtLdsMax = (size_t)150 * 1024;
+
+enum MtEpi { MT_STORE = 0, MT_RESID = 1, MT_SILU = 2 };
+
+// EPI: MT_STORE y[t][row] = v (+ add[row], a bias); MT_RESID y[t][row] = v + add[t][row];
+// MT_SILU rows 2j, 2j+1 are gate j and up j (interleaved): y[t][j] = SiLU(g)*u, y [T][N/2].
+template <int NT, int EPI>
+__global__ __launch_bounds__(kMtThreads) void k_gemv_multi(const uint8_t* __restrict__ W,
+                                                           const int8_t* __restrict__ xq,
+                                                           const uint16_t* __restrict__ xd, int T,
+                                                           const float* __restrict__ add, float* __restrict__ y,
+                                                           int N, int K) {
+  extern __shared__ __attribute__((aligned(16))) int8_t sxq[];   // [NT][K] quants, then [NT][nb] scales
+  __shared__ float s_v[NT][kMtRows];
+  const int nb = K >> 5;
+  const int lane = threadIdx.x & 31, hw = threadIdx.x >> 5;
+  const int row = blockIdx.x * kMtRows + hw;
+  const int t0 = blockIdx.y * NT;
+  const int nt = T - t0 < NT ? T - t0 : NT;
+  uint16_t* sxd = (uint16_t*)(sxq + (size_t)NT * K);
+  const size_t last = (size_t)N * nb - 1;
+  const size_t g0 = (size_t)(row < N ? row : 0) * nb;   // the row's first global block index
+
+  // this lane's first two blocks are requested before the activations are staged
+  BlockRegs r0, r1;
+  const bool has0 = row < N && lane < nb, has1 = row < N && lane + 32 < nb;
+  if (has0) load_q8_block(W, g0 + lane, last, r0);
+  if (has1) load_q8_block(W, g0 + lane + 32, last, r1);
+
+  // the nt tokens' quants (nt*K contiguous bytes) and scales into LDS, every load in flight
+  {
+    const u32x4* src = (const u32x4*)(xq + (size_t)t0 * K);
+    u32x4* dst = (u32x4*)sxq;
+    const int n16 = nt * K / 16;
+    for (int i = threadIdx.x; i < n16; i += kMtThreads) dst[i] = src[i];
+    const uint16_t* dsrc = xd + (size_t)t0 * nb;
+    for (int i = threadIdx.x; i < nt * nb; i += kMtThreads) sxd[i] = dsrc[i];
+  }
+  __syncthreads();
+
+  float acc[NT];
+#pragma unroll
+  for (int tt = 0; tt < NT; tt++) acc[tt] = 0.0f;
+  auto fold = [&](const BlockRegs& r, int b) {
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++)
+      if (tt < nt) acc[tt] = fold_block(r, sxq + (size_t)tt * K + (size_t)b * 32, sxd[tt * nb + b], acc[tt]);
+  };
+  if (has0) fold(r0, lane);
+  if (has1) fold(r1, lane + 32);
+  // blocks past the first 64 of the row: two in flight per lane
+  for (int b = lane + 64; b < nb && row < N; b += 64) {
+    BlockRegs ra, rb;
+    const bool hb = b + 32 < nb;
+    load_q8_block(W, g0 + b, last, ra);
+    if (hb) load_q8_block(W, g0 + b + 32, last, rb);
+    fold(ra, b);
+    if (hb) fold(rb, b + 32);
+  }
+
+  // the half-wave tree per token; lane 0 holds the row's value
+  float v[NT];
+#pragma unroll
+  for (int tt = 0; tt < NT; tt++) v[tt] = halfwave_tree_dpp(lane < nb ? acc[tt] : 0.0f);
+  if constexpr (EPI == MT_SILU) {
+    if (lane == 0)
+#pragma unroll
+      for (int tt = 0; tt < NT; tt++) s_v[tt][hw] = v[tt];
+    __syncthreads();
+    // 4 gate/up pairs per workgroup: thread (token tt, pair p)
+    const int i = threadIdx.x;
+    if (i < NT * (kMtRows / 2)) {
+      const int tt = i / (kMtRows / 2), p = i - tt * (kMtRows / 2);
+      const int j = blockIdx.x * (kMtRows / 2) + p;
+      if (tt < nt && 2 * j + 1 < N) y[(size_t)(t0 + tt) * (N / 2) + j] = lt_silu_mul(s_v[tt][2 * p], s_v[tt][2 * p + 1]);
+    }
+  } else {
+    if (lane == 0 && row < N) {
+#pragma unroll
+      for (int tt = 0; tt < NT; tt++) {
+        if (tt < nt) {
+          const size_t o = (size_t)(t0 + tt) * N + row;
+          float r = v[tt];
+          if (EPI == MT_STORE && add) r = r + add[row];
+          if (EPI == MT_RESID) r = r + add[o];
+          y[o] = r;
+        }
+      }
+    }
+  }
+}
+
+// tokens per workgroup: the most (up to 8, a power of two) whose staged quants fit the LDS budget
+int mt_tokens(int K, int T) {
+  const size_t per = (size_t)K + (size_t)(K / 32) * 2;
+  int nt = 8;
+  while (nt > 1 && ((size_t)nt * per > kMtLdsMax || nt / 2 >= T)) nt /= 2;
+  return (size_t)nt * per > kMtLdsMax ? 0 : nt;
+}
+
+template <int EPI>
+hipError_t launch_mt(int nt, dim3 grid, size_t shm, hipStream_t st, const uint8_t* W, const int8_t* xq,
+                     const uint16_t* xd, int T, const float* add, float* y, int N, int K) {
+  switch (nt) {
+    case 8: k_gemv_multi<8, EPI><<<grid, kMtThreads, shm, st>>>(W, xq, xd, T, add, y, N, K); break;
+    case 4: k_gemv_multi<4, EPI><<<grid, kMtThreads, shm, st>>>(W, xq, xd, T, add, y, N, K); break;
+    case 2: k_gemv_multi<2, EPI><<<grid, kMtThreads, shm, st>>>(W, xq, xd, T, add, y, N, K); break;
+    default: k_gemv_multi<1, EPI><<<grid, kMtThreads, shm, st>>>(W, xq, xd, T, add, y, N, K); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" {
+
+int lt_q8_gemv_multi(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd, int T, const float* add,
+                     float* y, int N, int K, int epi) {
+  LT_REQUIRE(ctx && W && xq && xd && y, "lt_q8_gemv_multi: null argument");
+  LT_REQUIRE(T > 0 && N > 0 && K > 0 && K % 32 == 0, "lt_q8_gemv_multi: T=%d N=%d K=%d", T, N, K);
+  LT_REQUIRE(epi == MT_STORE || epi == MT_RESID || epi == MT_SILU, "lt_q8_gemv_multi: epi=%d", epi);
+  LT_REQUIRE(epi != MT_RESID || add, "lt_q8_gemv_multi: the residual epilogue needs add");
+  LT_REQUIRE(epi != MT_SILU || N % 2 == 0, "lt_q8_gemv_multi: SiLU rows come in gate/up pairs (N=%d)", N);
+  LT_REQUIRE(lt_aligned(W, 4) && lt_aligned(xq, 16), "lt_q8_gemv_multi: W 4-byte and xq 16-byte aligned");
+  const int nt = mt_tokens(K, T);
+  LT_REQUIRE(nt > 0, "lt_q8_gemv_multi: K=%d: one token's quants exceed the LDS budget", K);
+  const size_t shm = (size_t)nt * ((size_t)K + (size_t)(K / 32) * 2);
+  const dim3 grid((N + kMtRows - 1) / kMtRows, (T + nt - 1) / nt);
+  const uint8_t* w = (const uint8_t*)W;
+  hipError_t e;
+  if (epi == MT_STORE) e = launch_mt<MT_STORE>(nt, grid, shm, ctx->stream, w, xq, xd, T, add, y, N, K);
+  else if (epi == MT_RESID) e = launch_mt<MT_RESID>(nt, grid, shm, ctx->stream, w, xq, xd, T, add, y, N, K);
+  else e = launch_mt<MT_SILU>(nt, grid, shm, ctx->stream, w, xq, xd, T, add, y, N, K);
+  if (e != hipSuccess) return lt_fail_hip(e, "k_gemv_multi", __FILE__, __LINE__);
+  return LT_OK;
+}
+
+}  // extern "C"

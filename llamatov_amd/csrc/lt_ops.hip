@@ -123,7 +123,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__
 // k_rmsnorm followed by k_quant_q8 per row: thread j's elements j, j+256, ... (NPT at most)
 // are loaded at once into registers, with the weights, and folded in that order, then the
 // block tree of rms_inv_block256.
-template <int NPT>
+template <int NPT, bool kRows = false>
 __global__ __launch_bounds__(256) void k_rmsnorm_quant_bm(const float* __restrict__ x,
                                                           const float* __restrict__ w,
                                                           int8_t* __restrict__ xq,
@@ -164,7 +164,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant_bm(const float* __restric
   // 8 lanes per block, 4 elements each (quant4: the quantizer of quant_block_hw)
   const int j = tid & 7;
   for (int b = tid >> 3; b < N / 32; b += 32) {
-    const size_t ob = (size_t)b * T + t;
+    const size_t ob = kRows ? (size_t)t * (N / 32) + b : (size_t)b * T + t;   // kRows: row-major
     const float4 v = *(const float4*)(ybuf + b * 32 + 4 * j);
     QScale sc;
     const uint32_t p = quant4(v.x, v.y, v.z, v.w, sc);
@@ -493,6 +493,19 @@ int lt_rmsnorm_quant_bm(lt_ctx* ctx, const float* x, const float* w, int8_t* xq,
   else if (N <= 4096) k_rmsnorm_quant_bm<16><<<T, 256, shm, ctx->stream>>>(x, w, xq, xd, T, N, eps);
   else k_rmsnorm_quant_bm<64><<<T, 256, shm, ctx->stream>>>(x, w, xq, xd, T, N, eps);
   return lt_check_launch("k_rmsnorm_quant_bm");
+}
+
+int lt_rmsnorm_quant_rows(lt_ctx* ctx, const float* x, const float* w, int8_t* xq, uint16_t* xd, int T, int N,
+                          float eps) {
+  LT_REQUIRE(ctx && x && w && xq && xd, "lt_rmsnorm_quant_rows: null argument");
+  LT_REQUIRE(T > 0 && N > 0 && N % 32 == 0 && N <= 16384,
+             "lt_rmsnorm_quant_rows: T=%d N=%d (N multiple of 32, <= 16384)", T, N);
+  LT_REQUIRE(lt_aligned(xq, 16) && lt_aligned(xd, 2), "lt_rmsnorm_quant_rows: misaligned argument");
+  const size_t shm = (size_t)N * sizeof(float);
+  if (N <= 1024) k_rmsnorm_quant_bm<4, true><<<T, 256, shm, ctx->stream>>>(x, w, xq, xd, T, N, eps);
+  else if (N <= 4096) k_rmsnorm_quant_bm<16, true><<<T, 256, shm, ctx->stream>>>(x, w, xq, xd, T, N, eps);
+  else k_rmsnorm_quant_bm<64, true><<<T, 256, shm, ctx->stream>>>(x, w, xq, xd, T, N, eps);
+  return lt_check_launch("k_rmsnorm_quant_rows");
 }
 
 int lt_q8_gemv_isums(lt_ctx* ctx, const void* W, const int8_t* xq, int32_t* isum, int N, int K) {

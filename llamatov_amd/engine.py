@@ -32,7 +32,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _lib
-from ._lib import LT_GGML_VEC, LT_KV_F16, LT_KV_F32, LT_SAMPLE_MAX_K, call
+from ._lib import LT_GGML_VEC, LT_KV_F16, LT_KV_F32, LT_MULTI_RESID, LT_MULTI_SILU, LT_MULTI_STORE, LT_SAMPLE_MAX_K, call
 from .model import ModelConfig, fused_layer_tensors, interleave_gateup
 
 
@@ -444,6 +444,21 @@ class Profile:
 PRODUCTION_PROFILE = Profile()
 GGML_PROFILE = Profile(fused_step=False, numerics="ggml")
 _CERTIFIED_NSPLIT = {1, 2, 4, 8, 16, 32, 64, 128}
+
+
+def attn_nsplit_for(batch: int, length: int, n_kv_heads: int, num_cus: int = 256) -> int:
+    """A split count for decode attention over `length` cached positions (the reference fixes
+    it per capture, ir_param_axes.pl:303-341): enough workgroups for 8 per CU (one per split,
+    KV group and sequence), at most 512 and at least 64 positions per split, a power of two in
+    1 .. 128.  Measured at C4 (32 q / 8 KV heads, hd 128, fp16): batch 1 picks 64 / 128 / 128
+    splits at 4k / 16k / 32k (15% / 32% / 46% of 8 TB/s; L/256 splits gave 8% / 29% / 46%),
+    batch 8 picks 32 / 32 / 64 (61% / 63% / 61%)."""
+    want = max((8 * num_cus + batch * n_kv_heads - 1) // (batch * n_kv_heads), (length + 511) // 512)
+    cap = min(128, max(1, length // 64))
+    n = 1
+    while n * 2 <= cap and n < want:
+        n *= 2
+    return n
 
 
 def attest_profile(p: Profile) -> dict:
@@ -1188,6 +1203,10 @@ class StepGraph:
 # ----------------------------------------------------------------------------------
 # Batched decode (bs > 1): B independent sequences, one token of each per step
 # ----------------------------------------------------------------------------------
+# the batched step's linear layers: the multi-token GEMV up to here, the GEMM above (C2, graph
+# replays: GEMV 5922 / 17969 / 25527 / 33741 tok/s at B = 8 / 32 / 64 / 128, GEMM 2590 / 10107
+# / 19686 / 38195)
+MULTI_GEMV_MAX_BATCH = 64
 class BatchDecodePlan:
     """B sequences decoded together (the reference's future-work note on batching its
     device-uniform path, bpd/lib/dev_residency.py:1344-1350).  Each step takes the next token
@@ -1202,8 +1221,14 @@ class BatchDecodePlan:
     attn[b] = pos[b] + 1 the rows its next step attends; toks[b]; histories hist[b][cap]."""
 
     def __init__(self, model: ResidentModel, batch: int, profile: Profile = PRODUCTION_PROFILE,
-                 max_ctx: int | None = None, hist_cap: int = 4096):
+                 max_ctx: int | None = None, hist_cap: int = 4096, linear: str = "auto"):
+        """linear: "gemv" runs the step's linear layers through the multi-token GEMV
+        (lt_q8_gemv_multi: GGUF-layout weights, row-major quants, each weight block read once
+        per 8 tokens), "gemm" through the prefill GEMM (tile-major weights), "auto" picks the
+        GEMV up to MULTI_GEMV_MAX_BATCH sequences.  Same bits either way."""
         assert_certified_composition(profile)
+        if linear not in ("auto", "gemv", "gemm"):
+            raise ValueError(f"linear={linear!r}")
         if profile.numerics != "engine":
             raise ValueError("batched decode runs the engine's numerics")
         if "wgu_il" not in model.layers[0]:
@@ -1212,6 +1237,7 @@ class BatchDecodePlan:
             raise ValueError(f"batch={batch}")
         self.model, self.cfg, self.profile, self.dev = model, model.cfg, profile, model.dev
         self.B = int(batch)
+        self.linear = linear if linear != "auto" else ("gemv" if self.B <= MULTI_GEMV_MAX_BATCH else "gemm")
         cfg, D = self.cfg, self.dev
         E, F, B = cfg.n_embd, cfg.n_ff, self.B
         self.max_ctx = int(max_ctx or cfg.max_ctx)
@@ -1330,6 +1356,9 @@ class BatchDecodePlan:
     # -- the batched step -----------------------------------------------------------
     def enqueue_step(self) -> None:
         """Launch one token of every sequence: embed -> layers -> vocab GEMM -> row argmax."""
+        if self.linear == "gemv":
+            self._enqueue_step_gemv()
+            return
         cfg, m, p, B = self.cfg, self.model, self.profile, self.B
         h = self.dev.handle
         E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
@@ -1356,6 +1385,39 @@ class BatchDecodePlan:
         call("lt_len_add_n", h, _vp(self.lens.ptr), 2 * B, 1, self.max_ctx)
         call("lt_rmsnorm_quant_bm", h, self.x.vp, m.output_norm.vp, self.xq.vp, self.xd.vp, B, E, eps)
         call("lt_q8_gemm_t", h, self.head.t.vp, self.xq.vp, self.xd.vp, None, None, self.logits.vp, B, V, E)
+        call("lt_argmax_rows", h, self.logits.vp, B, V, self.toks.vp, self.hist.vp, self.hist_count.vp,
+             self.hist_cap)
+
+    def _enqueue_step_gemv(self) -> None:
+        """The step with the multi-token GEMV: 10 launches per layer, each weight matrix
+        streamed once per 8 sequences from its GGUF-layout blocks."""
+        cfg, m, p, B = self.cfg, self.model, self.profile, self.B
+        h = self.dev.handle
+        E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
+        QD, NQ, V = cfg.q_dim, cfg.n_qkv, cfg.vocab
+        eps = ctypes.c_float(cfg.norm_eps)
+        pos, attn = _vp(self.lens.ptr), _vp(self.lens.ptr + 4 * B)
+        ws, ws_n = _vp(self.attn_ws), (self.attn_ws.nbytes if self.attn_ws is not None else 0)
+        xq, xd = self.xq.vp, self.xd.vp
+        call("lt_embed_q8_batch", h, m.tok_embd.t.vp, self.toks.vp, self.x.vp, B, E, cfg.vocab, self.err.vp)
+        for il, L in enumerate(m.layers):
+            kp, vp = self.k[il].vp, self.v[il].vp
+            call("lt_rmsnorm_quant_rows", h, self.x.vp, L["attn_norm"].vp, xq, xd, B, E, eps)
+            call("lt_q8_gemv_multi", h, L["wqkv"].t.vp, xq, xd, B, _vp(L["bqkv"]), self.qkv.vp, NQ, E,
+                 LT_MULTI_STORE)
+            call("lt_rope_append_seqs", h, self.qkv.vp, B, NQ, pos, nh, nkv, hd, m.freqs.vp, kp, vp, self.max_ctx,
+                 p.kv_dtype)
+            call("lt_attn_decode_rows", h, self.qkv.vp, NQ, kp, vp, attn, self.att.vp, B, nh, nkv, hd,
+                 ctypes.c_float(self.scale), self.max_ctx, p.attn_nsplit, p.kv_dtype, ws, ws_n)
+            call("lt_quant_q8", h, self.att.vp, xq, xd, B * QD)
+            call("lt_q8_gemv_multi", h, L["wo"].t.vp, xq, xd, B, self.x.vp, self.xres.vp, E, QD, LT_MULTI_RESID)
+            call("lt_rmsnorm_quant_rows", h, self.xres.vp, L["ffn_norm"].vp, xq, xd, B, E, eps)
+            call("lt_q8_gemv_multi", h, L["wgu_il"].t.vp, xq, xd, B, None, self.vbuf.vp, 2 * F, E, LT_MULTI_SILU)
+            call("lt_quant_q8", h, self.vbuf.vp, xq, xd, B * F)
+            call("lt_q8_gemv_multi", h, L["wdown"].t.vp, xq, xd, B, self.xres.vp, self.x.vp, E, F, LT_MULTI_RESID)
+        call("lt_len_add_n", h, _vp(self.lens.ptr), 2 * B, 1, self.max_ctx)
+        call("lt_rmsnorm_quant_rows", h, self.x.vp, m.output_norm.vp, xq, xd, B, E, eps)
+        call("lt_q8_gemv_multi", h, m.output.t.vp, xq, xd, B, None, self.logits.vp, V, E, LT_MULTI_STORE)
         call("lt_argmax_rows", h, self.logits.vp, B, V, self.toks.vp, self.hist.vp, self.hist_count.vp,
              self.hist_cap)
 
@@ -1423,7 +1485,7 @@ class BatchStepGraph:
 
 
 def batch_generate(model: ResidentModel, prompts, n_tokens: int, profile: Profile = PRODUCTION_PROFILE,
-                   max_ctx: int | None = None) -> list[list[int]]:
+                   max_ctx: int | None = None, linear: str = "auto") -> list[list[int]]:
     """Greedy generation of n_tokens after each of len(prompts) prompts, decoded together:
     each prompt prefilled (batched GEMM), the first token its greedy argmax, then n_tokens - 1
     replays of the captured batched step.  Sequence b's tokens equal generate(model,
@@ -1434,7 +1496,8 @@ def batch_generate(model: ResidentModel, prompts, n_tokens: int, profile: Profil
     if n_tokens < 1:
         return [[] for _ in prompts]
     need = max(len(pr) for pr in prompts) + n_tokens - 1
-    plan = BatchDecodePlan(model, len(prompts), profile, max_ctx=max(max_ctx or 0, need, 1), hist_cap=n_tokens)
+    plan = BatchDecodePlan(model, len(prompts), profile, max_ctx=max(max_ctx or 0, need, 1), hist_cap=n_tokens,
+                           linear=linear)
     gr = BatchStepGraph(plan)
     try:
         for b, pr in enumerate(prompts):

@@ -29,15 +29,18 @@ def weights(cfg):
     return _W[cfg.name]
 
 
+@pytest.mark.parametrize("linear", ["gemv", "gemm"])
 @pytest.mark.parametrize("kv_dtype,nsplit", [(LT_KV_F32, 1), (LT_KV_F16, 1), (LT_KV_F16, 4)])
-def test_batch_rows_equal_lone_sequences(gpu, oracle, kv_dtype, nsplit):
+def test_batch_rows_equal_lone_sequences(gpu, oracle, kv_dtype, nsplit, linear):
     cfg = M.SMALL_QWEN
-    case(f"batch vs lone sequences kv={kv_dtype} nsplit={nsplit}")
+    case(f"batch vs lone sequences kv={kv_dtype} nsplit={nsplit} linear={linear}")
     w = weights(cfg)
     model = dr.ResidentModel(cfg, w, gpu)
     lens = [3, 9, 1, 14]
     prompts = [M.random_prompt(cfg, n, seed=40 + i) for i, n in enumerate(lens)]
-    plan = dr.BatchDecodePlan(model, len(prompts), dr.Profile(kv_dtype=kv_dtype, attn_nsplit=nsplit), max_ctx=64)
+    plan = dr.BatchDecodePlan(model, len(prompts), dr.Profile(kv_dtype=kv_dtype, attn_nsplit=nsplit), max_ctx=64,
+                              linear=linear)
+    assert plan.linear == linear
     orcs = [oracle.OracleModel(cfg, w, kv_f16=kv_dtype == LT_KV_F16, attn_nsplit=nsplit) for _ in prompts]
     exp = []
     for b, pr in enumerate(prompts):
@@ -79,19 +82,56 @@ def test_batch_rows_equal_lone_sequences(gpu, oracle, kv_dtype, nsplit):
     model.free()
 
 
-def test_batch_generate_c2_geometry(gpu):
-    """batch_generate at the C2 model (Qwen2.5-0.5B geometry, 8 sequences of 32-token
-    prompts) equals generate per sequence."""
+@pytest.mark.parametrize("B,linear", [(8, "auto"), (20, "auto"), (20, "gemm")])
+def test_batch_generate_c2_geometry(gpu, B, linear):
+    """batch_generate at the C2 model (Qwen2.5-0.5B geometry, B sequences of ragged prompts,
+    multi-token GEMV or GEMM linear layers) equals generate per sequence."""
     cfg = M.QWEN25_05B
-    case("batch_generate C2 x8")
+    case(f"batch_generate C2 x{B} {linear}")
     w = weights(cfg)
     model = dr.ResidentModel(cfg, w, gpu)
-    prompts = [M.random_prompt(cfg, 32 - 3 * b, seed=70 + b) for b in range(8)]
+    prompts = [M.random_prompt(cfg, 32 - (3 * b) % 29, seed=70 + b) for b in range(B)]
     prof = dr.Profile(kv_dtype=LT_KV_F16)
-    got = dr.batch_generate(model, prompts, 24, prof)
+    got = dr.batch_generate(model, prompts, 24, prof, linear=linear)
     for b, pr in enumerate(prompts):
         assert got[b] == dr.generate(model, pr, 24, prof), f"sequence {b}"
     model.free()
+
+
+@pytest.mark.parametrize("N,K", [(1152, 896), (896, 4864), (9728, 896), (4096, 14336), (37, 96)])
+@pytest.mark.parametrize("T", [1, 3, 8, 11])
+def test_gemv_multi_equals_gemv(gpu, oracle, N, K, T):
+    """lt_q8_gemv_multi: every token's row values equal the oracle GEMV of that token, for
+    every epilogue; lt_rmsnorm_quant_rows equals the per-row oracle norm + quant."""
+    from llamatov_amd import _lib
+    from llamatov_amd import q8 as hq8
+    case(f"gemv_multi N={N} K={K} T={T}")
+    rng = np.random.default_rng(N + K + T)
+    W = hq8.quantize_rows((rng.standard_normal((N, K)) * 0.05).astype(np.float32))
+    X = (rng.standard_normal((T, K)) * 2).astype(np.float32)
+    nw = (rng.standard_normal(K) * 0.3 + 1).astype(np.float32)
+    xq = dr.DevTensor.empty((T * K,), np.int8, gpu)
+    xd = dr.DevTensor.empty((T * K // 32,), np.uint16, gpu)
+    call("lt_rmsnorm_quant_rows", gpu.handle, dr.DevTensor.from_host(X, gpu).vp, dr.DevTensor.from_host(nw, gpu).vp,
+         xq.vp, xd.vp, T, K, __import__("ctypes").c_float(1e-6))
+    eq, ed = zip(*[oracle.quant_q8(oracle.rmsnorm(X[t], nw, 1e-6)) for t in range(T)])
+    assert np.array_equal(xq.to_host().reshape(T, K), np.stack(eq))
+    assert np.array_equal(xd.to_host().reshape(T, K // 32), np.stack(ed))
+    dW = dr.DevTensor.from_host(W, gpu)
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    resid = rng.standard_normal((T, N)).astype(np.float32)
+    exp = np.stack([oracle.q8_gemv(W, eq[t], ed[t], K) for t in range(T)])
+    for epi, add, want in ((0, None, exp), (0, bias, np.stack([oracle.q8_gemv(W, eq[t], ed[t], K, bias) for t in range(T)])),
+                           (1, resid, np.stack([oracle.q8_gemv(W, eq[t], ed[t], K, resid[t]) for t in range(T)]))):
+        y = dr.DevTensor.empty((T, N), np.float32, gpu)
+        da = dr.DevTensor.from_host(add, gpu) if add is not None else None
+        call("lt_q8_gemv_multi", gpu.handle, dW.vp, xq.vp, xd.vp, T, da.vp if da is not None else None, y.vp, N, K, epi)
+        assert bitexact(y.to_host(), want), f"epi {epi}"
+    if N % 2 == 0:
+        y = dr.DevTensor.empty((T, N // 2), np.float32, gpu)
+        call("lt_q8_gemv_multi", gpu.handle, dW.vp, xq.vp, xd.vp, T, None, y.vp, N, K, 2)
+        want = np.stack([oracle.silu_mul(exp[t][0::2], exp[t][1::2]) for t in range(T)])
+        assert bitexact(y.to_host(), want), "silu"
 
 
 def test_argmax_rows_tie_rule(gpu):

@@ -267,7 +267,10 @@ def test_attention_prefill(gpu, oracle, kv_dtype, nh, nkv, hd, len0, T, nsplit):
 
 
 @pytest.mark.parametrize("B,L,nsplit", [(1, 4096, 32), (8, 4096, 32), (1, 16384, 64), (2, 32768, 128),
-                                         (8, 16384, 64), (8, 32768, 128)])
+                                         (8, 16384, 64), (8, 32768, 128),
+                                         # the split counts engine.attn_nsplit_for picks at C4
+                                         (1, 4096, 64), (1, 16384, 128), (1, 32768, 128), (8, 16384, 32),
+                                         (8, 32768, 64)])
 def test_attention_long_context_batched(gpu, oracle, B, L, nsplit):
     """BASELINE config 4 geometry: 32 Q heads, 8 KV heads, hd 128, fp16 KV."""
     case(f"attn C4 B={B} L={L} nsplit={nsplit}")

@@ -77,6 +77,18 @@ def test_engine_profile_refusals():
             E.assert_certified_composition(bad)
 
 
+def test_attn_nsplit_rule():
+    from llamatov_amd import engine as E
+    certified = {1, 2, 4, 8, 16, 32, 64, 128}
+    for B in (1, 2, 8, 32):
+        for L in (1, 30, 64, 100, 1000, 4096, 6400, 16384, 32768, 131072):
+            n = E.attn_nsplit_for(B, L, 8)
+            assert n in certified
+            assert n == 1 or L // n >= 64                      # at least 64 rows per split
+    assert [E.attn_nsplit_for(1, L, 8) for L in (4096, 16384, 32768)] == [64, 128, 128]
+    assert [E.attn_nsplit_for(8, L, 8) for L in (4096, 16384, 32768)] == [32, 32, 64]
+
+
 def test_load_model_orientation(tmp_path):
     from llamatov_amd import gguf
     from llamatov_amd import llamatov_run as R
