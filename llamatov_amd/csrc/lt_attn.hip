@@ -1055,15 +1055,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
 // split order (attn_decode_split.cu:37-91): M = max m_s, w_s = exp(m_s - M),
 // Z = sum fma(w_s, Z_s), O_d = sum fma(w_s, O_s,d), out = O/Z; optionally the quant of
 // the head's hd/32 blocks.  Every partial is fetched by independent buffer loads issued at
-// the start (kMergeQ >= nsplit: one memory round trip); the exps run one per thread.  len
-// (STEP) marks an out-of-range position: the output is then 0, as in the single pass.
-template <int kMergeQ>   // split outputs prefetched per thread
+// the start (kMergeQ >= nsplit: one memory round trip); the exps run one per thread.  Every
+// thread then runs the max and the two sequential chains (Z and its dimension's O) itself,
+// fully unrolled, so the broadcast LDS reads of m, w and Z_s are batched rather than paid
+// one round trip per split.  len (STEP) marks an out-of-range position: the output is then
+// 0, as in the single pass.
+template <int kMergeQ>   // split outputs prefetched per thread (>= nsplit)
 __global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ wsm, const float* __restrict__ wsz,
                                                     const float* __restrict__ wso, const int* __restrict__ len,
                                                     int maxt, float* __restrict__ out, int8_t* __restrict__ oq,
                                                     uint16_t* __restrict__ od, int nh, int hd, int nsplit) {
-  __shared__ float sm[128], sz[128], sw[128], sout[256];
-  __shared__ float s_Z;
+  __shared__ __attribute__((aligned(16))) float sm[kMergeQ];
+  __shared__ __attribute__((aligned(16))) float sz[kMergeQ];
+  __shared__ __attribute__((aligned(16))) float sw[kMergeQ];
+  __shared__ float sout[256];
   const size_t hrow = (size_t)blockIdx.y * nh + blockIdx.x;
   const int tid = threadIdx.x;
   const __amdgpu_buffer_rsrc_t orsrc =
@@ -1072,17 +1077,15 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ ws
   // surplus values are never folded), so no load waits behind a branch
   float po[kMergeQ];
   const int dcl = tid < hd ? tid : hd - 1;
-  auto load_po = [&](int q0) {
 #pragma unroll
-    for (int q = 0; q < kMergeQ; q++) {
-      const int sq_ = q0 + q < nsplit ? q0 + q : nsplit - 1;
-      po[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(orsrc, dcl * 4, sq_ * hd * 4, 0));
-    }
-  };
-  load_po(0);
-  if (tid < nsplit) {
-    sm[tid] = wsm[hrow * nsplit + tid];
-    sz[tid] = wsz[hrow * nsplit + tid];
+  for (int q = 0; q < kMergeQ; q++) {
+    const int sq_ = q < nsplit ? q : nsplit - 1;
+    po[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(orsrc, dcl * 4, sq_ * hd * 4, 0));
+  }
+  // splits past nsplit: m = -inf (no effect on the max), never folded into Z or O
+  if (tid < kMergeQ) {
+    sm[tid] = tid < nsplit ? wsm[hrow * nsplit + tid] : -INFINITY;
+    sz[tid] = tid < nsplit ? wsz[hrow * nsplit + tid] : 0.0f;
   }
   bool valid = true;
   if (len) {
@@ -1090,25 +1093,25 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ ws
     valid = L >= 0 && L < maxt;
   }
   __syncthreads();
-  float M = -1e30f;
-  for (int q = 0; q < nsplit; q++) M = fmaxf(M, sm[q]);
+  float M = -1e30f;   // fmax is exact and order-free
+#pragma unroll
+  for (int q = 0; q < kMergeQ; q += 4) {
+    const float4 m4 = *(const float4*)(sm + q);
+    M = fmaxf(M, fmaxf(fmaxf(m4.x, m4.y), fmaxf(m4.z, m4.w)));
+  }
   if (tid < nsplit) sw[tid] = lt_expf(sm[tid] - M);
   __syncthreads();
-  if (tid == 0) {
-    float Z = 0.0f;
-    for (int q = 0; q < nsplit; q++) Z = fmaf(sw[q], sz[q], Z);
-    s_Z = Z;
-  }
-  float a = 0.0f;
-  for (int q0 = 0; q0 < nsplit; q0 += kMergeQ) {
-    if (q0 > 0) load_po(q0);
+  float Z = 0.0f, a = 0.0f;
 #pragma unroll
-    for (int q = 0; q < kMergeQ; q++)
-      if (q0 + q < nsplit) a = fmaf(sw[q0 + q], po[q], a);
+  for (int q = 0; q < kMergeQ; q++) {
+    if (q < nsplit) {
+      const float w = sw[q];
+      Z = fmaf(w, sz[q], Z);
+      a = fmaf(w, po[q], a);
+    }
   }
-  __syncthreads();
   if (tid < hd) {
-    const float v = valid ? a / s_Z : 0.0f;
+    const float v = valid ? a / Z : 0.0f;
     if (out) out[hrow * hd + tid] = v;
     sout[tid] = v;
   }
