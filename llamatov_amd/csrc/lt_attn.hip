@@ -310,7 +310,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
   __syncthreads();
   for (int r = 0; r < HPW; r++)
     for (int t = tid; t < n; t += 256)
-      se[r * per_max + t] = lt_expf(se[r * per_max + t] - s_ms[r * nsub + t / spl]);
+      se[r * per_max + t] = lt_expf_sel(se[r * per_max + t] - s_ms[r * nsub + t / spl]);
   __syncthreads();
   for (int q = wave; q < HPW * nsub; q += 4) {
     const int r = q / nsub, sub = q - r * nsub;
@@ -403,7 +403,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
       for (int q = 0; q < nsub; q++) M = fmaxf(M, s_ms[tid * nsub + q]);
       float Z = 0.0f;
       for (int q = 0; q < nsub; q++) {
-        const float w = lt_expf(s_ms[tid * nsub + q] - M);
+        const float w = lt_expf_sel(s_ms[tid * nsub + q] - M);
         s_ms[tid * nsub + q] = w;
         Z = fmaf(w, s_zs[tid * nsub + q], Z);
       }
@@ -816,7 +816,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
       float* e = se + (ns > 0 ? q0 : 0) * HPW + r;
       float mx = -1e30f;
       for (int t = 0; t < ns; t++) mx = fmaxf(mx, e[t * HPW]);
-      for (int t = 0; t < ns; t++) e[t * HPW] = lt_expf(e[t * HPW] - mx);
+      for (int t = 0; t < ns; t++) e[t * HPW] = lt_expf_sel(e[t * HPW] - mx);
       float bt[32];
 #pragma unroll
       for (int j = 0; j < 32; j++) {
@@ -835,7 +835,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
       const int r = pi % HPW;
       float M = -1e30f;
       for (int q = 0; q < A.nsplit; q++) M = fmaxf(M, srm[q * HPW + r]);
-      srm[2 * rm_np + pi] = lt_expf(srm[pi] - M);
+      srm[2 * rm_np + pi] = lt_expf_sel(srm[pi] - M);
     }
     __syncthreads();
     if (l < HPW) {
@@ -847,6 +847,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   // max (order-free: from the stored scores), exps and Z
 #pragma unroll
   for (int r = 0; r < HPW; r++) m[r] = -1e30f;
+#pragma unroll 4
   for (int t = l; t < n; t += 64) {
 #pragma unroll
     for (int r = 0; r < HPW; r++) m[r] = fmaxf(m[r], se[t * HPW + r]);
@@ -856,10 +857,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     m[r] = wave_max(m[r]);
     zs[r] = 0.0f;
   }
+  // (branch-free exps: the heads' and two positions' evaluations interleave)
+#pragma unroll 2
   for (int t = l; t < n; t += 64) {
 #pragma unroll
     for (int r = 0; r < HPW; r++) {
-      const float e = lt_expf(se[t * HPW + r] - m[r]);
+      const float e = lt_expf_sel(se[t * HPW + r] - m[r]);
       se[t * HPW + r] = e;
       zs[r] = zs[r] + e;
     }
@@ -1099,7 +1102,7 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ ws
     const float4 m4 = *(const float4*)(sm + q);
     M = fmaxf(M, fmaxf(fmaxf(m4.x, m4.y), fmaxf(m4.z, m4.w)));
   }
-  if (tid < nsplit) sw[tid] = lt_expf(sm[tid] - M);
+  if (tid < nsplit) sw[tid] = lt_expf_sel(sm[tid] - M);
   __syncthreads();
   float Z = 0.0f, a = 0.0f;
 #pragma unroll
@@ -1124,6 +1127,87 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ ws
   }
 }
 
+// The same merge for head sizes that are a multiple of 32, one wave per (32-dim slice of a
+// query head, row): lane l owns dim l % 32 of the slice (the two half-waves compute the same
+// values; the first one writes them).  The slice's partial outputs of every split
+// (kMergeQ x 128 bytes) arrive by 16-byte loads, eight splits per instruction, all in
+// flight at once (kMergeQ / 8 <= 16 loads per lane; many small workgroups spread the
+// fetch over many CUs), and pass through LDS to the lanes' dims; m and Z of split s come
+// from lane s mod 64.  Splits past nsplit are padded with w = 0, Z_s = 0 and O_s = 0, so
+// the unrolled chains need no per-split test (which would put every step in its own
+// block and serialize the LDS reads): fma(0, 0, c) = c for every c that is not -0, and
+// neither chain is ever -0 (both start at +0, and an exact cancellation rounds to +0).
+// The declared chains over the splits in ascending order, as k_attn_merge runs them --
+// bit-identical to it.
+template <int kMergeQ>   // >= nsplit, a multiple of 8
+__global__ __launch_bounds__(64) void k_attn_merge32(const float* __restrict__ wsm, const float* __restrict__ wsz,
+                                                     const float* __restrict__ wso, const int* __restrict__ len,
+                                                     int maxt, float* __restrict__ out, int8_t* __restrict__ oq,
+                                                     uint16_t* __restrict__ od, int nh, int hd, int nsplit) {
+  constexpr int kM = kMergeQ < 64 ? 64 : kMergeQ;   // m/Z slots: a whole wave's worth
+  constexpr int kLd = kMergeQ / 8;                  // 16-byte loads per lane
+  __shared__ __attribute__((aligned(16))) float so[kMergeQ * 32];
+  __shared__ __attribute__((aligned(16))) float sw[kM];
+  __shared__ __attribute__((aligned(16))) float sz[kM];
+  const int l = threadIdx.x;
+  const int slices = hd >> 5;
+  const int c = (int)blockIdx.x % slices;
+  const size_t hrow = (size_t)blockIdx.y * nh + (size_t)blockIdx.x / slices;
+  // the slice's partials: split s, dims c*32 .. c*32+31 at wso[(hrow*nsplit + s)*hd + c*32]
+  const __amdgpu_buffer_rsrc_t orsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(wso + hrow * nsplit * hd), 0, nsplit * hd * 4, 0x00020000);
+  u32x4 po[kLd];
+#pragma unroll
+  for (int i = 0; i < kLd; i++) {
+    const int sp = 8 * i + (l >> 3);
+    const int sc = sp < nsplit ? sp : nsplit - 1;   // in range; replaced by zeros below
+    po[i] = __builtin_amdgcn_raw_buffer_load_b128(orsrc, (sc * hd + c * 32 + (l & 7) * 4) * 4, 0, 0);
+  }
+  float mv[kM / 64], zv[kM / 64];
+#pragma unroll
+  for (int j = 0; j < kM / 64; j++) {
+    const int sp = l + 64 * j;
+    mv[j] = sp < nsplit ? wsm[hrow * nsplit + sp] : -INFINITY;
+    zv[j] = sp < nsplit ? wsz[hrow * nsplit + sp] : 0.0f;
+  }
+  bool valid = true;
+  if (len) {
+    const int L = *len;
+    valid = L >= 0 && L < maxt;
+  }
+  float M = -1e30f;   // fmax is exact and order-free
+#pragma unroll
+  for (int j = 0; j < kM / 64; j++) M = fmaxf(M, mv[j]);
+  M = wave_max(M);
+#pragma unroll
+  for (int j = 0; j < kM / 64; j++) {
+    const int sp = l + 64 * j;
+    sw[sp] = sp < nsplit ? lt_expf_sel(mv[j] - M) : 0.0f;
+    sz[sp] = zv[j];
+  }
+#pragma unroll
+  for (int i = 0; i < kLd; i++) {
+    const int sp = 8 * i + (l >> 3);
+    const u32x4 z4 = {0u, 0u, 0u, 0u};
+    *(u32x4*)(so + sp * 32 + (l & 7) * 4) = sp < nsplit ? po[i] : z4;
+  }
+  __syncthreads();
+  const int d = l & 31;
+  float Z = 0.0f, a = 0.0f;
+#pragma unroll
+  for (int q = 0; q < kMergeQ; q++) {
+    const float w = sw[q];
+    Z = fmaf(w, sz[q], Z);
+    a = fmaf(w, so[q * 32 + d], a);
+  }
+  if (l < 32) {
+    const float v = valid ? a / Z : 0.0f;
+    const size_t o0 = hrow * hd + (size_t)c * 32;
+    if (out) out[o0 + l] = v;
+    if (oq) quant_block_hw(v, l, oq + o0, od + (o0 >> 5));
+  }
+}
+
 template <bool kF16, int MODE>
 hipError_t launch_attn_k(int hpw, dim3 grid, size_t shm, hipStream_t st, const AttnArgs& A) {
 #define LT_ATTN_CASE(H)                                    \
@@ -1143,9 +1227,29 @@ hipError_t launch_attn_k(int hpw, dim3 grid, size_t shm, hipStream_t st, const A
   return hipGetLastError();
 }
 
-// The merge with a prefetch depth covering nsplit (<= 128, checked by the callers).
+// The merge with a prefetch depth covering nsplit (<= 128, checked by the callers): one wave
+// per 32-dim slice where the head size allows (LT_ATTN_MERGE32=0 keeps k_attn_merge, for
+// comparisons).
 void launch_merge(dim3 grid, hipStream_t st, const float* wsm, const float* wsz, const float* wso, const int* len,
                   int maxt, float* out, int8_t* oq, uint16_t* od, int nh, int hd, int nsplit) {
+  static const bool m32 = [] {
+    const char* s = getenv("LT_ATTN_MERGE32");
+    return !(s && s[0] == '0');
+  }();
+  if (m32 && hd % 32 == 0) {
+    const dim3 g(grid.x * (hd / 32), grid.y);
+    if (nsplit <= 8)
+      k_attn_merge32<8><<<g, 64, 0, st>>>(wsm, wsz, wso, len, maxt, out, oq, od, nh, hd, nsplit);
+    else if (nsplit <= 16)
+      k_attn_merge32<16><<<g, 64, 0, st>>>(wsm, wsz, wso, len, maxt, out, oq, od, nh, hd, nsplit);
+    else if (nsplit <= 32)
+      k_attn_merge32<32><<<g, 64, 0, st>>>(wsm, wsz, wso, len, maxt, out, oq, od, nh, hd, nsplit);
+    else if (nsplit <= 64)
+      k_attn_merge32<64><<<g, 64, 0, st>>>(wsm, wsz, wso, len, maxt, out, oq, od, nh, hd, nsplit);
+    else
+      k_attn_merge32<128><<<g, 64, 0, st>>>(wsm, wsz, wso, len, maxt, out, oq, od, nh, hd, nsplit);
+    return;
+  }
   if (nsplit <= 16)
     k_attn_merge<16><<<grid, 256, 0, st>>>(wsm, wsz, wso, len, maxt, out, oq, od, nh, hd, nsplit);
   else if (nsplit <= 32)
@@ -1213,6 +1317,13 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
     }();
     const int c = cap > 0 ? cap : per_max <= 256 ? 1 : 8;
     while (h > c && h > 1) h /= 2;
+  } else if (mode == AM_DECODE) {
+    // LT_ATTN_DECODE_HPW=H caps a batched decode's heads per wave (sweeps)
+    static const int dcap = [] {
+      const char* s = getenv("LT_ATTN_DECODE_HPW");
+      return s ? atoi(s) : 0;
+    }();
+    while (dcap > 0 && h > dcap && h > 1) h /= 2;
   } else if (mode == AM_PREFILL) {
     // LT_ATTN_PREFILL_HPW=H caps a prefill's heads per wave (sweeps)
     static const int pcap = [] {

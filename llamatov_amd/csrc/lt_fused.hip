@@ -247,7 +247,7 @@ __device__ __forceinline__ void pro_merge_quant(const GemvParams& P, uint32_t* r
     for (int s = 0; s < S; s++) M = fmaxf(M, m[s]);
     float Z = 0.0f, acc = 0.0f;
     for (int s = 0; s < S; s++) {
-      const float w = lt_expf(m[s] - M);
+      const float w = lt_expf_sel(m[s] - M);
       Z = fmaf(w, z[s], Z);
       acc = fmaf(w, P.wso[((size_t)h * S + s) * P.hd + d], acc);
     }
@@ -865,7 +865,7 @@ __global__ __launch_bounds__(kAoThreads) void k_attn_o(AttnOParams P) {
     m = wave_max(m);
     float z = 0.0f;
     for (int t = wl; t < L; t += 64) {
-      const float e = lt_expf(sh[t] - m);
+      const float e = lt_expf_sel(sh[t] - m);
       sh[t] = e;
       z = z + e;
     }

@@ -132,6 +132,39 @@ LT_HD float lt_expf(float xf) {
   return (float)(p * two_k);
 }
 
+/* lt_expf without branches: the same binary64 path on the argument clamped to [-120, 100]
+ * (unchanged inside that range; a nan runs on 0), then selects give the nan, overflow and
+ * underflow results of lt_expf.  Equal to lt_expf for every input; on the GPU independent
+ * calls (several heads' or positions' exps) interleave instead of each running as its own
+ * masked branch. */
+LT_HD float lt_expf_sel(float xf) {
+  const int isnan_ = xf != xf;
+  const float xc = isnan_ ? 0.0f : (xf > 100.0f ? 100.0f : (xf < -120.0f ? -120.0f : xf));
+  double x = (double)xc;
+  double k = lt_rint_d(x * LT_LOG2E);
+  double r = fma(-k, LT_LN2_HI, x);
+  r = fma(-k, LT_LN2_LO, r);
+  double p = 1.0 / 479001600.0;
+  p = fma(p, r, 1.0 / 39916800.0);
+  p = fma(p, r, 1.0 / 3628800.0);
+  p = fma(p, r, 1.0 / 362880.0);
+  p = fma(p, r, 1.0 / 40320.0);
+  p = fma(p, r, 1.0 / 5040.0);
+  p = fma(p, r, 1.0 / 720.0);
+  p = fma(p, r, 1.0 / 120.0);
+  p = fma(p, r, 1.0 / 24.0);
+  p = fma(p, r, 1.0 / 6.0);
+  p = fma(p, r, 0.5);
+  p = fma(p, r, 1.0);
+  p = fma(p, r, 1.0);
+  int ki = (int)k;
+  double two_k = lt_u2d((uint64_t)(ki + 1023) << 52);
+  float v = (float)(p * two_k);
+  v = xf > 100.0f ? lt_u2f(0x7F800000u) : v;
+  v = xf < -120.0f ? 0.0f : v;
+  return isnan_ ? xf : v;
+}
+
 /* ---- sin / cos ------------------------------------------------------------------- */
 #define LT_PIO2_HI 0x1.921fb54442d18p+0   /* binary64(pi/2) */
 #define LT_PIO2_LO 0x1.1a62633145c07p-54  /* binary64(pi/2 - LT_PIO2_HI) */

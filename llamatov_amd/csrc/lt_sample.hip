@@ -300,7 +300,7 @@ __global__ __launch_bounds__(kSmThreads) void k_sample_final(lt_sample_params* _
   if (t < k) {
     const float l = key_logit((uint32_t)(s_key[t] >> 32));
     const float s = (l - l0) * invT;
-    s_e[t] = lt_expf(s);
+    s_e[t] = lt_expf_sel(s);
   }
   __syncthreads();
   if (t == 0) {

@@ -36,6 +36,17 @@ OR_API int or_max_threads(void) { return omp_get_max_threads(); }
 OR_API float or_half_to_float(uint16_t h) { return lt_half_to_float_bits(h); }
 OR_API uint16_t or_float_to_half(float f) { return lt_float_to_half_bits(f); }
 OR_API float or_expf(float x) { return lt_expf(x); }
+/* Bit patterns start, start + stride, ... (count of them, mod 2^32) on which the device's
+ * branch-free lt_expf_sel differs from lt_expf (0: the two forms agree). */
+OR_API uint64_t or_expf_sel_mismatches(uint32_t start, uint32_t stride, uint64_t count) {
+  uint64_t bad = 0;
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+  for (int64_t i = 0; i < (int64_t)count; i++) {
+    const float x = lt_u2f(start + (uint32_t)((uint64_t)i * stride));
+    if (lt_f2u(lt_expf_sel(x)) != lt_f2u(lt_expf(x))) bad++;
+  }
+  return bad;
+}
 OR_API void or_sincosf(float x, float* s, float* c) { lt_sincosf(x, s, c); }
 OR_API float or_rsqrtf(float x) { return lt_rsqrtf(x); }
 

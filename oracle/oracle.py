@@ -43,6 +43,7 @@ def lib() -> ctypes.CDLL:
             "or_half_to_float": (c_float, [ctypes.c_uint16]),
             "or_float_to_half": (ctypes.c_uint16, [c_float]),
             "or_expf": (c_float, [c_float]),
+            "or_expf_sel_mismatches": (ctypes.c_uint64, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint64]),
             "or_sincosf": (None, [c_float, P, P]),
             "or_rsqrtf": (c_float, [c_float]),
             "or_dequant_rows": (None, [P, c_int, c_int, P]),
@@ -98,6 +99,12 @@ def max_threads() -> int:
 # ---- scalar numerics ---------------------------------------------------------------
 def expf(x: float) -> float:
     return lib().or_expf(x)
+
+
+def expf_sel_mismatches(start: int, stride: int, count: int) -> int:
+    """Bit patterns start + i*stride (mod 2^32), i < count, where the device's branch-free
+    lt_expf_sel differs from lt_expf."""
+    return int(lib().or_expf_sel_mismatches(start & 0xFFFFFFFF, stride, count))
 
 
 def sincosf(x: float) -> tuple[float, float]:

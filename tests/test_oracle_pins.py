@@ -63,6 +63,12 @@ def test_expf_within_one_ulp_of_float64(oracle):
     assert oracle.expf(100.0) == float("inf")
 
 
+def test_expf_branch_free_form_equals_expf(oracle):
+    """The kernels' lt_expf_sel (selects instead of branches) equals lt_expf bit for bit on
+    every one of the 2^32 binary32 inputs (nans, infinities, subnormals included)."""
+    assert oracle.expf_sel_mismatches(0, 1, 1 << 32) == 0
+
+
 def test_sincosf_within_one_ulp_of_float64(oracle):
     rng = np.random.default_rng(12)
     x = np.concatenate([rng.uniform(-2100, 2100, 20000), rng.uniform(-4, 4, 10000)]).astype(np.float32)
