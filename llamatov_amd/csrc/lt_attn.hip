@@ -1156,6 +1156,17 @@ __global__ __launch_bounds__(64) void k_attn_merge32(const float* __restrict__ w
   // the slice's partials: split s, dims c*32 .. c*32+31 at wso[(hrow*nsplit + s)*hd + c*32]
   const __amdgpu_buffer_rsrc_t orsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)(wso + hrow * nsplit * hd), 0, nsplit * hd * 4, 0x00020000);
+  // m and Z first: loads complete in order, so the max and the exps then overlap the
+  // partial outputs' fetch
+  float mv[kM / 64], zv[kM / 64];
+#pragma unroll
+  for (int j = 0; j < kM / 64; j++) {
+    const int sp = l + 64 * j;
+    const int sc = sp < nsplit ? sp : nsplit - 1;
+    mv[j] = wsm[hrow * nsplit + sc];
+    zv[j] = wsz[hrow * nsplit + sc];
+  }
+  asm volatile("" ::: "memory");
   u32x4 po[kLd];
 #pragma unroll
   for (int i = 0; i < kLd; i++) {
@@ -1163,12 +1174,13 @@ __global__ __launch_bounds__(64) void k_attn_merge32(const float* __restrict__ w
     const int sc = sp < nsplit ? sp : nsplit - 1;   // in range; replaced by zeros below
     po[i] = __builtin_amdgcn_raw_buffer_load_b128(orsrc, (sc * hd + c * 32 + (l & 7) * 4) * 4, 0, 0);
   }
-  float mv[kM / 64], zv[kM / 64];
 #pragma unroll
   for (int j = 0; j < kM / 64; j++) {
     const int sp = l + 64 * j;
-    mv[j] = sp < nsplit ? wsm[hrow * nsplit + sp] : -INFINITY;
-    zv[j] = sp < nsplit ? wsz[hrow * nsplit + sp] : 0.0f;
+    if (sp >= nsplit) {
+      mv[j] = -INFINITY;
+      zv[j] = 0.0f;
+    }
   }
   bool valid = true;
   if (len) {
