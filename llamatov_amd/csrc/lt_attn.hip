@@ -847,7 +847,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   // max (order-free: from the stored scores), exps and Z
 #pragma unroll
   for (int r = 0; r < HPW; r++) m[r] = -1e30f;
-#pragma unroll 4
   for (int t = l; t < n; t += 64) {
 #pragma unroll
     for (int r = 0; r < HPW; r++) m[r] = fmaxf(m[r], se[t * HPW + r]);
@@ -857,8 +856,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     m[r] = wave_max(m[r]);
     zs[r] = 0.0f;
   }
-  // (branch-free exps: the heads' and two positions' evaluations interleave)
-#pragma unroll 2
   for (int t = l; t < n; t += 64) {
 #pragma unroll
     for (int r = 0; r < HPW; r++) {
