@@ -22,10 +22,12 @@
 // chunk's top k by a 4-pass 8-bit radix select on order-preserving keys (LDS histograms;
 // the crossing digit found by one wave with a shuffle scan) and compacts them in index
 // order, so ties at the threshold keep the lowest indices.  (2) k_sample_final: one
-// workgroup selects the global top k from the chunk survivors the same way (a second radix
-// select on the index resolves ties that straddle the threshold), sorts them by
-// (logit, -index) with a bitonic network in LDS, evaluates the weights in parallel and runs
-// the sequential cumulative sum, the nucleus cut and the draw on one thread.
+// workgroup sorts the chunk survivors by (logit, -index) with a bitonic network in LDS and
+// keeps the first k -- all of them when they are at most 1024; otherwise it first selects
+// the global top k the same way as the chunks (a second radix select on the index resolves
+// ties that straddle the threshold) and sorts those.  It evaluates the weights in parallel,
+// runs the sequential cumulative sum on one thread (its inputs read in batches), and finds
+// the nucleus cut and the draw as minimum indices over the threads.
 #include "lt_internal.h"
 #include "lt_q8_device.h"
 
@@ -60,8 +62,12 @@ __device__ __forceinline__ int sample_k(const lt_sample_params* P, int V) {
   return k < V ? k : V;
 }
 
+constexpr int kSmCopies = 16;    // pass-0 histogram copies (lane mod 16)
+constexpr int kSmCopyStride = 257;   // rows 257 apart: equal digits of different copies in different banks
+
 struct SmShared {
   int hist[256];
+  int hist16[kSmCopies * kSmCopyStride];
   int wave_sum[kSmWaves];
   int sel_digit, sel_rem;
 };
@@ -121,14 +127,36 @@ template <int N>
 __device__ uint32_t radix_select(const uint32_t (&key)[N], const bool (&live)[N], int rem, SmShared& S,
                                  int* rem_out) {
   uint32_t prefix = 0, mask = 0;
+  // pass 0 (the top byte: mostly the exponent, so a few digits hold most keys) counts into
+  // 16 copies of the histogram, one per lane mod 16, so lanes of one atomic instruction
+  // with the same digit hit different banks; the copies are then summed (integer counts:
+  // the same histogram)
+#pragma unroll
+  for (int i = threadIdx.x; i < kSmCopies * kSmCopyStride; i += kSmThreads) S.hist16[i] = 0;
+  __syncthreads();
+  {
+    int* h = S.hist16 + (threadIdx.x & (kSmCopies - 1)) * kSmCopyStride;
+#pragma unroll
+    for (int j = 0; j < N; j++)
+      if (live[j]) atomicAdd(&h[key[j] >> 24], 1);
+  }
+  __syncthreads();
+  if (threadIdx.x < 256) {
+    int c = 0;
+#pragma unroll
+    for (int q = 0; q < kSmCopies; q++) c += S.hist16[q * kSmCopyStride + threadIdx.x];
+    S.hist[threadIdx.x] = c;
+  }
 #pragma unroll 1
   for (int pass = 0; pass < 4; pass++) {
     const int shift = 24 - 8 * pass;
-    if (threadIdx.x < 256) S.hist[threadIdx.x] = 0;
-    __syncthreads();
+    if (pass > 0) {
+      if (threadIdx.x < 256) S.hist[threadIdx.x] = 0;
+      __syncthreads();
 #pragma unroll
-    for (int j = 0; j < N; j++)
-      if (live[j] && (key[j] & mask) == prefix) atomicAdd(&S.hist[(key[j] >> shift) & 255u], 1);
+      for (int j = 0; j < N; j++)
+        if (live[j] && (key[j] & mask) == prefix) atomicAdd(&S.hist[(key[j] >> shift) & 255u], 1);
+    }
     __syncthreads();
     if (threadIdx.x < 64) find_digit(S, rem);
     __syncthreads();
@@ -229,108 +257,185 @@ __global__ __launch_bounds__(kSmThreads) void k_sample_final(lt_sample_params* _
                                                             int* __restrict__ count, int cap) {
   __shared__ SmShared S;
   __shared__ unsigned long long s_key[kSmMaxK];
-  __shared__ float s_e[kSmMaxK];
+  __shared__ __attribute__((aligned(16))) float s_e[kSmMaxK];   // exps in rank order
+  __shared__ float s_c[kSmMaxK];                                // their running sums
   const int t = threadIdx.x;
   const int k = sample_k(P, V);
-  // candidate r of this thread: chunk r, slot t
-  uint32_t key[kSmMaxChunks], nidx[kSmMaxChunks];
-  bool live[kSmMaxChunks];
+  // the chunks' survivor counts (every load at once), then their total M
+  int cnts[kSmMaxChunks];
+  int M = 0;
 #pragma unroll
   for (int r = 0; r < kSmMaxChunks; r++) {
-    live[r] = r < chunks && t < ws.cnt[r];
-    const float v = live[r] ? ws.val[(size_t)r * kSmMaxK + t] : 0.0f;
-    key[r] = order_key(v);
-    nidx[r] = live[r] ? ~(uint32_t)ws.idx[(size_t)r * kSmMaxK + t] : 0u;   // larger = lower index
+    cnts[r] = r < chunks ? ws.cnt[r] : 0;
+    M += cnts[r];
   }
-  int rem;
-  const uint32_t T = radix_select<kSmMaxChunks>(key, live, k, S, &rem);
-  // keys equal to T: all of them, or (when the tie straddles rank k) the rem lowest indices
-  bool eq[kSmMaxChunks];
-  int neq = 0;
-#pragma unroll
-  for (int r = 0; r < kSmMaxChunks; r++) {
-    eq[r] = live[r] && key[r] == T;
-    neq += eq[r];
-  }
-  int eq_total;
-  (void)block_excl_scan(neq, S, &eq_total);
-  uint32_t NT = 0u;   // every equal key qualifies
-  if (eq_total > rem) {
-    int rem2;
-    NT = radix_select<kSmMaxChunks>(nidx, eq, rem, S, &rem2);
-  }
-  int nsel = 0;
-  bool sel[kSmMaxChunks];
-#pragma unroll
-  for (int r = 0; r < kSmMaxChunks; r++) {
-    sel[r] = live[r] && (key[r] > T || (key[r] == T && nidx[r] >= NT));
-    nsel += sel[r];
-  }
-  int total;
-  int o = block_excl_scan(nsel, S, &total);
-  // sort keys: (order key, -index) as one 64-bit value, larger first; padding = 0
+  // Sort keys: (order key, -index) as one 64-bit value, larger first, distinct for distinct
+  // candidates; padding = 0, below every candidate.  The first k of that order are the
+  // selection in either path.
   int P2 = 1;
-  while (P2 < k) P2 <<= 1;
-  if (t < P2) s_key[t] = 0ull;
-  __syncthreads();
+  if (M <= kSmThreads) {
+    // at most one survivor per thread: thread t takes the t-th survivor in chunk order and
+    // every survivor is sorted (no selection pass)
+    while (P2 < M) P2 <<= 1;
+    // its chunk r is the first whose running end exceeds t; `before` is that chunk's start
+    int r = 0, before = 0, end = 0;
 #pragma unroll
-  for (int r = 0; r < kSmMaxChunks; r++)
-    if (sel[r]) s_key[o++] = ((unsigned long long)key[r] << 32) | nidx[r];
-  __syncthreads();
-  for (int size = 2; size <= P2; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      if (t < P2) {
-        const int partner = t ^ stride;
-        if (partner > t) {
-          const bool desc = (t & size) == 0;
-          const unsigned long long a = s_key[t], b = s_key[partner];
-          if (desc ? (a < b) : (a > b)) {
-            s_key[t] = b;
-            s_key[partner] = a;
-          }
-        }
+    for (int q = 0; q < kSmMaxChunks; q++) {
+      end += cnts[q];
+      if (end <= t) {
+        r = q + 1;
+        before = end;
       }
-      __syncthreads();
     }
+    if (t < M) {
+      const size_t slot = (size_t)r * kSmMaxK + (size_t)(t - before);
+      s_key[t] = ((unsigned long long)order_key(ws.val[slot]) << 32) | (uint32_t)~(uint32_t)ws.idx[slot];
+    } else if (t < P2) {
+      s_key[t] = 0ull;
+    }
+    __syncthreads();
+  } else {
+    // candidate r of this thread: chunk r, slot t
+    uint32_t key[kSmMaxChunks], nidx[kSmMaxChunks];
+    bool live[kSmMaxChunks];
+#pragma unroll
+    for (int r = 0; r < kSmMaxChunks; r++) {
+      live[r] = t < cnts[r];
+      const float v = live[r] ? ws.val[(size_t)r * kSmMaxK + t] : 0.0f;
+      key[r] = order_key(v);
+      nidx[r] = live[r] ? ~(uint32_t)ws.idx[(size_t)r * kSmMaxK + t] : 0u;   // larger = lower index
+    }
+    int rem;
+    const uint32_t T = radix_select<kSmMaxChunks>(key, live, k, S, &rem);
+    // keys equal to T: all of them, or (when the tie straddles rank k) the rem lowest indices
+    bool eq[kSmMaxChunks];
+    int neq = 0;
+#pragma unroll
+    for (int r = 0; r < kSmMaxChunks; r++) {
+      eq[r] = live[r] && key[r] == T;
+      neq += eq[r];
+    }
+    int eq_total;
+    (void)block_excl_scan(neq, S, &eq_total);
+    uint32_t NT = 0u;   // every equal key qualifies
+    if (eq_total > rem) {
+      int rem2;
+      NT = radix_select<kSmMaxChunks>(nidx, eq, rem, S, &rem2);
+    }
+    int nsel = 0;
+    bool sel[kSmMaxChunks];
+#pragma unroll
+    for (int r = 0; r < kSmMaxChunks; r++) {
+      sel[r] = live[r] && (key[r] > T || (key[r] == T && nidx[r] >= NT));
+      nsel += sel[r];
+    }
+    int total;
+    int o = block_excl_scan(nsel, S, &total);
+    while (P2 < k) P2 <<= 1;
+    if (t < P2) s_key[t] = 0ull;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kSmMaxChunks; r++)
+      if (sel[r]) s_key[o++] = ((unsigned long long)key[r] << 32) | nidx[r];
+    __syncthreads();
   }
+  // The bitonic network over P2 slots, one key per thread in a register: in each stage the
+  // thread with the lower index of a pair keeps the larger key in a descending block (the
+  // smaller in an ascending one) and its partner the other.  Partners less than 64 apart
+  // are in the same wave and trade keys by shuffles; farther ones through LDS.
+  auto sort_reg = [&](unsigned long long x, int P2n) {
+    for (int size = 2; size <= P2n; size <<= 1)
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        unsigned long long y;
+        if (stride >= 64) {
+          s_key[t] = x;
+          __syncthreads();
+          y = s_key[t ^ stride];
+          __syncthreads();
+        } else {
+          y = __shfl_xor(x, stride, 64);
+        }
+        const bool desc = (t & size) == 0;
+        const bool lower = (t & stride) == 0;
+        const unsigned long long hi = x > y ? x : y, lo = x > y ? y : x;
+        x = desc == lower ? hi : lo;
+      }
+    return x;
+  };
+  if (P2 <= 64) {
+    if (t < 64) {
+      const unsigned long long x = sort_reg(t < P2 ? s_key[t] : 0ull, P2);
+      if (t < P2) s_key[t] = x;
+    }
+  } else {
+    const unsigned long long x = sort_reg(t < P2 ? s_key[t] : 0ull, P2);
+    if (t < P2) s_key[t] = x;
+  }
+  __syncthreads();
   // weights
   const float temp = P->temperature;
   const float invT = temp > 0.0f ? 1.0f / temp : 0.0f;
   const float l0 = key_logit((uint32_t)(s_key[0] >> 32));
-  if (t < k) {
-    const float l = key_logit((uint32_t)(s_key[t] >> 32));
-    const float s = (l - l0) * invT;
-    s_e[t] = lt_expf_sel(s);
+  // exps of the k candidates, zeros up to the next multiple of 16 (c + 0 = c: the sum
+  // is never -0, as every e >= +0)
+  if (t < ((k + 15) & ~15)) {
+    float e = 0.0f;
+    if (t < k) {
+      const float l = key_logit((uint32_t)(s_key[t] >> 32));
+      e = lt_expf_sel((l - l0) * invT);
+    }
+    s_e[t] = e;
   }
+  if (t == 0) S.sel_digit = k;   // the nucleus size n (k when top_p >= 1)
   __syncthreads();
+  const float topp = P->top_p;
+  if (k > 1) {
+    // c_i = c_{i-1} + e_i in rank order on one thread; the exps come in 16 at a time from
+    // an array the sums are not written to, so the reads are batched ahead of the chain
+    if (t == 0) {
+      float c = 0.0f;
+      for (int i = 0; i < k; i += 16) {
+        float e[16];
+#pragma unroll
+        for (int j = 0; j < 16; j += 4) {
+          const float4 v = *(const float4*)&s_e[i + j];
+          e[j] = v.x; e[j + 1] = v.y; e[j + 2] = v.z; e[j + 3] = v.w;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+          c = c + e[j];
+          s_c[i + j] = c;
+        }
+      }
+    }
+    __syncthreads();
+    // n = the smallest i + 1 with c_i >= top_p * c_{k-1}: c is nondecreasing, so the first
+    // such i is the minimum over the candidates that satisfy it
+    if (topp < 1.0f) {
+      const float thr = topp * s_c[k - 1];
+      if (t < k && s_c[t] >= thr) atomicMin(&S.sel_digit, t + 1);
+      __syncthreads();
+    }
+  }
   if (t == 0) {
     int pick = 0;
     if (k > 1) {
-      float c = 0.0f;
-      for (int i = 0; i < k; i++) {
-        c = c + s_e[i];
-        s_e[i] = c;
-      }
-      const float topp = P->top_p;
-      int n = k;
-      if (topp < 1.0f) {
-        const float thr = topp * s_e[k - 1];
-        for (int i = 0; i < k; i++)
-          if (s_e[i] >= thr) {
-            n = i + 1;
-            break;
-          }
-      }
+      const int n = S.sel_digit;
       const uint32_t x = philox_x(P->counter, P->seed);
       const float u = (float)(x >> 8) * 0x1.0p-24f;
-      const float target = u * s_e[n - 1];
-      pick = n - 1;
-      for (int i = 0; i < n; i++)
-        if (s_e[i] > target) {
-          pick = i;
-          break;
-        }
+      S.sel_rem = n - 1;   // the first i < n with c_i > u * c_{n-1}, else n - 1
+      S.wave_sum[0] = __float_as_int(u * s_c[n - 1]);
     }
+  }
+  __syncthreads();
+  if (k > 1) {
+    const int n = S.sel_digit;
+    const float target = __int_as_float(S.wave_sum[0]);
+    if (t < n && s_c[t] > target) atomicMin(&S.sel_rem, t);
+    __syncthreads();
+  }
+  if (t == 0) {
+    const int pick = k > 1 ? S.sel_rem : 0;
     const int id = (int)~(uint32_t)s_key[pick];
     *out = id;
     P->counter = P->counter + 1ull;
