@@ -370,6 +370,15 @@ LT_API int lt_attn_decode_rows(lt_ctx* ctx, const float* q, int q_stride, const 
                                const int* len, float* out, int batch, int nh, int nkv, int hd, float scale, int maxt,
                                int nsplit, int kv_dtype, void* ws, size_t ws_bytes);
 
+/* lt_attn_decode_rows writing each row's attention vector also (or only: out may be null) as
+ * Q8_0 activation quants, oq [batch][nh*hd] and od [batch][nh*hd/32]: bit-identical to
+ * lt_quant_q8 of the fp32 rows (the batched decode's input to the O projection; hd a multiple
+ * of 32). */
+LT_API int lt_attn_decode_rows_q8(lt_ctx* ctx, const float* q, int q_stride, const void* kc, const void* vc,
+                                  const int* len, float* out, int8_t* oq, uint16_t* od, int batch, int nh, int nkv,
+                                  int hd, float scale, int maxt, int nsplit, int kv_dtype, void* ws,
+                                  size_t ws_bytes);
+
 /* lt_rmsnorm_quant over T rows with row-major output (xq [T][N], xd [T][N/32]): row t is
  * bit-identical to lt_rmsnorm_quant of that row alone. */
 LT_API int lt_rmsnorm_quant_rows(lt_ctx* ctx, const float* x, const float* w, int8_t* xq, uint16_t* xd, int T,

@@ -51,7 +51,7 @@ struct AttnArgs {
   void* vc;
   const int* len;       // STEP: *len = position of the new token; DECODE: len[b]; PREFILL: len[0]
   float* out;           // [rows][nh*hd] (optional for STEP)
-  int8_t* oq;           // AM_STEP: quantized output (optional)
+  int8_t* oq;           // AM_STEP / AM_DECODE: quantized output (optional)
   uint16_t* od;
   float* wsm;           // nsplit > 1: partials
   float* wsz;
@@ -447,12 +447,12 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
     return;   // k_attn_merge combines the partials
   }
   // @phase attn 5
-  if (MODE == AM_STEP && A.oq) {
-    // the workgroup's heads are whole 32-element blocks of the attention vector: quantize
-    // them for the O projection (k_quant_q8's quantizer)
+  if ((MODE == AM_STEP || MODE == AM_DECODE) && A.oq) {
+    // the workgroup's heads are whole 32-element blocks of the row's attention vector:
+    // quantize them for the O projection (k_quant_q8's quantizer)
     __syncthreads();
     const int lane = tid & 31;
-    const size_t o0 = (size_t)h0 * hd;
+    const size_t o0 = hrow0 * hd;
     for (int q = tid >> 5; q < nout / 32; q += 8)
       quant_block_hw(svt[q * 32 + lane], lane, A.oq + o0 + q * 32, A.od + (o0 >> 5) + q);
   }
@@ -1024,15 +1024,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
       for (int k = 0; k < OPL; k++) {
         const float val = valid ? o[r][k] / z : 0.0f;
         if (A.out) A.out[(hrow0 + r) * HD + l * OPL + k] = val;
-        if (kStep) sq[r * HD + l * OPL + k] = val;
+        if (kStep || (MODE == AM_DECODE && A.oq)) sq[r * HD + l * OPL + k] = val;
       }
     }
-    if (kStep && A.oq) {
-      // the workgroup's heads are whole 32-element blocks of the attention vector: quantize
-      // them for the O projection (k_quant_q8's quantizer)
+    if ((kStep || MODE == AM_DECODE) && A.oq) {
+      // the workgroup's heads are whole 32-element blocks of the row's attention vector:
+      // quantize them for the O projection (k_quant_q8's quantizer)
       __syncthreads();
       const int lane = l & 31;
-      const size_t o0 = (size_t)h0 * HD;
+      const size_t o0 = hrow0 * HD;
       for (int qb = l >> 5; qb < HPW * HD / 32; qb += 2)
         quant_block_hw(sq[qb * 32 + lane], lane, A.oq + o0 + qb * 32, A.od + (o0 >> 5) + qb);
     }
@@ -1517,6 +1517,22 @@ int lt_attn_decode_rows(lt_ctx* ctx, const float* q, int q_stride, const void* k
   A.nh = nh; A.nkv = nkv; A.hd = hd; A.scale = scale; A.maxt = maxt; A.nsplit = nsplit;
   return launch_attn(ctx, AM_DECODE, kv_dtype == LT_KV_F16, pick_hpw(nh, nkv, hd, cb / batch), batch, A, ws,
                      ws_bytes, "lt_attn_decode_rows");
+}
+
+int lt_attn_decode_rows_q8(lt_ctx* ctx, const float* q, int q_stride, const void* kc, const void* vc, const int* len,
+                           float* out, int8_t* oq, uint16_t* od, int batch, int nh, int nkv, int hd, float scale,
+                           int maxt, int nsplit, int kv_dtype, void* ws, size_t ws_bytes) {
+  LT_REQUIRE(ctx && q && kc && vc && len && oq && od, "lt_attn_decode_rows_q8: null argument");
+  LT_REQUIRE(batch > 0 && q_stride >= nh * hd, "lt_attn_decode_rows_q8: batch=%d q_stride=%d", batch, q_stride);
+  LT_REQUIRE(hd % 32 == 0, "lt_attn_decode_rows_q8: hd=%d (the quant blocks are 32 elements of one head)", hd);
+  const size_t cb = cache_bytes_of(batch, maxt, nkv, hd, kv_dtype);
+  if (int rc = check_common(nh, nkv, hd, maxt, nsplit, kv_dtype, kc, vc, cb, "lt_attn_decode_rows_q8")) return rc;
+  AttnArgs A = {};
+  A.q = q; A.q_stride = q_stride; A.kc = (void*)kc; A.vc = (void*)vc; A.len = len; A.out = out;
+  A.oq = oq; A.od = od;
+  A.nh = nh; A.nkv = nkv; A.hd = hd; A.scale = scale; A.maxt = maxt; A.nsplit = nsplit;
+  return launch_attn(ctx, AM_DECODE, kv_dtype == LT_KV_F16, pick_hpw(nh, nkv, hd, cb / batch), batch, A, ws,
+                     ws_bytes, "lt_attn_decode_rows_q8");
 }
 
 int lt_attn_decode_noalloc(lt_ctx* ctx, const float* q, const void* kc, const void* vc, const int* len,

@@ -1,8 +1,8 @@
 // lt_multi.hip -- the Q8_0 GEMV over several tokens at once, for the batched decode step at
-// small batch: each weight block is read once and folded against every token's quantized
-// activation, so a step of B tokens streams each weight matrix once per 8 tokens (the prefill
-// GEMM streams it once too, but it is tuned for hundreds of tokens and takes 5x the
-// single-token time at B = 8).
+// small batch: each weight block a workgroup loads is folded against every one of its tokens'
+// quantized activations (2 to 8 tokens per workgroup, so a step of B tokens reads each weight
+// matrix from HBM once and from L2 a few times; the prefill GEMM streams it once too, but it
+// is tuned for hundreds of tokens and takes 5x the single-token time at B = 8).
 //
 // Per (row, token) the arithmetic is the single-token GEMV's, bit for bit: lane L of the
 // row's half-wave folds blocks L, L+32, ... with acc = fma(wd*xd, (float)isum, acc) (exact
@@ -15,6 +15,8 @@
 // (coalesced 16-byte loads, all in flight), and every half-wave streams its row's blocks --
 // each re-aligned to dwords once (load_q8_block) -- against all of them (fold_block, the same
 // fma as fold_raw).
+#include <cstdlib>
+
 #include "lt_internal.h"
 #include "lt_q8_device.h"
 
@@ -116,10 +118,18 @@ __global__ __launch_bounds__(kMtThreads) void k_gemv_multi(const uint8_t* __rest
   }
 }
 
-// tokens per workgroup: the most (up to 8, a power of two) whose staged quants fit the LDS budget
-int mt_tokens(int K, int T) {
+// Tokens per workgroup (a power of two; fewer tokens = more workgroups, each re-reading its rows
+// from L2): 4, or 2 for matrices of at most 2048 rows at up to 8 tokens (down 896 x 4864 at
+// T = 8: 6.5 us with 2, 7.9 with 4, 11.2 with 8; gate|up 9728 x 896 within 5% across 4 and 8);
+// never more than T needs, and within the LDS budget.  LT_MULTI_NT=n sets it, for sweeps.
+int mt_tokens(int K, int T, int N) {
+  static const int env = [] {
+    const char* s = getenv("LT_MULTI_NT");
+    const int v = s ? atoi(s) : 0;
+    return v == 1 || v == 2 || v == 4 || v == 8 ? v : 0;
+  }();
   const size_t per = (size_t)K + (size_t)(K / 32) * 2;
-  int nt = 8;
+  int nt = env ? env : (T <= 8 && N <= 2048 ? 2 : 4);
   while (nt > 1 && ((size_t)nt * per > kMtLdsMax || nt / 2 >= T)) nt /= 2;
   return (size_t)nt * per > kMtLdsMax ? 0 : nt;
 }
@@ -148,7 +158,7 @@ int lt_q8_gemv_multi(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_
   LT_REQUIRE(epi != MT_RESID || add, "lt_q8_gemv_multi: the residual epilogue needs add");
   LT_REQUIRE(epi != MT_SILU || N % 2 == 0, "lt_q8_gemv_multi: SiLU rows come in gate/up pairs (N=%d)", N);
   LT_REQUIRE(lt_aligned(W, 4) && lt_aligned(xq, 16), "lt_q8_gemv_multi: W 4-byte and xq 16-byte aligned");
-  const int nt = mt_tokens(K, T);
+  const int nt = mt_tokens(K, T, N);
   LT_REQUIRE(nt > 0, "lt_q8_gemv_multi: K=%d: one token's quants exceed the LDS budget", K);
   const size_t shm = (size_t)nt * ((size_t)K + (size_t)(K / 32) * 2);
   const dim3 grid((N + kMtRows - 1) / kMtRows, (T + nt - 1) / nt);

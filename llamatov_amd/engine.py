@@ -1389,8 +1389,9 @@ class BatchDecodePlan:
              self.hist_cap)
 
     def _enqueue_step_gemv(self) -> None:
-        """The step with the multi-token GEMV: 10 launches per layer, each weight matrix
-        streamed once per 8 sequences from its GGUF-layout blocks."""
+        """The step with the multi-token GEMV: 9 launches per layer (the attention writes the O
+        projection's activation quants itself), each weight matrix streamed from its GGUF-layout
+        blocks once per group of 2 to 8 sequences."""
         cfg, m, p, B = self.cfg, self.model, self.profile, self.B
         h = self.dev.handle
         E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
@@ -1407,9 +1408,8 @@ class BatchDecodePlan:
                  LT_MULTI_STORE)
             call("lt_rope_append_seqs", h, self.qkv.vp, B, NQ, pos, nh, nkv, hd, m.freqs.vp, kp, vp, self.max_ctx,
                  p.kv_dtype)
-            call("lt_attn_decode_rows", h, self.qkv.vp, NQ, kp, vp, attn, self.att.vp, B, nh, nkv, hd,
+            call("lt_attn_decode_rows_q8", h, self.qkv.vp, NQ, kp, vp, attn, None, xq, xd, B, nh, nkv, hd,
                  ctypes.c_float(self.scale), self.max_ctx, p.attn_nsplit, p.kv_dtype, ws, ws_n)
-            call("lt_quant_q8", h, self.att.vp, xq, xd, B * QD)
             call("lt_q8_gemv_multi", h, L["wo"].t.vp, xq, xd, B, self.x.vp, self.xres.vp, E, QD, LT_MULTI_RESID)
             call("lt_rmsnorm_quant_rows", h, self.xres.vp, L["ffn_norm"].vp, xq, xd, B, E, eps)
             call("lt_q8_gemv_multi", h, L["wgu_il"].t.vp, xq, xd, B, None, self.vbuf.vp, 2 * F, E, LT_MULTI_SILU)

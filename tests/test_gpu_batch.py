@@ -148,3 +148,42 @@ def test_argmax_rows_tie_rule(gpu):
     call("lt_argmax_rows", gpu.handle, d.vp, R, V, out.vp, None, None, 0)
     exp = [int(np.argmax(r)) for r in x]
     assert list(out.to_host()) == exp
+
+
+@pytest.mark.parametrize("nh,nkv,hd", [(14, 2, 64), (32, 8, 128), (8, 2, 32)])
+@pytest.mark.parametrize("kv_dtype,nsplit", [(LT_KV_F16, 1), (LT_KV_F32, 1), (LT_KV_F16, 4)])
+def test_attn_rows_q8_equals_attn_then_quant(gpu, nh, nkv, hd, kv_dtype, nsplit):
+    """lt_attn_decode_rows_q8 (the attention writing the O projection's activation quants):
+    bit-identical to lt_attn_decode_rows followed by lt_quant_q8 over the rows, with and
+    without the fp32 rows, over ragged lengths (hd 32 runs the 256-thread kernel)."""
+    from llamatov_amd import _lib
+    import ctypes
+    case(f"attn rows q8 nh={nh} nkv={nkv} hd={hd} kv={kv_dtype} nsplit={nsplit}")
+    rng = np.random.default_rng(nh * hd + nsplit)
+    B, maxt = 5, 96
+    qs = nh * hd + 2 * nkv * hd   # q|k|v rows
+    q = rng.standard_normal((B, qs)).astype(np.float32)
+    dt = np.float16 if kv_dtype == LT_KV_F16 else np.float32
+    kc = rng.standard_normal((B, maxt, nkv * hd)).astype(dt)
+    vc = rng.standard_normal((B, maxt, nkv * hd)).astype(dt)
+    lens = np.array([1, 17, 96, 40, 63], np.int32)
+    dq, dk, dv, dl = (dr.DevTensor.from_host(a, gpu) for a in (q, kc, vc, lens))
+    ws_n = max(_lib.raw("lt_attn_workspace_size")(B, nh, hd, nsplit), 16)
+    ws = dr.DevTensor.empty((ws_n,), np.uint8, gpu)
+    QD = nh * hd
+    ref = dr.DevTensor.empty((B * QD,), np.float32, gpu)
+    common = (B, nh, nkv, hd, ctypes.c_float(hd ** -0.5), maxt, nsplit, kv_dtype, ws.vp, ws_n)
+    call("lt_attn_decode_rows", gpu.handle, dq.vp, qs, dk.vp, dv.vp, dl.vp, ref.vp, *common)
+    rq = dr.DevTensor.empty((B * QD,), np.int8, gpu)
+    rd = dr.DevTensor.empty((B * QD // 32,), np.uint16, gpu)
+    call("lt_quant_q8", gpu.handle, ref.vp, rq.vp, rd.vp, B * QD)
+    for with_out in (False, True):
+        out = dr.DevTensor.empty((B * QD,), np.float32, gpu) if with_out else None
+        oq = dr.DevTensor.empty((B * QD,), np.int8, gpu)
+        od = dr.DevTensor.empty((B * QD // 32,), np.uint16, gpu)
+        call("lt_attn_decode_rows_q8", gpu.handle, dq.vp, qs, dk.vp, dv.vp, dl.vp, out.vp if out else None, oq.vp,
+             od.vp, *common)
+        assert np.array_equal(oq.to_host(), rq.to_host())
+        assert np.array_equal(od.to_host(), rd.to_host())
+        if out is not None:
+            assert bitexact(out.to_host(), ref.to_host())
