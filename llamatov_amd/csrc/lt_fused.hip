@@ -1027,7 +1027,8 @@ template <int KS, Pro PRO, Epi EPI, int D>
 hipError_t launch_gemv_k(GemvParams P, size_t shm, hipStream_t st, int num_cus, int* grid_out) {
   auto kern = k_gemv_fused<KS, PRO, EPI, D>;
   const int groups = (P.N + 7) / 8;
-  const bool one_item = (P.K / 32 + 31) / 32 == 1;
+  const int nk = (P.K / 32 + 31) / 32;   // items (32-block groups) per row
+  const bool one_item = nk == 1;
   int grid;
   bool stg = false;   // the 64-row mapping with one item per row: staged streaming
   if (EPI == EPI_SILU) {
@@ -1043,7 +1044,16 @@ hipError_t launch_gemv_k(GemvParams P, size_t shm, hipStream_t st, int num_cus, 
     grid = (P.N + R - 1) / R;
   } else {
     const int cap = resident_wgs(kern, shm, num_cus);
-    if (groups <= cap) {
+    if (P.N >= 4096 && nk >= 2 && nk <= 4 && (P.N <= 8192 || groups > cap)) {
+      // 2 to 4 items per row (K = 2048 .. 4096), 4096 to 8192 rows or more rows than one
+      // resident round of 8-row workgroups: 16 rows per workgroup, 2 per half-wave (8 items:
+      // the ring full).  Measured against 8 rows per workgroup (or the region walk past the
+      // resident cap): 4096 x 4096 7.19 -> 6.38 us, the same with the RMS prologue 8.80 ->
+      // 7.31, 6144 x 4096 10.86 -> 9.70, 128256 x 4096 96.6 -> 92.1; 14336 x 4096 (one
+      // resident round) stays on 8 rows (13.54 against 13.78)
+      P.row0 = 16; P.step = 8; P.max_rows = 2;
+      grid = (P.N + 15) / 16;
+    } else if (groups <= cap) {
       P.row0 = 8; P.step = 8; P.max_rows = 1;
       grid = groups;
     } else if (one_item) {
