@@ -290,7 +290,8 @@ def attention_sweep(dev, reps: int = 20) -> list[dict]:
     """GQA decode attention, 32 Q / 8 KV heads, head_dim 128, fp16 KV
     N(0,1), one query token per sequence, L in {4k, 16k, 32k}, batch 1 and 8 (split-K over
     context with the ascending-split merge).  Algorithmic bytes: the K and V rows read plus
-    q and out."""
+    q and out.  Per shape: 3 untimed calls, then the median of 5 timed runs of `reps` calls
+    (HIP events on the library's stream)."""
     from llamatov_amd import engine as dr
     from llamatov_amd._lib import LT_KV_F16, call, raw
     out = []
@@ -310,14 +311,18 @@ def attention_sweep(dev, reps: int = 20) -> list[dict]:
             ws = dr.DevTensor.empty((max(wsn, 16),), np.uint8, dev)
             args = (dev.handle, q.vp, kc.vp, vc.vp, lens.vp, o.vp, B, nh, nkv, hd, ctypes.c_float(hd ** -0.5), L,
                     nsplit, LT_KV_F16, ws.vp, ws.nbytes)
-            call("lt_attn_decode", *args)
-            dev.sync()
-            ev = Events(dev)
-            ev.start()
-            for _ in range(reps):
+            for _ in range(3):
                 call("lt_attn_decode", *args)
-            ms = ev.stop_ms() / reps
-            ev.free()
+            dev.sync()
+            runs = []
+            for _ in range(5):   # the median of 5 timed runs of `reps` calls
+                ev = Events(dev)
+                ev.start()
+                for _ in range(reps):
+                    call("lt_attn_decode", *args)
+                runs.append(ev.stop_ms() / reps)
+                ev.free()
+            ms = sorted(runs)[2]
             alg = B * 2 * L * nkv * hd * 2 + 2 * B * nh * hd * 4
             out.append({"L": L, "batch": B, "nsplit": nsplit, "us": round(ms * 1e3, 2),
                         "GB/s": round(alg / (ms * 1e-3) / 1e9, 1), "frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})

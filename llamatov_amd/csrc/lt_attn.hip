@@ -1056,6 +1056,210 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   }
 }
 
+// Batched decode (AM_DECODE) with one wave per query head of a KV group: a workgroup of NW
+// waves takes one split of one KV group (all its NW query heads) of one sequence.  Each K round
+// (64 positions) is loaded once by the whole workgroup into padded LDS rows; wave w scores its
+// head against it (lane = position), then runs its head's softmax and O chains exactly as
+// k_attn_w1 with one head per wave does -- the same per-head arithmetic (scores as fma chains
+// over the dims in ascending order times scale; max order-free; exps by lt_expf_sel; Z the
+// 64-lane strided fold plus tree; O per dim a chain over positions in ascending order), so
+// bit-identical to it, with the group's heads on NW waves instead of one wave's serial chains.
+// V is staged the same way, in chunks of 32 rows through a double-buffered LDS area, so each
+// cache row is read from HBM once per workgroup.
+
+template <bool kF16, int NW, int DPL>
+__global__ __launch_bounds__(64 * NW) void k_attn_dec(AttnArgs A) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  constexpr int HD = 64 * DPL;
+  constexpr int kEb = kF16 ? 2 : 4;
+  constexpr int KU = HD * kEb / 16;                 // 16-byte units per K row
+  constexpr int kPR = 64;                           // positions per K round
+  constexpr int kNT = 64 * NW;
+  constexpr int kLPT = (kPR * KU + kNT - 1) / kNT;  // K loads per thread per round
+  static_assert(KU >= 8 && KU <= 32, "k_attn_dec: unsupported head size / cache type");
+  const int per_up = (A.per_max + 63) / 64 * 64;
+  const int SE = per_up + 64;                       // a head's exps row (the spare past the end)
+  float* sq = lds;                                  // [NW][HD]
+  u32x4* sk = (u32x4*)(sq + NW * HD);               // [kPR][KU + 1]
+  float* se = (float*)(sk + kPR * (KU + 1));        // [NW][SE]
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  const int sp = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const int h = g * NW + w;                         // this wave's query head (NW = nh / nkv)
+  const int kvrow = A.nkv * HD;
+  const int len0 = A.len[b];
+  const int nctx = len0 < 0 ? 0 : (len0 > A.maxt ? A.maxt : len0);
+  const int per = (nctx + A.nsplit - 1) / A.nsplit;
+  const int p0 = sp * per;
+  const int p1 = p0 + per < nctx ? p0 + per : nctx;
+  const int n = p1 > p0 ? p1 - p0 : 0;
+  const uint32_t pitch = (uint32_t)kvrow * kEb;
+  const uint32_t base = ((uint32_t)b * (uint32_t)A.maxt + (uint32_t)p0) * pitch + (uint32_t)g * HD * kEb;
+  // rows past the split's end read zeros (the resources end after its n rows)
+  const __amdgpu_buffer_rsrc_t krsrc =
+      __builtin_amdgcn_make_buffer_rsrc(A.kc, 0, (int)(base + (uint32_t)n * pitch), 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrsrc =
+      __builtin_amdgcn_make_buffer_rsrc(A.vc, 0, (int)(base + (uint32_t)n * pitch), 0x00020000);
+  constexpr int kKvPolicy = 2;                      // every cache row is read once per workgroup
+
+  // K round loads: unit i = tid + kNT*j of the round is row i / KU, unit i % KU
+  auto load_round = [&](int t0, u32x4* dst) {
+#pragma unroll
+    for (int j = 0; j < kLPT; j++) {
+      const int i = tid + kNT * j;
+      const int r = i / KU, u = i - r * KU;
+      const uint32_t off = kPR * KU % kNT == 0 || i < kPR * KU ? base + (uint32_t)(t0 + r) * pitch + (uint32_t)u * 16u : kNoRow;
+      dst[j] = __builtin_amdgcn_raw_buffer_load_b128(krsrc, (int)off, 0, kKvPolicy);
+    }
+  };
+  float qv[DPL];
+  {
+    const float* qrow = A.q + (size_t)b * A.q_stride + (size_t)h * HD;
+#pragma unroll
+    for (int k = 0; k < DPL; k++) qv[k] = qrow[l + 64 * k];
+  }
+  u32x4 kb[kLPT];
+  load_round(0, kb);
+  // V in chunks of kVC rows, loaded once by the whole workgroup (16-byte units, coalesced)
+  // into a double-buffered LDS area, two chunks in flight: chunks 0 and 1 are requested after
+  // the last K round (requested with the first one they slow the K rounds down: 32k at batch
+  // 1 33 us against 30), chunk c + 2 while chunk c is folded.  The loop body is straight-line
+  // (no per-chunk tests), which lets the compiler wait for chunk c alone, not c + 1 too.
+  constexpr int kVC = 32;                           // rows per chunk
+  constexpr int kVU = kVC * KU;                     // 16-byte units per chunk
+  constexpr int kVLT = (kVU + kNT - 1) / kNT;       // V loads per thread per chunk
+  u32x4* sv = (u32x4*)(se + NW * SE);               // [2][kVC][KU] raw cache rows
+  auto load_chunk = [&](int c, u32x4* dst) {
+#pragma unroll
+    for (int j = 0; j < kVLT; j++) {
+      const int i = tid + kNT * j;
+      const int r = i / KU, u = i - r * KU;
+      const uint32_t off = kVU % kNT == 0 || i < kVU ? base + (uint32_t)(c * kVC + r) * pitch + (uint32_t)u * 16u : kNoRow;
+      dst[j] = __builtin_amdgcn_raw_buffer_load_b128(vrsrc, (int)off, 0, kKvPolicy);
+    }
+  };
+  // chunks come in pairs (a last odd chunk gets a zero partner: its rows are past the split's
+  // end, so its loads read zeros without touching memory, and their exps are 0)
+  const int nch = ((n + kVC - 1) / kVC + 1) & ~1;
+  u32x4 vb0[kVLT], vb1[kVLT];
+  // this wave's query row (requested before the cache rows, so storing it waits for it alone)
+#pragma unroll
+  for (int k = 0; k < DPL; k++) sq[w * HD + l + 64 * k] = qv[k];
+  const int srow = SE - 1;                          // spare slot for positions past n
+  for (int t0 = 0; t0 < n; t0 += kPR) {
+#pragma unroll
+    for (int j = 0; j < kLPT; j++) {
+      const int i = tid + kNT * j;
+      if (kPR * KU % kNT == 0 || i < kPR * KU) sk[(i / KU) * (KU + 1) + (i % KU)] = kb[j];
+    }
+    __syncthreads();
+    if (t0 + kPR < n) load_round(t0 + kPR, kb);
+    constexpr int kQu = kF16 ? 8 : 4;               // q values per K unit
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < KU; u++) {
+      const u32x4 kc = sk[l * (KU + 1) + u];
+      const uint32_t a4[4] = {kc.x, kc.y, kc.z, kc.w};
+      const float* qu = sq + w * HD + u * kQu;
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        if (kF16) {
+          acc = fmaf(qu[2 * c], lt_h2f((uint16_t)(a4[c] & 0xFFFFu)), acc);
+          acc = fmaf(qu[2 * c + 1], lt_h2f((uint16_t)(a4[c] >> 16)), acc);
+        } else {
+          acc = fmaf(qu[c], __uint_as_float(a4[c]), acc);
+        }
+      }
+    }
+    const int t = t0 + l;
+    se[w * SE + (t < n ? t : srow)] = acc * A.scale;
+    __syncthreads();                                // the next round rewrites sk
+  }
+
+  load_chunk(0, vb0);
+  load_chunk(1, vb1);
+  // softmax of this wave's head (under the first V chunks' loads)
+  float* e = se + w * SE;
+  float m = -1e30f;
+  for (int t = l; t < n; t += 64) m = fmaxf(m, e[t]);
+  m = wave_max(m);
+  float zs = 0.0f;
+  for (int t = l; t < n; t += 64) {
+    const float x = lt_expf_sel(e[t] - m);
+    e[t] = x;
+    zs = zs + x;
+  }
+  zs = wave_tree_dpp(zs);                           // lane 0: Z
+  const int n_up = nch * kVC;
+  for (int t = n + l; t < n_up; t += 64) e[t] = 0.0f;   // past n: exps of 0 (rows read zeros)
+
+  // O: lane l owns dims [l*DPL, l*DPL + DPL) of the head; rows in ascending order (o is never
+  // -0, so the zero rows past n leave it unchanged)
+  float o[DPL];
+#pragma unroll
+  for (int k = 0; k < DPL; k++) o[k] = 0.0f;
+  auto fold_chunk = [&](int c, u32x4 (&vb)[kVLT]) {
+    u32x4* buf = sv + (c & 1) * kVU;
+#pragma unroll
+    for (int j = 0; j < kVLT; j++) {
+      const int i = tid + kNT * j;
+      if (kVU % kNT == 0 || i < kVU) buf[i] = vb[j];
+    }
+    __syncthreads();                                // chunk c in LDS (and every wave's exps)
+    load_chunk(c + 2, vb);                          // past the split: zeros, no traffic
+    const uint8_t* rows = (const uint8_t*)buf;
+#pragma unroll 8
+    for (int r = 0; r < kVC; r++) {
+      const float ek = e[c * kVC + r];
+      const uint8_t* row = rows + r * KU * 16;
+      if (kF16) {
+        if (DPL == 1) {
+          const uint32_t x = ((const uint32_t*)row)[l >> 1];
+          o[0] = fmaf(ek, lt_h2f((uint16_t)((l & 1) ? (x >> 16) : (x & 0xFFFFu))), o[0]);
+        } else {
+          const uint32_t x = ((const uint32_t*)row)[l];
+          o[0] = fmaf(ek, lt_h2f((uint16_t)(x & 0xFFFFu)), o[0]);
+          o[1] = fmaf(ek, lt_h2f((uint16_t)(x >> 16)), o[1]);
+        }
+      } else {
+#pragma unroll
+        for (int d = 0; d < DPL; d++) o[d] = fmaf(ek, ((const float*)row)[l * DPL + d], o[d]);
+      }
+    }
+  };
+  for (int c = 0; c < nch; c += 2) {
+    fold_chunk(c, vb0);
+    fold_chunk(c + 1, vb1);
+  }
+
+  const size_t hrow = (size_t)b * A.nh + h;
+  if (A.nsplit == 1) {
+    const float z = __shfl(zs, 0, 64);
+#pragma unroll
+    for (int k = 0; k < DPL; k++) {
+      const float val = o[k] / z;
+      if (A.out) A.out[hrow * HD + l * DPL + k] = val;
+      sq[w * HD + l * DPL + k] = val;
+    }
+    if (A.oq) {
+      // the head's HD values are whole 32-element blocks of the row's attention vector
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int lane = l & 31;
+      const size_t o0 = hrow * HD;
+      for (int qb = l >> 5; qb < HD / 32; qb += 2)
+        quant_block_hw(sq[w * HD + qb * 32 + lane], lane, A.oq + o0 + qb * 32, A.od + (o0 >> 5) + qb);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < DPL; k++) A.wso[(hrow * A.nsplit + sp) * HD + l * DPL + k] = o[k];
+    if (l == 0) {
+      A.wsm[hrow * A.nsplit + sp] = m;
+      A.wsz[hrow * A.nsplit + sp] = zs;
+    }
+  }
+}
+
 // Split-K merge, one workgroup per (query head, row): the declared combine in ascending
 // split order (attn_decode_split.cu:37-91): M = max m_s, w_s = exp(m_s - M),
 // Z = sum fma(w_s, Z_s), O_d = sum fma(w_s, O_s,d), out = O/Z; optionally the quant of
@@ -1381,6 +1585,44 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
     A.wsm = w.m;
     A.wsz = w.z;
     A.wso = w.o;
+  }
+  // decode with 2, 4 or 8 query heads per KV group on a grid of at most 4 workgroups per CU
+  // (batch 1): one wave per head, K and V staged once per workgroup through LDS.  On larger
+  // grids its LDS footprint (3 workgroups per CU at 16k) loses to the single-wave kernel's
+  // occupancy (batch 8 at 16k: 105 us against 92).  LT_ATTN_DEC=0 keeps the single-wave
+  // kernel, LT_ATTN_DEC=2 takes this one at any grid size, for comparisons.
+  static const int dec_env = [] {
+    const char* s = getenv("LT_ATTN_DEC");
+    return s ? atoi(s) : 1;
+  }();
+  const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+  const bool dec_on = dec_env == 2 || (dec_env == 1 && (size_t)A.nsplit * A.nkv * rows <= (size_t)4 * cus);
+  if (dec_on && mode == AM_DECODE && (rep == 2 || rep == 4 || rep == 8) && A.hd % 64 == 0 && (dpl == 1 || dpl == 2)) {
+    const size_t per_up = (size_t)(per_max + 63) / 64 * 64;
+    const size_t dec_shm = ((size_t)rep * A.hd + 64 * (ku + 1) * 4 + (size_t)rep * (per_up + 64)) * sizeof(float) +
+                           2 * 32 * ku * 16;
+    if (dec_shm <= 64 * 1024) {
+      A.per_max = per_max;
+      const dim3 grid(A.nsplit, A.nkv, rows);
+      hipError_t e = hipErrorInvalidValue;
+#define LT_DEC_CASE(F, NW, D)                                                          \
+  if (f16 == F && rep == NW && dpl == D) {                                             \
+    k_attn_dec<F, NW, D><<<grid, 64 * NW, dec_shm, ctx->stream>>>(A);                  \
+    e = hipGetLastError();                                                             \
+  }
+      LT_DEC_CASE(true, 2, 1) LT_DEC_CASE(true, 4, 1) LT_DEC_CASE(true, 8, 1)
+      LT_DEC_CASE(true, 2, 2) LT_DEC_CASE(true, 4, 2) LT_DEC_CASE(true, 8, 2)
+      LT_DEC_CASE(false, 2, 1) LT_DEC_CASE(false, 4, 1) LT_DEC_CASE(false, 8, 1)
+      LT_DEC_CASE(false, 2, 2) LT_DEC_CASE(false, 4, 2) LT_DEC_CASE(false, 8, 2)
+#undef LT_DEC_CASE
+      if (e != hipSuccess) return lt_fail_hip(e, what, __FILE__, __LINE__);
+      if (A.nsplit > 1) {
+        launch_merge(dim3(A.nh, rows), ctx->stream, A.wsm, A.wsz, A.wso, nullptr, A.maxt, A.out, A.oq, A.od, A.nh,
+                     A.hd, A.nsplit);
+        return lt_check_launch("k_attn_merge");
+      }
+      return lt_check_launch("k_attn_dec");
+    }
   }
   if (w1) {
     A.per_max = per_max;
