@@ -306,7 +306,7 @@ def attention_sweep(dev, reps: int = 20) -> list[dict]:
             q = dr.DevTensor.from_host(rng.standard_normal(B * nh * hd).astype(np.float32), dev)
             lens = dr.DevTensor.from_host(np.full(B, L, np.int32), dev)
             o = dr.DevTensor.empty((B * nh * hd,), np.float32, dev)
-            nsplit = dr.attn_nsplit_for(B, L, nkv)   # 8 workgroups per CU, 64 .. 512 rows per split
+            nsplit = dr.attn_nsplit_for(B, L, nkv)   # CU-filling, 64 .. 512 rows per split
             wsn = raw("lt_attn_workspace_size")(B, nh, hd, nsplit)
             ws = dr.DevTensor.empty((max(wsn, 16),), np.uint8, dev)
             args = (dev.handle, q.vp, kc.vp, vc.vp, lens.vp, o.vp, B, nh, nkv, hd, ctypes.c_float(hd ** -0.5), L,

@@ -448,12 +448,17 @@ _CERTIFIED_NSPLIT = {1, 2, 4, 8, 16, 32, 64, 128}
 
 def attn_nsplit_for(batch: int, length: int, n_kv_heads: int, num_cus: int = 256) -> int:
     """A split count for decode attention over `length` cached positions (the reference fixes
-    it per capture, ir_param_axes.pl:303-341): enough workgroups for 8 per CU (one per split,
-    KV group and sequence), at most 512 and at least 64 positions per split, a power of two in
-    1 .. 128.  Measured at C4 (32 q / 8 KV heads, hd 128, fp16): batch 1 picks 64 / 128 / 128
-    splits at 4k / 16k / 32k (15% / 32% / 46% of 8 TB/s; L/256 splits gave 8% / 29% / 46%),
-    batch 8 picks 32 / 32 / 64 (61% / 63% / 61%)."""
-    want = max((8 * num_cus + batch * n_kv_heads - 1) // (batch * n_kv_heads), (length + 511) // 512)
+    it per capture, ir_param_axes.pl:303-341): a power of two in 1 .. 128 with at least 64
+    and at most 512 positions per split, and enough workgroups to fill the CUs --
+      batch 1: two per CU of the small-grid kernel, whose workgroups hold one wave per query
+        head of a KV group (4 waves at C4);
+      batch > 1: eight single-wave workgroups per CU (one per split, KV group and sequence).
+    Measured at C4 (32 q / 8 KV heads, hd 128, fp16; attention + merge, median of 5 runs):
+    batch 1 at 4k / 16k / 32k takes 9.6-9.7 / 18.4-18.9 / 29.8-30.3 us at 64 splits against
+    9.9-10.3 / 23.6-24.2 / 43.8 at 32 and 13.1 / 19.5-20.1 / 30.7-31.7 at 128;
+    batch 8 picks 32 / 32 / 64 (61% / 63% / 61% of 8 TB/s)."""
+    per_cu = 2 if batch == 1 else 8
+    want = max((per_cu * num_cus + batch * n_kv_heads - 1) // (batch * n_kv_heads), (length + 511) // 512)
     cap = min(128, max(1, length // 64))
     n = 1
     while n * 2 <= cap and n < want:

@@ -269,7 +269,8 @@ def test_attention_prefill(gpu, oracle, kv_dtype, nh, nkv, hd, len0, T, nsplit):
 @pytest.mark.parametrize("B,L,nsplit", [(1, 4096, 32), (8, 4096, 32), (1, 16384, 64), (2, 32768, 128),
                                          (8, 16384, 64), (8, 32768, 128),
                                          # the split counts engine.attn_nsplit_for picks at C4
-                                         (1, 4096, 64), (1, 16384, 128), (1, 32768, 128), (8, 16384, 32),
+                                         (1, 4096, 64), (1, 16384, 128), (1, 32768, 128), (1, 32768, 64),
+                                         (8, 16384, 32),
                                          (8, 32768, 64)])
 def test_attention_long_context_batched(gpu, oracle, B, L, nsplit):
     """BASELINE config 4 geometry: 32 Q heads, 8 KV heads, hd 128, fp16 KV."""
@@ -290,6 +291,31 @@ def test_attention_long_context_batched(gpu, oracle, B, L, nsplit):
         exp = oracle.attn_decode(q[b], k[b], v[b], lens[b], nh, nkv, hd, scale, True, nsplit)
         assert_bitexact(got[b], exp, f"attn b={b}")
 
+
+
+@pytest.mark.parametrize("kv_dtype,hd", [(LT_KV_F16, 128), (LT_KV_F16, 64), (LT_KV_F32, 128), (LT_KV_F32, 64)])
+@pytest.mark.parametrize("nh,nkv", [(32, 8), (16, 8), (16, 2)])
+def test_attention_decode_one_round_splits(gpu, oracle, kv_dtype, hd, nh, nkv):
+    """Small-grid batched decode whose splits hold at most one 64-row K round (maxt / nsplit
+    <= 64), where V is requested together with K: NaN past each length, lengths that end
+    inside, at and one past a round, ragged and empty splits."""
+    f16 = kv_dtype == LT_KV_F16
+    rng = np.random.default_rng(7 * hd + nh)
+    maxt, B = 256, 3
+    for nsplit, lens in ((4, [256, 255, 1]), (4, [64, 65, 63]), (8, [200, 3, 129]), (16, [17, 256, 100])):
+        case(f"attn one-round hd={hd} nh={nh} nkv={nkv} f16={f16} nsplit={nsplit} lens={lens}")
+        q = rng.standard_normal((B, nh * hd)).astype(np.float32)
+        k, v = _attn_setup(rng, B, maxt, nkv, hd, kv_dtype, lens, np.nan)
+        ws_n = _lib.raw("lt_attn_workspace_size")(B, nh, hd, nsplit)
+        ws = empty((max(ws_n, 1),), np.uint8)
+        out = empty((B, nh * hd), np.float32)
+        scale = float(hd ** -0.5)
+        call("lt_attn_decode", gpu.handle, up(q).vp, up(k).vp, up(v).vp, up(np.array(lens, np.int32)).vp,
+             out.vp, B, nh, nkv, hd, ctypes.c_float(scale), maxt, nsplit, kv_dtype, ws.vp, ws.nbytes)
+        got = out.to_host()
+        for b in range(B):
+            exp = oracle.attn_decode(q[b], k[b], v[b], lens[b], nh, nkv, hd, scale, f16, nsplit)
+            assert_bitexact(got[b], exp, f"attn b={b} L={lens[b]}")
 
 def test_argmax_ties(gpu, oracle):
     case("argmax V=151936")

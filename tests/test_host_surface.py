@@ -85,7 +85,7 @@ def test_attn_nsplit_rule():
             n = E.attn_nsplit_for(B, L, 8)
             assert n in certified
             assert n == 1 or L // n >= 64                      # at least 64 rows per split
-    assert [E.attn_nsplit_for(1, L, 8) for L in (4096, 16384, 32768)] == [64, 128, 128]
+    assert [E.attn_nsplit_for(1, L, 8) for L in (4096, 16384, 32768)] == [64, 64, 64]
     assert [E.attn_nsplit_for(8, L, 8) for L in (4096, 16384, 32768)] == [32, 32, 64]
 
 
