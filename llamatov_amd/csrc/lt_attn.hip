@@ -513,8 +513,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   // through 1 KB of LDS to the lanes' dims -- 8x fewer load instructions than a row per
   // load, so a whole short context is in flight at once.
   constexpr bool kChunk = kStep && kF16 && DPL == 1;
+  // kK2 (the chunked step): K rounds are requested two ahead (round r + 2 while round r is
+  // scored, rounds 0 and 1 at the start), so a context of two or three rounds waits for one
+  // round trip instead of one per round; 16 chunks in flight instead of 24 make the room
+  constexpr bool kK2 = kChunk;
   constexpr int kCR = 8;                            // rows per chunk (one exp group)
-  constexpr int kNC = 24;                           // chunks in flight
+  constexpr int kNC = kK2 ? 16 : 24;                // chunks in flight
   static_assert(!kChunk || kCR == kEg, "k_attn_w1: a V chunk is one exp group");
   constexpr int kPR = HPW >= 2 ? 32 : 64;           // positions per score round
   static_assert(KU >= 8 && KU <= 32, "k_attn_w1: unsupported head size / cache type");
@@ -665,6 +669,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     }
   }
   load_round(0, kb);
+  u32x4 kb2[kK2 ? kNI : 1];
+  if constexpr (kK2) load_round(kPR, kb2);          // past n: clamped rows (scores reach the spare row)
   uint32_t fv[VD];                                  // step: this lane's part of the new V row
   if (kStep) {
     // RoPE (the arithmetic of k_rope, rope_from_facts.pl:40-69) of the q heads and the
@@ -732,7 +738,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
       if (tr >= 0 && tr < kPR && l < KU) sk[tr * (KU + 1) + l] = sfk[l];
     }
     asm volatile("" ::: "memory");
-    if constexpr (decltype(prefetch)::value) load_round(t0 + kPR, buf);
+    // prefetch: the round decltype(prefetch)::value rounds ahead into the same registers (0: none)
+    if constexpr (decltype(prefetch)::value > 0) load_round(t0 + decltype(prefetch)::value * kPR, buf);
     // passes of kHg heads over this lane's K row in LDS; within a pass, K unit u and q of
     // unit u (kQu dims per head) are read one unit ahead of their use, and the fence keeps
     // the compiler from hoisting more
@@ -793,8 +800,29 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
   // the last round loads nothing ahead: loads still pending when the O loop reuses their
   // registers would make it wait for them
   int t0s = 0;
-  for (; t0s + kPR < n; t0s += kPR) score_round(t0s, kb, std::true_type{});
-  if (n > 0) score_round(t0s, kb, std::false_type{});
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  using P2 = std::integral_constant<int, 2>;
+  if constexpr (kK2) {
+    // round r in kb (r even) or kb2 (r odd); each refilled with round r + 2 while one exists
+    for (; t0s + 3 * kPR < n; t0s += 2 * kPR) {
+      score_round(t0s, kb, P2{});
+      score_round(t0s + kPR, kb2, P2{});
+    }
+    if (t0s + 2 * kPR < n) {                        // three rounds left
+      score_round(t0s, kb, P2{});
+      score_round(t0s + kPR, kb2, P0{});
+      score_round(t0s + 2 * kPR, kb, P0{});
+    } else if (t0s + kPR < n) {                     // two
+      score_round(t0s, kb, P0{});
+      score_round(t0s + kPR, kb2, P0{});
+    } else if (n > 0) {
+      score_round(t0s, kb, P0{});
+    }
+  } else {
+    for (; t0s + kPR < n; t0s += kPR) score_round(t0s, kb, P1{});
+    if (n > 0) score_round(t0s, kb, P0{});
+  }
   // @phase attn 2
   // batched decode: the first kVRing V rows go out now, under the softmax
   if (!kStep) {

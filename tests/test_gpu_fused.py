@@ -248,9 +248,10 @@ def test_attn_step_then_out(gpu, oracle, kv_dtype, nsplit, geom):
 @pytest.mark.parametrize("nsplit", [1, 3, 16])
 @pytest.mark.parametrize("nh,nkv,hd", [(14, 2, 64), (8, 1, 64), (32, 8, 128), (16, 2, 128)])
 def test_attn_step_long_context(gpu, oracle, nsplit, nh, nkv, hd):
-    """The fp16 step with 64 or 128 dims streams V in 8-row chunks (24 or 12 in flight):
-    lengths around one ring (192 / 96 rows), ragged chunk tails, refills up to the cache's
-    end, splits of a few rows, with poison past the new row."""
+    """The fp16 step with 64 dims streams V in 8-row chunks (16 in flight) and requests its
+    64-position K rounds two ahead; with 128 dims V runs through a ring of rows: lengths around
+    one V ring (128 rows at 64 dims) and around one to four K rounds, ragged chunk tails,
+    refills up to the cache's end, splits of a few rows, with poison past the new row."""
     theta, maxt = 1e6, 1024
     rng = np.random.default_rng(29)
     width = nkv * hd
@@ -260,7 +261,8 @@ def test_attn_step_long_context(gpu, oracle, nsplit, nh, nkv, hd):
     ws_n = _lib.raw("lt_attn_workspace_size")(1, nh, hd, nsplit)
     ws = dr.DevTensor.zeros((max(ws_n, 16),), np.uint8, gpu)
     scale = float(hd ** -0.5)
-    for L in (0, 5, 95, 96, 97, 190, 191, 192, 193, 200, 383, 577, 1023):
+    for L in (0, 5, 63, 64, 65, 95, 96, 97, 127, 128, 129, 190, 191, 192, 193, 200, 255, 256, 257, 383, 577,
+              1023):
         case(f"attn_step long nh={nh} nkv={nkv} nsplit={nsplit} L={L}")
         kc, vc = base_k.copy(), base_v.copy()
         kc[L:] = 0x7E00
