@@ -12,9 +12,12 @@ Printed (one JSON line on stdout): decode tok/s; `step_kernels`, every launch of
 timed live with HIP events on the library's stream (a captured graph of back-to-back
 launches over rotated weight copies >= 600 MB, so the 256 MB Infinity Cache cannot serve
 them), with its algorithmic bytes, HBM rate and share of the step's kernel time;
-`roofline`, the largest-share kernel of that table; and the CPU baseline: the oracle (C
+`roofline`, the largest-share kernel of that table; the CPU baseline: the oracle (C
 restatement of the reference arithmetic, OpenMP over GEMV rows) decoding a bounded sample of
-the same workload and timing the C1 GEMV on the host cores, all cores and one core.
+the same workload and timing the C1 GEMV on the host cores, all cores and one core; and the
+other BASELINE configs as legs of the same line (`gemv_sweep`: C1 and C3; `c4_attention`: C4;
+`c5`: the 8B prefill and decode), selected by --legs (default all three) or by naming legs
+one by one (--gemv-sweep, --c4, --c5: then only those).
 """
 from __future__ import annotations
 
@@ -581,13 +584,17 @@ def main() -> int:
     ap.add_argument("--cpu-tokens-1core", type=int, default=12, help="decode tokens of the 1-core CPU figure")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
-    ap.add_argument("--c4", action="store_true", help="also time BASELINE config 4 attention (adds c4_attention)")
+    ap.add_argument("--legs", default="gemv,c4,c5",
+                    help="the other BASELINE configs to run after C2, from gemv (C1/C3 GEMV sweep), c4 (attention "
+                         "sweep), c5 (8B prefill + decode); empty for none.  Naming a leg by its own flag "
+                         "(--gemv-sweep, --c4, --c5) runs only the legs so named")
+    ap.add_argument("--c4", action="store_true", help="time BASELINE config 4 attention (adds c4_attention)")
     ap.add_argument("--c5", action="store_true",
-                    help="also run BASELINE config 5 (Llama-3-8B arch: 512-token MFMA prefill + 256 decode; adds c5)")
+                    help="run BASELINE config 5 (Llama-3-8B arch: 512-token MFMA prefill + 256 decode; adds c5)")
     ap.add_argument("--c5-decode", type=int, default=256,
                     help="C5 decode tokens (at most 4: prefill only, for counter runs)")
     ap.add_argument("--gemv-sweep", action="store_true",
-                    help="also time the Q8_0 GEMV on the BASELINE config 1/3 shapes (adds gemv_sweep)")
+                    help="time the Q8_0 GEMV on the BASELINE config 1/3 shapes (adds gemv_sweep)")
     ap.add_argument("--per-op", action="store_true",
                     help="thirteen per-op launches per layer (the reference's kernel-per-op chain) "
                          "instead of the five fused launches")
@@ -606,6 +613,11 @@ def main() -> int:
                     help="launch the step's kernels directly instead of replaying the captured graph "
                          "(same kernels; for profilers that cannot trace graph launches)")
     args = ap.parse_args()
+    named = {k for k, on in (("gemv", args.gemv_sweep), ("c4", args.c4), ("c5", args.c5)) if on}
+    legs = named or {x.strip() for x in args.legs.split(",") if x.strip()}
+    bad = legs - {"gemv", "c4", "c5"}
+    if bad:
+        raise SystemExit(f"bench.py: unknown legs {sorted(bad)} (gemv, c4, c5)")
 
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU; --gpus {args.gpus} is not supported "
@@ -734,10 +746,10 @@ def main() -> int:
         result["step_kernels"] = table
         result["roofline"] = roofline_of(max(table, key=lambda e: e["share"]))
 
-    if args.gemv_sweep:
+    if "gemv" in legs:
         log("GEMV sweep")
         result["gemv_sweep"] = gemv_sweep(dev)
-    if args.c4:
+    if "c4" in legs:
         log("C4 attention sweep")
         result["c4_attention"] = attention_sweep(dev)
 
@@ -761,7 +773,7 @@ def main() -> int:
     if batches and not args.per_op:
         log("batched decode leg")
         result["batched_decode"] = batched_leg(dev, model, cfg, kv_dtype, batches, len(prompt), 64, 8)
-    if args.c5:
+    if "c5" in legs:
         model.free()
         log("C5 leg")
         result["c5"] = c5_leg(dev, n_decode=args.c5_decode, eager=args.eager)
