@@ -617,7 +617,8 @@ def main() -> int:
     legs = named or {x.strip() for x in args.legs.split(",") if x.strip()}
     bad = legs - {"gemv", "c4", "c5"}
     if bad:
-        raise SystemExit(f"bench.py: unknown legs {sorted(bad)} (gemv, c4, c5)")
+        print(f"bench.py: unknown legs {sorted(bad)} (gemv, c4, c5)", file=sys.stderr)
+        return 2
 
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU; --gpus {args.gpus} is not supported "
