@@ -938,6 +938,9 @@ __global__ __launch_bounds__(kFinThreads) void k_argmax_finalize(const float* __
                                                                  int* __restrict__ count, int cap) {
   __shared__ float sv[kFinThreads / 64];
   __shared__ int si[kFinThreads / 64];
+  // the history count is requested first (only this launch writes it), so the final write
+  // does not wait for a load issued after the reduction
+  const int c0 = hist ? *count : 0;
   float bv = -__builtin_inff();
   int bi = 0x7FFFFFFF;
   for (int base = 0; base < G; base += kFinThreads * kFinPer) {
@@ -967,7 +970,7 @@ __global__ __launch_bounds__(kFinThreads) void k_argmax_finalize(const float* __
       if (am_better(sv[k], si[k], bv, bi)) { bv = sv[k]; bi = si[k]; }
     *out = bi;
     if (hist) {
-      const int c = *count;
+      const int c = c0;
       if (c >= 0 && c < cap) {
         hist[c] = bi;
         *count = c + 1;
