@@ -251,6 +251,45 @@ LT_API int lt_q8_gemv_attn_o(lt_ctx* ctx, const float* qkv, const void* kc, cons
 LT_API int lt_q8_gemv_rms_silu_len(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* Wgu,
                                    int8_t* vq, uint16_t* vd, int F, int K, int* len, int maxt);
 
+/* ---- the persistent step: every layer of forward_pass_resident's fully-device branch
+ * (bpd/lib/dev_residency.py:1380-1477; the layers of GraphRunner's captured step, :1739-1765)
+ * in one launch, with the same bits as the five- and per-op launches -----------------------
+ * One workgroup per CU runs all layers.  Each layer passes through five phases (rmsnorm ->
+ * quant -> QKV + bias -> RoPE -> KV append; masked attention -> quant; O + residual; rmsnorm ->
+ * quant -> gate|up -> SiLU(g)*u -> quant; down + residual), their outputs exchanged between
+ * workgroups through ws as words tagged with the step's serial (no fences).  Layer l reads its
+ * position from lens[l], appends the new k/v rows at that row and attends lens[l] + 1 rows;
+ * after the step every lens[l] < maxt is incremented.  Layer 0 takes the embedding row of *tok
+ * from the Q8_0 token_embd emb [vocab][E/32] (out-of-range token: a zero row and *err = 1), or
+ * x_in[E] when emb is null; the last layer's output row goes to x_out[E] (the input of
+ * lt_q8_gemv_rms_argmax).  Errors found on the device go to *err: 2 = an exchange wait ran out
+ * (bounded; the launch still ends), 3 = a length outside [0, lt_decode_step_max_len).
+ * Geometry: hd = 64, E and nh*hd at most 1024, n_ff F at most 5120, multiples of 32.
+ * lt_decode_step_max_len returns the rows the step attends at most (0: the geometry, the
+ * cache type or the device's residency rules the step out); callers take the five-launch step
+ * past it.  ws holds lt_decode_step_workspace_size(...) bytes, 256-byte aligned, zero-filled
+ * before the plan's first step and kept across steps (a step's tag is one more than the last;
+ * clear ws or its first 256 bytes' fail word after an error).  One step at a time per ws. */
+typedef struct lt_step_layer {
+  const float* attn_norm;   /* fp32 [E] */
+  const void* wqkv;         /* Q8_0 [(nh + 2*nkv)*hd][E/32]: q, k, v rows */
+  const float* bqkv;        /* fp32 [(nh + 2*nkv)*hd] or NULL */
+  const void* wo;           /* Q8_0 [E][nh*hd/32] */
+  const float* ffn_norm;    /* fp32 [E] */
+  const void* wgu;          /* Q8_0 [2F][E/32], rows interleaved: 2j = gate j, 2j+1 = up j */
+  const void* wdown;        /* Q8_0 [E][F/32] */
+  void* kc;                 /* caches [maxt][nkv*hd], fp16 or fp32 per kv_dtype */
+  void* vc;
+} lt_step_layer;
+LT_API size_t lt_decode_step_workspace_size(int n_layers, int E, int F, int nh, int nkv, int hd);
+LT_API int lt_decode_step_max_len(lt_ctx* ctx, int n_layers, int E, int F, int nh, int nkv, int hd, int kv_dtype,
+                                  int maxt);
+/* layers: a device array of n_layers descriptors */
+LT_API int lt_decode_step(lt_ctx* ctx, const lt_step_layer* layers, int n_layers, int E, int F, int nh, int nkv,
+                          int hd, float eps, float scale, const float* freqs, int* lens, int maxt, int kv_dtype,
+                          const void* emb, const int* tok, int vocab, const float* x_in, float* x_out, int* err,
+                          void* ws, size_t ws_bytes);
+
 /* Final norm -> quant -> vocab GEMV -> greedy argmax (_compute_folded_logits
  * bpd/lib/dev_residency.py:1596-1623 + argmax_dev :1074-1110): writes logits[N], then the
  * index of the maximum (ties to the lowest index) to *out, appending it to hist like

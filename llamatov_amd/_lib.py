@@ -88,6 +88,10 @@ _SIGS = {
     "lt_q8_gemv_rms_argmax": (c_int, [_P, _P, _P, c_float, _P, _P, c_int, c_int, _P, _P, _P, c_int,
                                       _P, c_size_t]),
     "lt_q8_gemv_argmax_workspace_size": (c_size_t, [c_int]),
+    "lt_decode_step_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
+    "lt_decode_step_max_len": (c_int, [_P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
+    "lt_decode_step": (c_int, [_P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_float, _P, _P, c_int,
+                               c_int, _P, _P, c_int, _P, _P, _P, _P, c_size_t]),
     "lt_attn_step": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_float, c_int, c_int,
                              c_int, _P, c_size_t]),
     "lt_q8_gemm": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int]),

@@ -432,6 +432,12 @@ class Profile:
     # each workgroup's CU measured slower at C2 than the separate attention launch, which
     # spreads the heads over 14 CUs
     attn_in_o: bool = False
+    # fused step, nsplit 1, engine numerics: the whole step (every layer) in one persistent
+    # launch (lt_decode_step: workgroups exchange each phase's outputs through step-tagged
+    # words, no kernel boundaries between layers) while the geometry allows it (head dim 64,
+    # n_embd <= 1024, n_ff <= 5120) and the cache holds at most lt_decode_step_max_len rows;
+    # otherwise the five launches (same bits)
+    persistent_step: bool = True
     fused_rms_quant: bool = False   # per-op path only: k_rms_quant instead of k_rmsnorm + k_quant_q8
     graph: bool = True
     # "engine": the reference engine's quantizer and canonical GEMV order (every field above);
@@ -613,6 +619,12 @@ class ResidentModel:
         self.arena.free()
 
 
+class _StepLayer(ctypes.Structure):
+    """lt_step_layer of include/llamatov_hip.h: one layer's device pointers."""
+    _fields_ = [(n, ctypes.c_void_p) for n in ("attn_norm", "wqkv", "bqkv", "wo", "ffn_norm", "wgu", "wdown",
+                                                "kc", "vc")]
+
+
 class DecodePlan:
     """Fixed device buffers and the launch sequence of one decode token."""
 
@@ -659,11 +671,54 @@ class DecodePlan:
                                      len_ptr=self.lens.ptr + 4 * il, dev=D)
                        for il in range(cfg.n_layers)]
         self.scale = float(hd ** -0.5)
+        self._setup_persistent()
         self._prefill: PrefillBuffers | None = None
         self.sampling = False
         self._sample_params: DevTensor | None = None
         self._sample_ws: DevTensor | None = None
         self.reset()
+
+    def _setup_persistent(self) -> None:
+        """The persistent step's workspace (zero-filled: its tags start above every stored
+        word) and the device array of per-layer descriptors, when the profile and the
+        geometry take it (lt_decode_step_max_len > 0)."""
+        self.persistent_len = 0
+        self.step_ws: DevTensor | None = None
+        self.step_layers: DevTensor | None = None
+        p, cfg, m = self.profile, self.cfg, self.model
+        if not (p.fused_step and p.persistent_step and p.attn_nsplit == 1 and not p.swiglu_fp32
+                and p.numerics == "engine"):
+            return
+        E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
+        n = int(_lib.raw("lt_decode_step_max_len")(self.dev.handle, cfg.n_layers, E, F, nh, nkv, hd, p.kv_dtype,
+                                                    self.max_ctx))
+        if n <= 0:
+            return
+        wsb = int(_lib.raw("lt_decode_step_workspace_size")(cfg.n_layers, E, F, nh, nkv, hd))
+        self.step_ws = DevTensor.empty((wsb,), np.uint8, self.dev)
+        self.dev.fill(self.step_ws.ptr, 0, wsb)
+        descs = (_StepLayer * cfg.n_layers)()
+        for il, L in enumerate(m.layers):
+            d = descs[il]
+            d.attn_norm, d.wqkv, d.bqkv = L["attn_norm"].ptr, L["wqkv"].t.ptr, (L["bqkv"].ptr if L["bqkv"] is not None else None)
+            d.wo, d.ffn_norm, d.wgu, d.wdown = L["wo"].t.ptr, L["ffn_norm"].ptr, L["wgu_il"].t.ptr, L["wdown"].t.ptr
+            d.kc, d.vc = self.caches[il].k.ptr, self.caches[il].v.ptr
+        raw = np.frombuffer(bytes(descs), np.uint8).copy()
+        self.step_layers = DevTensor.empty((raw.size,), np.uint8, self.dev)
+        self.dev.h2d(self.step_layers.ptr, raw)
+        self.persistent_len = n
+
+    @property
+    def persistent(self) -> bool:
+        """The next step (at the current host length) runs as one persistent launch."""
+        return self.persistent_len > 0 and self.caches[0].length + 1 <= self.persistent_len
+
+    def error(self) -> int:
+        """The step's device error word: 0 = none, 1 = a token outside the vocabulary, 2 = a
+        persistent step's exchange wait ran out, 3 = a persistent step past its length."""
+        out = np.zeros(1, np.int32)
+        self.dev.d2h(out, self.err.ptr)
+        return int(out[0])
 
     def prefill_buffers(self, T: int) -> "PrefillBuffers":
         if self._prefill is None or self._prefill.T < T:
@@ -681,6 +736,8 @@ class DecodePlan:
             c.length = 0
         self.dev.h2d(self.hist_count.ptr, np.zeros(1, np.int32))
         self.dev.h2d(self.err.ptr, np.zeros(1, np.int32))
+        if getattr(self, "step_ws", None) is not None:
+            self.dev.h2d(self.step_ws.ptr + 8, np.zeros(1, np.uint32))   # StepState.fail
 
     def set_token(self, tok: int) -> None:
         self.dev.h2d(self.tok.ptr, np.array([tok], np.int32))
@@ -717,13 +774,37 @@ class DecodePlan:
         return self.dev.d2h(out, self.lens.ptr)
 
     # -- the step ----------------------------------------------------------------
-    def enqueue_step(self, four: bool | None = None) -> None:
-        """Launch one decode token (fused or per-op, as the profile says).  four selects the
-        four-launch fused step (default: when the current length allows it)."""
+    def enqueue_step(self, four: bool | None = None, persistent: bool | None = None) -> None:
+        """Launch one decode token (fused or per-op, as the profile says).  persistent selects
+        the one-launch step and four the four-launch fused step (default: each when the
+        current length allows it; the persistent step first)."""
         if self.profile.fused_step:
-            self._enqueue_fused(self.four_launch if four is None else four)
+            if persistent is None:
+                persistent = self.persistent and not four
+            if persistent:
+                self._enqueue_persistent()
+            else:
+                self._enqueue_fused(self.four_launch if four is None else four)
         else:
             self._enqueue_per_op()
+
+    def _enqueue_persistent(self) -> None:
+        """Every layer in one launch (lt_decode_step), then the vocab GEMV with its argmax:
+        the same arithmetic as _enqueue_fused, bit for bit."""
+        if self.persistent_len <= 0:
+            raise ValueError("the persistent step does not apply to this profile or geometry")
+        cfg, m, p = self.cfg, self.model, self.profile
+        h = self.dev.handle
+        eps = ctypes.c_float(cfg.norm_eps)
+        gather = not self.host_embed
+        call("lt_decode_step", h, self.step_layers.vp, cfg.n_layers, cfg.n_embd, cfg.n_ff, cfg.n_head,
+             cfg.n_head_kv, cfg.head_dim, eps, ctypes.c_float(self.scale), m.freqs.vp, self.lens.vp, self.max_ctx,
+             p.kv_dtype, m.tok_embd.t.vp if gather else None, self.tok.vp if gather else None, cfg.vocab,
+             None if gather else self.resid_in.vp, self.carry.vp, self.err.vp, self.step_ws.vp,
+             self.step_ws.nbytes)
+        call("lt_q8_gemv_rms_argmax", h, self.carry.vp, m.output_norm.vp, eps, m.output.t.vp, self.logits.vp,
+             cfg.vocab, cfg.n_embd, self.tok.vp, *self._hist_args(), self.am_ws.vp, self.am_ws.nbytes)
+        self._enqueue_sample_if_on()
 
     def _enqueue_fused(self, four: bool = False) -> None:
         """Five launches per layer (lt_fused.hip), then the vocab GEMV with its argmax:
@@ -972,7 +1053,8 @@ class DecodePlan:
             c.free()
         for t in (self.tok, self.err, self.hist, self.hist_count, self.lens, self.resid_in, self.carry,
                   self.xres, self.h, self.qkv, self.att, self.gu, self.v, self.logits, self.xq, self.xd,
-                  self.am_ws, self.attn_ws, self._sample_params, self._sample_ws):
+                  self.am_ws, self.attn_ws, self._sample_params, self._sample_ws, self.step_ws,
+                  self.step_layers):
             if t is not None:
                 t.free()
 
@@ -1106,6 +1188,7 @@ class StepGraph:
         self.dev = plan.dev
         self.graph = ctypes.c_void_p()    # the five-launch step (every length)
         self.graph4 = ctypes.c_void_p()   # the four-launch step (lengths up to plan.four_launch_len)
+        self.graphp = ctypes.c_void_p()   # the persistent step (lengths up to plan.persistent_len)
         self.captured = False
         self.captured_sampling = False
 
@@ -1121,10 +1204,10 @@ class StepGraph:
         self.dev.sync()
         return logits
 
-    def _capture_one(self, out: ctypes.c_void_p, four: bool) -> None:
+    def _capture_one(self, out: ctypes.c_void_p, four: bool, persistent: bool = False) -> None:
         call("lt_graph_begin", self.dev.handle)
         try:
-            self.plan.enqueue_step(four=four)
+            self.plan.enqueue_step(four=four, persistent=persistent)
         except Exception:
             g = ctypes.c_void_p()
             _lib.raw("lt_graph_end")(self.dev.handle, ctypes.byref(g))
@@ -1139,13 +1222,17 @@ class StepGraph:
         if self.captured:
             raise RuntimeError("StepGraph.capture: already captured")
         self._capture_one(self.graph, False)
-        if self.plan.four_launch_len > 0 and self.plan.profile.fused_step:
-            try:
+        try:
+            if self.plan.four_launch_len > 0 and self.plan.profile.fused_step:
                 self._capture_one(self.graph4, True)
-            except Exception:
-                _lib.raw("lt_graph_free")(self.graph)
-                self.graph = ctypes.c_void_p()
-                raise
+            if self.plan.persistent_len > 0:
+                self._capture_one(self.graphp, False, persistent=True)
+        except Exception:
+            for g in (self.graph, self.graph4):
+                if g.value:
+                    _lib.raw("lt_graph_free")(g)
+            self.graph, self.graph4 = ctypes.c_void_p(), ctypes.c_void_p()
+            raise
         self.captured = True
         self.captured_sampling = self.plan.sampling
 
@@ -1155,7 +1242,12 @@ class StepGraph:
         if self.plan.sampling != self.captured_sampling:
             raise RuntimeError("the plan switched between greedy and sampling after capture: capture again")
         self.plan.check_room(1)
-        g = self.graph4 if self.graph4.value and self.plan.four_launch else self.graph
+        if self.graphp.value and self.plan.persistent:
+            g = self.graphp
+        elif self.graph4.value and self.plan.four_launch:
+            g = self.graph4
+        else:
+            g = self.graph
         call("lt_graph_launch", self.dev.handle, g)
         for c in self.plan.caches:
             c.length += 1
@@ -1198,10 +1290,12 @@ class StepGraph:
     def free(self) -> None:
         if self.captured:
             call("lt_graph_free", self.graph)
-            if self.graph4.value:
-                call("lt_graph_free", self.graph4)
+            for g in (self.graph4, self.graphp):
+                if g.value:
+                    call("lt_graph_free", g)
             self.graph = ctypes.c_void_p()
             self.graph4 = ctypes.c_void_p()
+            self.graphp = ctypes.c_void_p()
             self.captured = False
 
 

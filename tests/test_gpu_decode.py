@@ -73,7 +73,7 @@ def test_small_qwen_four_launch_step_bitexact(gpu, oracle, kv_dtype, four):
     (head dim 64: the fused attention applies)."""
     cfg = M.SMALL_QWEN
     case(f"small-qwen stepwise four={four} kv={kv_dtype}")
-    plan = dr.DecodePlan(resident(cfg, gpu), dr.Profile(kv_dtype=kv_dtype, attn_in_o=four))
+    plan = dr.DecodePlan(resident(cfg, gpu), dr.Profile(kv_dtype=kv_dtype, attn_in_o=four, persistent_step=False))
     assert plan.four_launch == four
     orc = oracle.OracleModel(cfg, weights(cfg), kv_f16=kv_dtype == LT_KV_F16)
     toks = M.random_prompt(cfg, 5, seed=13)
@@ -169,26 +169,33 @@ def test_prefill_kv_equals_incremental(gpu):
 @pytest.mark.parametrize("cfg_name,n_prompt,n_gen,kv_dtype,step", [
     ("small-qwen-arch", 32, 32, LT_KV_F32, "fused"),
     ("small-qwen-arch", 32, 32, LT_KV_F32, "per_op"),
+    ("small-qwen-arch", 32, 32, LT_KV_F16, "persistent"),
     ("qwen2.5-0.5b-arch", 32, 128, LT_KV_F32, "fused"),
     ("qwen2.5-0.5b-arch", 32, 128, LT_KV_F16, "fused"),
+    ("qwen2.5-0.5b-arch", 32, 128, LT_KV_F32, "persistent"),
+    ("qwen2.5-0.5b-arch", 32, 128, LT_KV_F16, "persistent"),
     ("qwen2.5-0.5b-arch", 32, 128, LT_KV_F16, "per_op"),
     ("qwen2.5-0.5b-arch", 32, 128, LT_KV_F16, "fused_swiglu_fp32"),
 ])
 def test_greedy_tokens_identical(gpu, oracle, cfg_name, n_prompt, n_gen, kv_dtype, step):
-    """Greedy token identity with the oracle, through the captured graph."""
+    """Greedy token identity with the oracle, through the captured graph ("fused": the
+    five-launch step; "persistent": the one-launch step)."""
     cfg = M.CONFIGS[cfg_name]
     case(f"greedy {cfg_name} {n_prompt}+{n_gen} kv={kv_dtype} {step}")
     prompt = M.random_prompt(cfg, n_prompt, seed=7)
     orc = oracle.OracleModel(cfg, weights(cfg), kv_f16=kv_dtype == LT_KV_F16)
     exp, margins = orc.generate(prompt, n_gen)
     plan = dr.DecodePlan(resident(cfg, gpu), dr.Profile(kv_dtype=kv_dtype, fused_step=step != "per_op",
-                                                        swiglu_fp32=step == "fused_swiglu_fp32"))
+                                                        swiglu_fp32=step == "fused_swiglu_fp32",
+                                                        persistent_step=step == "persistent"))
+    assert (plan.persistent_len > 0) == (step == "persistent")
     gr = dr.StepGraph(plan)
     gr.seed(prompt)
     first = plan.read_token()
     gr.capture()
     got = [first] + gr.replay_tokens(n_gen - 1)
     print(f"[margins] min top1-top2 margin {float(margins.min()):.3e}", flush=True)
+    assert plan.error() == 0
     assert got == exp
     gr.free()
     plan.free()
@@ -201,7 +208,7 @@ def test_step_switches_from_four_to_five_launches(gpu, oracle):
     case("four -> five launch switch")
     w = weights(M.SMALL_QWEN)
     plan = dr.DecodePlan(dr.ResidentModel(cfg, w, gpu, layouts="fused"),
-                         dr.Profile(kv_dtype=LT_KV_F16, attn_in_o=True))
+                         dr.Profile(kv_dtype=LT_KV_F16, attn_in_o=True, persistent_step=False))
     lim = plan.four_launch_len
     assert 0 < lim < 400
     orc = oracle.OracleModel(cfg, w, kv_f16=True)
