@@ -233,25 +233,40 @@ __device__ __forceinline__ float q8_elem(const uint8_t* row, int i) {
   return (float)(int8_t)blk[2 + (i & 31)] * lt_h2f(d);
 }
 
+// halfwave_tree_dpp on 8 values at once, level by level: the same pairing for each value, the
+// cross-lane reads of the 8 values in flight together.
+__device__ __forceinline__ void halfwave_tree_dpp8(float (&a)[8]) {
+  float b[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) b[i] = swz_xor16(a[i]);
+#pragma unroll
+  for (int i = 0; i < 8; i++) a[i] = a[i] + b[i];
+#pragma unroll
+  for (int i = 0; i < 8; i++) a[i] = a[i] + dpp_f<0x108>(a[i]);
+#pragma unroll
+  for (int i = 0; i < 8; i++) a[i] = a[i] + dpp_f<0x104>(a[i]);
+#pragma unroll
+  for (int i = 0; i < 8; i++) a[i] = a[i] + dpp_f<0x102>(a[i]);
+#pragma unroll
+  for (int i = 0; i < 8; i++) a[i] = a[i] + dpp_f<0x101>(a[i]);
+}
+
 // ---- the pieces of the fused GEMV prologues ---------------------------------------------
 // rms_ss order (norm_softmax_from_facts.pl:49, 83-108): thread t folds x[t], x[t+256], ... by
 // fma (slots past K hold 0, which leave the fold unchanged), then the pairwise tree 128..1;
-// inv = rsqrt(ss/N + eps).  red: kT + 1 floats.
+// inv = rsqrt(ss/N + eps).  red: kT floats.
 __device__ __forceinline__ float rms_inv4(const float (&s)[4], int K, float eps, float* red) {
   float p = 0.0f;
 #pragma unroll
   for (int k = 0; k < 4; k++) p = fmaf(s[k], s[k], p);
   red[threadIdx.x] = p;
   lds_barrier();
-  if (threadIdx.x < 64) {
-    const int t = threadIdx.x;
-    const float a = red[t] + red[t + 128];
-    const float b = red[t + 64] + red[t + 192];
-    const float c = wave_tree_dpp(a + b);
-    if (t == 0) red[kT] = lt_rsqrtf(c / (float)K + eps);
-  }
-  lds_barrier();
-  return red[kT];
+  // every wave evaluates the last levels and the rsqrt itself (no second barrier)
+  const int t = threadIdx.x & 63;
+  const float a = red[t] + red[t + 128];
+  const float b = red[t + 64] + red[t + 192];
+  const float c = __shfl(wave_tree_dpp(a + b), 0, 64);
+  return lt_rsqrtf(c / (float)K + eps);
 }
 
 // The normalized row y = (x*inv)*w quantized into the GEMV's activation records: thread t
@@ -341,9 +356,13 @@ struct AttnLds {
   static constexpr int kEsz = kF16 ? 2 : 4;
   static constexpr int kRow = kHd * kEsz;          // bytes of one cache row of one KV group
   static constexpr int kKRow = kRow + 16;          // the pad puts a wave's rows on distinct banks
-  static __host__ __device__ int k_off(int nmax) { return nmax * 4 + kHd * 4 + 16; }
+  // V is staged transposed, one row of nmax positions per head dim, so a lane reads 8
+  // positions of its dim in one 16-byte read; the 16-byte pad puts the 16 lanes of a read
+  // phase on distinct banks (nmax is a multiple of 64)
+  static __host__ __device__ int vt_pitch(int nmax) { return nmax * kEsz + 16; }
+  static __host__ __device__ int k_off(int nmax) { return nmax * 4 + kHd * 4 + 32; }
   static __host__ __device__ int v_off(int nmax) { return k_off(nmax) + nmax * kKRow; }
-  static __host__ __device__ int bytes(int nmax) { return kLdsSlots + v_off(nmax) + nmax * kRow; }
+  static __host__ __device__ int bytes(int nmax) { return kLdsSlots + v_off(nmax) + kHd * vt_pitch(nmax); }
 };
 
 template <bool kF16>
@@ -373,9 +392,10 @@ __device__ __forceinline__ bool attn_worker(const StepParams& P, uint8_t* smem, 
     lds_barrier();   // wave 0 may still be reading the previous layer's V rows and exps
     float* ss = (float*)smem;                              // [nmax] scores, then exps
     float* sq = ss + P.nmax;                               // [64]
-    float* smx = sq + kHd;                                 // [4] wave maxima
+    float* smx = sq + kHd;                                 // [4] wave maxima, then [1] Z
     uint8_t* sK = smem + AL::k_off(P.nmax);
-    uint8_t* sV = smem + AL::v_off(P.nmax);
+    uint8_t* sV = smem + AL::v_off(P.nmax);                // [hd][vpitch]: V transposed
+    const int vpitch = AL::vt_pitch(P.nmax);
     const int g = head / (nh / nkv);
     const int n = L + 1;
     const bool ok_len = lvalid && n <= P.nmax;
@@ -404,7 +424,15 @@ __device__ __forceinline__ bool attn_worker(const StepParams& P, uint8_t* smem, 
           if (i < units) {
             const int r = i / kUR, u = i - r * kUR;
             *(u32x4*)(sK + r * AL::kKRow + u * 16) = kk[j];
-            *(u32x4*)(sV + r * AL::kRow + u * 16) = vv[j];
+            // V transposed: the unit's dims each to their own row, at position r
+            const uint32_t a[4] = {vv[j].x, vv[j].y, vv[j].z, vv[j].w};
+            constexpr int kPer = 16 / AL::kEsz;
+#pragma unroll
+            for (int k = 0; k < kPer; k++) {
+              uint8_t* dst = sV + (u * kPer + k) * vpitch + r * AL::kEsz;
+              if constexpr (kF16) *(uint16_t*)dst = (uint16_t)(a[k >> 1] >> (16 * (k & 1)));
+              else *(uint32_t*)dst = a[k];
+            }
           }
         }
       }
@@ -423,7 +451,7 @@ __device__ __forceinline__ bool attn_worker(const StepParams& P, uint8_t* smem, 
       sq[t] = __uint_as_float(qv);
     } else if (t < 3 * kHd && ok_len) {
       const int d = (t - kHd) & (kHd - 1);
-      uint8_t* dst = (t < 2 * kHd ? sK + L * AL::kKRow : sV + L * AL::kRow) + d * AL::kEsz;
+      uint8_t* dst = t < 2 * kHd ? sK + L * AL::kKRow + d * AL::kEsz : sV + d * vpitch + L * AL::kEsz;
       if constexpr (kF16) *(uint16_t*)dst = lt_f2h(__uint_as_float(qv));
       else *(float*)dst = __uint_as_float(qv);
     }
@@ -467,50 +495,70 @@ __device__ __forceinline__ bool attn_worker(const StepParams& P, uint8_t* smem, 
     if (ok_len)
       for (int p = t; p < n; p += kT) ss[p] = lt_expf_sel(ss[p] - m);
     lds_barrier();
-    if (t < 64) {
-      // Z: lane l folds the exps of positions l, l+64, ... in order, then the 64-lane tree
+    // Z on wave 1 while wave 0 runs the O chains: lane l folds the exps of positions l, l+64,
+    // ... in order, then the 64-lane tree
+    if (t >= 64 && t < 128) {
       float z = 0.0f;
       if (ok_len)
-        for (int p = t; p < n; p += 64) z = z + ss[p];
-      z = __shfl(wave_tree_dpp(z), 0, 64);
+        for (int p = t - 64; p < n; p += 64) z = z + ss[p];
+      z = wave_tree_dpp(z);
+      if (t == 64) smx[4] = z;
+    }
+    float o = 0.0f;
+    if (t < 64) {
       // O: lane d's sequential fma chain over the positions
-      float o = 0.0f;
       if (ok_len) {
-        // groups of 8 positions, each group's LDS reads issued one group ahead of its fmas
-        // (a wave alone on its SIMD otherwise waits out an LDS round trip per group)
-        // (V values stay raw cache bits until their fma, so no conversion consumes a read early;
-        // the last group's look-ahead re-reads that group, which is discarded)
-        const uint8_t* vp = sV + t * AL::kEsz;
+        // groups of 8 positions: the exps in two 16-byte reads, the lane's V values in one
+        // (fp16) or two (fp32) from the transposed rows; two groups' reads in flight ahead of
+        // the chain (a wave alone on its SIMD would otherwise wait out an LDS round trip per
+        // group).  V stays raw cache bits until its fma; a look-ahead past the last group
+        // re-reads that group and is discarded.
+        const uint8_t* vrow = sV + t * vpitch;
         const int ng = n >> 3;
-        float e[8];
-        uint32_t vx[8];
-        auto read_group = [&](int p0, float (&eg)[8], uint32_t (&vg)[8]) {
+        struct Grp {
+          f32x4 e0, e1;
+          u32x4 v0, v1;
+        };
+        auto rd = [&](int gi, Grp& g) {
+          const int p0 = (gi < ng ? gi : ng - 1) * 8;
+          g.e0 = *(const f32x4*)(ss + p0);
+          g.e1 = *(const f32x4*)(ss + p0 + 4);
+          g.v0 = *(const u32x4*)(vrow + p0 * AL::kEsz);
+          if constexpr (!kF16) g.v1 = *(const u32x4*)(vrow + p0 * AL::kEsz + 16);
+        };
+        auto fold8 = [&](const Grp& g) {
+          const float e[8] = {g.e0.x, g.e0.y, g.e0.z, g.e0.w, g.e1.x, g.e1.y, g.e1.z, g.e1.w};
+          const uint32_t v[8] = {g.v0.x, g.v0.y, g.v0.z, g.v0.w, g.v1.x, g.v1.y, g.v1.z, g.v1.w};
 #pragma unroll
           for (int j = 0; j < 8; j++) {
-            eg[j] = ss[p0 + j];
-            if constexpr (kF16) vg[j] = *(const uint16_t*)(vp + (p0 + j) * AL::kRow);
-            else vg[j] = *(const uint32_t*)(vp + (p0 + j) * AL::kRow);
+            if constexpr (kF16) o = fmaf(e[j], lt_h2f((uint16_t)(v[j >> 1] >> (16 * (j & 1)))), o);
+            else o = fmaf(e[j], __uint_as_float(v[j]), o);
           }
         };
-        auto widen = [](uint32_t b) -> float {
-          if constexpr (kF16) return lt_h2f((uint16_t)b);
-          else return __uint_as_float(b);
-        };
-        if (ng > 0) read_group(0, e, vx);
-        for (int gi = 0; gi < ng; gi++) {
-          float en[8];
-          uint32_t vn[8];
-          read_group((gi + 1 < ng ? gi + 1 : gi) * 8, en, vn);
+        // kRot register groups in rotation (kRot - 1 groups' reads in flight); the empty asm
+        // statements keep the compiler from moving a group's reads down to its fold
+        constexpr int kRot = 4;
+        if (ng > 0) {
+          Grp g[kRot];
 #pragma unroll
-          for (int j = 0; j < 8; j++) o = fmaf(e[j], widen(vx[j]), o);
+          for (int k = 0; k < kRot - 1; k++) rd(k, g[k]);
+#pragma unroll 1
+          for (int gi = 0; gi < ng; gi += kRot) {
 #pragma unroll
-          for (int j = 0; j < 8; j++) {
-            e[j] = en[j];
-            vx[j] = vn[j];
+            for (int k = 0; k < kRot; k++) {
+              rd(gi + k + kRot - 1, g[(k + kRot - 1) % kRot]);
+              asm volatile("" ::: "memory");
+              if (gi + k >= ng) break;
+              fold8(g[k]);
+            }
           }
         }
-        for (int p = ng * 8; p < n; p++) o = fmaf(ss[p], kv_at<kF16>(vp + p * AL::kRow), o);
+        for (int p = ng * 8; p < n; p++) o = fmaf(ss[p], kv_at<kF16>(vrow + p * AL::kEsz), o);
       }
+    }
+    lds_barrier();
+    if (t < 64) {
+      const float z = smx[4];
       const float out = ok_len ? o / z : 0.0f;
       // quantized for the O projection: the head's two 32-element blocks, one per half-wave
       const QScale sc = q8_scale(halfwave_max(fabsf(out)));
@@ -617,7 +665,7 @@ __device__ __forceinline__ bool gemv_worker(const StepParams& P, uint8_t* smem, 
       const f32x4 nw4 = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rn, t * 16, 0, 0));
       // the rotation of pair j = 4*ac + t at position L (k_rope's arithmetic), under the poll
       float sn = 0.0f, cs = 1.0f;
-      if (t < 4) lt_sincosf((float)L * P.freqs[ac * 4 + t], &sn, &cs);
+      if (t < 8) lt_sincosf((float)L * P.freqs[ac * 4 + (t & 3)], &sn, &cs);
       float xv[4];
       bool ok = true;
       if (l == 0) {
@@ -641,28 +689,27 @@ __device__ __forceinline__ bool gemv_worker(const StepParams& P, uint8_t* smem, 
       const float rv = halfwave_tree_dpp(lane < nbE ? folded : 0.0f);
       if (lane == 0) srow[hw] = Ly.bqkv ? rv + bias : rv;
       lds_barrier();
-      if (t < 4) {
-        const int j = ac * 4 + t;
-        float x1 = srow[t], x2 = srow[t + 4];
+      if (t < 8) {
+        // thread i takes pair i & 3 (rows j and j + hd/2) and keeps its first (i < 4) or
+        // second output: the unit's 8 words go out in one store instruction
+        const int i = t & 3;
+        const int j = ac * 4 + i;
+        float x1 = srow[i], x2 = srow[i + 4];
         if (ahead < nh + nkv) {   // q and k heads rotate, v heads pass
           const float y1 = fmaf(x1, cs, -(x2 * sn));
           const float y2 = fmaf(x1, sn, x2 * cs);
           x1 = y1;
           x2 = y2;
         }
-        xput(XA + uA * 8 + t, tag, __float_as_uint(x1));
-        xput(XA + uA * 8 + 4 + t, tag, __float_as_uint(x2));
+        const float y = t < 4 ? x1 : x2;
+        xput(XA + uA * 8 + t, tag, __float_as_uint(y));
         if (ahead >= nh && lvalid) {   // the k and v rows into the caches at row L
           const bool isv = ahead >= nh + nkv;
-          const size_t off = (size_t)L * nkv * kHd + (size_t)(ahead - nh - (isv ? nkv : 0)) * kHd + j;
+          const size_t off = (size_t)L * nkv * kHd + (size_t)(ahead - nh - (isv ? nkv : 0)) * kHd + j +
+                             (t < 4 ? 0 : kHd / 2);
           void* c = isv ? Ly.vc : Ly.kc;
-          if constexpr (kF16) {
-            ((uint16_t*)c)[off] = lt_f2h(x1);
-            ((uint16_t*)c)[off + kHd / 2] = lt_f2h(x2);
-          } else {
-            ((float*)c)[off] = x1;
-            ((float*)c)[off + kHd / 2] = x2;
-          }
+          if constexpr (kF16) ((uint16_t*)c)[off] = lt_f2h(y);
+          else ((float*)c)[off] = y;
         }
       }
     }
@@ -688,7 +735,11 @@ __device__ __forceinline__ bool gemv_worker(const StepParams& P, uint8_t* smem, 
       if (wg_any(!ok, slots, par)) return false;
       const float folded = fold_raw(wC, (blk_off(row, nbO, lane, true) & 2u) != 0, rec + (lane < nbO ? lane : 0) * kRecDwords, 0.0f);
       const float rv = halfwave_tree_dpp(lane < nbO ? folded : 0.0f);
-      if (lane == 0) xput(XC + row, tag, __float_as_uint(rv + xres));
+      // the unit's 8 rows leave in one store instruction (a word per half-wave measured
+      // ~0.6 us slower to exchange)
+      if (lane == 0) srow[hw] = rv + xres;
+      lds_barrier();
+      if (t < 8) xput(XC + uC * 8 + t, tag, __float_as_uint(srow[t]));
     }
     if (uA >= 0 && l + 1 < NL) issue_A(l + 1);
 
@@ -710,12 +761,19 @@ __device__ __forceinline__ bool gemv_worker(const StepParams& P, uint8_t* smem, 
       norm_to_rec(xs, nw4, inv, E, rec);
       lds_barrier();
       const uint32_t* ra = rec + (lane < nbE ? lane : 0) * kRecDwords;
+      // the 8 rows' folds first, then their trees level by level (one row at a time would
+      // wait out each tree's cross-lane latencies in turn)
+      float f[8];
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         const int row = uD * kGuRows + hw + 8 * i;
         const float folded = fold_raw(wD[i], (blk_off(row, nbE, lane, true) & 2u) != 0, ra, 0.0f);
-        const float rv = halfwave_tree_dpp(lane < nbE ? folded : 0.0f);
-        if (lane == 0) srow[hw + 8 * i] = rv;
+        f[i] = lane < nbE ? folded : 0.0f;
+      }
+      halfwave_tree_dpp8(f);
+      if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) srow[hw + 8 * i] = f[i];
       }
       lds_barrier();
       if (t < 64) {
@@ -748,10 +806,12 @@ __device__ __forceinline__ bool gemv_worker(const StepParams& P, uint8_t* smem, 
           acc = fold_raw(wE[k], (blk_off(row, nbF, b, true) & 2u) != 0, rec + b * kRecDwords, acc);
       }
       const float rv = halfwave_tree_dpp(acc);
-      if (lane == 0) {
-        const float y = rv + xres;
-        xput(XE + row, tag, __float_as_uint(y));
-        if (l == NL - 1) P.x_out[row] = y;
+      if (lane == 0) srow[hw] = rv + xres;
+      lds_barrier();
+      if (t < 8) {
+        const float y = srow[t];
+        xput(XE + uE * 8 + t, tag, __float_as_uint(y));
+        if (l == NL - 1) P.x_out[uE * 8 + t] = y;
       }
     }
   }
