@@ -105,7 +105,50 @@ def rotation(dev, mats, min_bytes: float = 600e6):
     return out, extra
 
 
-def step_kernels(dev, plan, only: str | None = None, attn_len: int | None = None) -> list[dict]:
+def persistent_entry(dev, plan, L: int) -> dict:
+    """The persistent step (lt_decode_step: every layer in one launch) timed on its own: a
+    graph of back-to-back launches alternating between the plan's weights and a device copy of
+    every layer matrix (~760 MB together, more than the 256 MB Infinity Cache holds), the caches
+    at length L (each launch appends a row; the lengths are restored after).  Algorithmic bytes
+    per launch: every layer's Q8_0 weights, the K/V rows attended (at the mean length of the
+    launches) and appended, the norm and bias vectors, the embedding row and the output row."""
+    from llamatov_amd import engine as dr
+    cfg, m = plan.cfg, plan.model
+    copies, extra = {}, []
+    for il, Ly in enumerate(m.layers):
+        for name in ("wqkv", "wo", "wgu_il", "wdown"):
+            src = Ly[name].t
+            t = dr.DevTensor.empty(src.shape, src.dtype, dev)
+            dev.d2d(t.ptr, src.ptr, src.nbytes)
+            copies[(il, name)] = t
+            extra.append(t)
+    alt = plan.step_layer_descs(copies)
+    launches = [lambda: plan.enqueue_layers(), lambda: plan.enqueue_layers(alt)] * 4
+    saved = plan.lengths().copy()
+    dev.h2d(plan.lens.ptr, np.full(cfg.n_layers, L, np.int32))
+    us = graph_us_per_launch(dev, launches)   # 5 x 8 launches: lengths L .. L + 39
+    dev.h2d(plan.lens.ptr, saved)
+    if plan.error():
+        raise RuntimeError(f"persistent step reported device error {plan.error()} while timed")
+    for t in extra:
+        t.free()
+    alt.free()
+    rb = lambda N, K: N * (K // 32) * 34
+    E, F, QD, NQ = cfg.n_embd, cfg.n_ff, cfg.q_dim, cfg.n_qkv
+    esz = 2 if plan.profile.kv_dtype else 4
+    per_layer = (rb(NQ, E) + rb(E, QD) + rb(2 * F, E) + rb(E, F) + 2 * (L + 20) * cfg.kv_dim * esz
+                 + 2 * cfg.kv_dim * esz + 8 * E + (4 * NQ if cfg.qkv_bias else 0))
+    nbytes = cfg.n_layers * per_layer + (E // 32) * 34 + 4 * E
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"step kernel step (persistent): {us:.2f} us, {gbs:.0f} GB/s")
+    return {"name": "step", "kernel": "k_decode_step<f16> (lt_decode_step: every layer in one launch)",
+            "shape": [cfg.n_layers, E, F, cfg.n_head, cfg.n_head_kv, cfg.head_dim, L + 20], "launches_per_step": 1,
+            "avg_launch_us": round(us, 3), "bytes_per_launch": int(nbytes), "GB/s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def step_kernels(dev, plan, only: str | None = None, attn_len: int | None = None,
+                 five: bool = False) -> list[dict]:
     """Every launch of the fused C2 decode step, timed on its own (graph of back-to-back
     launches over rotated weights), with its algorithmic bytes per launch:
       qkv     rmsnorm -> quant -> QKV GEMV + bias         N(K/32)34 + 8K + 8N
@@ -116,13 +159,17 @@ def step_kernels(dev, plan, only: str | None = None, attn_len: int | None = None
       vocab   final rmsnorm -> quant -> vocab GEMV -> argmax        V(K/32)34 + 8K + 4V
     The attention runs at cache length attn_len (default: the plan's current length; the
     decode bench passes the mean length of its timed tokens), over rows the decode wrote; its
-    launches leave the lengths unchanged."""
+    launches leave the lengths unchanged.  When the plan runs the persistent step at that
+    length (and five is False) the table is that launch (persistent_entry) and the vocab
+    launch."""
     from llamatov_amd import engine as dr
     from llamatov_amd._lib import call
     cfg, m, p = plan.cfg, plan.model, plan.profile
     if not p.fused_step or p.swiglu_fp32 or p.attn_nsplit != 1:
         raise ValueError("step_kernels times the default fused step (nsplit 1, quantizing gate|up epilogue)")
-    four = plan.four_launch_len >= (attn_len if attn_len is not None else plan.caches[0].length) + 1
+    Lq = attn_len if attn_len is not None else plan.caches[0].length
+    persistent = not five and plan.persistent_len >= Lq + 1
+    four = not persistent and plan.four_launch_len >= Lq + 1
     h = dev.handle
     E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
     QD, NQ, V = cfg.q_dim, cfg.n_qkv, cfg.vocab
@@ -193,6 +240,10 @@ def step_kernels(dev, plan, only: str | None = None, attn_len: int | None = None
         kinds = {"qkv": kinds4["qkv"], "attn_o": kinds4["attn_o"], "gateup": kinds4["gateup"],
                  "down": kinds["down"], "vocab": kinds["vocab"]}
     out = []
+    if persistent:
+        kinds = {"vocab": kinds["vocab"]}
+        if not only or only == "step":
+            out.append(persistent_entry(dev, plan, L))
     for name, k in kinds.items():
         if only and name != only:
             continue
@@ -335,7 +386,27 @@ def attention_sweep(dev, reps: int = 20) -> list[dict]:
     return out
 
 
-def c5_leg(dev, n_prefill: int = 512, n_decode: int = 256, eager: bool = False) -> dict:
+def c5_cpu_decode(cfg, w, n_prompt: int = 4, n_decode: int = 3) -> dict:
+    """The oracle decoding the C5 model on the host (all cores): n_prompt tokens stepped
+    untimed, then n_decode greedy tokens timed."""
+    from oracle import oracle as orc
+    from llamatov_amd import model as M
+    cores = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
+    orc.set_threads(cores)
+    m = orc.OracleModel(cfg, w, kv_f16=True, attn_nsplit=C5_ATTN_NSPLIT, max_ctx=n_prompt + n_decode + 4)
+    logits = None
+    for t in M.random_prompt(cfg, n_prompt, seed=17):
+        logits = m.step(t)
+    t0 = time.perf_counter()
+    for _ in range(n_decode):
+        logits = m.step(orc.argmax(logits))
+    dt = time.perf_counter() - t0
+    return {"value": round(n_decode / dt, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"C5 model, {n_prompt}-token prompt stepped untimed, then {n_decode} greedy decode steps "
+                      f"timed on {cores} threads (oracle/lt_oracle.c)"}
+
+
+def c5_leg(dev, n_prefill: int = 512, n_decode: int = 256, eager: bool = False, cpu: bool = False) -> dict:
     """random-init Llama-3-8B-architecture Q8_0 model (N(0,0.02) weights
     quantized with the engine quantizer), a 512-token prefill of random ids through the
     tiled int8-MFMA GEMM, then 256 greedy decode tokens (graph replay) with an fp16 KV cache."""
@@ -346,6 +417,10 @@ def c5_leg(dev, n_prefill: int = 512, n_decode: int = 256, eager: bool = False) 
     t0 = time.perf_counter()
     w = M.synth_weights(cfg, seed=4321)
     log(f"C5 weights generated in {time.perf_counter() - t0:.1f}s")
+    cpu_res = None
+    if cpu:
+        log("C5 CPU baseline: oracle decode")
+        cpu_res = c5_cpu_decode(cfg, w)
     model = dr.ResidentModel(cfg, w, dev, layouts="fused")
     del w
     # split-K over the context (the declared split order, merged in the attention launch)
@@ -363,7 +438,7 @@ def c5_leg(dev, n_prefill: int = 512, n_decode: int = 256, eager: bool = False) 
     pre_ms = ev.stop_ms()
     macs = n_prefill * cfg.n_layers * (cfg.n_qkv * cfg.n_embd + cfg.n_embd * cfg.q_dim + 2 * cfg.n_ff * cfg.n_embd
                                       + cfg.n_embd * cfg.n_ff)
-    res = {"model": cfg.name, "prefill_tokens": n_prefill, "prefill_ms": round(pre_ms, 3),
+    res = {"model": cfg.name, "cpu_baseline": cpu_res, "prefill_tokens": n_prefill, "prefill_ms": round(pre_ms, 3),
            "prefill_tok_s": round(n_prefill / (pre_ms / 1e3), 1),
            "prefill_mfma_util": round(2 * macs / (pre_ms / 1e3) / (INT8_PEAK_TOPS * 1e12), 4),
            "prefill_gemm_macs": int(macs)}
@@ -578,6 +653,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=128, help="timed decode tokens")
     ap.add_argument("--warmup", type=int, default=16, help="untimed decode tokens before timing")
+    ap.add_argument("--repeats", type=int, default=5,
+                    help="timed runs of --steps tokens each, from the same post-prompt state; value is their "
+                         "median (the reference's protocol takes the median of 6 runs, rms_quant_prod_ab.py:38-47)")
     ap.add_argument("--kv", choices=["f16", "f32"], default="f16")
     ap.add_argument("--prompt", type=int, default=32)
     ap.add_argument("--cpu-tokens", type=int, default=128, help="decode tokens in the CPU baseline sample")
@@ -602,8 +680,8 @@ def main() -> int:
                     help="only one step kernel's timing loop (--roofline-kernel), plus a device copy of a weight "
                          "matrix (the known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE); "
                          "for counter runs")
-    ap.add_argument("--roofline-kernel", default="gateup",
-                    choices=["qkv", "attn", "o", "attn_o", "gateup", "down", "vocab"])
+    ap.add_argument("--roofline-kernel", default="step",
+                    choices=["step", "qkv", "attn", "o", "attn_o", "gateup", "down", "vocab"])
     ap.add_argument("--batched", default="8,64",
                     help="batch sizes of the batched-decode leg (adds batched_decode; empty to skip)")
     ap.add_argument("--no-sampled", action="store_true", help="skip the sampled-decode leg")
@@ -638,7 +716,8 @@ def main() -> int:
         # the cache as the timed decode sees it on average (prompt + half the steps), so the
         # attention runs at the length of the main bench line's step table
         dr.forward_prefill(plan, M.random_prompt(cfg, args.prompt + args.steps // 2, seed=7))
-        entry = step_kernels(dev, plan, only=args.roofline_kernel)[0]
+        entry = step_kernels(dev, plan, only=args.roofline_kernel,
+                             five=args.roofline_kernel not in ("step", "vocab"))[0]
         src = model.layers[0]["wgu_il"].t
         dst = dr.DevTensor.empty(src.shape, src.dtype, dev)
         dev.d2d(dst.ptr, src.ptr, src.nbytes)   # calibration: a plain copy of known size
@@ -685,29 +764,47 @@ def main() -> int:
         one_step()
     dev.sync()
 
-    # timed: K back-to-back replays from the post-prompt state (the C2 decode)
-    rewind()
-    hist0 = plan.history_count()
-    ev = Events(dev)
-    t0 = time.perf_counter()
-    ev.start()
-    for _ in range(args.steps):
-        one_step()
-    gpu_ms = ev.stop_ms()
-    dev.sync()
-    wall = time.perf_counter() - t0
-    tokens = [first] + plan.history()[hist0:hist0 + args.steps]
-    log(f"timed {args.steps} steps: wall {wall * 1e3:.2f} ms, events {gpu_ms:.2f} ms")
+    # timed: K back-to-back replays from the post-prompt state (the C2 decode), repeated; each
+    # run is bracketed by device synchronizations and times exactly K steps
+    runs = []
+    tokens = None
+    for r in range(max(1, args.repeats)):
+        rewind()
+        hist0 = plan.history_count()
+        ev = Events(dev)
+        t0 = time.perf_counter()
+        ev.start()
+        for _ in range(args.steps):
+            one_step()
+        gpu_ms = ev.stop_ms()
+        dev.sync()
+        wall_r = time.perf_counter() - t0
+        ev.free()
+        run_tokens = [first] + plan.history()[hist0:hist0 + args.steps]
+        if tokens is None:
+            tokens = run_tokens
+        elif run_tokens != tokens:
+            raise RuntimeError(f"bench: timed run {r} decoded other tokens than run 0")
+        runs.append((wall_r, gpu_ms))
+        log(f"timed run {r}: {args.steps} steps, wall {wall_r * 1e3:.2f} ms, events {gpu_ms:.2f} ms")
+    order = sorted(range(len(runs)), key=lambda i: runs[i][0])
+    wall, gpu_ms = runs[order[len(runs) // 2]]
 
-    # the same decode with a host round trip per token (reference replay_token protocol)
+    # the same decode with a host round trip per token (reference replay_token protocol), run
+    # on to the CPU baseline's token count (untimed past --steps)
+    n_cpu = 0 if args.no_cpu_baseline else min(args.cpu_tokens, cfg.max_ctx - len(prompt))
     rewind()
     t1 = time.perf_counter()
     sync_tokens = [first]
-    for _ in range(args.steps):
+    for i in range(max(args.steps, n_cpu)):
+        if i == args.steps:
+            wall_sync = time.perf_counter() - t1
         one_step()
         sync_tokens.append(plan.read_token())
-    wall_sync = time.perf_counter() - t1
-    ev.free()
+    if args.steps >= n_cpu:
+        wall_sync = time.perf_counter() - t1
+    long_tokens = sync_tokens
+    sync_tokens = sync_tokens[:args.steps + 1]
 
     tok_s = args.steps / wall
     step_bytes = cfg.weight_bytes() + sum(
@@ -737,6 +834,10 @@ def main() -> int:
         "decode_step_bytes": int(step_bytes),
         "decode_roofline_frac": round(step_bytes * tok_s / (HBM_PEAK_GBS * 1e9), 4),
         "tokens_consistent": tokens == sync_tokens,
+        "repeats": len(runs),
+        "runs_tok_s": [round(args.steps / w_, 2) for w_, _ in runs],
+        "timing": f"median of {len(runs)} timed runs of {args.steps} graph replays each (wall clock between "
+                  f"device synchronizations), all from the same post-prompt state",
         "launch_mode": "eager" if args.eager else "graph",
         "step_kernels": "per_op" if args.per_op else "fused",
     }
@@ -746,6 +847,11 @@ def main() -> int:
         table = step_kernels(dev, plan, attn_len=len(prompt) + args.steps // 2)
         result["step_kernels"] = table
         result["roofline"] = roofline_of(max(table, key=lambda e: e["share"]))
+        if plan.persistent_len > 0:
+            # the five-launch step the plan takes past the persistent step's length
+            log("five-launch step kernels")
+            result["five_launch_step_kernels"] = step_kernels(dev, plan, attn_len=len(prompt) + args.steps // 2,
+                                                              five=True)
 
     if "gemv" in legs:
         log("GEMV sweep")
@@ -755,12 +861,11 @@ def main() -> int:
         result["c4_attention"] = attention_sweep(dev)
 
     if not args.no_cpu_baseline:
-        n_cpu = min(args.cpu_tokens, args.steps)
         log(f"CPU baseline: oracle over {n_cpu} decode tokens")
         cb, cpu_tokens = cpu_baseline(cfg, w, prompt, n_cpu, kv_dtype == LT_KV_F16,
                                       n_decode_1core=min(args.cpu_tokens_1core, n_cpu))
         result["cpu_baseline"] = cb
-        result["tokens_match_cpu"] = cpu_tokens == tokens[:n_cpu]
+        result["tokens_match_cpu"] = cpu_tokens == long_tokens[:n_cpu]
 
     runner.free()
     if not args.no_sampled and not args.eager:
@@ -777,7 +882,9 @@ def main() -> int:
     if "c5" in legs:
         model.free()
         log("C5 leg")
-        result["c5"] = c5_leg(dev, n_decode=args.c5_decode, eager=args.eager)
+        result["c5"] = c5_leg(dev, n_decode=args.c5_decode, eager=args.eager, cpu=not args.no_cpu_baseline)
+        if result["c5"].get("cpu_baseline") and "cpu_baseline" in result:
+            result["cpu_baseline"]["c5_decode_tok_s"] = result["c5"]["cpu_baseline"]["value"]
     print(json.dumps(result), flush=True)
     return 0
 

@@ -697,15 +697,7 @@ class DecodePlan:
         wsb = int(_lib.raw("lt_decode_step_workspace_size")(cfg.n_layers, E, F, nh, nkv, hd))
         self.step_ws = DevTensor.empty((wsb,), np.uint8, self.dev)
         self.dev.fill(self.step_ws.ptr, 0, wsb)
-        descs = (_StepLayer * cfg.n_layers)()
-        for il, L in enumerate(m.layers):
-            d = descs[il]
-            d.attn_norm, d.wqkv, d.bqkv = L["attn_norm"].ptr, L["wqkv"].t.ptr, (L["bqkv"].ptr if L["bqkv"] is not None else None)
-            d.wo, d.ffn_norm, d.wgu, d.wdown = L["wo"].t.ptr, L["ffn_norm"].ptr, L["wgu_il"].t.ptr, L["wdown"].t.ptr
-            d.kc, d.vc = self.caches[il].k.ptr, self.caches[il].v.ptr
-        raw = np.frombuffer(bytes(descs), np.uint8).copy()
-        self.step_layers = DevTensor.empty((raw.size,), np.uint8, self.dev)
-        self.dev.h2d(self.step_layers.ptr, raw)
+        self.step_layers = self.step_layer_descs()
         self.persistent_len = n
 
     @property
@@ -793,15 +785,10 @@ class DecodePlan:
         the same arithmetic as _enqueue_fused, bit for bit."""
         if self.persistent_len <= 0:
             raise ValueError("the persistent step does not apply to this profile or geometry")
-        cfg, m, p = self.cfg, self.model, self.profile
+        cfg, m = self.cfg, self.model
         h = self.dev.handle
         eps = ctypes.c_float(cfg.norm_eps)
-        gather = not self.host_embed
-        call("lt_decode_step", h, self.step_layers.vp, cfg.n_layers, cfg.n_embd, cfg.n_ff, cfg.n_head,
-             cfg.n_head_kv, cfg.head_dim, eps, ctypes.c_float(self.scale), m.freqs.vp, self.lens.vp, self.max_ctx,
-             p.kv_dtype, m.tok_embd.t.vp if gather else None, self.tok.vp if gather else None, cfg.vocab,
-             None if gather else self.resid_in.vp, self.carry.vp, self.err.vp, self.step_ws.vp,
-             self.step_ws.nbytes)
+        self.enqueue_layers()
         call("lt_q8_gemv_rms_argmax", h, self.carry.vp, m.output_norm.vp, eps, m.output.t.vp, self.logits.vp,
              cfg.vocab, cfg.n_embd, self.tok.vp, *self._hist_args(), self.am_ws.vp, self.am_ws.nbytes)
         self._enqueue_sample_if_on()
@@ -866,6 +853,36 @@ class DecodePlan:
     def four_launch(self) -> bool:
         """The next step (at the current host length) runs four launches per layer."""
         return self.caches[0].length + 1 <= self.four_launch_len
+
+    def enqueue_layers(self, layers: DevTensor | None = None) -> None:
+        """The persistent step's launch alone (every layer; the last one's output row in
+        carry), over the plan's layer descriptors or another array of them (`layers`: same
+        caches and vectors, other weight copies -- the benchmark's rotation)."""
+        cfg, m, p = self.cfg, self.model, self.profile
+        gather = not self.host_embed
+        call("lt_decode_step", self.dev.handle, (layers or self.step_layers).vp, cfg.n_layers, cfg.n_embd,
+             cfg.n_ff, cfg.n_head, cfg.n_head_kv, cfg.head_dim, ctypes.c_float(cfg.norm_eps),
+             ctypes.c_float(self.scale), m.freqs.vp, self.lens.vp, self.max_ctx, p.kv_dtype,
+             m.tok_embd.t.vp if gather else None, self.tok.vp if gather else None, cfg.vocab,
+             None if gather else self.resid_in.vp, self.carry.vp, self.err.vp, self.step_ws.vp,
+             self.step_ws.nbytes)
+
+    def step_layer_descs(self, weights: dict | None = None) -> DevTensor:
+        """A device array of the persistent step's layer descriptors; `weights` maps
+        (layer, name) for name in wqkv, wo, wgu_il, wdown to other device copies of those
+        matrices (the plan's own otherwise)."""
+        descs = (_StepLayer * self.cfg.n_layers)()
+        for il, L in enumerate(self.model.layers):
+            mat = lambda name: (weights or {}).get((il, name), L[name].t).ptr
+            d = descs[il]
+            d.attn_norm, d.bqkv = L["attn_norm"].ptr, (L["bqkv"].ptr if L["bqkv"] is not None else None)
+            d.wqkv, d.wo, d.wgu, d.wdown = mat("wqkv"), mat("wo"), mat("wgu_il"), mat("wdown")
+            d.ffn_norm = L["ffn_norm"].ptr
+            d.kc, d.vc = self.caches[il].k.ptr, self.caches[il].v.ptr
+        raw = np.frombuffer(bytes(descs), np.uint8).copy()
+        t = DevTensor.empty((raw.size,), np.uint8, self.dev)
+        self.dev.h2d(t.ptr, raw)
+        return t
 
     def _enqueue_four(self) -> None:
         """Four launches per layer, the same bits as the five-launch step:
