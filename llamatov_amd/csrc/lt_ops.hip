@@ -52,9 +52,10 @@ __global__ __launch_bounds__(256) void k_silu_mul_quant(const float* __restrict_
 // ---------------------------------------------------------------------------------
 // Elementwise SiLU(g)*u and a + b (k_silu_mul / k_add, bpd/lib/dev_residency.py:545-555):
 // the per-element expressions of the fused kernels, for callers that keep fp32 vectors.
+// y may alias g or u (an in-place update: each thread reads its element before writing it),
+// so none of the three pointers is declared restrict.
 // ---------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_silu_mul(const float* __restrict__ g, const float* __restrict__ u,
-                                                  float* __restrict__ y, int n) {
+__global__ __launch_bounds__(256) void k_silu_mul(const float* g, const float* u, float* y, int n) {
   int i = blockIdx.x * 256 + threadIdx.x;
   if (i < n) y[i] = lt_silu_mul(g[i], u[i]);
 }

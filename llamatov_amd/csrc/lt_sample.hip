@@ -8,7 +8,8 @@
 //   order       candidates rank by logit, larger first, ties to the lower index (the argmax
 //               rule); -0 and +0 tie
 //   top-k       the first k = clamp(top_k, 1, LT_SAMPLE_MAX_K) candidates (k = 1 when
-//               temperature <= 0: greedy)
+//               temperature <= 0 or 1/temperature is not finite: greedy; a non-finite top
+//               logit also draws the top candidate)
 //   weights     e_i = lt_expf((l_i - l_0) * invT), invT = 1 / temperature (fp32, rounded once)
 //   cumulative  c_i = c_{i-1} + e_i, sequential in rank order (c_{-1} = 0)
 //   top-p       n = the smallest i + 1 with c_i >= top_p * c_{k-1} (n = k when top_p >= 1)
@@ -58,7 +59,9 @@ __device__ __forceinline__ float key_logit(uint32_t k) {
 __device__ __forceinline__ int sample_k(const lt_sample_params* P, int V) {
   int k = P->top_k;
   k = k < 1 ? 1 : (k > kSmMaxK ? kSmMaxK : k);
-  if (!(P->temperature > 0.0f)) k = 1;
+  // greedy when the temperature is not positive, or so small that 1/T is not finite (its
+  // weights would be exp(0 * inf) = NaN)
+  if (!(P->temperature > 0.0f) || !__builtin_isfinite(1.0f / P->temperature)) k = 1;
   return k < V ? k : V;
 }
 
@@ -260,7 +263,7 @@ __global__ __launch_bounds__(kSmThreads) void k_sample_final(lt_sample_params* _
   __shared__ __attribute__((aligned(16))) float s_e[kSmMaxK];   // exps in rank order
   __shared__ float s_c[kSmMaxK];                                // their running sums
   const int t = threadIdx.x;
-  const int k = sample_k(P, V);
+  const int kc = sample_k(P, V);   // candidates
   // the chunks' survivor counts (every load at once), then their total M
   int cnts[kSmMaxChunks];
   int M = 0;
@@ -306,7 +309,7 @@ __global__ __launch_bounds__(kSmThreads) void k_sample_final(lt_sample_params* _
       nidx[r] = live[r] ? ~(uint32_t)ws.idx[(size_t)r * kSmMaxK + t] : 0u;   // larger = lower index
     }
     int rem;
-    const uint32_t T = radix_select<kSmMaxChunks>(key, live, k, S, &rem);
+    const uint32_t T = radix_select<kSmMaxChunks>(key, live, kc, S, &rem);
     // keys equal to T: all of them, or (when the tie straddles rank k) the rem lowest indices
     bool eq[kSmMaxChunks];
     int neq = 0;
@@ -331,7 +334,7 @@ __global__ __launch_bounds__(kSmThreads) void k_sample_final(lt_sample_params* _
     }
     int total;
     int o = block_excl_scan(nsel, S, &total);
-    while (P2 < k) P2 <<= 1;
+    while (P2 < kc) P2 <<= 1;
     if (t < P2) s_key[t] = 0ull;
     __syncthreads();
 #pragma unroll
@@ -376,6 +379,9 @@ __global__ __launch_bounds__(kSmThreads) void k_sample_final(lt_sample_params* _
   const float temp = P->temperature;
   const float invT = temp > 0.0f ? 1.0f / temp : 0.0f;
   const float l0 = key_logit((uint32_t)(s_key[0] >> 32));
+  // a non-finite top logit (its differences would be inf - inf) draws greedily: the top
+  // candidate; k below is the weighted count
+  const int k = __builtin_isfinite(l0) ? kc : 1;
   // exps of the k candidates, zeros up to the next multiple of 16 (c + 0 = c: the sum
   // is never -0, as every e >= +0)
   if (t < ((k + 15) & ~15)) {

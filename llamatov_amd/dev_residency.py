@@ -530,25 +530,47 @@ def _engine_weights(w, cfg: ModelConfig) -> dict:
     return out
 
 
+# id(weight dict) -> (the dict itself, its content fingerprint, cfg items, ResidentModel,
+# exact_embedding, embedding rows).  An entry holds its dict, so the id cannot be reused by
+# another dict while cached; a hit also needs the same dict object and the same per-tensor
+# content samples (the reference keys each weight on its own content sample, fact_dispatch.py).
 _MODELS: dict = {}
 
 
+def _fingerprint(w) -> tuple:
+    return tuple((name, _sample_key(np.asarray(_np(w[name])))) for name in sorted(w))
+
+
 def _resident(w, cfg: dict):
-    """(ResidentModel, exact_embedding): the model uploaded once per weight dict.  When every
-    token_embd row round-trips through Q8_0 unchanged (any Q8_0 GGUF), the step gathers its
-    input row on the device; otherwise the fp32 host row is written before each step, as
-    the reference does."""
+    """(ResidentModel, exact_embedding, embedding rows): the model uploaded once per weight
+    dict.  When every token_embd row round-trips through Q8_0 unchanged (any Q8_0 GGUF), the
+    step gathers its input row on the device; otherwise the fp32 host row is written before
+    each step, as the reference does.  A dict whose tensors changed since it was uploaded is
+    uploaded again (the stale model is freed)."""
     E = int(cfg["n_embd"])
+    fp = _fingerprint(w)
+    items = tuple(sorted(cfg.items()))
+    hit = _MODELS.get(id(w))
+    if hit is not None and hit[0] is w and hit[1] == fp and hit[2] == items:
+        return hit[3:]
+    if hit is not None:
+        release_resident(hit[0])
     emb = _embedding_rows(w, E)
-    key = (id(w), len(w), _sample_key(np.asarray(emb[:1], np.float32)), tuple(sorted(cfg.items())))
-    hit = _MODELS.get(key)
-    if hit is None:
-        mc = _engine_cfg(cfg, w)
-        ew = _engine_weights(w, mc)
-        exact = bool(np.array_equal(q8.dequantize_rows(ew["token_embd.weight"], E), np.asarray(emb, np.float32)))
-        hit = (engine.ResidentModel(mc, ew, _dev(), layouts="fused"), exact, emb)
-        _MODELS[key] = hit
-    return hit
+    mc = _engine_cfg(cfg, w)
+    ew = _engine_weights(w, mc)
+    exact = bool(np.array_equal(q8.dequantize_rows(ew["token_embd.weight"], E), np.asarray(emb, np.float32)))
+    entry = (w, fp, items, engine.ResidentModel(mc, ew, _dev(), layouts="fused"), exact, emb)
+    _MODELS[id(w)] = entry
+    return entry[3:]
+
+
+def release_resident(w) -> None:
+    """Free the device model uploaded for weight dict w (a no-op when there is none).  Plans
+    built on it must be freed first."""
+    hit = _MODELS.get(id(w))
+    if hit is not None and hit[0] is w:
+        del _MODELS[id(w)]
+        hit[3].free()
 
 
 def _plan_for(w, cfg, kv_cache, create: bool = True) -> engine.DecodePlan:

@@ -962,12 +962,15 @@ class DecodePlan:
 
     # -- sampling beyond greedy ----------------------------------------------------
     def set_sampling(self, temperature: float | None, top_k: int = 40, top_p: float = 1.0, seed: int = 0,
-                     counter: int = 0) -> None:
+                     counter: int | None = None) -> None:
         """Draw every step's token with lt_sample (temperature, top-k, top-p; Philox stream
         `seed`, starting at draw `counter`) instead of the greedy argmax; temperature=None
-        returns to greedy.  The parameters live on the device: a captured graph reads them at
-        every replay, so new values apply without re-capture; switching between greedy and
-        sampling changes the launch sequence and needs a new capture."""
+        returns to greedy.  counter=None keeps the device's draw count when the plan already
+        has sampling parameters (changing the temperature or the cuts mid-generation does not
+        replay draws already spent), and starts at 0 otherwise.  The parameters live on the
+        device: a captured graph reads them at every replay, so new values apply without
+        re-capture; switching between greedy and sampling changes the launch sequence and
+        needs a new capture."""
         if temperature is None:
             self.sampling = False
             return
@@ -979,6 +982,10 @@ class DecodePlan:
                 raise ValueError(f"lt_sample: vocab {self.cfg.vocab} is outside 1 .. 262144")
             self._sample_params = DevTensor.empty((32,), np.uint8, self.dev)
             self._sample_ws = DevTensor.empty((n,), np.uint8, self.dev)
+            if counter is None:
+                counter = 0
+        elif counter is None:
+            counter = self.sample_counter()
         rec = np.zeros(1, np.dtype([("temperature", "<f4"), ("top_k", "<i4"), ("top_p", "<f4"), ("reserved", "<i4"),
                                     ("seed", "<u8"), ("counter", "<u8")]))
         rec["temperature"], rec["top_k"], rec["top_p"] = temperature, int(top_k), top_p

@@ -89,6 +89,7 @@ def generate(path, input_ids, n_tokens=20, device="cpu", preloaded=None):
             plan = getattr(kv[0], "_plan", None)
             if plan is not None:
                 plan.free()
+            dr.release_resident(w)   # the device copy of this dict's weights
             dr._KV_MAX_SEQ = saved
     else:
         model = engine.ResidentModel.from_gguf(path, max_ctx=max(1024, len(ids) + n_tokens))

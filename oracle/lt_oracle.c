@@ -332,17 +332,19 @@ static int cmp_desc_u64(const void* a, const void* b) {
 }
 
 /* Rank by (logit desc, index asc) with -0 == +0; k = clamp(top_k, 1, 1024) (1 when
- * temperature <= 0), at most V; e_i = lt_expf((l_i - l_0) * (1/T)); c_i sequential;
+ * temperature <= 0 or 1/T is not finite), at most V; the top candidate when its logit is not
+ * finite; e_i = lt_expf((l_i - l_0) * (1/T)); c_i sequential;
  * n = smallest count with c_{n-1} >= top_p * c_{k-1} (k when top_p >= 1);
  * u = (philox4x32_10({counter, 0}, seed).x >> 8) * 2^-24; first i < n with c_i > u*c_{n-1}. */
 OR_API int or_sample(const float* logits, int V, float temperature, int top_k, float top_p, uint64_t seed,
                      uint64_t counter) {
   int k = top_k < 1 ? 1 : (top_k > 1024 ? 1024 : top_k);
-  if (!(temperature > 0.0f)) k = 1;
+  if (!(temperature > 0.0f) || !isfinite(1.0f / temperature)) k = 1;
   if (k > V) k = V;
   uint64_t* key = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
   for (int i = 0; i < V; i++) key[i] = ((uint64_t)sample_order_key(logits[i]) << 32) | (uint32_t)~(uint32_t)i;
   qsort(key, (size_t)V, sizeof(uint64_t), cmp_desc_u64);
+  if (!isfinite(logits[~(uint32_t)key[0]])) k = 1;
   int pick = 0;
   if (k > 1) {
     float invT = 1.0f / temperature;

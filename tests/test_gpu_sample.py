@@ -68,6 +68,32 @@ def test_sample_matches_oracle(gpu, oracle, V):
     assert 0 <= h.min() and h.max() < V
 
 
+@pytest.mark.parametrize("V", [1000, 151936])
+def test_sample_non_finite_weights_draw_the_argmax(gpu, oracle, V):
+    """A temperature whose reciprocal overflows (1e-39) and a +inf top logit both draw the
+    argmax on the device, as in the oracle (their weights would otherwise all be NaN)."""
+    rng = np.random.default_rng(V + 1)
+    ws_n = _lib.raw("lt_sample_workspace_size")(V)
+    ws = dr.DevTensor.empty((ws_n,), np.uint8, gpu)
+    tok = dr.DevTensor.empty((1,), np.int32, gpu)
+    par = dr.DevTensor.empty((32,), np.uint8, gpu)
+    l = (rng.standard_normal(V) * 3).astype(np.float32)
+    l[[5, V - 3]] = l.max() + 2.0
+    li = l.copy()
+    li[[V // 2, V - 1]] = np.inf
+    for logits, T, k, p in ((l, 1e-39, 40, 0.9), (l, 2.0e-39, 1024, 1.0), (li, 0.8, 40, 0.95), (li, 1.0, 1, 1.0)):
+        dl = dr.DevTensor.from_host(logits, gpu)
+        for c in range(3):
+            case(f"sample non-finite V={V} T={T} k={k} counter={c}")
+            gpu.h2d(par.ptr, params(T, k, p, 7, c))
+            call("lt_sample", gpu.handle, dl.vp, V, par.vp, tok.vp, None, None, 0, ws.vp, ws_n)
+            got = int(tok.to_host()[0])
+            assert got == oracle.sample(logits, T, k, p, 7, c) == oracle.argmax(logits)
+        dl.free()
+    for t in (ws, tok, par):
+        t.free()
+
+
 def test_sample_refusals(gpu):
     case("sample refusals")
     f = _lib.raw("lt_sample")
@@ -147,6 +173,16 @@ def test_sampling_parameters_change_between_replays(gpu, oracle):
             t = oracle.sample(lg, T, k, p, seed, c0 + i)
             assert t_dev == t
         assert plan.sample_counter() == c0 + 4
+    # new parameters without a counter continue the device's draw count (4 after the last
+    # setting), so no draw already spent is replayed
+    plan.set_sampling(0.9, top_k=10, top_p=1.0, seed=9)
+    assert plan.sample_counter() == 4
+    for i in range(3):
+        lg = orc.step(t)
+        t_dev = gr.replay_token()
+        t = oracle.sample(lg, 0.9, 10, 1.0, 9, 4 + i)
+        assert t_dev == t
+    assert plan.sample_counter() == 7
     plan.set_sampling(None)
     with pytest.raises(RuntimeError):
         gr.replay_token()

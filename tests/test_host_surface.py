@@ -106,3 +106,37 @@ def test_load_model_orientation(tmp_path):
     assert emb.shape == (cfg.n_embd, cfg.vocab)
     ew = dr._engine_weights(w, dr._engine_cfg(c, w))
     assert np.array_equal(ew["token_embd.weight"], qw["token_embd.weight"])
+
+
+def test_resident_cache_keys_on_the_dict_and_its_content(monkeypatch):
+    """Two weight dicts that share token_embd but differ in one layer weight get separate
+    device models; the same unchanged dict hits; a dict whose tensor was replaced is uploaded
+    again (the stale model freed); release_resident frees and forgets.  (No GPU: the upload is
+    replaced by a recorder.)"""
+    built = []
+
+    class Recorder:
+        def __init__(self, mc, ew, dev, layouts):
+            self.freed = False
+            built.append(self)
+
+        def free(self):
+            self.freed = True
+
+    monkeypatch.setattr(dr.engine, "ResidentModel", Recorder)
+    monkeypatch.setattr(dr, "_dev", lambda: None)
+    monkeypatch.setattr(dr, "_MODELS", {})
+    cfg = M.TINY
+    w1 = reference_w(cfg, M.synth_weights(cfg, seed=3))
+    w2 = dict(w1)   # the same arrays, token_embd included
+    w2["blk.1.ffn_down.weight"] = (w1["blk.1.ffn_down.weight"] * np.float32(1.5)).astype(np.float32)
+    m1 = dr._resident(w1, cfg.as_cfg())[0]
+    m2 = dr._resident(w2, cfg.as_cfg())[0]
+    assert m1 is not m2 and len(built) == 2
+    assert dr._resident(w1, cfg.as_cfg())[0] is m1 and len(built) == 2
+    w1["blk.0.attn_q.weight"] = (w1["blk.0.attn_q.weight"] + np.float32(0.01)).astype(np.float32)
+    m1b = dr._resident(w1, cfg.as_cfg())[0]
+    assert m1b is not m1 and m1.freed and not m1b.freed
+    dr.release_resident(w1)
+    dr.release_resident(w2)
+    assert m1b.freed and m2.freed and not dr._MODELS

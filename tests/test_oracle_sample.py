@@ -35,6 +35,22 @@ def test_greedy_special_cases():
     assert oracle.sample(z2, 0.0, 10, 1.0, 0, 0) == 1
 
 
+def test_non_finite_weights_draw_the_argmax():
+    """A temperature so small that 1/T overflows, and a +inf top logit, would make every weight
+    exp(0 * inf) or exp(inf - inf) = NaN: both draw greedily (the argmax, lowest index)."""
+    rng = np.random.default_rng(4)
+    l = rng.standard_normal(5000).astype(np.float32)
+    l[[33, 700]] = 7.5
+    assert np.isinf(np.float32(1.0) / np.float32(1e-39))
+    for c in range(10):
+        assert oracle.sample(l, 1e-39, 40, 0.9, 3, c) == 33
+        assert oracle.sample(l, np.float32(2.0e-39), 1024, 1.0, 3, c) == 33
+    li = l.copy()
+    li[[91, 4000]] = np.inf
+    for c in range(10):
+        assert oracle.sample(li, 0.8, 40, 0.95, 3, c) == 91
+
+
 def test_candidates_are_the_ranked_top_k():
     rng = np.random.default_rng(2)
     l = np.round(rng.standard_normal(3000), 1).astype(np.float32)   # many ties
