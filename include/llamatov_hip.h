@@ -75,7 +75,7 @@ LT_API int lt_quant_q8(lt_ctx* ctx, const float* x, int8_t* xq, uint16_t* xd, in
 LT_API int lt_silu_mul_quant(lt_ctx* ctx, const float* g, const float* u, int8_t* xq, uint16_t* xd, int K);
 
 /* k_silu_mul (bpd/lib/dev_residency.py:545-551, silu_mul_dev :632-637):
- * y = (g/(1+exp(-g)))*u elementwise, n elements. */
+ * y = (g/(1+exp(-g)))*u elementwise, n elements; y may be g or u (in place). */
 LT_API int lt_silu_mul(lt_ctx* ctx, const float* g, const float* u, float* y, int n);
 
 /* k_add (bpd/lib/dev_residency.py:552-555, add_dev :639-642): y = a + b elementwise. */
@@ -142,8 +142,10 @@ LT_API size_t lt_attn_workspace_size(int batch, int nh, int hd, int nsplit);
  * tight serving loops, harnesses that forbid hipMalloc).  The split-K partials live in a
  * file-scope device array of 16 MiB (one per GPU, held until the process ends), so
  * lt_attn_workspace_size(batch, nh, hd, nsplit) must be at most 16 MiB (else LT_EINVAL, nothing
- * launched).  Same results as lt_attn_decode, bit for bit.  Calls that overlap on one GPU
- * (from two contexts' streams) share the array and race; calls on one context are ordered. */
+ * launched).  Same results as lt_attn_decode, bit for bit.  The array is per GPU, so one
+ * context per GPU may use it: the first call that needs it (nsplit > 1) claims it for its
+ * context, a call from another context on that GPU is refused with LT_ESTATE (the two streams
+ * would race on it), and lt_free_ctx releases it.  Calls on one context are stream-ordered. */
 LT_API int lt_attn_decode_noalloc(lt_ctx* ctx, const float* q, const void* kc, const void* vc, const int* len,
                                   float* out, int batch, int nh, int nkv, int hd, float scale, int maxt,
                                   int nsplit, int kv_dtype);
@@ -484,7 +486,8 @@ LT_API int lt_qmatmul_q8_0_llamafile(lt_ctx* ctx, const void* W, const float* X,
  * 1795-1818) is the k = 1 case, planned there to extend to top-k/top-p/temperature; there is
  * no reference signature.  Semantics (exact, reproduced by the CPU restatement): candidates
  * ranked by logit (ties to the lower index, -0 == +0); the first k = clamp(top_k, 1,
- * LT_SAMPLE_MAX_K) of them (k = 1 when temperature <= 0); e_i = exp((l_i - l_0) / T) with the
+ * LT_SAMPLE_MAX_K) of them (k = 1 when temperature <= 0 or 1/temperature is not finite, and
+ * the top candidate drawn when its logit is not finite); e_i = exp((l_i - l_0) / T) with the
  * division as one multiply by the fp32 reciprocal; c_i the sequential cumulative sum; n the
  * smallest count with c_{n-1} >= top_p * c_{k-1} (all k when top_p >= 1); u from
  * Philox4x32-10 (counter {counter, 0}, key seed): u = (x0 >> 8) * 2^-24; the token is the

@@ -31,6 +31,8 @@
 
 #include "lt_q8_device.h"
 
+#include <mutex>
+
 namespace {
 
 using namespace lt;
@@ -1759,6 +1761,35 @@ void lt_attn_scratch_bind(lt_ctx* ctx) {
   ctx->attn_scratch_bytes = e == hipSuccess ? kAttnScratchBytes : 0;
 }
 
+// One context per GPU may use the scratch: the first whose call needs it claims it, later
+// contexts on that GPU are refused (their streams are not ordered with the owner's, so their
+// calls would race on the one array), and lt_free_ctx gives it back.
+namespace {
+constexpr int kScratchMaxDevices = 64;
+std::mutex g_scratch_mu;
+lt_ctx* g_scratch_owner[kScratchMaxDevices] = {};
+}  // namespace
+
+static int claim_scratch(lt_ctx* ctx) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (ctx->device < 0 || ctx->device >= kScratchMaxDevices)
+    return lt_fail(LT_ESTATE, "lt_attn_decode_noalloc: device %d has no scratch slot", ctx->device);
+  lt_ctx*& owner = g_scratch_owner[ctx->device];
+  if (!owner) owner = ctx;
+  if (owner != ctx)
+    return lt_fail(LT_ESTATE,
+                   "lt_attn_decode_noalloc: device %d's scratch belongs to another context (calls from two "
+                   "contexts would race on it); free that context first, or call lt_attn_decode with a workspace",
+                   ctx->device);
+  return LT_OK;
+}
+
+void lt_attn_scratch_release(lt_ctx* ctx) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (ctx->device >= 0 && ctx->device < kScratchMaxDevices && g_scratch_owner[ctx->device] == ctx)
+    g_scratch_owner[ctx->device] = nullptr;
+}
+
 extern "C" {
 
 size_t lt_attn_workspace_size(int batch, int nh, int hd, int nsplit) {
@@ -1827,6 +1858,7 @@ int lt_attn_decode_noalloc(lt_ctx* ctx, const float* q, const void* kc, const vo
                      "lt_attn_decode_noalloc: batch=%d nh=%d hd=%d nsplit=%d needs %zu bytes of split partials, "
                      "more than the %zu-byte device scratch; lower nsplit or batch, or call lt_attn_decode "
                      "with a workspace", batch, nh, hd, nsplit, need, ctx->attn_scratch_bytes);
+    if (int rc = claim_scratch(ctx)) return rc;
   }
   AttnArgs A = {};
   A.q = q; A.q_stride = nh * hd; A.kc = (void*)kc; A.vc = (void*)vc; A.len = len; A.out = out;

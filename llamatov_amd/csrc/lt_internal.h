@@ -24,6 +24,8 @@ struct lt_ctx {
 // must be current).  Never fails the caller: a failed lookup is kept in attn_scratch_err and
 // reported by the entry point that needs the scratch.
 void lt_attn_scratch_bind(lt_ctx* ctx);
+// Gives the scratch back when ctx owns it (lt_free_ctx).
+void lt_attn_scratch_release(lt_ctx* ctx);
 
 int lt_fail(int code, const char* fmt, ...);
 int lt_fail_hip(hipError_t e, const char* what, const char* file, int line);

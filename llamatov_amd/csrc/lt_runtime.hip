@@ -74,6 +74,7 @@ int lt_free_ctx(lt_ctx* ctx) {
   LT_CHECK(hipSetDevice(ctx->device));
   LT_CHECK(hipStreamSynchronize(ctx->stream));
   LT_CHECK(hipStreamDestroy(ctx->stream));
+  lt_attn_scratch_release(ctx);
   delete ctx;
   return LT_OK;
 }

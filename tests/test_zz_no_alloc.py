@@ -80,3 +80,41 @@ def test_noalloc_refuses_more_than_its_scratch(gpu):
                                             ctypes.c_float(1.0), L, nsplit, LT_KV_F16)
     assert rc == -1 and "scratch" in _lib.last_error()
     assert np.all(out.to_host().view(np.uint32) == 0x7F7F7F7F)   # nothing launched
+
+
+def test_noalloc_refuses_a_second_context(gpu):
+    """The scratch is one array per GPU: once a context has used it, a call from another
+    context on that GPU is refused (LT_ESTATE, nothing launched), a call that needs no
+    scratch (nsplit 1) still runs there, and the owner keeps working."""
+    rng = np.random.default_rng(7)
+    shape = (2, 300, 14, 2, 64, 4, LT_KV_F16)
+    case("noalloc owner claims the scratch")
+    r, g, *_ = run_pair(gpu, rng, *shape)
+    assert np.array_equal(r.view(np.uint32), g.view(np.uint32))
+    other = ctypes.c_void_p()
+    call("lt_init", gpu.index, ctypes.byref(other))
+    try:
+        case("noalloc second context refused")
+        B, L, nh, nkv, hd, nsplit, kvd = shape
+        k = up(np.zeros((B, L, nkv * hd), np.uint16))
+        q = up(rng.standard_normal((B, nh * hd), dtype=np.float32))
+        lens = up(np.full(B, L, np.int32))
+        out = dr.DevTensor.empty((B, nh * hd), np.float32)
+        gpu.fill(out.ptr, 0x7F, out.nbytes)
+        fn = _lib.raw("lt_attn_decode_noalloc")
+        rc = fn(other, q.vp, k.vp, k.vp, lens.vp, out.vp, B, nh, nkv, hd, ctypes.c_float(0.125), L, nsplit, kvd)
+        assert rc == -2 and "another context" in _lib.last_error()
+        gpu.sync()
+        assert np.all(out.to_host().view(np.uint32) == 0x7F7F7F7F)
+        case("noalloc second context, nsplit 1")
+        rc = fn(other, q.vp, k.vp, k.vp, lens.vp, out.vp, B, nh, nkv, hd, ctypes.c_float(0.125), L, 1, kvd)
+        assert rc == 0
+        call("lt_sync", other)
+        assert np.all(out.to_host() == 0.0)    # zero K and V rows give zero outputs
+        for t in (k, q, lens, out):
+            t.free()
+    finally:
+        call("lt_free_ctx", other)
+    case("noalloc owner after the refusal")
+    r, g, *_ = run_pair(gpu, rng, 1, 100, 14, 2, 64, 3, LT_KV_F32)
+    assert np.array_equal(r.view(np.uint32), g.view(np.uint32))
