@@ -577,9 +577,11 @@ def gguf_arch(cfg: ModelConfig) -> str:
     return "qwen2" if cfg.qkv_bias else "llama"
 
 
-def save_q8_model(path, cfg: ModelConfig, weights: dict, alignment: int = DEFAULT_ALIGNMENT) -> None:
+def save_q8_model(path, cfg: ModelConfig, weights: dict, alignment: int = DEFAULT_ALIGNMENT,
+                  metadata: dict | None = None) -> None:
     """Write a ModelConfig and its GGUF-named tensors (Q8_0 blocks, float32 vectors) as a GGUF
-    file that load_q8_model reads back to the same configuration and bytes."""
+    file that load_q8_model reads back to the same configuration and bytes.  `metadata` adds
+    keys (write_gguf's value forms), e.g. tokenizer.ggml.tokens."""
     arch = gguf_arch(cfg)
     md = {
         "general.architecture": arch,
@@ -594,6 +596,7 @@ def save_q8_model(path, cfg: ModelConfig, weights: dict, alignment: int = DEFAUL
         f"{arch}.rope.freq_base": (GGUF_FLOAT32, cfg.rope_theta),
         f"{arch}.attention.layer_norm_rms_epsilon": (GGUF_FLOAT32, cfg.norm_eps),
     }
+    md.update(metadata or {})
     tensors = []
     for tname, kind, shape in weight_specs(cfg):
         a = weights[tname]

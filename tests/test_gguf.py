@@ -309,6 +309,32 @@ def test_model_write_read_roundtrip(tmp_path, cfg):
         reader.close()
 
 
+def test_model_file_carries_extra_metadata(tmp_path):
+    """save_q8_model's extra keys (a tokenizer's token strings and BOS id) read back through
+    parse_gguf, where llamatov_gpu_resident's command line looks them up."""
+    cfg = M.TINY
+    toks = [f"t{i}" for i in range(cfg.vocab)]
+    toks[17] = "Hello"
+    p = tmp_path / "m.gguf"
+    G.save_q8_model(p, cfg, M.synth_weights(cfg, seed=5), metadata={
+        "tokenizer.ggml.tokens": (G.GGUF_ARRAY, G.GGUF_STRING, toks),
+        "tokenizer.ggml.bos_token_id": (G.GGUF_UINT32, 3)})
+    md, ts, _ = G.parse_gguf(p)
+    assert md["tokenizer.ggml.tokens"] == toks and md["tokenizer.ggml.bos_token_id"] == 3
+    assert len(ts) == len(M.weight_specs(cfg))
+
+
+def test_gpu_resident_run_signature():
+    """The reference's run(path, input_ids, n_tokens=10) signature (llamatov_gpu_resident.py:20);
+    without arguments its command line prints its usage instead of loading anything."""
+    import inspect
+    from llamatov_amd import llamatov_gpu_resident as R
+    sig = inspect.signature(R.run)
+    assert list(sig.parameters) == ["path", "input_ids", "n_tokens"]
+    assert sig.parameters["n_tokens"].default == 10
+    assert R.main([]) == 2
+
+
 def test_loader_requantizes_other_types(tmp_path):
     cfg = M.TINY
     w = M.synth_weights(cfg, seed=3)

@@ -7,8 +7,9 @@ hidden 4096, FFN 14336, 32 Q / 8 KV heads, head_dim 128, vocab 128256, untied he
   single-token device path fed the 512 tokens one at a time -- the reference's
   device-uniformity requirement for a batched prefill (bpd/lib/dev_residency.py:1344-1350).
 * 256 greedy decode tokens by graph replay equal 256 eager steps (the reference's GR gate).
-* A truncated model (2 layers at the full 4096 / 14336 widths, the untied 128256 x 4096
-  head) matches the CPU oracle token by token.
+* The full 32-layer model matches the CPU oracle in the logits, bit for bit, over a short
+  prompt and 4 greedy graph replays; a truncated model (2 layers at the full widths, the
+  untied 128256 x 4096 head) does so over a longer continuation.
 """
 import numpy as np
 import pytest
@@ -32,11 +33,14 @@ def bits(a):
 
 
 @pytest.fixture(scope="module")
-def c5_model(gpu):
+def c5_weights():
     case("C5 weights")
-    w = M.synth_weights(M.LLAMA3_8B, seed=4321)
-    m = dr.ResidentModel(M.LLAMA3_8B, w, gpu, layouts="fused")
-    del w
+    return M.synth_weights(M.LLAMA3_8B, seed=4321)
+
+
+@pytest.fixture(scope="module")
+def c5_model(gpu, c5_weights):
+    m = dr.ResidentModel(M.LLAMA3_8B, c5_weights, gpu, layouts="fused")
     yield m
     m.free()
 
@@ -90,6 +94,37 @@ def test_c5_graph_replay_equals_eager_256(gpu, c5_model):
     assert np.array_equal(bits(plan.read_logits()), bits(lg))
     for key, rows in _kv(plan, N_PREFILL + N_DECODE - 1, (0, 15, 31)).items():
         assert np.array_equal(rows, kv_g[key]), key
+    gr.free()
+    plan.free()
+
+
+def test_c5_full_depth_matches_oracle(gpu, oracle, c5_model, c5_weights):
+    """All 32 layers against the oracle: the last prompt position's logits after the batched
+    prefill and the logits of 4 greedy graph replays, bit for bit, and the greedy tokens."""
+    cfg = M.LLAMA3_8B
+    case("C5 32-layer oracle")
+    orc = oracle.OracleModel(cfg, c5_weights, kv_f16=True, attn_nsplit=C5_NSPLIT, max_ctx=64)
+    prompt = M.random_prompt(cfg, 6, seed=23)
+    for t in prompt:
+        exp = orc.step(t)
+    plan = dr.DecodePlan(c5_model, dr.Profile(kv_dtype=LT_KV_F16, attn_nsplit=C5_NSPLIT), max_ctx=64)
+    case("C5 32-layer prefill + 4 replays")
+    dr.forward_prefill(plan, prompt)
+    assert np.array_equal(bits(plan.read_logits()), bits(exp))
+    got, want = [plan.read_token()], [oracle.argmax(exp)]
+    gr = dr.StepGraph(plan)
+    gr.capture()
+    for i in range(4):
+        exp = orc.step(want[-1])
+        lg = gr.replay_logits(got[-1])
+        assert np.array_equal(bits(lg), bits(exp)), f"replay {i}: max |d| {np.abs(lg - exp).max()}"
+        got.append(plan.read_token())
+        want.append(oracle.argmax(exp))
+    assert got == want
+    for il in (0, 31):
+        for which in "kv":
+            assert np.array_equal(plan.caches[il].rows_host(which, len(prompt) + 4),
+                                  orc.kv_rows(il, which, len(prompt) + 4)), (il, which)
     gr.free()
     plan.free()
 

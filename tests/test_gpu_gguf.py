@@ -77,6 +77,46 @@ def test_generate_from_path(gpu, oracle, tiny_file, kv_dtype, batched):
     assert got == exp
 
 
+def test_gpu_resident_run_and_command_line(gpu, oracle, tmp_path, capsys):
+    """llamatov_gpu_resident.run(path, input_ids, n_tokens): the prompt's greedy continuation
+    and n_tokens more (n_tokens + 1 new tokens, as the reference's loop decodes), equal to the
+    oracle's; its command line decodes [BOS, 'Hello'] from the file's tokenizer metadata."""
+    from llamatov_amd import llamatov_gpu_resident as R
+    cfg = M.TINY
+    w = M.synth_weights(cfg, seed=99)
+    vocab = [f"t{i}" for i in range(cfg.vocab)]
+    vocab[17] = "Hello"
+    path = tmp_path / "tiny_tok.gguf"
+    G.save_q8_model(path, cfg, w, metadata={
+        "tokenizer.ggml.tokens": (G.GGUF_ARRAY, G.GGUF_STRING, vocab),
+        "tokenizer.ggml.bos_token_id": (G.GGUF_UINT32, 3)})
+    orc = oracle.OracleModel(cfg, w)
+
+    def greedy(prompt, n):
+        for t in prompt:
+            logits = orc.step(t)
+        out = []
+        for _ in range(n):
+            out.append(oracle.argmax(logits))
+            logits = orc.step(out[-1])
+        return out
+
+    case("llamatov_gpu_resident.run tiny")
+    prompt = M.random_prompt(cfg, 6, seed=8)
+    got = R.run(str(path), prompt, 12)
+    assert got == prompt + greedy(prompt, 13)
+    printed = capsys.readouterr().out
+    assert "Prefill → first token" in printed and "Throughput" in printed
+    case("llamatov_gpu_resident command line")
+    orc.reset()
+    assert R.main([str(path), "5"]) == 0
+    printed = capsys.readouterr().out
+    assert "BOS=3, Hello=17" in printed
+    exp = greedy([3, 17], 6)
+    assert f"Prefill → first token: {exp[0]} = {vocab[exp[0]]!r}" in printed
+    assert f"Step 4: token {exp[5]} = {vocab[exp[5]]!r}" in printed
+
+
 def test_known_answer_qwen25_05b(gpu):
     path = os.environ.get("LLAMATOV_QWEN25_05B_GGUF")
     if not path or not os.path.exists(path):
