@@ -317,22 +317,44 @@ def gemv_sweep(dev, launches: int = 40) -> list[dict]:
         xq = dr.DevTensor.from_host(rng.integers(-127, 128, K, dtype=np.int64).astype(np.int8), dev)
         xd = dr.DevTensor.from_host((rng.standard_normal(nb) * 0.05).astype(np.float16).view(np.uint16), dev)
         y = dr.DevTensor.empty((N,), np.float32, dev)
-        for i in range(copies):
-            call("lt_q8_gemv", dev.handle, ws[i].vp, xq.vp, xd.vp, None, y.vp, N, K)
-        dev.sync()
-        ev = Events(dev)
-        ev.start()
-        for i in range(launches):
-            call("lt_q8_gemv", dev.handle, ws[i % copies].vp, xq.vp, xd.vp, None, y.vp, N, K)
-        ms = ev.stop_ms()
-        ev.free()
+
+        def timed(fn, mats):
+            for i in range(copies):
+                call(fn, dev.handle, mats[i].vp, xq.vp, xd.vp, None, y.vp, N, K)
+            dev.sync()
+            ev = Events(dev)
+            ev.start()
+            for i in range(launches):
+                call(fn, dev.handle, mats[i % copies].vp, xq.vp, xd.vp, None, y.vp, N, K)
+            ms = ev.stop_ms()
+            ev.free()
+            return ms / 1e3 / launches
+        alg = N * nb * 34 + K + 2 * nb + 4 * N
+        avg_b = timed("lt_q8_gemv", ws)
+        row = {"shape": f"{name} {N}x{K}"}
+        if K % 1024 == 0:
+            # the decode path streams planar copies of such matrices (lt_q8_to_planar): the
+            # figure is lt_q8_gemv_pl's, the GGUF-block kernel's beside it
+            pls = []
+            for t in ws:
+                p = dr.DevTensor.empty((t.nbytes,), np.uint8, dev)
+                call("lt_q8_to_planar", dev.handle, t.vp, p.vp, N, K)
+                pls.append(p)
+            avg = timed("lt_q8_gemv_pl", pls)
+            for t in pls:
+                t.free()
+            row["layout"] = "planar"
+            row["blocks_us"] = round(avg_b * 1e6, 2)
+        else:
+            avg = avg_b
+            row["layout"] = "blocks"
         for t in ws + [xq, xd, y]:
             t.free()
-        avg = ms / 1e3 / launches
-        alg = N * nb * 34 + K + 2 * nb + 4 * N
-        out.append({"shape": f"{name} {N}x{K}", "us": round(avg * 1e6, 2), "GB/s": round(alg / avg / 1e9, 1),
+        row.update({"us": round(avg * 1e6, 2), "GB/s": round(alg / avg / 1e9, 1),
                     "frac": round(alg / avg / 1e9 / HBM_PEAK_GBS, 4)})
-        log(f"gemv {name} {N}x{K}: {avg * 1e6:.2f} us, {alg / avg / 1e9:.0f} GB/s")
+        out.append(row)
+        log(f"gemv {name} {N}x{K} ({row['layout']}): {avg * 1e6:.2f} us, {alg / avg / 1e9:.0f} GB/s"
+            + (f" (blocks {avg_b * 1e6:.2f} us)" if K % 1024 == 0 else ""))
     return out
 
 

@@ -301,6 +301,31 @@ LT_API int lt_q8_gemv_rms_argmax(lt_ctx* ctx, const float* x, const float* nw, f
                                  void* ws, size_t ws_bytes);
 LT_API size_t lt_q8_gemv_argmax_workspace_size(int N);
 
+/* ---- the planar weight layout (no counterpart in the reference, whose GEMVs read GGUF
+ * blocks; a residency choice of this library for matrices with K % 1024 == 0) -------------
+ * lt_q8_to_planar repacks a Q8_0 matrix [N][K/32] of 34-byte blocks into dst (the same
+ * N*K/32*34 bytes, 16-byte aligned, not overlapping src): per row and 32-block group, the
+ * leading 16 quants of the 32 blocks, then their trailing 16 (1024 bytes), and after all N
+ * rows the fp16 scales [N][K/32].  Every load instruction of a GEMV over it reads whole,
+ * aligned cache lines.  The *_pl entry points are their namesakes above over such a copy
+ * (W or Wgu planar; K % 1024 == 0, else LT_EINVAL): the same arguments, arithmetic and bits. */
+LT_API int lt_q8_to_planar(lt_ctx* ctx, const void* src, void* dst, int N, int K);
+LT_API int lt_q8_gemv_pl(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd, const float* resid,
+                         float* y, int N, int K);
+LT_API int lt_q8_gemv_rms_pl(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* W,
+                             const float* resid, float* y, int N, int K);
+LT_API int lt_q8_gemv_embed_rms_pl(lt_ctx* ctx, const void* emb, const int* tok, int vocab, float* x_out, int* err,
+                                   const float* nw, float eps, const void* W, const float* resid, float* y, int N,
+                                   int K);
+LT_API int lt_q8_gemv_attn_out_pl(lt_ctx* ctx, const int8_t* xq, const uint16_t* xd, const void* ws,
+                                  size_t ws_bytes, int nsplit, int nh, int hd, const void* W, const float* resid,
+                                  float* y, int N, int K, int* len, int maxt);
+LT_API int lt_q8_gemv_rms_silu_pl(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* Wgu,
+                                  int8_t* vq, uint16_t* vd, int F, int K);
+LT_API int lt_q8_gemv_rms_argmax_pl(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* W,
+                                    float* logits, int N, int K, int* out, int* hist, int* count, int cap,
+                                    void* ws, size_t ws_bytes);
+
 /* RoPE(q, k) -> KV append -> decode attention for one token of one sequence
  * (rope_dev_qk_fused + DeviceKVCache.append_at_len_incr + attn_decode_from_cache_masked,
  * bpd/lib/dev_residency.py:1396-1425).  qkv = [q (nh*hd) | k (nkv*hd) | v (nkv*hd)] before

@@ -88,6 +88,7 @@ _SIGS = {
     "lt_q8_gemv_rms_argmax": (c_int, [_P, _P, _P, c_float, _P, _P, c_int, c_int, _P, _P, _P, c_int,
                                       _P, c_size_t]),
     "lt_q8_gemv_argmax_workspace_size": (c_size_t, [c_int]),
+    "lt_q8_to_planar": (c_int, [_P, _P, _P, c_int, c_int]),
     "lt_decode_step_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "lt_decode_step_max_len": (c_int, [_P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
     "lt_decode_step": (c_int, [_P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_float, _P, _P, c_int,
@@ -120,6 +121,10 @@ _SIGS = {
     "lt_event_elapsed_ms": (c_int, [_P, _P, POINTER(c_float)]),
     "lt_event_destroy": (c_int, [_P]),
 }
+# the planar-layout twins take their namesakes' arguments
+for _n in ("lt_q8_gemv", "lt_q8_gemv_rms", "lt_q8_gemv_embed_rms", "lt_q8_gemv_attn_out", "lt_q8_gemv_rms_silu",
+           "lt_q8_gemv_rms_argmax"):
+    _SIGS[_n + "_pl"] = _SIGS[_n]
 
 
 class LtError(RuntimeError):

@@ -65,6 +65,7 @@ struct GemvParams {
   void* vc;
   const int* lenr;
   int nkv, kv_f16;
+  int planar;              // W is in the planar layout (lt_q8_to_planar; K % 1024 == 0)
   int* len_bump;           // any PRO but PRO_MERGE: block 0 bumps *len_bump (when < maxt) at its end
 };
 
@@ -338,8 +339,11 @@ constexpr uint32_t kNoBlock = 0x80000000u;
 constexpr int kStgRows = 64;
 constexpr int kStgLoads = (kStgRows * 32 * (int)kBlockBytes + 4095) / 4096;   // 17
 constexpr uint32_t kStgBytes = (uint32_t)kStgLoads * 4096u + 16u;   // + the last block's 9th dword
+// Planar weights (kPL, K % 1024 == 0, lt_q8_to_planar): the same ring and item order, each
+// item read as two coalesced non-temporal 16-byte loads per lane plus its scale (lt_q8_device.h,
+// fold_planar); every other stage is unchanged.
 
-template <int KS, Pro PRO, Epi EPI, int D, bool kStg = false>
+template <int KS, Pro PRO, Epi EPI, int D, bool kStg = false, bool kPL = false>
 __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int K = P.K;
@@ -412,17 +416,30 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
   RawBlock ring[D];
   int is = 0, ik = 0;                                                   // next item to issue
   uint32_t issue_row = (uint32_t)rbase * (uint32_t)nb * (uint32_t)kBlockBytes;
+  // planar: the item index row*nk + slot, and the scale plane after the N*nb*32 quant bytes
+  uint32_t issue_item = (uint32_t)rbase * (uint32_t)nk;
+  const uint32_t scale_base = (uint32_t)P.N * (uint32_t)nb * 32u;
   auto issue = [&](RawBlock& r) {
     const bool real = is < total && lane + 32 * ik < nb;
-    const uint32_t off = real ? issue_row + lane_bytes + (uint32_t)ik * kSlotBytes : kNoBlock;
-    const uint32_t o4 = off & ~3u;
-    const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)o4, 0, 0);
-    const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)(o4 + 16u), 0, 0);
-    r.w[0] = v0.x; r.w[1] = v0.y; r.w[2] = v0.z; r.w[3] = v0.w;
-    r.w[4] = v1.x; r.w[5] = v1.y; r.w[6] = v1.z; r.w[7] = v1.w;
-    r.w[8] = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)(o4 + 32u), 0, 0);
+    if constexpr (kPL) {
+      const uint32_t qo = real ? (issue_item + (uint32_t)ik) * kPlanarItemBytes + (uint32_t)lane * 16u : kNoBlock;
+      const uint32_t so = real ? scale_base + ((issue_item + (uint32_t)ik) * 32u + (uint32_t)lane) * 2u : kNoBlock;
+      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)qo, 0, 2);
+      const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)(qo + kPlanarItemBytes / 2u), 0, 2);
+      r.w[0] = v0.x; r.w[1] = v0.y; r.w[2] = v0.z; r.w[3] = v0.w;
+      r.w[4] = v1.x; r.w[5] = v1.y; r.w[6] = v1.z; r.w[7] = v1.w;
+      r.w[8] = __builtin_amdgcn_raw_buffer_load_b16(wrsrc, (int)so, 0, 2);
+    } else {
+      const uint32_t off = real ? issue_row + lane_bytes + (uint32_t)ik * kSlotBytes : kNoBlock;
+      const uint32_t o4 = off & ~3u;
+      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)o4, 0, 0);
+      const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)(o4 + 16u), 0, 0);
+      r.w[0] = v0.x; r.w[1] = v0.y; r.w[2] = v0.z; r.w[3] = v0.w;
+      r.w[4] = v1.x; r.w[5] = v1.y; r.w[6] = v1.z; r.w[7] = v1.w;
+      r.w[8] = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)(o4 + 32u), 0, 0);
+    }
     is++;
-    if (++ik == nk) { ik = 0; issue_row += row_step_bytes; }
+    if (++ik == nk) { ik = 0; issue_row += row_step_bytes; issue_item += (uint32_t)step * (uint32_t)nk; }
   };
   if constexpr (!kStg) {
 #pragma unroll
@@ -565,8 +582,13 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
     // all trips but the last refill the ring; the last one only drains it
     auto fold_item = [&](RawBlock& r, bool refill) {
       const int b = lane + 32 * fk;
-      const bool odd = ((fold_row + lane_bytes + (uint32_t)fk * kSlotBytes) & 2u) != 0;
-      const float folded = fold_raw(r, odd, rec + (b < nb ? b : 0) * kRecDwords, acc);
+      float folded;
+      if constexpr (kPL) {
+        folded = fold_planar(r, rec + (b < nb ? b : 0) * kRecDwords, acc);
+      } else {
+        const bool odd = ((fold_row + lane_bytes + (uint32_t)fk * kSlotBytes) & 2u) != 0;
+        folded = fold_raw(r, odd, rec + (b < nb ? b : 0) * kRecDwords, acc);
+      }
       acc = (fm < total && b < nb) ? folded : acc;
       if (refill) issue(r);
       fm++;
@@ -1087,6 +1109,31 @@ hipError_t launch_gemv_k(GemvParams P, size_t shm, hipStream_t st, int num_cus, 
   return hipGetLastError();
 }
 
+// Planar weights: a ring of 4 items (the probes of this layout on the box: 4 beats 8 by
+// occupancy, 8 waves per SIMD against 4) and one row per half-wave -- 8 rows per workgroup,
+// 16 for matrices of 64k rows or more, 64 for the gate|up SiLU block.  Measured by rows per
+// half-wave 1 / 2 / 4 (14336 x 4096: 11.4 / 12.3 / 12.2 us; 4096 x 14336: 11.2 / 11.8 us;
+// 4096 x 4096: 5.2 / 5.3 us; 128256 x 4096 at 2: 82.7 us).
+template <int KS, Pro PRO, Epi EPI>
+hipError_t launch_gemv_pl(GemvParams P, size_t shm, hipStream_t st, int* grid_out) {
+  int grid;
+  if (EPI == EPI_SILU) {
+    P.row0 = kSiluRows; P.step = 8; P.max_rows = kSiluRows / 8;
+    grid = P.N / kSiluRows;
+  } else if (env_rows() > 0) {
+    const int R = env_rows();
+    P.row0 = R; P.step = 8; P.max_rows = R / 8;
+    grid = (P.N + R - 1) / R;
+  } else {
+    const int R = P.N >= 65536 ? 16 : 8;
+    P.row0 = R; P.step = 8; P.max_rows = R / 8;
+    grid = (P.N + R - 1) / R;
+  }
+  if (grid_out) *grid_out = grid;
+  k_gemv_fused<KS, PRO, EPI, 4, false, true><<<grid, kThreads, shm, st>>>(P);
+  return hipGetLastError();
+}
+
 template <Pro PRO, Epi EPI>
 hipError_t launch_gemv(const GemvParams& P, lt_ctx* ctx, int* grid_out) {
   const int nb = P.K / 32;
@@ -1098,6 +1145,14 @@ hipError_t launch_gemv(const GemvParams& P, lt_ctx* ctx, int* grid_out) {
   // ring depth: 2 when a half-wave has at most 2 blocks to stream, else 8 (4 for the
   // register-heavy K > 4096 prologues)
   const int nk = (P.K / 32 + 31) / 32;
+  if constexpr (EPI != EPI_ROPE_KV) {
+    if (P.planar) {
+      if constexpr (PRO == PRO_STAGE) return launch_gemv_pl<1, PRO, EPI>(P, shm, st, grid_out);
+      else if constexpr (PRO == PRO_EMBED_RMS) return launch_gemv_pl<16, PRO, EPI>(P, shm, st, grid_out);
+      else return P.K <= 4096 ? launch_gemv_pl<16, PRO, EPI>(P, shm, st, grid_out)
+                              : launch_gemv_pl<64, PRO, EPI>(P, shm, st, grid_out);
+    }
+  }
   const bool shallow = EPI != EPI_SILU && (env_rows() == 0 || EPI == EPI_ROPE_KV) && (P.N + 7) / 8 <= 1024 &&
                        nk <= 2;
   if constexpr (PRO == PRO_STAGE) {
@@ -1140,6 +1195,14 @@ int attn_o_max_len(int nh, int nkv, int hd) {
   return maxL;
 }
 
+// The planar entry points (the *_pl twins): rows of whole 32-block items, and a 16-byte
+// aligned planar copy (lt_q8_to_planar).
+int check_planar(const char* fn, const void* W, int K) {
+  LT_REQUIRE(K % 1024 == 0, "%s: K=%d: the planar layout needs K a multiple of 1024", fn, K);
+  LT_REQUIRE(lt_aligned(W, 16), "%s: the planar weight must be 16-byte aligned", fn);
+  return LT_OK;
+}
+
 int finish(hipError_t e, const char* kernel) {
   if (e != hipSuccess) return lt_fail_hip(e, kernel, __FILE__, __LINE__);
   return LT_OK;
@@ -1149,42 +1212,84 @@ int finish(hipError_t e, const char* kernel) {
 
 extern "C" {
 
-int lt_q8_gemv(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd, const float* resid,
-               float* y, int N, int K) {
+static int lt_q8_gemv_impl(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd, const float* resid,
+               float* y, int N, int K, bool pl) {
   LT_REQUIRE(ctx && xq && xd && y, "lt_q8_gemv: null argument");
   if (int rc = check_gemv("lt_q8_gemv", W, N, K)) return rc;
   LT_REQUIRE(lt_aligned(xq, 16), "lt_q8_gemv: xq must be 16-byte aligned");
   LT_REQUIRE(lt_aligned(xd, 2), "lt_q8_gemv: xd must be 2-byte aligned");
   GemvParams P{};
+  P.planar = pl;
+  if (pl) {
+    if (int rc = check_planar("lt_q8_gemv_pl", W, K)) return rc;
+  }
   P.W = (const uint8_t*)W; P.N = N; P.K = K; P.xq = xq; P.xd = xd; P.resid = resid; P.y = y;
   hipError_t e = resid ? launch_gemv<PRO_STAGE, EPI_RESID>(P, ctx, nullptr)
                        : launch_gemv<PRO_STAGE, EPI_STORE>(P, ctx, nullptr);
   return finish(e, "k_gemv_fused<stage>");
 }
 
-int lt_q8_gemv_rms(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* W,
-                   const float* resid, float* y, int N, int K) {
+int lt_q8_gemv(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd, const float* resid,
+               float* y, int N, int K) {
+  return lt_q8_gemv_impl(ctx, W, xq, xd, resid, y, N, K, false);
+}
+
+int lt_q8_gemv_pl(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd, const float* resid,
+               float* y, int N, int K) {
+  return lt_q8_gemv_impl(ctx, W, xq, xd, resid, y, N, K, true);
+}
+
+static int lt_q8_gemv_rms_impl(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* W,
+                   const float* resid, float* y, int N, int K, bool pl) {
   LT_REQUIRE(ctx && x && nw && y, "lt_q8_gemv_rms: null argument");
   if (int rc = check_gemv("lt_q8_gemv_rms", W, N, K)) return rc;
   GemvParams P{};
+  P.planar = pl;
+  if (pl) {
+    if (int rc = check_planar("lt_q8_gemv_rms_pl", W, K)) return rc;
+  }
   P.W = (const uint8_t*)W; P.N = N; P.K = K; P.x = x; P.nw = nw; P.eps = eps; P.resid = resid; P.y = y;
   hipError_t e = resid ? launch_gemv<PRO_RMS, EPI_RESID>(P, ctx, nullptr)
                        : launch_gemv<PRO_RMS, EPI_STORE>(P, ctx, nullptr);
   return finish(e, "k_gemv_fused<rms>");
 }
 
-int lt_q8_gemv_embed_rms(lt_ctx* ctx, const void* emb, const int* tok, int vocab, float* x_out, int* err,
-                         const float* nw, float eps, const void* W, const float* resid, float* y, int N, int K) {
+int lt_q8_gemv_rms(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* W,
+                   const float* resid, float* y, int N, int K) {
+  return lt_q8_gemv_rms_impl(ctx, x, nw, eps, W, resid, y, N, K, false);
+}
+
+int lt_q8_gemv_rms_pl(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* W,
+                   const float* resid, float* y, int N, int K) {
+  return lt_q8_gemv_rms_impl(ctx, x, nw, eps, W, resid, y, N, K, true);
+}
+
+static int lt_q8_gemv_embed_rms_impl(lt_ctx* ctx, const void* emb, const int* tok, int vocab, float* x_out, int* err,
+                         const float* nw, float eps, const void* W, const float* resid, float* y, int N, int K, bool pl) {
   LT_REQUIRE(ctx && emb && tok && x_out && nw && y, "lt_q8_gemv_embed_rms: null argument");
   LT_REQUIRE(vocab > 0, "lt_q8_gemv_embed_rms: vocab=%d", vocab);
   LT_REQUIRE(K <= 4096, "lt_q8_gemv_embed_rms: K=%d (<= 4096)", K);
   if (int rc = check_gemv("lt_q8_gemv_embed_rms", W, N, K)) return rc;
   GemvParams P{};
+  P.planar = pl;
+  if (pl) {
+    if (int rc = check_planar("lt_q8_gemv_embed_rms_pl", W, K)) return rc;
+  }
   P.W = (const uint8_t*)W; P.N = N; P.K = K; P.emb = (const uint8_t*)emb; P.tok = tok; P.vocab = vocab;
   P.x_out = x_out; P.err = err; P.nw = nw; P.eps = eps; P.resid = resid; P.y = y;
   hipError_t e = resid ? launch_gemv<PRO_EMBED_RMS, EPI_RESID>(P, ctx, nullptr)
                        : launch_gemv<PRO_EMBED_RMS, EPI_STORE>(P, ctx, nullptr);
   return finish(e, "k_gemv_fused<embed_rms>");
+}
+
+int lt_q8_gemv_embed_rms(lt_ctx* ctx, const void* emb, const int* tok, int vocab, float* x_out, int* err,
+                         const float* nw, float eps, const void* W, const float* resid, float* y, int N, int K) {
+  return lt_q8_gemv_embed_rms_impl(ctx, emb, tok, vocab, x_out, err, nw, eps, W, resid, y, N, K, false);
+}
+
+int lt_q8_gemv_embed_rms_pl(lt_ctx* ctx, const void* emb, const int* tok, int vocab, float* x_out, int* err,
+                         const float* nw, float eps, const void* W, const float* resid, float* y, int N, int K) {
+  return lt_q8_gemv_embed_rms_impl(ctx, emb, tok, vocab, x_out, err, nw, eps, W, resid, y, N, K, true);
 }
 
 int lt_q8_gemv_quant(lt_ctx* ctx, const float* x, const void* W, const float* resid, float* y, int N, int K) {
@@ -1197,15 +1302,19 @@ int lt_q8_gemv_quant(lt_ctx* ctx, const float* x, const void* W, const float* re
   return finish(e, "k_gemv_fused<quant>");
 }
 
-int lt_q8_gemv_attn_out(lt_ctx* ctx, const int8_t* xq, const uint16_t* xd, const void* ws, size_t ws_bytes,
+static int lt_q8_gemv_attn_out_impl(lt_ctx* ctx, const int8_t* xq, const uint16_t* xd, const void* ws, size_t ws_bytes,
                         int nsplit, int nh, int hd, const void* W, const float* resid, float* y, int N, int K,
-                        int* len, int maxt) {
+                        int* len, int maxt, bool pl) {
   LT_REQUIRE(ctx && y, "lt_q8_gemv_attn_out: null argument");
   if (int rc = check_gemv("lt_q8_gemv_attn_out", W, N, K)) return rc;
   LT_REQUIRE(nh > 0 && hd > 0 && nh * hd == K, "lt_q8_gemv_attn_out: nh*hd=%d*%d must equal K=%d", nh, hd, K);
   LT_REQUIRE(nsplit >= 1, "lt_q8_gemv_attn_out: nsplit=%d", nsplit);
   LT_REQUIRE(!len || maxt > 0, "lt_q8_gemv_attn_out: maxt=%d", maxt);
   GemvParams P{};
+  P.planar = pl;
+  if (pl) {
+    if (int rc = check_planar("lt_q8_gemv_attn_out_pl", W, K)) return rc;
+  }
   P.W = (const uint8_t*)W; P.N = N; P.K = K; P.nsplit = nsplit; P.nh = nh; P.hd = hd;
   P.resid = resid; P.y = y; P.len = len; P.maxt = maxt;
   if (nsplit == 1) {
@@ -1226,14 +1335,40 @@ int lt_q8_gemv_attn_out(lt_ctx* ctx, const int8_t* xq, const uint16_t* xd, const
   return finish(e, "k_gemv_fused<merge>");
 }
 
-int lt_q8_gemv_rms_silu(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* Wgu, int8_t* vq,
-                        uint16_t* vd, int F, int K) {
+int lt_q8_gemv_attn_out(lt_ctx* ctx, const int8_t* xq, const uint16_t* xd, const void* ws, size_t ws_bytes,
+                        int nsplit, int nh, int hd, const void* W, const float* resid, float* y, int N, int K,
+                        int* len, int maxt) {
+  return lt_q8_gemv_attn_out_impl(ctx, xq, xd, ws, ws_bytes, nsplit, nh, hd, W, resid, y, N, K, len, maxt, false);
+}
+
+int lt_q8_gemv_attn_out_pl(lt_ctx* ctx, const int8_t* xq, const uint16_t* xd, const void* ws, size_t ws_bytes,
+                        int nsplit, int nh, int hd, const void* W, const float* resid, float* y, int N, int K,
+                        int* len, int maxt) {
+  return lt_q8_gemv_attn_out_impl(ctx, xq, xd, ws, ws_bytes, nsplit, nh, hd, W, resid, y, N, K, len, maxt, true);
+}
+
+static int lt_q8_gemv_rms_silu_impl(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* Wgu, int8_t* vq,
+                        uint16_t* vd, int F, int K, bool pl) {
   LT_REQUIRE(ctx && x && nw && vq && vd, "lt_q8_gemv_rms_silu: null argument");
   LT_REQUIRE(F > 0 && F % 32 == 0, "lt_q8_gemv_rms_silu: F=%d (multiple of 32)", F);
   if (int rc = check_gemv("lt_q8_gemv_rms_silu", Wgu, 2 * F, K)) return rc;
   GemvParams P{};
+  P.planar = pl;
+  if (pl) {
+    if (int rc = check_planar("lt_q8_gemv_rms_silu_pl", Wgu, K)) return rc;
+  }
   P.W = (const uint8_t*)Wgu; P.N = 2 * F; P.K = K; P.x = x; P.nw = nw; P.eps = eps; P.yq = vq; P.yd = vd;
   return finish(launch_gemv<PRO_RMS, EPI_SILU>(P, ctx, nullptr), "k_gemv_fused<rms,silu>");
+}
+
+int lt_q8_gemv_rms_silu(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* Wgu, int8_t* vq,
+                        uint16_t* vd, int F, int K) {
+  return lt_q8_gemv_rms_silu_impl(ctx, x, nw, eps, Wgu, vq, vd, F, K, false);
+}
+
+int lt_q8_gemv_rms_silu_pl(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* Wgu, int8_t* vq,
+                        uint16_t* vd, int F, int K) {
+  return lt_q8_gemv_rms_silu_impl(ctx, x, nw, eps, Wgu, vq, vd, F, K, true);
 }
 
 int lt_q8_gemv_rms_swiglu(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* Wgu, float* v,
@@ -1314,9 +1449,9 @@ size_t lt_q8_gemv_argmax_workspace_size(int N) {
   return (size_t)G * 8 + 64;
 }
 
-int lt_q8_gemv_rms_argmax(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* W,
+static int lt_q8_gemv_rms_argmax_impl(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* W,
                           float* logits, int N, int K, int* out, int* hist, int* count, int cap,
-                          void* ws, size_t ws_bytes) {
+                          void* ws, size_t ws_bytes, bool pl) {
   LT_REQUIRE(ctx && x && nw && logits && out && ws, "lt_q8_gemv_rms_argmax: null argument");
   LT_REQUIRE(!hist || (count && cap > 0), "lt_q8_gemv_rms_argmax: history needs count and cap > 0");
   if (int rc = check_gemv("lt_q8_gemv_rms_argmax", W, N, K)) return rc;
@@ -1324,6 +1459,10 @@ int lt_q8_gemv_rms_argmax(lt_ctx* ctx, const float* x, const float* nw, float ep
   if (ws_bytes < need) return lt_fail(LT_ENOMEM, "lt_q8_gemv_rms_argmax: workspace %zu < %zu bytes", ws_bytes, need);
   LT_REQUIRE(lt_aligned(ws, 4), "lt_q8_gemv_rms_argmax: workspace must be 4-byte aligned");
   GemvParams P{};
+  P.planar = pl;
+  if (pl) {
+    if (int rc = check_planar("lt_q8_gemv_rms_argmax_pl", W, K)) return rc;
+  }
   P.W = (const uint8_t*)W; P.N = N; P.K = K; P.x = x; P.nw = nw; P.eps = eps; P.y = logits;
   const int env = env_rows();
   const int G = grid_for(N, env > 0 ? env : 8);
@@ -1333,6 +1472,18 @@ int lt_q8_gemv_rms_argmax(lt_ctx* ctx, const float* x, const float* nw, float ep
   if (int rc = finish(launch_gemv<PRO_RMS, EPI_ARGMAX>(P, ctx, &grid), "k_gemv_fused<rms,argmax>")) return rc;
   k_argmax_finalize<<<1, kFinThreads, 0, ctx->stream>>>(P.pval, P.pidx, grid, out, hist, count, cap);
   return lt_check_launch("k_argmax_finalize");
+}
+
+int lt_q8_gemv_rms_argmax(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* W,
+                          float* logits, int N, int K, int* out, int* hist, int* count, int cap,
+                          void* ws, size_t ws_bytes) {
+  return lt_q8_gemv_rms_argmax_impl(ctx, x, nw, eps, W, logits, N, K, out, hist, count, cap, ws, ws_bytes, false);
+}
+
+int lt_q8_gemv_rms_argmax_pl(lt_ctx* ctx, const float* x, const float* nw, float eps, const void* W,
+                          float* logits, int N, int K, int* out, int* hist, int* count, int cap,
+                          void* ws, size_t ws_bytes) {
+  return lt_q8_gemv_rms_argmax_impl(ctx, x, nw, eps, W, logits, N, K, out, hist, count, cap, ws, ws_bytes, true);
 }
 
 }  // extern "C"

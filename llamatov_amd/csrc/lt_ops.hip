@@ -425,9 +425,43 @@ __global__ __launch_bounds__(256) void k_check_quotient(unsigned long long* out)
   atomicAdd(&out[2], cases);
 }
 
+// Repack a Q8_0 matrix [N][nb] (34-byte blocks) into the planar layout (lt_q8_device.h):
+// thread per block; its 32 quants go to the two 16-byte halves of its item slot, its scale to
+// the scale plane.  Byte loads: the source blocks are only 2-byte aligned.
+__global__ __launch_bounds__(256) void k_q8_to_planar(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                      uint32_t n_blocks, int nb) {
+  const uint32_t gi = blockIdx.x * 256u + threadIdx.x;
+  if (gi >= n_blocks) return;
+  const uint8_t* b = src + (size_t)gi * kBlockBytes;
+  uint32_t w[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++)
+    w[j] = (uint32_t)b[2 + 4 * j] | ((uint32_t)b[3 + 4 * j] << 8) | ((uint32_t)b[4 + 4 * j] << 16) |
+           ((uint32_t)b[5 + 4 * j] << 24);
+  const uint32_t row = gi / (uint32_t)nb, blk = gi - row * (uint32_t)nb;
+  const uint32_t item = row * (uint32_t)(nb / 32) + blk / 32u, lane = blk & 31u;
+  uint8_t* q = dst + (size_t)item * kPlanarItemBytes + lane * 16u;
+  *(u32x4*)q = u32x4{w[0], w[1], w[2], w[3]};
+  *(u32x4*)(q + kPlanarItemBytes / 2u) = u32x4{w[4], w[5], w[6], w[7]};
+  uint16_t* sc = (uint16_t*)(dst + (size_t)n_blocks * 32u);
+  sc[gi] = (uint16_t)(b[0] | (b[1] << 8));
+}
+
 }  // namespace
 
 extern "C" {
+
+int lt_q8_to_planar(lt_ctx* ctx, const void* src, void* dst, int N, int K) {
+  LT_REQUIRE(ctx && src && dst, "lt_q8_to_planar: null argument");
+  LT_REQUIRE(N > 0 && K > 0 && K % 1024 == 0 && K <= 16384, "lt_q8_to_planar: N=%d K=%d (K a multiple of 1024, <= 16384)",
+             N, K);
+  LT_REQUIRE((uint64_t)N * (uint64_t)(K / 32) * 34u < ((uint64_t)1 << 32), "lt_q8_to_planar: matrix must be below 4 GiB");
+  LT_REQUIRE(lt_aligned(dst, 16), "lt_q8_to_planar: dst must be 16-byte aligned");
+  LT_REQUIRE(src != dst, "lt_q8_to_planar: dst must not be src");
+  const uint32_t n = (uint32_t)N * (uint32_t)(K / 32);
+  k_q8_to_planar<<<(n + 255) / 256, 256, 0, ctx->stream>>>((const uint8_t*)src, (uint8_t*)dst, n, K / 32);
+  return lt_check_launch("k_q8_to_planar");
+}
 
 int lt_fill_u8(lt_ctx* ctx, void* dst, uint8_t value, size_t nbytes) {
   LT_REQUIRE(ctx && (dst || !nbytes), "lt_fill_u8: null argument");

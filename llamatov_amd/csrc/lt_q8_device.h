@@ -243,6 +243,27 @@ __device__ __forceinline__ float fold_raw(const RawBlock& r, bool odd, const uin
   return fmaf(lt_h2f(d16) * xdv, (float)s, acc);
 }
 
+// Planar Q8_0 layout, for matrices whose rows are whole 32-block items (K % 1024 == 0): the
+// quants of item (row r, slot k) -- blocks 32k .. 32k+31 of row r -- are 1024 contiguous
+// bytes at (r*nk + k)*1024, first the leading 16 quants of each of the 32 blocks (16 bytes
+// per block, in block order), then their trailing 16; the fp16 scales follow the whole quant
+// plane as [N][nb].  A half-wave reads one item with two fully coalesced 512-byte loads and
+// one 64-byte load, and every cache line is consumed by a single load instruction.  Lane L
+// holds block 32k+L as w[0..7] = quants 0..31 in fours and w[8] = the scale bits.  Against
+// the activation record's phase O (dwords kRecPhase+1 .. kRecPhase+8 hold quants 0..31,
+// kRecPhase+9 the scale) the 8 v_dot4_i32_i8 give the same exact isum as fold_raw's 9, and
+// the fma is the same.
+constexpr uint32_t kPlanarItemBytes = 1024;
+
+__device__ __forceinline__ float fold_planar(const RawBlock& r, const uint32_t* rec, float acc) {
+  const uint32_t* a = rec + kRecPhase + 1;
+  int s = 0;
+#pragma unroll
+  for (int j = 0; j < 8; j++) s = __builtin_amdgcn_sdot4((int)r.w[j], (int)a[j], s, false);
+  const float xdv = __builtin_bit_cast(float, a[8]);
+  return fmaf(lt_h2f((uint16_t)(r.w[8] & 0xFFFFu)) * xdv, (float)s, acc);
+}
+
 // Build the activation records of nb blocks from the staged quants sxq[32*nb] (int8) and
 // scales sxd[nb] (fp16 bits); called by every thread of the workgroup.
 // Write a block quantized by quant4 into its record: lane j of the block's 8-lane group

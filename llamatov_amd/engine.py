@@ -438,6 +438,10 @@ class Profile:
     # n_embd <= 1024, n_ff <= 5120) and the cache holds at most lt_decode_step_max_len rows;
     # otherwise the five launches (same bits)
     persistent_step: bool = True
+    # fused step: the five launches stream planar copies of their matrices (lt_q8_to_planar,
+    # *_pl GEMVs: whole aligned cache lines per load) when every K is a multiple of 1024
+    # (the 8B geometry; same bits)
+    planar: bool = True
     fused_rms_quant: bool = False   # per-op path only: k_rms_quant instead of k_rmsnorm + k_quant_q8
     graph: bool = True
     # "engine": the reference engine's quantizer and canonical GEMV order (every field above);
@@ -550,6 +554,8 @@ class ResidentModel:
         self.load_report = None
         self.tiles = None   # the prefill GEMM's tile-major copies (prefill_tiles)
         self.output_t: Q8Weight | None = None   # the lm_head's tile-major copy (head_tiles)
+        self.planar = None  # the planar copies of the decode GEMVs' matrices (planar_copies)
+        self.output_pl: Q8Weight | None = None
         self.tok_embd = top["tok_embd"]
         self.output = top.get("output", self.tok_embd)
         self.output_norm = top["output_norm"]
@@ -598,6 +604,42 @@ class ResidentModel:
             L[k + "_t"] = Q8Weight(None, W.K, t=t, N=W.N)
         self.tiles = base
 
+    def planar_eligible(self) -> bool:
+        """Every matrix the five-launch step streams (q|k|v, o, interleaved gate|up, down, the
+        lm_head) has K a multiple of 1024, the planar layout's condition."""
+        c = self.cfg
+        return "wgu_il" in self.layers[0] and all(k % 1024 == 0 for k in (c.n_embd, c.q_dim, c.n_ff))
+
+    def planar_copies(self) -> bool:
+        """Planar copies (lt_q8_to_planar) of the step's matrices, built on the device from the
+        resident blocks at first use: one allocation, one more copy of those weights in HBM.
+        The five-launch step then streams them through the *_pl GEMVs (same bits).  False when
+        the geometry is not eligible."""
+        if self.planar is not None:
+            return True
+        if not self.planar_eligible():
+            return False
+        names = ("wqkv", "wo", "wgu_il", "wdown")
+        plan = []
+        total = 0
+        for L in self.layers:
+            for k in names:
+                W = L[k]
+                plan.append((L, k, W, total))
+                total += (W.t.nbytes + 255) // 256 * 256
+        plan.append((None, "output", self.output, total))
+        total += (self.output.t.nbytes + 255) // 256 * 256
+        base = self.dev.malloc(total)
+        for L, k, W, off in plan:
+            t = DevTensor(base + off, (W.t.nbytes,), np.uint8, owns=False, dev=self.dev)
+            call("lt_q8_to_planar", self.dev.handle, W.t.vp, t.vp, W.N, W.K)
+            if L is None:
+                self.output_pl = Q8Weight(None, W.K, t=t, N=W.N)
+            else:
+                L[k + "_pl"] = Q8Weight(None, W.K, t=t, N=W.N)
+        self.planar = base
+        return True
+
     def head_tiles(self) -> Q8Weight:
         """Tile-major copy of the lm_head (the batched decode step's vocab GEMM), built on the
         device at first use."""
@@ -613,6 +655,13 @@ class ResidentModel:
         if self.tiles is not None:
             self.dev.free(self.tiles)
             self.tiles = None
+        if self.planar is not None:
+            self.dev.free(self.planar)
+            self.planar = None
+            self.output_pl = None
+            for L in self.layers:
+                for k in ("wqkv_pl", "wo_pl", "wgu_il_pl", "wdown_pl"):
+                    L.pop(k, None)
         if self.output_t is not None:
             self.output_t.t.free()
             self.output_t = None
@@ -671,6 +720,9 @@ class DecodePlan:
                                      len_ptr=self.lens.ptr + 4 * il, dev=D)
                        for il in range(cfg.n_layers)]
         self.scale = float(hd ** -0.5)
+        # planar copies for the five-launch step (engine numerics, SiLU-quant gate|up)
+        self.planar = bool(profile.fused_step and profile.planar and profile.numerics == "engine"
+                           and not profile.swiglu_fp32 and model.planar_copies())
         self._setup_persistent()
         self._prefill: PrefillBuffers | None = None
         self.sampling = False
@@ -811,30 +863,37 @@ class DecodePlan:
             self._enqueue_four()
             return
         ws, ws_n = _vp(self.attn_ws), (self.attn_ws.nbytes if self.attn_ws is not None else 0)
+        pl = self.planar
+        sfx = "_pl" if pl else ""
+
+        def w(L, k):   # the matrix the step streams: its planar copy on planar plans
+            return L[k + "_pl"].t.vp if pl else L[k].t.vp
         for il, L in enumerate(m.layers):
             cache = self.caches[il]
             x = self.resid_in if il == 0 else self.carry
             if il == 0 and not self.host_embed:
-                call("lt_q8_gemv_embed_rms", h, m.tok_embd.t.vp, self.tok.vp, cfg.vocab, self.resid_in.vp,
-                     self.err.vp, L["attn_norm"].vp, eps, L["wqkv"].t.vp, _vp(L["bqkv"]), self.qkv.vp,
+                call("lt_q8_gemv_embed_rms" + sfx, h, m.tok_embd.t.vp, self.tok.vp, cfg.vocab, self.resid_in.vp,
+                     self.err.vp, L["attn_norm"].vp, eps, w(L, "wqkv"), _vp(L["bqkv"]), self.qkv.vp,
                      cfg.n_qkv, E)
             else:
-                call("lt_q8_gemv_rms", h, x.vp, L["attn_norm"].vp, eps, L["wqkv"].t.vp, _vp(L["bqkv"]),
+                call("lt_q8_gemv_rms" + sfx, h, x.vp, L["attn_norm"].vp, eps, w(L, "wqkv"), _vp(L["bqkv"]),
                      self.qkv.vp, cfg.n_qkv, E)
             call("lt_attn_step", h, self.qkv.vp, m.freqs.vp, cache.k.vp, cache.v.vp, _vp(cache.len_ptr),
                  None, self.xq.vp, self.xd.vp, nh, nkv, hd, ctypes.c_float(self.scale), cache.max_seq,
                  p.attn_nsplit, p.kv_dtype, ws, ws_n)
-            call("lt_q8_gemv_attn_out", h, self.xq.vp, self.xd.vp, None, 0, 1, nh, hd, L["wo"].t.vp,
+            call("lt_q8_gemv_attn_out" + sfx, h, self.xq.vp, self.xd.vp, None, 0, 1, nh, hd, w(L, "wo"),
                  x.vp, self.xres.vp, E, cfg.q_dim, _vp(cache.len_ptr), cache.max_seq)
             if p.swiglu_fp32:
                 call("lt_q8_gemv_rms_swiglu", h, self.xres.vp, L["ffn_norm"].vp, eps, L["wgu_il"].t.vp,
                      self.v.vp, F, E)
                 call("lt_q8_gemv_quant", h, self.v.vp, L["wdown"].t.vp, self.xres.vp, self.carry.vp, E, F)
             else:
-                call("lt_q8_gemv_rms_silu", h, self.xres.vp, L["ffn_norm"].vp, eps, L["wgu_il"].t.vp,
+                call("lt_q8_gemv_rms_silu" + sfx, h, self.xres.vp, L["ffn_norm"].vp, eps, w(L, "wgu_il"),
                      self.xq.vp, self.xd.vp, F, E)
-                call("lt_q8_gemv", h, L["wdown"].t.vp, self.xq.vp, self.xd.vp, self.xres.vp, self.carry.vp, E, F)
-        call("lt_q8_gemv_rms_argmax", h, self.carry.vp, m.output_norm.vp, eps, m.output.t.vp, self.logits.vp,
+                call("lt_q8_gemv" + sfx, h, w(L, "wdown"), self.xq.vp, self.xd.vp, self.xres.vp, self.carry.vp,
+                     E, F)
+        out_w = m.output_pl.t.vp if pl else m.output.t.vp
+        call("lt_q8_gemv_rms_argmax" + sfx, h, self.carry.vp, m.output_norm.vp, eps, out_w, self.logits.vp,
              cfg.vocab, E, self.tok.vp, *self._hist_args(), self.am_ws.vp, self.am_ws.nbytes)
         self._enqueue_sample_if_on()
 
