@@ -162,7 +162,7 @@ __device__ __forceinline__ void load_slots(const float* __restrict__ x, const fl
 
 // Quantize the vector groups into records (optionally normalized: y = (x*inv)*w).  The
 // groups past the first KV are loaded here (K > 16*NT).
-template <int KS, bool kNorm, int NT = kThreads>
+template <int KS, bool kNorm, int NT = kThreads, bool kPL = false>
 __device__ __forceinline__ void slots_to_rec(Slots<KS, NT>& S, const float* __restrict__ x,
                                              const float* __restrict__ w, float inv, int K, uint32_t* rec) {
   const int t = threadIdx.x;
@@ -188,7 +188,14 @@ __device__ __forceinline__ void slots_to_rec(Slots<KS, NT>& S, const float* __re
 #pragma unroll
     for (int v = 0; v < KV; v++) {
       const int b = (t >> 3) + (NT / 8) * (v0 + v);
-      q4_to_rec(p[v], sc[v].dq, j, b < nb, rec + b * kRecDwords);
+      if constexpr (kPL) {   // planar folds read phase O and the scale only
+        if (b < nb) {
+          rec[b * kRecDwords + kRecPhase + 1 + j] = p[v];
+          if (j == 0) rec[b * kRecDwords + kRecPhase + 9] = __builtin_bit_cast(uint32_t, sc[v].dq);
+        }
+      } else {
+        q4_to_rec(p[v], sc[v].dq, j, b < nb, rec + b * kRecDwords);
+      }
     }
   }
 }
@@ -309,6 +316,27 @@ __device__ __forceinline__ void stage_to_rec(const StageRegs<NT>& R, int K, uint
       rec[b * kRecDwords + 9] = xdf;
       rec[b * kRecDwords + kRecPhase + 9] = xdf;
     }
+  }
+}
+
+// The planar folds' records straight from the staged registers: 16-byte chunk i is half
+// (i & 1) of block i / 2, i.e. dwords kRecPhase+1+4(i&1) .. +3 of its record (phase O), and
+// the scale goes to dword kRecPhase+9; no LDS copy of xq, no extra barrier.
+template <int NT = kThreads>
+__device__ __forceinline__ void stage_to_rec_pl(const StageRegs<NT>& R, int K, uint32_t* rec) {
+  const int nb = K >> 5;
+#pragma unroll
+  for (int k = 0; k < StageRegs<NT>::C; k++) {
+    const int i = threadIdx.x + NT * k;
+    if (i < K / 16) {
+      uint32_t* r = rec + (i >> 1) * kRecDwords + kRecPhase + 1 + 4 * (i & 1);
+      r[0] = R.c[k].x; r[1] = R.c[k].y; r[2] = R.c[k].z; r[3] = R.c[k].w;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < StageRegs<NT>::DS; k++) {
+    const int b = threadIdx.x + NT * k;
+    if (b < nb) rec[b * kRecDwords + kRecPhase + 9] = __builtin_bit_cast(uint32_t, lt_h2f(R.d[k]));
   }
 }
 
@@ -476,13 +504,15 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
   if constexpr (PRO == PRO_RMS) {
     const float inv = rms_inv<KS>(S, K, P.eps, red, sinv);
     // @phase gemv 5
-    slots_to_rec<KS, true>(S, P.x, P.nw, inv, K, rec);
+    slots_to_rec<KS, true, kThreads, kPL>(S, P.x, P.nw, inv, K, rec);
   } else if constexpr (PRO == PRO_QUANT) {
-    slots_to_rec<KS, false>(S, P.x, nullptr, 0.0f, K, rec);
+    slots_to_rec<KS, false, kThreads, kPL>(S, P.x, nullptr, 0.0f, K, rec);
   } else if constexpr (PRO == PRO_STAGE) {
-    stage_to_rec(SR, K, sxq, rec);
+    if constexpr (kPL) stage_to_rec_pl(SR, K, rec);
+    else stage_to_rec(SR, K, sxq, rec);
   } else if constexpr (PRO == PRO_MERGE) {
     if (P.nsplit > 1) pro_merge_quant(P, rec);
+    else if constexpr (kPL) stage_to_rec_pl(SR, K, rec);
     else stage_to_rec(SR, K, sxq, rec);
     if (P.len && blockIdx.x == 0 && threadIdx.x == 0) {
       const int L = *P.len;
@@ -507,7 +537,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
     static_assert(KS <= 16, "the embedding prologue holds every vector group (K <= 4096)");
     lds_slots<KS>(xrow, P.nw, K, S);
     const float inv = rms_inv<KS>(S, K, P.eps, red, sinv);
-    slots_to_rec<KS, true>(S, nullptr, P.nw, inv, K, rec);
+    slots_to_rec<KS, true, kThreads, kPL>(S, nullptr, P.nw, inv, K, rec);
   }
   // staged: the region into LDS, after the prologue's buffers (the host sizes the launch's
   // LDS the same way)
