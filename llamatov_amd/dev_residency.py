@@ -18,10 +18,11 @@ with the engine quantizer at first use and cached on the device, as the referenc
 (fact_dispatch.py:255-299); a Q8_0 GGUF's weights round-trip to the same blocks.
 
 What differs, and why:
-  * Kernel-selection flags (_QFUSED, _FUSE_QKV, _RMS_BLOCKROW, ...) are accepted, listed by
-    PRODUCTION_PROFILE and attested, but do not select kernels: the engine always runs its
-    five fused launches per layer, which are bit-identical to every certified ensemble of the
-    reference's per-op kernels.  Flags that would ask for a host island or a lossy transform
+  * Kernel-selection flags (_QFUSED, _FUSE_QKV, _RMS_BLOCKROW, ...) are accepted and listed by
+    PRODUCTION_PROFILE, but do not select kernels: the engine runs one kernel set (the
+    persistent step or five fused launches per layer), bit-identical to every certified
+    ensemble of the reference's per-op kernels.  attest_profile says so: next to the flags'
+    live values it reports `_INERT_FLAGS` (these flags) and `_ENGINE` (what the engine runs).  Flags that would ask for a host island or a lossy transform
     (_KV_QUANT_Q8, device paths turned off) are refused by assert_certified_composition.
   * The KV cache is the engine's (fp32 by default, the reference's elem_bytes=4; elem_bytes=2
     selects fp16), allocated for _KV_MAX_SEQ positions on the first forward.
@@ -81,6 +82,13 @@ _ROPE_QK_FUSED = True
 _SILU_QUANT_FUSED = True
 _RMS_QUANT_FUSED = False
 
+# The reference's flags that choose among its bit-identical kernel variants: accepted and
+# attested with their values, but this build runs one kernel set whatever they say.
+_INERT_FLAGS = ("_QFUSED", "_GEMV_TILED_V4_QFUSED", "_ADDRES_FUSED", "_BIAS_FOLD", "_RMS_BLOCKROW", "_GEMV_TILED",
+                "_GEMV_TILED_V4", "_GEMV_TILED_BM", "_QUANT_PAR", "_ARGMAX2", "_FUSE_QKV", "_FUSE_GATEUP",
+                "_APPEND_KV_FUSED", "_APPEND_INCR_FUSED", "_RESID_CARRY_FUSED", "_ROPE_QK_FUSED",
+                "_SILU_QUANT_FUSED", "_RMS_QUANT_FUSED")
+
 PRODUCTION_PROFILE = {
     "_DEVICE_KV_CACHE": True, "_DEVICE_ATTN": True, "_MASKED_ATTN": True,
     "_GRAPH_PREP": True, "_KV_MAX_SEQ": 256, "_ATTN_SPLIT_K": False,
@@ -115,11 +123,19 @@ def apply_production_profile() -> dict:
 
 
 def attest_profile() -> dict:
-    """The live values of every production-profile flag (reference :1241-1248)."""
+    """The live values of every production-profile flag (reference :1241-1248), plus what
+    they mean here: `_INERT_FLAGS`, the flags that select nothing in this build, and
+    `_ENGINE`, the engine profile the flags map to (the fields that do select kernels or
+    numerics)."""
     g = globals()
     live = {k: g.get(k) for k in PRODUCTION_PROFILE}
     live["_KV_ELEM_BYTES"] = _KV_ELEM_BYTES
     live["_ATTN_NSPLIT"] = _ATTN_NSPLIT
+    p = _engine_profile()
+    live["_INERT_FLAGS"] = list(_INERT_FLAGS)
+    live["_ENGINE"] = {"kv_dtype": "f16" if p.kv_dtype == LT_KV_F16 else "f32", "attn_nsplit": p.attn_nsplit,
+                       "fused_step": p.fused_step, "persistent_step": p.persistent_step, "planar": p.planar,
+                       "swiglu_fp32": p.swiglu_fp32, "attn_in_o": p.attn_in_o, "numerics": p.numerics}
     return live
 
 

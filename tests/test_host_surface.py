@@ -62,6 +62,11 @@ def test_composition_gate_on_the_host():
         dr._KV_ELEM_BYTES = 4
     live = dr.attest_profile()
     assert all(live[k] == v for k, v in dr.PRODUCTION_PROFILE.items())
+    # the attestation names the flags that select nothing here, and what the engine runs
+    assert set(live["_INERT_FLAGS"]) <= set(dr.PRODUCTION_PROFILE) | {"_RMS_QUANT_FUSED"}
+    assert "_KV_ELEM_BYTES" not in live["_INERT_FLAGS"] and "_ATTN_SPLIT_K" not in live["_INERT_FLAGS"]
+    assert live["_ENGINE"]["fused_step"] and live["_ENGINE"]["numerics"] == "engine"
+    assert live["_ENGINE"]["kv_dtype"] == ("f16" if dr._KV_ELEM_BYTES == 2 else "f32")
 
 
 def test_engine_profile_refusals():
