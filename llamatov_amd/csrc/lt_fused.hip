@@ -1154,7 +1154,17 @@ hipError_t launch_gemv_pl(GemvParams P, size_t shm, hipStream_t st, int* grid_ou
     const int R = env_rows();
     P.row0 = R; P.step = 8; P.max_rows = R / 8;
     grid = (P.N + R - 1) / R;
+  } else if (PRO == PRO_RMS || PRO == PRO_EMBED_RMS) {
+    // every workgroup of an RMSNorm prologue reads x (twice) and the norm weight and
+    // normalizes and quantizes the whole row: about 384 workgroups (8 .. 64 rows each)
+    // balance that against the streaming.  Measured against 8 rows (16 from 64k rows):
+    // 6144 x 4096 8.27 -> 7.63 us, 4096 x 4096 6.42 -> 6.15, 128256 x 4096 90.1 -> 85.0
+    int R = ((P.N + 383) / 384 + 7) & ~7;
+    R = R < 8 ? 8 : (R > kSiluRows ? kSiluRows : R);
+    P.row0 = R; P.step = 8; P.max_rows = R / 8;
+    grid = (P.N + R - 1) / R;
   } else {
+    // a staged prologue is a copy: short-lived 8-row workgroups stream best (16 from 64k rows)
     const int R = P.N >= 65536 ? 16 : 8;
     P.row0 = R; P.step = 8; P.max_rows = R / 8;
     grid = (P.N + R - 1) / R;
