@@ -239,6 +239,21 @@ __device__ __forceinline__ float rms_inv(const Slots<KS, NT>& S, int K, float ep
   return *sinv;
 }
 
+// rms_inv over a single (vector) load of x: the vector groups go to LDS (xs, KS*256 floats)
+// and each thread reads its strided slots back, so x is read from L2 once per workgroup; the
+// fold and the tree are rms_inv's.  All vector groups are held (KS*256 <= 4*4*NT).
+template <int KS>
+__device__ __forceinline__ float rms_inv_lds(Slots<KS>& S, int K, float eps, float* red, float* sinv, float* xs) {
+  static_assert(Slots<KS>::NV == Slots<KS>::KV, "every vector group in registers");
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int v = 0; v < Slots<KS>::KV; v++) *(f32x4*)(xs + 4 * (t + kThreads * v)) = S.x[v];
+  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < KS; s++) S.s[s] = xs[s * kThreads + t];
+  return rms_inv<KS, kThreads>(S, K, eps, red, sinv);
+}
+
 // Split-K merge of the attention partials (the declared combine, ascending split order,
 // bpd/kernelgen/experimental/attn_decode_split.cu:37-91: M = max m_s, w_s = exp(m_s - M),
 // Z = sum fma(w_s, Z_s), O = sum fma(w_s, O_s), out = O/Z), then the quant.
@@ -391,7 +406,9 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
   Slots<KS> S;
   StageRegs<> SR;
   int tok = 0;
-  if constexpr (PRO == PRO_RMS) load_slots<KS, true>(P.x, P.nw, K, S);
+  // planar RMS prologues with every vector group held read x once (rms_inv_lds)
+  constexpr bool kXLds = kPL && PRO == PRO_RMS && KS <= 16;
+  if constexpr (PRO == PRO_RMS) load_slots<KS, !kXLds>(P.x, P.nw, K, S);
   else if constexpr (PRO == PRO_QUANT) load_slots<KS, false>(P.x, nullptr, K, S);
   else if constexpr (PRO == PRO_STAGE) load_stage(P.xq, P.xd, K, SR);
   else if constexpr (PRO == PRO_MERGE) { if (P.nsplit == 1) load_stage(P.xq, P.xd, K, SR); }
@@ -502,7 +519,9 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
 
   // (3) the prologue's arithmetic, under the weight loads
   if constexpr (PRO == PRO_RMS) {
-    const float inv = rms_inv<KS>(S, K, P.eps, red, sinv);
+    float inv;
+    if constexpr (kXLds) inv = rms_inv_lds<KS>(S, K, P.eps, red, sinv, (float*)sxq);
+    else inv = rms_inv<KS>(S, K, P.eps, red, sinv);
     // @phase gemv 5
     slots_to_rec<KS, true, kThreads, kPL>(S, P.x, P.nw, inv, K, rec);
   } else if constexpr (PRO == PRO_QUANT) {
@@ -1180,6 +1199,7 @@ hipError_t launch_gemv(const GemvParams& P, lt_ctx* ctx, int* grid_out) {
   size_t shm = (kThreads + 4) * sizeof(float) + (size_t)((nb * kRecDwords + 3) & ~3) * 4;
   if (PRO == PRO_STAGE || PRO == PRO_MERGE) shm += (size_t)((P.K + 15) & ~15);
   if (PRO == PRO_EMBED_RMS) shm += (size_t)((P.K + 15) & ~15) + (size_t)P.K * sizeof(float);
+  if (PRO == PRO_RMS && P.planar && P.K <= 4096) shm += (size_t)16 * kThreads * sizeof(float);   // rms_inv_lds's xs
   hipStream_t st = ctx->stream;
   const int ncu = ctx->num_cus;
   // ring depth: 2 when a half-wave has at most 2 blocks to stream, else 8 (4 for the
