@@ -297,10 +297,11 @@ GEMV_SWEEP = [("C1 ffn_up 0.5B", 4864, 896), ("C3 q/o 8B", 4096, 4096), ("C3 gat
               ("C3 down 8B", 4096, 14336), ("C3 lm_head 8B", 128256, 4096), ("C2 lm_head 0.5B", 151936, 896)]
 
 
-def gemv_sweep(dev, launches: int = 40) -> list[dict]:
+def gemv_sweep(dev, launches: int = 60, reps: int = 5) -> list[dict]:
     """Q8_0 GEMV bandwidth (BASELINE configs 1 and 3, plus the 0.5B vocab projection):
     lt_q8_gemv on random blocks, rotating >= 600 MB of weight copies so the MALL cannot
-    serve them, timed with HIP events on the library's stream."""
+    serve them, timed with HIP events on the library's stream: one untimed pass over the
+    copies, then the median of `reps` timed runs of `launches` back-to-back launches."""
     from llamatov_amd import engine as dr
     from llamatov_amd._lib import call
     out = []
@@ -322,13 +323,15 @@ def gemv_sweep(dev, launches: int = 40) -> list[dict]:
             for i in range(copies):
                 call(fn, dev.handle, mats[i].vp, xq.vp, xd.vp, None, y.vp, N, K)
             dev.sync()
-            ev = Events(dev)
-            ev.start()
-            for i in range(launches):
-                call(fn, dev.handle, mats[i % copies].vp, xq.vp, xd.vp, None, y.vp, N, K)
-            ms = ev.stop_ms()
-            ev.free()
-            return ms / 1e3 / launches
+            runs = []
+            for _ in range(reps):
+                ev = Events(dev)
+                ev.start()
+                for i in range(launches):
+                    call(fn, dev.handle, mats[i % copies].vp, xq.vp, xd.vp, None, y.vp, N, K)
+                runs.append(ev.stop_ms() / 1e3 / launches)
+                ev.free()
+            return float(np.median(runs))
         alg = N * nb * 34 + K + 2 * nb + 4 * N
         avg_b = timed("lt_q8_gemv", ws)
         row = {"shape": f"{name} {N}x{K}"}
