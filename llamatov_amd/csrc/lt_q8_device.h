@@ -243,6 +243,23 @@ __device__ __forceinline__ float fold_raw(const RawBlock& r, bool odd, const uin
   return fmaf(lt_h2f(d16) * xdv, (float)s, acc);
 }
 
+// fold_raw in two steps, so a caller can have every record read in flight before the first
+// dot: rec_regs copies the 10 dwords of the block's phase into registers, fold_regs is
+// fold_raw's arithmetic on them (the same 9 v_dot4_i32_i8, scale product and fma).
+__device__ __forceinline__ void rec_regs(const uint32_t* rec, bool odd, uint32_t (&a)[10]) {
+  const uint32_t* p = rec + (odd ? kRecPhase : 0);
+#pragma unroll
+  for (int j = 0; j < 10; j++) a[j] = p[j];
+}
+__device__ __forceinline__ float fold_regs(const RawBlock& r, bool odd, const uint32_t (&a)[10], float acc) {
+  int s = 0;
+#pragma unroll
+  for (int j = 0; j < 9; j++) s = __builtin_amdgcn_sdot4((int)r.w[j], (int)a[j], s, false);
+  const float xdv = __builtin_bit_cast(float, a[9]);
+  const uint16_t d16 = (uint16_t)(odd ? (r.w[0] >> 16) : (r.w[0] & 0xFFFFu));
+  return fmaf(lt_h2f(d16) * xdv, (float)s, acc);
+}
+
 // Planar Q8_0 layout, for matrices whose rows are whole 32-block items (K % 1024 == 0): the
 // quants of item (row r, slot k) -- blocks 32k .. 32k+31 of row r -- are 1024 contiguous
 // bytes at (r*nk + k)*1024, first the leading 16 quants of each of the 32 blocks (16 bytes

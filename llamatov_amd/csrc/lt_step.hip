@@ -685,7 +685,13 @@ __device__ __forceinline__ bool gemv_worker(const StepParams& P, uint8_t* smem, 
       lds_barrier();
       norm_to_rec(xs, nw4, inv, E, rec);
       lds_barrier();
-      const float folded = fold_raw(wA, (blk_off(arow, nbE, lane, true) & 2u) != 0, rec + (lane < nbE ? lane : 0) * kRecDwords, 0.0f);
+      // the record's reads all in flight before the first dot (fold_raw, read by read, waits
+      // out one LDS round trip per two dots)
+      const bool oddA = (blk_off(arow, nbE, lane, true) & 2u) != 0;
+      uint32_t ra[10];
+      rec_regs(rec + (lane < nbE ? lane : 0) * kRecDwords, oddA, ra);
+      asm volatile("" ::: "memory");
+      const float folded = fold_regs(wA, oddA, ra, 0.0f);
       const float rv = halfwave_tree_dpp(lane < nbE ? folded : 0.0f);
       if (lane == 0) srow[hw] = Ly.bqkv ? rv + bias : rv;
       lds_barrier();
@@ -733,7 +739,11 @@ __device__ __forceinline__ bool gemv_worker(const StepParams& P, uint8_t* smem, 
         }
       }
       if (wg_any(!ok, slots, par)) return false;
-      const float folded = fold_raw(wC, (blk_off(row, nbO, lane, true) & 2u) != 0, rec + (lane < nbO ? lane : 0) * kRecDwords, 0.0f);
+      const bool oddC = (blk_off(row, nbO, lane, true) & 2u) != 0;
+      uint32_t ra[10];
+      rec_regs(rec + (lane < nbO ? lane : 0) * kRecDwords, oddC, ra);
+      asm volatile("" ::: "memory");
+      const float folded = fold_regs(wC, oddC, ra, 0.0f);
       const float rv = halfwave_tree_dpp(lane < nbO ? folded : 0.0f);
       // the unit's 8 rows leave in one store instruction (a word per half-wave measured
       // ~0.6 us slower to exchange)
@@ -798,12 +808,24 @@ __device__ __forceinline__ bool gemv_worker(const StepParams& P, uint8_t* smem, 
         xres = __uint_as_float(r);
       }
       if (wg_any(!ok, slots, par)) return false;
-      float acc = 0.0f;
+      // every item's record read first (all in flight together), then the folds in block
+      // order; a lane past the row's last block folds block 0's record and keeps acc (a
+      // select, not a branch: the items' reads and dots interleave)
+      uint32_t ra[kDownItems][10];
+      bool oddE[kDownItems];
 #pragma unroll
       for (int k = 0; k < kDownItems; k++) {
         const int b = lane + 32 * k;
-        if (b < nbF)
-          acc = fold_raw(wE[k], (blk_off(row, nbF, b, true) & 2u) != 0, rec + b * kRecDwords, acc);
+        const int bb = b < nbF ? b : 0;
+        oddE[k] = (blk_off(row, nbF, bb, true) & 2u) != 0;
+        rec_regs(rec + bb * kRecDwords, oddE[k], ra[k]);
+      }
+      asm volatile("" ::: "memory");
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kDownItems; k++) {
+        const float f = fold_regs(wE[k], oddE[k], ra[k], acc);
+        acc = lane + 32 * k < nbF ? f : acc;
       }
       const float rv = halfwave_tree_dpp(acc);
       if (lane == 0) srow[hw] = rv + xres;
