@@ -468,10 +468,16 @@ __device__ __forceinline__ bool attn_worker(const StepParams& P, uint8_t* smem, 
       }
       for (int p = t; p < n; p += kT) {
         const u32x4* kr = (const u32x4*)(sK + p * AL::kKRow);
+        // the whole K row's reads in flight before the first fma (read unit by unit, each
+        // later unit waits out its own LDS round trip)
+        u32x4 krow[AL::kRow / 16];
+#pragma unroll
+        for (int u = 0; u < AL::kRow / 16; u++) krow[u] = kr[u];
+        asm volatile("" ::: "memory");
         float acc = 0.0f;
 #pragma unroll
         for (int u = 0; u < AL::kRow / 16; u++) {
-          const u32x4 k4 = kr[u];
+          const u32x4 k4 = krow[u];
           const uint32_t a[4] = {k4.x, k4.y, k4.z, k4.w};
 #pragma unroll
           for (int c = 0; c < 4; c++) {
@@ -535,23 +541,31 @@ __device__ __forceinline__ bool attn_worker(const StepParams& P, uint8_t* smem, 
             else o = fmaf(e[j], __uint_as_float(v[j]), o);
           }
         };
-        // kRot register groups in rotation (kRot - 1 groups' reads in flight); the empty asm
-        // statements keep the compiler from moving a group's reads down to its fold
+        // kRot register groups in rotation (kRot - 1 groups' reads in flight).  Whole
+        // rotations run without an exit (an exit inside one makes every fold wait for all
+        // reads in flight), then the last ng % kRot groups, already read into slots 0, 1, 2
         constexpr int kRot = 4;
         if (ng > 0) {
           Grp g[kRot];
 #pragma unroll
           for (int k = 0; k < kRot - 1; k++) rd(k, g[k]);
+          const int ngf = ng & ~(kRot - 1);
 #pragma unroll 1
-          for (int gi = 0; gi < ng; gi += kRot) {
+          for (int gi = 0; gi < ngf; gi += kRot) {
 #pragma unroll
             for (int k = 0; k < kRot; k++) {
               rd(gi + k + kRot - 1, g[(k + kRot - 1) % kRot]);
-              asm volatile("" ::: "memory");
-              if (gi + k >= ng) break;
+              // the chain value through an empty statement after the reads: the fold
+              // cannot be hoisted above them, so kRot - 1 groups stay in flight
+              asm volatile("" : "+v"(o) : : "memory");
               fold8(g[k]);
             }
           }
+          const int rem = ng - ngf;
+          static_assert(kRot == 4, "the tail takes slots 0 .. 2");
+          if (rem > 0) fold8(g[0]);
+          if (rem > 1) fold8(g[1]);
+          if (rem > 2) fold8(g[2]);
         }
         for (int p = ng * 8; p < n; p++) o = fmaf(ss[p], kv_at<kF16>(vrow + p * AL::kEsz), o);
       }
