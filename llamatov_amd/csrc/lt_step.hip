@@ -692,11 +692,12 @@ __device__ __forceinline__ bool gemv_worker(const StepParams& P, uint8_t* smem, 
         for (int k = 0; k < 4; k++) xv[k] = __uint_as_float(v[k]);
       }
       if (wg_any(!ok, slots, par)) return false;
-      const float inv = rms_inv4(xv, E, P.eps, red);
+      // x into LDS before the norm's reduction: its barrier also publishes xs (the last
+      // reads of xs, the previous phase's norm_to_rec, ended at a barrier since)
 #pragma unroll
       for (int k = 0; k < 4; k++)
         if (t + kT * k < E) xs[t + kT * k] = xv[k];
-      lds_barrier();
+      const float inv = rms_inv4(xv, E, P.eps, red);
       norm_to_rec(xs, nw4, inv, E, rec);
       lds_barrier();
       // the record's reads all in flight before the first dot (fold_raw, read by read, waits
@@ -777,11 +778,12 @@ __device__ __forceinline__ bool gemv_worker(const StepParams& P, uint8_t* smem, 
       float xv[4];
 #pragma unroll
       for (int k = 0; k < 4; k++) xv[k] = __uint_as_float(v[k]);
-      const float inv = rms_inv4(xv, E, P.eps, red);
+      // x into LDS before the norm's reduction: its barrier also publishes xs (the last
+      // reads of xs, the previous phase's norm_to_rec, ended at a barrier since)
 #pragma unroll
       for (int k = 0; k < 4; k++)
         if (t + kT * k < E) xs[t + kT * k] = xv[k];
-      lds_barrier();
+      const float inv = rms_inv4(xv, E, P.eps, red);
       norm_to_rec(xs, nw4, inv, E, rec);
       lds_barrier();
       const uint32_t* ra = rec + (lane < nbE ? lane : 0) * kRecDwords;
