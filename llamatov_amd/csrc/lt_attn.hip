@@ -742,37 +742,42 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
     asm volatile("" ::: "memory");
     // prefetch: the round decltype(prefetch)::value rounds ahead into the same registers (0: none)
     if constexpr (decltype(prefetch)::value > 0) load_round(t0 + decltype(prefetch)::value * kPR, buf);
-    // passes of kHg heads over this lane's K row in LDS; within a pass, K unit u and q of
-    // unit u (kQu dims per head) are read one unit ahead of their use, and the fence keeps
-    // the compiler from hoisting more
+    // passes of kHg heads over this lane's K row in LDS (K unit u with q of unit u, kQu dims
+    // per head)
     constexpr int kHg = kHL < 2 ? kHL : 2;
     constexpr int kQu = kF16 ? 8 : 4;
     // stored unconditionally (lanes past the range write the spare row), so the
     // chains are computed in place rather than sunk into branches
     const int t = t0 + lr;
     const int ts = t < n ? t : srow;
+    // units in flight: kUD - 1 units' K and q reads ahead of the unit being folded (one
+    // head per lane has the registers for 3 ahead; each unit's fmas are tied to the reads
+    // before them through the chains, so the compiler cannot hoist them above the reads and
+    // wait out one LDS round trip per unit)
+    constexpr int kUD = kHg == 1 ? 4 : 2;
 #pragma unroll
     for (int g0 = 0; g0 < kHL; g0 += kHg) {
       float acc[kHg];
-      float qc[kHg][kQu], qn[kHg][kQu];
-      u32x4 kc = sk[lr * (KU + 1)], kn;
+      float qb[kUD][kHg][kQu];
+      u32x4 kb_[kUD];
+      auto read_unit = [&](int u, int slot) {
+        kb_[slot] = sk[lr * (KU + 1) + u];
 #pragma unroll
-      for (int r = 0; r < kHg; r++) {
-        acc[r] = 0.0f;
+        for (int r = 0; r < kHg; r++)
 #pragma unroll
-        for (int i = 0; i < kQu; i++) qc[r][i] = sq[(hb + g0 + r) * HD + i];
-      }
+          for (int i = 0; i < kQu; i++) qb[slot][r][i] = sq[(hb + g0 + r) * HD + u * kQu + i];
+      };
+#pragma unroll
+      for (int r = 0; r < kHg; r++) acc[r] = 0.0f;
+#pragma unroll
+      for (int u = 0; u < kUD - 1 && u < KU; u++) read_unit(u, u);
 #pragma unroll
       for (int u = 0; u < KU; u++) {
-        asm volatile("" ::: "memory");
-        uint32_t a[4] = {kc.x, kc.y, kc.z, kc.w};
-        if (u + 1 < KU) {
-          kn = sk[lr * (KU + 1) + u + 1];
+        if (u + kUD - 1 < KU) read_unit(u + kUD - 1, (u + kUD - 1) % kUD);
 #pragma unroll
-          for (int r = 0; r < kHg; r++)
-#pragma unroll
-            for (int i = 0; i < kQu; i++) qn[r][i] = sq[(hb + g0 + r) * HD + (u + 1) * kQu + i];
-        }
+        for (int r = 0; r < kHg; r++) asm volatile("" : "+v"(acc[r]) : : "memory");
+        const int sl = u % kUD;
+        uint32_t a[4] = {kb_[sl].x, kb_[sl].y, kb_[sl].z, kb_[sl].w};
 #pragma unroll
         for (int c = 0; c < 4; c++) {
           if (kF16) {
@@ -780,20 +785,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
             const float k1 = lt_h2f((uint16_t)(a[c] >> 16));
 #pragma unroll
             for (int r = 0; r < kHg; r++) {
-              acc[r] = fmaf(qc[r][2 * c], k0, acc[r]);
-              acc[r] = fmaf(qc[r][2 * c + 1], k1, acc[r]);
+              acc[r] = fmaf(qb[sl][r][2 * c], k0, acc[r]);
+              acc[r] = fmaf(qb[sl][r][2 * c + 1], k1, acc[r]);
             }
           } else {
             const float k0 = __builtin_bit_cast(float, a[c]);
 #pragma unroll
-            for (int r = 0; r < kHg; r++) acc[r] = fmaf(qc[r][c], k0, acc[r]);
+            for (int r = 0; r < kHg; r++) acc[r] = fmaf(qb[sl][r][c], k0, acc[r]);
           }
         }
-#pragma unroll
-        for (int r = 0; r < kHg; r++)
-#pragma unroll
-          for (int i = 0; i < kQu; i++) qc[r][i] = qn[r][i];
-        kc = kn;
       }
 #pragma unroll
       for (int r = 0; r < kHg; r++) se[ts * HPW + hb + g0 + r] = acc[r] * A.scale;
