@@ -428,6 +428,204 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSL >= 2 ? 
   }
 }
 
+// Leaf-split tiled GEMM, for launches with few tiles (the batched decode step: tens of
+// tokens).  A workgroup of 4 waves takes one 32-row x 32-token tile, so a launch has four
+// times the waves of k_q8_gemm's, and each wave folds a quarter of the tile's leaves.  The
+// GEMV's tree (halfwave_tree_dpp) pairs lanes l and l+16, then +8, +4, +2, +1, so the 8
+// leaves L = w, w+4, ..., w+28 form the subtree of its level-3 partial d_w:
+//   b(L) = a(L) + a(L+16),  c(L) = b(L) + b(L+8),  d_w = c(w) + c(w+4);
+// wave w folds its leaves (the fma chains over blocks L, L+32, ... as in k_q8_gemm) in that
+// subtree's post-order -- L = w, w+16, w+8, w+24, w+4, w+20, w+12, w+28 -- closing each
+// pair in place, and wave 0 adds the last two levels from LDS: (d0 + d2) + (d1 + d3).  Every
+// element is the single-token GEMV's, bit for bit.
+template <GemmEpi EPI>
+__global__ __launch_bounds__(256) void k_q8_gemm_ls(GemmParams P) {
+  __shared__ float s_d[3][16 * 64];                 // d_1 .. d_3 of the tile
+  // the wave index through readfirstlane: everything derived from it (the leaves, the block
+  // offsets, the buffer resources) is then wave-uniform, and no buffer load is a waterfall
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63;
+  const int h = l >> 5;
+  const int c = l & 31;
+  // XCD-aware tile order, as k_q8_gemm's: the token tiles of one row tile share an XCD
+  const int g = blockIdx.x;
+  const int rt = (g / (8 * P.ntt)) * 8 + (g & 7);
+  const int tt = (g >> 3) % P.ntt;
+  if (rt >= P.nrt) return;   // uniform per workgroup
+  const int n0 = rt * 32;
+  const int t0 = tt * 32;
+  const int nb = P.K >> 5;
+  const int btok = t0 + c < P.T ? t0 + c : P.T - 1;
+
+  struct Ops {
+    v4i w03, bq;
+    uint32_t wdw, xdw;
+  };
+  const uint8_t* wbase = P.W + (size_t)rt * (size_t)nb * kTileBlk;
+  const uint32_t mat_bytes = (uint32_t)nb * kTileBlk;
+  const uint32_t aq_v = (uint32_t)c * 32u + 16u * (uint32_t)h;
+  const uint32_t ad_v = h ? kNoBlk : kTileQ + 2u * (uint32_t)c;
+  const uint32_t bq_v = (uint32_t)btok * 32u + 16u * (uint32_t)h;
+  const uint32_t bd_v = h ? kNoBlk : (uint32_t)btok * 2u;
+  const uint32_t x_bytes = (uint32_t)P.T * (uint32_t)P.K;
+  const uint32_t xd_bytes = (uint32_t)P.T * (uint32_t)nb * 2u;
+  // block b's operands (b < 0: resources of no records, every load reads zeros)
+  auto load_ops = [&](int b, Ops& o) {
+    const bool real = b >= 0;
+    const __amdgpu_buffer_rsrc_t wr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)wbase, 0, real ? (int)mat_bytes : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)P.Xq, 0, real ? (int)x_bytes : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t xdr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)P.Xd, 0, real ? (int)((xd_bytes + 3u) & ~3u) : 0, 0x00020000);
+    const int bb = real ? b : 0;
+    const int sa = (int)((uint32_t)bb * kTileBlk);
+    const int sq = (int)((uint32_t)bb * (uint32_t)P.T * 32u);
+    const int sd = (int)((uint32_t)bb * (uint32_t)P.T * 2u);
+    o.w03 = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)aq_v, sa, 0));
+    o.wdw = __builtin_amdgcn_raw_buffer_load_b16(wr, (int)ad_v, sa, 0);
+    o.bq = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)bq_v, sq, 0));
+    o.xdw = __builtin_amdgcn_raw_buffer_load_b16(xdr, (int)bd_v, sd, 0);
+  };
+  // the wave's leaves in its subtree's post-order (L = wave + 4 * kOrd[i])
+  auto leaf_of = [&](int i) {
+    const int k = (i & 1) * 4 + ((i >> 1) & 1) * 2 + (i >> 2);   // 0, 4, 2, 6, 1, 5, 3, 7
+    return wave + 4 * k;
+  };
+  // producer: position pi (0..7) of the post-order, next block pb (-1: done)
+  int pi = 0, pb = wave;
+  while (pb >= nb) {                                // leading empty leaves
+    if (++pi == 8) { pb = -1; break; }
+    pb = leaf_of(pi);
+  }
+  const int first_pi = pi;
+  auto produce = [&](Ops& o) {
+    load_ops(pb, o);
+    if (pb >= 0) {
+      pb += 32;
+      while (pb >= nb) {
+        if (++pi == 8) { pb = -1; break; }
+        pb = leaf_of(pi);
+      }
+    }
+  };
+  // blocks of the wave: every leaf's count
+  int total = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int L = wave + 4 * i;
+    total += L < nb ? (nb - L + 31) / 32 : 0;
+  }
+  constexpr int kR = 4;                             // blocks in flight
+  Ops ring[kR];
+#pragma unroll
+  for (int d = 0; d < kR; d++) produce(ring[d]);
+
+  float a[16], s0[16], s1[16], s2[16];
+#pragma unroll
+  for (int r = 0; r < 16; r++) { a[r] = 0.0f; s0[r] = 0.0f; s1[r] = 0.0f; s2[r] = 0.0f; }
+  // close the leaf at post-order position i (a holds its value): the subtree's pairings
+  auto close_leaf = [&](int i) {
+    // (static register arrays in every branch: a pointer to one would put them in scratch)
+    switch (i) {
+      case 0:
+#pragma unroll
+        for (int r = 0; r < 16; r++) s0[r] = a[r];
+        break;
+      case 2:
+      case 4:
+#pragma unroll
+        for (int r = 0; r < 16; r++) s1[r] = a[r];
+        break;
+      case 6:
+#pragma unroll
+        for (int r = 0; r < 16; r++) s2[r] = a[r];
+        break;
+      case 1:
+#pragma unroll
+        for (int r = 0; r < 16; r++) s0[r] = s0[r] + a[r];
+        break;
+      case 3:
+#pragma unroll
+        for (int r = 0; r < 16; r++) { s1[r] = s1[r] + a[r]; s0[r] = s0[r] + s1[r]; }
+        break;
+      case 5:
+#pragma unroll
+        for (int r = 0; r < 16; r++) s1[r] = s1[r] + a[r];
+        break;
+      default:   // 7
+#pragma unroll
+        for (int r = 0; r < 16; r++) { s2[r] = s2[r] + a[r]; s1[r] = s1[r] + s2[r]; s0[r] = s0[r] + s1[r]; }
+        break;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) a[r] = 0.0f;
+  };
+  // leading empty leaves close with a = 0
+  for (int i = 0; i < first_pi; i++) close_leaf(i);
+  int ci = first_pi, cb = ci < 8 ? leaf_of(ci) : 0;   // consumer: position, block
+  const v16i z = {};
+  const v16f zf = {};
+  // whole groups of kR slots, every slot folded: past the wave's last block a slot holds
+  // zeros (fma(0, 0, a) = a, and a is +0 once every leaf is closed), so the body has no
+  // per-slot test and each fold waits for its own slot's loads only
+  for (int s = 0; s < total; s += kR) {
+#pragma unroll
+    for (int d = 0; d < kR; d++) {
+      const v16i isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(ring[d].w03, ring[d].bq, z, 0, 0, 0);
+      const u32x2 aw = {ring[d].wdw, 0u}, bw = {ring[d].xdw, 0u};
+      const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(h4, aw), __builtin_bit_cast(h4, bw), zf,
+                                                             0, 0, 0);
+      produce(ring[d]);
+#pragma unroll
+      for (int r = 0; r < 16; r++) a[r] = fmaf(sc[r], (float)isum[r], a[r]);
+      if (ci < 8) {                                 // uniform
+        cb += 32;
+        if (cb >= nb) {                             // the leaf is complete; close it and any empty ones after
+          close_leaf(ci);
+          while (++ci < 8 && (cb = leaf_of(ci)) >= nb) close_leaf(ci);
+        }
+      }
+    }
+  }
+  // empty leaves at the end (a wave with no blocks at all closes everything here)
+  for (; ci < 8; ci++) close_leaf(ci);
+  // s0 = d_wave; the last two levels on wave 0
+  if (wave > 0) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) s_d[wave - 1][r * 64 + l] = s0[r];
+  }
+  __syncthreads();
+  if (wave > 0) return;
+  float v[16];
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const float e0 = s0[r] + s_d[1][r * 64 + l];               // d0 + d2
+    const float e1 = s_d[0][r * 64 + l] + s_d[2][r * 64 + l];  // d1 + d3
+    v[r] = e0 + e1;
+  }
+  const int t = t0 + c;
+  if (t >= P.T) return;
+  if constexpr (EPI == GE_SILU) {
+    const int F = P.N >> 1;
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) {
+      const int n = n0 + c_row(r, h);
+      if (n < P.N) P.Y[(size_t)t * F + (n >> 1)] = lt_silu_mul(v[r], v[r + 1]);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int n = n0 + c_row(r, h);
+      if (n < P.N) {
+        float o = v[r];
+        if constexpr (EPI == GE_BIAS) o = o + P.bias[n];
+        if constexpr (EPI == GE_RESID) o = o + P.resid[(size_t)t * P.N + n];
+        P.Y[(size_t)t * P.N + n] = o;
+      }
+    }
+  }
+}
+
 // RoPE of T rows of q|k at positions *pos0 + t (k_rope's arithmetic per token).
 __global__ __launch_bounds__(256) void k_rope_batch(float* __restrict__ x, int T, int row_stride,
                                                     const int* __restrict__ pos0, int nheads, int hd,
@@ -603,9 +801,34 @@ int check_gemm(const char* fn, const void* W, const int8_t* Xq, const uint16_t* 
   return LT_OK;
 }
 
+// LT_GEMM_LS=0 keeps every launch on k_q8_gemm (for comparisons), 1 sends every tiled launch
+// to the leaf-split kernel.  By default a tiled launch takes it when it holds at most kLsMaxT
+// tokens, or when k_q8_gemm's grid (64-token tiles) would hold fewer than kLsFill workgroups per
+// CU: there the leaf-split kernel's four times as many waves per tile fill the chip.  Measured
+// per launch, k_q8_gemm / leaf-split (us): 896 x 4864 at T = 512 40.5 / 15.4, 1152 x 896 at
+// 512 19.7 / 10.6, 9728 x 896 at 128 22.1 / 18.4 but at 256 28.3 / 31.7, 4096 x 4096 at 256
+// 30.6 / 27.7 but at 512 40.7 / 46.6, 151936 x 896 at 128 169 / 206.
+constexpr int kLsMaxT = 64;
+constexpr int kLsFill = 4;
+int ls_mode() {
+  const char* s = getenv("LT_GEMM_LS");
+  return s ? atoi(s) : -1;
+}
+
 template <GemmEpi EPI, bool kTiled>
 int launch_gemm(lt_ctx* ctx, GemmParams P) {
   P.nrt = (P.N + 31) / 32;
+  if constexpr (kTiled) {
+    const int mode = ls_mode();
+    const long wgs64 = (long)((P.nrt + 7) / 8) * 8 * ((P.T + kGemmTokens - 1) / kGemmTokens);
+    const long fill = (long)kLsFill * (ctx->num_cus > 0 ? ctx->num_cus : 256);
+    if (mode == 1 || (mode < 0 && (P.T <= kLsMaxT || wgs64 < fill))) {
+      P.ntt = (P.T + 31) / 32;
+      const long gls = (long)((P.nrt + 7) / 8) * 8 * P.ntt;
+      k_q8_gemm_ls<EPI><<<(unsigned)gls, 256, 0, ctx->stream>>>(P);
+      return lt_check_launch("k_q8_gemm_ls");
+    }
+  }
   P.ntt = (P.T + kGemmTokens - 1) / kGemmTokens;
   const long grid = (long)((P.nrt + 7) / 8) * 8 * P.ntt;
   if constexpr (kTiled) {

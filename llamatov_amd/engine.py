@@ -1388,7 +1388,11 @@ class StepGraph:
 # the batched step's linear layers: the multi-token GEMV up to here, the GEMM above (C2, graph
 # replays: GEMV 5922 / 17969 / 25527 / 33741 tok/s at B = 8 / 32 / 64 / 128, GEMM 2590 / 10107
 # / 19686 / 38195)
-MULTI_GEMV_MAX_BATCH = 64
+# from this many sequences the step's gate|up, down and vocab projections run the tiled GEMM
+# (linear "mixed"); measured C2 step tok/s, GEMV / mixed / GEMM: B = 16 13062 / 11650 / 9402,
+# 32 21101 / 22344 / 18199, 48 26489 / 30827 / 25841, 64 30078 / 38863 / 33737,
+# 96 - / 37074 / 29471, 128 - / 47522 / 38567
+MIXED_MIN_BATCH = 32
 class BatchDecodePlan:
     """B sequences decoded together (the reference's future-work note on batching its
     device-uniform path, bpd/lib/dev_residency.py:1344-1350).  Each step takes the next token
@@ -1406,10 +1410,12 @@ class BatchDecodePlan:
                  max_ctx: int | None = None, hist_cap: int = 4096, linear: str = "auto"):
         """linear: "gemv" runs the step's linear layers through the multi-token GEMV
         (lt_q8_gemv_multi: GGUF-layout weights, row-major quants, each weight block read once
-        per 8 tokens), "gemm" through the prefill GEMM (tile-major weights), "auto" picks the
-        GEMV up to MULTI_GEMV_MAX_BATCH sequences.  Same bits either way."""
+        per 8 tokens), "gemm" through the prefill GEMM (tile-major weights), "mixed" QKV and O
+        through the GEMV and the rest through the GEMM; "auto" picks the GEMV below
+        MIXED_MIN_BATCH sequences and "mixed" from there on.
+        Same bits every way."""
         assert_certified_composition(profile)
-        if linear not in ("auto", "gemv", "gemm"):
+        if linear not in ("auto", "gemv", "gemm", "mixed"):
             raise ValueError(f"linear={linear!r}")
         if profile.numerics != "engine":
             raise ValueError("batched decode runs the engine's numerics")
@@ -1419,7 +1425,9 @@ class BatchDecodePlan:
             raise ValueError(f"batch={batch}")
         self.model, self.cfg, self.profile, self.dev = model, model.cfg, profile, model.dev
         self.B = int(batch)
-        self.linear = linear if linear != "auto" else ("gemv" if self.B <= MULTI_GEMV_MAX_BATCH else "gemm")
+        if linear == "auto":
+            linear = "gemv" if self.B < MIXED_MIN_BATCH else "mixed"
+        self.linear = linear
         cfg, D = self.cfg, self.dev
         E, F, B = cfg.n_embd, cfg.n_ff, self.B
         self.max_ctx = int(max_ctx or cfg.max_ctx)
@@ -1538,8 +1546,8 @@ class BatchDecodePlan:
     # -- the batched step -----------------------------------------------------------
     def enqueue_step(self) -> None:
         """Launch one token of every sequence: embed -> layers -> vocab GEMM -> row argmax."""
-        if self.linear == "gemv":
-            self._enqueue_step_gemv()
+        if self.linear in ("gemv", "mixed"):
+            self._enqueue_step_gemv(mixed=self.linear == "mixed")
             return
         cfg, m, p, B = self.cfg, self.model, self.profile, self.B
         h = self.dev.handle
@@ -1570,10 +1578,13 @@ class BatchDecodePlan:
         call("lt_argmax_rows", h, self.logits.vp, B, V, self.toks.vp, self.hist.vp, self.hist_count.vp,
              self.hist_cap)
 
-    def _enqueue_step_gemv(self) -> None:
+    def _enqueue_step_gemv(self, mixed: bool = False) -> None:
         """The step with the multi-token GEMV: 9 launches per layer (the attention writes the O
         projection's activation quants itself), each weight matrix streamed from its GGUF-layout
-        blocks once per group of 2 to 8 sequences."""
+        blocks once per group of 2 to 8 sequences.  mixed: gate|up, down and the vocab
+        projection run the tiled GEMM instead (tile-major weights, block-major quants; the
+        leaf-split kernel at these token counts), whose weight blocks are read once per 32
+        sequences; QKV and O, with the fewest rows, stay on the GEMV."""
         cfg, m, p, B = self.cfg, self.model, self.profile, self.B
         h = self.dev.handle
         E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
@@ -1593,13 +1604,25 @@ class BatchDecodePlan:
             call("lt_attn_decode_rows_q8", h, self.qkv.vp, NQ, kp, vp, attn, None, xq, xd, B, nh, nkv, hd,
                  ctypes.c_float(self.scale), self.max_ctx, p.attn_nsplit, p.kv_dtype, ws, ws_n)
             call("lt_q8_gemv_multi", h, L["wo"].t.vp, xq, xd, B, self.x.vp, self.xres.vp, E, QD, LT_MULTI_RESID)
-            call("lt_rmsnorm_quant_rows", h, self.xres.vp, L["ffn_norm"].vp, xq, xd, B, E, eps)
-            call("lt_q8_gemv_multi", h, L["wgu_il"].t.vp, xq, xd, B, None, self.vbuf.vp, 2 * F, E, LT_MULTI_SILU)
-            call("lt_quant_q8", h, self.vbuf.vp, xq, xd, B * F)
-            call("lt_q8_gemv_multi", h, L["wdown"].t.vp, xq, xd, B, self.xres.vp, self.x.vp, E, F, LT_MULTI_RESID)
+            if mixed:
+                call("lt_rmsnorm_quant_bm", h, self.xres.vp, L["ffn_norm"].vp, xq, xd, B, E, eps)
+                call("lt_q8_gemm_silu_t", h, L["wgu_il_t"].t.vp, xq, xd, self.vbuf.vp, B, F, E)
+                call("lt_quant_q8_bm", h, self.vbuf.vp, xq, xd, B, F)
+                call("lt_q8_gemm_t", h, L["wdown_t"].t.vp, xq, xd, None, self.xres.vp, self.x.vp, B, E, F)
+            else:
+                call("lt_rmsnorm_quant_rows", h, self.xres.vp, L["ffn_norm"].vp, xq, xd, B, E, eps)
+                call("lt_q8_gemv_multi", h, L["wgu_il"].t.vp, xq, xd, B, None, self.vbuf.vp, 2 * F, E,
+                     LT_MULTI_SILU)
+                call("lt_quant_q8", h, self.vbuf.vp, xq, xd, B * F)
+                call("lt_q8_gemv_multi", h, L["wdown"].t.vp, xq, xd, B, self.xres.vp, self.x.vp, E, F,
+                     LT_MULTI_RESID)
         call("lt_len_add_n", h, _vp(self.lens.ptr), 2 * B, 1, self.max_ctx)
-        call("lt_rmsnorm_quant_rows", h, self.x.vp, m.output_norm.vp, xq, xd, B, E, eps)
-        call("lt_q8_gemv_multi", h, m.output.t.vp, xq, xd, B, None, self.logits.vp, V, E, LT_MULTI_STORE)
+        if mixed:
+            call("lt_rmsnorm_quant_bm", h, self.x.vp, m.output_norm.vp, xq, xd, B, E, eps)
+            call("lt_q8_gemm_t", h, self.head.t.vp, xq, xd, None, None, self.logits.vp, B, V, E)
+        else:
+            call("lt_rmsnorm_quant_rows", h, self.x.vp, m.output_norm.vp, xq, xd, B, E, eps)
+            call("lt_q8_gemv_multi", h, m.output.t.vp, xq, xd, B, None, self.logits.vp, V, E, LT_MULTI_STORE)
         call("lt_argmax_rows", h, self.logits.vp, B, V, self.toks.vp, self.hist.vp, self.hist_count.vp,
              self.hist_cap)
 

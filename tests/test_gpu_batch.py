@@ -29,7 +29,7 @@ def weights(cfg):
     return _W[cfg.name]
 
 
-@pytest.mark.parametrize("linear", ["gemv", "gemm"])
+@pytest.mark.parametrize("linear", ["gemv", "gemm", "mixed"])
 @pytest.mark.parametrize("kv_dtype,nsplit", [(LT_KV_F32, 1), (LT_KV_F16, 1), (LT_KV_F16, 4)])
 def test_batch_rows_equal_lone_sequences(gpu, oracle, kv_dtype, nsplit, linear):
     cfg = M.SMALL_QWEN
@@ -82,7 +82,7 @@ def test_batch_rows_equal_lone_sequences(gpu, oracle, kv_dtype, nsplit, linear):
     model.free()
 
 
-@pytest.mark.parametrize("B,linear", [(8, "auto"), (20, "auto"), (20, "gemm")])
+@pytest.mark.parametrize("B,linear", [(8, "auto"), (20, "auto"), (20, "gemm"), (40, "auto")])
 def test_batch_generate_c2_geometry(gpu, B, linear):
     """batch_generate at the C2 model (Qwen2.5-0.5B geometry, B sequences of ragged prompts,
     multi-token GEMV or GEMM linear layers) equals generate per sequence."""
