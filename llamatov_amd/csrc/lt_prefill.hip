@@ -117,7 +117,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSL >= 2 ? 
   const uint32_t bd_v = h ? kNoBlk : (uint32_t)btok * 2u;
   const uint32_t x_bytes = (uint32_t)P.T * (uint32_t)P.K;
   const uint32_t xd_bytes = (uint32_t)P.T * (uint32_t)nb * 2u;
-  auto load_ops = [&](int b, bool real, Ops& o) {
+  // scale loads in chain pairs (grouped walks): lanes of the second k half fetch the scales
+  // of the next block of the leaf's chain (32 blocks on) instead of reading zeros
+  const uint32_t ad2_v = kTileQ + 2u * (uint32_t)c + (h ? 32u * kTileBlk : 0u);
+  const uint32_t bd2_v = (uint32_t)btok * 2u + (h ? 64u * (uint32_t)P.T : 0u);
+  // smode: 0 the block's own scales (second k half zero), 1 the chain pair's, 2 none
+  auto load_ops = [&](int b, bool real, Ops& o, int smode = 0) {
     if constexpr (kTiled) {
       // past the last block: resources of no records (every load reads zeros)
       const __amdgpu_buffer_rsrc_t wr =
@@ -130,9 +135,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSL >= 2 ? 
       const int sq = (int)((uint32_t)bb * (uint32_t)P.T * 32u);
       const int sd = (int)((uint32_t)bb * (uint32_t)P.T * 2u);
       o.w03 = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, (int)aq_v, sa, 0));
-      o.wdw = __builtin_amdgcn_raw_buffer_load_b16(wr, (int)ad_v, sa, 0);
+      if (smode != 2) o.wdw = __builtin_amdgcn_raw_buffer_load_b16(wr, (int)(smode ? ad2_v : ad_v), sa, 0);
       o.bq = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)bq_v, sq, 0));
-      o.xdw = __builtin_amdgcn_raw_buffer_load_b16(xdr, (int)bd_v, sd, 0);
+      if (smode != 2) o.xdw = __builtin_amdgcn_raw_buffer_load_b16(xdr, (int)(smode ? bd2_v : bd_v), sd, 0);
     } else {
       const __amdgpu_buffer_rsrc_t wr =
           __builtin_amdgcn_make_buffer_rsrc((void*)P.W, 0, (int)((mat_bytes + 3u) & ~3u), 0x00020000);
@@ -314,41 +319,60 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSL >= 2 ? 
     // i·bpl, slot (i·bpl) % kRD); a slot is refilled with position p + kRD once its MFMAs are
     // issued.  With kRD = 4 the MFMAs of position p + 1 run before position p's fold (result
     // sets A / B by the parity of p).
+    // The scales come in chain pairs: the slot of an even chain position k (bpl and kRD are
+    // even, so slot parity is chain parity) loads the rows' and tokens' scales of blocks k
+    // (lanes h = 0, the scale MFMA's k-slot 0) and k + 1 (lanes h = 1, k-slot 4) -- one load
+    // each for two blocks; block k's scale MFMA keeps the h = 0 halves and k + 1's the h = 1
+    // halves, the other half masked to zero, so each is the single product wd * xd.
     constexpr int kRD = kSL == 1 ? 2 : 4;
     const int bpl = nb >> 5;
+    const uint32_t m_lo = h ? 0u : 0xFFFFFFFFu, m_hi = ~m_lo;
     Ops ring[kRD];
 #pragma unroll
-    for (int d = 0; d < kRD; d++) load_ops(32 * d, true, ring[d]);   // leaf 0's first kRD blocks
+    for (int d = 0; d < kRD; d++) load_ops(32 * d, true, ring[d], (d & 1) ? 2 : 1);   // leaf 0's first kRD blocks
     const v16i z = {};
     const v16f zf = {};
-    auto mfma_t = [&](const Ops& o, v16i& isum, v16f& sc) {
+    // block o's MFMAs with the scale pair's dwords sw (rows) and sx (tokens) masked by m
+    auto mfma_t = [&](const Ops& o, uint32_t sw, uint32_t sx, uint32_t m, v16i& isum, v16f& sc) {
       isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.w03, o.bq, z, 0, 0, 0);
-      const u32x2 aw = {o.wdw, 0u}, bw = {o.xdw, 0u};
+      const u32x2 aw = {sw & m, 0u}, bw = {sx & m, 0u};
       sc = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(h4, aw), __builtin_bit_cast(h4, bw), zf, 0, 0, 0);
     };
     v16i isA, isB;
     v16f scA, scB;
-    if constexpr (kRD == 4) mfma_t(ring[0], isA, scA);
-    // one block from ring slot sl, which is then refilled with the block kRD positions on
-    auto step = [&](auto S, float (&acc)[16], int rb, bool rreal) {
+    uint32_t pw = 0u, px = 0u;   // kRD == 2: the pair's scales for the odd slot
+    if constexpr (kRD == 4) mfma_t(ring[0], ring[0].wdw, ring[0].xdw, m_lo, isA, scA);
+    // one block from ring slot sl, which is then refilled with the block kRD positions on; a
+    // leaf's first block (kFirst) folds into +0.0 as an fma operand, so no register is zeroed
+    auto step = [&](auto S, auto F, float (&acc)[16], int rb, bool rreal) {
       constexpr int sl = decltype(S)::value;
+      constexpr bool kFirst = decltype(F)::value;
+      auto fold = [&](const v16f& sc, const v16i& isum) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[r] = fmaf(sc[r], (float)isum[r], kFirst ? 0.0f : acc[r]);
+      };
       if constexpr (kRD == 2) {
         v16i isum;
         v16f sc;
-        mfma_t(ring[sl], isum, sc);
-        load_ops(rb, rreal, ring[sl]);
-#pragma unroll
-        for (int r = 0; r < 16; r++) acc[r] = fmaf(sc[r], (float)isum[r], acc[r]);
+        if constexpr (sl == 0) {
+          pw = ring[0].wdw;
+          px = ring[0].xdw;
+          mfma_t(ring[0], pw, px, m_lo, isum, sc);
+          load_ops(rb, rreal, ring[0], 1);
+        } else {
+          mfma_t(ring[1], pw, px, m_hi, isum, sc);
+          load_ops(rb, rreal, ring[1], 2);
+        }
+        fold(sc, isum);
       } else if constexpr ((sl & 1) == 0) {
-        mfma_t(ring[(sl + 1) & 3], isB, scB);
-        load_ops(rb, rreal, ring[sl]);
-#pragma unroll
-        for (int r = 0; r < 16; r++) acc[r] = fmaf(scA[r], (float)isA[r], acc[r]);
+        // the odd block sl + 1 from this slot's pair, before the slot is refilled
+        mfma_t(ring[(sl + 1) & 3], ring[sl].wdw, ring[sl].xdw, m_hi, isB, scB);
+        load_ops(rb, rreal, ring[sl], 1);
+        fold(scA, isA);
       } else {
-        mfma_t(ring[(sl + 1) & 3], isA, scA);
-        load_ops(rb, rreal, ring[sl]);
-#pragma unroll
-        for (int r = 0; r < 16; r++) acc[r] = fmaf(scB[r], (float)isB[r], acc[r]);
+        mfma_t(ring[(sl + 1) & 3], ring[(sl + 1) & 3].wdw, ring[(sl + 1) & 3].xdw, m_lo, isA, scA);
+        load_ops(rb, rreal, ring[sl], 2);
+        fold(scB, isB);
       }
     };
     auto leaf = [&](auto J, int i, float (&acc)[16]) {
@@ -357,24 +381,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSL >= 2 ? 
       const int L = leaf_lane(i);
       const int Ln = i < 31 ? leaf_lane(i + 1) : 0;
       // position (i, k) + kRD: the same leaf or the next one (past leaf 31: zeros)
-      auto ref = [&](int k, auto S) {
+      using first = std::true_type;
+      using next = std::false_type;
+      auto ref = [&](int k, auto S, auto F) {
         const bool same = k + kRD < bpl;
-        step(S, acc, same ? L + 32 * (k + kRD) : Ln + 32 * (k + kRD - bpl), same || i < 31);
+        step(S, F, acc, same ? L + 32 * (k + kRD) : Ln + 32 * (k + kRD - bpl), same || i < 31);
       };
-#pragma unroll
-      for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+      // bpl >= kRD: the first kRD blocks are peeled (the leaf's first block starts the chain)
       if constexpr (kRD == 2) {
-        for (int k = 0; k < bpl; k += 2) {
-          ref(k, std::integral_constant<int, 0>{});
-          ref(k + 1, std::integral_constant<int, 1>{});
+        ref(0, std::integral_constant<int, 0>{}, first{});
+        ref(1, std::integral_constant<int, 1>{}, next{});
+        for (int k = 2; k < bpl; k += 2) {
+          ref(k, std::integral_constant<int, 0>{}, next{});
+          ref(k + 1, std::integral_constant<int, 1>{}, next{});
         }
       } else {
-        int k = 0;
-        for (; k + 4 <= bpl; k += 4) {
-          ref(k, std::integral_constant<int, 0>{});
-          ref(k + 1, std::integral_constant<int, 1>{});
-          ref(k + 2, std::integral_constant<int, 2>{});
-          ref(k + 3, std::integral_constant<int, 3>{});
+        ref(0, std::integral_constant<int, 0>{}, first{});
+        ref(1, std::integral_constant<int, 1>{}, next{});
+        ref(2, std::integral_constant<int, 2>{}, next{});
+        ref(3, std::integral_constant<int, 3>{}, next{});
+        for (int k = 4; k + 4 <= bpl; k += 4) {
+          ref(k, std::integral_constant<int, 0>{}, next{});
+          ref(k + 1, std::integral_constant<int, 1>{}, next{});
+          ref(k + 2, std::integral_constant<int, 2>{}, next{});
+          ref(k + 3, std::integral_constant<int, 3>{}, next{});
         }
       }
     };
@@ -803,13 +833,13 @@ int check_gemm(const char* fn, const void* W, const int8_t* Xq, const uint16_t* 
 
 // LT_GEMM_LS=0 keeps every launch on k_q8_gemm (for comparisons), 1 sends every tiled launch
 // to the leaf-split kernel.  By default a tiled launch takes it when it holds at most kLsMaxT
-// tokens, or when k_q8_gemm's grid (64-token tiles) would hold fewer than kLsFill workgroups per
-// CU: there the leaf-split kernel's four times as many waves per tile fill the chip.  Measured
-// per launch, k_q8_gemm / leaf-split (us): 896 x 4864 at T = 512 40.5 / 15.4, 1152 x 896 at
-// 512 19.7 / 10.6, 9728 x 896 at 128 22.1 / 18.4 but at 256 28.3 / 31.7, 4096 x 4096 at 256
-// 30.6 / 27.7 but at 512 40.7 / 46.6, 151936 x 896 at 128 169 / 206.
+// tokens, or when k_q8_gemm's grid (kGemmTokens-token tiles) would hold fewer than kLsFill
+// workgroups per CU: there the leaf-split kernel's 32-token tiles, four waves each, fill the
+// chip.  Measured per launch, k_q8_gemm / leaf-split (us): 896 x 4864 at T = 512 40.5 / 15.4,
+// 1152 x 896 at 512 19.7 / 10.6, 9728 x 896 at 128 22.1 / 18.4 but at 256 28.3 / 31.7,
+// 4096 x 4096 at 256 30.6 / 27.7 but at 512 40.7 / 46.6, 151936 x 896 at 128 169 / 206.
 constexpr int kLsMaxT = 64;
-constexpr int kLsFill = 4;
+constexpr int kLsFill = 2;
 int ls_mode() {
   const char* s = getenv("LT_GEMM_LS");
   return s ? atoi(s) : -1;
@@ -820,9 +850,9 @@ int launch_gemm(lt_ctx* ctx, GemmParams P) {
   P.nrt = (P.N + 31) / 32;
   if constexpr (kTiled) {
     const int mode = ls_mode();
-    const long wgs64 = (long)((P.nrt + 7) / 8) * 8 * ((P.T + kGemmTokens - 1) / kGemmTokens);
+    const long wgs = (long)((P.nrt + 7) / 8) * 8 * ((P.T + kGemmTokens - 1) / kGemmTokens);
     const long fill = (long)kLsFill * (ctx->num_cus > 0 ? ctx->num_cus : 256);
-    if (mode == 1 || (mode < 0 && (P.T <= kLsMaxT || wgs64 < fill))) {
+    if (mode == 1 || (mode < 0 && (P.T <= kLsMaxT || wgs < fill))) {
       P.ntt = (P.T + 31) / 32;
       const long gls = (long)((P.nrt + 7) / 8) * 8 * P.ntt;
       k_q8_gemm_ls<EPI><<<(unsigned)gls, 256, 0, ctx->stream>>>(P);

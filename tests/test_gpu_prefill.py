@@ -173,16 +173,27 @@ def subnormal_scales(rng, W, xd, frac=0.25):
     xd[m] = rng.integers(1, 0x400, m.sum()).astype(np.uint16)
 
 
+def force_walk(monkeypatch, walk: str) -> None:
+    """Pin the tiled GEMM's kernel: "ls" the leaf-split kernel, else k_q8_gemm with the leaf
+    walk LT_GEMM_GROUPED = walk (both read at every launch)."""
+    if walk == "ls":
+        monkeypatch.setenv("LT_GEMM_LS", "1")
+    else:
+        monkeypatch.setenv("LT_GEMM_LS", "0")
+        monkeypatch.setenv("LT_GEMM_GROUPED", walk)
+
+
 @pytest.mark.parametrize("N,K,T,epi", [(1152, 896, 37, "bias"), (896, 4864, 130, "resid"), (100, 96, 5, "store"),
                                        (64, 1024, 129, "store"), (4096, 4096, 33, "store"), (40, 14336, 3, "resid"),
                                        (96, 256, 70, "subnormal"), (64, 2048, 45, "bias"), (72, 6144, 130, "resid"),
-                                       (33, 4096, 7, "subnormal")])
-@pytest.mark.parametrize("grouped", ["2", "1", "0"])
+                                       (33, 4096, 7, "subnormal"), (96, 8192, 77, "subnormal"),
+                                       (130, 14336, 67, "bias")])
+@pytest.mark.parametrize("grouped", ["2", "1", "0", "ls"])
 def test_q8_gemm_tiled_matches_gemv_per_token(gpu, oracle, N, K, T, epi, grouped, monkeypatch):
     """Every leaf walk of the tiled kernel (grouped leaves with a 4- or 2-slot ring where K
-    allows them, the dynamic walk; forced with LT_GEMM_GROUPED) against the oracle's GEMV
-    per token."""
-    monkeypatch.setenv("LT_GEMM_GROUPED", grouped)
+    allows them, the dynamic walk; forced with LT_GEMM_GROUPED) and the leaf-split kernel
+    (forced with LT_GEMM_LS) against the oracle's GEMV per token."""
+    force_walk(monkeypatch, grouped)
     case(f"q8_gemm_t N={N} K={K} T={T} {epi} grouped={grouped}")
     rng = np.random.default_rng(33)
     W = hq8.quantize_rows((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
@@ -210,9 +221,9 @@ def test_q8_gemm_tiled_matches_gemv_per_token(gpu, oracle, N, K, T, epi, grouped
 
 
 @pytest.mark.parametrize("F,K,T", [(4864, 896, 40), (64, 128, 7), (48, 96, 70), (128, 6144, 33), (96, 4096, 140)])
-@pytest.mark.parametrize("grouped", ["2", "1", "0"])
+@pytest.mark.parametrize("grouped", ["2", "1", "0", "ls"])
 def test_q8_gemm_silu_tiled(gpu, oracle, F, K, T, grouped, monkeypatch):
-    monkeypatch.setenv("LT_GEMM_GROUPED", grouped)
+    force_walk(monkeypatch, grouped)
     case(f"q8_gemm_silu_t F={F} K={K} T={T} grouped={grouped}")
     rng = np.random.default_rng(34)
     Wg = hq8.quantize_rows((rng.standard_normal((F, K)) * 0.02).astype(np.float32))
