@@ -459,18 +459,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSL >= 2 ? 
 }
 
 // Leaf-split tiled GEMM, for launches with few tiles (the batched decode step: tens of
-// tokens).  A workgroup of 4 waves takes one 32-row x 32-token tile, so a launch has four
-// times the waves of k_q8_gemm's, and each wave folds a quarter of the tile's leaves.  The
-// GEMV's tree (halfwave_tree_dpp) pairs lanes l and l+16, then +8, +4, +2, +1, so the 8
-// leaves L = w, w+4, ..., w+28 form the subtree of its level-3 partial d_w:
+// tokens).  A workgroup of kW waves (4 or 8) takes one 32-row x 32-token tile, so a launch
+// has kW times the waves of a one-wave-per-tile walk, and each wave folds 32/kW of the
+// tile's leaves.  The GEMV's tree (halfwave_tree_dpp) pairs lanes l and l+16, then +8, +4,
+// +2, +1, so the leaves L = w, w+kW, ..., w+32-kW form the subtree of its partial at level
+// log2(32/kW) -- with kW = 4 the 8 leaves of d_w:
 //   b(L) = a(L) + a(L+16),  c(L) = b(L) + b(L+8),  d_w = c(w) + c(w+4);
 // wave w folds its leaves (the fma chains over blocks L, L+32, ... as in k_q8_gemm) in that
-// subtree's post-order -- L = w, w+16, w+8, w+24, w+4, w+20, w+12, w+28 -- closing each
-// pair in place, and wave 0 adds the last two levels from LDS: (d0 + d2) + (d1 + d3).  Every
+// subtree's post-order -- L = w + kW * bitrev(i) (kW = 4: w, w+16, w+8, w+24, w+4, w+20,
+// w+12, w+28) -- closing each pair in place, and wave 0 adds the remaining levels from LDS,
+// the tree's pairings over the waves' partials (kW = 4: (d0 + d2) + (d1 + d3)).  Every
 // element is the single-token GEMV's, bit for bit.
-template <GemmEpi EPI>
-__global__ __launch_bounds__(256) void k_q8_gemm_ls(GemmParams P) {
-  __shared__ float s_d[3][16 * 64];                 // d_1 .. d_3 of the tile
+template <GemmEpi EPI, int kW>
+__global__ __launch_bounds__(64 * kW) void k_q8_gemm_ls(GemmParams P) {
+  static_assert(kW == 4 || kW == 8, "k_q8_gemm_ls: 4 or 8 waves per tile");
+  constexpr int kNL = 32 / kW;                      // leaves per wave
+  __shared__ float s_d[kW - 1][16 * 64];            // the partials of waves 1 .. kW-1
   // the wave index through readfirstlane: everything derived from it (the leaves, the block
   // offsets, the buffer resources) is then wave-uniform, and no buffer load is a waterfall
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -516,15 +520,16 @@ __global__ __launch_bounds__(256) void k_q8_gemm_ls(GemmParams P) {
     o.bq = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)bq_v, sq, 0));
     o.xdw = __builtin_amdgcn_raw_buffer_load_b16(xdr, (int)bd_v, sd, 0);
   };
-  // the wave's leaves in its subtree's post-order (L = wave + 4 * kOrd[i])
+  // the wave's leaves in its subtree's post-order: L = wave + kW * bitrev(i) over
+  // log2(kNL) bits (kW = 4: offsets 0, 16, 8, 24, 4, 20, 12, 28)
   auto leaf_of = [&](int i) {
-    const int k = (i & 1) * 4 + ((i >> 1) & 1) * 2 + (i >> 2);   // 0, 4, 2, 6, 1, 5, 3, 7
-    return wave + 4 * k;
+    const int k = (int)(__builtin_bitreverse32((uint32_t)i) >> (32 - __builtin_ctz(kNL)));
+    return wave + kW * k;
   };
-  // producer: position pi (0..7) of the post-order, next block pb (-1: done)
+  // producer: position pi (0..kNL-1) of the post-order, next block pb (-1: done)
   int pi = 0, pb = wave;
   while (pb >= nb) {                                // leading empty leaves
-    if (++pi == 8) { pb = -1; break; }
+    if (++pi == kNL) { pb = -1; break; }
     pb = leaf_of(pi);
   }
   const int first_pi = pi;
@@ -533,7 +538,7 @@ __global__ __launch_bounds__(256) void k_q8_gemm_ls(GemmParams P) {
     if (pb >= 0) {
       pb += 32;
       while (pb >= nb) {
-        if (++pi == 8) { pb = -1; break; }
+        if (++pi == kNL) { pb = -1; break; }
         pb = leaf_of(pi);
       }
     }
@@ -541,8 +546,8 @@ __global__ __launch_bounds__(256) void k_q8_gemm_ls(GemmParams P) {
   // blocks of the wave: every leaf's count
   int total = 0;
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const int L = wave + 4 * i;
+  for (int i = 0; i < kNL; i++) {
+    const int L = wave + kW * i;
     total += L < nb ? (nb - L + 31) / 32 : 0;
   }
   constexpr int kR = 4;                             // blocks in flight
@@ -554,8 +559,31 @@ __global__ __launch_bounds__(256) void k_q8_gemm_ls(GemmParams P) {
 #pragma unroll
   for (int r = 0; r < 16; r++) { a[r] = 0.0f; s0[r] = 0.0f; s1[r] = 0.0f; s2[r] = 0.0f; }
   // close the leaf at post-order position i (a holds its value): the subtree's pairings
+  // (static register arrays in every branch: a pointer to one would put them in scratch)
   auto close_leaf = [&](int i) {
-    // (static register arrays in every branch: a pointer to one would put them in scratch)
+    if constexpr (kNL == 4) {
+      switch (i) {
+        case 0:
+#pragma unroll
+          for (int r = 0; r < 16; r++) s0[r] = a[r];
+          break;
+        case 1:
+#pragma unroll
+          for (int r = 0; r < 16; r++) s0[r] = s0[r] + a[r];
+          break;
+        case 2:
+#pragma unroll
+          for (int r = 0; r < 16; r++) s1[r] = a[r];
+          break;
+        default:   // 3
+#pragma unroll
+          for (int r = 0; r < 16; r++) { s1[r] = s1[r] + a[r]; s0[r] = s0[r] + s1[r]; }
+          break;
+      }
+#pragma unroll
+      for (int r = 0; r < 16; r++) a[r] = 0.0f;
+      return;
+    }
     switch (i) {
       case 0:
 #pragma unroll
@@ -592,7 +620,7 @@ __global__ __launch_bounds__(256) void k_q8_gemm_ls(GemmParams P) {
   };
   // leading empty leaves close with a = 0
   for (int i = 0; i < first_pi; i++) close_leaf(i);
-  int ci = first_pi, cb = ci < 8 ? leaf_of(ci) : 0;   // consumer: position, block
+  int ci = first_pi, cb = ci < kNL ? leaf_of(ci) : 0;   // consumer: position, block
   const v16i z = {};
   const v16f zf = {};
   // whole groups of kR slots, every slot folded: past the wave's last block a slot holds
@@ -608,18 +636,19 @@ __global__ __launch_bounds__(256) void k_q8_gemm_ls(GemmParams P) {
       produce(ring[d]);
 #pragma unroll
       for (int r = 0; r < 16; r++) a[r] = fmaf(sc[r], (float)isum[r], a[r]);
-      if (ci < 8) {                                 // uniform
+      if (ci < kNL) {                               // uniform
         cb += 32;
         if (cb >= nb) {                             // the leaf is complete; close it and any empty ones after
           close_leaf(ci);
-          while (++ci < 8 && (cb = leaf_of(ci)) >= nb) close_leaf(ci);
+          while (++ci < kNL && (cb = leaf_of(ci)) >= nb) close_leaf(ci);
         }
       }
     }
   }
   // empty leaves at the end (a wave with no blocks at all closes everything here)
-  for (; ci < 8; ci++) close_leaf(ci);
-  // s0 = d_wave; the last two levels on wave 0
+  for (; ci < kNL; ci++) close_leaf(ci);
+  // s0 = the wave's subtree partial; the remaining levels on wave 0: pairs (w, w + s) for
+  // s = kW/2, ..., 1, each into the lower wave's value
   if (wave > 0) {
 #pragma unroll
     for (int r = 0; r < 16; r++) s_d[wave - 1][r * 64 + l] = s0[r];
@@ -629,9 +658,15 @@ __global__ __launch_bounds__(256) void k_q8_gemm_ls(GemmParams P) {
   float v[16];
 #pragma unroll
   for (int r = 0; r < 16; r++) {
-    const float e0 = s0[r] + s_d[1][r * 64 + l];               // d0 + d2
-    const float e1 = s_d[0][r * 64 + l] + s_d[2][r * 64 + l];  // d1 + d3
-    v[r] = e0 + e1;
+    float t[kW];
+    t[0] = s0[r];
+#pragma unroll
+    for (int w = 1; w < kW; w++) t[w] = s_d[w - 1][r * 64 + l];
+#pragma unroll
+    for (int st = kW / 2; st >= 1; st /= 2)
+#pragma unroll
+      for (int w = 0; w < st; w++) t[w] = t[w] + t[w + st];
+    v[r] = t[0];
   }
   const int t = t0 + c;
   if (t >= P.T) return;
@@ -855,7 +890,16 @@ int launch_gemm(lt_ctx* ctx, GemmParams P) {
     if (mode == 1 || (mode < 0 && (P.T <= kLsMaxT || wgs < fill))) {
       P.ntt = (P.T + 31) / 32;
       const long gls = (long)((P.nrt + 7) / 8) * 8 * P.ntt;
-      k_q8_gemm_ls<EPI><<<(unsigned)gls, 256, 0, ctx->stream>>>(P);
+      // 8 waves per tile when the launch holds at most one tile per CU (LT_GEMM_LS_W=4 / 8
+      // forces one, read at every launch).  Measured at T = 64, 4 / 8 waves (us): 896 x 4864
+      // 13.4 / 8.9, 896 x 896 7.9 / 5.6, 4096 x 4096 13.1 / 10.3, 4096 x 14336 29.4 / 24.7,
+      // but 6144 x 4096 15.2 / 17.4 and 9728 x 896 10.8 / 14.0 (384 and 608 tiles).
+      const char* wenv = getenv("LT_GEMM_LS_W");
+      const int wforce = wenv ? atoi(wenv) : 0;
+      const long cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+      const bool w8 = wforce ? wforce == 8 : gls <= cus;
+      if (w8) k_q8_gemm_ls<EPI, 8><<<(unsigned)gls, 512, 0, ctx->stream>>>(P);
+      else k_q8_gemm_ls<EPI, 4><<<(unsigned)gls, 256, 0, ctx->stream>>>(P);
       return lt_check_launch("k_q8_gemm_ls");
     }
   }

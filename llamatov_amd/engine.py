@@ -1388,11 +1388,12 @@ class StepGraph:
 # the batched step's linear layers: the multi-token GEMV up to here, the GEMM above (C2, graph
 # replays: GEMV 5922 / 17969 / 25527 / 33741 tok/s at B = 8 / 32 / 64 / 128, GEMM 2590 / 10107
 # / 19686 / 38195)
-# from this many sequences the step's gate|up, down and vocab projections run the tiled GEMM
-# (linear "mixed"); measured C2 step tok/s, GEMV / mixed / GEMM: B = 16 13062 / 11650 / 9402,
-# 32 21101 / 22344 / 18199, 48 26489 / 30827 / 25841, 64 30078 / 38863 / 33737,
-# 96 - / 37074 / 29471, 128 - / 47522 / 38567
+# from MIXED_MIN_BATCH sequences the step's gate|up, down and vocab projections run the tiled
+# GEMM (linear "mixed"), past MIXED_MAX_BATCH every projection does ("gemm"); measured C2 step
+# tok/s, GEMV / mixed / GEMM: B = 16 13011 / 12904 / 11212, 32 21067 / 24170 / 21146,
+# 64 30029 / 42102 / 39232, 96 - / 54407 / 53606, 128 37039 / 66689 / 68220
 MIXED_MIN_BATCH = 32
+MIXED_MAX_BATCH = 96
 class BatchDecodePlan:
     """B sequences decoded together (the reference's future-work note on batching its
     device-uniform path, bpd/lib/dev_residency.py:1344-1350).  Each step takes the next token
@@ -1412,7 +1413,7 @@ class BatchDecodePlan:
         (lt_q8_gemv_multi: GGUF-layout weights, row-major quants, each weight block read once
         per 8 tokens), "gemm" through the prefill GEMM (tile-major weights), "mixed" QKV and O
         through the GEMV and the rest through the GEMM; "auto" picks the GEMV below
-        MIXED_MIN_BATCH sequences and "mixed" from there on.
+        MIXED_MIN_BATCH sequences, "mixed" up to MIXED_MAX_BATCH and "gemm" past that.
         Same bits every way."""
         assert_certified_composition(profile)
         if linear not in ("auto", "gemv", "gemm", "mixed"):
@@ -1426,7 +1427,7 @@ class BatchDecodePlan:
         self.model, self.cfg, self.profile, self.dev = model, model.cfg, profile, model.dev
         self.B = int(batch)
         if linear == "auto":
-            linear = "gemv" if self.B < MIXED_MIN_BATCH else "mixed"
+            linear = "gemv" if self.B < MIXED_MIN_BATCH else "mixed" if self.B <= MIXED_MAX_BATCH else "gemm"
         self.linear = linear
         cfg, D = self.cfg, self.dev
         E, F, B = cfg.n_embd, cfg.n_ff, self.B

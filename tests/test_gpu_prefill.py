@@ -174,10 +174,11 @@ def subnormal_scales(rng, W, xd, frac=0.25):
 
 
 def force_walk(monkeypatch, walk: str) -> None:
-    """Pin the tiled GEMM's kernel: "ls" the leaf-split kernel, else k_q8_gemm with the leaf
-    walk LT_GEMM_GROUPED = walk (both read at every launch)."""
-    if walk == "ls":
+    """Pin the tiled GEMM's kernel: "ls" / "ls8" the leaf-split kernel with 4 / 8 waves per
+    tile, else k_q8_gemm with the leaf walk LT_GEMM_GROUPED = walk (read at every launch)."""
+    if walk.startswith("ls"):
         monkeypatch.setenv("LT_GEMM_LS", "1")
+        monkeypatch.setenv("LT_GEMM_LS_W", walk[2:] or "4")
     else:
         monkeypatch.setenv("LT_GEMM_LS", "0")
         monkeypatch.setenv("LT_GEMM_GROUPED", walk)
@@ -188,7 +189,7 @@ def force_walk(monkeypatch, walk: str) -> None:
                                        (96, 256, 70, "subnormal"), (64, 2048, 45, "bias"), (72, 6144, 130, "resid"),
                                        (33, 4096, 7, "subnormal"), (96, 8192, 77, "subnormal"),
                                        (130, 14336, 67, "bias")])
-@pytest.mark.parametrize("grouped", ["2", "1", "0", "ls"])
+@pytest.mark.parametrize("grouped", ["2", "1", "0", "ls", "ls8"])
 def test_q8_gemm_tiled_matches_gemv_per_token(gpu, oracle, N, K, T, epi, grouped, monkeypatch):
     """Every leaf walk of the tiled kernel (grouped leaves with a 4- or 2-slot ring where K
     allows them, the dynamic walk; forced with LT_GEMM_GROUPED) and the leaf-split kernel
@@ -221,7 +222,7 @@ def test_q8_gemm_tiled_matches_gemv_per_token(gpu, oracle, N, K, T, epi, grouped
 
 
 @pytest.mark.parametrize("F,K,T", [(4864, 896, 40), (64, 128, 7), (48, 96, 70), (128, 6144, 33), (96, 4096, 140)])
-@pytest.mark.parametrize("grouped", ["2", "1", "0", "ls"])
+@pytest.mark.parametrize("grouped", ["2", "1", "0", "ls", "ls8"])
 def test_q8_gemm_silu_tiled(gpu, oracle, F, K, T, grouped, monkeypatch):
     force_walk(monkeypatch, grouped)
     case(f"q8_gemm_silu_t F={F} K={K} T={T} grouped={grouped}")
