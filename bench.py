@@ -561,10 +561,12 @@ def cpu_baseline(cfg, weights, prompt, n_decode: int, kv_f16: bool, n_decode_1co
              "tokens_1core_match": toks1 == toks[:n_decode_1core]}, toks)
 
 
-def batched_leg(dev, model, cfg, kv_dtype, batches, prompt_len: int, steps: int, warmup: int) -> list:
+def batched_leg(dev, model, cfg, kv_dtype, batches, prompt_len: int, steps: int, warmup: int,
+                eager: bool = False) -> list:
     """Batched decode (BatchDecodePlan): B sequences with prompt_len-token random prompts,
     prefilled, then `steps` replays of the captured batched step timed with HIP events;
-    aggregate decode tok/s = B * steps / time.  Not the headline (BASELINE's metric is bs=1)."""
+    aggregate decode tok/s = B * steps / time.  Not the headline (BASELINE's metric is bs=1).
+    eager: eager steps (a host synchronization each) instead of graph replays, for traced runs."""
     from llamatov_amd import engine as dr
     from llamatov_amd import model as M
     out = []
@@ -575,19 +577,22 @@ def batched_leg(dev, model, cfg, kv_dtype, batches, prompt_len: int, steps: int,
         try:
             for b in range(B):
                 plan.prefill(b, M.random_prompt(cfg, prompt_len, seed=100 + b))
-            gr.capture()
+            step = plan.step if eager else gr.replay
+            if not eager:
+                gr.capture()
             for _ in range(warmup):
-                gr.replay()
+                step()
             dev.sync()
             ev = Events(dev)
             ev.start()
             for _ in range(steps):
-                gr.replay()
+                step()
             ms = ev.stop_ms()
             dev.sync()
             ev.free()
             out.append({"batch": B, "tok_s": round(B * steps / (ms / 1e3), 1),
-                        "ms_per_step": round(ms / steps, 4), "steps": steps,
+                        "ms_per_step": round(ms / steps, 4), "steps": steps, "linear": plan.linear,
+                        "launch": "eager" if eager else "graph",
                         "context": f"{prompt_len + warmup} .. {prompt_len + warmup + steps}"})
             log(f"batched decode B={B}: {out[-1]['tok_s']} tok/s, {out[-1]['ms_per_step']} ms/step")
         finally:
@@ -903,7 +908,8 @@ def main() -> int:
     batches = [int(b) for b in args.batched.split(",") if b.strip()]
     if batches and not args.per_op:
         log("batched decode leg")
-        result["batched_decode"] = batched_leg(dev, model, cfg, kv_dtype, batches, len(prompt), 64, 8)
+        result["batched_decode"] = batched_leg(dev, model, cfg, kv_dtype, batches, len(prompt), 64, 8,
+                                               eager=args.eager)
     if "c5" in legs:
         model.free()
         log("C5 leg")
