@@ -230,11 +230,13 @@ def step_kernels(dev, plan, only: str | None = None, attn_len: int | None = None
                      bytes=rb(E, F) + F + F // 16 + 8 * E,
                      fn=lambda w, il: call("lt_q8_gemv", h, w.vp, plan.xq.vp, plan.xd.vp, plan.xres.vp, plan.carry.vp,
                                            E, F)),
-        "vocab": dict(kernel="k_gemv_fused<4, PRO_RMS, EPI_ARGMAX> + k_argmax_finalize (lt_q8_gemv_rms_argmax)",
-                      shape=[V, E], mats=[m.output.t], count=1, bytes=rb(V, E) + 8 * E + 4 * V,
-                      fn=lambda w, il: call("lt_q8_gemv_rms_argmax", h, plan.carry.vp, m.output_norm.vp, eps, w.vp,
-                                            plan.logits.vp, V, E, plan.tok.vp, None, None, 0, plan.am_ws.vp,
-                                            plan.am_ws.nbytes)),
+        "vocab": dict(kernel=("k_gemv_fused<16, PRO_RMS, EPI_ARGMAX, planar> + k_argmax_finalize "
+                              "(lt_q8_gemv_rms_argmax_pl)" if plan.head_pl else
+                              "k_gemv_fused<4, PRO_RMS, EPI_ARGMAX> + k_argmax_finalize (lt_q8_gemv_rms_argmax)"),
+                      shape=[V, E], mats=[(plan.head_pl or m.output).t], count=1, bytes=rb(V, E) + 8 * E + 4 * V,
+                      fn=lambda w, il: call("lt_q8_gemv_rms_argmax" + ("_pl" if plan.head_pl else ""), h,
+                                            plan.carry.vp, m.output_norm.vp, eps, w.vp, plan.logits.vp, V, E,
+                                            plan.tok.vp, None, None, 0, plan.am_ws.vp, plan.am_ws.nbytes)),
     }
     if four:
         kinds = {"qkv": kinds4["qkv"], "attn_o": kinds4["attn_o"], "gateup": kinds4["gateup"],

@@ -65,7 +65,7 @@ struct GemvParams {
   void* vc;
   const int* lenr;
   int nkv, kv_f16;
-  int planar;              // W is in the planar layout (lt_q8_to_planar; K % 1024 == 0)
+  int planar;              // W is in the planar layout (lt_q8_to_planar)
   int* len_bump;           // any PRO but PRO_MERGE: block 0 bumps *len_bump (when < maxt) at its end
 };
 
@@ -382,7 +382,7 @@ constexpr uint32_t kNoBlock = 0x80000000u;
 constexpr int kStgRows = 64;
 constexpr int kStgLoads = (kStgRows * 32 * (int)kBlockBytes + 4095) / 4096;   // 17
 constexpr uint32_t kStgBytes = (uint32_t)kStgLoads * 4096u + 16u;   // + the last block's 9th dword
-// Planar weights (kPL, K % 1024 == 0, lt_q8_to_planar): the same ring and item order, each
+// Planar weights (kPL, lt_q8_to_planar): the same ring and item order, each
 // item read as two coalesced non-temporal 16-byte loads per lane plus its scale (lt_q8_device.h,
 // fold_planar); every other stage is unchanged.
 
@@ -461,16 +461,19 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
   RawBlock ring[D];
   int is = 0, ik = 0;                                                   // next item to issue
   uint32_t issue_row = (uint32_t)rbase * (uint32_t)nb * (uint32_t)kBlockBytes;
-  // planar: the item index row*nk + slot, and the scale plane after the N*nb*32 quant bytes
-  uint32_t issue_item = (uint32_t)rbase * (uint32_t)nk;
+  // planar: the row's first block index row*nb (an item starts at (row*nb + 32k)*32 bytes, its
+  // second halves 16m bytes on, m its blocks), and the scale plane after the N*nb*32 quant bytes
+  uint32_t issue_blk = (uint32_t)rbase * (uint32_t)nb;
   const uint32_t scale_base = (uint32_t)P.N * (uint32_t)nb * 32u;
   auto issue = [&](RawBlock& r) {
     const bool real = is < total && lane + 32 * ik < nb;
     if constexpr (kPL) {
-      const uint32_t qo = real ? (issue_item + (uint32_t)ik) * kPlanarItemBytes + (uint32_t)lane * 16u : kNoBlock;
-      const uint32_t so = real ? scale_base + ((issue_item + (uint32_t)ik) * 32u + (uint32_t)lane) * 2u : kNoBlock;
+      const uint32_t k0 = 32u * (uint32_t)ik;
+      const uint32_t m = (uint32_t)nb - k0 < 32u ? (uint32_t)nb - k0 : 32u;
+      const uint32_t qo = real ? (issue_blk + k0) * 32u + (uint32_t)lane * 16u : kNoBlock;
+      const uint32_t so = real ? scale_base + (issue_blk + k0 + (uint32_t)lane) * 2u : kNoBlock;
       const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)qo, 0, 2);
-      const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)(qo + kPlanarItemBytes / 2u), 0, 2);
+      const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(wrsrc, (int)(qo + m * 16u), 0, 2);
       r.w[0] = v0.x; r.w[1] = v0.y; r.w[2] = v0.z; r.w[3] = v0.w;
       r.w[4] = v1.x; r.w[5] = v1.y; r.w[6] = v1.z; r.w[7] = v1.w;
       r.w[8] = __builtin_amdgcn_raw_buffer_load_b16(wrsrc, (int)so, 0, 2);
@@ -484,7 +487,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_fused(GemvParams P) {
       r.w[8] = __builtin_amdgcn_raw_buffer_load_b32(wrsrc, (int)(o4 + 32u), 0, 0);
     }
     is++;
-    if (++ik == nk) { ik = 0; issue_row += row_step_bytes; issue_item += (uint32_t)step * (uint32_t)nk; }
+    if (++ik == nk) { ik = 0; issue_row += row_step_bytes; issue_blk += (uint32_t)step * (uint32_t)nb; }
   };
   if constexpr (!kStg) {
 #pragma unroll
@@ -1255,10 +1258,10 @@ int attn_o_max_len(int nh, int nkv, int hd) {
   return maxL;
 }
 
-// The planar entry points (the *_pl twins): rows of whole 32-block items, and a 16-byte
-// aligned planar copy (lt_q8_to_planar).
+// The planar entry points (the *_pl twins): K a multiple of 32, and a 16-byte aligned
+// planar copy (lt_q8_to_planar).
 int check_planar(const char* fn, const void* W, int K) {
-  LT_REQUIRE(K % 1024 == 0, "%s: K=%d: the planar layout needs K a multiple of 1024", fn, K);
+  LT_REQUIRE(K % 32 == 0, "%s: K=%d: the planar layout needs K a multiple of 32", fn, K);
   LT_REQUIRE(lt_aligned(W, 16), "%s: the planar weight must be 16-byte aligned", fn);
   return LT_OK;
 }

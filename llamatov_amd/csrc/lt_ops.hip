@@ -439,10 +439,11 @@ __global__ __launch_bounds__(256) void k_q8_to_planar(const uint8_t* __restrict_
     w[j] = (uint32_t)b[2 + 4 * j] | ((uint32_t)b[3 + 4 * j] << 8) | ((uint32_t)b[4 + 4 * j] << 16) |
            ((uint32_t)b[5 + 4 * j] << 24);
   const uint32_t row = gi / (uint32_t)nb, blk = gi - row * (uint32_t)nb;
-  const uint32_t item = row * (uint32_t)(nb / 32) + blk / 32u, lane = blk & 31u;
-  uint8_t* q = dst + (size_t)item * kPlanarItemBytes + lane * 16u;
+  const uint32_t k0 = blk & ~31u, lane = blk & 31u;
+  const uint32_t m = (uint32_t)nb - k0 < 32u ? (uint32_t)nb - k0 : 32u;   // blocks of this item
+  uint8_t* q = dst + ((size_t)row * (size_t)nb + k0) * 32u + lane * 16u;
   *(u32x4*)q = u32x4{w[0], w[1], w[2], w[3]};
-  *(u32x4*)(q + kPlanarItemBytes / 2u) = u32x4{w[4], w[5], w[6], w[7]};
+  *(u32x4*)(q + m * 16u) = u32x4{w[4], w[5], w[6], w[7]};
   uint16_t* sc = (uint16_t*)(dst + (size_t)n_blocks * 32u);
   sc[gi] = (uint16_t)(b[0] | (b[1] << 8));
 }
@@ -453,7 +454,7 @@ extern "C" {
 
 int lt_q8_to_planar(lt_ctx* ctx, const void* src, void* dst, int N, int K) {
   LT_REQUIRE(ctx && src && dst, "lt_q8_to_planar: null argument");
-  LT_REQUIRE(N > 0 && K > 0 && K % 1024 == 0 && K <= 16384, "lt_q8_to_planar: N=%d K=%d (K a multiple of 1024, <= 16384)",
+  LT_REQUIRE(N > 0 && K > 0 && K % 32 == 0 && K <= 16384, "lt_q8_to_planar: N=%d K=%d (K a multiple of 32, <= 16384)",
              N, K);
   LT_REQUIRE((uint64_t)N * (uint64_t)(K / 32) * 34u < ((uint64_t)1 << 32), "lt_q8_to_planar: matrix must be below 4 GiB");
   LT_REQUIRE(lt_aligned(dst, 16), "lt_q8_to_planar: dst must be 16-byte aligned");

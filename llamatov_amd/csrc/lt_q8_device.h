@@ -260,18 +260,17 @@ __device__ __forceinline__ float fold_regs(const RawBlock& r, bool odd, const ui
   return fmaf(lt_h2f(d16) * xdv, (float)s, acc);
 }
 
-// Planar Q8_0 layout, for matrices whose rows are whole 32-block items (K % 1024 == 0): the
-// quants of item (row r, slot k) -- blocks 32k .. 32k+31 of row r -- are 1024 contiguous
-// bytes at (r*nk + k)*1024, first the leading 16 quants of each of the 32 blocks (16 bytes
-// per block, in block order), then their trailing 16; the fp16 scales follow the whole quant
-// plane as [N][nb].  A half-wave reads one item with two fully coalesced 512-byte loads and
-// one 64-byte load, and every cache line is consumed by a single load instruction.  Lane L
+// Planar Q8_0 layout (K % 32 == 0): the quants of item (row r, slot k) -- blocks 32k ..
+// 32k+m-1 of row r, m = min(32, nb - 32k) -- are 32m contiguous bytes at (r*nb + 32k)*32,
+// first the leading 16 quants of each of the m blocks (16 bytes per block, in block order),
+// then their trailing 16; the fp16 scales follow the whole quant plane as [N][nb].  With
+// K % 1024 == 0 every item is 1024 bytes at (r*nk + k)*1024.  A half-wave reads a whole item
+// with two coalesced loads of 16m bytes and one of 2m, and every cache line of a full item
+// is consumed by a single load instruction.  Lane L
 // holds block 32k+L as w[0..7] = quants 0..31 in fours and w[8] = the scale bits.  Against
 // the activation record's phase O (dwords kRecPhase+1 .. kRecPhase+8 hold quants 0..31,
 // kRecPhase+9 the scale) the 8 v_dot4_i32_i8 give the same exact isum as fold_raw's 9, and
 // the fma is the same.
-constexpr uint32_t kPlanarItemBytes = 1024;
-
 __device__ __forceinline__ float fold_planar(const RawBlock& r, const uint32_t* rec, float acc) {
   const uint32_t* a = rec + kRecPhase + 1;
   int s = 0;

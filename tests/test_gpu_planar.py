@@ -1,8 +1,8 @@
 """The planar weight layout: lt_q8_to_planar's bytes against a numpy restatement of the
 layout, every *_pl GEMV against its namesake over the GGUF blocks (outputs equal bit for bit,
-and against the oracle where the namesake's tests do not already pin it), the K % 1024
-refusal, and decode through planar copies equal to decode through the blocks and to the
-oracle."""
+and against the oracle where the namesake's tests do not already pin it), rows whose last
+32-block group is partial (K % 1024 != 0), the K % 32 refusal, and decode through planar
+copies equal to decode through the blocks and to the oracle."""
 import ctypes
 
 import numpy as np
@@ -33,12 +33,17 @@ def rand_blocks(rng, N, K):
 
 
 def planar_host(blocks, N, K):
-    """The layout restated: per (row, 32-block group) the leading 16 quants of the 32 blocks,
-    then their trailing 16; then the scales [N][nb]."""
+    """The layout restated: per row, per group of up to 32 blocks (the last group of a row
+    may hold fewer), the leading 16 quants of the group's blocks, then their trailing 16;
+    then the scales [N][nb]."""
     nb = K // 32
-    b = blocks.reshape(N, nb // 32, 32, 34)
-    q = b[..., 2:]                                        # [N][nk][32 blocks][32 quants]
-    quant = np.concatenate([q[..., :16].reshape(N, nb // 32, 512), q[..., 16:].reshape(N, nb // 32, 512)], axis=2)
+    b = blocks.reshape(N, nb, 34)
+    rows = []
+    for k0 in range(0, nb, 32):
+        q = b[:, k0:k0 + 32, 2:]                          # [N][m blocks][32 quants]
+        m = q.shape[1]
+        rows.append(np.concatenate([q[..., :16].reshape(N, 16 * m), q[..., 16:].reshape(N, 16 * m)], axis=1))
+    quant = np.concatenate(rows, axis=1)                  # [N][nb * 32]
     scales = b[..., :2].reshape(N, nb * 2)
     return np.concatenate([quant.reshape(-1), scales.reshape(-1)])
 
@@ -53,7 +58,7 @@ def planar_copy(gpu, W, N, K):
     return t
 
 
-@pytest.mark.parametrize("N,K", [(37, 1024), (8, 14336), (300, 4096)])
+@pytest.mark.parametrize("N,K", [(37, 1024), (8, 14336), (300, 4096), (33, 896), (5, 4864), (7, 32)])
 def test_planar_repack_layout(gpu, N, K):
     case(f"planar repack {N}x{K}")
     blk = rand_blocks(np.random.default_rng(N), N, K)
@@ -67,18 +72,19 @@ def test_planar_repack_layout(gpu, N, K):
 def test_planar_refuses_k_outside_the_layout(gpu):
     case("planar refusal")
     W = dr.DevTensor.empty((64 * 28 * 34,), np.uint8)
-    y = dr.DevTensor.empty((64,), np.float32)
+    y = dr.DevTensor.empty((64 * 28 * 34,), np.uint8)
     xq = dr.DevTensor.empty((896,), np.int8)
     xd = dr.DevTensor.empty((28,), np.uint16)
-    rc = _lib.raw("lt_q8_to_planar")(gpu.handle, W.vp, y.vp, 64, 896)
-    assert rc == -1 and "1024" in _lib.last_error()
-    rc = _lib.raw("lt_q8_gemv_pl")(gpu.handle, W.vp, xq.vp, xd.vp, None, y.vp, 64, 896)
-    assert rc == -1 and "1024" in _lib.last_error()
+    rc = _lib.raw("lt_q8_to_planar")(gpu.handle, W.vp, y.vp, 64, 880)
+    assert rc == -1 and "multiple of 32" in _lib.last_error()
+    rc = _lib.raw("lt_q8_gemv_pl")(gpu.handle, W.vp, xq.vp, xd.vp, None, y.vp, 64, 880)
+    assert rc == -1 and "multiple of 32" in _lib.last_error()
     for t in (W, y, xq, xd):
         t.free()
 
 
-SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336), (6144, 4096), (333, 1024), (1000, 2048)]
+SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336), (6144, 4096), (333, 1024), (1000, 2048), (151936, 896),
+          (896, 4864), (1152, 896), (70, 96)]
 
 
 @pytest.mark.parametrize("N,K", SHAPES)
@@ -107,7 +113,7 @@ def test_planar_gemv_stage_equals_blocks(gpu, oracle, N, K):
         t.free()
 
 
-@pytest.mark.parametrize("N,K", [(6144, 4096), (4096, 4096), (1000, 2048), (5000, 14336)])
+@pytest.mark.parametrize("N,K", [(6144, 4096), (4096, 4096), (1000, 2048), (5000, 14336), (1152, 896), (96, 4864)])
 def test_planar_rms_and_embed_equal_blocks(gpu, N, K):
     """lt_q8_gemv_rms_pl (with a bias and without) and lt_q8_gemv_embed_rms_pl against their
     namesakes."""
@@ -145,7 +151,7 @@ def test_planar_rms_and_embed_equal_blocks(gpu, N, K):
         t.free()
 
 
-@pytest.mark.parametrize("F,K", [(14336, 4096), (2048, 1024)])
+@pytest.mark.parametrize("F,K", [(14336, 4096), (2048, 1024), (4864, 896)])
 def test_planar_rms_silu_equals_blocks(gpu, F, K):
     case(f"planar rms_silu F={F} K={K}")
     rng = np.random.default_rng(F)
@@ -203,7 +209,7 @@ def test_planar_attn_out_equals_blocks(gpu, nsplit):
         t.free()
 
 
-@pytest.mark.parametrize("N,K", [(128256, 4096), (3000, 1024)])
+@pytest.mark.parametrize("N,K", [(128256, 4096), (3000, 1024), (151936, 896)])
 def test_planar_rms_argmax_equals_blocks(gpu, N, K):
     case(f"planar rms_argmax {N}x{K}")
     rng = np.random.default_rng(3)
