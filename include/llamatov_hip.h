@@ -302,13 +302,15 @@ LT_API int lt_q8_gemv_rms_argmax(lt_ctx* ctx, const float* x, const float* nw, f
 LT_API size_t lt_q8_gemv_argmax_workspace_size(int N);
 
 /* ---- the planar weight layout (no counterpart in the reference, whose GEMVs read GGUF
- * blocks; a residency choice of this library for matrices with K % 1024 == 0) -------------
+ * blocks; a residency choice of this library) ----------------------------------------------
  * lt_q8_to_planar repacks a Q8_0 matrix [N][K/32] of 34-byte blocks into dst (the same
- * N*K/32*34 bytes, 16-byte aligned, not overlapping src): per row and 32-block group, the
- * leading 16 quants of the 32 blocks, then their trailing 16 (1024 bytes), and after all N
- * rows the fp16 scales [N][K/32].  Every load instruction of a GEMV over it reads whole,
- * aligned cache lines.  The *_pl entry points are their namesakes above over such a copy
- * (W or Wgu planar; K % 1024 == 0, else LT_EINVAL): the same arguments, arithmetic and bits. */
+ * N*K/32*34 bytes, 16-byte aligned, not overlapping src): per row and group of up to 32
+ * blocks (the row's last group holds K/32 mod 32 blocks when that is not 0), the leading 16
+ * quants of the group's blocks, then their trailing 16 (1024 bytes for a full group), and
+ * after all N rows the fp16 scales [N][K/32].  Every load instruction of a GEMV over it reads
+ * aligned, contiguous bytes.  The *_pl entry points are their namesakes above over such a
+ * copy (W or Wgu planar; K % 32 == 0, else LT_EINVAL): the same arguments, arithmetic and
+ * bits. */
 LT_API int lt_q8_to_planar(lt_ctx* ctx, const void* src, void* dst, int N, int K);
 LT_API int lt_q8_gemv_pl(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd, const float* resid,
                          float* y, int N, int K);
