@@ -1616,7 +1616,7 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
     A.wsz = w.z;
     A.wso = w.o;
   }
-  // decode with 2, 4 or 8 query heads per KV group on a grid of at most 4 workgroups per CU
+  // decode with 2, 4, 7 or 8 query heads per KV group on a grid of at most 4 workgroups per CU
   // (batch 1): one wave per head, K and V staged once per workgroup through LDS.  On larger
   // grids its LDS footprint (3 workgroups per CU at 16k) loses to the single-wave kernel's
   // occupancy (batch 8 at 16k: 105 us against 92).  LT_ATTN_DEC=0 keeps the single-wave
@@ -1627,7 +1627,8 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
   }();
   const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
   const bool dec_on = dec_env == 2 || (dec_env == 1 && (size_t)A.nsplit * A.nkv * rows <= (size_t)4 * cus);
-  if (dec_on && mode == AM_DECODE && (rep == 2 || rep == 4 || rep == 8) && A.hd % 64 == 0 && (dpl == 1 || dpl == 2)) {
+  if (dec_on && mode == AM_DECODE && (rep == 2 || rep == 4 || rep == 7 || rep == 8) && A.hd % 64 == 0 &&
+      (dpl == 1 || dpl == 2)) {
     const size_t per_up = (size_t)(per_max + 63) / 64 * 64;
     const size_t dec_shm = ((size_t)rep * A.hd + 64 * (ku + 1) * 4 + (size_t)rep * (per_up + 64)) * sizeof(float) +
                            2 * 32 * ku * 16;
@@ -1640,9 +1641,9 @@ int launch_attn(lt_ctx* ctx, int mode, bool f16, int hpw, int rows, AttnArgs A, 
     k_attn_dec<F, NW, D><<<grid, 64 * NW, dec_shm, ctx->stream>>>(A);                  \
     e = hipGetLastError();                                                             \
   }
-      LT_DEC_CASE(true, 2, 1) LT_DEC_CASE(true, 4, 1) LT_DEC_CASE(true, 8, 1)
+      LT_DEC_CASE(true, 2, 1) LT_DEC_CASE(true, 4, 1) LT_DEC_CASE(true, 7, 1) LT_DEC_CASE(true, 8, 1)
       LT_DEC_CASE(true, 2, 2) LT_DEC_CASE(true, 4, 2) LT_DEC_CASE(true, 8, 2)
-      LT_DEC_CASE(false, 2, 1) LT_DEC_CASE(false, 4, 1) LT_DEC_CASE(false, 8, 1)
+      LT_DEC_CASE(false, 2, 1) LT_DEC_CASE(false, 4, 1) LT_DEC_CASE(false, 7, 1) LT_DEC_CASE(false, 8, 1)
       LT_DEC_CASE(false, 2, 2) LT_DEC_CASE(false, 4, 2) LT_DEC_CASE(false, 8, 2)
 #undef LT_DEC_CASE
       if (e != hipSuccess) return lt_fail_hip(e, what, __FILE__, __LINE__);
