@@ -463,6 +463,14 @@ LT_API int lt_rmsnorm_quant_rows(lt_ctx* ctx, const float* x, const float* w, in
 LT_API int lt_q8_gemv_multi(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd, int T,
                             const float* add, float* y, int N, int K, int epi);
 
+/* lt_q8_gemv_multi (LT_MULTI_STORE with the bias) over the q|k|v rows of the next token of T
+ * sequences followed by lt_rope_append_seqs of its output, in one launch: qkv [T][N] as the two
+ * calls leave it (q rotated, k and v as computed), the same cache rows written; N = (nh +
+ * 2 nkv) hd, hd a multiple of 8. */
+LT_API int lt_q8_gemv_multi_rope(lt_ctx* ctx, const void* W, const int8_t* xq, const uint16_t* xd, int T,
+                                 const float* bias, float* qkv, int N, int K, const int* len, int nh, int nkv,
+                                 int hd, const float* freqs, void* kc, void* vc, int maxt, int kv_dtype);
+
 /* out[r] = argmax of row r of x [rows][n] (ties to the lowest index, as lt_argmax); with
  * hist, also hist[r][count[r]] = out[r], count[r] += 1 while < cap. */
 LT_API int lt_argmax_rows(lt_ctx* ctx, const float* x, int rows, int n, int* out, int* hist, int* count, int cap);

@@ -1418,10 +1418,10 @@ class StepGraph:
 # / 19686 / 38195)
 # from MIXED_MIN_BATCH sequences the step's gate|up, down and vocab projections run the tiled
 # GEMM (linear "mixed"), past MIXED_MAX_BATCH every projection does ("gemm"); measured C2 step
-# tok/s, GEMV / mixed / GEMM: B = 16 13011 / 12904 / 11212, 32 21067 / 24170 / 21146,
-# 64 30029 / 42102 / 39232, 96 - / 54407 / 53606, 128 37039 / 66689 / 68220
+# tok/s, GEMV / mixed / GEMM: B = 8 8176 / 6974 / 5675, 16 13626 / 13488 / 11194, 32 21951 /
+# 25259 / 21165, 64 31268 / 44419 / 39651, 96 35061 / 57007 / 54339, 128 38245 / 70172 / 69351
 MIXED_MIN_BATCH = 32
-MIXED_MAX_BATCH = 96
+MIXED_MAX_BATCH = 128
 class BatchDecodePlan:
     """B sequences decoded together (the reference's future-work note on batching its
     device-uniform path, bpd/lib/dev_residency.py:1344-1350).  Each step takes the next token
@@ -1608,8 +1608,9 @@ class BatchDecodePlan:
              self.hist_cap)
 
     def _enqueue_step_gemv(self, mixed: bool = False) -> None:
-        """The step with the multi-token GEMV: 9 launches per layer (the attention writes the O
-        projection's activation quants itself), each weight matrix streamed from its GGUF-layout
+        """The step with the multi-token GEMV: 8 launches per layer (the QKV launch also rotates
+        q and k and appends k and v; the attention writes the O projection's activation quants
+        itself), each weight matrix streamed from its GGUF-layout
         blocks once per group of 2 to 8 sequences.  mixed: gate|up, down and the vocab
         projection run the tiled GEMM instead (tile-major weights, block-major quants; the
         leaf-split kernel at these token counts), whose weight blocks are read once per 32
@@ -1626,10 +1627,9 @@ class BatchDecodePlan:
         for il, L in enumerate(m.layers):
             kp, vp = self.k[il].vp, self.v[il].vp
             call("lt_rmsnorm_quant_rows", h, self.x.vp, L["attn_norm"].vp, xq, xd, B, E, eps)
-            call("lt_q8_gemv_multi", h, L["wqkv"].t.vp, xq, xd, B, _vp(L["bqkv"]), self.qkv.vp, NQ, E,
-                 LT_MULTI_STORE)
-            call("lt_rope_append_seqs", h, self.qkv.vp, B, NQ, pos, nh, nkv, hd, m.freqs.vp, kp, vp, self.max_ctx,
-                 p.kv_dtype)
+            # q|k|v + bias, RoPE and the KV append in one launch
+            call("lt_q8_gemv_multi_rope", h, L["wqkv"].t.vp, xq, xd, B, _vp(L["bqkv"]), self.qkv.vp, NQ, E, pos,
+                 nh, nkv, hd, m.freqs.vp, kp, vp, self.max_ctx, p.kv_dtype)
             call("lt_attn_decode_rows_q8", h, self.qkv.vp, NQ, kp, vp, attn, None, xq, xd, B, nh, nkv, hd,
                  ctypes.c_float(self.scale), self.max_ctx, p.attn_nsplit, p.kv_dtype, ws, ws_n)
             call("lt_q8_gemv_multi", h, L["wo"].t.vp, xq, xd, B, self.x.vp, self.xres.vp, E, QD, LT_MULTI_RESID)

@@ -134,6 +134,48 @@ def test_gemv_multi_equals_gemv(gpu, oracle, N, K, T):
         assert bitexact(y.to_host(), want), "silu"
 
 
+@pytest.mark.parametrize("nh,nkv,hd,K", [(14, 2, 64, 896), (8, 2, 128, 1024), (4, 4, 64, 96)])
+@pytest.mark.parametrize("T", [1, 3, 8, 13])
+@pytest.mark.parametrize("kv_dtype", [LT_KV_F16, LT_KV_F32])
+def test_gemv_multi_rope_equals_gemv_then_rope(gpu, nh, nkv, hd, K, T, kv_dtype):
+    """lt_q8_gemv_multi_rope equals lt_q8_gemv_multi (bias) followed by lt_rope_append_seqs:
+    the q|k|v buffer and both caches byte for byte, with positions spread over the cache and
+    one past its end (no append)."""
+    from llamatov_amd import q8 as hq8
+    case(f"gemv_multi_rope nh={nh} nkv={nkv} hd={hd} K={K} T={T} kv={kv_dtype}")
+    rng = np.random.default_rng(T * 7 + nh + kv_dtype)
+    N, maxt = (nh + 2 * nkv) * hd, 40
+    W = dr.DevTensor.from_host(hq8.quantize_rows((rng.standard_normal((N, K)) * 0.05).astype(np.float32)), gpu)
+    xq = dr.DevTensor.from_host(rng.integers(-127, 128, (T, K), dtype=np.int64).astype(np.int8), gpu)
+    xd = dr.DevTensor.from_host((rng.random((T, K // 32)) * 0.05 + 0.01).astype(np.float16).view(np.uint16), gpu)
+    bias = dr.DevTensor.from_host((rng.standard_normal(N) * 0.1).astype(np.float32), gpu)
+    pos = rng.integers(0, maxt, T).astype(np.int32)
+    if T > 2:
+        pos[1] = maxt          # past the cache: rotated q, no append
+    lens = dr.DevTensor.from_host(pos, gpu)
+    freqs = dr.DevTensor.from_host((10000.0 ** (-np.arange(hd // 2) * 2.0 / hd)).astype(np.float32), gpu)
+    eb = 2 if kv_dtype == LT_KV_F16 else 4
+    init = rng.integers(0, 255, T * maxt * nkv * hd * eb, dtype=np.int64).astype(np.uint8)
+    outs = []
+    for fused in (False, True):
+        qkv = dr.DevTensor.empty((T, N), np.float32, gpu)
+        kc, vc = dr.DevTensor.from_host(init, gpu), dr.DevTensor.from_host(init[::-1].copy(), gpu)
+        if fused:
+            call("lt_q8_gemv_multi_rope", gpu.handle, W.vp, xq.vp, xd.vp, T, bias.vp, qkv.vp, N, K, lens.vp, nh, nkv,
+                 hd, freqs.vp, kc.vp, vc.vp, maxt, kv_dtype)
+        else:
+            call("lt_q8_gemv_multi", gpu.handle, W.vp, xq.vp, xd.vp, T, bias.vp, qkv.vp, N, K, 0)
+            call("lt_rope_append_seqs", gpu.handle, qkv.vp, T, N, lens.vp, nh, nkv, hd, freqs.vp, kc.vp, vc.vp, maxt,
+                 kv_dtype)
+        outs.append((qkv.to_host(), kc.to_host(), vc.to_host()))
+        for t in (qkv, kc, vc):
+            t.free()
+    assert bitexact(outs[0][0], outs[1][0]), "q|k|v rows"
+    assert np.array_equal(outs[0][1], outs[1][1]) and np.array_equal(outs[0][2], outs[1][2]), "caches"
+    for t in (W, xq, xd, bias, lens, freqs):
+        t.free()
+
+
 def test_argmax_rows_tie_rule(gpu):
     case("argmax rows")
     rng = np.random.default_rng(5)
