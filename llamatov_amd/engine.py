@@ -1422,6 +1422,10 @@ class StepGraph:
 # 25259 / 21165, 64 31268 / 44419 / 39651, 96 35061 / 57007 / 54339, 128 38245 / 70172 / 69351
 MIXED_MIN_BATCH = 32
 MIXED_MAX_BATCH = 128
+# from this many sequences the vocab projection runs the tiled GEMM in every form; measured
+# 151936 x 896 per launch, multi-token GEMV / tiled GEMM (us): T = 1 32.3 / 54.2, 4 39.2 / 51.5,
+# 6 63.2 / 51.8, 8 73.9 / 55.5, 16 125.6 / 56.8
+HEAD_GEMM_MIN_BATCH = 5
 class BatchDecodePlan:
     """B sequences decoded together (the reference's future-work note on batching its
     device-uniform path, bpd/lib/dev_residency.py:1344-1350).  Each step takes the next token
@@ -1646,7 +1650,7 @@ class BatchDecodePlan:
                 call("lt_q8_gemv_multi", h, L["wdown"].t.vp, xq, xd, B, self.xres.vp, self.x.vp, E, F,
                      LT_MULTI_RESID)
         call("lt_len_add_n", h, _vp(self.lens.ptr), 2 * B, 1, self.max_ctx)
-        if mixed:
+        if mixed or B >= HEAD_GEMM_MIN_BATCH:
             call("lt_rmsnorm_quant_bm", h, self.x.vp, m.output_norm.vp, xq, xd, B, E, eps)
             call("lt_q8_gemm_t", h, self.head.t.vp, xq, xd, None, None, self.logits.vp, B, V, E)
         else:
