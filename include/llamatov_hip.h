@@ -385,6 +385,12 @@ LT_API int lt_q8_gemm_t(lt_ctx* ctx, const void* Wt, const int8_t* Xq, const uin
                         const float* resid, float* Y, int T, int N, int K);
 LT_API int lt_q8_gemm_silu_t(lt_ctx* ctx, const void* Wgut, const int8_t* Xq, const uint16_t* Xd, float* V, int T,
                              int F, int K);
+/* lt_q8_gemm_silu_t followed by lt_quant_q8_bm of its output, in one launch (no fp32 output):
+ * Vq [F/32][T][32], Vd [F/32][T], bit-identical to the two calls; F a multiple of 32, Vq/Vd
+ * not the input's buffers.  For launches of tens of tokens (the batched decode step: its
+ * leaf-split kernel), any T accepted. */
+LT_API int lt_q8_gemm_silu_quant_t(lt_ctx* ctx, const void* Wgut, const int8_t* Xq, const uint16_t* Xd, int8_t* Vq,
+                                   uint16_t* Vd, int T, int F, int K);
 
 /* RoPE (lt_rope_qk's arithmetic) of T rows of q|k, row t at position *pos0 + t; rows are
  * row_stride floats apart and hold nheads contiguous heads of hd. */

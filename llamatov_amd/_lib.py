@@ -105,6 +105,7 @@ _SIGS = {
     "lt_rmsnorm_quant_bm": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_float]),
     "lt_q8_gemm_t": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int]),
     "lt_q8_gemm_silu_t": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int]),
+    "lt_q8_gemm_silu_quant_t": (c_int, [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int]),
     "lt_rope_batch": (c_int, [_P, _P, c_int, c_int, _P, c_int, c_int, _P]),
     "lt_kv_append_batch": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, _P, c_int, c_int, c_int]),
     "lt_len_add": (c_int, [_P, _P, c_int, c_int]),

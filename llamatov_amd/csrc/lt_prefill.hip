@@ -38,6 +38,8 @@ struct GemmParams {
   const float* bias;     // [N] (GE_BIAS)
   const float* resid;    // [T][N] (GE_RESID)
   float* Y;              // [T][N], or [T][N/2] for GE_SILU
+  int8_t* Yq;            // the leaf-split SiLU + quant variant: block-major quants of Y, [N/64][T][32]
+  uint16_t* Yd;          //   and their scales [N/64][T]
   int T, N, K;
   int nrt, ntt;          // row tiles (32 rows), token tiles (kGemmTokens)
 };
@@ -470,22 +472,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSL >= 2 ? 
 // w+12, w+28) -- closing each pair in place, and wave 0 adds the remaining levels from LDS,
 // the tree's pairings over the waves' partials (kW = 4: (d0 + d2) + (d1 + d3)).  Every
 // element is the single-token GEMV's, bit for bit.
-template <GemmEpi EPI, int kW>
-__global__ __launch_bounds__(64 * kW) void k_q8_gemm_ls(GemmParams P) {
+//
+// kQ (SiLU gate|up only): a workgroup of two such halves takes two adjacent row tiles -- 64
+// interleaved rows, the gate/up pairs of one 32-element block of the SiLU output -- and, after
+// each half's tree, quantizes every token's block (the activation quantizer, q8_scale /
+// q8_quant, one half-wave per token) into block-major Yq / Yd, the down projection's input:
+// bit-identical to the SiLU output quantized by lt_quant_q8_bm, with no fp32 round trip.
+template <GemmEpi EPI, int kW, bool kQ = false>
+__global__ __launch_bounds__(64 * kW * (kQ ? 2 : 1)) void k_q8_gemm_ls(GemmParams P) {
   static_assert(kW == 4 || kW == 8, "k_q8_gemm_ls: 4 or 8 waves per tile");
+  static_assert(!kQ || (EPI == GE_SILU && kW == 4), "k_q8_gemm_ls: the quantizing variant is SiLU, 4 waves per tile");
   constexpr int kNL = 32 / kW;                      // leaves per wave
-  __shared__ float s_d[kW - 1][16 * 64];            // the partials of waves 1 .. kW-1
+  __shared__ float s_d[kQ ? 2 : 1][kW - 1][16 * 64];   // the partials of waves 1 .. kW-1 (per half)
   // the wave index through readfirstlane: everything derived from it (the leaves, the block
   // offsets, the buffer resources) is then wave-uniform, and no buffer load is a waterfall
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wall = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int half = kQ ? wall / kW : 0;
+  const int wave = kQ ? wall - half * kW : wall;
   const int l = threadIdx.x & 63;
   const int h = l >> 5;
   const int c = l & 31;
-  // XCD-aware tile order, as k_q8_gemm's: the token tiles of one row tile share an XCD
+  // XCD-aware tile order, as k_q8_gemm's: the token tiles of one row tile share an XCD (kQ:
+  // of one pair of row tiles)
   const int g = blockIdx.x;
-  const int rt = (g / (8 * P.ntt)) * 8 + (g & 7);
+  const int rtg = (g / (8 * P.ntt)) * 8 + (g & 7);
   const int tt = (g >> 3) % P.ntt;
-  if (rt >= P.nrt) return;   // uniform per workgroup
+  if (kQ ? 2 * rtg >= P.nrt : rtg >= P.nrt) return;   // uniform per workgroup
+  const int rt = kQ ? 2 * rtg + half : rtg;
   const int n0 = rt * 32;
   const int t0 = tt * 32;
   const int nb = P.K >> 5;
@@ -651,23 +664,48 @@ __global__ __launch_bounds__(64 * kW) void k_q8_gemm_ls(GemmParams P) {
   // s = kW/2, ..., 1, each into the lower wave's value
   if (wave > 0) {
 #pragma unroll
-    for (int r = 0; r < 16; r++) s_d[wave - 1][r * 64 + l] = s0[r];
+    for (int r = 0; r < 16; r++) s_d[half][wave - 1][r * 64 + l] = s0[r];
   }
   __syncthreads();
+  auto combine = [&](float (&v)[16]) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      float t[kW];
+      t[0] = s0[r];
+#pragma unroll
+      for (int w = 1; w < kW; w++) t[w] = s_d[half][w - 1][r * 64 + l];
+#pragma unroll
+      for (int st = kW / 2; st >= 1; st /= 2)
+#pragma unroll
+        for (int w = 0; w < st; w++) t[w] = t[w] + t[w + st];
+      v[r] = t[0];
+    }
+  };
+  if constexpr (kQ) {
+    // every wave stays to the end (the barriers below are the whole workgroup's)
+    __shared__ float s_o[32][33];                   // [token][SiLU element of the block] (+1 pad)
+    if (wave == 0) {
+      float v[16];
+      combine(v);
+      // rows 2j (gate) and 2j+1 (up) are registers r, r+1 of one lane; this half's rows are
+      // the block's elements half*16 .. half*16 + 15
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) s_o[c][(half * 32 + c_row(r, h)) >> 1] = lt_silu_mul(v[r], v[r + 1]);
+    }
+    __syncthreads();
+    // half-wave q quantizes tokens q and q + 16 of the tile (lane = element of the block)
+    const int q = threadIdx.x >> 5, e = threadIdx.x & 31;
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const int tq = q + 16 * k, t = t0 + tq;
+      if (t < P.T)   // uniform per half-wave
+        quant_block_hw(s_o[tq][e], e, P.Yq + ((size_t)rtg * P.T + t) * 32, P.Yd + (size_t)rtg * P.T + t);
+    }
+    return;
+  }
   if (wave > 0) return;
   float v[16];
-#pragma unroll
-  for (int r = 0; r < 16; r++) {
-    float t[kW];
-    t[0] = s0[r];
-#pragma unroll
-    for (int w = 1; w < kW; w++) t[w] = s_d[w - 1][r * 64 + l];
-#pragma unroll
-    for (int st = kW / 2; st >= 1; st /= 2)
-#pragma unroll
-      for (int w = 0; w < st; w++) t[w] = t[w] + t[w + st];
-    v[r] = t[0];
-  }
+  combine(v);
   const int t = t0 + c;
   if (t >= P.T) return;
   if constexpr (EPI == GE_SILU) {
@@ -948,7 +986,19 @@ int gemm_entry(const char* fn, lt_ctx* ctx, const void* W, const int8_t* Xq, con
   return launch_gemm<GE_STORE, kTiled>(ctx, P);
 }
 
+// The leaf-split SiLU GEMM with the quant of its output fused (k_q8_gemm_ls<GE_SILU, 4, true>):
+// every launch on it, whatever T (its grid: pairs of row tiles x 32-token tiles).
+int launch_gemm_silu_q(lt_ctx* ctx, GemmParams P) {
+  P.nrt = (P.N + 31) / 32;
+  P.ntt = (P.T + 31) / 32;
+  const int npair = P.nrt / 2;
+  const long gls = (long)((npair + 7) / 8) * 8 * P.ntt;
+  k_q8_gemm_ls<GE_SILU, 4, true><<<(unsigned)gls, 512, 0, ctx->stream>>>(P);
+  return lt_check_launch("k_q8_gemm_ls");
+}
+
 template <bool kTiled>
+
 int gemm_silu_entry(const char* fn, lt_ctx* ctx, const void* Wgu, const int8_t* Xq, const uint16_t* Xd, float* V,
                     int T, int F, int K) {
   LT_REQUIRE(ctx && F > 0, "%s: null ctx or F=%d", fn, F);
@@ -1008,6 +1058,22 @@ int lt_q8_gemm_t(lt_ctx* ctx, const void* Wt, const int8_t* Xq, const uint16_t* 
 int lt_q8_gemm_silu_t(lt_ctx* ctx, const void* Wgut, const int8_t* Xq, const uint16_t* Xd, float* V, int T, int F,
                       int K) {
   return gemm_silu_entry<true>("lt_q8_gemm_silu_t", ctx, Wgut, Xq, Xd, V, T, F, K);
+}
+
+int lt_q8_gemm_silu_quant_t(lt_ctx* ctx, const void* Wgut, const int8_t* Xq, const uint16_t* Xd, int8_t* Vq,
+                            uint16_t* Vd, int T, int F, int K) {
+  const char* fn = "lt_q8_gemm_silu_quant_t";
+  LT_REQUIRE(ctx && Vq && Vd, "%s: null argument", fn);
+  LT_REQUIRE(F > 0 && F % 32 == 0, "%s: F=%d (a multiple of 32: whole quant blocks)", fn, F);
+  if (int rc = check_gemm(fn, Wgut, Xq, Xd, (const float*)Vq, T, 2 * F, K)) return rc;
+  LT_REQUIRE(tiles_bytes(2 * F, K) < ((size_t)1 << 31), "%s: tile copy above 2 GiB", fn);
+  LT_REQUIRE((uint64_t)T * (uint64_t)F < ((uint64_t)1 << 31), "%s: T=%d x F=%d output quants above 2 GiB", fn, T, F);
+  LT_REQUIRE((void*)Vq != (const void*)Xq && (const void*)Vd != (const void*)Xd,
+             "%s: the output quants must not overwrite the input quants", fn);
+  GemmParams P{};
+  P.W = (const uint8_t*)Wgut; P.Xq = Xq; P.Xd = Xd; P.Yq = Vq; P.Yd = Vd;
+  P.T = T; P.N = 2 * F; P.K = K;
+  return launch_gemm_silu_q(ctx, P);
 }
 
 int lt_rope_batch(lt_ctx* ctx, float* qk, int T, int row_stride, const int* pos0, int nheads, int hd,

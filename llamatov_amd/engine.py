@@ -1426,6 +1426,12 @@ MIXED_MAX_BATCH = 128
 # 151936 x 896 per launch, multi-token GEMV / tiled GEMM (us): T = 1 32.3 / 54.2, 4 39.2 / 51.5,
 # 6 63.2 / 51.8, 8 73.9 / 55.5, 16 125.6 / 56.8
 HEAD_GEMM_MIN_BATCH = 5
+# up to this many sequences the mixed form's gate|up launch also quantizes its SiLU output
+# (lt_q8_gemm_silu_quant_t: workgroups of two row tiles, 8 waves, one per CU); past it the
+# separate quant launch is cheaper (C2 tok/s fused / separate: B = 32 25894 / 25259, 64 40921
+# / 44419, 128 64023 / 70172: the fused kernel's 8-wave workgroups leave 8 waves per CU where
+# the 4-wave ones fit 12)
+SILU_QUANT_MAX_BATCH = 32
 class BatchDecodePlan:
     """B sequences decoded together (the reference's future-work note on batching its
     device-uniform path, bpd/lib/dev_residency.py:1344-1350).  Each step takes the next token
@@ -1484,6 +1490,10 @@ class BatchDecodePlan:
         self.vbuf = DevTensor.empty((B, F), np.float32, D)
         self.xq = DevTensor.empty((B * kmax,), np.int8, D)
         self.xd = DevTensor.empty((B * kmax // 32,), np.uint16, D)
+        # the mixed form's SiLU output quants (the gate|up launch writes them while its input
+        # quants are still being read, so not into xq / xd)
+        self.vq = DevTensor.empty((B * F,), np.int8, D)
+        self.vd = DevTensor.empty((B * F // 32,), np.uint16, D)
         self.logits = DevTensor.empty((B, cfg.vocab), np.float32, D)
         aw = _lib.raw("lt_attn_workspace_size")(B, cfg.n_head, cfg.head_dim, profile.attn_nsplit)
         self.attn_ws = DevTensor.empty((aw,), np.uint8, D) if aw else None
@@ -1639,9 +1649,16 @@ class BatchDecodePlan:
             call("lt_q8_gemv_multi", h, L["wo"].t.vp, xq, xd, B, self.x.vp, self.xres.vp, E, QD, LT_MULTI_RESID)
             if mixed:
                 call("lt_rmsnorm_quant_bm", h, self.xres.vp, L["ffn_norm"].vp, xq, xd, B, E, eps)
-                call("lt_q8_gemm_silu_t", h, L["wgu_il_t"].t.vp, xq, xd, self.vbuf.vp, B, F, E)
-                call("lt_quant_q8_bm", h, self.vbuf.vp, xq, xd, B, F)
-                call("lt_q8_gemm_t", h, L["wdown_t"].t.vp, xq, xd, None, self.xres.vp, self.x.vp, B, E, F)
+                if B <= SILU_QUANT_MAX_BATCH:
+                    # gate|up + SiLU with the block-major quant of its output in one launch
+                    call("lt_q8_gemm_silu_quant_t", h, L["wgu_il_t"].t.vp, xq, xd, self.vq.vp, self.vd.vp, B, F,
+                         E)
+                    call("lt_q8_gemm_t", h, L["wdown_t"].t.vp, self.vq.vp, self.vd.vp, None, self.xres.vp,
+                         self.x.vp, B, E, F)
+                else:
+                    call("lt_q8_gemm_silu_t", h, L["wgu_il_t"].t.vp, xq, xd, self.vbuf.vp, B, F, E)
+                    call("lt_quant_q8_bm", h, self.vbuf.vp, xq, xd, B, F)
+                    call("lt_q8_gemm_t", h, L["wdown_t"].t.vp, xq, xd, None, self.xres.vp, self.x.vp, B, E, F)
             else:
                 call("lt_rmsnorm_quant_rows", h, self.xres.vp, L["ffn_norm"].vp, xq, xd, B, E, eps)
                 call("lt_q8_gemv_multi", h, L["wgu_il"].t.vp, xq, xd, B, None, self.vbuf.vp, 2 * F, E,
@@ -1673,7 +1690,7 @@ class BatchDecodePlan:
         if self._prefill is not None:
             self._prefill.free()
         for t in [*self.k, *self.v, self.lens, self.toks, self.err, self.hist, self.hist_count, self.x, self.xres,
-                  self.qkv, self.att, self.vbuf, self.xq, self.xd, self.logits, self.attn_ws]:
+                  self.qkv, self.att, self.vbuf, self.xq, self.xd, self.vq, self.vd, self.logits, self.attn_ws]:
             if t is not None:
                 t.free()
 

@@ -247,6 +247,34 @@ def test_q8_gemm_silu_tiled(gpu, oracle, F, K, T, grouped, monkeypatch):
         assert np.array_equal(bits(got[t]), bits(oracle.silu_mul(g, u))), f"token {t}"
 
 
+@pytest.mark.parametrize("F,K,T", [(4864, 896, 64), (4864, 896, 37), (64, 128, 7), (96, 4096, 70), (128, 6144, 33),
+                                   (4864, 896, 128)])
+def test_q8_gemm_silu_quant_equals_gemm_then_quant(gpu, F, K, T):
+    """lt_q8_gemm_silu_quant_t equals lt_q8_gemm_silu_t followed by lt_quant_q8_bm of its
+    output: the block-major quants and scales byte for byte."""
+    case(f"q8_gemm_silu_quant_t F={F} K={K} T={T}")
+    rng = np.random.default_rng(F + T)
+    Wgu = hq8.quantize_rows((rng.standard_normal((2 * F, K)) * 0.02).astype(np.float32))
+    X = rng.standard_normal((T, K)).astype(np.float32)
+    xq = dr.DevTensor.empty((T * K,), np.int8)
+    xd = dr.DevTensor.empty((T * K // 32,), np.uint16)
+    call("lt_quant_q8_bm", gpu.handle, up(X).vp, xq.vp, xd.vp, T, K)
+    Wt = up(tiles_host(Wgu, 2 * F, K))
+    V = dr.DevTensor.empty((T, F), np.float32)
+    vq_a, vd_a = dr.DevTensor.empty((T * F,), np.int8), dr.DevTensor.empty((T * F // 32,), np.uint16)
+    vq_b, vd_b = dr.DevTensor.empty((T * F,), np.int8), dr.DevTensor.empty((T * F // 32,), np.uint16)
+    call("lt_q8_gemm_silu_t", gpu.handle, Wt.vp, xq.vp, xd.vp, V.vp, T, F, K)
+    call("lt_quant_q8_bm", gpu.handle, V.vp, vq_a.vp, vd_a.vp, T, F)
+    call("lt_q8_gemm_silu_quant_t", gpu.handle, Wt.vp, xq.vp, xd.vp, vq_b.vp, vd_b.vp, T, F, K)
+    assert np.array_equal(vq_a.to_host(), vq_b.to_host()), "quants"
+    assert np.array_equal(vd_a.to_host(), vd_b.to_host()), "scales"
+    from llamatov_amd._lib import raw
+    rc = raw("lt_q8_gemm_silu_quant_t")(gpu.handle, Wt.vp, xq.vp, xd.vp, xq.vp, vd_b.vp, T, F, K)
+    assert rc != 0, "in-place output refused"
+    for t in (xq, xd, Wt, V, vq_a, vd_a, vq_b, vd_b):
+        t.free()
+
+
 _W = {}
 
 
