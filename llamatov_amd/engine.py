@@ -1419,8 +1419,10 @@ class StepGraph:
 # from MIXED_MIN_BATCH sequences the step's gate|up, down and vocab projections run the tiled
 # GEMM (linear "mixed"), past MIXED_MAX_BATCH every projection does ("gemm"); measured C2 step
 # tok/s, GEMV / mixed / GEMM: B = 8 8176 / 6974 / 5675, 16 13626 / 13488 / 11194, 32 21951 /
-# 25259 / 21165, 64 31268 / 44419 / 39651, 96 35061 / 57007 / 54339, 128 38245 / 70172 / 69351
-MIXED_MIN_BATCH = 32
+# 25259 / 21165, 64 31268 / 44419 / 39651, 96 35061 / 57007 / 54339, 128 38245 / 70172 / 69351;
+# with the vocab GEMM and the fused SiLU quant, GEMV / mixed: 16 14328 / 13942, 20 17031 /
+# 17058, 24 19902 / 20197, 28 22229 / 23110
+MIXED_MIN_BATCH = 24
 MIXED_MAX_BATCH = 128
 # from this many sequences the vocab projection runs the tiled GEMM in every form; measured
 # 151936 x 896 per launch, multi-token GEMV / tiled GEMM (us): T = 1 32.3 / 54.2, 4 39.2 / 51.5,
