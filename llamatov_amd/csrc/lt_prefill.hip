@@ -478,7 +478,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSL >= 2 ? 
 // each half's tree, quantizes every token's block (the activation quantizer, q8_scale /
 // q8_quant, one half-wave per token) into block-major Yq / Yd, the down projection's input:
 // bit-identical to the SiLU output quantized by lt_quant_q8_bm, with no fp32 round trip.
-template <GemmEpi EPI, int kW, bool kQ = false>
+//
+// kP > 0 (K at most kP * 1024): every leaf is padded to kP blocks -- the blocks past the
+// matrix read zeros through resources of no records, and fma(0, 0, a) = a for the leaf
+// values, which are never -0 -- so the wave's kNL * kP slots, the ring over them and the
+// leaf closes are all fixed at compile time: no per-slot branches, and the tree's pairings
+// are register additions the compiler schedules freely.  kP = 0: the leaf lengths are read
+// at run time (any K).
+template <GemmEpi EPI, int kW, bool kQ = false, int kP = 0>
 __global__ __launch_bounds__(64 * kW * (kQ ? 2 : 1)) void k_q8_gemm_ls(GemmParams P) {
   static_assert(kW == 4 || kW == 8, "k_q8_gemm_ls: 4 or 8 waves per tile");
   static_assert(!kQ || (EPI == GE_SILU && kW == 4), "k_q8_gemm_ls: the quantizing variant is SiLU, 4 waves per tile");
@@ -539,35 +546,6 @@ __global__ __launch_bounds__(64 * kW * (kQ ? 2 : 1)) void k_q8_gemm_ls(GemmParam
     const int k = (int)(__builtin_bitreverse32((uint32_t)i) >> (32 - __builtin_ctz(kNL)));
     return wave + kW * k;
   };
-  // producer: position pi (0..kNL-1) of the post-order, next block pb (-1: done)
-  int pi = 0, pb = wave;
-  while (pb >= nb) {                                // leading empty leaves
-    if (++pi == kNL) { pb = -1; break; }
-    pb = leaf_of(pi);
-  }
-  const int first_pi = pi;
-  auto produce = [&](Ops& o) {
-    load_ops(pb, o);
-    if (pb >= 0) {
-      pb += 32;
-      while (pb >= nb) {
-        if (++pi == kNL) { pb = -1; break; }
-        pb = leaf_of(pi);
-      }
-    }
-  };
-  // blocks of the wave: every leaf's count
-  int total = 0;
-#pragma unroll
-  for (int i = 0; i < kNL; i++) {
-    const int L = wave + kW * i;
-    total += L < nb ? (nb - L + 31) / 32 : 0;
-  }
-  constexpr int kR = 4;                             // blocks in flight
-  Ops ring[kR];
-#pragma unroll
-  for (int d = 0; d < kR; d++) produce(ring[d]);
-
   float a[16], s0[16], s1[16], s2[16];
 #pragma unroll
   for (int r = 0; r < 16; r++) { a[r] = 0.0f; s0[r] = 0.0f; s1[r] = 0.0f; s2[r] = 0.0f; }
@@ -631,35 +609,90 @@ __global__ __launch_bounds__(64 * kW * (kQ ? 2 : 1)) void k_q8_gemm_ls(GemmParam
 #pragma unroll
     for (int r = 0; r < 16; r++) a[r] = 0.0f;
   };
-  // leading empty leaves close with a = 0
-  for (int i = 0; i < first_pi; i++) close_leaf(i);
-  int ci = first_pi, cb = ci < kNL ? leaf_of(ci) : 0;   // consumer: position, block
-  const v16i z = {};
-  const v16f zf = {};
-  // whole groups of kR slots, every slot folded: past the wave's last block a slot holds
-  // zeros (fma(0, 0, a) = a, and a is +0 once every leaf is closed), so the body has no
-  // per-slot test and each fold waits for its own slot's loads only
-  for (int s = 0; s < total; s += kR) {
+  if constexpr (kP > 0) {
+    constexpr int kS = kNL * kP;                    // slots of the wave
+    constexpr int kRS = kS < 8 ? kS : 8;            // blocks in flight
+    // slot j: block j % kP of the leaf at post-order position j / kP (-1: past the matrix)
+    auto blk = [&](int j) {
+      const int b = leaf_of(j / kP) + 32 * (j % kP);
+      return b < nb ? b : -1;
+    };
+    Ops ring[kRS];
 #pragma unroll
-    for (int d = 0; d < kR; d++) {
-      const v16i isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(ring[d].w03, ring[d].bq, z, 0, 0, 0);
-      const u32x2 aw = {ring[d].wdw, 0u}, bw = {ring[d].xdw, 0u};
+    for (int j = 0; j < kRS; j++) load_ops(blk(j), ring[j]);
+    const v16i z = {};
+    const v16f zf = {};
+#pragma unroll
+    for (int j = 0; j < kS; j++) {
+      Ops& o = ring[j % kRS];
+      const v16i isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.w03, o.bq, z, 0, 0, 0);
+      const u32x2 aw = {o.wdw, 0u}, bw = {o.xdw, 0u};
       const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(h4, aw), __builtin_bit_cast(h4, bw), zf,
                                                              0, 0, 0);
-      produce(ring[d]);
+      if (j + kRS < kS) load_ops(blk(j + kRS), o);
 #pragma unroll
       for (int r = 0; r < 16; r++) a[r] = fmaf(sc[r], (float)isum[r], a[r]);
-      if (ci < kNL) {                               // uniform
-        cb += 32;
-        if (cb >= nb) {                             // the leaf is complete; close it and any empty ones after
-          close_leaf(ci);
-          while (++ci < kNL && (cb = leaf_of(ci)) >= nb) close_leaf(ci);
+      if (j % kP == kP - 1) close_leaf(j / kP);
+    }
+  } else {
+    // producer: position pi (0..kNL-1) of the post-order, next block pb (-1: done)
+    int pi = 0, pb = wave;
+    while (pb >= nb) {                                // leading empty leaves
+      if (++pi == kNL) { pb = -1; break; }
+      pb = leaf_of(pi);
+    }
+    const int first_pi = pi;
+    auto produce = [&](Ops& o) {
+      load_ops(pb, o);
+      if (pb >= 0) {
+        pb += 32;
+        while (pb >= nb) {
+          if (++pi == kNL) { pb = -1; break; }
+          pb = leaf_of(pi);
+        }
+      }
+    };
+    // blocks of the wave: every leaf's count
+    int total = 0;
+#pragma unroll
+    for (int i = 0; i < kNL; i++) {
+      const int L = wave + kW * i;
+      total += L < nb ? (nb - L + 31) / 32 : 0;
+    }
+    constexpr int kR = 4;                             // blocks in flight
+    Ops ring[kR];
+#pragma unroll
+    for (int d = 0; d < kR; d++) produce(ring[d]);
+    // leading empty leaves close with a = 0
+    for (int i = 0; i < first_pi; i++) close_leaf(i);
+    int ci = first_pi, cb = ci < kNL ? leaf_of(ci) : 0;   // consumer: position, block
+    const v16i z = {};
+    const v16f zf = {};
+    // whole groups of kR slots, every slot folded: past the wave's last block a slot holds
+    // zeros (fma(0, 0, a) = a, and a is +0 once every leaf is closed), so the body has no
+    // per-slot test and each fold waits for its own slot's loads only
+    for (int s = 0; s < total; s += kR) {
+#pragma unroll
+      for (int d = 0; d < kR; d++) {
+        const v16i isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(ring[d].w03, ring[d].bq, z, 0, 0, 0);
+        const u32x2 aw = {ring[d].wdw, 0u}, bw = {ring[d].xdw, 0u};
+        const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(h4, aw), __builtin_bit_cast(h4, bw), zf,
+                                                               0, 0, 0);
+        produce(ring[d]);
+#pragma unroll
+        for (int r = 0; r < 16; r++) a[r] = fmaf(sc[r], (float)isum[r], a[r]);
+        if (ci < kNL) {                               // uniform
+          cb += 32;
+          if (cb >= nb) {                             // the leaf is complete; close it and any empty ones after
+            close_leaf(ci);
+            while (++ci < kNL && (cb = leaf_of(ci)) >= nb) close_leaf(ci);
+          }
         }
       }
     }
+    // empty leaves at the end (a wave with no blocks at all closes everything here)
+    for (; ci < kNL; ci++) close_leaf(ci);
   }
-  // empty leaves at the end (a wave with no blocks at all closes everything here)
-  for (; ci < kNL; ci++) close_leaf(ci);
   // s0 = the wave's subtree partial; the remaining levels on wave 0: pairs (w, w + s) for
   // s = kW/2, ..., 1, each into the lower wave's value
   if (wave > 0) {
@@ -918,6 +951,31 @@ int ls_mode() {
   return s ? atoi(s) : -1;
 }
 
+// A leaf-split launch: the compile-time schedule (k_q8_gemm_ls's kP, blocks per leaf) when a
+// wave's slots, (32 / kW) * kP, number at most 20 -- 4 waves per tile: K <= 2048, 8 waves:
+// K <= 5120 -- else the run-time walk.  LT_GEMM_LS_STATIC=0 forces the run-time walk (read at
+// every launch).  Measured at T = 64, run-time / compile-time walk (us): 9728 x 896 11.2 /
+// 8.0, 151936 x 896 115 / 83, 1152 x 896 5.5 / 4.2, 896 x 4864 (8 waves) 8.7 / 7.9, 4096 x
+// 4096 (8 waves) 9.7 / 9.4; but with 32 slots, 6144 x 4096 (4 waves) 15.6 / 16.7.
+template <GemmEpi EPI, int kW, bool kQ>
+void launch_ls(lt_ctx* ctx, const GemmParams& P, unsigned grid) {
+  constexpr unsigned kThreads = 64u * kW * (kQ ? 2u : 1u);
+  const char* senv = getenv("LT_GEMM_LS_STATIC");
+  const int bpl = (senv && atoi(senv) == 0) ? 0 : (P.K / 32 + 31) / 32;
+  if (bpl == 1) {
+    k_q8_gemm_ls<EPI, kW, kQ, 1><<<grid, kThreads, 0, ctx->stream>>>(P);
+  } else if (bpl == 2) {
+    k_q8_gemm_ls<EPI, kW, kQ, 2><<<grid, kThreads, 0, ctx->stream>>>(P);
+  } else if constexpr (kW == 8) {
+    if (bpl == 3) k_q8_gemm_ls<EPI, kW, kQ, 3><<<grid, kThreads, 0, ctx->stream>>>(P);
+    else if (bpl == 4) k_q8_gemm_ls<EPI, kW, kQ, 4><<<grid, kThreads, 0, ctx->stream>>>(P);
+    else if (bpl == 5) k_q8_gemm_ls<EPI, kW, kQ, 5><<<grid, kThreads, 0, ctx->stream>>>(P);
+    else k_q8_gemm_ls<EPI, kW, kQ, 0><<<grid, kThreads, 0, ctx->stream>>>(P);
+  } else {
+    k_q8_gemm_ls<EPI, kW, kQ, 0><<<grid, kThreads, 0, ctx->stream>>>(P);
+  }
+}
+
 template <GemmEpi EPI, bool kTiled>
 int launch_gemm(lt_ctx* ctx, GemmParams P) {
   P.nrt = (P.N + 31) / 32;
@@ -936,8 +994,8 @@ int launch_gemm(lt_ctx* ctx, GemmParams P) {
       const int wforce = wenv ? atoi(wenv) : 0;
       const long cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
       const bool w8 = wforce ? wforce == 8 : gls <= cus;
-      if (w8) k_q8_gemm_ls<EPI, 8><<<(unsigned)gls, 512, 0, ctx->stream>>>(P);
-      else k_q8_gemm_ls<EPI, 4><<<(unsigned)gls, 256, 0, ctx->stream>>>(P);
+      if (w8) launch_ls<EPI, 8, false>(ctx, P, (unsigned)gls);
+      else launch_ls<EPI, 4, false>(ctx, P, (unsigned)gls);
       return lt_check_launch("k_q8_gemm_ls");
     }
   }
@@ -993,7 +1051,7 @@ int launch_gemm_silu_q(lt_ctx* ctx, GemmParams P) {
   P.ntt = (P.T + 31) / 32;
   const int npair = P.nrt / 2;
   const long gls = (long)((npair + 7) / 8) * 8 * P.ntt;
-  k_q8_gemm_ls<GE_SILU, 4, true><<<(unsigned)gls, 512, 0, ctx->stream>>>(P);
+  launch_ls<GE_SILU, 4, true>(ctx, P, (unsigned)gls);
   return lt_check_launch("k_q8_gemm_ls");
 }
 

@@ -175,10 +175,14 @@ def subnormal_scales(rng, W, xd, frac=0.25):
 
 def force_walk(monkeypatch, walk: str) -> None:
     """Pin the tiled GEMM's kernel: "ls" / "ls8" the leaf-split kernel with 4 / 8 waves per
-    tile, else k_q8_gemm with the leaf walk LT_GEMM_GROUPED = walk (read at every launch)."""
+    tile (its compile-time schedule where K <= 5120), "lsd" / "lsd8" the same with the
+    run-time walk at every K, else k_q8_gemm with the leaf walk LT_GEMM_GROUPED = walk (all
+    read at every launch)."""
     if walk.startswith("ls"):
+        dyn = walk.startswith("lsd")
         monkeypatch.setenv("LT_GEMM_LS", "1")
-        monkeypatch.setenv("LT_GEMM_LS_W", walk[2:] or "4")
+        monkeypatch.setenv("LT_GEMM_LS_W", walk[3 if dyn else 2:] or "4")
+        monkeypatch.setenv("LT_GEMM_LS_STATIC", "0" if dyn else "1")
     else:
         monkeypatch.setenv("LT_GEMM_LS", "0")
         monkeypatch.setenv("LT_GEMM_GROUPED", walk)
@@ -189,7 +193,7 @@ def force_walk(monkeypatch, walk: str) -> None:
                                        (96, 256, 70, "subnormal"), (64, 2048, 45, "bias"), (72, 6144, 130, "resid"),
                                        (33, 4096, 7, "subnormal"), (96, 8192, 77, "subnormal"),
                                        (130, 14336, 67, "bias")])
-@pytest.mark.parametrize("grouped", ["2", "1", "0", "ls", "ls8"])
+@pytest.mark.parametrize("grouped", ["2", "1", "0", "ls", "ls8", "lsd", "lsd8"])
 def test_q8_gemm_tiled_matches_gemv_per_token(gpu, oracle, N, K, T, epi, grouped, monkeypatch):
     """Every leaf walk of the tiled kernel (grouped leaves with a 4- or 2-slot ring where K
     allows them, the dynamic walk; forced with LT_GEMM_GROUPED) and the leaf-split kernel
@@ -222,7 +226,7 @@ def test_q8_gemm_tiled_matches_gemv_per_token(gpu, oracle, N, K, T, epi, grouped
 
 
 @pytest.mark.parametrize("F,K,T", [(4864, 896, 40), (64, 128, 7), (48, 96, 70), (128, 6144, 33), (96, 4096, 140)])
-@pytest.mark.parametrize("grouped", ["2", "1", "0", "ls", "ls8"])
+@pytest.mark.parametrize("grouped", ["2", "1", "0", "ls", "ls8", "lsd", "lsd8"])
 def test_q8_gemm_silu_tiled(gpu, oracle, F, K, T, grouped, monkeypatch):
     force_walk(monkeypatch, grouped)
     case(f"q8_gemm_silu_t F={F} K={K} T={T} grouped={grouped}")
@@ -249,10 +253,13 @@ def test_q8_gemm_silu_tiled(gpu, oracle, F, K, T, grouped, monkeypatch):
 
 @pytest.mark.parametrize("F,K,T", [(4864, 896, 64), (4864, 896, 37), (64, 128, 7), (96, 4096, 70), (128, 6144, 33),
                                    (4864, 896, 128)])
-def test_q8_gemm_silu_quant_equals_gemm_then_quant(gpu, F, K, T):
+@pytest.mark.parametrize("static", ["1", "0"])
+def test_q8_gemm_silu_quant_equals_gemm_then_quant(gpu, F, K, T, static, monkeypatch):
     """lt_q8_gemm_silu_quant_t equals lt_q8_gemm_silu_t followed by lt_quant_q8_bm of its
-    output: the block-major quants and scales byte for byte."""
-    case(f"q8_gemm_silu_quant_t F={F} K={K} T={T}")
+    output: the block-major quants and scales byte for byte (both leaf-split schedules,
+    LT_GEMM_LS_STATIC)."""
+    monkeypatch.setenv("LT_GEMM_LS_STATIC", static)
+    case(f"q8_gemm_silu_quant_t F={F} K={K} T={T} static={static}")
     rng = np.random.default_rng(F + T)
     Wgu = hq8.quantize_rows((rng.standard_normal((2 * F, K)) * 0.02).astype(np.float32))
     X = rng.standard_normal((T, K)).astype(np.float32)
