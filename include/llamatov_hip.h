@@ -392,6 +392,19 @@ LT_API int lt_q8_gemm_silu_t(lt_ctx* ctx, const void* Wgut, const int8_t* Xq, co
 LT_API int lt_q8_gemm_silu_quant_t(lt_ctx* ctx, const void* Wgut, const int8_t* Xq, const uint16_t* Xd, int8_t* Vq,
                                    uint16_t* Vd, int T, int F, int K);
 
+/* The q|k|v projection of the batched decode step with RoPE and the KV append in its
+ * epilogue (no reference counterpart: lt_q8_gemm_t with the bias followed by
+ * lt_rope_append_seqs, in one launch; qkv [T][N] and the cache rows bit-identical to those two
+ * calls).  Wt is lt_q8_tiles_rope's copy of the q|k|v matrix W [N][K/32]: the tile-major copy
+ * with the rows of each q and k head of hd in the rope-pair order -- row 2j + e of the head
+ * is row j + e*hd/2 of W -- so the two rows RoPE rotates together land in one lane; v rows keep
+ * their places.  N = (nh + 2 nkv) hd, hd even; row t of Xq / Xd (block-major) is sequence t at
+ * position len[t], its cache rows at kc / vc + t*maxt*nkv*hd elements. */
+LT_API int lt_q8_tiles_rope(lt_ctx* ctx, const void* W, void* Wt, int N, int K, int nh, int nkv, int hd);
+LT_API int lt_q8_gemm_rope_t(lt_ctx* ctx, const void* Wt, const int8_t* Xq, const uint16_t* Xd, int T,
+                             const float* bias, float* qkv, int N, int K, const int* len, int nh, int nkv, int hd,
+                             const float* freqs, void* kc, void* vc, int maxt, int kv_dtype);
+
 /* RoPE (lt_rope_qk's arithmetic) of T rows of q|k, row t at position *pos0 + t; rows are
  * row_stride floats apart and hold nheads contiguous heads of hd. */
 LT_API int lt_rope_batch(lt_ctx* ctx, float* qk, int T, int row_stride, const int* pos0, int nheads, int hd,

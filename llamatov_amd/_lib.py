@@ -106,6 +106,9 @@ _SIGS = {
     "lt_q8_gemm_t": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int]),
     "lt_q8_gemm_silu_t": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int]),
     "lt_q8_gemm_silu_quant_t": (c_int, [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int]),
+    "lt_q8_tiles_rope": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int, c_int]),
+    "lt_q8_gemm_rope_t": (c_int, [_P, _P, _P, _P, c_int, _P, _P, c_int, c_int, _P, c_int, c_int, c_int, _P, _P, _P,
+                                  c_int, c_int]),
     "lt_rope_batch": (c_int, [_P, _P, c_int, c_int, _P, c_int, c_int, _P]),
     "lt_kv_append_batch": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, _P, c_int, c_int, c_int]),
     "lt_len_add": (c_int, [_P, _P, c_int, c_int]),

@@ -29,7 +29,9 @@ constexpr int kGemmTokens = 32 * kGemmWaves;   // tokens per workgroup
 constexpr int kDepth = 4;                      // blocks in flight per wave
 constexpr uint32_t kNoBlk = 0x80000000u;       // out-of-range buffer offset: reads zeros
 
-enum GemmEpi { GE_STORE = 0, GE_BIAS = 1, GE_RESID = 2, GE_SILU = 3 };
+// GE_ROPE (leaf-split kernel only): the q|k|v rows of the next token of each of T sequences
+// in the rope-pair order of lt_q8_tiles_rope, + bias, then RoPE and the KV append
+enum GemmEpi { GE_STORE = 0, GE_BIAS = 1, GE_RESID = 2, GE_SILU = 3, GE_ROPE = 4 };
 
 struct GemmParams {
   const uint8_t* W;      // Q8_0 blocks [N][K/32]; tiled: [ceil(N/32)][K/32][32 rows][34 B]
@@ -42,6 +44,13 @@ struct GemmParams {
   uint16_t* Yd;          //   and their scales [N/64][T]
   int T, N, K;
   int nrt, ntt;          // row tiles (32 rows), token tiles (kGemmTokens)
+  // GE_ROPE: row t is sequence t at position len[t]; its cache rows at kc / vc + t*maxt*nkv*hd
+  // elements (fp16 when f16)
+  const int* len;
+  const float* freqs;    // [hd/2]
+  void* kc;
+  void* vc;
+  int nh, nkv, hd, maxt, f16;
 };
 
 // C layout of v_mfma_i32_32x32x32_i8: register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4,
@@ -736,6 +745,67 @@ __global__ __launch_bounds__(64 * kW * (kQ ? 2 : 1)) void k_q8_gemm_ls(GemmParam
     }
     return;
   }
+  if constexpr (EPI == GE_ROPE) {
+    // the tile through LDS, then one rotation pair per thread: pair p of token q is rows
+    // 2p, 2p+1 of the tile -- below nqk, rows j and j + hd/2 of one head, rotated with
+    // k_rope_append_batch's arithmetic (sin / cos of pos * freqs[j], two fmas); q rotated
+    // into Y, k rotated into the cache and as it was into Y, v into the cache and Y
+    __shared__ float s_o[32][33];                   // [token][row of the tile] (+1 pad)
+    if (wave == 0) {
+      float v[16];
+      combine(v);
+#pragma unroll
+      for (int r = 0; r < 16; r++) s_o[c][c_row(r, h)] = v[r];
+    }
+    __syncthreads();
+    const int half = P.hd >> 1, nqk = (P.nh + P.nkv) * P.hd, width = P.nkv * P.hd;
+    auto put = [&](void* cache, size_t off, float val) {
+      if (P.f16) ((uint16_t*)cache)[off] = lt_float_to_half_bits(val);
+      else ((float*)cache)[off] = val;
+    };
+    for (int i = threadIdx.x; i < 32 * 16; i += 64 * kW) {
+      const int tq = i >> 4, pr = i & 15;
+      const int t = t0 + tq, n = n0 + 2 * pr;       // N is even: n < N means n + 1 < N
+      if (t >= P.T || n >= P.N) continue;
+      const int pos = P.len[t];
+      const bool app = pos >= 0 && pos < P.maxt;
+      const size_t cbase = ((size_t)t * P.maxt + (size_t)(app ? pos : 0)) * width;
+      float* yt = P.Y + (size_t)t * P.N;
+      const float v0 = s_o[tq][2 * pr], v1 = s_o[tq][2 * pr + 1];
+      if (n < nqk) {
+        const int head = n / P.hd, j = (n - head * P.hd) >> 1;
+        const int ra = head * P.hd + j, rb = ra + half;
+        const float x1 = P.bias ? v0 + P.bias[ra] : v0;
+        const float x2 = P.bias ? v1 + P.bias[rb] : v1;
+        float sn, cs;
+        lt_sincosf((float)pos * P.freqs[j], &sn, &cs);
+        const float o1 = fmaf(x1, cs, -(x2 * sn));
+        const float o2 = fmaf(x1, sn, x2 * cs);
+        if (head < P.nh) {
+          yt[ra] = o1;
+          yt[rb] = o2;
+        } else {
+          yt[ra] = x1;
+          yt[rb] = x2;
+          if (app) {
+            const size_t off = cbase + (size_t)(head - P.nh) * P.hd + j;
+            put(P.kc, off, o1);
+            put(P.kc, off + half, o2);
+          }
+        }
+      } else {
+        const float x1 = P.bias ? v0 + P.bias[n] : v0;
+        const float x2 = P.bias ? v1 + P.bias[n + 1] : v1;
+        yt[n] = x1;
+        yt[n + 1] = x2;
+        if (app) {
+          put(P.vc, cbase + (size_t)(n - nqk), x1);
+          put(P.vc, cbase + (size_t)(n - nqk) + 1, x2);
+        }
+      }
+    }
+    return;
+  }
   if (wave > 0) return;
   float v[16];
   combine(v);
@@ -894,9 +964,12 @@ __global__ void k_len_add(int* __restrict__ len, int T, int maxt) {
 
 // The tile-major copy of a Q8_0 matrix: tile rt, block b holds the quants of rows
 // 32*rt .. 32*rt+31 of block b (32 bytes each), then their fp16 scales (rows past N are
-// zero).  One 2-byte unit per thread, written in order.
+// zero).  One 2-byte unit per thread, written in order.  nqk > 0: the rope-pair order --
+// within each of the first nqk rows' heads of hd rows, row 2j + e of the copy is row
+// j + e*hd/2 of the head (the two rows RoPE rotates together are adjacent); rows from nqk
+// on keep their places.
 __global__ __launch_bounds__(256) void k_q8_tiles(const uint16_t* __restrict__ W, uint16_t* __restrict__ Wt, int N,
-                                                  int nb, uint32_t units) {
+                                                  int nb, uint32_t units, int hd, int nqk) {
   constexpr uint32_t kUnits = kBlockBytes / 2;             // 17 per block
   constexpr uint32_t kTileUnits = kTileBlk / 2;            // 544 per tile block
   for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < units; i += gridDim.x * 256u) {
@@ -906,7 +979,11 @@ __global__ __launch_bounds__(256) void k_q8_tiles(const uint16_t* __restrict__ W
     // of row j-512 (block unit 0)
     const uint32_t r = j < 512u ? j >> 4 : j - 512u;
     const uint32_t u = j < 512u ? 1u + (j & 15u) : 0u;
-    const uint32_t row = rt * 32u + r;
+    uint32_t row = rt * 32u + r;
+    if ((int)row < nqk) {
+      const uint32_t head = row / (uint32_t)hd, q = row - head * (uint32_t)hd;
+      row = head * (uint32_t)hd + (q >> 1) + (q & 1u) * ((uint32_t)hd >> 1);
+    }
     Wt[i] = row < (uint32_t)N ? W[((size_t)row * nb + b) * kUnits + u] : (uint16_t)0;
   }
 }
@@ -1044,6 +1121,19 @@ int gemm_entry(const char* fn, lt_ctx* ctx, const void* W, const int8_t* Xq, con
   return launch_gemm<GE_STORE, kTiled>(ctx, P);
 }
 
+// q|k|v of the next token of T sequences on the leaf-split kernel with the RoPE + KV-append
+// epilogue (k_q8_gemm_ls<GE_ROPE, ...>): the weights in lt_q8_tiles_rope's order, 8 waves per
+// tile when the launch holds at most one tile per CU.
+int launch_gemm_rope(lt_ctx* ctx, GemmParams P) {
+  P.nrt = (P.N + 31) / 32;
+  P.ntt = (P.T + 31) / 32;
+  const long gls = (long)((P.nrt + 7) / 8) * 8 * P.ntt;
+  const long cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+  if (gls <= cus) launch_ls<GE_ROPE, 8, false>(ctx, P, (unsigned)gls);
+  else launch_ls<GE_ROPE, 4, false>(ctx, P, (unsigned)gls);
+  return lt_check_launch("k_q8_gemm_ls");
+}
+
 // The leaf-split SiLU GEMM with the quant of its output fused (k_q8_gemm_ls<GE_SILU, 4, true>):
 // every launch on it, whatever T (its grid: pairs of row tiles x 32-token tiles).
 int launch_gemm_silu_q(lt_ctx* ctx, GemmParams P) {
@@ -1094,7 +1184,20 @@ int lt_q8_tiles(lt_ctx* ctx, const void* W, void* Wt, int N, int K) {
   const size_t units = tiles_bytes(N, K) / 2;
   LT_REQUIRE(units < ((size_t)1 << 32), "lt_q8_tiles: %d x %d too large", N, K);
   const unsigned grid = (unsigned)(units / 256 < 65536 ? (units + 255) / 256 : 65536);
-  k_q8_tiles<<<grid, 256, 0, ctx->stream>>>((const uint16_t*)W, (uint16_t*)Wt, N, K / 32, (uint32_t)units);
+  k_q8_tiles<<<grid, 256, 0, ctx->stream>>>((const uint16_t*)W, (uint16_t*)Wt, N, K / 32, (uint32_t)units, 1, 0);
+  return lt_check_launch("k_q8_tiles");
+}
+
+int lt_q8_tiles_rope(lt_ctx* ctx, const void* W, void* Wt, int N, int K, int nh, int nkv, int hd) {
+  LT_REQUIRE(ctx && W && Wt, "lt_q8_tiles_rope: null argument");
+  LT_REQUIRE(K > 0 && K % 32 == 0 && nh > 0 && nkv > 0 && hd > 0 && hd % 2 == 0 && N == (nh + 2 * nkv) * hd,
+             "lt_q8_tiles_rope: N=%d K=%d nh=%d nkv=%d hd=%d (N = (nh + 2 nkv) hd, hd even)", N, K, nh, nkv, hd);
+  LT_REQUIRE(lt_aligned(W, 4) && lt_aligned(Wt, 16), "lt_q8_tiles_rope: misaligned argument");
+  const size_t units = tiles_bytes(N, K) / 2;
+  LT_REQUIRE(units < ((size_t)1 << 32), "lt_q8_tiles_rope: %d x %d too large", N, K);
+  const unsigned grid = (unsigned)(units / 256 < 65536 ? (units + 255) / 256 : 65536);
+  k_q8_tiles<<<grid, 256, 0, ctx->stream>>>((const uint16_t*)W, (uint16_t*)Wt, N, K / 32, (uint32_t)units, hd,
+                                            (nh + nkv) * hd);
   return lt_check_launch("k_q8_tiles");
 }
 
@@ -1132,6 +1235,24 @@ int lt_q8_gemm_silu_quant_t(lt_ctx* ctx, const void* Wgut, const int8_t* Xq, con
   P.W = (const uint8_t*)Wgut; P.Xq = Xq; P.Xd = Xd; P.Yq = Vq; P.Yd = Vd;
   P.T = T; P.N = 2 * F; P.K = K;
   return launch_gemm_silu_q(ctx, P);
+}
+
+int lt_q8_gemm_rope_t(lt_ctx* ctx, const void* Wt, const int8_t* Xq, const uint16_t* Xd, int T, const float* bias,
+                      float* qkv, int N, int K, const int* len, int nh, int nkv, int hd, const float* freqs, void* kc,
+                      void* vc, int maxt, int kv_dtype) {
+  const char* fn = "lt_q8_gemm_rope_t";
+  LT_REQUIRE(ctx && len && freqs && kc && vc, "%s: null argument", fn);
+  if (int rc = check_gemm(fn, Wt, Xq, Xd, qkv, T, N, K)) return rc;
+  LT_REQUIRE(nh > 0 && nkv > 0 && hd > 0 && hd % 2 == 0 && maxt > 0 && N == (nh + 2 * nkv) * hd,
+             "%s: N=%d nh=%d nkv=%d hd=%d maxt=%d (N = (nh + 2 nkv) hd, hd even)", fn, N, nh, nkv, hd, maxt);
+  LT_REQUIRE(kv_dtype == LT_KV_F32 || kv_dtype == LT_KV_F16, "%s: kv_dtype=%d", fn, kv_dtype);
+  LT_REQUIRE(tiles_bytes(N, K) < ((size_t)1 << 31), "%s: tile copy of %d x %d above 2 GiB", fn, N, K);
+  GemmParams P{};
+  P.W = (const uint8_t*)Wt; P.Xq = Xq; P.Xd = Xd; P.bias = bias; P.Y = qkv;
+  P.T = T; P.N = N; P.K = K;
+  P.len = len; P.freqs = freqs; P.kc = kc; P.vc = vc;
+  P.nh = nh; P.nkv = nkv; P.hd = hd; P.maxt = maxt; P.f16 = kv_dtype == LT_KV_F16 ? 1 : 0;
+  return launch_gemm_rope(ctx, P);
 }
 
 int lt_rope_batch(lt_ctx* ctx, float* qk, int T, int row_stride, const int* pos0, int nheads, int hd,

@@ -557,6 +557,7 @@ class ResidentModel:
         self.planar = None  # the planar copies of the decode GEMVs' matrices (planar_copies)
         self.output_pl: Q8Weight | None = None
         self._head_pl: DevTensor | None = None   # head_planar's own allocation
+        self.qkv_rope = None  # the q|k|v matrices' rope-pair tile copies (qkv_rope_tiles)
         self.tok_embd = top["tok_embd"]
         self.output = top.get("output", self.tok_embd)
         self.output_norm = top["output_norm"]
@@ -604,6 +605,23 @@ class ResidentModel:
             call("lt_q8_tiles", self.dev.handle, W.t.vp, t.vp, W.N, W.K)
             L[k + "_t"] = Q8Weight(None, W.K, t=t, N=W.N)
         self.tiles = base
+
+    def qkv_rope_tiles(self) -> None:
+        """Tile-major copies of every layer's q|k|v matrix in the rope-pair row order
+        (lt_q8_tiles_rope), built on the device at first use: one allocation.  The batched
+        step's q|k|v GEMM with the RoPE + KV-append epilogue (lt_q8_gemm_rope_t) reads them."""
+        if self.qkv_rope is not None:
+            return
+        c = self.cfg
+        n = int(_lib.raw("lt_q8_tiles_bytes")(c.n_qkv, c.n_embd))
+        step = (n + 255) // 256 * 256
+        base = self.dev.malloc(step * len(self.layers))
+        for il, L in enumerate(self.layers):
+            W = L["wqkv"]
+            t = DevTensor(base + il * step, (n,), np.uint8, owns=False, dev=self.dev)
+            call("lt_q8_tiles_rope", self.dev.handle, W.t.vp, t.vp, W.N, W.K, c.n_head, c.n_head_kv, c.head_dim)
+            L["wqkv_rt"] = Q8Weight(None, W.K, t=t, N=W.N)
+        self.qkv_rope = base
 
     def planar_eligible(self) -> bool:
         """Every matrix the five-launch step streams (q|k|v, o, interleaved gate|up, down, the
@@ -680,6 +698,11 @@ class ResidentModel:
             for L in self.layers:
                 for k in ("wqkv_pl", "wo_pl", "wgu_il_pl", "wdown_pl"):
                     L.pop(k, None)
+        if self.qkv_rope is not None:
+            self.dev.free(self.qkv_rope)
+            self.qkv_rope = None
+            for L in self.layers:
+                L.pop("wqkv_rt", None)
         if self._head_pl is not None:
             self._head_pl.free()
             self._head_pl = None
@@ -1434,6 +1457,14 @@ HEAD_GEMM_MIN_BATCH = 5
 # / 44419, 128 64023 / 70172: the fused kernel's 8-wave workgroups leave 8 waves per CU where
 # the 4-wave ones fit 12)
 SILU_QUANT_MAX_BATCH = 32
+# from this many sequences the mixed and GEMM forms run q|k|v on the tiled GEMM with the RoPE +
+# KV-append epilogue (lt_q8_gemm_rope_t, the weights in the rope-pair order) instead of the
+# multi-token GEMV with it (mixed) or the GEMM followed by lt_rope_append_seqs (GEMM form);
+# C2 mixed-form tok/s, GEMV / GEMM q|k|v: B = 24 21428 / 21050, 32 27692 / 27312, 64 48003 /
+# 49424, 128 77421 / 83263
+QKV_GEMM_MIN_BATCH = 48
+
+
 class BatchDecodePlan:
     """B sequences decoded together (the reference's future-work note on batching its
     device-uniform path, bpd/lib/dev_residency.py:1344-1350).  Each step takes the next token
@@ -1474,6 +1505,9 @@ class BatchDecodePlan:
         self.max_ctx = int(max_ctx or cfg.max_ctx)
         model.prefill_tiles()
         self.head = model.head_tiles()
+        self.qkv_gemm = linear in ("mixed", "gemm") and self.B >= QKV_GEMM_MIN_BATCH
+        if self.qkv_gemm:
+            model.qkv_rope_tiles()
         esz = 2 if profile.kv_dtype == LT_KV_F16 else 4
         self.slot_bytes = self.max_ctx * cfg.kv_dim * esz
         self.k = [DevTensor.empty((B * self.slot_bytes,), np.uint8, D) for _ in range(cfg.n_layers)]
@@ -1605,10 +1639,14 @@ class BatchDecodePlan:
         for il, L in enumerate(m.layers):
             kp, vp = self.k[il].vp, self.v[il].vp
             call("lt_rmsnorm_quant_bm", h, self.x.vp, L["attn_norm"].vp, self.xq.vp, self.xd.vp, B, E, eps)
-            call("lt_q8_gemm_t", h, L["wqkv_t"].t.vp, self.xq.vp, self.xd.vp, _vp(L["bqkv"]), None, self.qkv.vp,
-                 B, NQ, E)
-            call("lt_rope_append_seqs", h, self.qkv.vp, B, NQ, pos, nh, nkv, hd, m.freqs.vp, kp, vp, self.max_ctx,
-                 p.kv_dtype)
+            if self.qkv_gemm:
+                call("lt_q8_gemm_rope_t", h, L["wqkv_rt"].t.vp, self.xq.vp, self.xd.vp, B, _vp(L["bqkv"]),
+                     self.qkv.vp, NQ, E, pos, nh, nkv, hd, m.freqs.vp, kp, vp, self.max_ctx, p.kv_dtype)
+            else:
+                call("lt_q8_gemm_t", h, L["wqkv_t"].t.vp, self.xq.vp, self.xd.vp, _vp(L["bqkv"]), None,
+                     self.qkv.vp, B, NQ, E)
+                call("lt_rope_append_seqs", h, self.qkv.vp, B, NQ, pos, nh, nkv, hd, m.freqs.vp, kp, vp,
+                     self.max_ctx, p.kv_dtype)
             call("lt_attn_decode_rows", h, self.qkv.vp, NQ, kp, vp, attn, self.att.vp, B, nh, nkv, hd,
                  ctypes.c_float(self.scale), self.max_ctx, p.attn_nsplit, p.kv_dtype, ws, ws_n)
             call("lt_quant_q8_bm", h, self.att.vp, self.xq.vp, self.xd.vp, B, QD)
@@ -1630,7 +1668,8 @@ class BatchDecodePlan:
         blocks once per group of 2 to 8 sequences.  mixed: gate|up, down and the vocab
         projection run the tiled GEMM instead (tile-major weights, block-major quants; the
         leaf-split kernel at these token counts), whose weight blocks are read once per 32
-        sequences; QKV and O, with the fewest rows, stay on the GEMV."""
+        sequences; O stays on the GEMV, and QKV too below QKV_GEMM_MIN_BATCH sequences (from
+        there the GEMM with the RoPE + KV-append epilogue)."""
         cfg, m, p, B = self.cfg, self.model, self.profile, self.B
         h = self.dev.handle
         E, F, hd, nh, nkv = cfg.n_embd, cfg.n_ff, cfg.head_dim, cfg.n_head, cfg.n_head_kv
@@ -1642,10 +1681,15 @@ class BatchDecodePlan:
         call("lt_embed_q8_batch", h, m.tok_embd.t.vp, self.toks.vp, self.x.vp, B, E, cfg.vocab, self.err.vp)
         for il, L in enumerate(m.layers):
             kp, vp = self.k[il].vp, self.v[il].vp
-            call("lt_rmsnorm_quant_rows", h, self.x.vp, L["attn_norm"].vp, xq, xd, B, E, eps)
             # q|k|v + bias, RoPE and the KV append in one launch
-            call("lt_q8_gemv_multi_rope", h, L["wqkv"].t.vp, xq, xd, B, _vp(L["bqkv"]), self.qkv.vp, NQ, E, pos,
-                 nh, nkv, hd, m.freqs.vp, kp, vp, self.max_ctx, p.kv_dtype)
+            if self.qkv_gemm:
+                call("lt_rmsnorm_quant_bm", h, self.x.vp, L["attn_norm"].vp, xq, xd, B, E, eps)
+                call("lt_q8_gemm_rope_t", h, L["wqkv_rt"].t.vp, xq, xd, B, _vp(L["bqkv"]), self.qkv.vp, NQ, E, pos,
+                     nh, nkv, hd, m.freqs.vp, kp, vp, self.max_ctx, p.kv_dtype)
+            else:
+                call("lt_rmsnorm_quant_rows", h, self.x.vp, L["attn_norm"].vp, xq, xd, B, E, eps)
+                call("lt_q8_gemv_multi_rope", h, L["wqkv"].t.vp, xq, xd, B, _vp(L["bqkv"]), self.qkv.vp, NQ, E,
+                     pos, nh, nkv, hd, m.freqs.vp, kp, vp, self.max_ctx, p.kv_dtype)
             call("lt_attn_decode_rows_q8", h, self.qkv.vp, NQ, kp, vp, attn, None, xq, xd, B, nh, nkv, hd,
                  ctypes.c_float(self.scale), self.max_ctx, p.attn_nsplit, p.kv_dtype, ws, ws_n)
             call("lt_q8_gemv_multi", h, L["wo"].t.vp, xq, xd, B, self.x.vp, self.xres.vp, E, QD, LT_MULTI_RESID)

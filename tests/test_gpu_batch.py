@@ -176,6 +176,57 @@ def test_gemv_multi_rope_equals_gemv_then_rope(gpu, nh, nkv, hd, K, T, kv_dtype)
         t.free()
 
 
+@pytest.mark.parametrize("nh,nkv,hd,K,T", [(14, 2, 64, 896, 1), (14, 2, 64, 896, 13), (14, 2, 64, 896, 64),
+                                          (14, 2, 64, 896, 70), (8, 2, 128, 1024, 8), (4, 4, 64, 96, 33),
+                                          (32, 8, 128, 4096, 5)])
+@pytest.mark.parametrize("kv_dtype", [LT_KV_F16, LT_KV_F32])
+@pytest.mark.parametrize("static", ["1", "0"])
+def test_gemm_rope_equals_gemm_then_rope(gpu, nh, nkv, hd, K, T, kv_dtype, static, monkeypatch):
+    """lt_q8_gemm_rope_t (weights in lt_q8_tiles_rope's order) equals lt_q8_gemm_t (bias) on
+    the plain tile copy followed by lt_rope_append_seqs: the q|k|v buffer and both caches
+    byte for byte, with positions spread over the cache and one past its end (no append);
+    both leaf-split schedules (LT_GEMM_LS_STATIC)."""
+    from llamatov_amd import q8 as hq8
+    monkeypatch.setenv("LT_GEMM_LS_STATIC", static)
+    case(f"gemm_rope nh={nh} nkv={nkv} hd={hd} K={K} T={T} kv={kv_dtype} static={static}")
+    rng = np.random.default_rng(T * 5 + nh + kv_dtype)
+    N, maxt = (nh + 2 * nkv) * hd, 40
+    W = dr.DevTensor.from_host(hq8.quantize_rows((rng.standard_normal((N, K)) * 0.05).astype(np.float32)), gpu)
+    n = int(dr._lib.raw("lt_q8_tiles_bytes")(N, K))
+    Wt, Wr = dr.DevTensor.empty((n,), np.uint8, gpu), dr.DevTensor.empty((n,), np.uint8, gpu)
+    call("lt_q8_tiles", gpu.handle, W.vp, Wt.vp, N, K)
+    call("lt_q8_tiles_rope", gpu.handle, W.vp, Wr.vp, N, K, nh, nkv, hd)
+    X = dr.DevTensor.from_host((rng.standard_normal((T, K)) * 2.0).astype(np.float32), gpu)
+    xq, xd = dr.DevTensor.empty((T * K,), np.int8, gpu), dr.DevTensor.empty((T * K // 32,), np.uint16, gpu)
+    call("lt_quant_q8_bm", gpu.handle, X.vp, xq.vp, xd.vp, T, K)
+    bias = dr.DevTensor.from_host((rng.standard_normal(N) * 0.1).astype(np.float32), gpu)
+    pos = rng.integers(0, maxt, T).astype(np.int32)
+    if T > 2:
+        pos[1] = maxt          # past the cache: rotated q, no append
+    lens = dr.DevTensor.from_host(pos, gpu)
+    freqs = dr.DevTensor.from_host((10000.0 ** (-np.arange(hd // 2) * 2.0 / hd)).astype(np.float32), gpu)
+    eb = 2 if kv_dtype == LT_KV_F16 else 4
+    init = rng.integers(0, 255, T * maxt * nkv * hd * eb, dtype=np.int64).astype(np.uint8)
+    outs = []
+    for fused in (False, True):
+        qkv = dr.DevTensor.empty((T, N), np.float32, gpu)
+        kc, vc = dr.DevTensor.from_host(init, gpu), dr.DevTensor.from_host(init[::-1].copy(), gpu)
+        if fused:
+            call("lt_q8_gemm_rope_t", gpu.handle, Wr.vp, xq.vp, xd.vp, T, bias.vp, qkv.vp, N, K, lens.vp, nh, nkv,
+                 hd, freqs.vp, kc.vp, vc.vp, maxt, kv_dtype)
+        else:
+            call("lt_q8_gemm_t", gpu.handle, Wt.vp, xq.vp, xd.vp, bias.vp, None, qkv.vp, T, N, K)
+            call("lt_rope_append_seqs", gpu.handle, qkv.vp, T, N, lens.vp, nh, nkv, hd, freqs.vp, kc.vp, vc.vp, maxt,
+                 kv_dtype)
+        outs.append((qkv.to_host(), kc.to_host(), vc.to_host()))
+        for t in (qkv, kc, vc):
+            t.free()
+    assert bitexact(outs[0][0], outs[1][0]), "q|k|v rows"
+    assert np.array_equal(outs[0][1], outs[1][1]) and np.array_equal(outs[0][2], outs[1][2]), "caches"
+    for t in (W, Wt, Wr, X, xq, xd, bias, lens, freqs):
+        t.free()
+
+
 def test_argmax_rows_tie_rule(gpu):
     case("argmax rows")
     rng = np.random.default_rng(5)

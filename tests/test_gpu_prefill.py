@@ -144,6 +144,33 @@ def test_q8_tiles_layout(gpu, N, K):
     assert np.array_equal(Wt.to_host(), tiles_host(W, N, K).reshape(-1))
 
 
+def rope_pair_rows(nh, nkv, hd):
+    """The rope-pair row order restated: within each q and k head, row 2j + e of the copy is
+    row j + e*hd/2 of the head; v rows keep their places."""
+    head = np.arange(hd)
+    per = (head >> 1) + (head & 1) * (hd // 2)
+    qk = (np.arange(nh + nkv)[:, None] * hd + per[None, :]).reshape(-1)
+    return np.concatenate([qk, np.arange((nh + nkv) * hd, (nh + 2 * nkv) * hd)])
+
+
+@pytest.mark.parametrize("nh,nkv,hd,K", [(14, 2, 64, 896), (4, 4, 64, 96), (2, 1, 6, 64)])
+def test_q8_tiles_rope_layout(gpu, nh, nkv, hd, K):
+    """lt_q8_tiles_rope = the tile-major copy of the rows in the rope-pair order."""
+    case(f"q8_tiles_rope nh={nh} nkv={nkv} hd={hd} K={K}")
+    N = (nh + 2 * nkv) * hd
+    rng = np.random.default_rng(N + K)
+    W = rng.integers(0, 256, (N, K // 32 * 34), dtype=np.uint8)
+    perm = rope_pair_rows(nh, nkv, hd)
+    assert sorted(perm.tolist()) == list(range(N))
+    n = int(dr._lib.raw("lt_q8_tiles_bytes")(N, K))
+    Wt = dr.DevTensor.empty((n,), np.uint8)
+    Wt.dev.fill(Wt.ptr, 0xA5, Wt.nbytes)
+    call("lt_q8_tiles_rope", gpu.handle, up(W).vp, Wt.vp, N, K, nh, nkv, hd)
+    assert np.array_equal(Wt.to_host(), tiles_host(W[perm], N, K).reshape(-1))
+    with pytest.raises(RuntimeError, match="N = \\(nh \\+ 2 nkv\\) hd"):
+        call("lt_q8_tiles_rope", gpu.handle, up(W).vp, Wt.vp, N - hd, K, nh, nkv, hd)
+
+
 @pytest.mark.parametrize("T,K", [(37, 896), (1, 32), (130, 4864), (67, 14336)])
 def test_quant_q8_block_major(gpu, oracle, T, K):
     case(f"quant_q8_bm T={T} K={K}")
