@@ -465,6 +465,12 @@ LT_API int lt_attn_decode_rows_q8(lt_ctx* ctx, const float* q, int q_stride, con
                                   const int* len, float* out, int8_t* oq, uint16_t* od, int batch, int nh, int nkv,
                                   int hd, float scale, int maxt, int nsplit, int kv_dtype, void* ws,
                                   size_t ws_bytes);
+/* The same with one split (no workspace) and the quants block-major, oq [nh*hd/32][batch][32]
+ * and od [nh*hd/32][batch]: lt_quant_q8_bm of the fp32 rows, the tiled GEMM's input (no
+ * reference counterpart: the batched step's O projection on the GEMM). */
+LT_API int lt_attn_decode_rows_q8_bm(lt_ctx* ctx, const float* q, int q_stride, const void* kc, const void* vc,
+                                     const int* len, float* out, int8_t* oq, uint16_t* od, int batch, int nh,
+                                     int nkv, int hd, float scale, int maxt, int kv_dtype);
 
 /* lt_rmsnorm_quant over T rows with row-major output (xq [T][N], xd [T][N/32]): row t is
  * bit-identical to lt_rmsnorm_quant of that row alone. */

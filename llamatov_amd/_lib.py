@@ -45,6 +45,8 @@ _SIGS = {
                                     c_int, c_int, _P, c_size_t]),
     "lt_attn_decode_rows_q8": (c_int, [_P, _P, c_int, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float,
                                        c_int, c_int, c_int, _P, c_size_t]),
+    "lt_attn_decode_rows_q8_bm": (c_int, [_P, _P, c_int, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float,
+                                          c_int, c_int]),
     "lt_argmax_rows": (c_int, [_P, _P, c_int, c_int, _P, _P, _P, c_int]),
     "lt_rmsnorm_quant_rows": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_float]),
     "lt_q8_gemv_multi": (c_int, [_P, _P, _P, _P, c_int, _P, _P, c_int, c_int, c_int]),

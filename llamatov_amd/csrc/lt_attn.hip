@@ -55,6 +55,7 @@ struct AttnArgs {
   float* out;           // [rows][nh*hd] (optional for STEP)
   int8_t* oq;           // AM_STEP / AM_DECODE: quantized output (optional)
   uint16_t* od;
+  int obm;              // > 0: oq / od block-major over obm rows (q8_out_block)
   float* wsm;           // nsplit > 1: partials
   float* wsz;
   float* wso;
@@ -66,6 +67,16 @@ struct AttnArgs {
 };
 
 constexpr int kMaxInWgSplits = 16;   // splits one workgroup can hold (partial outputs in registers)
+
+// Where block g of the quantized output goes (g counts the blocks of the [rows][nh*hd] output
+// row by row): row-major, or with obm > 0 block-major over obm rows -- quants [nh*hd/32][obm]
+// [32], scales [nh*hd/32][obm], the tiled GEMM's activation layout.
+__device__ __forceinline__ size_t q8_out_block(int obm, int nh, int hd, size_t g) {
+  if (obm <= 0) return g;
+  const size_t nbr = (size_t)(nh * hd / 32);
+  const size_t row = g / nbr;
+  return (g - row * nbr) * (size_t)obm + row;
+}
 
 template <bool kF16>
 __device__ __forceinline__ float kv_round(float v) {
@@ -455,8 +466,10 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs A) {
     __syncthreads();
     const int lane = tid & 31;
     const size_t o0 = hrow0 * hd;
-    for (int q = tid >> 5; q < nout / 32; q += 8)
-      quant_block_hw(svt[q * 32 + lane], lane, A.oq + o0 + q * 32, A.od + (o0 >> 5) + q);
+    for (int q = tid >> 5; q < nout / 32; q += 8) {
+      const size_t gb = q8_out_block(A.obm, A.nh, A.hd, (o0 >> 5) + q);
+      quant_block_hw(svt[q * 32 + lane], lane, A.oq + gb * 32, A.od + gb);
+    }
   }
   // @phase attn 6
 }
@@ -1068,8 +1081,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(
       __syncthreads();
       const int lane = l & 31;
       const size_t o0 = hrow0 * HD;
-      for (int qb = l >> 5; qb < HPW * HD / 32; qb += 2)
-        quant_block_hw(sq[qb * 32 + lane], lane, A.oq + o0 + qb * 32, A.od + (o0 >> 5) + qb);
+      for (int qb = l >> 5; qb < HPW * HD / 32; qb += 2) {
+        const size_t gb = q8_out_block(A.obm, A.nh, A.hd, (o0 >> 5) + qb);
+        quant_block_hw(sq[qb * 32 + lane], lane, A.oq + gb * 32, A.od + gb);
+      }
     }
   } else {
 #pragma unroll
@@ -1277,8 +1292,10 @@ __global__ __launch_bounds__(64 * NW) void k_attn_dec(AttnArgs A) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       const int lane = l & 31;
       const size_t o0 = hrow * HD;
-      for (int qb = l >> 5; qb < HD / 32; qb += 2)
-        quant_block_hw(sq[w * HD + qb * 32 + lane], lane, A.oq + o0 + qb * 32, A.od + (o0 >> 5) + qb);
+      for (int qb = l >> 5; qb < HD / 32; qb += 2) {
+        const size_t gb = q8_out_block(A.obm, A.nh, A.hd, (o0 >> 5) + qb);
+        quant_block_hw(sq[w * HD + qb * 32 + lane], lane, A.oq + gb * 32, A.od + gb);
+      }
     }
   } else {
 #pragma unroll
@@ -1840,6 +1857,23 @@ int lt_attn_decode_rows_q8(lt_ctx* ctx, const float* q, int q_stride, const void
   A.nh = nh; A.nkv = nkv; A.hd = hd; A.scale = scale; A.maxt = maxt; A.nsplit = nsplit;
   return launch_attn(ctx, AM_DECODE, kv_dtype == LT_KV_F16, pick_hpw(nh, nkv, hd, cb / batch), batch, A, ws,
                      ws_bytes, "lt_attn_decode_rows_q8");
+}
+
+int lt_attn_decode_rows_q8_bm(lt_ctx* ctx, const float* q, int q_stride, const void* kc, const void* vc,
+                              const int* len, float* out, int8_t* oq, uint16_t* od, int batch, int nh, int nkv, int hd,
+                              float scale, int maxt, int kv_dtype) {
+  const char* fn = "lt_attn_decode_rows_q8_bm";
+  LT_REQUIRE(ctx && q && kc && vc && len && oq && od, "%s: null argument", fn);
+  LT_REQUIRE(batch > 0 && q_stride >= nh * hd, "%s: batch=%d q_stride=%d", fn, batch, q_stride);
+  LT_REQUIRE(hd % 32 == 0, "%s: hd=%d (the quant blocks are 32 elements of one head)", fn, hd);
+  const size_t cb = cache_bytes_of(batch, maxt, nkv, hd, kv_dtype);
+  if (int rc = check_common(nh, nkv, hd, maxt, 1, kv_dtype, kc, vc, cb, fn)) return rc;
+  AttnArgs A = {};
+  A.q = q; A.q_stride = q_stride; A.kc = (void*)kc; A.vc = (void*)vc; A.len = len; A.out = out;
+  A.oq = oq; A.od = od; A.obm = batch;
+  A.nh = nh; A.nkv = nkv; A.hd = hd; A.scale = scale; A.maxt = maxt; A.nsplit = 1;
+  return launch_attn(ctx, AM_DECODE, kv_dtype == LT_KV_F16, pick_hpw(nh, nkv, hd, cb / batch), batch, A, nullptr,
+                     0, fn);
 }
 
 int lt_attn_decode_noalloc(lt_ctx* ctx, const float* q, const void* kc, const void* vc, const int* len,

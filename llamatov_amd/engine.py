@@ -1463,6 +1463,11 @@ SILU_QUANT_MAX_BATCH = 32
 # C2 mixed-form tok/s, GEMV / GEMM q|k|v: B = 24 21428 / 21050, 32 27692 / 27312, 64 48003 /
 # 49424, 128 77421 / 83263
 QKV_GEMM_MIN_BATCH = 48
+# from this many sequences the mixed form's attention writes block-major quants
+# (lt_attn_decode_rows_q8_bm, one split) and O runs the tiled GEMM with the residual epilogue
+# (the GEMM form always does, with one split); C2 mixed-form tok/s, O on the GEMV / GEMM: B =
+# 48 38518 / 37539, 64 49727 / 48617, 128 83618 / 86406
+O_GEMM_MIN_BATCH = 128
 
 
 class BatchDecodePlan:
@@ -1506,6 +1511,8 @@ class BatchDecodePlan:
         model.prefill_tiles()
         self.head = model.head_tiles()
         self.qkv_gemm = linear in ("mixed", "gemm") and self.B >= QKV_GEMM_MIN_BATCH
+        self.o_gemm = profile.attn_nsplit == 1 and (linear == "gemm" or
+                                                    (linear == "mixed" and self.B >= O_GEMM_MIN_BATCH))
         if self.qkv_gemm:
             model.qkv_rope_tiles()
         esz = 2 if profile.kv_dtype == LT_KV_F16 else 4
@@ -1647,9 +1654,14 @@ class BatchDecodePlan:
                      self.qkv.vp, B, NQ, E)
                 call("lt_rope_append_seqs", h, self.qkv.vp, B, NQ, pos, nh, nkv, hd, m.freqs.vp, kp, vp,
                      self.max_ctx, p.kv_dtype)
-            call("lt_attn_decode_rows", h, self.qkv.vp, NQ, kp, vp, attn, self.att.vp, B, nh, nkv, hd,
-                 ctypes.c_float(self.scale), self.max_ctx, p.attn_nsplit, p.kv_dtype, ws, ws_n)
-            call("lt_quant_q8_bm", h, self.att.vp, self.xq.vp, self.xd.vp, B, QD)
+            if self.o_gemm:
+                # the attention writes the O projection's block-major quants itself
+                call("lt_attn_decode_rows_q8_bm", h, self.qkv.vp, NQ, kp, vp, attn, None, self.xq.vp, self.xd.vp,
+                     B, nh, nkv, hd, ctypes.c_float(self.scale), self.max_ctx, p.kv_dtype)
+            else:
+                call("lt_attn_decode_rows", h, self.qkv.vp, NQ, kp, vp, attn, self.att.vp, B, nh, nkv, hd,
+                     ctypes.c_float(self.scale), self.max_ctx, p.attn_nsplit, p.kv_dtype, ws, ws_n)
+                call("lt_quant_q8_bm", h, self.att.vp, self.xq.vp, self.xd.vp, B, QD)
             call("lt_q8_gemm_t", h, L["wo_t"].t.vp, self.xq.vp, self.xd.vp, None, self.x.vp, self.xres.vp, B, E, QD)
             call("lt_rmsnorm_quant_bm", h, self.xres.vp, L["ffn_norm"].vp, self.xq.vp, self.xd.vp, B, E, eps)
             call("lt_q8_gemm_silu_t", h, L["wgu_il_t"].t.vp, self.xq.vp, self.xd.vp, self.vbuf.vp, B, F, E)
@@ -1690,9 +1702,15 @@ class BatchDecodePlan:
                 call("lt_rmsnorm_quant_rows", h, self.x.vp, L["attn_norm"].vp, xq, xd, B, E, eps)
                 call("lt_q8_gemv_multi_rope", h, L["wqkv"].t.vp, xq, xd, B, _vp(L["bqkv"]), self.qkv.vp, NQ, E,
                      pos, nh, nkv, hd, m.freqs.vp, kp, vp, self.max_ctx, p.kv_dtype)
-            call("lt_attn_decode_rows_q8", h, self.qkv.vp, NQ, kp, vp, attn, None, xq, xd, B, nh, nkv, hd,
-                 ctypes.c_float(self.scale), self.max_ctx, p.attn_nsplit, p.kv_dtype, ws, ws_n)
-            call("lt_q8_gemv_multi", h, L["wo"].t.vp, xq, xd, B, self.x.vp, self.xres.vp, E, QD, LT_MULTI_RESID)
+            if self.o_gemm:
+                call("lt_attn_decode_rows_q8_bm", h, self.qkv.vp, NQ, kp, vp, attn, None, xq, xd, B, nh, nkv, hd,
+                     ctypes.c_float(self.scale), self.max_ctx, p.kv_dtype)
+                call("lt_q8_gemm_t", h, L["wo_t"].t.vp, xq, xd, None, self.x.vp, self.xres.vp, B, E, QD)
+            else:
+                call("lt_attn_decode_rows_q8", h, self.qkv.vp, NQ, kp, vp, attn, None, xq, xd, B, nh, nkv, hd,
+                     ctypes.c_float(self.scale), self.max_ctx, p.attn_nsplit, p.kv_dtype, ws, ws_n)
+                call("lt_q8_gemv_multi", h, L["wo"].t.vp, xq, xd, B, self.x.vp, self.xres.vp, E, QD,
+                     LT_MULTI_RESID)
             if mixed:
                 call("lt_rmsnorm_quant_bm", h, self.xres.vp, L["ffn_norm"].vp, xq, xd, B, E, eps)
                 if B <= SILU_QUANT_MAX_BATCH:

@@ -29,18 +29,25 @@ def weights(cfg):
     return _W[cfg.name]
 
 
-@pytest.mark.parametrize("linear", ["gemv", "gemm", "mixed"])
+@pytest.mark.parametrize("linear", ["gemv", "gemm", "mixed", "gemm+rope", "mixed+rope"])
 @pytest.mark.parametrize("kv_dtype,nsplit", [(LT_KV_F32, 1), (LT_KV_F16, 1), (LT_KV_F16, 4)])
-def test_batch_rows_equal_lone_sequences(gpu, oracle, kv_dtype, nsplit, linear):
+def test_batch_rows_equal_lone_sequences(gpu, oracle, kv_dtype, nsplit, linear, monkeypatch):
+    """+rope: q|k|v on the GEMM with the RoPE + KV-append epilogue and, in the mixed form with
+    one split, O on the GEMM fed by the attention's block-major quants (QKV_GEMM_MIN_BATCH and
+    O_GEMM_MIN_BATCH lowered to this batch)."""
     cfg = M.SMALL_QWEN
     case(f"batch vs lone sequences kv={kv_dtype} nsplit={nsplit} linear={linear}")
+    linear, rope = linear.split("+")[0], linear.endswith("+rope")
+    monkeypatch.setattr(dr, "QKV_GEMM_MIN_BATCH", 1 if rope else 10 ** 6)
+    monkeypatch.setattr(dr, "O_GEMM_MIN_BATCH", 1 if rope else 10 ** 6)
     w = weights(cfg)
     model = dr.ResidentModel(cfg, w, gpu)
     lens = [3, 9, 1, 14]
     prompts = [M.random_prompt(cfg, n, seed=40 + i) for i, n in enumerate(lens)]
     plan = dr.BatchDecodePlan(model, len(prompts), dr.Profile(kv_dtype=kv_dtype, attn_nsplit=nsplit), max_ctx=64,
                               linear=linear)
-    assert plan.linear == linear
+    assert plan.linear == linear and plan.qkv_gemm == rope
+    assert plan.o_gemm == (nsplit == 1 and (linear == "gemm" or (rope and linear == "mixed")))
     orcs = [oracle.OracleModel(cfg, w, kv_f16=kv_dtype == LT_KV_F16, attn_nsplit=nsplit) for _ in prompts]
     exp = []
     for b, pr in enumerate(prompts):
@@ -82,7 +89,7 @@ def test_batch_rows_equal_lone_sequences(gpu, oracle, kv_dtype, nsplit, linear):
     model.free()
 
 
-@pytest.mark.parametrize("B,linear", [(8, "auto"), (20, "auto"), (20, "gemm"), (40, "auto")])
+@pytest.mark.parametrize("B,linear", [(8, "auto"), (20, "auto"), (20, "gemm"), (40, "auto"), (64, "auto")])
 def test_batch_generate_c2_geometry(gpu, B, linear):
     """batch_generate at the C2 model (Qwen2.5-0.5B geometry, B sequences of ragged prompts,
     multi-token GEMV or GEMM linear layers) equals generate per sequence."""
@@ -280,3 +287,14 @@ def test_attn_rows_q8_equals_attn_then_quant(gpu, nh, nkv, hd, kv_dtype, nsplit)
         assert np.array_equal(od.to_host(), rd.to_host())
         if out is not None:
             assert bitexact(out.to_host(), ref.to_host())
+    if nsplit == 1:
+        # the block-major variant: lt_quant_q8_bm of the fp32 rows
+        bq = dr.DevTensor.empty((B * QD,), np.int8, gpu)
+        bd = dr.DevTensor.empty((B * QD // 32,), np.uint16, gpu)
+        call("lt_quant_q8_bm", gpu.handle, ref.vp, bq.vp, bd.vp, B, QD)
+        oq = dr.DevTensor.empty((B * QD,), np.int8, gpu)
+        od = dr.DevTensor.empty((B * QD // 32,), np.uint16, gpu)
+        call("lt_attn_decode_rows_q8_bm", gpu.handle, dq.vp, qs, dk.vp, dv.vp, dl.vp, None, oq.vp, od.vp, B, nh, nkv,
+             hd, ctypes.c_float(hd ** -0.5), maxt, kv_dtype)
+        assert np.array_equal(oq.to_host(), bq.to_host()), "block-major quants"
+        assert np.array_equal(od.to_host(), bd.to_host()), "block-major scales"
