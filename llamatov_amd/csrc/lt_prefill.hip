@@ -725,14 +725,20 @@ __global__ __launch_bounds__(64 * kW * (kQ ? 2 : 1)) void k_q8_gemm_ls(GemmParam
   };
   if constexpr (kQ) {
     // every wave stays to the end (the barriers below are the whole workgroup's)
+    __shared__ float s_raw[2][32][33];              // [half][token][row of the half's tile] (+1 pad)
     __shared__ float s_o[32][33];                   // [token][SiLU element of the block] (+1 pad)
     if (wave == 0) {
       float v[16];
       combine(v);
-      // rows 2j (gate) and 2j+1 (up) are registers r, r+1 of one lane; this half's rows are
-      // the block's elements half*16 .. half*16 + 15
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) s_o[c][(half * 32 + c_row(r, h)) >> 1] = lt_silu_mul(v[r], v[r + 1]);
+      for (int r = 0; r < 16; r++) s_raw[half][c][c_row(r, h)] = v[r];
+    }
+    __syncthreads();
+    // the SiLU products over every wave: rows 2j (gate) and 2j+1 (up) of a half are the
+    // block's element half*16 + j
+    for (int i = threadIdx.x; i < 2 * 32 * 16; i += 2 * 64 * kW) {
+      const int hf = i >> 9, tq = (i >> 4) & 31, pr = i & 15;
+      s_o[tq][hf * 16 + pr] = lt_silu_mul(s_raw[hf][tq][2 * pr], s_raw[hf][tq][2 * pr + 1]);
     }
     __syncthreads();
     // half-wave q quantizes tokens q and q + 16 of the tile (lane = element of the block)
@@ -742,6 +748,25 @@ __global__ __launch_bounds__(64 * kW * (kQ ? 2 : 1)) void k_q8_gemm_ls(GemmParam
       const int tq = q + 16 * k, t = t0 + tq;
       if (t < P.T)   // uniform per half-wave
         quant_block_hw(s_o[tq][e], e, P.Yq + ((size_t)rtg * P.T + t) * 32, P.Yd + (size_t)rtg * P.T + t);
+    }
+    return;
+  }
+  if constexpr (EPI == GE_SILU) {
+    // the tile through LDS, then the SiLU products spread over every wave (each one's exp and
+    // division are binary64 work): output j of token q is rows 2j (gate) and 2j+1 (up)
+    __shared__ float s_o[32][33];                   // [token][row of the tile] (+1 pad)
+    if (wave == 0) {
+      float v[16];
+      combine(v);
+#pragma unroll
+      for (int r = 0; r < 16; r++) s_o[c][c_row(r, h)] = v[r];
+    }
+    __syncthreads();
+    const int F = P.N >> 1;
+    for (int i = threadIdx.x; i < 32 * 16; i += 64 * kW) {
+      const int tq = i >> 4, pr = i & 15;
+      const int t = t0 + tq, n = n0 + 2 * pr;       // N is even: n < N means n + 1 < N
+      if (t < P.T && n < P.N) P.Y[(size_t)t * F + (n >> 1)] = lt_silu_mul(s_o[tq][2 * pr], s_o[tq][2 * pr + 1]);
     }
     return;
   }
@@ -811,23 +836,14 @@ __global__ __launch_bounds__(64 * kW * (kQ ? 2 : 1)) void k_q8_gemm_ls(GemmParam
   combine(v);
   const int t = t0 + c;
   if (t >= P.T) return;
-  if constexpr (EPI == GE_SILU) {
-    const int F = P.N >> 1;
 #pragma unroll
-    for (int r = 0; r < 16; r += 2) {
-      const int n = n0 + c_row(r, h);
-      if (n < P.N) P.Y[(size_t)t * F + (n >> 1)] = lt_silu_mul(v[r], v[r + 1]);
-    }
-  } else {
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int n = n0 + c_row(r, h);
-      if (n < P.N) {
-        float o = v[r];
-        if constexpr (EPI == GE_BIAS) o = o + P.bias[n];
-        if constexpr (EPI == GE_RESID) o = o + P.resid[(size_t)t * P.N + n];
-        P.Y[(size_t)t * P.N + n] = o;
-      }
+  for (int r = 0; r < 16; r++) {
+    const int n = n0 + c_row(r, h);
+    if (n < P.N) {
+      float o = v[r];
+      if constexpr (EPI == GE_BIAS) o = o + P.bias[n];
+      if constexpr (EPI == GE_RESID) o = o + P.resid[(size_t)t * P.N + n];
+      P.Y[(size_t)t * P.N + n] = o;
     }
   }
 }

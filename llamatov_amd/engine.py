@@ -1452,11 +1452,10 @@ MIXED_MAX_BATCH = 128
 # 6 63.2 / 51.8, 8 73.9 / 55.5, 16 125.6 / 56.8
 HEAD_GEMM_MIN_BATCH = 5
 # up to this many sequences the mixed form's gate|up launch also quantizes its SiLU output
-# (lt_q8_gemm_silu_quant_t: workgroups of two row tiles, 8 waves, one per CU); past it the
-# separate quant launch is cheaper (C2 tok/s fused / separate: B = 32 25894 / 25259, 64 40921
-# / 44419, 128 64023 / 70172: the fused kernel's 8-wave workgroups leave 8 waves per CU where
-# the 4-wave ones fit 12)
-SILU_QUANT_MAX_BATCH = 32
+# (lt_q8_gemm_silu_quant_t: workgroups of two row tiles, 8 waves); past it the separate quant
+# launch; C2 tok/s fused / separate: B = 64 51389 / 50691, 128 90007 / 88532 (the mixed
+# form's whole range)
+SILU_QUANT_MAX_BATCH = 128
 # from this many sequences the mixed and GEMM forms run q|k|v on the tiled GEMM with the RoPE +
 # KV-append epilogue (lt_q8_gemm_rope_t, the weights in the rope-pair order) instead of the
 # multi-token GEMV with it (mixed) or the GEMM followed by lt_rope_append_seqs (GEMM form);
