@@ -496,7 +496,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSL >= 2 ? 
 // at run time (any K).
 template <GemmEpi EPI, int kW, bool kQ = false, int kP = 0>
 __global__ __launch_bounds__(64 * kW * (kQ ? 2 : 1)) void k_q8_gemm_ls(GemmParams P) {
-  static_assert(kW == 4 || kW == 8, "k_q8_gemm_ls: 4 or 8 waves per tile");
+  static_assert(kW == 4 || kW == 8 || kW == 16, "k_q8_gemm_ls: 4, 8 or 16 waves per tile");
+  static_assert(!(kQ && kW == 16), "k_q8_gemm_ls: the quantizing variant has 8 waves per half");
   static_assert(!kQ || (EPI == GE_SILU && kW == 4), "k_q8_gemm_ls: the quantizing variant is SiLU, 4 waves per tile");
   constexpr int kNL = 32 / kW;                      // leaves per wave
   __shared__ float s_d[kQ ? 2 : 1][kW - 1][16 * 64];   // the partials of waves 1 .. kW-1 (per half)
@@ -561,6 +562,18 @@ __global__ __launch_bounds__(64 * kW * (kQ ? 2 : 1)) void k_q8_gemm_ls(GemmParam
   // close the leaf at post-order position i (a holds its value): the subtree's pairings
   // (static register arrays in every branch: a pointer to one would put them in scratch)
   auto close_leaf = [&](int i) {
+    if constexpr (kNL == 2) {
+      if (i == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) s0[r] = a[r];
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; r++) s0[r] = s0[r] + a[r];
+      }
+#pragma unroll
+      for (int r = 0; r < 16; r++) a[r] = 0.0f;
+      return;
+    }
     if constexpr (kNL == 4) {
       switch (i) {
         case 0:
@@ -620,7 +633,8 @@ __global__ __launch_bounds__(64 * kW * (kQ ? 2 : 1)) void k_q8_gemm_ls(GemmParam
   };
   if constexpr (kP > 0) {
     constexpr int kS = kNL * kP;                    // slots of the wave
-    constexpr int kRS = kS < 8 ? kS : 8;            // blocks in flight
+    constexpr int kRmax = kW == 16 ? 4 : 8;         // 16 waves: at most 128 registers a wave
+    constexpr int kRS = kS < kRmax ? kS : kRmax;    // blocks in flight
     // slot j: block j % kP of the leaf at post-order position j / kP (-1: past the matrix)
     auto blk = [&](int j) {
       const int b = leaf_of(j / kP) + 32 * (j % kP);
@@ -704,12 +718,35 @@ __global__ __launch_bounds__(64 * kW * (kQ ? 2 : 1)) void k_q8_gemm_ls(GemmParam
   }
   // s0 = the wave's subtree partial; the remaining levels on wave 0: pairs (w, w + s) for
   // s = kW/2, ..., 1, each into the lower wave's value
-  if (wave > 0) {
+  if constexpr (kW == 16) {
+    // the levels on every wave, one barrier each (wave 0 alone would hold 15 partials): at
+    // level s, waves s .. 2s-1 publish their values and wave w < s adds wave w + s's into its
+    // own -- the same pairs in the same order
 #pragma unroll
-    for (int r = 0; r < 16; r++) s_d[half][wave - 1][r * 64 + l] = s0[r];
+    for (int st = kW / 2; st >= 1; st /= 2) {
+      if (wave >= st && wave < 2 * st) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) s_d[half][wave - 1][r * 64 + l] = s0[r];
+      }
+      __syncthreads();
+      if (wave < st) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) s0[r] = s0[r] + s_d[half][wave + st - 1][r * 64 + l];
+      }
+    }
+  } else {
+    if (wave > 0) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) s_d[half][wave - 1][r * 64 + l] = s0[r];
+    }
+    __syncthreads();
   }
-  __syncthreads();
   auto combine = [&](float (&v)[16]) {
+    if constexpr (kW == 16) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) v[r] = s0[r];
+      return;
+    }
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       float t[kW];
@@ -1059,7 +1096,7 @@ void launch_ls(lt_ctx* ctx, const GemmParams& P, unsigned grid) {
     k_q8_gemm_ls<EPI, kW, kQ, 1><<<grid, kThreads, 0, ctx->stream>>>(P);
   } else if (bpl == 2) {
     k_q8_gemm_ls<EPI, kW, kQ, 2><<<grid, kThreads, 0, ctx->stream>>>(P);
-  } else if constexpr (kW == 8) {
+  } else if constexpr (kW >= 8) {
     if (bpl == 3) k_q8_gemm_ls<EPI, kW, kQ, 3><<<grid, kThreads, 0, ctx->stream>>>(P);
     else if (bpl == 4) k_q8_gemm_ls<EPI, kW, kQ, 4><<<grid, kThreads, 0, ctx->stream>>>(P);
     else if (bpl == 5) k_q8_gemm_ls<EPI, kW, kQ, 5><<<grid, kThreads, 0, ctx->stream>>>(P);
@@ -1079,15 +1116,20 @@ int launch_gemm(lt_ctx* ctx, GemmParams P) {
     if (mode == 1 || (mode < 0 && (P.T <= kLsMaxT || wgs < fill))) {
       P.ntt = (P.T + 31) / 32;
       const long gls = (long)((P.nrt + 7) / 8) * 8 * P.ntt;
-      // 8 waves per tile when the launch holds at most one tile per CU (LT_GEMM_LS_W=4 / 8
-      // forces one, read at every launch).  Measured at T = 64, 4 / 8 waves (us): 896 x 4864
-      // 13.4 / 8.9, 896 x 896 7.9 / 5.6, 4096 x 4096 13.1 / 10.3, 4096 x 14336 29.4 / 24.7,
-      // but 6144 x 4096 15.2 / 17.4 and 9728 x 896 10.8 / 14.0 (384 and 608 tiles).
+      // 8 waves per tile when the launch holds at most one tile per CU, 16 when in addition
+      // each leaf holds 3 to 5 blocks (K 2049 .. 5120; LT_GEMM_LS_W=4 / 8 / 16 forces one,
+      // read at every launch).  Measured at T = 64, 4 / 8 waves (us): 896 x 4864 13.4 / 8.9,
+      // 896 x 896 7.9 / 5.6, 4096 x 4096 13.1 / 10.3, 4096 x 14336 29.4 / 24.7, but 6144 x
+      // 4096 15.2 / 17.4 and 9728 x 896 10.8 / 14.0 (384 and 608 tiles); 8 / 16 waves on the
+      // compile-time schedule: 896 x 4864 7.95 / 7.58, 4096 x 4096 9.52 / 9.12, 896 x 896
+      // 4.19 / 4.26.
       const char* wenv = getenv("LT_GEMM_LS_W");
       const int wforce = wenv ? atoi(wenv) : 0;
       const long cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
-      const bool w8 = wforce ? wforce == 8 : gls <= cus;
-      if (w8) launch_ls<EPI, 8, false>(ctx, P, (unsigned)gls);
+      const int bpl = (P.K / 32 + 31) / 32;
+      const int w = wforce ? wforce : gls > cus ? 4 : (bpl >= 3 && bpl <= 5) ? 16 : 8;
+      if (w == 16) launch_ls<EPI, 16, false>(ctx, P, (unsigned)gls);
+      else if (w == 8) launch_ls<EPI, 8, false>(ctx, P, (unsigned)gls);
       else launch_ls<EPI, 4, false>(ctx, P, (unsigned)gls);
       return lt_check_launch("k_q8_gemm_ls");
     }

@@ -220,7 +220,7 @@ def force_walk(monkeypatch, walk: str) -> None:
                                        (96, 256, 70, "subnormal"), (64, 2048, 45, "bias"), (72, 6144, 130, "resid"),
                                        (33, 4096, 7, "subnormal"), (96, 8192, 77, "subnormal"),
                                        (130, 14336, 67, "bias")])
-@pytest.mark.parametrize("grouped", ["2", "1", "0", "ls", "ls8", "lsd", "lsd8"])
+@pytest.mark.parametrize("grouped", ["2", "1", "0", "ls", "ls8", "ls16", "lsd", "lsd8", "lsd16"])
 def test_q8_gemm_tiled_matches_gemv_per_token(gpu, oracle, N, K, T, epi, grouped, monkeypatch):
     """Every leaf walk of the tiled kernel (grouped leaves with a 4- or 2-slot ring where K
     allows them, the dynamic walk; forced with LT_GEMM_GROUPED) and the leaf-split kernel
@@ -253,7 +253,7 @@ def test_q8_gemm_tiled_matches_gemv_per_token(gpu, oracle, N, K, T, epi, grouped
 
 
 @pytest.mark.parametrize("F,K,T", [(4864, 896, 40), (64, 128, 7), (48, 96, 70), (128, 6144, 33), (96, 4096, 140)])
-@pytest.mark.parametrize("grouped", ["2", "1", "0", "ls", "ls8", "lsd", "lsd8"])
+@pytest.mark.parametrize("grouped", ["2", "1", "0", "ls", "ls8", "ls16", "lsd", "lsd8", "lsd16"])
 def test_q8_gemm_silu_tiled(gpu, oracle, F, K, T, grouped, monkeypatch):
     force_walk(monkeypatch, grouped)
     case(f"q8_gemm_silu_t F={F} K={K} T={T} grouped={grouped}")
