@@ -868,16 +868,21 @@ __global__ __launch_bounds__(64 * kW * (kQ ? 2 : 1)) void k_q8_gemm_ls(GemmParam
     }
     return;
   }
-  if (wave > 0) return;
-  float v[16];
-  combine(v);
-  const int t = t0 + c;
-  if (t >= P.T) return;
+  // the tile through LDS, then the epilogue over every wave, element (token q, row e) on
+  // thread 32q + e: each token's 32 rows are one 128-byte run of Y (and of the residual)
+  __shared__ float s_o[32][33];                     // [token][row of the tile] (+1 pad)
+  if (wave == 0) {
+    float v[16];
+    combine(v);
 #pragma unroll
-  for (int r = 0; r < 16; r++) {
-    const int n = n0 + c_row(r, h);
-    if (n < P.N) {
-      float o = v[r];
+    for (int r = 0; r < 16; r++) s_o[c][c_row(r, h)] = v[r];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 32 * 32; i += 64 * kW) {
+    const int tq = i >> 5, e = i & 31;
+    const int t = t0 + tq, n = n0 + e;
+    if (t < P.T && n < P.N) {
+      float o = s_o[tq][e];
       if constexpr (EPI == GE_BIAS) o = o + P.bias[n];
       if constexpr (EPI == GE_RESID) o = o + P.resid[(size_t)t * P.N + n];
       P.Y[(size_t)t * P.N + n] = o;
