@@ -445,22 +445,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSL >= 2 ? 
     for (int r = 0; r < 16; r++) v[r] = vc[r];
   }
 
-  const int t = t0 + c;
-  if (t >= P.T) return;
+  // the wave's tile through its own (now free) tree level-2 buffer, then stores along the
+  // rows: each token's 32 rows (16 SiLU outputs) are one contiguous run of Y.  Element (token
+  // q, row e) sits at 32q + (e ^ q): both the column writes and the row reads are free of
+  // bank conflicts.
+  float* tile = s_st[wave][0];
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int e = c_row(r, h);
+    tile[32 * c + (e ^ c)] = v[r];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   if constexpr (EPI == GE_SILU) {
-    // rows 2j (gate) and 2j+1 (up) are registers r, r+1 of the same lane
+    // output j of token q is rows 2j (gate) and 2j+1 (up); 4 tokens per pass
     const int F = P.N >> 1;
 #pragma unroll
-    for (int r = 0; r < 16; r += 2) {
-      const int n = n0 + c_row(r, h);
-      if (n < P.N) P.Y[(size_t)t * F + (n >> 1)] = lt_silu_mul(v[r], v[r + 1]);
+    for (int k = 0; k < 8; k++) {
+      const int q = 4 * k + (l >> 4), j = l & 15;
+      const int t = t0 + q, n = n0 + 2 * j;         // N is even: n < N means n + 1 < N
+      if (t < P.T && n < P.N)
+        P.Y[(size_t)t * F + (n >> 1)] = lt_silu_mul(tile[32 * q + ((2 * j) ^ q)], tile[32 * q + ((2 * j + 1) ^ q)]);
     }
   } else {
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int n = n0 + c_row(r, h);
-      if (n < P.N) {
-        float o = v[r];
+    for (int k = 0; k < 16; k++) {
+      const int q = 2 * k + h, t = t0 + q, n = n0 + c;
+      if (t < P.T && n < P.N) {
+        float o = tile[32 * q + (c ^ q)];
         if constexpr (EPI == GE_BIAS) o = o + P.bias[n];
         if constexpr (EPI == GE_RESID) o = o + P.resid[(size_t)t * P.N + n];
         P.Y[(size_t)t * P.N + n] = o;
