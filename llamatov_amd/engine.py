@@ -1444,8 +1444,10 @@ class StepGraph:
 # tok/s, GEMV / mixed / GEMM: B = 8 8176 / 6974 / 5675, 16 13626 / 13488 / 11194, 32 21951 /
 # 25259 / 21165, 64 31268 / 44419 / 39651, 96 35061 / 57007 / 54339, 128 38245 / 70172 / 69351;
 # with the vocab GEMM and the fused SiLU quant, GEMV / mixed: 16 14328 / 13942, 20 17031 /
-# 17058, 24 19902 / 20197, 28 22229 / 23110
-MIXED_MIN_BATCH = 24
+# 17058, 24 19902 / 20197, 28 22229 / 23110; after the leaf-split kernel's compile-time
+# schedule and coalesced epilogues, GEMV / mixed: 2 2311 / 2253, 4 4430 / 4390, 8 8530 / 8654,
+# 12 11381 / 12523, 16 14651 / 16491, 24 20275 / 23831
+MIXED_MIN_BATCH = 8
 MIXED_MAX_BATCH = 128
 # from this many sequences the vocab projection runs the tiled GEMM in every form; measured
 # 151936 x 896 per launch, multi-token GEMV / tiled GEMM (us): T = 1 32.3 / 54.2, 4 39.2 / 51.5,
@@ -1465,8 +1467,9 @@ QKV_GEMM_MIN_BATCH = 48
 # from this many sequences the mixed form's attention writes block-major quants
 # (lt_attn_decode_rows_q8_bm, one split) and O runs the tiled GEMM with the residual epilogue
 # (the GEMM form always does, with one split); C2 mixed-form tok/s, O on the GEMV / GEMM: B =
-# 48 38518 / 37539, 64 49727 / 48617, 128 83618 / 86406
-O_GEMM_MIN_BATCH = 128
+# 48 38518 / 37539, 64 49727 / 48617, 128 83618 / 86406; after the coalesced epilogues: 8 8654
+# / 8506, 12 12523 / 12526, 16 16491 / 16536, 32 30830 / 31088, 64 55985 / 57325
+O_GEMM_MIN_BATCH = 16
 
 
 class BatchDecodePlan:
