@@ -483,7 +483,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSL >= 2 ? 
 }
 
 // Leaf-split tiled GEMM, for launches with few tiles (the batched decode step: tens of
-// tokens).  A workgroup of kW waves (4 or 8) takes one 32-row x 32-token tile, so a launch
+// tokens).  A workgroup of kW waves (4, 8 or 16) takes one 32-row x 32-token tile, so a launch
 // has kW times the waves of a one-wave-per-tile walk, and each wave folds 32/kW of the
 // tile's leaves.  The GEMV's tree (halfwave_tree_dpp) pairs lanes l and l+16, then +8, +4,
 // +2, +1, so the leaves L = w, w+kW, ..., w+32-kW form the subtree of its partial at level
@@ -492,8 +492,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSL >= 2 ? 
 // wave w folds its leaves (the fma chains over blocks L, L+32, ... as in k_q8_gemm) in that
 // subtree's post-order -- L = w + kW * bitrev(i) (kW = 4: w, w+16, w+8, w+24, w+4, w+20,
 // w+12, w+28) -- closing each pair in place, and wave 0 adds the remaining levels from LDS,
-// the tree's pairings over the waves' partials (kW = 4: (d0 + d2) + (d1 + d3)).  Every
-// element is the single-token GEMV's, bit for bit.
+// the tree's pairings over the waves' partials (kW = 4: (d0 + d2) + (d1 + d3); kW = 16: the
+// same pairs level by level on every wave).  Every element is the single-token GEMV's, bit
+// for bit.  The combined tile then goes through LDS to an epilogue over every thread.
 //
 // kQ (SiLU gate|up only): a workgroup of two such halves takes two adjacent row tiles -- 64
 // interleaved rows, the gate/up pairs of one 32-element block of the SiLU output -- and, after
