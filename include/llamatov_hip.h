@@ -499,6 +499,12 @@ LT_API int lt_q8_gemv_multi_rope(lt_ctx* ctx, const void* W, const int8_t* xq, c
 /* out[r] = argmax of row r of x [rows][n] (ties to the lowest index, as lt_argmax); with
  * hist, also hist[r][count[r]] = out[r], count[r] += 1 while < cap. */
 LT_API int lt_argmax_rows(lt_ctx* ctx, const float* x, int rows, int n, int* out, int* hist, int* count, int cap);
+/* lt_argmax_rows over 8 workgroups per row (no reference counterpart; the same results):
+ * each takes a contiguous slice and writes its winner to ws, then one wave per row reduces
+ * the slices.  ws: lt_argmax_rows_workspace_size(rows) bytes, 4-byte aligned; rows <= 65535. */
+LT_API size_t lt_argmax_rows_workspace_size(int rows);
+LT_API int lt_argmax_rows_ws(lt_ctx* ctx, const float* x, int rows, int n, int* out, int* hist, int* count, int cap,
+                             void* ws, size_t ws_bytes);
 
 /* ---- ggml-compatible numerics (the optional profile; the reference's CPU substrate,
  *      bpd-substrate/bench/bpd_cpu.c:4005-4446 and bpd_gemm_q8_0_cpu.c:22-258) ----

@@ -48,6 +48,8 @@ _SIGS = {
     "lt_attn_decode_rows_q8_bm": (c_int, [_P, _P, c_int, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float,
                                           c_int, c_int]),
     "lt_argmax_rows": (c_int, [_P, _P, c_int, c_int, _P, _P, _P, c_int]),
+    "lt_argmax_rows_workspace_size": (c_size_t, [c_int]),
+    "lt_argmax_rows_ws": (c_int, [_P, _P, c_int, c_int, _P, _P, _P, c_int, _P, c_size_t]),
     "lt_rmsnorm_quant_rows": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_float]),
     "lt_q8_gemv_multi": (c_int, [_P, _P, _P, _P, c_int, _P, _P, c_int, c_int, c_int]),
     "lt_q8_gemv_multi_rope": (c_int, [_P, _P, _P, _P, c_int, _P, _P, c_int, c_int, _P, c_int, c_int, c_int, _P, _P,

@@ -380,6 +380,76 @@ __global__ __launch_bounds__(1024) void k_argmax_rows(const float* __restrict__ 
   }
 }
 
+// The same argmax over kArgmaxSlices workgroups per row: slice s of row r takes a contiguous
+// range and writes its (value, index) winner to ws; k_argmax_rows_fin reduces a row's slices
+// in one wave.  The winner under the total order (value, then lowest index; NaN never wins)
+// does not depend on how the row is cut, so the result is k_argmax_rows's.
+constexpr int kArgmaxSlices = 8;
+
+__global__ __launch_bounds__(1024) void k_argmax_rows_part(const float* __restrict__ x, int n, float* __restrict__ wv,
+                                                           int* __restrict__ wi) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  const int r = blockIdx.y, sl = blockIdx.x;
+  const int chunk = ((n + kArgmaxSlices - 1) / kArgmaxSlices + 1023) & ~1023;
+  const int lo = sl * chunk, hi = lo + chunk < n ? lo + chunk : n;
+  const float* xr = x + (size_t)r * n;
+  float bv = -__builtin_inff();
+  int bi = 0x7FFFFFFF;
+  for (int base = lo; base < hi; base += 1024 * 4) {
+    float v[4];
+    int ix[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int i = base + k * 1024 + (int)threadIdx.x;
+      v[k] = i < hi ? xr[i] : -__builtin_inff();
+      ix[k] = i < hi ? i : 0x7FFFFFFF;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+      if (am_better(v[k], ix[k], bv, bi)) { bv = v[k]; bi = ix[k]; }
+  }
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) {
+    const float ov = __shfl_xor(bv, m, 64);
+    const int oi = __shfl_xor(bi, m, 64);
+    if (am_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { sv[w] = bv; si[w] = bi; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < 16; k++)
+      if (am_better(sv[k], si[k], bv, bi)) { bv = sv[k]; bi = si[k]; }
+    wv[r * kArgmaxSlices + sl] = bv;
+    wi[r * kArgmaxSlices + sl] = bi;
+  }
+}
+
+__global__ __launch_bounds__(64) void k_argmax_rows_fin(const float* __restrict__ wv, const int* __restrict__ wi,
+                                                        int* __restrict__ out, int* __restrict__ hist,
+                                                        int* __restrict__ count, int cap) {
+  const int r = blockIdx.x, l = threadIdx.x;
+  float bv = l < kArgmaxSlices ? wv[r * kArgmaxSlices + l] : -__builtin_inff();
+  int bi = l < kArgmaxSlices ? wi[r * kArgmaxSlices + l] : 0x7FFFFFFF;
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) {
+    const float ov = __shfl_xor(bv, m, 64);
+    const int oi = __shfl_xor(bi, m, 64);
+    if (am_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  if (l == 0) {
+    out[r] = bi;
+    if (hist) {
+      const int c = count[r];
+      if (c >= 0 && c < cap) {
+        hist[(size_t)r * cap + c] = bi;
+        count[r] = c + 1;
+      }
+    }
+  }
+}
+
 inline int grid_for(long n, int per) { return (int)((n + per - 1) / per); }
 
 // ---- numerics self-check (lt_selftest_numerics) ---------------------------------------
@@ -622,6 +692,24 @@ int lt_argmax_rows(lt_ctx* ctx, const float* x, int rows, int n, int* out, int* 
   LT_REQUIRE(!hist || (count && cap > 0), "lt_argmax_rows: a history needs count and cap > 0");
   k_argmax_rows<<<rows, 1024, 0, ctx->stream>>>(x, n, out, hist, count, cap);
   return lt_check_launch("k_argmax_rows");
+}
+
+size_t lt_argmax_rows_workspace_size(int rows) { return rows > 0 ? (size_t)rows * kArgmaxSlices * 8u : 0; }
+
+int lt_argmax_rows_ws(lt_ctx* ctx, const float* x, int rows, int n, int* out, int* hist, int* count, int cap,
+                      void* ws, size_t ws_bytes) {
+  LT_REQUIRE(ctx && x && out && ws, "lt_argmax_rows_ws: null argument");
+  LT_REQUIRE(rows > 0 && n > 0 && rows <= 65535, "lt_argmax_rows_ws: rows=%d n=%d", rows, n);
+  LT_REQUIRE(!hist || (count && cap > 0), "lt_argmax_rows_ws: a history needs count and cap > 0");
+  LT_REQUIRE(ws_bytes >= lt_argmax_rows_workspace_size(rows) && lt_aligned(ws, 4),
+             "lt_argmax_rows_ws: workspace of %zu bytes, %zu needed (4-byte aligned)", ws_bytes,
+             lt_argmax_rows_workspace_size(rows));
+  float* wv = (float*)ws;
+  int* wi = (int*)(wv + (size_t)rows * kArgmaxSlices);
+  k_argmax_rows_part<<<dim3(kArgmaxSlices, rows), 1024, 0, ctx->stream>>>(x, n, wv, wi);
+  if (int rc = lt_check_launch("k_argmax_rows_part")) return rc;
+  k_argmax_rows_fin<<<rows, 64, 0, ctx->stream>>>(wv, wi, out, hist, count, cap);
+  return lt_check_launch("k_argmax_rows_fin");
 }
 
 int lt_selftest_numerics(lt_ctx* ctx, unsigned long long* out) {

@@ -1542,6 +1542,7 @@ class BatchDecodePlan:
         self.logits = DevTensor.empty((B, cfg.vocab), np.float32, D)
         aw = _lib.raw("lt_attn_workspace_size")(B, cfg.n_head, cfg.head_dim, profile.attn_nsplit)
         self.attn_ws = DevTensor.empty((aw,), np.uint8, D) if aw else None
+        self.am_ws = DevTensor.empty((int(_lib.raw("lt_argmax_rows_workspace_size")(B)),), np.uint8, D)
         self.scale = float(cfg.head_dim ** -0.5)
         self._prefill: PrefillBuffers | None = None
         self.length = [0] * B
@@ -1672,8 +1673,8 @@ class BatchDecodePlan:
         call("lt_len_add_n", h, _vp(self.lens.ptr), 2 * B, 1, self.max_ctx)
         call("lt_rmsnorm_quant_bm", h, self.x.vp, m.output_norm.vp, self.xq.vp, self.xd.vp, B, E, eps)
         call("lt_q8_gemm_t", h, self.head.t.vp, self.xq.vp, self.xd.vp, None, None, self.logits.vp, B, V, E)
-        call("lt_argmax_rows", h, self.logits.vp, B, V, self.toks.vp, self.hist.vp, self.hist_count.vp,
-             self.hist_cap)
+        call("lt_argmax_rows_ws", h, self.logits.vp, B, V, self.toks.vp, self.hist.vp, self.hist_count.vp,
+             self.hist_cap, self.am_ws.vp, self.am_ws.nbytes)
 
     def _enqueue_step_gemv(self, mixed: bool = False) -> None:
         """The step with the multi-token GEMV: 8 launches per layer (the QKV launch also rotates
@@ -1739,8 +1740,8 @@ class BatchDecodePlan:
         else:
             call("lt_rmsnorm_quant_rows", h, self.x.vp, m.output_norm.vp, xq, xd, B, E, eps)
             call("lt_q8_gemv_multi", h, m.output.t.vp, xq, xd, B, None, self.logits.vp, V, E, LT_MULTI_STORE)
-        call("lt_argmax_rows", h, self.logits.vp, B, V, self.toks.vp, self.hist.vp, self.hist_count.vp,
-             self.hist_cap)
+        call("lt_argmax_rows_ws", h, self.logits.vp, B, V, self.toks.vp, self.hist.vp, self.hist_count.vp,
+             self.hist_cap, self.am_ws.vp, self.am_ws.nbytes)
 
     def step(self, toks=None) -> None:
         """Eager step (toks=None: each sequence continues from its device token)."""
@@ -1756,7 +1757,8 @@ class BatchDecodePlan:
         if self._prefill is not None:
             self._prefill.free()
         for t in [*self.k, *self.v, self.lens, self.toks, self.err, self.hist, self.hist_count, self.x, self.xres,
-                  self.qkv, self.att, self.vbuf, self.xq, self.xd, self.vq, self.vd, self.logits, self.attn_ws]:
+                  self.qkv, self.att, self.vbuf, self.xq, self.xd, self.vq, self.vd, self.logits, self.attn_ws,
+                  self.am_ws]:
             if t is not None:
                 t.free()
 

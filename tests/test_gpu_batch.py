@@ -248,6 +248,27 @@ def test_argmax_rows_tie_rule(gpu):
     call("lt_argmax_rows", gpu.handle, d.vp, R, V, out.vp, None, None, 0)
     exp = [int(np.argmax(r)) for r in x]
     assert list(out.to_host()) == exp
+    # the sliced variant: ties across slice boundaries (19456 elements a slice here), a row of
+    # -inf, NaN never chosen, small rows (most slices empty), and the history append
+    x[1, [19455, 19456, 140000]] = 60.0
+    x[0, 3] = np.nan
+    x[0, 5] = 70.0
+    d = dr.DevTensor.from_host(x, gpu)
+    exp = [int(np.argmax(np.where(np.isnan(r), -np.inf, r))) for r in x]
+    from llamatov_amd import _lib
+    for n in (V, 100):
+        ws_n = int(_lib.raw("lt_argmax_rows_workspace_size")(R))
+        ws = dr.DevTensor.empty((ws_n,), np.uint8, gpu)
+        hist = dr.DevTensor.from_host(np.full((R, 4), -7, np.int32), gpu)
+        cnt = dr.DevTensor.from_host(np.array([0, 1, 3, 4, 2], np.int32), gpu)
+        xs = d if n == V else dr.DevTensor.from_host(np.ascontiguousarray(x[:, :n]), gpu)
+        call("lt_argmax_rows_ws", gpu.handle, xs.vp, R, n, out.vp, hist.vp, cnt.vp, 4, ws.vp, ws_n)
+        want = exp if n == V else [int(np.argmax(np.where(np.isnan(r), -np.inf, r))) for r in x[:, :n]]
+        assert list(out.to_host()) == want, n
+        h = hist.to_host()
+        for r, c in enumerate([0, 1, 3, 4, 2]):
+            assert (h[r, c] == want[r]) if c < 4 else (h[r] == -7).all()
+        assert list(cnt.to_host()) == [1, 2, 4, 4, 3]
 
 
 @pytest.mark.parametrize("nh,nkv,hd", [(14, 2, 64), (32, 8, 128), (8, 2, 32)])
